@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Benchmark of the token-selection step on one MI355X.
+
+Default workload: batched full penalty stack, B=64, V=128256 fp32 logits
+(Llama-3 head shape) ~ N(0, 4^2), 2048-id Zipf(1.1) history per row,
+repetition 1.15 / presence 0.5 / frequency 0.3, T 0.8, top-k 50, top-p 0.95,
+min-p 0.05, one seeded uniform per row.  One step = one llima_sample launch over
+one batch.  Inputs rotate over >= 1 GiB of distinct device buffers so that the
+256 MB Infinity Cache cannot serve them; they are resident in HBM before the
+timed region starts.
+
+Prints ONE JSON line.  value = sampled rows/s (whole job), ms_per_step from a
+HIP-graph replay of K steps bracketed by synchronisation; roofline.achieved =
+algorithmic bytes per launch / mean kernel duration from per-launch HIP events
+on the launch stream; cpu_baseline = the CPU oracle on a bounded sample of the
+same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "sampled rows/sec + µs/step at B=64,V=128256; achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="batched_penalties",
+                    choices=["batched_penalties", "single_row", "constrained",
+                             "large_vocab_bf16", "large_vocab_bf16_greedy", "speculative"])
+    ap.add_argument("--rotate-gib", type=float, default=1.0)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--profile-steps", type=int, default=0,
+                    help="only run this many plain launches (for rocprofv3 counter runs)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the selection step shards by rows with no exchange, "
+              "and multi-GPU runs are not part of this build (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import llima_amd
+    from llima_amd import _lib, workloads as wl
+    from llima_amd._lib import lib, check
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = lib()
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+
+    name = args.workload
+    greedy_variant = name.endswith("_greedy")
+    gen = wl.WORKLOADS["large_vocab_bf16" if greedy_variant else name]
+    w = gen()
+    t0 = time.time()
+
+    launches = []          # one callable per rotated input, taking a stream pointer
+    if name == "speculative":
+        B, D, V = w["target"].shape[0], w["target"].shape[1] - 1, w["target"].shape[2]
+        per = w["target"].nbytes + w["draft"].nbytes
+        nbuf = max(2, int(np.ceil(args.rotate_gib * 2**30 / per)))
+        g = torch.Generator(device=dev)
+        g.manual_seed(1004)
+        base_t = torch.from_numpy(w["target"]).to(dev)
+        base_d = torch.from_numpy(w["draft"]).to(dev)
+        ids = torch.from_numpy(w["draft_ids"]).to(dev)
+        ua = torch.from_numpy(w["u_accept"]).to(dev)
+        ur = torch.from_numpy(w["u_resample"]).to(dev)
+        acc = torch.empty(B, dtype=torch.int32, device=dev)
+        em = torch.empty((B, D + 1), dtype=torch.int32, device=dev)
+        nws = L.llima_verify_rejection_workspace_bytes(B, D, V)
+        ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+        bufs = [(base_t, base_d)]
+        for i in range(1, nbuf):
+            tt = torch.randn(base_t.shape, generator=g, device=dev) * 4.0
+            dd = tt[:, :D] + torch.randn(base_d.shape, generator=g, device=dev) * 1.5
+            bufs.append((tt.contiguous(), dd.contiguous()))
+        for tt, dd in bufs:
+            launches.append(lambda sp, tt=tt, dd=dd: check(L.llima_verify_rejection(
+                tt.data_ptr(), dd.data_ptr(), B, D, V, ids.data_ptr(), ua.data_ptr(),
+                ur.data_ptr(), acc.data_ptr(), em.data_ptr(), ws.data_ptr(), nws, sp),
+                "verify_rejection"))
+        alg_bytes = w["target"].nbytes + w["draft"].nbytes + ids.numel() * 4 + ua.numel() * 4 + \
+            ur.numel() * 4 + acc.numel() * 4 + em.numel() * 4
+        rows = B
+        unit_rows = "sequences/s"
+        dtype = "f32"
+        kernel_names = ["vr_rowmax", "vr_rowsum", "vr_draw"]
+        config = {"workload": "speculative", "B": B, "draft_len": D, "V": V}
+    else:
+        lg = w["logits"]
+        B, V = lg.shape
+        is_bf16 = lg.dtype == np.uint16
+        dt = _lib.LLIMA_BF16 if is_bf16 else _lib.LLIMA_F32
+        per = lg.nbytes
+        nbuf = max(2, int(np.ceil(args.rotate_gib * 2**30 / per)))
+        if is_bf16:
+            base = torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.bfloat16)
+        else:
+            base = torch.from_numpy(lg).to(dev)
+        g = torch.Generator(device=dev)
+        g.manual_seed(2000)
+        sigma = {"single_row": 3.0, "batched_penalties": 4.0, "constrained": 3.0}.get(name, 5.0)
+        bufs = [base]
+        for i in range(1, nbuf):
+            x = torch.randn((B, V), generator=g, device=dev) * sigma
+            if is_bf16:
+                x = (30.0 * torch.tanh(x / 30.0)).to(torch.bfloat16)
+            bufs.append(x.contiguous())
+        hist = None if w["history"] is None else torch.from_numpy(w["history"]).to(dev)
+        H = 0 if hist is None else hist.shape[1]
+        mask = None if w["bitmask"] is None else \
+            torch.from_numpy(w["bitmask"].view(np.int32)).to(dev)
+        u = torch.from_numpy(w["uniforms"]).to(dev)
+        cfgd = dict(w["cfg"])
+        if greedy_variant:
+            cfgd = dict(greedy=True)
+        cfg, keep_alive = llima_amd.SamplerConfig(**cfgd).to_c(B, dev)
+        out_ids = torch.empty(B, dtype=torch.int32, device=dev)
+        out_p = torch.empty(B, dtype=torch.float32, device=dev)
+        nws = L.llima_sample_workspace_bytes(B, V, dt)
+        ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+        cref = ctypes.byref(cfg)
+        hp = None if hist is None else hist.data_ptr()
+        mp = None if mask is None else mask.data_ptr()
+        for x in bufs:
+            launches.append(lambda sp, x=x: check(L.llima_sample(
+                x.data_ptr(), dt, B, V, V, hp, None, H, mp, u.data_ptr(), cref,
+                out_ids.data_ptr(), out_p.data_ptr(), None, ws.data_ptr(), nws, sp),
+                "llima_sample"))
+        alg_bytes = lg.nbytes + (0 if hist is None else hist.numel() * 4) + \
+            (0 if mask is None else mask.numel() * 4) + u.numel() * 4 + out_ids.numel() * 4 + \
+            out_p.numel() * 4
+        rows = B
+        unit_rows = "rows/s"
+        dtype = "bf16" if is_bf16 else "f32"
+        kernel_names = ["sample_kernel"]
+        config = {"workload": name, "B": B, "V": V, "history": H,
+                  "logits_dtype": "bf16" if is_bf16 else "fp32"}
+        config.update({k: v for k, v in cfgd.items()})
+    torch.cuda.synchronize()
+    setup_s = time.time() - t0
+
+    if args.profile_steps:
+        for i in range(args.profile_steps):
+            launches[i % len(launches)](sptr)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.profile_steps, "workload": name}), flush=True)
+        return
+
+    # ---- warmup
+    for i in range(args.warmup):
+        launches[i % len(launches)](sptr)
+    torch.cuda.synchronize()
+
+    # ---- per-launch kernel time with HIP events on the launch stream
+    K = args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    for i in range(K):
+        starts[i].record(stream)
+        launches[i % len(launches)](sptr)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    per_launch_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+    launch_ms = float(np.mean(per_launch_ms))
+
+    # ---- timed region: K steps, HIP graph replay (no host gaps) unless --no-graph
+    graph = None
+    if not args.no_graph:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            cap = torch.cuda.Stream(dev)
+            cap.wait_stream(stream)
+            with torch.cuda.graph(graph, stream=cap):
+                for i in range(K):
+                    launches[i % len(launches)](cap.cuda_stream)
+            torch.cuda.synchronize()
+        except Exception as e:  # pragma: no cover - reported, then eager timing
+            print(f"graph capture failed ({e}); timing eager launches", file=sys.stderr)
+            graph = None
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    if graph is not None:
+        graph.replay()          # one untimed replay
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        graph.replay()
+        ev1.record(stream)
+    else:
+        ev0.record(stream)
+        for i in range(K):
+            launches[i % len(launches)](sptr)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = ev0.elapsed_time(ev1)
+    ms_per_step = total_ms / K
+
+    achieved = alg_bytes / (launch_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": rows / (ms_per_step * 1e-3),
+        "unit": unit_rows,
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "us_per_step": ms_per_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded; inputs rotate over %d device buffers, %.2f GiB)" % (
+            len(launches), len(launches) * per / 2**30),
+        "config": config,
+        "timing": "graph replay" if graph is not None else "eager launches",
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": kernel_names,
+            "algorithmic_bytes_per_launch": int(alg_bytes),
+            "mean_launch_us": launch_ms * 1e3,
+            "median_launch_us": float(np.median(per_launch_ms)) * 1e3,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(name, w, args.cpu_seconds, greedy_variant)
+    result["setup_s"] = round(setup_s, 2)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(name, w, seconds, greedy_variant):
+    """The CPU oracle (oracle/llima_oracle.cpp, OpenMP over rows) timed on a
+    bounded sample of the same workload on this host."""
+    from oracle import oracle as orc
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    orc.lib()
+    t_end = time.time() + seconds
+    n_rows, reps = 0, 0
+    t0 = time.time()
+    if name == "speculative":
+        while time.time() < t_end or reps == 0:
+            orc.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
+                                 w["u_resample"])
+            n_rows += w["target"].shape[0]
+            reps += 1
+        unit = "sequences/s"
+        sample = f"{reps} x verify_rejection over the full [16,8,128256] batch"
+    else:
+        cfg = orc.SamplerConfig(greedy=True) if greedy_variant else orc.SamplerConfig(**w["cfg"])
+        lg = w["logits"]
+        while time.time() < t_end or reps == 0:
+            orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])
+            n_rows += lg.shape[0]
+            reps += 1
+        unit = "rows/s"
+        sample = f"{reps} x the full {list(lg.shape)} batch"
+    dt = time.time() - t0
+    return {"value": n_rows / dt, "unit": unit, "cores": threads, "kind": "port",
+            "sample": sample + f", {dt:.1f} s", "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

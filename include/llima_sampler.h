@@ -1,0 +1,165 @@
+/* llima_sampler.h -- C ABI of the MI355X logits -> token-selection library
+ * (libllima_sampler.so, built for gfx950).
+ *
+ * Every entry point takes device pointers (any HIP allocation, e.g. a PyTorch
+ * ROCm tensor's data_ptr()), plain sizes, a caller-owned workspace and a
+ * hipStream_t passed as void* (NULL = the default stream).  Launches are
+ * asynchronous on that stream; the return value only reports argument and
+ * launch errors.  No entry point allocates memory and no C++ exception
+ * crosses this boundary.
+ *
+ * Workspace contract: the workspace must be zero-filled before its first use
+ * (llima_workspace_init does that) and every call leaves it zero-filled again.
+ * Calls that share one workspace must be ordered (same stream, or synchronised).
+ *
+ * Reference interfaces replaced (sima-neat/llima, paths relative to that repo).
+ * The reference selects tokens on the host CPU through free functions and
+ * private LanguageModel members over host-mapped bf16 buffers; these entry
+ * points take the same inputs and semantics on device memory:
+ *   llima_argmax          <- argmax_bf16              sima_lmm/devkit/cpp/utils.hpp:80-152
+ *                            _calc_next_token_id      sima_lmm/devkit/cpp/language_model.cpp:3689-3714
+ *                            _argmax_lm_head_row(s)   sima_lmm/devkit/cpp/language_model.cpp:3616-3687
+ *                            spec-path argmax         sima_lmm/devkit/cpp/language_model.cpp:1518-1611
+ *                            EAGLE3 verify argmax     sima_lmm/devkit/cpp/language_model_eagle3.cpp:486-522
+ *                            DFlash proposals         sima_lmm/devkit/cpp/language_model_dflash.cpp:334-349
+ *   llima_verify_greedy   <- _argmax_lm_head_rows + resolve_draft_tokens
+ *                            sima_lmm/devkit/cpp/language_model.cpp:3636-3687,
+ *                            sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111
+ *   llima_verify_tree     <- tree_decoding gather + evaluate_posterior
+ *                            sima_lmm/devkit/cpp/language_model_eagle3.cpp:530-567,
+ *                            sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195
+ *   llima_sample          <- no reference counterpart: the reference decodes
+ *                            greedily only (sima_lmm/devkit/cpp/zmq_server.cpp:39,
+ *                            sima_lmm/mole/multimodal.py:89-95); the config
+ *                            names follow the HF GenerationConfig fields the
+ *                            reference's compiler writes (sima_lmm/model/base.py:554-583).
+ *   llima_verify_rejection <- no reference counterpart (the reference verifies
+ *                            drafts greedily, eagle_helpers.hpp:153-195); the
+ *                            greedy limit equals resolve_draft_tokens.
+ */
+#ifndef LLIMA_SAMPLER_H
+#define LLIMA_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (the reference raises std::invalid_argument / std::runtime_error
+ * for the corresponding conditions, e.g. utils.hpp:86, gemma4_mtp_helpers.cpp:89). */
+enum {
+    LLIMA_OK = 0,
+    LLIMA_E_INVAL = -1,      /* bad argument: size, dtype, config value */
+    LLIMA_E_RANGE = -2,      /* id or length out of range */
+    LLIMA_E_HIP = -3,        /* the HIP runtime reported an error at launch */
+    LLIMA_E_WORKSPACE = -4   /* workspace missing or too small */
+};
+
+enum { LLIMA_F32 = 0, LLIMA_BF16 = 1 };
+
+/* argmax modes (NaN and split handling of the reference variants):
+ *  SPLIT_FIRST: per split of split_dim values, argmax_bf16 semantics (start at
+ *               the split's first value, strict '>': a NaN first value hides
+ *               its split); splits merged keeping the greater value, or the
+ *               lower index on equal values; an all -inf row gives id 0.
+ *               One split (split_dim <= 0) is argmax_bf16 itself.
+ *  NEG_INF:     start at -inf, strict '>' over the row: NaN never wins and an
+ *               all -inf/NaN row gives id 0 (language_model_eagle3.cpp:486-522).
+ *  QUARTERS:    four parts [V*p/4, V*(p+1)/4) merged from (values[0], 0), as
+ *               _calc_next_token_id (language_model.cpp:3689-3714). */
+enum { LLIMA_ARGMAX_SPLIT_FIRST = 0, LLIMA_ARGMAX_NEG_INF = 1, LLIMA_ARGMAX_QUARTERS = 2 };
+
+/* Sampler configuration (host struct).  Scalars apply to every row unless the
+ * matching *_rows device pointer (length B) is non-NULL.
+ *   temperature        <= 0 (or greedy != 0) selects the argmax of the
+ *                      penalised, masked row (lowest index on ties)
+ *   top_k              <= 0 or >= V disables
+ *   top_p              >= 1 (or NaN) disables
+ *   min_p              <= 0 (or NaN) disables
+ *   repetition_penalty 1 disables (HF: score < 0 ? score * p : score / p)
+ *   presence_penalty, frequency_penalty  0 disables (OpenAI convention) */
+typedef struct llima_sampler_config {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    float presence_penalty;
+    float frequency_penalty;
+    int32_t greedy;
+    const float* temperature_rows;
+    const int32_t* top_k_rows;
+    const float* top_p_rows;
+    const float* min_p_rows;
+    const float* repetition_penalty_rows;
+    const float* presence_penalty_rows;
+    const float* frequency_penalty_rows;
+} llima_sampler_config;
+
+/* Zero-fills a workspace on the stream (hipMemsetAsync). */
+int llima_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Greedy selection over B rows of V logits (dtype LLIMA_F32 or LLIMA_BF16, row
+ * r at logits + r*row_stride elements).  out_ids[B] receives the index;
+ * out_vals[B] (nullable) the selected value as fp32. */
+size_t llima_argmax_workspace_bytes(int32_t B, int32_t V, int32_t dtype);
+int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
+                 int32_t split_dim, int32_t mode, int32_t* out_ids, float* out_vals,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Full sampler over B rows: grammar bitmask (nullable, [B][ceil(V/32)] uint32,
+ * bit i of word i>>5 LSB-first, 0 = masked), history (nullable, [B][H_max]
+ * int32 token ids; ids outside [0, V) are ignored; history_len nullable [B]),
+ * repetition -> frequency/presence penalties, temperature, top-k, top-p, min-p,
+ * and an inverse-CDF draw with uniforms[B] in [0, 1).
+ * out_ids[B]: token id, or -1 when no token is admissible (every value masked
+ * or -inf).  out_probs[B] (nullable): the token's probability under the final
+ * distribution (1 for greedy rows).  out_keep (nullable, [B][ceil(V/32)]):
+ * the final kept set as a bitmask (finite values only). */
+size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype);
+int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
+                 const int32_t* history, const int32_t* history_len, int32_t H_max,
+                 const uint32_t* bitmask, const float* uniforms,
+                 const llima_sampler_config* cfg, int32_t* out_ids, float* out_probs,
+                 uint32_t* out_keep, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Greedy chain verification of B sequences with D draft tokens each.
+ * target_logits: [B][D+1][V]; draft_ids: [B][D].  accepted_len[B] = length of
+ * the matching prefix; emitted[B][D+1] = accepted drafts, then the target
+ * argmax at the first mismatch (or the bonus token), then -1 padding. */
+size_t llima_verify_greedy_workspace_bytes(int32_t B, int32_t D, int32_t V, int32_t dtype);
+int llima_verify_greedy(const void* target_logits, int32_t dtype, int32_t B, int32_t D,
+                        int32_t V, const int32_t* draft_ids, int32_t* accepted_len,
+                        int32_t* emitted, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tree verification: K tree rows of logits [K][V]; retrieve_indices and
+ * candidates [n_paths][L] int32 (device).  out[3] = {best path, accept length,
+ * bonus token}. */
+size_t llima_verify_tree_workspace_bytes(int32_t K, int32_t V, int32_t dtype);
+int llima_verify_tree(const void* tree_logits, int32_t dtype, int32_t K, int32_t V,
+                      const int32_t* retrieve_indices, const int32_t* candidates,
+                      int32_t n_paths, int32_t L, int32_t* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Stochastic speculative verification (rejection sampling) of B sequences with
+ * D drafts: target_logits [B][D+1][V] fp32, draft_logits [B][D][V] fp32,
+ * draft_ids [B][D], u_accept [B][D], u_resample [B].  Accept draft k iff
+ * p_t(x_k) >= u_k * p_d(x_k); at the first rejection resample from
+ * max(0, p_t - p_d); after D acceptances draw a bonus token from p_t[D]. */
+size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, int32_t V);
+int llima_verify_rejection(const float* target_logits, const float* draft_logits, int32_t B,
+                           int32_t D, int32_t V, const int32_t* draft_ids,
+                           const float* u_accept, const float* u_resample,
+                           int32_t* accepted_len, int32_t* emitted, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+const char* llima_status_string(int status);
+int llima_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLIMA_SAMPLER_H */

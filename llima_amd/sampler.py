@@ -1,0 +1,313 @@
+"""Host API of the MI355X token-selection path.
+
+Function names and argument meanings follow the reference runtime's selection
+functions (sima-neat/llima, paths relative to that repository); the compute
+runs in the HIP kernels of libllima_sampler.so, and torch ROCm tensors are only
+the buffers handed to it (inputs must already be on the GPU).
+
+  argmax_bf16(values)                 utils.hpp:80-152
+  calc_next_token_id(logits)          language_model.cpp:3689-3714
+  argmax_lm_head_rows(rows, drafts)   language_model.cpp:3636-3687
+  resolve_draft_tokens(...)           gemma4_mtp_helpers.cpp:81-111 (via verify_greedy)
+  evaluate_posterior / verify_tree    eagle_helpers.hpp:153-195, language_model_eagle3.cpp:530-567
+  sample(...)                         the sampler stages (no reference counterpart)
+  verify_rejection(...)               stochastic draft verification (no reference counterpart)
+
+Errors: the reference throws std::invalid_argument / std::runtime_error; here
+ValueError / RuntimeError are raised for the same conditions.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+__all__ = [
+    "SamplerConfig", "argmax", "argmax_bf16", "calc_next_token_id", "argmax_lm_head_rows",
+    "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
+    "Workspace",
+]
+
+
+@dataclass
+class SamplerConfig:
+    """Per-step sampler settings (HF GenerationConfig names plus OpenAI
+    presence/frequency penalties).  Any field may instead be a CUDA tensor of
+    shape [B] giving a per-row value."""
+    temperature: float | torch.Tensor = 1.0
+    top_k: int | torch.Tensor = 0
+    top_p: float | torch.Tensor = 1.0
+    min_p: float | torch.Tensor = 0.0
+    repetition_penalty: float | torch.Tensor = 1.0
+    presence_penalty: float | torch.Tensor = 0.0
+    frequency_penalty: float | torch.Tensor = 0.0
+    greedy: bool = False
+
+    def to_c(self, B: int, device) -> tuple[_lib.SamplerConfigC, list]:
+        c = _lib.SamplerConfigC()
+        keep = []
+        for name, dtype, default in (("temperature", torch.float32, 1.0),
+                                     ("top_k", torch.int32, 0),
+                                     ("top_p", torch.float32, 1.0),
+                                     ("min_p", torch.float32, 0.0),
+                                     ("repetition_penalty", torch.float32, 1.0),
+                                     ("presence_penalty", torch.float32, 0.0),
+                                     ("frequency_penalty", torch.float32, 0.0)):
+            v = getattr(self, name)
+            if isinstance(v, torch.Tensor):
+                t = v.to(device=device, dtype=dtype).contiguous()
+                if t.numel() != B:
+                    raise ValueError(f"{name} has {t.numel()} values for {B} rows")
+                keep.append(t)
+                setattr(c, name, default)
+                setattr(c, name + "_rows", t.data_ptr())
+            else:
+                setattr(c, name, v)
+                setattr(c, name + "_rows", None)
+        c.greedy = int(bool(self.greedy))
+        return c, keep
+
+
+class Workspace:
+    """Per-device zero-filled scratch buffers, grown on demand (the kernels
+    leave them zero-filled).  Allocation happens only when a call needs more
+    than any earlier call on that device."""
+    _bufs: dict = {}
+
+    @classmethod
+    def get(cls, device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
+        key = (device.index, kind)
+        buf = cls._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            cls._bufs[key] = buf
+        return buf
+
+
+def _stream(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return _lib.LLIMA_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.LLIMA_BF16
+    raise ValueError(f"logits must be float32 or bfloat16, got {t.dtype}")
+
+
+def _on_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must be on a ROCm device")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _rows2d(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [V] or [B, V]")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    return logits
+
+
+MODES = {"split_first": _lib.ARGMAX_SPLIT_FIRST, "neg_inf": _lib.ARGMAX_NEG_INF,
+         "quarters": _lib.ARGMAX_QUARTERS}
+
+
+def argmax(logits: torch.Tensor, split_dim: int = 0, mode: str = "split_first"):
+    """Greedy selection over [B, V] rows -> (ids int32 [B], values float32 [B]).
+
+    mode "split_first": per split of split_dim values, argmax_bf16 semantics
+    (utils.hpp:80-152) merged as _argmax_lm_head_row (language_model.cpp:3616-3633);
+    "neg_inf": the EAGLE3 verify scan (language_model_eagle3.cpp:486-522);
+    "quarters": _calc_next_token_id's four-way split (language_model.cpp:3689-3714)."""
+    x = _rows2d(logits)
+    _on_gpu(x)
+    B, V = x.shape
+    if V == 0:
+        raise ValueError("argmax_bf16 requires at least one value")
+    dev = x.device
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    vals = torch.empty(B, dtype=torch.float32, device=dev)
+    dt = _dtype_code(x)
+    nb = lib().llima_argmax_workspace_bytes(B, V, dt)
+    ws = Workspace.get(dev, "argmax", nb)
+    check(lib().llima_argmax(x.data_ptr(), dt, B, V, x.stride(0), split_dim, MODES[mode],
+                             ids.data_ptr(), vals.data_ptr(), ws.data_ptr(), ws.numel(),
+                             _stream(dev)), "llima_argmax")
+    return ids, vals
+
+
+def argmax_bf16(values: torch.Tensor):
+    """{maximum value, lowest index containing it} of one row (utils.hpp:80-152)."""
+    ids, vals = argmax(values.reshape(1, -1))
+    return float(vals[0]), int(ids[0])
+
+
+def calc_next_token_id(logits: torch.Tensor) -> int:
+    """Next token of a non-speculative decode step (language_model.cpp:3689-3714)."""
+    ids, _ = argmax(logits.reshape(1, -1), mode="quarters")
+    return int(ids[0])
+
+
+def argmax_lm_head_rows(rows: torch.Tensor, expected_draft_tokens, split_dim: int = 0):
+    """_argmax_lm_head_rows (language_model.cpp:3636-3687): per-row argmax of the
+    first len(expected)+1 rows, truncated after the first row whose argmax differs
+    from the expected draft token."""
+    n = len(expected_draft_tokens) + 1
+    if n > rows.shape[0]:
+        raise RuntimeError(f"Requested {n} lm_head rows from n{rows.shape[0]} output")
+    ids, _ = argmax(rows[:n], split_dim=split_dim)
+    ids = ids.tolist()
+    out = []
+    for r, t in enumerate(ids):
+        out.append(t)
+        if r < len(expected_draft_tokens) and t != int(expected_draft_tokens[r]):
+            break
+    return out
+
+
+def sample(logits: torch.Tensor, uniforms: torch.Tensor, config: SamplerConfig,
+           history: Optional[torch.Tensor] = None, history_len: Optional[torch.Tensor] = None,
+           bitmask: Optional[torch.Tensor] = None, return_keep: bool = False):
+    """One sampling step over [B, V] logits.
+
+    history: int32 [B, H] token ids (ids outside [0, V) are padding), with an
+    optional int32 [B] history_len; bitmask: int32/uint32 [B, ceil(V/32)]
+    (bit i of word i>>5, LSB first, 0 = masked); uniforms: float32 [B] in [0,1).
+    Returns (ids int32 [B], probs float32 [B]) and, if return_keep, the final
+    kept set as a [B, ceil(V/32)] int32 bitmask.  A row with no admissible
+    token yields id -1."""
+    x = _rows2d(logits)
+    B, V = x.shape
+    dev = x.device
+    u = uniforms.to(device=dev, dtype=torch.float32).contiguous()
+    if u.numel() != B:
+        raise ValueError("one uniform per row is required")
+    H = 0
+    if history is not None:
+        history = history.to(device=dev, dtype=torch.int32).contiguous()
+        if history.dim() != 2 or history.shape[0] != B:
+            raise ValueError("history must be [B, H]")
+        H = history.shape[1]
+        if history_len is not None:
+            history_len = history_len.to(device=dev, dtype=torch.int32).contiguous()
+    nw = (V + 31) // 32
+    if bitmask is not None:
+        bitmask = bitmask.to(device=dev).contiguous()
+        if bitmask.dtype not in (torch.int32, torch.uint32):
+            raise ValueError("bitmask must be 32-bit words")
+        if tuple(bitmask.shape) != (B, nw):
+            raise ValueError(f"bitmask must be [{B}, {nw}]")
+    _on_gpu(x, u, history, history_len, bitmask)
+    cfg, keep_alive = config.to_c(B, dev)
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    probs = torch.empty(B, dtype=torch.float32, device=dev)
+    keep = torch.empty((B, nw), dtype=torch.int32, device=dev) if return_keep else None
+    dt = _dtype_code(x)
+    ws = Workspace.get(dev, "sample", lib().llima_sample_workspace_bytes(B, V, dt))
+    check(lib().llima_sample(x.data_ptr(), dt, B, V, x.stride(0), _ptr(history),
+                             _ptr(history_len), H, _ptr(bitmask), u.data_ptr(),
+                             ctypes.byref(cfg), ids.data_ptr(), probs.data_ptr(), _ptr(keep),
+                             ws.data_ptr(), ws.numel(), _stream(dev)), "llima_sample")
+    del keep_alive
+    return (ids, probs, keep) if return_keep else (ids, probs)
+
+
+def verify_greedy(target_logits: torch.Tensor, draft_ids: torch.Tensor):
+    """Greedy chain verification: target_logits [B, D+1, V], draft_ids [B, D] ->
+    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded)."""
+    t = target_logits.contiguous()
+    if t.dim() != 3:
+        raise ValueError("target_logits must be [B, D+1, V]")
+    B, D1, V = t.shape
+    D = D1 - 1
+    dev = t.device
+    d = draft_ids.to(device=dev, dtype=torch.int32).contiguous().reshape(B, D)
+    _on_gpu(t, d)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    em = torch.empty((B, D1), dtype=torch.int32, device=dev)
+    dt = _dtype_code(t)
+    ws = Workspace.get(dev, "verify_greedy", lib().llima_verify_greedy_workspace_bytes(B, D, V, dt))
+    check(lib().llima_verify_greedy(t.data_ptr(), dt, B, D, V, d.data_ptr(), acc.data_ptr(),
+                                    em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_verify_greedy")
+    return acc, em
+
+
+def resolve_draft_tokens(draft_token_ids, target_next_token_ids):
+    """gemma4_mtp_helpers.cpp:81-111 on host lists (the device path computes the
+    same rule inside verify_greedy)."""
+    drafts = [int(x) for x in draft_token_ids]
+    targets = [int(x) for x in target_next_token_ids]
+    if not targets or len(targets) > len(drafts) + 1:
+        raise RuntimeError("Invalid Gemma4 MTP verification result")
+    out = []
+    for depth, tgt in enumerate(targets):
+        if depth == len(drafts) or drafts[depth] != tgt:
+            out.append((tgt, False))
+            return out
+        out.append((drafts[depth], True))
+    raise RuntimeError("Gemma4 MTP verification ended without a mismatch or bonus token")
+
+
+def verify_tree(tree_logits: torch.Tensor, retrieve_indices: torch.Tensor,
+                candidates: torch.Tensor):
+    """EAGLE3 tree verification: argmax of each tree row (from -inf,
+    language_model_eagle3.cpp:486-522), gather along retrieve_indices (-1 -> last
+    row), evaluate_posterior -> (best_candidate, accept_length, bonus_token)."""
+    t = _rows2d(tree_logits).contiguous()
+    K, V = t.shape
+    dev = t.device
+    ri = retrieve_indices.to(device=dev, dtype=torch.int32).contiguous()
+    ca = candidates.to(device=dev, dtype=torch.int32).contiguous()
+    if ri.shape != ca.shape or ri.dim() != 2:
+        raise ValueError("retrieve_indices and candidates must both be [n_paths, L]")
+    P, L = ri.shape
+    out = torch.empty(3, dtype=torch.int32, device=dev)
+    dt = _dtype_code(t)
+    ws = Workspace.get(dev, "verify_tree", lib().llima_verify_tree_workspace_bytes(K, V, dt))
+    check(lib().llima_verify_tree(t.data_ptr(), dt, K, V, ri.data_ptr(), ca.data_ptr(), P, L,
+                                  out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_verify_tree")
+    o = out.tolist()
+    return o[0], o[1], o[2]
+
+
+def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
+                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_resample: torch.Tensor):
+    """Stochastic verification: target [B, D+1, V] and draft [B, D, V] fp32
+    logits, draft ids [B, D], uniforms u_accept [B, D] and u_resample [B] ->
+    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded)."""
+    t = target_logits.contiguous()
+    dl = draft_logits.contiguous()
+    if t.dtype != torch.float32 or dl.dtype != torch.float32:
+        raise ValueError("verify_rejection takes fp32 logits")
+    B, D1, V = t.shape
+    D = D1 - 1
+    if tuple(dl.shape) != (B, D, V):
+        raise ValueError("draft_logits must be [B, D, V]")
+    dev = t.device
+    ids = draft_ids.to(device=dev, dtype=torch.int32).contiguous()
+    ua = u_accept.to(device=dev, dtype=torch.float32).contiguous()
+    ur = u_resample.to(device=dev, dtype=torch.float32).contiguous()
+    _on_gpu(t, dl, ids, ua, ur)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    em = torch.empty((B, D1), dtype=torch.int32, device=dev)
+    ws = Workspace.get(dev, "verify_rejection", lib().llima_verify_rejection_workspace_bytes(B, D, V))
+    check(lib().llima_verify_rejection(t.data_ptr(), dl.data_ptr(), B, D, V, ids.data_ptr(),
+                                       ua.data_ptr(), ur.data_ptr(), acc.data_ptr(),
+                                       em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_verify_rejection")
+    return acc, em

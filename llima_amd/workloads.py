@@ -1,0 +1,145 @@
+"""Seeded synthetic inputs for the five token-selection workloads (NumPy PCG64,
+seed = 1000 + workload number).  Shapes follow the head shapes of the models the
+reference runtime ships configs for (Qwen2.5 V=151936, Llama-3 V=128256, Gemma
+V=262144: tests/compilation/configuration/references/*_vlm_config.json in the
+reference).  Every generator accepts smaller B / V / H for quick tests.
+
+Each returns a dict of host numpy arrays:
+  logits  float32 [B, V]   (or uint16 bf16 bit patterns for the bf16 workload)
+  history int32 [B, H] or None, uniforms float32 [B], bitmask uint32 [B, V/32] or None,
+  cfg     dict of sampler settings (SamplerConfig field names).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (NaN stays NaN)."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _normal(rng, shape, sigma):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+def single_row(B=1, V=151936, H=64, seed=1001):
+    """Batch 1, fp32 vocab 151936 (Qwen2.5 head), N(0, 3^2) with 20 hot ids +8;
+    repetition 1.1 over a 64-id uniform history, T 0.7, top-k 40, top-p 0.9."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 3.0)
+    for b in range(B):
+        hot = rng.choice(V, size=min(20, V), replace=False)
+        logits[b, hot] += np.float32(8.0)
+    history = rng.integers(0, V, size=(B, H), dtype=np.int32)
+    u = rng.random(B, dtype=np.float32)
+    cfg = dict(temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.1)
+    return dict(name="single_row", logits=logits, history=history, uniforms=u, bitmask=None,
+                cfg=cfg)
+
+
+def zipf_ids(rng, V, n, s=1.1):
+    """n ids from a Zipf(s) law truncated to ranks 1..V, ranks mapped to ids by
+    a seeded permutation."""
+    ranks = np.arange(1, V + 1, dtype=np.float64)
+    cdf = np.cumsum(ranks ** -s)
+    cdf /= cdf[-1]
+    perm = rng.permutation(V).astype(np.int32)
+    r = np.searchsorted(cdf, rng.random(n), side="right")
+    return perm[np.minimum(r, V - 1)]
+
+
+def batched_penalties(B=64, V=128256, H=2048, seed=1002):
+    """B=64, fp32 vocab 128256 (Llama-3 head), N(0, 4^2); 2048-id Zipf(1.1)
+    history per row; repetition 1.15, presence 0.5, frequency 0.3, T 0.8,
+    top-k 50, top-p 0.95, min-p 0.05."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 4.0)
+    history = np.stack([zipf_ids(rng, V, H) for _ in range(B)]).astype(np.int32)
+    u = rng.random(B, dtype=np.float32)
+    cfg = dict(temperature=0.8, top_k=50, top_p=0.95, min_p=0.05, repetition_penalty=1.15,
+               presence_penalty=0.5, frequency_penalty=0.3)
+    return dict(name="batched_penalties", logits=logits, history=history, uniforms=u,
+                bitmask=None, cfg=cfg)
+
+
+def constrained(B=32, V=151936, runs=47, seed=1003):
+    """B=32, fp32 vocab 151936, N(0, 3^2); a packed uint32 grammar bitmask with
+    about 2% of the ids allowed in 64-id runs at 64-aligned starts; each row's
+    maximum is moved onto a masked-out id; T 1.0, top-p 0.9."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 3.0)
+    nw = (V + 31) // 32
+    mask = np.zeros((B, nw), np.uint32)
+    nblocks = V // 64
+    for b in range(B):
+        blocks = rng.choice(nblocks, size=min(runs, nblocks), replace=False)
+        for blk in blocks:
+            mask[b, 2 * blk] = 0xFFFFFFFF
+            mask[b, 2 * blk + 1] = 0xFFFFFFFF
+        allowed = ((mask[b, np.arange(V) >> 5] >> (np.arange(V) & 31).astype(np.uint32)) & 1)
+        banned = np.flatnonzero(allowed == 0)
+        j = banned[rng.integers(0, len(banned))]
+        logits[b, j] = logits[b].max() + np.float32(5.0)
+    u = rng.random(B, dtype=np.float32)
+    cfg = dict(temperature=1.0, top_p=0.9)
+    return dict(name="constrained", logits=logits, history=None, uniforms=u, bitmask=mask,
+                cfg=cfg)
+
+
+def _softmax64(x):
+    x = x.astype(np.float64)
+    x = x - x.max(axis=-1, keepdims=True)
+    e = np.exp(x)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def speculative(B=16, D=7, V=128256, seed=1004):
+    """EAGLE3-style verification: target [B, D+1, V] ~ N(0, 4^2); draft =
+    target[:, :D] + N(0, 1.5^2); draft ids drawn from the draft softmax."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    tgt = _normal(rng, (B, D + 1, V), 4.0)
+    drf = (tgt[:, :D] + _normal(rng, (B, D, V), 1.5)).astype(np.float32)
+    ids = np.empty((B, D), np.int32)
+    for b in range(B):
+        p = _softmax64(drf[b])
+        c = np.cumsum(p, axis=-1)
+        r = rng.random(D)
+        ids[b] = np.minimum((c < r[:, None]).sum(axis=-1), V - 1)
+    ua = rng.random((B, D), dtype=np.float32)
+    ur = rng.random(B, dtype=np.float32)
+    return dict(name="speculative", target=tgt, draft=drf, draft_ids=ids, u_accept=ua,
+                u_resample=ur)
+
+
+def large_vocab_bf16(B=256, V=262144, H=512, seed=1005):
+    """B=256, bf16 vocab 262144 (Gemma head), N(0, 5^2) soft-capped 30*tanh(x/30);
+    repetition 1.05 over a 512-id uniform history, T 1.0, top-k 64, top-p 0.95."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = _normal(rng, (B, V), 5.0)
+    x = (np.float32(30.0) * np.tanh(x / np.float32(30.0))).astype(np.float32)
+    logits = f32_to_bf16_bits(x)
+    history = rng.integers(0, V, size=(B, H), dtype=np.int32)
+    u = rng.random(B, dtype=np.float32)
+    cfg = dict(temperature=1.0, top_k=64, top_p=0.95, repetition_penalty=1.05)
+    return dict(name="large_vocab_bf16", logits=logits, history=history, uniforms=u,
+                bitmask=None, cfg=cfg)
+
+
+WORKLOADS = {
+    "single_row": single_row,
+    "batched_penalties": batched_penalties,
+    "constrained": constrained,
+    "speculative": speculative,
+    "large_vocab_bf16": large_vocab_bf16,
+}

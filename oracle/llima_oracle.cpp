@@ -1,0 +1,574 @@
+// llima_oracle.cpp -- CPU oracle for the logits -> token-selection path.
+//
+// TEST INFRASTRUCTURE ONLY.  Nothing in the product (llima_amd/) links, loads
+// or calls this file; only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg do, and only as the checker.  It is a plain, sequential
+// restatement of (1) the reference runtime's greedy selection functions and
+// (2) the written sampler specification the MI355X kernels implement, chosen to
+// be obviously correct rather than fast (full sorts, one row at a time, a dense
+// count array per row).  OpenMP is used across rows only.
+//
+// Reference behaviour restated (sima-neat/llima, paths relative to the repo):
+//   argmax_bf16                     sima_lmm/devkit/cpp/utils.hpp:80-152
+//   _calc_next_token_id (4 parts)   sima_lmm/devkit/cpp/language_model.cpp:3689-3714
+//   _argmax_lm_head_row(s)          sima_lmm/devkit/cpp/language_model.cpp:3616-3687
+//   EAGLE3 verify argmax (-inf)     sima_lmm/devkit/cpp/language_model_eagle3.cpp:486-522
+//   tree_decoding gather            sima_lmm/devkit/cpp/language_model_eagle3.cpp:551-567
+//   evaluate_posterior              sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195
+//   resolve_draft_tokens            sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111
+//   select_candidate_tokens         sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:113-167
+//   _argmax_gemma4_mtp_masked_row   sima_lmm/devkit/cpp/language_model_gemma4_mtp.cpp:31-97
+//   score_logits                    sima_lmm/devkit/cpp/language_model.cpp:29-62
+//
+// The reference has no stochastic sampler.  The sampler stages below follow the
+// specification adopted for this path (HF-transformers order and definitions:
+// transformers/generation/logits_process.py RepetitionPenalty, Temperature,
+// TopK, TopP, MinP; OpenAI presence/frequency penalties; xgrammar-style LSB-first
+// uint32 token bitmask), made bit-reproducible by integer (fixed-point) weights:
+//
+//   W(d)  = round(exp(d) * 2^36) for d = x - x_max <= 0, computed by the shared
+//           exp below (IEEE fma / rint / ldexp only); 0 for d < -26.
+//   Z     = sum of W (uint64, exact, order independent).
+//   top-p : keep i iff  S_i * 2^32 < P32 * Z  or x_i == x_max,
+//           S_i = sum of W_j over x_j > x_i, P32 = rint(p * 2^32).
+//   min-p : keep i iff  W_i >= M32 * 16   (W_max == 2^36), M32 = rint(m * 2^32).
+//   draw  : U32 = floor(u * 2^32); target = (U32 * Z') >> 32; token = smallest id
+//           whose ascending-id prefix sum of W exceeds target.
+//
+// Build: oracle/Makefile (g++ -O2 -fopenmp -ffp-contract=off).  Floating-point
+// contraction is disabled so that every product and sum is the IEEE operation
+// written in the source, exactly as in the HIP kernels.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <numeric>
+#include <vector>
+
+typedef unsigned __int128 u128;
+
+extern "C" {
+
+// ---------------------------------------------------------------- status codes
+enum { ORC_OK = 0, ORC_E_INVAL = -1, ORC_E_RANGE = -2 };
+
+// ---------------------------------------------------------------- primitives
+static inline float bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+static inline float load_logit(const void* base, int dtype, int64_t i) {
+    if (dtype == 0) return ((const float*)base)[i];
+    return bf16_to_f32(((const uint16_t*)base)[i]);
+}
+
+// exp(d) for d <= 0 by Cody-Waite reduction and a degree-7 Taylor polynomial,
+// written from the mathematics (e^d = 2^n * e^r, r = d - n ln2, |r| <= ln2/2).
+// Every step is a single IEEE operation (mul, rint, fma, ldexp), so the result
+// is identical on any IEEE-754 machine that honours fma.
+static const float ORC_LOG2E = 1.44269502162933349609375f;   // fl(log2(e))
+static const float ORC_LN2_HI = 0.693145751953125f;          // 0x3F317200
+static const float ORC_LN2_LO = 1.428606765330187045e-06f;   // ln2 - LN2_HI
+
+float orc_exp_neg(float d) {
+    if (!(d >= -26.0f)) return 0.0f;
+    float n = rintf(d * ORC_LOG2E);
+    float r = fmaf(n, -ORC_LN2_HI, d);
+    r = fmaf(n, -ORC_LN2_LO, r);
+    float p = 1.98412698412698412698e-04f;            // 1/5040
+    p = fmaf(p, r, 1.38888888888888888889e-03f);      // 1/720
+    p = fmaf(p, r, 8.33333333333333333333e-03f);      // 1/120
+    p = fmaf(p, r, 4.16666666666666666667e-02f);      // 1/24
+    p = fmaf(p, r, 1.66666666666666666667e-01f);      // 1/6
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+// Fixed-point weight of a value x given the row maximum xmax (both after all
+// transforms).  x == xmax (including xmax == +inf) has weight exactly 2^36.
+uint64_t orc_weight(float x, float xmax) {
+    if (x == xmax) return (uint64_t)1 << 36;
+    float d = x - xmax;
+    if (!(d >= -26.0f)) return 0;
+    float e = orc_exp_neg(d);
+    return (uint64_t)rintf(ldexpf(e, 36));
+}
+
+static inline uint64_t frac32(float v) {
+    // rint(v * 2^32) clamped to [0, 2^32]; v is a probability-like parameter.
+    double s = (double)v * 4294967296.0;
+    if (!(s > 0.0)) return 0;
+    if (s >= 4294967296.0) return (uint64_t)1 << 32;
+    return (uint64_t)nearbyint(s);
+}
+
+static inline uint64_t uniform32(float u) {
+    if (!(u > 0.0f)) return 0;                       // also NaN
+    if (u >= 1.0f) return 0xFFFFFFFFull;
+    return (uint64_t)floor((double)u * 4294967296.0);
+}
+
+static inline int bitlen128(u128 v) {
+    int n = 0;
+    while (v) { ++n; v >>= 1; }
+    return n;
+}
+
+// ---------------------------------------------------------------- argmax
+// mode 0: per split, argmax_bf16 semantics (best starts at the split's first
+//         element, strict '>'); splits merged from (-inf, 0) keeping the greater
+//         value or, on equal value, the lower index  (utils.hpp:80-152 and
+//         language_model.cpp:3616-3633; one split == argmax_bf16 itself).
+// mode 1: best starts at -inf, strict '>' over the whole row in order; NaN never
+//         wins and an all -inf/NaN row yields id 0 (language_model_eagle3.cpp:486-522).
+// mode 2: four parts [V*p/4, V*(p+1)/4), each argmax_bf16, merged from
+//         (values[0], 0) with the same rule (language_model.cpp:3689-3714).
+static void argmax_split(const void* row, int dtype, int64_t begin, int64_t size,
+                         float* best_v, int64_t* best_i) {
+    float best = load_logit(row, dtype, begin);
+    int64_t idx = 0;
+    for (int64_t i = 1; i < size; ++i) {
+        float v = load_logit(row, dtype, begin + i);
+        if (v > best) { best = v; idx = i; }
+    }
+    *best_v = best;
+    *best_i = begin + idx;
+}
+
+int orc_argmax(const void* logits, int dtype, int B, int V, int64_t row_stride,
+               int split_dim, int mode, int32_t* out_ids, float* out_vals) {
+    if (B < 0 || V <= 0 || (dtype != 0 && dtype != 1)) return ORC_E_INVAL;
+    if (mode < 0 || mode > 2) return ORC_E_INVAL;
+    const size_t esz = dtype == 0 ? 4 : 2;
+#pragma omp parallel for schedule(static)
+    for (int b = 0; b < B; ++b) {
+        const void* row = (const char*)logits + (size_t)b * row_stride * esz;
+        float bv;
+        int64_t bi;
+        if (mode == 1) {
+            bv = -std::numeric_limits<float>::infinity();
+            bi = 0;
+            for (int64_t i = 0; i < V; ++i) {
+                float v = load_logit(row, dtype, i);
+                if (v > bv) { bv = v; bi = i; }
+            }
+        } else if (mode == 0) {
+            int sd = (split_dim <= 0 || split_dim >= V) ? V : split_dim;
+            bv = -std::numeric_limits<float>::infinity();
+            bi = 0;
+            for (int64_t s = 0; s < V; s += sd) {
+                int64_t size = std::min<int64_t>(sd, V - s);
+                float v; int64_t i;
+                argmax_split(row, dtype, s, size, &v, &i);
+                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+            }
+        } else {
+            bv = load_logit(row, dtype, 0);
+            bi = 0;
+            for (int p = 0; p < 4; ++p) {
+                int64_t begin = (int64_t)V * p / 4, end = (int64_t)V * (p + 1) / 4;
+                if (end <= begin) continue;
+                float v; int64_t i;
+                argmax_split(row, dtype, begin, end - begin, &v, &i);
+                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+            }
+        }
+        out_ids[b] = (int32_t)bi;
+        if (out_vals) out_vals[b] = bv;
+    }
+    return ORC_OK;
+}
+
+// ---------------------------------------------------------------- sampler
+typedef struct {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    float presence_penalty;
+    float frequency_penalty;
+    int32_t greedy;
+} orc_sampler_config;
+
+// Step 1-3 of the specification: mask, NaN, repetition, frequency/presence.
+static void penalised_row(const void* row, int dtype, int V, const int32_t* hist, int hlen,
+                          const uint32_t* mask, const orc_sampler_config* c,
+                          std::vector<float>& out, std::vector<uint32_t>& counts) {
+    const float NEG_INF = -std::numeric_limits<float>::infinity();
+    out.resize(V);
+    counts.assign(V, 0);
+    for (int j = 0; j < hlen; ++j) {
+        int32_t id = hist[j];
+        if (id >= 0 && id < V) counts[id]++;
+    }
+    for (int i = 0; i < V; ++i) {
+        float l = load_logit(row, dtype, i);
+        if (l != l) l = NEG_INF;
+        if (mask && !((mask[i >> 5] >> (i & 31)) & 1u)) l = NEG_INF;
+        uint32_t cnt = counts[i];
+        if (cnt) {
+            // HF RepetitionPenaltyLogitsProcessor: score < 0 ? score * p : score / p
+            l = (l < 0.0f) ? l * c->repetition_penalty : l / c->repetition_penalty;
+            // OpenAI frequency then presence, in that order, in fp32.
+            l = (l - c->frequency_penalty * (float)cnt) - c->presence_penalty;
+        }
+        out[i] = l;
+    }
+}
+
+static bool is_greedy(const orc_sampler_config* c) {
+    return c->greedy != 0 || !(c->temperature > 0.0f);
+}
+
+// Samples one row.  Returns the token (-1 when no token is admissible) and
+// writes its probability under the final distribution.  keep (optional, V/32
+// words) receives the final kept set restricted to finite values.
+static int32_t sample_row(const void* row, int dtype, int V, const int32_t* hist, int hlen,
+                          const uint32_t* mask, float u, const orc_sampler_config* c,
+                          float* prob, uint32_t* keep) {
+    const float NEG_INF = -std::numeric_limits<float>::infinity();
+    std::vector<float> l;
+    std::vector<uint32_t> counts;
+    penalised_row(row, dtype, V, hist, hlen, mask, c, l, counts);
+    const int nwords = (V + 31) / 32;
+    if (keep) std::memset(keep, 0, sizeof(uint32_t) * nwords);
+
+    if (is_greedy(c)) {
+        float best = NEG_INF;
+        int32_t id = -1;
+        for (int i = 0; i < V; ++i)
+            if (l[i] > best) { best = l[i]; id = i; }
+        if (prob) *prob = id >= 0 ? 1.0f : 0.0f;
+        if (keep && id >= 0) keep[id >> 5] |= 1u << (id & 31);
+        return id;
+    }
+
+    // Temperature (IEEE division).
+    std::vector<float> x(V);
+    for (int i = 0; i < V; ++i) x[i] = l[i] / c->temperature;
+
+    // Top-k: tau = k-th largest with multiplicity; keep x >= tau.
+    float tau = NEG_INF;
+    if (c->top_k > 0 && c->top_k < V) {
+        std::vector<float> tmp(x);
+        std::nth_element(tmp.begin(), tmp.begin() + (c->top_k - 1), tmp.end(),
+                         [](float a, float b) { return a > b; });
+        tau = tmp[c->top_k - 1];
+    }
+    std::vector<int32_t> kept;
+    for (int i = 0; i < V; ++i)
+        if (x[i] > NEG_INF && x[i] >= tau) kept.push_back(i);
+    if (kept.empty()) { if (prob) *prob = 0.0f; return -1; }
+
+    float xmax = NEG_INF;
+    for (int32_t i : kept) xmax = std::max(xmax, x[i]);
+    std::vector<uint64_t> w(V, 0);
+    uint64_t Z = 0;
+    for (int32_t i : kept) { w[i] = orc_weight(x[i], xmax); Z += w[i]; }
+
+    // Top-p over the top-k survivors.
+    std::vector<char> fin(V, 0);
+    for (int32_t i : kept) fin[i] = 1;
+    if (c->top_p < 1.0f) {                          // NaN compares false: disabled
+        const u128 PZ = (u128)frac32(c->top_p) * Z;
+        std::vector<int32_t> order(kept);
+        std::sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+            return x[a] > x[b] || (x[a] == x[b] && a < b);
+        });
+        uint64_t above = 0;                          // mass strictly above current group
+        size_t g = 0;
+        while (g < order.size()) {
+            size_t h = g;
+            uint64_t gmass = 0;
+            while (h < order.size() && x[order[h]] == x[order[g]]) { gmass += w[order[h]]; ++h; }
+            bool k = ((u128)above << 32) < PZ || x[order[g]] == xmax;
+            for (size_t t = g; t < h; ++t) fin[order[t]] = k ? 1 : 0;
+            above += gmass;
+            g = h;
+        }
+    }
+    // Min-p relative to the maximum (whose weight is exactly 2^36).
+    if (c->min_p > 0.0f) {
+        const uint64_t thr = frac32(c->min_p) << 4;
+        for (int32_t i : kept)
+            if (fin[i] && w[i] < thr) fin[i] = 0;
+    }
+
+    uint64_t Zf = 0;
+    for (int i = 0; i < V; ++i) if (fin[i]) Zf += w[i];
+    if (keep)
+        for (int i = 0; i < V; ++i) if (fin[i]) keep[i >> 5] |= 1u << (i & 31);
+    if (Zf == 0) { if (prob) *prob = 0.0f; return -1; }
+    const uint64_t target = (uint64_t)(((u128)uniform32(u) * Zf) >> 32);
+    uint64_t acc = 0;
+    for (int i = 0; i < V; ++i) {
+        if (!fin[i]) continue;
+        acc += w[i];
+        if (acc > target) {
+            if (prob) *prob = (float)((double)w[i] / (double)Zf);
+            return i;
+        }
+    }
+    return -1;  // unreachable: acc reaches Zf > target
+}
+
+// cfg_rows: B configs (or 1 broadcast when cfg_stride == 0).
+int orc_sample(const void* logits, int dtype, int B, int V, int64_t row_stride,
+               const int32_t* hist, const int32_t* hist_len, int H_max,
+               const uint32_t* bitmask, const float* uniforms,
+               const orc_sampler_config* cfg, int cfg_stride,
+               int32_t* out_ids, float* out_probs, uint32_t* out_keep) {
+    if (B < 0 || V <= 0 || (dtype != 0 && dtype != 1) || H_max < 0) return ORC_E_INVAL;
+    const size_t esz = dtype == 0 ? 4 : 2;
+    const int nwords = (V + 31) / 32;
+#pragma omp parallel for schedule(dynamic)
+    for (int b = 0; b < B; ++b) {
+        const orc_sampler_config* c = cfg + (size_t)b * cfg_stride;
+        const void* row = (const char*)logits + (size_t)b * row_stride * esz;
+        int hl = hist ? (hist_len ? std::min(std::max(hist_len[b], 0), H_max) : H_max) : 0;
+        float p = 0.0f;
+        int32_t id = sample_row(row, dtype, V, hist ? hist + (size_t)b * H_max : nullptr, hl,
+                                bitmask ? bitmask + (size_t)b * nwords : nullptr,
+                                uniforms ? uniforms[b] : 0.0f, c, &p,
+                                out_keep ? out_keep + (size_t)b * nwords : nullptr);
+        out_ids[b] = id;
+        if (out_probs) out_probs[b] = p;
+    }
+    return ORC_OK;
+}
+
+// ---------------------------------------------------------------- verification
+// Greedy chain verification: argmax (mode 0, one split) of each target row, then
+// resolve_draft_tokens (gemma4_mtp_helpers.cpp:81-111): accept while the draft
+// equals the target argmax; emit the first mismatching target token, or the
+// bonus target token after a full match.
+int orc_resolve_draft_tokens(const int32_t* drafts, int D, const int32_t* targets, int T,
+                             int32_t* emitted, int32_t* accepted_flags, int* n_emitted) {
+    if (T <= 0 || T > D + 1) return ORC_E_RANGE;
+    int n = 0;
+    for (int depth = 0; depth < T; ++depth) {
+        if (depth == D) {
+            emitted[n] = targets[depth]; accepted_flags[n] = 0; ++n;
+            *n_emitted = n; return ORC_OK;
+        }
+        if (drafts[depth] != targets[depth]) {
+            emitted[n] = targets[depth]; accepted_flags[n] = 0; ++n;
+            *n_emitted = n; return ORC_OK;
+        }
+        emitted[n] = drafts[depth]; accepted_flags[n] = 1; ++n;
+    }
+    *n_emitted = n;
+    return ORC_E_RANGE;  // ended without a mismatch or bonus token
+}
+
+int orc_verify_greedy(const void* target_logits, int dtype, int B, int D, int V,
+                      const int32_t* draft_ids, int32_t* accepted_len, int32_t* emitted) {
+    if (B < 0 || D < 0 || V <= 0) return ORC_E_INVAL;
+    std::vector<int32_t> tgt((size_t)B * (D + 1));
+    int rc = orc_argmax(target_logits, dtype, B * (D + 1), V, V, 0, 0, tgt.data(), nullptr);
+    if (rc) return rc;
+    for (int b = 0; b < B; ++b) {
+        std::vector<int32_t> em(D + 1), fl(D + 1);
+        int n = 0;
+        orc_resolve_draft_tokens(draft_ids + (size_t)b * D, D, tgt.data() + (size_t)b * (D + 1),
+                                 D + 1, em.data(), fl.data(), &n);
+        accepted_len[b] = n - 1;
+        for (int j = 0; j < D + 1; ++j) emitted[(size_t)b * (D + 1) + j] = j < n ? em[j] : -1;
+    }
+    return ORC_OK;
+}
+
+// evaluate_posterior (eagle_helpers.hpp:153-195): per path, count leading
+// positions where the target next-token equals the next candidate (a negative
+// candidate ends the path); the first path with the strictly longest count wins;
+// bonus = target token at the accept length on that path.
+int orc_evaluate_posterior(const int32_t* next_ids, const int32_t* candidates, int n_paths,
+                           int L, int32_t* best, int32_t* accept_len, int32_t* bonus) {
+    if (n_paths <= 0 || L <= 0) return ORC_E_INVAL;
+    int32_t max_acc = 0, best_c = 0;
+    for (int c = 0; c < n_paths; ++c) {
+        int32_t acc = 0;
+        for (int i = 0; i + 1 < L; ++i) {
+            int32_t arg = next_ids[c * L + i], nxt = candidates[c * L + i + 1];
+            if (nxt < 0 || arg != nxt) break;
+            ++acc;
+        }
+        if (acc > max_acc) { max_acc = acc; best_c = c; }
+    }
+    *best = best_c;
+    *accept_len = max_acc;
+    *bonus = next_ids[best_c * L + max_acc];
+    return ORC_OK;
+}
+
+// tree_decoding gather (language_model_eagle3.cpp:551-567): -1 -> last tree row.
+int orc_tree_gather(const int32_t* row_tokens, int K, const int32_t* retrieve, int n_paths,
+                    int L, int32_t* next_ids) {
+    for (int p = 0; p < n_paths; ++p)
+        for (int d = 0; d < L; ++d) {
+            int32_t idx = retrieve[p * L + d];
+            if (idx < 0) idx = K - 1;
+            if (idx >= K) return ORC_E_RANGE;
+            next_ids[p * L + d] = row_tokens[idx];
+        }
+    return ORC_OK;
+}
+
+// Row statistics for rejection verification: max (NaN -> -inf) and Z.
+static void row_stats(const float* row, int V, float* xmax, uint64_t* Z) {
+    float m = -std::numeric_limits<float>::infinity();
+    for (int i = 0; i < V; ++i) { float v = row[i]; if (v > m) m = v; }
+    uint64_t z = 0;
+    if (m > -std::numeric_limits<float>::infinity())
+        for (int i = 0; i < V; ++i) { float v = row[i]; if (v == v) z += orc_weight(v, m); }
+    *xmax = m; *Z = z;
+}
+
+static inline uint64_t wt(const float* row, int i, float m) {
+    float v = row[i];
+    if (v != v || !(m > -std::numeric_limits<float>::infinity())) return 0;
+    return orc_weight(v, m);
+}
+
+}  // extern "C"
+
+// Draw by the specification's rule from integer weights given by f(i).
+template <class F>
+static int32_t draw_weights(int V, F f, uint64_t total, float u) {
+    if (total == 0) return -1;
+    const uint64_t target = (uint64_t)(((u128)uniform32(u) * total) >> 32);
+    uint64_t acc = 0;
+    for (int i = 0; i < V; ++i) {
+        acc += f(i);
+        if (acc > target) return i;
+    }
+    return -1;
+}
+
+extern "C" {
+
+// Stochastic speculative verification (Leviathan et al. 2023; Chen et al. 2023)
+// on fixed-point softmax weights.  target: [B, D+1, V] fp32, draft: [B, D, V] fp32.
+int orc_verify_rejection(const float* tgt, const float* drf, int B, int D, int V,
+                         const int32_t* draft_ids, const float* u_accept, const float* u_resample,
+                         int32_t* accepted_len, int32_t* emitted) {
+    if (B < 0 || D < 0 || V <= 0) return ORC_E_INVAL;
+#pragma omp parallel for schedule(dynamic)
+    for (int b = 0; b < B; ++b) {
+        int32_t* em = emitted + (size_t)b * (D + 1);
+        for (int j = 0; j <= D; ++j) em[j] = -1;
+        int k = 0;
+        bool rejected = false;
+        for (; k < D; ++k) {
+            const float* t = tgt + ((size_t)b * (D + 1) + k) * V;
+            const float* d = drf + ((size_t)b * D + k) * V;
+            float mt, md; uint64_t Zt, Zd;
+            row_stats(t, V, &mt, &Zt);
+            row_stats(d, V, &md, &Zd);
+            int32_t x = draft_ids[(size_t)b * D + k];
+            bool acc = false;
+            if (x >= 0 && x < V && Zt > 0) {
+                u128 lhs = ((u128)wt(t, x, mt) * Zd) << 32;
+                u128 rhs = (u128)uniform32(u_accept[(size_t)b * D + k]) * ((u128)wt(d, x, md) * Zt);
+                acc = lhs >= rhs;
+            }
+            if (!acc) {
+                // Residual max(0, p_t - p_d), scaled by Zt*Zd and shifted into 64 bits.
+                int shift = std::max(0, bitlen128((u128)Zt) + bitlen128((u128)Zd) - 63);
+                auto res = [&](int i) -> uint64_t {
+                    u128 a = (u128)wt(t, i, mt) * Zd, c = (u128)wt(d, i, md) * Zt;
+                    return a > c ? (uint64_t)((a - c) >> shift) : 0;
+                };
+                uint64_t R = 0;
+                for (int i = 0; i < V; ++i) R += res(i);
+                int32_t tok;
+                if (R > 0) tok = draw_weights(V, res, R, u_resample[b]);
+                else tok = draw_weights(V, [&](int i) { return wt(t, i, mt); }, Zt, u_resample[b]);
+                em[k] = tok;
+                rejected = true;
+                break;
+            }
+            em[k] = x;
+        }
+        if (!rejected) {
+            const float* t = tgt + ((size_t)b * (D + 1) + D) * V;
+            float mt; uint64_t Zt;
+            row_stats(t, V, &mt, &Zt);
+            em[D] = draw_weights(V, [&](int i) { return wt(t, i, mt); }, Zt, u_resample[b]);
+        }
+        accepted_len[b] = k;
+    }
+    return ORC_OK;
+}
+
+// ---------------------------------------------------------------- MTP centroid selection
+// select_candidate_tokens (gemma4_mtp_helpers.cpp:113-167): top-k centroids by
+// (value desc, index asc), expanded through token_ordering.
+int orc_select_candidate_tokens(const uint16_t* centroid_bf16, int n_centroids,
+                                const uint32_t* ordering, int n_ordering, int top_k,
+                                uint32_t* out_tokens, int* n_out) {
+    if (n_centroids <= 0 || n_ordering <= 0 || n_ordering % n_centroids != 0) return ORC_E_INVAL;
+    if (top_k <= 0 || top_k > n_centroids) return ORC_E_INVAL;
+    std::vector<uint32_t> idx(n_centroids);
+    std::iota(idx.begin(), idx.end(), 0u);
+    std::partial_sort(idx.begin(), idx.begin() + top_k, idx.end(), [&](uint32_t a, uint32_t b) {
+        float va = bf16_to_f32(centroid_bf16[a]), vb = bf16_to_f32(centroid_bf16[b]);
+        return va != vb ? va > vb : a < b;
+    });
+    const int per = n_ordering / n_centroids;
+    int n = 0;
+    for (int r = 0; r < top_k; ++r)
+        for (int o = 0; o < per; ++o) {
+            uint32_t tok = ordering[(size_t)idx[r] * per + o];
+            if (tok >= (uint32_t)n_ordering) return ORC_E_RANGE;
+            out_tokens[n++] = tok;
+        }
+    *n_out = n;
+    return ORC_OK;
+}
+
+// _argmax_gemma4_mtp_masked_row (language_model_gemma4_mtp.cpp:31-97): argmax
+// over candidate ids only, from (-inf, UINT32_MAX), greater value or equal value
+// with lower token id.
+int orc_masked_argmax(const void* row, int dtype, int V, const uint32_t* cand, int n_cand,
+                      int32_t* out_id) {
+    float best = -std::numeric_limits<float>::infinity();
+    uint32_t tok = 0xFFFFFFFFu;
+    for (int j = 0; j < n_cand; ++j) {
+        uint32_t t = cand[j];
+        if (t >= (uint32_t)V) continue;
+        float v = load_logit(row, dtype, t);
+        if (v > best || (v == best && t < tok)) { best = v; tok = t; }
+    }
+    if (tok == 0xFFFFFFFFu) return ORC_E_RANGE;
+    *out_id = (int32_t)tok;
+    return ORC_OK;
+}
+
+// score_logits (language_model.cpp:29-62): double log-softmax at the target id
+// and whether the target is the (first) argmax.
+int orc_score_logits(const void* row, int dtype, int V, int32_t target, double* logprob,
+                     int32_t* is_greedy_out) {
+    if (target < 0 || target >= V) return ORC_E_RANGE;
+    double mx = -std::numeric_limits<double>::infinity();
+    int32_t am = 0;
+    for (int i = 0; i < V; ++i) {
+        double v = load_logit(row, dtype, i);
+        if (v > mx) { mx = v; am = i; }
+    }
+    double s = 0.0;
+    for (int i = 0; i < V; ++i) s += std::exp((double)load_logit(row, dtype, i) - mx);
+    *logprob = (double)load_logit(row, dtype, target) - (mx + std::log(s));
+    *is_greedy_out = am == target;
+    return ORC_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+"""CPU tests of the C ABI library and the host-side Python logic (no GPU calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "llima_sampler.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(llima_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ["llima_argmax", "llima_sample", "llima_verify_greedy", "llima_verify_tree",
+              "llima_verify_rejection", "llima_workspace_init"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from llima_amd import _lib
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(L, name), name
+    assert set(_lib.SIGNATURES) == set(_declared())
+
+
+def test_host_only_entry_points():
+    from llima_amd._lib import lib
+    L = lib()
+    assert L.llima_abi_version() == 1
+    assert L.llima_status_string(-4).decode() == "workspace missing or too small"
+    assert L.llima_sample_workspace_bytes(64, 128256, 0) > 0
+    assert L.llima_argmax_workspace_bytes(0, 10, 0) == 0
+    # argument validation happens before any launch
+    assert L.llima_argmax(None, 0, 1, 10, 10, 0, 0, None, None, None, 0, None) == -1
+    assert L.llima_sample(ctypes.c_void_p(16), 7, 1, 10, 10, None, None, 0, None,
+                          ctypes.c_void_p(16), None, ctypes.c_void_p(16), None, None, None, 0,
+                          None) == -1
+    assert L.llima_verify_rejection(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 1, (1 << 22) + 4,
+                                    ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                    ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == -1
+
+
+def test_config_struct_layout_matches_header():
+    from llima_amd._lib import SamplerConfigC
+    # 8 scalar 4-byte fields then 7 pointers
+    assert ctypes.sizeof(SamplerConfigC) == 8 * 4 + 7 * 8
+    assert SamplerConfigC.temperature_rows.offset == 32
+
+
+def test_sampler_config_rows_to_c():
+    import torch
+    from llima_amd import SamplerConfig
+    cfg = SamplerConfig(temperature=torch.tensor([0.5, 0.7]), top_k=3, top_p=0.9)
+    c, keep = cfg.to_c(2, torch.device("cpu"))
+    assert c.top_k == 3 and abs(c.top_p - 0.9) < 1e-7
+    assert c.temperature_rows == keep[0].data_ptr()
+    assert c.top_k_rows is None
+    with pytest.raises(ValueError):
+        cfg.to_c(3, torch.device("cpu"))
+
+
+def test_python_api_rejects_host_tensors():
+    import torch
+    import llima_amd
+    with pytest.raises(ValueError):
+        llima_amd.argmax(torch.zeros(2, 8))
+    assert llima_amd.resolve_draft_tokens([1, 2], [1, 3]) == [(1, True), (3, False)]
+    with pytest.raises(RuntimeError):
+        llima_amd.resolve_draft_tokens([1, 2], [1, 2])

@@ -1,0 +1,327 @@
+"""GPU parity: every entry point of libllima_sampler.so (through the C ABI via
+llima_amd) against the CPU oracle on identical inputs and uniforms.  Token ids,
+index sets, kept-set bitmasks, accepted lengths are compared bit for bit; the
+sampled token's probability is compared bit for bit as well (both sides compute
+W/Z from the same integers)."""
+import numpy as np
+import pytest
+
+from llima_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[gpu-case]", *a, flush=True)
+
+
+def _t(a, dev):
+    import torch
+    if a is None:
+        return None
+    if a.dtype == np.uint16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev).view(torch.bfloat16)
+    if a.dtype == np.uint32:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+# ----------------------------------------------------------------- argmax
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,V", [(1, 1), (3, 7), (1, 151936), (8, 128256), (5, 5003),
+                                 (16, 262144), (64, 4096)])
+def test_argmax_parity(gpu, oracle, dtype, B, V):
+    import llima_amd
+    _say("argmax", dtype, B, V)
+    rng = np.random.default_rng(B * 1000 + V)
+    x = rng.integers(-50, 51, size=(B, V)).astype(np.float32) * np.float32(0.25)  # ties
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters")]:
+        ids, vals = llima_amd.argmax(_t(x, gpu), mode=mname)
+        eids, evals = oracle.argmax(x, mode=mode)
+        assert (_np(ids) == eids).all(), mname
+        assert (_np(vals).view(np.uint32) == evals.view(np.uint32)).all()
+
+
+def test_argmax_nan_split_rules(gpu, oracle):
+    import llima_amd
+    _say("argmax nan/splits")
+    rng = np.random.default_rng(9)
+    V = 20000
+    x = rng.normal(0, 1, (12, V)).astype(np.float32)
+    x[0, 0] = np.nan                        # NaN at index 0
+    x[1, 5000] = np.nan; x[1, 4999] = 50    # NaN at a 5000-split start
+    x[2, :] = -np.inf                       # all -inf
+    x[3, :] = np.nan                        # all NaN
+    x[4, V // 4] = np.nan; x[4, V // 4 + 3] = 99   # hidden quarter
+    x[5, 7] = np.inf; x[5, 9] = np.inf
+    x[6, 3] = np.nan; x[6, 10] = 1e30
+    x[7, 10000] = np.nan; x[7, 12000] = 77         # NaN at the start of split 2
+    for split in [0, 5000, 4096, 1]:
+        for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters")]:
+            ids, vals = llima_amd.argmax(_t(x, gpu), split_dim=split, mode=mname)
+            eids, evals = oracle.argmax(x, split_dim=split, mode=mode)
+            assert (_np(ids) == eids).all(), (split, mname, _np(ids), eids)
+            g, e = _np(vals), evals
+            assert ((g == e) | (np.isnan(g) & np.isnan(e))).all(), (split, mname)
+
+
+def test_argmax_strided_rows(gpu, oracle):
+    import llima_amd
+    _say("argmax strided")
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, (6, 1001)).astype(np.float32)
+    xt = _t(x, gpu)[:, 3:1000]                 # row stride 1001, unaligned start
+    ids, _ = llima_amd.argmax(xt)
+    assert (_np(ids) == oracle.argmax(np.ascontiguousarray(x[:, 3:1000]))[0]).all()
+
+
+# ----------------------------------------------------------------- sampler
+def _cfg_obj(d, rows=None):
+    import llima_amd
+    return llima_amd.SamplerConfig(**d)
+
+
+def _sample_both(gpu, oracle, logits, u, cfgd, history=None, hist_len=None, mask=None,
+                 cfg_rows=None):
+    import llima_amd
+    from oracle.oracle import SamplerConfig as OC
+    if cfg_rows is None:
+        gcfg = llima_amd.SamplerConfig(**cfgd)
+        ocfg = OC(**cfgd)
+    else:
+        import torch
+        gcfg = llima_amd.SamplerConfig(**{k: (torch.tensor(v) if isinstance(v, list) else v)
+                                          for k, v in cfg_rows.items()})
+        B = logits.shape[0]
+        ocfg = [OC(**{k: (v[b] if isinstance(v, list) else v) for k, v in cfg_rows.items()})
+                for b in range(B)]
+    ids, probs, keep = llima_amd.sample(_t(logits, gpu), _t(u, gpu), gcfg,
+                                        history=_t(history, gpu), history_len=_t(hist_len, gpu),
+                                        bitmask=_t(mask, gpu), return_keep=True)
+    eids, eprobs, ekeep = oracle.sample(logits, u, ocfg, history=history, hist_len=hist_len,
+                                        bitmask=mask, want_keep=True)
+    gi, gp, gk = _np(ids), _np(probs), _np(keep).view(np.uint32)
+    bad = np.flatnonzero(gi != eids)
+    assert bad.size == 0, f"ids differ at rows {bad[:8]}: gpu {gi[bad[:8]]} oracle {eids[bad[:8]]}"
+    assert (gp.view(np.uint32) == eprobs.view(np.uint32)).all()
+    assert (gk == ekeep).all(), np.flatnonzero((gk != ekeep).any(axis=1))[:8]
+    return gi
+
+
+WORKLOADS_SMALL = [
+    ("single_row", dict()),
+    ("batched_penalties", dict(B=16, V=128256, H=2048)),
+    ("constrained", dict(B=8)),
+    ("large_vocab_bf16", dict(B=16, V=262144, H=512)),
+]
+
+
+@pytest.mark.parametrize("name,kw", WORKLOADS_SMALL)
+def test_sample_workloads(gpu, oracle, name, kw):
+    _say("sample", name, kw)
+    w = wl.WORKLOADS[name](**kw)
+    _sample_both(gpu, oracle, w["logits"], w["uniforms"], w["cfg"], history=w["history"],
+                 mask=w["bitmask"])
+
+
+@pytest.mark.parametrize("name", ["batched_penalties", "constrained", "large_vocab_bf16"])
+def test_sample_workloads_full_size(gpu, oracle, name):
+    _say("sample full", name)
+    w = wl.WORKLOADS[name]()
+    _sample_both(gpu, oracle, w["logits"], w["uniforms"], w["cfg"], history=w["history"],
+                 mask=w["bitmask"])
+
+
+def test_sample_greedy_variants_equal_argmax(gpu, oracle):
+    """Greedy sampling without penalties or mask is the reference argmax."""
+    import llima_amd
+    _say("sample greedy == argmax")
+    for name, kw in [("single_row", {}), ("large_vocab_bf16", dict(B=32, H=8))]:
+        w = wl.WORKLOADS[name](**kw)
+        ids, _ = llima_amd.sample(_t(w["logits"], gpu), _t(w["uniforms"], gpu),
+                                  llima_amd.SamplerConfig(greedy=True))
+        am, _ = llima_amd.argmax(_t(w["logits"], gpu))
+        assert (_np(ids) == _np(am)).all()
+        assert (_np(am) == oracle.argmax(w["logits"])[0]).all()
+
+
+CONFIGS = [
+    dict(temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.1),
+    dict(temperature=1.3, top_k=1),
+    dict(temperature=0.5, top_k=257),                      # beyond the fast path's k
+    dict(temperature=1.0, top_p=0.8),                      # no top-k, no mask: full-row path
+    dict(temperature=1.0, top_p=0.0),
+    dict(temperature=0.9, min_p=1.0, top_k=20),
+    dict(temperature=1e-30, top_k=10),                     # overflowing quotients
+    dict(temperature=2.0, top_k=100, top_p=0.99, min_p=0.01, presence_penalty=-0.7,
+         frequency_penalty=0.2, repetition_penalty=0.9),
+    dict(greedy=True, repetition_penalty=1.5, presence_penalty=1.0),
+    dict(temperature=1.0),                                  # plain softmax sampling
+]
+
+
+@pytest.mark.parametrize("ci", range(len(CONFIGS)))
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_configs(gpu, oracle, ci, dtype):
+    cfgd = CONFIGS[ci]
+    _say("sample config", ci, dtype, cfgd)
+    rng = np.random.default_rng(ci * 7 + (dtype == "bf16"))
+    B, V = 12, 50000
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    x[0] = np.round(x[0])                                  # heavy ties
+    x[1, 100:200] = np.nan
+    x[2, 5] = np.inf
+    x[3, :] = -np.inf
+    x[3, 77] = 1.0
+    x[4, :] = 0.0                                          # all equal
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    hist = rng.integers(-5, V + 5, size=(B, 300)).astype(np.int32)
+    hl = rng.integers(0, 301, size=B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    u[0] = 0.0
+    u[1] = np.float32(1.0) - np.float32(2**-24)
+    _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl)
+
+
+def test_sample_masks_and_edges(gpu, oracle):
+    _say("sample masks/edges")
+    rng = np.random.default_rng(21)
+    for B, V in [(1, 1), (3, 33), (8, 1000), (9, 70001)]:
+        x = rng.normal(0, 2, (B, V)).astype(np.float32)
+        mask = rng.integers(0, 2**32, size=(B, (V + 31) // 32), dtype=np.uint64).astype(np.uint32)
+        mask[0] = 0                                         # fully masked row -> -1
+        u = rng.random(B).astype(np.float32)
+        for cfgd in [dict(temperature=1.0, top_p=0.9), dict(temperature=0.8, top_k=5),
+                     dict(greedy=True)]:
+            gi = _sample_both(gpu, oracle, x, u, cfgd, mask=mask)
+            assert gi[0] == -1
+
+
+def test_sample_per_row_configs(gpu, oracle):
+    _say("sample per-row configs")
+    rng = np.random.default_rng(5)
+    B, V = 8, 30000
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    rows = dict(temperature=[0.5, 1.0, 0.0, 2.0, 0.7, 1.0, 0.3, 1.5],
+                top_k=[10, 0, 5, 300, 50, 1, 64, 0],
+                top_p=[0.9, 0.5, 1.0, 0.95, 1.0, 0.9, 0.8, 1.0],
+                min_p=[0.0, 0.1, 0.0, 0.0, 0.05, 0.0, 0.2, 0.0],
+                repetition_penalty=1.2)
+    hist = rng.integers(0, V, size=(B, 64)).astype(np.int32)
+    _sample_both(gpu, oracle, x, u, None, history=hist, cfg_rows=rows)
+
+
+def test_sample_repeatable_and_workspace_reset(gpu, oracle):
+    """Back-to-back calls sharing one workspace give identical results."""
+    import llima_amd
+    _say("sample repeat")
+    w = wl.batched_penalties(B=24, V=40000, H=256)
+    cfg = llima_amd.SamplerConfig(**w["cfg"])
+    args = (_t(w["logits"], gpu), _t(w["uniforms"], gpu), cfg)
+    first = _np(llima_amd.sample(*args, history=_t(w["history"], gpu))[0])
+    for _ in range(5):
+        again = _np(llima_amd.sample(*args, history=_t(w["history"], gpu))[0])
+        assert (again == first).all()
+
+
+# ----------------------------------------------------------------- verification
+def test_verify_greedy_parity(gpu, oracle):
+    import llima_amd
+    _say("verify_greedy")
+    rng = np.random.default_rng(8)
+    for B, D, V, dt in [(16, 7, 128256, "f32"), (4, 6, 262144, "bf16"), (3, 0, 100, "f32")]:
+        tgt = rng.integers(-20, 21, size=(B, D + 1, V)).astype(np.float32)
+        am = tgt.argmax(axis=-1)
+        drafts = np.where(rng.random((B, D)) < 0.8, am[:, :D], rng.integers(0, V, (B, D)))
+        drafts = drafts.astype(np.int32)
+        if dt == "bf16":
+            tgt = wl.f32_to_bf16_bits(tgt)
+        acc, em = llima_amd.verify_greedy(_t(tgt, gpu), _t(drafts, gpu))
+        eacc, eem = oracle.verify_greedy(tgt, drafts)
+        assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
+
+
+def test_verify_greedy_reference_vectors(gpu, oracle):
+    import json, os
+    import llima_amd
+    _say("verify_greedy golden")
+    with open(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")) as f:
+        v = json.load(f)
+    for case in v["resolve_draft_tokens"]:
+        drafts, targets = case["drafts"], case["targets"]
+        D = len(drafts)
+        targets = targets + [0] * (D + 1 - len(targets))
+        logits = np.zeros((1, D + 1, 64), np.float32)
+        for k, t in enumerate(targets):
+            logits[0, k, t] = 1.0
+        acc, em = llima_amd.verify_greedy(_t(logits, gpu), _t(np.array(drafts, np.int32).reshape(1, D), gpu))
+        exp = case["expected"]
+        assert int(_np(acc)[0]) == sum(1 for _, a in exp if a)
+        assert _np(em)[0, :len(exp)].tolist() == [t for t, _ in exp]
+
+
+def test_verify_tree_parity(gpu, oracle):
+    import llima_amd
+    _say("verify_tree")
+    rng = np.random.default_rng(12)
+    K, V = 16, 128256
+    for trial in range(4):
+        logits = rng.normal(0, 2, (K, V)).astype(np.float32)
+        row_tok = oracle.argmax(logits, mode=1)[0]
+        P, L = 10, 5
+        ri = rng.integers(-1, K, size=(P, L)).astype(np.int32)
+        gathered = oracle.tree_gather(row_tok, ri)
+        cand = rng.integers(0, V, size=(P, L)).astype(np.int32)
+        # make some paths match the gathered target tokens
+        for p in range(P):
+            m = rng.integers(0, L)
+            cand[p, 1:m + 1] = gathered[p, :m]
+        cand[rng.random((P, L)) < 0.05] = -1
+        exp = oracle.evaluate_posterior(gathered, cand)
+        got = llima_amd.verify_tree(_t(logits, gpu), _t(ri, gpu), _t(cand, gpu))
+        assert got == exp, (trial, got, exp)
+
+
+@pytest.mark.parametrize("B,D,V", [(16, 7, 128256), (5, 3, 1000), (2, 0, 4096), (3, 6, 262144)])
+def test_verify_rejection_parity(gpu, oracle, B, D, V):
+    import llima_amd
+    _say("verify_rejection", B, D, V)
+    w = wl.speculative(B=B, D=D, V=V, seed=1004 + V)
+    acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
+                                         _t(w["draft_ids"], gpu), _t(w["u_accept"], gpu),
+                                         _t(w["u_resample"], gpu))
+    eacc, eem = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
+                                        w["u_resample"])
+    assert (_np(acc) == eacc).all(), (_np(acc), eacc)
+    assert (_np(em) == eem).all()
+
+
+def test_verify_rejection_edges(gpu, oracle):
+    import llima_amd
+    _say("verify_rejection edges")
+    rng = np.random.default_rng(3)
+    B, D, V = 6, 4, 3000
+    tgt = rng.normal(0, 3, (B, D + 1, V)).astype(np.float32)
+    drf = tgt[:, :D].copy()
+    drf[1] += rng.normal(0, 3, (D, V)).astype(np.float32)
+    drf[2, 0, :] = -np.inf; drf[2, 0, 5] = 0.0            # one-hot draft row
+    tgt[3, 1, :] = -np.inf                                  # degenerate target row
+    tgt[4, 0, 100:200] = np.nan
+    ids = rng.integers(0, V, (B, D)).astype(np.int32)
+    ids[5, 2] = V + 10                                      # out-of-range draft id
+    ids[2, 0] = 5
+    ua = rng.random((B, D)).astype(np.float32)
+    ur = rng.random(B).astype(np.float32)
+    acc, em = llima_amd.verify_rejection(_t(tgt, gpu), _t(drf, gpu), _t(ids, gpu), _t(ua, gpu),
+                                         _t(ur, gpu))
+    eacc, eem = oracle.verify_rejection(tgt, drf, ids, ua, ur)
+    assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
+    assert eacc[0] == D                                     # identical rows accept every draft
