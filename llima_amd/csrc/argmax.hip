@@ -27,10 +27,15 @@
 
 namespace llima {
 
+// Workspace: one 32-byte slot per row index; the completion counter of
+// verification group g lives in slot g, so the layout never depends on the
+// call's shape and a workspace can be reused for any shape.
 struct ArgmaxRowWs {
     uint64_t best;
     uint32_t done;
     int32_t token;
+    uint32_t group_done;
+    uint32_t pad[3];
 };
 
 enum { EPI_NONE = 0, EPI_CHAIN = 1, EPI_TREE = 2 };
@@ -41,7 +46,6 @@ struct ArgmaxParams {
     int32_t* out_ids;
     float* out_vals;
     ArgmaxRowWs* ws;
-    uint32_t* group_done;          // per sequence (chain) or one (tree)
     int32_t B, V, S, split_dim, mode, vec_ok;
     // epilogues
     int32_t epi, D;                // chain: rows per sequence = D + 1
@@ -101,16 +105,14 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
 
     // Splits whose first value is NaN are invisible (argmax_bf16 starts its
     // running maximum at values[0]).  Rare: detected per chunk, handled slowly.
-    if (threadIdx.x == 0) {
-        uint32_t bad = 0;
-        if (P.mode != LLIMA_ARGMAX_NEG_INF) {
-            const int s_lo = split_of(c0, V, sd, P.mode), s_hi = split_of(c1 - 1, V, sd, P.mode);
-            for (int s = s_lo; s <= s_hi && s - s_lo < 32; ++s) {
-                float f = ld1<TL>(rowp, split_begin(s, V, sd, P.mode));
-                if (f != f) bad |= 1u << (s - s_lo);
-            }
+    if (threadIdx.x == 0) bad_splits = 0;
+    __syncthreads();
+    if (P.mode != LLIMA_ARGMAX_NEG_INF) {
+        const int s_lo = split_of(c0, V, sd, P.mode), s_hi = split_of(c1 - 1, V, sd, P.mode);
+        for (int s = s_lo + (int)threadIdx.x; s <= s_hi; s += LLIMA_WG) {
+            const float f = ld1<TL>(rowp, split_begin(s, V, sd, P.mode));
+            if (f != f) bad_splits = 1u;
         }
-        bad_splits = bad;
     }
     __syncthreads();
     const uint32_t bad = bad_splits;
@@ -145,11 +147,11 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
                 if (t[e] > best) { best = t[e]; bidx = (uint32_t)(i0 + e); }
         }
     } else {
-        const int s_lo = split_of(c0, V, sd, P.mode);
+        // element-wise: skip values whose split starts with NaN
         for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) {
-            const int s = split_of(i, V, sd, P.mode);
-            if (s - s_lo < 32 && ((bad >> (s - s_lo)) & 1u)) continue;
-            float x = ld1<TL>(rowp, i);
+            const float f = ld1<TL>(rowp, split_begin(split_of(i, V, sd, P.mode), V, sd, P.mode));
+            if (f != f) continue;
+            const float x = ld1<TL>(rowp, i);
             if (x > best) { best = x; bidx = (uint32_t)i; }
         }
     }
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
     // ---- verification epilogues: the last row of the group resolves it
     const uint32_t grp = P.epi == EPI_CHAIN ? row / (uint32_t)(P.D + 1) : 0u;
     const uint32_t grp_rows = P.epi == EPI_CHAIN ? (uint32_t)(P.D + 1) : (uint32_t)P.B;
-    if (!arrive_last(&P.group_done[grp], grp_rows, &flag)) return;
+    if (!arrive_last(&P.ws[grp].group_done, grp_rows, &flag)) return;
     if (threadIdx.x != 0) return;
     if (P.epi == EPI_CHAIN) {
         const int D = P.D;
@@ -289,7 +291,7 @@ extern "C" int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_
 extern "C" size_t llima_verify_greedy_workspace_bytes(int32_t B, int32_t D, int32_t V,
                                                       int32_t dtype) {
     if (B <= 0 || D < 0) return 0;
-    return llima_argmax_workspace_bytes(B * (D + 1), V, dtype) + align256((size_t)B * 4);
+    return llima_argmax_workspace_bytes(B * (D + 1), V, dtype);
 }
 
 extern "C" int llima_verify_greedy(const void* target_logits, int32_t dtype, int32_t B, int32_t D,
@@ -306,7 +308,6 @@ extern "C" int llima_verify_greedy(const void* target_logits, int32_t dtype, int
     P.logits = target_logits;
     P.row_stride = V;
     P.ws = (ArgmaxRowWs*)workspace;
-    P.group_done = (uint32_t*)((char*)workspace + llima_argmax_workspace_bytes(B * (D + 1), V, dtype));
     P.B = B * (D + 1); P.V = V; P.split_dim = 0; P.mode = LLIMA_ARGMAX_SPLIT_FIRST;
     P.epi = EPI_CHAIN; P.D = D;
     P.draft_ids = draft_ids; P.accepted_len = accepted_len; P.emitted = emitted;
@@ -315,7 +316,7 @@ extern "C" int llima_verify_greedy(const void* target_logits, int32_t dtype, int
 
 extern "C" size_t llima_verify_tree_workspace_bytes(int32_t K, int32_t V, int32_t dtype) {
     if (K <= 0) return 0;
-    return llima_argmax_workspace_bytes(K, V, dtype) + 256;
+    return llima_argmax_workspace_bytes(K, V, dtype);
 }
 
 extern "C" int llima_verify_tree(const void* tree_logits, int32_t dtype, int32_t K, int32_t V,
@@ -331,7 +332,6 @@ extern "C" int llima_verify_tree(const void* tree_logits, int32_t dtype, int32_t
     P.logits = tree_logits;
     P.row_stride = V;
     P.ws = (ArgmaxRowWs*)workspace;
-    P.group_done = (uint32_t*)((char*)workspace + llima_argmax_workspace_bytes(K, V, dtype));
     // The EAGLE3 verify argmax starts from -inf (language_model_eagle3.cpp:491-521).
     P.B = K; P.V = V; P.split_dim = 0; P.mode = LLIMA_ARGMAX_NEG_INF;
     P.epi = EPI_TREE;

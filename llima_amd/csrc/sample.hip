@@ -48,6 +48,12 @@ struct RowCtl {
     uint64_t pad;
 };
 
+// Workspace: one fixed-size slot per row index, [RowCtl | SAMPLE_RCAP candidates],
+// so the position of a row's control words never depends on B or V and a
+// workspace can be reused for any shape (control words are left zero).
+#define SAMPLE_CTL_BYTES 256
+#define SAMPLE_SLOT_BYTES (SAMPLE_CTL_BYTES + SAMPLE_RCAP * 8)
+
 struct SampleParams {
     const void* logits;
     int64_t row_stride;
@@ -59,8 +65,7 @@ struct SampleParams {
     int32_t* out_ids;
     float* out_probs;
     uint32_t* out_keep;
-    RowCtl* ctl;
-    uint64_t* cand;      // [B][SAMPLE_RCAP] (value bits << 32 | id)
+    char* ws;            // B slots of SAMPLE_SLOT_BYTES
     int32_t B, V, H_max, S;
     int32_t vec_ok;
 };
@@ -280,7 +285,9 @@ __device__ __forceinline__ void write_keep(const SampleParams& P, int row, Visit
     for (int i = threadIdx.x; i < nw; i += LLIMA_WG) km[i] = 0;
     __threadfence_block();
     __syncthreads();
-    visit([&](uint32_t id) { atomicOr(&km[id >> 5], 1u << (id & 31u)); });
+    visit([&](uint32_t id) {
+        if (id < (uint32_t)P.V) atomicOr(&km[id >> 5], 1u << (id & 31u));
+    });
     __syncthreads();
 }
 
@@ -437,7 +444,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
     // ---- load candidates into registers: slot j of thread t is candidate t + 256 j
     uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
     float xs[SAMPLE_SLOTS];
-    const uint64_t* src = P.cand + (size_t)row * SAMPLE_RCAP;
+    const uint64_t* src = (const uint64_t*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES + SAMPLE_CTL_BYTES);
     uint32_t kmax = 0;
 #pragma unroll
     for (int j = 0; j < SAMPLE_SLOTS; ++j) {
@@ -545,7 +552,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_kernel(SampleParams P) {
     const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
     const int nw = (V + 31) >> 5;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
-    RowCtl* ctl = P.ctl + row;
+    RowCtl* ctl = (RowCtl*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES);
     const float NEG_INF = -__builtin_inff();
 
     if (threadIdx.x == 0) { sh.n_pre = 0; sh.flags = 0; sh.n_exc = 0; }
@@ -689,7 +696,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_kernel(SampleParams P) {
         __syncthreads();
         const uint32_t base = sh.base;
         if (base != 0xFFFFFFFFu) {
-            uint64_t* dst = P.cand + (size_t)row * SAMPLE_RCAP + base;
+            uint64_t* dst = (uint64_t*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES + SAMPLE_CTL_BYTES) + base;
             for (uint32_t j = threadIdx.x; j < n_pre; j += LLIMA_WG) dst[j] = sh.s.pre[j];
         }
     }
@@ -736,7 +743,7 @@ using namespace llima;
 extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
     (void)V; (void)dtype;
     if (B <= 0) return 0;
-    return (size_t)B * sizeof(RowCtl) + (size_t)B * SAMPLE_RCAP * sizeof(uint64_t);
+    return (size_t)B * SAMPLE_SLOT_BYTES;
 }
 
 extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V,
@@ -772,8 +779,7 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.out_ids = out_ids;
     P.out_probs = out_probs;
     P.out_keep = out_keep;
-    P.ctl = (RowCtl*)workspace;
-    P.cand = (uint64_t*)((char*)workspace + (size_t)B * sizeof(RowCtl));
+    P.ws = (char*)workspace;
     P.B = B;
     P.V = V;
     P.H_max = history ? H_max : 0;

@@ -31,15 +31,22 @@ namespace llima {
 
 enum { JOB_RESIDUAL = 0, JOB_BONUS = 1 };
 
-struct VerifyWs {
-    uint32_t* row_max;    // [NR] key of the row maximum (0 = no value)
-    uint64_t* row_z;      // [NR]
-    uint64_t* row_wx;     // [NR] weight of the draft token in rows k < D
-    uint64_t* chunk_sum;  // [NR][S]
-    uint64_t* res_sum;    // [B][S]
-    uint32_t* seq_done2;  // [B]
-    uint32_t* seq_done3;  // [B]
-    int32_t* seq_job;     // [B][2] {kind, k}
+// Workspace: one fixed-size slot per row index r (target rows first, then
+// draft rows).  Slot b also carries sequence b's counters, job and residual
+// chunk sums.  Positions never depend on the call's shape, so a workspace can
+// be reused for any shape; the control words are left zero after every call.
+#define VR_SMAX 512                       // chunks per row: V <= 2^22
+struct VRowSlot {
+    uint32_t row_max;     // key of the row maximum (0 = no value)
+    uint32_t seq_done2;   // sequence counters (slot b)
+    uint32_t seq_done3;
+    int32_t job_kind;
+    uint64_t row_z;
+    uint64_t row_wx;      // weight of the draft token in rows k < D
+    int32_t job_k;
+    int32_t pad[7];
+    uint64_t chunk_sum[VR_SMAX];
+    uint64_t res_sum[VR_SMAX];
 };
 
 struct VerifyParams {
@@ -50,7 +57,7 @@ struct VerifyParams {
     const float* u_resample;
     int32_t* accepted_len;
     int32_t* emitted;
-    VerifyWs ws;
+    VRowSlot* ws;
     int32_t B, D, V, S, NR;
 };
 
@@ -87,10 +94,6 @@ __device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, fl
         }
     }
 }
-__device__ __forceinline__ int elem_index(int c0, int j, int e) {
-    return c0 + (j >> 2) * (LLIMA_WG * 4) + (int)threadIdx.x * 4 + (j & 3) * 0 + e;
-}
-
 // Weight of a value given its row maximum key (0 when the row has no value).
 __device__ __forceinline__ uint64_t row_weight(float x, uint32_t mkey) {
     if (mkey <= LLIMA_KEY_NEG_INF) return 0;
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
         m = k > m ? k : m;
     }
     m = block_max_u32(m, bs);
-    if (threadIdx.x == 0 && m) atomicMax(&P.ws.row_max[r], m);
+    if (threadIdx.x == 0 && m) atomicMax(&P.ws[r].row_max, m);
 }
 
 __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
-    const uint32_t mkey = P.ws.row_max[r];
+    const uint32_t mkey = P.ws[r].row_max;
     float v[VR_E];
     load_chunk(rowp, c0, c1, v);
     uint64_t s = 0;
@@ -128,15 +131,15 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     s = block_sum_u64(s, bs);
     const int b = seq_of(P, r), k = pos_of(P, r);
     if (threadIdx.x == 0) {
-        P.ws.chunk_sum[(size_t)r * P.S + c] = s;
-        if (s) atomicAdd((unsigned long long*)&P.ws.row_z[r], (unsigned long long)s);
+        P.ws[r].chunk_sum[c] = s;
+        if (s) atomicAdd((unsigned long long*)&P.ws[r].row_z, (unsigned long long)s);
         if (k < P.D) {
             const int x = P.draft_ids[b * P.D + k];
-            if (x >= c0 && x < c1) P.ws.row_wx[r] = row_weight(rowp[x], mkey);
+            if (x >= c0 && x < c1) P.ws[r].row_wx = row_weight(rowp[x], mkey);
         }
     }
     const uint32_t expected = (uint32_t)(2 * P.D + 1) * (uint32_t)P.S;
-    if (!arrive_last(&P.ws.seq_done2[b], expected, &flag)) return;
+    if (!arrive_last(&P.ws[b].seq_done2, expected, &flag)) return;
     if (threadIdx.x != 0) return;
 
     // ---- acceptance scan of sequence b
@@ -145,10 +148,10 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     for (; acc < P.D; ++acc) {
         const int x = P.draft_ids[b * P.D + acc];
         const int rt = trow(P, b, acc), rd = drow(P, b, acc);
-        const uint64_t zt = load_coherent(&P.ws.row_z[rt]), zd = load_coherent(&P.ws.row_z[rd]);
+        const uint64_t zt = load_coherent(&P.ws[rt].row_z), zd = load_coherent(&P.ws[rd].row_z);
         bool ok = false;
         if (x >= 0 && x < P.V && zt > 0) {
-            const uint64_t wt = load_coherent(&P.ws.row_wx[rt]), wd = load_coherent(&P.ws.row_wx[rd]);
+            const uint64_t wt = load_coherent(&P.ws[rt].row_wx), wd = load_coherent(&P.ws[rd].row_wx);
             const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
             const llima_u128 rhs = (llima_u128)uniform32(P.u_accept[b * P.D + acc]) * ((llima_u128)wd * zt);
             ok = lhs >= rhs;
@@ -158,8 +161,8 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     }
     for (int j = acc; j <= P.D; ++j) em[j] = -1;
     P.accepted_len[b] = acc;
-    P.ws.seq_job[2 * b] = acc < P.D ? JOB_RESIDUAL : JOB_BONUS;
-    P.ws.seq_job[2 * b + 1] = acc;
+    P.ws[b].job_kind = acc < P.D ? JOB_RESIDUAL : JOB_BONUS;
+    P.ws[b].job_k = acc;
 }
 
 __device__ __forceinline__ int bitlen64(uint64_t z) { return z ? 64 - __clzll((long long)z) : 0; }
@@ -188,32 +191,34 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
     __shared__ uint64_t s_before, s_target;
     __shared__ bool s_residual;
     const int b = blockIdx.x / P.S, c = blockIdx.x % P.S;
-    const int kind = P.ws.seq_job[2 * b], k = P.ws.seq_job[2 * b + 1];
+    int kind = P.ws[b].job_kind, k = P.ws[b].job_k;
+    // a job is only ever {RESIDUAL, k < D} or {BONUS, D}
+    if (!(kind == JOB_RESIDUAL && k >= 0 && k < P.D)) { kind = JOB_BONUS; k = P.D; }
     const int rt = trow(P, b, k);
     DrawCtx q;
     q.residual = kind == JOB_RESIDUAL;
     q.t = row_ptr(P, rt);
-    q.mt = P.ws.row_max[rt];
-    q.zt = P.ws.row_z[rt];
+    q.mt = P.ws[rt].row_max;
+    q.zt = P.ws[rt].row_z;
     q.d = nullptr; q.md = 0; q.zd = 0; q.shift = 0;
     if (q.residual) {
         const int rd = drow(P, b, k);
         q.d = row_ptr(P, rd);
-        q.md = P.ws.row_max[rd];
-        q.zd = P.ws.row_z[rd];
+        q.md = P.ws[rd].row_max;
+        q.zd = P.ws[rd].row_z;
         const int sh = bitlen64(q.zt) + bitlen64(q.zd) - 63;
         q.shift = sh > 0 ? sh : 0;
         const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
         uint64_t s = 0;
         for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) s += draw_weight(q, i);
         s = block_sum_u64(s, bs);
-        if (threadIdx.x == 0) P.ws.res_sum[(size_t)b * P.S + c] = s;
+        if (threadIdx.x == 0) P.ws[b].res_sum[c] = s;
     }
-    if (!arrive_last(&P.ws.seq_done3[b], (uint32_t)P.S, &flag)) return;
+    if (!arrive_last(&P.ws[b].seq_done3, (uint32_t)P.S, &flag)) return;
 
     // ---- last workgroup of the sequence: locate the chunk, then the id
     if (threadIdx.x == 0) {
-        const uint64_t* sums = P.ws.res_sum + (size_t)b * P.S;
+        const uint64_t* sums = P.ws[b].res_sum;
         uint64_t total = 0;
         bool residual = q.residual;
         if (residual) {
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
             if (total == 0) residual = false;          // p_t == p_d: draw from p_t
         }
         if (!residual) {
-            sums = P.ws.chunk_sum + (size_t)rt * P.S;
+            sums = P.ws[rt].chunk_sum;
             total = q.zt;
         }
         int32_t chunk = -1;
@@ -263,36 +268,13 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
         // leave the workspace zeroed for the next call
         for (int j = 0; j <= P.D; ++j) {
             const int r1 = trow(P, b, j);
-            P.ws.row_max[r1] = 0; P.ws.row_z[r1] = 0; P.ws.row_wx[r1] = 0;
+            P.ws[r1].row_max = 0; P.ws[r1].row_z = 0; P.ws[r1].row_wx = 0;
             if (j < P.D) {
                 const int r2 = drow(P, b, j);
-                P.ws.row_max[r2] = 0; P.ws.row_z[r2] = 0; P.ws.row_wx[r2] = 0;
+                P.ws[r2].row_max = 0; P.ws[r2].row_z = 0; P.ws[r2].row_wx = 0;
             }
         }
     }
-}
-
-static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-static VerifyWs carve(void* base, int B, int D, int S) {
-    const int NR = B * (2 * D + 1);
-    char* p = (char*)base;
-    VerifyWs w;
-    w.row_max = (uint32_t*)p; p += al256((size_t)NR * 4);
-    w.row_z = (uint64_t*)p; p += al256((size_t)NR * 8);
-    w.row_wx = (uint64_t*)p; p += al256((size_t)NR * 8);
-    w.chunk_sum = (uint64_t*)p; p += al256((size_t)NR * S * 8);
-    w.res_sum = (uint64_t*)p; p += al256((size_t)B * S * 8);
-    w.seq_done2 = (uint32_t*)p; p += al256((size_t)B * 4);
-    w.seq_done3 = (uint32_t*)p; p += al256((size_t)B * 4);
-    w.seq_job = (int32_t*)p; p += al256((size_t)B * 8);
-    return w;
-}
-
-static size_t carve_bytes(int B, int D, int S) {
-    const size_t NR = (size_t)B * (2 * D + 1);
-    return al256(NR * 4) + 2 * al256(NR * 8) + al256(NR * S * 8) + al256((size_t)B * S * 8) +
-           2 * al256((size_t)B * 4) + al256((size_t)B * 8);
 }
 
 }  // namespace llima
@@ -301,8 +283,7 @@ using namespace llima;
 
 extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, int32_t V) {
     if (B <= 0 || D < 0 || V <= 0) return 0;
-    const int S = (V + VR_CHUNK - 1) / VR_CHUNK;
-    return carve_bytes(B, D, S);
+    return (size_t)B * (2 * D + 1) * sizeof(VRowSlot);
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -325,7 +306,7 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.B = B; P.D = D; P.V = V;
     P.S = (V + VR_CHUNK - 1) / VR_CHUNK;
     P.NR = B * (2 * D + 1);
-    P.ws = carve(workspace, B, D, P.S);
+    P.ws = (VRowSlot*)workspace;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
     hipLaunchKernelGGL(vr_rowmax, dim3(g12), dim3(LLIMA_WG), 0, st, P);

@@ -325,3 +325,30 @@ def test_verify_rejection_edges(gpu, oracle):
     eacc, eem = oracle.verify_rejection(tgt, drf, ids, ua, ur)
     assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
     assert eacc[0] == D                                     # identical rows accept every draft
+
+
+def test_workspace_reuse_across_shapes(gpu, oracle):
+    """One workspace buffer per entry point serves calls of any shape, in any
+    order (per-row workspace slots; control words left zero by every call)."""
+    import llima_amd
+    _say("workspace reuse across shapes")
+    rng = np.random.default_rng(77)
+    for B, V in [(16, 30000), (4, 30000), (16, 9000), (1, 70000), (12, 30000)]:
+        x = rng.normal(0, 2, (B, V)).astype(np.float32)
+        h = rng.integers(0, V, size=(B, 100)).astype(np.int32)
+        u = rng.random(B).astype(np.float32)
+        _sample_both(gpu, oracle, x, u, dict(temperature=0.9, top_k=30, top_p=0.9,
+                                             repetition_penalty=1.2), history=h)
+    for B, D, V in [(6, 5, 3000), (2, 0, 4096), (3, 2, 9000), (6, 6, 3000)]:
+        w = wl.speculative(B=B, D=D, V=V, seed=B + D)
+        acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
+                                             _t(w["draft_ids"], gpu), _t(w["u_accept"], gpu),
+                                             _t(w["u_resample"], gpu))
+        eacc, eem = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"],
+                                            w["u_accept"], w["u_resample"])
+        assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
+        tgt = w["target"]
+        dr = tgt[:, :D].argmax(-1).astype(np.int32)
+        acc, em = llima_amd.verify_greedy(_t(tgt, gpu), _t(dr, gpu))
+        eacc, eem = oracle.verify_greedy(tgt, dr)
+        assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
