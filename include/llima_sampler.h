@@ -8,9 +8,12 @@
  * launch errors.  No entry point allocates memory and no C++ exception
  * crosses this boundary.
  *
- * Workspace contract: the workspace must be zero-filled before its first use
- * (llima_workspace_init does that) and every call leaves it zero-filled again.
- * Calls that share one workspace must be ordered (same stream, or synchronised).
+ * Workspace contract: a workspace is scratch of at least the size the matching
+ * *_workspace_bytes function returns; no state survives a call, so it needs no
+ * initialisation and any large-enough buffer may be reused for any shape.  Calls
+ * that share one workspace must be ordered (same stream, or synchronised).
+ * Each entry point launches a fixed sequence of kernels with no host
+ * synchronisation and no memset, so it can be captured in a HIP graph.
  *
  * Reference interfaces replaced (sima-neat/llima, paths relative to that repo).
  * The reference selects tokens on the host CPU through free functions and
@@ -98,7 +101,8 @@ typedef struct llima_sampler_config {
     const float* frequency_penalty_rows;
 } llima_sampler_config;
 
-/* Zero-fills a workspace on the stream (hipMemsetAsync). */
+/* Zero-fills a workspace on the stream (hipMemsetAsync); optional, kept for
+ * callers that want deterministic scratch contents. */
 int llima_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Greedy selection over B rows of V logits (dtype LLIMA_F32 or LLIMA_BF16, row

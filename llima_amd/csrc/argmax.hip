@@ -11,32 +11,25 @@
 //                               sima_lmm/devkit/cpp/language_model_eagle3.cpp:551-567,
 //                               sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195
 //
-// Layout: a [rows][V] logits matrix is cut into B x S workgroups of 256*E
-// values; each workgroup streams its chunk with 16-byte loads, keeps a running
-// (value, first index) per thread with a strict '>' (so NaN never wins and the
-// first maximum is kept, as the reference's scalar loop), reduces the chunk to a
-// 64-bit key (value key << 32 | ~index) and merges it into the row with one
-// device-scope atomicMax.  The last workgroup of a row (completion counter)
-// writes the result; with the verification epilogues the last row of a
-// sequence (or of the tree) also resolves the drafts.  The reference's early
-// exit after the first mismatching row (language_model.cpp:3679-3684) is a host
-// latency optimisation; every row is computed here and the emitted tokens are
-// identical.
+// Two launches, no atomics or fences between workgroups.  argmax_sweep cuts a
+// [rows][V] logits matrix into rows x S workgroups of 256*E values; each streams
+// its chunk with 16-byte loads, keeps a running (value, first index) per thread
+// with a strict '>' (so NaN never wins and the first maximum is kept, as the
+// reference's scalar loop) and writes the chunk's 64-bit key
+// (value key << 32 | ~index) to its own workspace slot.  argmax_finish reduces
+// the S keys of each row with one wavefront per row and writes the result; with
+// the verification epilogues one workgroup takes a whole sequence (or the whole
+// tree) and resolves its drafts.  The reference's early exit after the first
+// mismatching row (language_model.cpp:3679-3684) is a host latency
+// optimisation; every row is computed here and the emitted tokens are identical.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
 namespace llima {
 
-// Workspace: one 32-byte slot per row index; the completion counter of
-// verification group g lives in slot g, so the layout never depends on the
-// call's shape and a workspace can be reused for any shape.
-struct ArgmaxRowWs {
-    uint64_t best;
-    uint32_t done;
-    int32_t token;
-    uint32_t group_done;
-    uint32_t pad[3];
-};
+// Workspace: [rows][S] chunk keys (uint64).  Nothing persists between calls.
+#define ARGMAX_MIN_CHUNK 2048
+#define ARGMAX_MAX_GROUP 1024       // rows of one sequence / of one tree
 
 enum { EPI_NONE = 0, EPI_CHAIN = 1, EPI_TREE = 2 };
 
@@ -45,7 +38,7 @@ struct ArgmaxParams {
     int64_t row_stride;
     int32_t* out_ids;
     float* out_vals;
-    ArgmaxRowWs* ws;
+    uint64_t* keys;                // [rows][S]
     int32_t B, V, S, split_dim, mode, vec_ok;
     // epilogues
     int32_t epi, D;                // chain: rows per sequence = D + 1
@@ -87,12 +80,12 @@ __device__ __forceinline__ int64_t split_begin(int s, int V, int sd, int mode) {
 }
 
 template <typename TL, int E>
-__global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
+__global__ __launch_bounds__(LLIMA_WG) void argmax_sweep(ArgmaxParams P) {
     constexpr int EPL = 16 / sizeof(TL);
     constexpr int NL = E / EPL;
     constexpr int CHUNK = LLIMA_WG * E;
     __shared__ BlockScratch bs;
-    __shared__ uint32_t flag, bad_splits;
+    __shared__ uint32_t bad_splits;
 
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
@@ -125,11 +118,11 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
             const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
             float t[EPL];
             if (P.vec_ok && i0 + EPL <= c1) {
+                const llima_u32x4 q = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
                 if constexpr (sizeof(TL) == 4) {
-                    float4 q = *(const float4*)(rowp + i0);
-                    t[0] = q.x; t[1] = q.y; t[2] = q.z; t[3] = q.w;
+                    t[0] = __uint_as_float(q.x); t[1] = __uint_as_float(q.y);
+                    t[2] = __uint_as_float(q.z); t[3] = __uint_as_float(q.w);
                 } else {
-                    uint4 q = *(const uint4*)(rowp + i0);
                     const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -155,43 +148,66 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
             if (x > best) { best = x; bidx = (uint32_t)i; }
         }
     }
-    uint64_t key = block_max_u64(pack_best(best, bidx), bs);
-    ArgmaxRowWs* rw = P.ws + row;
-    if (threadIdx.x == 0 && key) atomicMax((unsigned long long*)&rw->best, (unsigned long long)key);
-    if (!arrive_last(&rw->done, (uint32_t)P.S, &flag)) return;
+    const uint64_t key = block_max_u64(pack_best(best, bidx), bs);
+    if (threadIdx.x == 0) P.keys[(size_t)row * P.S + chunk] = key;
+}
 
-    // ---- row result
-    if (threadIdx.x == 0) {
-        const uint64_t k = load_coherent(&rw->best);
-        rw->best = 0;
-        int32_t id = 0;
-        float val = -__builtin_inff();
-        if (k) { id = (int32_t)(~(uint32_t)k); val = ld1<TL>(rowp, id); }
-        if (P.mode == LLIMA_ARGMAX_QUARTERS) {
-            const float v0 = ld1<TL>(rowp, 0);
-            if (v0 != v0) { id = 0; val = v0; }
-        }
-        if (P.out_ids) P.out_ids[row] = id;
-        if (P.out_vals) P.out_vals[row] = val;
-        rw->token = id;
+// Row result from its S chunk keys (one wavefront).  An all -inf row gives id 0.
+template <typename TL>
+__device__ __forceinline__ int32_t row_result(const ArgmaxParams& P, int row, float* val) {
+    const uint64_t* k = P.keys + (size_t)row * P.S;
+    uint64_t best = 0;
+    for (int i = (int)lane_id(); i < P.S; i += 64) best = k[i] > best ? k[i] : best;
+    best = wave_max_u64(best);
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    int32_t id = 0;
+    float v = -__builtin_inff();
+    if (best) { id = (int32_t)(~(uint32_t)best); v = ld1<TL>(rowp, id); }
+    if (P.mode == LLIMA_ARGMAX_QUARTERS) {
+        // merged from (values[0], 0): a NaN there is kept
+        const float v0 = ld1<TL>(rowp, 0);
+        if (v0 != v0) { id = 0; v = v0; }
     }
-    if (P.epi == EPI_NONE) return;
+    *val = v;
+    return id;
+}
 
-    // ---- verification epilogues: the last row of the group resolves it
-    const uint32_t grp = P.epi == EPI_CHAIN ? row / (uint32_t)(P.D + 1) : 0u;
-    const uint32_t grp_rows = P.epi == EPI_CHAIN ? (uint32_t)(P.D + 1) : (uint32_t)P.B;
-    if (!arrive_last(&P.ws[grp].group_done, grp_rows, &flag)) return;
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void argmax_finish(ArgmaxParams P) {
+    __shared__ int32_t tok[ARGMAX_MAX_GROUP];
+    const int wave = (int)(threadIdx.x >> 6);
+    if (P.epi == EPI_NONE) {
+        const int row = (int)blockIdx.x * LLIMA_WAVES + wave;
+        if (row >= P.B) return;
+        float v;
+        const int32_t id = row_result<TL>(P, row, &v);
+        if (lane_id() == 0) {
+            if (P.out_ids) P.out_ids[row] = id;
+            if (P.out_vals) P.out_vals[row] = v;
+        }
+        return;
+    }
+    // one workgroup per sequence (chain) or for the whole tree
+    const int nrows = P.epi == EPI_CHAIN ? P.D + 1 : P.B;
+    const int row0 = P.epi == EPI_CHAIN ? (int)blockIdx.x * nrows : 0;
+    for (int r = wave; r < nrows; r += LLIMA_WAVES) {
+        float v;
+        const int32_t id = row_result<TL>(P, row0 + r, &v);
+        if (lane_id() == 0) tok[r] = id;
+    }
+    __syncthreads();
     if (threadIdx.x != 0) return;
     if (P.epi == EPI_CHAIN) {
-        const int D = P.D;
-        const ArgmaxRowWs* g = P.ws + (size_t)grp * (D + 1);
-        const int32_t* dr = P.draft_ids + (size_t)grp * D;
-        int32_t* em = P.emitted + (size_t)grp * (D + 1);
+        // resolve_draft_tokens: accept while the draft equals the target argmax,
+        // then emit the target token at the first mismatch (or the bonus).
+        const int D = P.D, g = (int)blockIdx.x;
+        const int32_t* dr = P.draft_ids + (size_t)g * D;
+        int32_t* em = P.emitted + (size_t)g * (D + 1);
         int acc = 0;
-        while (acc < D && dr[acc] == load_coherent(&g[acc].token)) { em[acc] = dr[acc]; ++acc; }
-        em[acc] = load_coherent(&g[acc].token);
+        while (acc < D && dr[acc] == tok[acc]) { em[acc] = dr[acc]; ++acc; }
+        em[acc] = tok[acc];
         for (int j = acc + 1; j <= D; ++j) em[j] = -1;
-        P.accepted_len[grp] = acc;
+        P.accepted_len[g] = acc;
     } else {
         // gather target tokens along each path (-1 -> last tree row), then the
         // first path with the strictly longest accepted prefix wins.
@@ -201,25 +217,25 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_kernel(ArgmaxParams P) {
             int32_t acc = 0;
             for (int i = 0; i + 1 < L; ++i) {
                 int32_t idx = P.retrieve[p * L + i];
-                if (idx < 0) idx = K - 1;
-                const int32_t arg = load_coherent(&P.ws[idx < K ? idx : K - 1].token);
+                if (idx < 0 || idx >= K) idx = K - 1;
                 const int32_t nxt = P.candidates[p * L + i + 1];
-                if (nxt < 0 || arg != nxt) break;
+                if (nxt < 0 || tok[idx] != nxt) break;
                 ++acc;
             }
             if (acc > max_acc) { max_acc = acc; best_c = p; }
         }
         int32_t idx = P.retrieve[best_c * L + max_acc];
-        if (idx < 0) idx = K - 1;
+        if (idx < 0 || idx >= K) idx = K - 1;
         P.tree_out[0] = best_c;
         P.tree_out[1] = max_acc;
-        P.tree_out[2] = load_coherent(&P.ws[idx < K ? idx : K - 1].token);
+        P.tree_out[2] = tok[idx];
     }
 }
 
 struct ATile { int E, S; };
 static ATile argmax_tile(int B, int V, int dtype) {
-    int E = dtype == LLIMA_F32 ? 32 : 64;
+    // 16 KB per workgroup streams best on MI355X; smaller when the grid is small.
+    int E = dtype == LLIMA_F32 ? 16 : 32;
     auto S_of = [&](int e) { return (V + LLIMA_WG * e - 1) / (LLIMA_WG * e); };
     while (E > 8 && (int64_t)B * S_of(E) < 1024) E /= 2;
     return {E, S_of(E)};
@@ -227,8 +243,11 @@ static ATile argmax_tile(int B, int V, int dtype) {
 
 template <typename TL, int E>
 static hipError_t launch_argmax(const ArgmaxParams& P, hipStream_t st) {
-    hipLaunchKernelGGL((argmax_kernel<TL, E>), dim3((uint32_t)P.B * (uint32_t)P.S), dim3(LLIMA_WG),
+    hipLaunchKernelGGL((argmax_sweep<TL, E>), dim3((uint32_t)P.B * (uint32_t)P.S), dim3(LLIMA_WG),
                        0, st, P);
+    const uint32_t nfin = P.epi == EPI_NONE ? (uint32_t)(P.B + LLIMA_WAVES - 1) / LLIMA_WAVES
+                        : P.epi == EPI_CHAIN ? (uint32_t)(P.B / (P.D + 1)) : 1u;
+    hipLaunchKernelGGL((argmax_finish<TL>), dim3(nfin), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError();
 }
 
@@ -262,8 +281,9 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 using namespace llima;
 
 extern "C" size_t llima_argmax_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
-    (void)V; (void)dtype;
-    return B > 0 ? align256((size_t)B * sizeof(ArgmaxRowWs)) : 0;
+    (void)dtype;
+    if (B <= 0 || V <= 0) return 0;
+    return align256((size_t)B * ((V + ARGMAX_MIN_CHUNK - 1) / ARGMAX_MIN_CHUNK) * sizeof(uint64_t));
 }
 
 extern "C" int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_t V,
@@ -282,7 +302,7 @@ extern "C" int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_
     P.row_stride = row_stride;
     P.out_ids = out_ids;
     P.out_vals = out_vals;
-    P.ws = (ArgmaxRowWs*)workspace;
+    P.keys = (uint64_t*)workspace;
     P.B = B; P.V = V; P.split_dim = split_dim; P.mode = mode;
     P.epi = EPI_NONE;
     return run_argmax(P, dtype, (hipStream_t)stream);
@@ -300,14 +320,14 @@ extern "C" int llima_verify_greedy(const void* target_logits, int32_t dtype, int
                                    void* stream) {
     if (!target_logits || !accepted_len || !emitted || (D > 0 && !draft_ids)) return LLIMA_E_INVAL;
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
-    if (B < 0 || D < 0 || V <= 0) return LLIMA_E_INVAL;
+    if (B < 0 || D < 0 || D + 1 > ARGMAX_MAX_GROUP || V <= 0) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_verify_greedy_workspace_bytes(B, D, V, dtype))
         return LLIMA_E_WORKSPACE;
     ArgmaxParams P = {};
     P.logits = target_logits;
     P.row_stride = V;
-    P.ws = (ArgmaxRowWs*)workspace;
+    P.keys = (uint64_t*)workspace;
     P.B = B * (D + 1); P.V = V; P.split_dim = 0; P.mode = LLIMA_ARGMAX_SPLIT_FIRST;
     P.epi = EPI_CHAIN; P.D = D;
     P.draft_ids = draft_ids; P.accepted_len = accepted_len; P.emitted = emitted;
@@ -325,13 +345,13 @@ extern "C" int llima_verify_tree(const void* tree_logits, int32_t dtype, int32_t
                                  size_t workspace_bytes, void* stream) {
     if (!tree_logits || !retrieve_indices || !candidates || !out) return LLIMA_E_INVAL;
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
-    if (K <= 0 || V <= 0 || n_paths <= 0 || L <= 0) return LLIMA_E_INVAL;
+    if (K <= 0 || K > ARGMAX_MAX_GROUP || V <= 0 || n_paths <= 0 || L <= 0) return LLIMA_E_INVAL;
     if (!workspace || workspace_bytes < llima_verify_tree_workspace_bytes(K, V, dtype))
         return LLIMA_E_WORKSPACE;
     ArgmaxParams P = {};
     P.logits = tree_logits;
     P.row_stride = V;
-    P.ws = (ArgmaxRowWs*)workspace;
+    P.keys = (uint64_t*)workspace;
     // The EAGLE3 verify argmax starts from -inf (language_model_eagle3.cpp:491-521).
     P.B = K; P.V = V; P.split_dim = 0; P.mode = LLIMA_ARGMAX_NEG_INF;
     P.epi = EPI_TREE;

@@ -18,6 +18,7 @@
 #define LLIMA_W_ONE (1ull << 36)
 
 typedef unsigned __int128 llima_u128;
+typedef uint32_t llima_u32x4 __attribute__((ext_vector_type(4)));   // 16-byte load unit
 
 namespace llima {
 
@@ -259,36 +260,6 @@ __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* to
     __syncthreads();
     *total = t;
     return before + inc - v;
-}
-
-// ------------------------------------------------------------------ cross-workgroup
-// Release this workgroup's global writes, then count it in; returns true in the
-// workgroup that arrives last (which then sees every other workgroup's writes).
-__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected,
-                                            uint32_t* lds_flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t last = (old == expected - 1) ? 1u : 0u;
-        if (last) {
-            // Reset for the next launch that uses this workspace.
-            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        *lds_flag = last;
-    }
-    __syncthreads();
-    bool last = *lds_flag != 0;
-    if (last) __threadfence();
-    return last;
-}
-
-// Loads that must observe other workgroups' writes made before their release:
-// bypass the per-CU vector L1.
-template <typename T>
-__device__ __forceinline__ T load_coherent(const T* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // blockIdx -> (row, chunk).  With B a multiple of 8 every chunk of a row is

@@ -1,58 +1,60 @@
 // sample.hip -- fused penalty / temperature / mask / top-k / top-p / min-p /
 // inverse-CDF sampling over [B, V] logits rows on MI355X (gfx950).
 //
-// One launch per step.  The grid is B x S workgroups; workgroup (row, chunk)
-// streams a 256*E-element chunk of its row once from HBM with 16-byte loads
-// and keeps it in registers:
-//   1. history ids of the row that fall in the chunk are counted in an LDS
-//      table (packed u16 counts); distinct ids become "exceptions" whose
-//      penalised value is computed separately, so the streaming loop only
-//      tests a count != 0 per element (no division in the hot loop);
-//   2. masked (packed-uint32 grammar bitmask, LSB first), NaN and history
-//      elements are set to -inf in registers;
-//   3. a lower bound t of the chunk's k-th largest value is found from the
-//      lane maxima (wavefront bitonic sort, min over the 4 waves) and every
-//      element >= t - |t|*2^-20 is appended to the row's candidate list;
-//   4. the last workgroup of the row to finish (device-scope counter) divides
-//      the candidates by the temperature, verifies that the bound could not
-//      have dropped a member of the top-k set, and runs three radix selects
-//      over LDS histograms on register-resident candidates: top-k threshold
-//      (count), top-p threshold (fixed-point mass), and the draw (mass by id).
-// Rows the fast path cannot prove complete (candidate overflow, very large k,
-// top-k disabled without a mask, degenerate temperatures) are finished by the
-// same last workgroup with a full-row multi-pass version of the same selects.
+// Two launches per step, with no atomics or fences between workgroups (on
+// this part, device-scope cache maintenance and same-address atomics cost far
+// more than the whole sweep):
+//
+// sample_sweep: B x S workgroups; workgroup (row, chunk) streams a 256*E chunk
+//   of its row from HBM with 16-byte loads, issued before anything else, and
+//   keeps it in registers.  While the loads are in flight it counts the row's
+//   history ids that fall in the chunk in an LDS table (packed u16 counts);
+//   distinct ids become "exceptions" whose penalised value is computed apart, so
+//   the per-element work is a count != 0 test (no division in the stream).
+//   Masked (packed-uint32 grammar bitmask, LSB first), NaN and history values
+//   become -inf.  A lower bound t of the chunk's k-th largest value comes from
+//   the lane maxima (wavefront bitonic sort, min over the 4 waves) and every
+//   value >= t - |t| 2^-20 is written, with its id, to the chunk's own slot of
+//   the workspace together with a small header.
+//
+// sample_finish: one workgroup per row gathers the candidates into LDS, divides
+//   them by the temperature, proves that the bound could not have dropped a
+//   member of the top-k set (else falls back), and runs three radix selects over
+//   LDS histograms on register-resident candidates: top-k threshold (count),
+//   top-p threshold (fixed-point mass) and the draw (mass by ascending id).
+//   Rows that the candidates cannot serve (overflow, k beyond the fast path,
+//   top-k disabled without a mask, degenerate temperatures) are finished by the
+//   same workgroup with a full-row multi-pass version of the same selects.
 //
 // The sampling semantics have no counterpart in the reference runtime, which
 // only ever takes the argmax (sima_lmm/devkit/cpp/utils.hpp:80-152,
-// sima_lmm/devkit/cpp/language_model.cpp:3689-3714); greedy rows here follow
-// that argmax (first index of the maximum) over the masked, penalised row.
+// sima_lmm/devkit/cpp/language_model.cpp:3689-3714); greedy rows follow that
+// argmax (first index of the maximum) over the masked, penalised row.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
 namespace llima {
 
-#define SAMPLE_RCAP 4096          // candidates per row (finish holds 16 per thread)
-#define SAMPLE_SLOTS (SAMPLE_RCAP / LLIMA_WG)
-#define SAMPLE_PRECAP 1024        // candidates per chunk staged in LDS
-#define SAMPLE_EXC_CAP 512        // distinct history ids per chunk
+#define SAMPLE_SLOTS 16                            // candidates per finishing thread
+#define SAMPLE_FIN_CAP (SAMPLE_SLOTS * LLIMA_WG)   // 4096
+#define SAMPLE_ROW_CAND 16384                      // candidate slots per row (all chunks)
+#define SAMPLE_PRECAP 1024                         // candidates staged in LDS per chunk
+#define SAMPLE_EXC_CAP 512                         // distinct history ids per chunk
+#define SAMPLE_MIN_CHUNK 2048                      // 256 threads x E = 8
+#define SAMPLE_SEG 8192                            // full-row path segment
 
-#define CTL_OVERFLOW 1u
-#define CTL_FILTERED 2u
+#define HDR_OVERFLOW 1u
+#define HDR_FILTERED 2u
 
-struct RowCtl {
-    uint32_t done;       // workgroups of the row that have finished the sweep
-    uint32_t count;      // candidates appended
-    uint32_t flags;      // CTL_*
-    uint32_t tmax_key;   // max over chunks of the filter bound's key
-    uint64_t greedy;     // max over chunks of (key << 32 | ~index)
-    uint64_t pad;
+// Written by every sweep workgroup (no state survives a call).
+struct ChunkHdr {
+    uint32_t count;      // candidates in this chunk's slot
+    uint32_t flags;      // HDR_*
+    uint32_t bound;      // key of the pre-filter bound (when FILTERED)
+    uint32_t pad;
+    uint64_t greedy;     // (key << 32 | ~index) of the chunk maximum
+    uint64_t pad2;
 };
-
-// Workspace: one fixed-size slot per row index, [RowCtl | SAMPLE_RCAP candidates],
-// so the position of a row's control words never depends on B or V and a
-// workspace can be reused for any shape (control words are left zero).
-#define SAMPLE_CTL_BYTES 256
-#define SAMPLE_SLOT_BYTES (SAMPLE_CTL_BYTES + SAMPLE_RCAP * 8)
 
 struct SampleParams {
     const void* logits;
@@ -65,8 +67,9 @@ struct SampleParams {
     int32_t* out_ids;
     float* out_probs;
     uint32_t* out_keep;
-    char* ws;            // B slots of SAMPLE_SLOT_BYTES
-    int32_t B, V, H_max, S;
+    ChunkHdr* hdr;       // [B][S]
+    uint64_t* cand;      // [B][S][share]  (value bits << 32 | id)
+    int32_t B, V, H_max, S, share;
     int32_t vec_ok;
 };
 
@@ -99,6 +102,8 @@ __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
     return r;
 }
 
+// HF RepetitionPenalty (score < 0 ? score * p : score / p), then OpenAI
+// frequency and presence, each one IEEE operation (no contraction).
 __device__ __forceinline__ float penalize(float l, uint32_t c, const RowCfg& cfg) {
     l = (l < 0.0f) ? l * cfg.R : l / cfg.R;
     return (l - cfg.beta * (float)c) - cfg.alpha;
@@ -108,49 +113,6 @@ __device__ __forceinline__ float penalize(float l, uint32_t c, const RowCfg& cfg
 // quotient by T can round onto the bound's quotient is filtered out.
 __device__ __forceinline__ float lower_bound_margin(float t) {
     return t - __builtin_fabsf(t) * 0x1p-20f;
-}
-
-template <int CHUNK>
-struct SampleShared {
-    struct {
-        uint32_t cnt[CHUNK / 2];              // packed u16 history counts
-        int32_t exc_id[SAMPLE_EXC_CAP];
-        float exc_val[SAMPLE_EXC_CAP];
-        uint64_t pre[SAMPLE_PRECAP];
-    } s;
-    struct {
-        uint32_t hcnt[256];
-        uint64_t hmass[256];
-    } f;
-    uint32_t n_exc, n_pre, flags, base;
-    uint32_t sel, wave_bound[LLIMA_WAVES];
-    uint64_t sel64, sel64b;
-    uint32_t last;
-    BlockScratch bs;
-};
-
-// Builds the history count table for [lo, hi) (requires hi - lo <= CHUNK).
-// When exc is set the distinct ids are listed (first occurrence wins the slot).
-template <int CHUNK>
-__device__ __forceinline__ void build_hist_table(const SampleParams& P, int row, const RowCfg& c, int lo, int hi,
-                                 uint32_t* table, SampleShared<CHUNK>& sh, bool exc) {
-    for (int i = threadIdx.x; i < CHUNK / 2; i += LLIMA_WG) table[i] = 0;
-    if (threadIdx.x == 0) sh.n_exc = 0;
-    __syncthreads();
-    const int32_t* h = P.hist + (size_t)row * P.H_max;
-    for (int j = threadIdx.x; j < c.hlen; j += LLIMA_WG) {
-        int32_t id = h[j];
-        if (id >= lo && id < hi) {
-            uint32_t off = (uint32_t)(id - lo);
-            uint32_t sh16 = (off & 1u) * 16u;
-            uint32_t old = atomicAdd(&table[off >> 1], 1u << sh16);
-            if (exc && ((old >> sh16) & 0xFFFFu) == 0) {
-                uint32_t slot = atomicAdd(&sh.n_exc, 1u);
-                if (slot < SAMPLE_EXC_CAP) sh.s.exc_id[slot] = id;
-            }
-        }
-    }
-    __syncthreads();
 }
 
 __device__ __forceinline__ uint32_t table_count(const uint32_t* table, uint32_t off) {
@@ -166,24 +128,252 @@ __device__ __forceinline__ float load_one<uint16_t>(const uint16_t* rowp, int i)
     return bf16_bits_to_f32(rowp[i]);
 }
 
+// Counts the row's history ids in [lo, lo + nslots*2) into an LDS table of
+// packed u16 counts; with exc, lists the distinct ids (first occurrence).
+__device__ __forceinline__ void count_history(const SampleParams& P, int row, int hlen, int lo,
+                                              int hi, uint32_t* table, int nwords,
+                                              int32_t* exc_id, uint32_t* n_exc) {
+    for (int i = threadIdx.x; i < nwords; i += LLIMA_WG) table[i] = 0;
+    __syncthreads();
+    const int32_t* h = P.hist + (size_t)row * P.H_max;
+    for (int j = threadIdx.x; j < hlen; j += LLIMA_WG) {
+        const int32_t id = h[j];
+        if (id >= lo && id < hi) {
+            const uint32_t off = (uint32_t)(id - lo);
+            const uint32_t sh16 = (off & 1u) * 16u;
+            const uint32_t old = atomicAdd(&table[off >> 1], 1u << sh16);
+            if (exc_id && ((old >> sh16) & 0xFFFFu) == 0) {
+                const uint32_t slot = atomicAdd(n_exc, 1u);
+                if (slot < SAMPLE_EXC_CAP) exc_id[slot] = id;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ================================================================== sweep
+template <int CHUNK>
+struct SweepShared {
+    uint32_t cnt[CHUNK / 2];
+    int32_t exc_id[SAMPLE_EXC_CAP];
+    float exc_val[SAMPLE_EXC_CAP];
+    uint64_t pre[SAMPLE_PRECAP];
+    uint32_t n_exc, n_pre;
+    uint32_t wave_bound[LLIMA_WAVES];
+    BlockScratch bs;
+};
+
+template <typename TL, int E>
+__global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
+    constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
+    constexpr int NL = E / EPL;                // loads per thread
+    constexpr int CHUNK = LLIMA_WG * E;
+    __shared__ SweepShared<CHUNK> sh;
+    const float NEG_INF = -__builtin_inff();
+
+    uint32_t row, chunk;
+    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
+    if (row >= (uint32_t)P.B) return;
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    const int V = P.V;
+    const int c0 = (int)chunk * CHUNK;
+    const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
+    const int nw = (V + 31) >> 5;
+    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
+
+    // ---- 1. issue the chunk's loads first
+    llima_u32x4 raw[NL];
+    uint32_t mbits[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        if (P.vec_ok && i0 + EPL <= c1) {
+            raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
+        } else {
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float f = (i0 + e < c1) ? load_one<TL>(rowp, i0 + e) : NEG_INF;
+                if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
+                else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+            }
+            raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
+        }
+        mbits[j] = (mrow && i0 < c1) ? (mrow[i0 >> 5] >> (i0 & 31)) : 0xFFFFFFFFu;
+    }
+    const RowCfg c = load_cfg(P, row);
+
+    // ---- 2. while they are in flight: the chunk's history counts
+    if (threadIdx.x == 0) { sh.n_exc = 0; sh.n_pre = 0; }
+    if (c.pen) count_history(P, row, c.hlen, c0, c1, sh.cnt, CHUNK / 2, sh.exc_id, &sh.n_exc);
+    else __syncthreads();
+
+    // ---- 3. values after mask / NaN / history exclusion
+    float v[E];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        float t[EPL];
+        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+        if constexpr (sizeof(TL) == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] = __uint_as_float(w4[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                t[2 * e] = __uint_as_float(w4[e] << 16);
+                t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
+            }
+        }
+        uint32_t cw[EPL / 2];
+#pragma unroll
+        for (int e = 0; e < EPL / 2; ++e) cw[e] = 0;
+        if (c.pen && i0 < c1) {
+            const uint32_t off = (uint32_t)(i0 - c0);
+#pragma unroll
+            for (int e = 0; e < EPL / 2; ++e) cw[e] = sh.cnt[(off >> 1) + e];
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float x = t[e];
+            const bool hist_hit = ((cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) != 0;
+            if (x != x || !((mbits[j] >> e) & 1u) || hist_hit) x = NEG_INF;
+            v[j * EPL + e] = x;
+        }
+    }
+
+    // ---- 4. exceptions: distinct history ids of this chunk, penalised exactly
+    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
+    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
+    uint32_t flags = n_exc > SAMPLE_EXC_CAP ? HDR_OVERFLOW : 0u;
+    float tmax = NEG_INF;
+    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
+        const int id = sh.exc_id[j];
+        float l = load_one<TL>(rowp, id);
+        if (l != l) l = NEG_INF;
+        if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) l = NEG_INF;
+        l = penalize(l, table_count(sh.cnt, (uint32_t)(id - c0)), c);
+        sh.exc_val[j] = l;
+        tmax = l > tmax ? l : tmax;
+    }
+
+    ChunkHdr* hdr = P.hdr + (size_t)row * P.S + chunk;
+    if (c.greedy) {
+        // ---- argmax: first index of the maximum
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const uint64_t kk = ((uint64_t)f32_key(v[j * EPL + e]) << 32) |
+                                    (uint64_t)(~(uint32_t)(i0 + e));
+                best = kk > best ? kk : best;
+            }
+        }
+        for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
+            const uint64_t kk = ((uint64_t)f32_key(sh.exc_val[j]) << 32) |
+                                (uint64_t)(~(uint32_t)sh.exc_id[j]);
+            best = kk > best ? kk : best;
+        }
+        best = block_max_u64(best, sh.bs);
+        if (threadIdx.x == 0) {
+            hdr->count = 0;
+            hdr->flags = flags;
+            hdr->bound = 0;
+            hdr->greedy = best;
+        }
+        return;
+    }
+
+    // ---- 5. pre-filter bound from lane maxima (any bound is safe: the finish
+    //         kernel proves completeness before trusting the candidates)
+    float g = NEG_INF;
+    uint32_t tb = 0;
+    if (c.k > 0 && c.k <= 4 * 64) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) tmax = v[e] > tmax ? v[e] : tmax;
+        const uint32_t r = (uint32_t)(c.k + 3) >> 2;          // ceil(k/4) <= 64
+        const uint32_t sorted = wave_sort_desc(f32_key(tmax));
+        const uint32_t wb = __shfl(sorted, (int)r - 1, 64);
+        if (lane_id() == 0) sh.wave_bound[threadIdx.x >> 6] = wb;
+        __syncthreads();
+        tb = sh.wave_bound[0];
+#pragma unroll
+        for (int w = 1; w < LLIMA_WAVES; ++w) tb = sh.wave_bound[w] < tb ? sh.wave_bound[w] : tb;
+        if (tb > LLIMA_KEY_NEG_INF) {
+            g = lower_bound_margin(key_f32(tb));
+            flags |= HDR_FILTERED;
+        }
+    }
+    // ---- 6. stage candidates in LDS, then copy them to the chunk's slot
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const float x = v[j * EPL + e];
+            if (x > NEG_INF && x >= g) {
+                const uint32_t s = atomicAdd(&sh.n_pre, 1u);
+                if (s < SAMPLE_PRECAP)
+                    sh.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
+            }
+        }
+    }
+    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
+        const float x = sh.exc_val[j];
+        if (x > NEG_INF && x >= g) {
+            const uint32_t s = atomicAdd(&sh.n_pre, 1u);
+            if (s < SAMPLE_PRECAP)
+                sh.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)sh.exc_id[j];
+        }
+    }
+    __syncthreads();
+    uint32_t n_pre = sh.n_pre;
+    const uint32_t cap = (uint32_t)P.share < SAMPLE_PRECAP ? (uint32_t)P.share : SAMPLE_PRECAP;
+    if (n_pre > cap) { flags |= HDR_OVERFLOW; n_pre = 0; }
+    uint64_t* dst = P.cand + ((size_t)row * P.S + chunk) * P.share;
+    for (uint32_t j = threadIdx.x; j < n_pre; j += LLIMA_WG) dst[j] = sh.pre[j];
+    if (threadIdx.x == 0) {
+        hdr->count = n_pre;
+        hdr->flags = flags;
+        hdr->bound = tb;
+        hdr->greedy = 0;
+    }
+}
+
+// ================================================================== finish
+struct FinishShared {
+    union {
+        uint64_t cbuf[SAMPLE_FIN_CAP];         // gathered candidates
+        uint32_t table[SAMPLE_SEG / 2];        // full-row path history counts
+    } u;
+    uint32_t hcnt[256];
+    uint64_t hmass[256];
+    uint32_t off[LLIMA_WG];
+    uint32_t sel;
+    uint64_t sel64, sel64b;
+    BlockScratch bs;
+};
+
 // ------------------------------------------------------------------ radix selects
 // Each select runs over a set of (key, id, weight) elements presented by a
 // visitor; every thread visits its own elements.  Histograms live in LDS; the
 // boundary bin of each 8-bit digit is found with one workgroup scan.
 
 // k-th largest key (with multiplicity) among visited elements.
-template <int CHUNK, class Visit>
-__device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, SampleShared<CHUNK>& sh) {
+template <class Visit>
+__device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, FinishShared& sh) {
     uint32_t prefix = 0, pmask = 0, rem = k;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        sh.f.hcnt[threadIdx.x] = 0;
+        sh.hcnt[threadIdx.x] = 0;
         __syncthreads();
         visit([&](uint32_t key, uint32_t, uint64_t) {
-            if ((key & pmask) == prefix) atomicAdd(&sh.f.hcnt[(key >> shift) & 255u], 1u);
+            if ((key & pmask) == prefix) atomicAdd(&sh.hcnt[(key >> shift) & 255u], 1u);
         });
         __syncthreads();
         const uint32_t bin = 255u - threadIdx.x;          // thread 0 <-> top bin
-        uint32_t c = sh.f.hcnt[bin], tot;
+        uint32_t c = sh.hcnt[bin], tot;
         uint32_t above = block_excl_scan_u32(c, &tot, sh.bs);
         if (above < rem && above + c >= rem) { sh.sel = bin; sh.sel64 = rem - above; }
         __syncthreads();
@@ -197,31 +387,31 @@ __device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, Sam
 
 // Top-p boundary: the smallest key theta such that an element with key theta has
 // (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
-template <int CHUNK, class Visit>
-__device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ, SampleShared<CHUNK>& sh) {
+template <class Visit>
+__device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ, FinishShared& sh) {
     uint32_t prefix = 0, pmask = 0;
     uint64_t acc = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        sh.f.hcnt[threadIdx.x] = 0;
-        sh.f.hmass[threadIdx.x] = 0;
+        sh.hcnt[threadIdx.x] = 0;
+        sh.hmass[threadIdx.x] = 0;
         __syncthreads();
         visit([&](uint32_t key, uint32_t, uint64_t w) {
             if ((key & pmask) == prefix) {
-                uint32_t b = (key >> shift) & 255u;
-                atomicAdd(&sh.f.hcnt[b], 1u);
-                if (w) atomicAdd((unsigned long long*)&sh.f.hmass[b], (unsigned long long)w);
+                const uint32_t b = (key >> shift) & 255u;
+                atomicAdd(&sh.hcnt[b], 1u);
+                if (w) atomicAdd((unsigned long long*)&sh.hmass[b], (unsigned long long)w);
             }
         });
         __syncthreads();
         const uint32_t t = threadIdx.x, bin = 255u - t;
-        uint32_t c = sh.f.hcnt[bin];
-        uint64_t m = sh.f.hmass[bin], tot;
-        uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
-        bool cond = c > 0 && (((llima_u128)above << 32) < PZ);
+        const uint32_t c = sh.hcnt[bin];
+        uint64_t m = sh.hmass[bin], tot;
+        const uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
+        const bool cond = c > 0 && (((llima_u128)above << 32) < PZ);
         // lowest qualifying bin = highest t; else the top non-empty bin = lowest t
-        uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
-        uint32_t top_nonempty = 255u - block_max_u32(c > 0 ? 255u - t : 0u, sh.bs);
-        uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
+        const uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
+        const uint32_t top_nonempty = 255u - block_max_u32(c > 0 ? 255u - t : 0u, sh.bs);
+        const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
         if (t == sel_t) { sh.sel = bin; sh.sel64 = above; }
         __syncthreads();
         prefix |= sh.sel << shift;
@@ -232,25 +422,24 @@ __device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ,
     return prefix;
 }
 
-// Draw: the smallest id whose ascending-id prefix mass exceeds target.  Also
-// returns that element's weight.
-template <int CHUNK, class Visit>
+// Draw: the smallest id whose ascending-id prefix mass exceeds target; also
+// returns that element's weight.  Ids are < 2^24.
+template <class Visit>
 __device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target, uint64_t* w_out,
-                                    SampleShared<CHUNK>& sh) {
+                                                    FinishShared& sh) {
     uint32_t prefix = 0, pmask = 0;
     uint64_t acc = 0;
     for (int shift = 16; shift >= 0; shift -= 8) {
-        sh.f.hmass[threadIdx.x] = 0;
+        sh.hmass[threadIdx.x] = 0;
         __syncthreads();
         visit([&](uint32_t, uint32_t id, uint64_t w) {
             if (w && (id & pmask) == prefix)
-                atomicAdd((unsigned long long*)&sh.f.hmass[(id >> shift) & 255u],
-                          (unsigned long long)w);
+                atomicAdd((unsigned long long*)&sh.hmass[(id >> shift) & 255u], (unsigned long long)w);
         });
         __syncthreads();
         const uint32_t bin = threadIdx.x;
-        uint64_t m = sh.f.hmass[bin], tot;
-        uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
+        uint64_t m = sh.hmass[bin], tot;
+        const uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
         if (m > 0 && below <= target && target < below + m) {
             sh.sel = bin; sh.sel64 = below; sh.sel64b = m;
         }
@@ -264,17 +453,9 @@ __device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target
     return prefix;
 }
 
-__device__ __forceinline__ void write_result(const SampleParams& P, int row, int32_t id,
-                                             float prob) {
+__device__ __forceinline__ void write_result(const SampleParams& P, int row, int32_t id, float prob) {
     P.out_ids[row] = id;
     if (P.out_probs) P.out_probs[row] = prob;
-}
-
-__device__ __forceinline__ void reset_ctl(RowCtl* ctl) {
-    ctl->count = 0;
-    ctl->flags = 0;
-    ctl->tmax_key = 0;
-    ctl->greedy = 0;
 }
 
 // Writes the kept set of a row as a bitmask (zero-filled first).
@@ -293,26 +474,27 @@ __device__ __forceinline__ void write_keep(const SampleParams& P, int row, Visit
 
 // ------------------------------------------------------------------ full-row path
 // Exact multi-pass selection by one workgroup; recomputes x for the whole row on
-// every pass (history table rebuilt per CHUNK segment).
-template <typename TL, int CHUNK>
+// every pass (history table rebuilt per segment).
+template <typename TL>
 __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, const RowCfg& c,
-                                SampleShared<CHUNK>& sh) {
+                                                FinishShared& sh) {
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
     const int nw = (V + 31) >> 5;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
-    uint32_t* table = sh.s.cnt;
+    uint32_t* table = sh.u.table;
+    __syncthreads();
     // fn(x, id) for every element of the row.
     auto for_each_x = [&](auto fn) {
-        for (int lo = 0; lo < V; lo += CHUNK) {
-            const int hi = lo + CHUNK < V ? lo + CHUNK : V;
-            if (c.pen) build_hist_table<CHUNK>(P, row, c, lo, hi, table, sh, false);
+        for (int lo = 0; lo < V; lo += SAMPLE_SEG) {
+            const int hi = lo + SAMPLE_SEG < V ? lo + SAMPLE_SEG : V;
+            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2, nullptr, nullptr);
             for (int i = lo + threadIdx.x; i < hi; i += LLIMA_WG) {
                 float l = load_one<TL>(rowp, i);
                 if (l != l) l = -__builtin_inff();
                 if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) l = -__builtin_inff();
                 if (c.pen) {
-                    uint32_t cnt = table_count(table, (uint32_t)(i - lo));
+                    const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
                     if (cnt) l = penalize(l, cnt, c);
                 }
                 fn(c.greedy ? l : l / c.T, (uint32_t)i);
@@ -324,25 +506,22 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     if (c.greedy) {
         uint64_t best = 0;
         for_each_x([&](float x, uint32_t id) {
-            uint64_t kk = ((uint64_t)f32_key(x) << 32) | (uint64_t)(~id);
+            const uint64_t kk = ((uint64_t)f32_key(x) << 32) | (uint64_t)(~id);
             best = kk > best ? kk : best;
         });
         best = block_max_u64(best, sh.bs);
-        if (threadIdx.x == 0) {
-            bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
-            write_result(P, row, ok ? (int32_t)(~(uint32_t)best) : -1, ok ? 1.0f : 0.0f);
-        }
-        if (P.out_keep) {
-            const uint32_t tok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF ? ~(uint32_t)best : 0xFFFFFFFFu;
-            write_keep(P, row, [&](auto set) { if (threadIdx.x == 0 && tok != 0xFFFFFFFFu) set(tok); });
-        }
+        const bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
+        const uint32_t tok = ok ? ~(uint32_t)best : 0xFFFFFFFFu;
+        if (threadIdx.x == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+        if (P.out_keep)
+            write_keep(P, row, [&](auto set) { if (threadIdx.x == 0 && ok) set(tok); });
         return;
     }
 
     // Pass: maximum and number of finite values.
     uint32_t kmax = 0, nfin = 0;
     for_each_x([&](float x, uint32_t) {
-        uint32_t k = f32_key(x);
+        const uint32_t k = f32_key(x);
         if (k > LLIMA_KEY_NEG_INF) { nfin++; kmax = k > kmax ? k : kmax; }
     });
     kmax = block_max_u32(kmax, sh.bs);
@@ -353,18 +532,18 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         return;
     }
     const float xmax = key_f32(kmax);
-    auto visit_fin = [&](auto fn) {   // finite elements, weights not needed
+    auto visit_fin = [&](auto fn) {
         for_each_x([&](float x, uint32_t id) {
-            uint32_t k = f32_key(x);
+            const uint32_t k = f32_key(x);
             if (k > LLIMA_KEY_NEG_INF) fn(k, id, 0ull);
         });
     };
     uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
-    if (c.k > 0 && (uint32_t)c.k <= nfin) tau = select_kth_desc<CHUNK>(visit_fin, (uint32_t)c.k, sh);
+    if (c.k > 0 && (uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, sh);
 
-    auto visit_k = [&](auto fn) {     // top-k survivors with weights
+    auto visit_k = [&](auto fn) {
         for_each_x([&](float x, uint32_t id) {
-            uint32_t k = f32_key(x);
+            const uint32_t k = f32_key(x);
             if (k >= tau) fn(k, id, weight(x, xmax));
         });
     };
@@ -373,8 +552,8 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         uint64_t Z = 0;
         visit_k([&](uint32_t, uint32_t, uint64_t w) { Z += w; });
         Z = block_sum_u64(Z, sh.bs);
-        llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc<CHUNK>(visit_k, PZ, sh);
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+        theta = select_topp_desc(visit_k, PZ, sh);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     auto visit_final = [&](auto fn) {
@@ -390,7 +569,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
         uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc<CHUNK>(visit_final, target, &wtok, sh);
+        tok = (int32_t)select_draw_asc(visit_final, target, &wtok, sh);
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
@@ -400,58 +579,22 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         });
 }
 
-// Greedy rows: the row's best (key, index) was merged by atomicMax.  Returns
-// false when the row must be redone by the full-row path.
-template <typename TL, int CHUNK>
-__device__ __forceinline__ bool finish_greedy(const SampleParams& P, int row, const RowCfg& c,
-                                              RowCtl* ctl, SampleShared<CHUNK>& sh) {
-    (void)c;
-    // More distinct history ids in a chunk than the exception list holds.
-    const bool ovf = (load_coherent(&ctl->flags) & CTL_OVERFLOW) != 0;
-    __syncthreads();
-    if (ovf) {
-        if (threadIdx.x == 0) reset_ctl(ctl);
-        return false;
-    }
-    if (threadIdx.x == 0) {
-        const uint64_t best = load_coherent(&ctl->greedy);
-        const bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
-        write_result(P, row, ok ? (int32_t)(~(uint32_t)best) : -1, ok ? 1.0f : 0.0f);
-        sh.sel = ok ? ~(uint32_t)best : 0xFFFFFFFFu;
-        reset_ctl(ctl);
-    }
-    if (P.out_keep) {
-        __syncthreads();
-        const uint32_t tok = sh.sel;
-        write_keep(P, row, [&](auto set) { if (threadIdx.x == 0 && tok != 0xFFFFFFFFu) set(tok); });
-    }
-    return true;
-}
-
-// Sampling rows from the candidate list.  Returns false when the candidates
-// cannot be proven to contain the kept set (the full-row path then runs).
-template <typename TL, int CHUNK>
+// ------------------------------------------------------------------ fast path
+// Sampling from the gathered candidates.  Returns false when they cannot be
+// proven to contain the kept set (the caller then runs the full-row path).
 __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, const RowCfg& c,
-                                            RowCtl* ctl, SampleShared<CHUNK>& sh) {
+                                            uint32_t n, uint32_t flags, uint32_t bound_key,
+                                            FinishShared& sh) {
     const float NEG_INF = -__builtin_inff();
-    const uint32_t flags = load_coherent(&ctl->flags);
-    const uint32_t n = load_coherent(&ctl->count);
-    const uint32_t tmax_key = load_coherent(&ctl->tmax_key);
-    __syncthreads();
-    if (threadIdx.x == 0) reset_ctl(ctl);
-    if ((flags & CTL_OVERFLOW) || n > SAMPLE_RCAP) return false;
-
-    // ---- load candidates into registers: slot j of thread t is candidate t + 256 j
     uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
     float xs[SAMPLE_SLOTS];
-    const uint64_t* src = (const uint64_t*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES + SAMPLE_CTL_BYTES);
     uint32_t kmax = 0;
 #pragma unroll
     for (int j = 0; j < SAMPLE_SLOTS; ++j) {
         const uint32_t s = threadIdx.x + j * LLIMA_WG;
         key[j] = 0; id[j] = 0; xs[j] = NEG_INF;
         if (s < n) {
-            const uint64_t q = src[s];
+            const uint64_t q = sh.u.cbuf[s];
             const float x = __uint_as_float((uint32_t)(q >> 32)) / c.T;
             xs[j] = x;
             key[j] = f32_key(x);
@@ -462,7 +605,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
     kmax = block_max_u32(kmax, sh.bs);
     if (kmax <= LLIMA_KEY_NEG_INF) {
         // Every candidate is -inf after the temperature (or there are none).
-        if (flags & CTL_FILTERED) return false;
+        if (flags & HDR_FILTERED) return false;
         if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
         if (P.out_keep) write_keep(P, row, [&](auto) {});
         return true;
@@ -474,17 +617,18 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
             if (key[j] > LLIMA_KEY_NEG_INF) fn(key[j], id[j], 0ull);
     };
 
-    // ---- top-k threshold, then proof that the pre-filter kept every member
+    // ---- top-k threshold, then the proof that the pre-filter kept every member:
+    // a value below a chunk's lowered bound g has x <= fl(g / T) < tau.
     uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
     if (c.k > 0) {
         uint32_t nfin = 0;
 #pragma unroll
         for (int j = 0; j < SAMPLE_SLOTS; ++j) nfin += key[j] > LLIMA_KEY_NEG_INF;
         nfin = block_sum_u32(nfin, sh.bs);
-        if ((uint32_t)c.k <= nfin) tau = select_kth_desc<CHUNK>(visit_all, (uint32_t)c.k, sh);
-        else if (flags & CTL_FILTERED) return false;
-        if (flags & CTL_FILTERED) {
-            const float gq = lower_bound_margin(key_f32(tmax_key)) / c.T;
+        if ((uint32_t)c.k <= nfin) tau = select_kth_desc(visit_all, (uint32_t)c.k, sh);
+        else if (flags & HDR_FILTERED) return false;
+        if (flags & HDR_FILTERED) {
+            const float gq = lower_bound_margin(key_f32(bound_key)) / c.T;
             if (!(gq < key_f32(tau))) return false;
         }
     }
@@ -507,7 +651,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
         for (int j = 0; j < SAMPLE_SLOTS; ++j) Z += w[j];
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc<CHUNK>(visit_k, PZ, sh);
+        theta = select_topp_desc(visit_k, PZ, sh);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     auto visit_final = [&](auto fn) {
@@ -523,7 +667,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
         uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc<CHUNK>(visit_final, target, &wtok, sh);
+        tok = (int32_t)select_draw_asc(visit_final, target, &wtok, sh);
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
@@ -534,206 +678,90 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
     return true;
 }
 
-// ------------------------------------------------------------------ the kernel
-template <typename TL, int E>
-__global__ __launch_bounds__(LLIMA_WG) void sample_kernel(SampleParams P) {
-    constexpr int EPL = 16 / sizeof(TL);       // elements per 16-byte load
-    constexpr int NL = E / EPL;                // loads per thread
-    constexpr int CHUNK = LLIMA_WG * E;
-    __shared__ SampleShared<CHUNK> sh;
-
-    uint32_t row, chunk;
-    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
-    if (row >= (uint32_t)P.B) return;
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
+    __shared__ FinishShared sh;
+    const int row = blockIdx.x;
     const RowCfg c = load_cfg(P, row);
-    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
-    const int V = P.V;
-    const int c0 = (int)chunk * CHUNK;
-    const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
-    const int nw = (V + 31) >> 5;
-    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
-    RowCtl* ctl = (RowCtl*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES);
-    const float NEG_INF = -__builtin_inff();
+    const ChunkHdr* hdr = P.hdr + (size_t)row * P.S;
 
-    if (threadIdx.x == 0) { sh.n_pre = 0; sh.flags = 0; sh.n_exc = 0; }
-    if (c.pen) build_hist_table<CHUNK>(P, row, c, c0, c1, sh.s.cnt, sh, true);
-    else __syncthreads();
-
-    // ---- stream the chunk into registers (value after mask / NaN / history exclusion)
-    float v[E];
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-        float t[EPL];
-        if (P.vec_ok && i0 + EPL <= c1) {
-            if constexpr (sizeof(TL) == 4) {
-                float4 q = *(const float4*)(rowp + i0);
-                t[0] = q.x; t[1] = q.y; t[2] = q.z; t[3] = q.w;
-            } else {
-                uint4 q = *(const uint4*)(rowp + i0);
-                const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    t[2 * e] = __uint_as_float(w4[e] << 16);
-                    t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) t[e] = (i0 + e < c1) ? load_one<TL>(rowp, i0 + e) : NEG_INF;
-        }
-        uint32_t mbits = 0xFFFFFFFFu;
-        if (mrow && i0 < c1) mbits = mrow[i0 >> 5] >> (i0 & 31);
-        uint32_t cw[EPL / 2];
-        if (c.pen && i0 < c1) {
-            const uint32_t off = (uint32_t)(i0 - c0);
-#pragma unroll
-            for (int e = 0; e < EPL / 2; ++e) cw[e] = sh.s.cnt[(off >> 1) + e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPL / 2; ++e) cw[e] = 0;
-        }
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float x = t[e];
-            const bool hist_hit = ((cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) != 0;
-            if (x != x || !((mbits >> e) & 1u) || hist_hit) x = NEG_INF;
-            v[j * EPL + e] = x;
-        }
+    // ---- merge the chunk headers
+    uint32_t flags = 0, bound = 0, n = 0;
+    uint64_t greedy = 0;
+    for (int ch = threadIdx.x; ch < P.S; ch += LLIMA_WG) {
+        const ChunkHdr h = hdr[ch];
+        flags |= h.flags;
+        n += h.count;
+        if (h.flags & HDR_FILTERED) bound = h.bound > bound ? h.bound : bound;
+        greedy = h.greedy > greedy ? h.greedy : greedy;
     }
+    // OR of flags through a max of the two flag bits
+    const uint32_t fl = block_max_u32(flags & HDR_OVERFLOW, sh.bs) |
+                        block_max_u32(flags & HDR_FILTERED, sh.bs);
+    bound = block_max_u32(bound, sh.bs);
+    n = block_sum_u32(n, sh.bs);
 
-    // ---- exceptions: distinct history ids of this chunk, penalised exactly
-    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
-    if (n_exc > SAMPLE_EXC_CAP) {
-        if (threadIdx.x == 0) atomicOr(&ctl->flags, CTL_OVERFLOW);
-    }
-    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
-    float tmax = NEG_INF;
-    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-        const int id = sh.s.exc_id[j];
-        float l = load_one<TL>(rowp, id);
-        if (l != l) l = NEG_INF;
-        if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) l = NEG_INF;
-        l = penalize(l, table_count(sh.s.cnt, (uint32_t)(id - c0)), c);
-        sh.s.exc_val[j] = l;
-        tmax = l > tmax ? l : tmax;
-    }
-
+    bool done = false;
     if (c.greedy) {
-        // ---- argmax: first index of the maximum
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                uint64_t kk = ((uint64_t)f32_key(v[j * EPL + e]) << 32) | (uint64_t)(~(uint32_t)(i0 + e));
-                best = kk > best ? kk : best;
-            }
+        greedy = block_max_u64(greedy, sh.bs);
+        if (!(fl & HDR_OVERFLOW)) {
+            const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
+            const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
+            if (threadIdx.x == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+            if (P.out_keep)
+                write_keep(P, row, [&](auto set) { if (threadIdx.x == 0 && ok) set(tok); });
+            done = true;
         }
-        for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-            uint64_t kk = ((uint64_t)f32_key(sh.s.exc_val[j]) << 32) |
-                          (uint64_t)(~(uint32_t)sh.s.exc_id[j]);
-            best = kk > best ? kk : best;
-        }
-        best = block_max_u64(best, sh.bs);
-        if (threadIdx.x == 0) atomicMax((unsigned long long*)&ctl->greedy, (unsigned long long)best);
-    } else {
-        // ---- pre-filter bound from lane maxima
-        float g = NEG_INF;
-        if (c.k > 0 && c.k <= 4 * 64) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) tmax = v[e] > tmax ? v[e] : tmax;
-            const uint32_t r = (uint32_t)(c.k + 3) >> 2;          // ceil(k/4) <= 64
-            uint32_t sorted = wave_sort_desc(f32_key(tmax));
-            uint32_t wb = __shfl(sorted, (int)r - 1, 64);
-            if (lane_id() == 0) sh.wave_bound[threadIdx.x >> 6] = wb;
+    } else if (!(fl & HDR_OVERFLOW) && n <= SAMPLE_FIN_CAP) {
+        // ---- gather the candidates into LDS: chunk offsets by a block scan,
+        //      then one wave per chunk copies its slot
+        uint32_t base = 0;
+        for (int g0 = 0; g0 < P.S; g0 += LLIMA_WG) {
+            const int ch = g0 + (int)threadIdx.x;
+            const uint32_t cnt = ch < P.S ? hdr[ch].count : 0u;
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u32(cnt, &tot, sh.bs);
+            sh.off[threadIdx.x] = base + ex;
             __syncthreads();
-            uint32_t tb = sh.wave_bound[0];
-#pragma unroll
-            for (int w = 1; w < LLIMA_WAVES; ++w) tb = sh.wave_bound[w] < tb ? sh.wave_bound[w] : tb;
-            if (tb > LLIMA_KEY_NEG_INF) {
-                g = lower_bound_margin(key_f32(tb));
-                if (threadIdx.x == 0) {
-                    atomicMax(&ctl->tmax_key, tb);
-                    atomicOr(&ctl->flags, CTL_FILTERED);
-                }
+            const int nch = P.S - g0 < LLIMA_WG ? P.S - g0 : LLIMA_WG;
+            for (int k = (int)(threadIdx.x >> 6); k < nch; k += LLIMA_WAVES) {
+                const uint32_t o = sh.off[k];
+                const uint32_t m = hdr[g0 + k].count;
+                const uint64_t* src = P.cand + ((size_t)row * P.S + g0 + k) * P.share;
+                for (uint32_t i = lane_id(); i < m; i += 64) sh.u.cbuf[o + i] = src[i];
             }
+            base += tot;
+            __syncthreads();
         }
-        // ---- stage candidates in LDS
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float x = v[j * EPL + e];
-                if (x > NEG_INF && x >= g) {
-                    uint32_t s = atomicAdd(&sh.n_pre, 1u);
-                    if (s < SAMPLE_PRECAP)
-                        sh.s.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
-                }
-            }
-        }
-        for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-            const float x = sh.s.exc_val[j];
-            if (x > NEG_INF && x >= g) {
-                uint32_t s = atomicAdd(&sh.n_pre, 1u);
-                if (s < SAMPLE_PRECAP)
-                    sh.s.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)sh.s.exc_id[j];
-            }
-        }
-        __syncthreads();
-        const uint32_t n_pre = sh.n_pre;
-        if (threadIdx.x == 0) {
-            uint32_t base = 0xFFFFFFFFu;
-            if (n_pre > SAMPLE_PRECAP) atomicOr(&ctl->flags, CTL_OVERFLOW);
-            else if (n_pre) {
-                base = atomicAdd(&ctl->count, n_pre);
-                if (base + n_pre > SAMPLE_RCAP) { atomicOr(&ctl->flags, CTL_OVERFLOW); base = 0xFFFFFFFFu; }
-            }
-            sh.base = base;
-        }
-        __syncthreads();
-        const uint32_t base = sh.base;
-        if (base != 0xFFFFFFFFu) {
-            uint64_t* dst = (uint64_t*)(P.ws + (size_t)row * SAMPLE_SLOT_BYTES + SAMPLE_CTL_BYTES) + base;
-            for (uint32_t j = threadIdx.x; j < n_pre; j += LLIMA_WG) dst[j] = sh.s.pre[j];
-        }
+        done = finish_fast(P, row, c, n, fl, bound, sh);
     }
-
-    // ---- the last workgroup of the row finishes it
-    if (!arrive_last(&ctl->done, (uint32_t)P.S, &sh.last)) return;
-
-    bool done;
-    if (c.greedy) done = finish_greedy<TL, CHUNK>(P, row, c, ctl, sh);
-    else done = finish_fast<TL, CHUNK>(P, row, c, ctl, sh);
-    if (!done) finish_full_row<TL, CHUNK>(P, row, c, sh);
+    if (!done) finish_full_row<TL>(P, row, c, sh);
 }
 
-// ------------------------------------------------------------------ host side
+// ================================================================== host side
 struct Tile { int E; int S; };
 
 static Tile choose_tile(int B, int V, int dtype, int k) {
     // Largest E first; shrink while the grid is small, but keep the row's
-    // candidate count (about 2k per chunk) well inside SAMPLE_RCAP.
+    // candidate count (about 2k per chunk) well inside the finish capacity.
     const int emax = dtype == LLIMA_F32 ? 32 : 64;
     int E = emax;
     auto S_of = [&](int e) { return (V + LLIMA_WG * e - 1) / (LLIMA_WG * e); };
     while (E > 8) {
-        const int S2 = S_of(E / 2);
         if ((int64_t)B * S_of(E) >= 1024) break;
-        if (k > 0 && (int64_t)S2 * 2 * k > SAMPLE_RCAP / 2) break;
+        if (k > 0 && (int64_t)S_of(E / 2) * 2 * k > SAMPLE_FIN_CAP / 2) break;
         E /= 2;
-        (void)S2;
     }
     return {E, S_of(E)};
 }
 
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+static int max_chunks(int V) { return (V + SAMPLE_MIN_CHUNK - 1) / SAMPLE_MIN_CHUNK; }
+
 template <typename TL, int E>
-static hipError_t launch(const SampleParams& P, hipStream_t st) {
-    const uint32_t nblk = (uint32_t)P.B * (uint32_t)P.S;
-    hipLaunchKernelGGL((sample_kernel<TL, E>), dim3(nblk), dim3(LLIMA_WG), 0, st, P);
-    return hipGetLastError();
+static void launch_sweep(const SampleParams& P, hipStream_t st) {
+    hipLaunchKernelGGL((sample_sweep<TL, E>), dim3((uint32_t)P.B * (uint32_t)P.S), dim3(LLIMA_WG),
+                       0, st, P);
 }
 
 }  // namespace llima
@@ -741,9 +769,10 @@ static hipError_t launch(const SampleParams& P, hipStream_t st) {
 using namespace llima;
 
 extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
-    (void)V; (void)dtype;
-    if (B <= 0) return 0;
-    return (size_t)B * SAMPLE_SLOT_BYTES;
+    (void)dtype;
+    if (B <= 0 || V <= 0) return 0;
+    return al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)) +
+           (size_t)B * SAMPLE_ROW_CAND * sizeof(uint64_t);
 }
 
 extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V,
@@ -779,7 +808,6 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.out_ids = out_ids;
     P.out_probs = out_probs;
     P.out_keep = out_keep;
-    P.ws = (char*)workspace;
     P.B = B;
     P.V = V;
     P.H_max = history ? H_max : 0;
@@ -788,21 +816,25 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     const int k_hint = cfg->top_k_rows ? 0 : cfg->top_k;
     const Tile t = choose_tile(B, V, dtype, (k_hint > 0 && k_hint < V) ? k_hint : 0);
     P.S = t.S;
+    P.share = SAMPLE_ROW_CAND / t.S;
+    P.hdr = (ChunkHdr*)workspace;
+    P.cand = (uint64_t*)((char*)workspace + al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)));
     hipStream_t st = (hipStream_t)stream;
-    hipError_t e;
     if (dtype == LLIMA_F32) {
         switch (t.E) {
-            case 8: e = launch<float, 8>(P, st); break;
-            case 16: e = launch<float, 16>(P, st); break;
-            default: e = launch<float, 32>(P, st); break;
+            case 8: launch_sweep<float, 8>(P, st); break;
+            case 16: launch_sweep<float, 16>(P, st); break;
+            default: launch_sweep<float, 32>(P, st); break;
         }
+        hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
         switch (t.E) {
-            case 8: e = launch<uint16_t, 8>(P, st); break;
-            case 16: e = launch<uint16_t, 16>(P, st); break;
-            case 32: e = launch<uint16_t, 32>(P, st); break;
-            default: e = launch<uint16_t, 64>(P, st); break;
+            case 8: launch_sweep<uint16_t, 8>(P, st); break;
+            case 16: launch_sweep<uint16_t, 16>(P, st); break;
+            case 32: launch_sweep<uint16_t, 32>(P, st); break;
+            default: launch_sweep<uint16_t, 64>(P, st); break;
         }
+        hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
-    return e == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }

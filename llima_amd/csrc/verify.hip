@@ -15,12 +15,17 @@
 // sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111); with one-hot distributions
 // this reduces to that rule.
 //
-// Three launches: (1) row maxima, (2) row sums Z, per-chunk sums and the weight
-// at each draft token, with the acceptance scan run by the last workgroup of
-// each sequence, (3) the residual (or bonus) draw: per-chunk residual sums, then
-// the last workgroup of the sequence finds the chunk holding the target and
-// scans it.  Pass (2) re-reads the rows right after pass (1); at these sizes
-// they are still resident in the 256 MB Infinity Cache.
+// Four launches, no atomics or fences between workgroups (each writes its own
+// workspace slots; a later launch reads them):
+//   vr_rowmax   per (row, chunk) maximum key
+//   vr_rowsum   per (row, chunk) sum of W, and W at each row's draft token
+//   vr_drawsum  per (sequence, chunk): the acceptance scan (recomputed from the
+//               sums by every workgroup of the sequence), then the chunk's sum
+//               of residual weights when a draft was rejected
+//   vr_final    per sequence: acceptance, emitted drafts, the chunk holding the
+//               draw target, and the scan of that chunk for the token.
+// Pass 2 re-reads the rows right after pass 1; at these sizes they are still
+// resident in the 256 MB Infinity Cache.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -28,26 +33,7 @@ namespace llima {
 
 #define VR_E 32
 #define VR_CHUNK (LLIMA_WG * VR_E)
-
-enum { JOB_RESIDUAL = 0, JOB_BONUS = 1 };
-
-// Workspace: one fixed-size slot per row index r (target rows first, then
-// draft rows).  Slot b also carries sequence b's counters, job and residual
-// chunk sums.  Positions never depend on the call's shape, so a workspace can
-// be reused for any shape; the control words are left zero after every call.
-#define VR_SMAX 512                       // chunks per row: V <= 2^22
-struct VRowSlot {
-    uint32_t row_max;     // key of the row maximum (0 = no value)
-    uint32_t seq_done2;   // sequence counters (slot b)
-    uint32_t seq_done3;
-    int32_t job_kind;
-    uint64_t row_z;
-    uint64_t row_wx;      // weight of the draft token in rows k < D
-    int32_t job_k;
-    int32_t pad[7];
-    uint64_t chunk_sum[VR_SMAX];
-    uint64_t res_sum[VR_SMAX];
-};
+#define VR_MAX_D 255
 
 struct VerifyParams {
     const float* tgt;
@@ -57,7 +43,10 @@ struct VerifyParams {
     const float* u_resample;
     int32_t* accepted_len;
     int32_t* emitted;
-    VRowSlot* ws;
+    uint32_t* maxk;      // [NR][S]
+    uint64_t* sums;      // [NR][S]
+    uint64_t* wx;        // [NR]
+    uint64_t* res;       // [B][S]
     int32_t B, D, V, S, NR;
 };
 
@@ -86,14 +75,16 @@ __device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, fl
     for (int j = 0; j < VR_E / 4; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
         if (i0 + 4 <= c1) {
-            float4 q = *(const float4*)(rowp + i0);
-            v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+            const llima_u32x4 q = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
+            v[4 * j] = __uint_as_float(q.x); v[4 * j + 1] = __uint_as_float(q.y);
+            v[4 * j + 2] = __uint_as_float(q.z); v[4 * j + 3] = __uint_as_float(q.w);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[4 * j + e] = i0 + e < c1 ? rowp[i0 + e] : -__builtin_inff();
         }
     }
 }
+
 // Weight of a value given its row maximum key (0 when the row has no value).
 __device__ __forceinline__ uint64_t row_weight(float x, uint32_t mkey) {
     if (mkey <= LLIMA_KEY_NEG_INF) return 0;
@@ -113,56 +104,85 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
         m = k > m ? k : m;
     }
     m = block_max_u32(m, bs);
-    if (threadIdx.x == 0 && m) atomicMax(&P.ws[r].row_max, m);
+    if (threadIdx.x == 0) P.maxk[(size_t)r * P.S + c] = m;
 }
 
 __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     __shared__ BlockScratch bs;
-    __shared__ uint32_t flag;
+    __shared__ uint32_t s_mkey;
     const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
-    const uint32_t mkey = P.ws[r].row_max;
     float v[VR_E];
     load_chunk(rowp, c0, c1, v);
+    if (threadIdx.x < 64) {
+        const uint32_t* m = P.maxk + (size_t)r * P.S;
+        uint32_t best = 0;
+        for (int i = (int)threadIdx.x; i < P.S; i += 64) best = m[i] > best ? m[i] : best;
+        best = wave_max_u32(best);
+        if (threadIdx.x == 0) s_mkey = best;
+    }
+    __syncthreads();
+    const uint32_t mkey = s_mkey;
     uint64_t s = 0;
 #pragma unroll
     for (int e = 0; e < VR_E; ++e) s += row_weight(v[e], mkey);
     s = block_sum_u64(s, bs);
-    const int b = seq_of(P, r), k = pos_of(P, r);
     if (threadIdx.x == 0) {
-        P.ws[r].chunk_sum[c] = s;
-        if (s) atomicAdd((unsigned long long*)&P.ws[r].row_z, (unsigned long long)s);
+        P.sums[(size_t)r * P.S + c] = s;
+        const int b = seq_of(P, r), k = pos_of(P, r);
         if (k < P.D) {
             const int x = P.draft_ids[b * P.D + k];
-            if (x >= c0 && x < c1) P.ws[r].row_wx = row_weight(rowp[x], mkey);
+            if (x >= c0 && x < c1) P.wx[r] = row_weight(rowp[x], mkey);
         }
     }
-    const uint32_t expected = (uint32_t)(2 * P.D + 1) * (uint32_t)P.S;
-    if (!arrive_last(&P.ws[b].seq_done2, expected, &flag)) return;
-    if (threadIdx.x != 0) return;
+}
 
-    // ---- acceptance scan of sequence b
-    int32_t* em = P.emitted + (size_t)b * (P.D + 1);
-    int acc = 0;
-    for (; acc < P.D; ++acc) {
-        const int x = P.draft_ids[b * P.D + acc];
-        const int rt = trow(P, b, acc), rd = drow(P, b, acc);
-        const uint64_t zt = load_coherent(&P.ws[rt].row_z), zd = load_coherent(&P.ws[rd].row_z);
-        bool ok = false;
-        if (x >= 0 && x < P.V && zt > 0) {
-            const uint64_t wt = load_coherent(&P.ws[rt].row_wx), wd = load_coherent(&P.ws[rd].row_wx);
-            const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
-            const llima_u128 rhs = (llima_u128)uniform32(P.u_accept[b * P.D + acc]) * ((llima_u128)wd * zt);
-            ok = lhs >= rhs;
+// ------------------------------------------------------------------ acceptance
+struct SeqShared {
+    uint64_t z[2 * VR_MAX_D + 1];      // Z of target rows 0..D then draft rows 0..D-1
+    uint32_t m[2 * VR_MAX_D + 1];      // maximum keys, same order
+    int32_t acc;
+    BlockScratch bs;
+};
+
+// Z and maximum of every row of sequence b (one wavefront per row), then the
+// acceptance scan.  Returns the number of accepted drafts (same in every thread).
+__device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShared& sh) {
+    const int nr = 2 * P.D + 1;
+    for (int q = (int)(threadIdx.x >> 6); q < nr; q += LLIMA_WAVES) {
+        const int r = q <= P.D ? trow(P, b, q) : drow(P, b, q - P.D - 1);
+        uint64_t z = 0;
+        uint32_t m = 0;
+        for (int i = (int)lane_id(); i < P.S; i += 64) {
+            z += P.sums[(size_t)r * P.S + i];
+            const uint32_t mk = P.maxk[(size_t)r * P.S + i];
+            m = mk > m ? mk : m;
         }
-        if (!ok) break;
-        em[acc] = x;
+        z = wave_sum_u64(z);
+        m = wave_max_u32(m);
+        if (lane_id() == 0) { sh.z[q] = z; sh.m[q] = m; }
     }
-    for (int j = acc; j <= P.D; ++j) em[j] = -1;
-    P.accepted_len[b] = acc;
-    P.ws[b].job_kind = acc < P.D ? JOB_RESIDUAL : JOB_BONUS;
-    P.ws[b].job_k = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (; acc < P.D; ++acc) {
+            const int x = P.draft_ids[b * P.D + acc];
+            const uint64_t zt = sh.z[acc], zd = sh.z[P.D + 1 + acc];
+            bool ok = false;
+            if (x >= 0 && x < P.V && zt > 0) {
+                const uint64_t wt = P.wx[trow(P, b, acc)], wd = P.wx[drow(P, b, acc)];
+                const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
+                const llima_u128 rhs = (llima_u128)uniform32(P.u_accept[b * P.D + acc]) *
+                                       ((llima_u128)wd * zt);
+                ok = lhs >= rhs;
+            }
+            if (!ok) break;
+        }
+        sh.acc = acc;
+    }
+    __syncthreads();
+    return sh.acc;
 }
 
 __device__ __forceinline__ int bitlen64(uint64_t z) { return z ? 64 - __clzll((long long)z) : 0; }
@@ -176,6 +196,25 @@ struct DrawCtx {
     int shift;
 };
 
+__device__ __forceinline__ DrawCtx draw_ctx(const VerifyParams& P, int b, int acc,
+                                            const SeqShared& sh) {
+    DrawCtx q;
+    q.residual = acc < P.D;
+    const int k = acc;                                 // target row of the draw
+    q.t = row_ptr(P, trow(P, b, k));
+    q.mt = sh.m[k];
+    q.zt = sh.z[k];
+    q.d = nullptr; q.md = 0; q.zd = 0; q.shift = 0;
+    if (q.residual) {
+        q.d = row_ptr(P, drow(P, b, k));
+        q.md = sh.m[P.D + 1 + k];
+        q.zd = sh.z[P.D + 1 + k];
+        const int s = bitlen64(q.zt) + bitlen64(q.zd) - 63;
+        q.shift = s > 0 ? s : 0;
+    }
+    return q;
+}
+
 __device__ __forceinline__ uint64_t draw_weight(const DrawCtx& q, int i) {
     const uint64_t wt = row_weight(q.t[i], q.mt);
     if (!q.residual) return wt;
@@ -184,49 +223,43 @@ __device__ __forceinline__ uint64_t draw_weight(const DrawCtx& q, int i) {
     return a > c ? (uint64_t)((a - c) >> q.shift) : 0ull;
 }
 
-__global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
-    __shared__ BlockScratch bs;
-    __shared__ uint32_t flag;
+__global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
+    __shared__ SeqShared sh;
+    const int b = blockIdx.x / P.S, c = blockIdx.x % P.S;
+    const int acc = accept_scan(P, b, sh);
+    if (acc >= P.D) return;                          // bonus draw: no residual
+    const DrawCtx q = draw_ctx(P, b, acc, sh);
+    const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
+    uint64_t s = 0;
+    for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) s += draw_weight(q, i);
+    s = block_sum_u64(s, sh.bs);
+    if (threadIdx.x == 0) P.res[(size_t)b * P.S + c] = s;
+}
+
+__global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
+    __shared__ SeqShared sh;
     __shared__ int32_t s_chunk, s_tok;
     __shared__ uint64_t s_before, s_target;
     __shared__ bool s_residual;
-    const int b = blockIdx.x / P.S, c = blockIdx.x % P.S;
-    int kind = P.ws[b].job_kind, k = P.ws[b].job_k;
-    // a job is only ever {RESIDUAL, k < D} or {BONUS, D}
-    if (!(kind == JOB_RESIDUAL && k >= 0 && k < P.D)) { kind = JOB_BONUS; k = P.D; }
-    const int rt = trow(P, b, k);
-    DrawCtx q;
-    q.residual = kind == JOB_RESIDUAL;
-    q.t = row_ptr(P, rt);
-    q.mt = P.ws[rt].row_max;
-    q.zt = P.ws[rt].row_z;
-    q.d = nullptr; q.md = 0; q.zd = 0; q.shift = 0;
-    if (q.residual) {
-        const int rd = drow(P, b, k);
-        q.d = row_ptr(P, rd);
-        q.md = P.ws[rd].row_max;
-        q.zd = P.ws[rd].row_z;
-        const int sh = bitlen64(q.zt) + bitlen64(q.zd) - 63;
-        q.shift = sh > 0 ? sh : 0;
-        const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
-        uint64_t s = 0;
-        for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) s += draw_weight(q, i);
-        s = block_sum_u64(s, bs);
-        if (threadIdx.x == 0) P.ws[b].res_sum[c] = s;
-    }
-    if (!arrive_last(&P.ws[b].seq_done3, (uint32_t)P.S, &flag)) return;
-
-    // ---- last workgroup of the sequence: locate the chunk, then the id
+    const int b = blockIdx.x;
+    const int acc = accept_scan(P, b, sh);
+    DrawCtx q = draw_ctx(P, b, acc, sh);
+    const int rt = trow(P, b, acc);
     if (threadIdx.x == 0) {
-        const uint64_t* sums = P.ws[b].res_sum;
+        int32_t* em = P.emitted + (size_t)b * (P.D + 1);
+        for (int j = 0; j < acc; ++j) em[j] = P.draft_ids[b * P.D + j];
+        for (int j = acc; j <= P.D; ++j) em[j] = -1;
+        P.accepted_len[b] = acc;
+        // locate the chunk that holds the draw target
+        const uint64_t* sums = P.res + (size_t)b * P.S;
         uint64_t total = 0;
         bool residual = q.residual;
         if (residual) {
-            for (int j = 0; j < P.S; ++j) total += load_coherent(&sums[j]);
+            for (int j = 0; j < P.S; ++j) total += sums[j];
             if (total == 0) residual = false;          // p_t == p_d: draw from p_t
         }
         if (!residual) {
-            sums = P.ws[rt].chunk_sum;
+            sums = P.sums + (size_t)rt * P.S;
             total = q.zt;
         }
         int32_t chunk = -1;
@@ -234,7 +267,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
         if (total > 0) {
             target = (uint64_t)(((llima_u128)uniform32(P.u_resample[b]) * total) >> 32);
             for (int j = 0; j < P.S; ++j) {
-                const uint64_t sj = load_coherent(&sums[j]);
+                const uint64_t sj = sums[j];
                 if (before + sj > target) { chunk = j; break; }
                 before += sj;
             }
@@ -253,29 +286,20 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
         uint64_t sub = 0;
         for (int i = lo; i < hi; ++i) sub += draw_weight(q, i);
         uint64_t tot;
-        uint64_t acc = s_before + block_excl_scan_u64(sub, &tot, bs);
+        uint64_t a = s_before + block_excl_scan_u64(sub, &tot, sh.bs);
         const uint64_t target = s_target;
-        if (sub > 0 && acc <= target && target < acc + sub) {
+        if (sub > 0 && a <= target && target < a + sub) {
             for (int i = lo; i < hi; ++i) {
-                acc += draw_weight(q, i);
-                if (acc > target) { s_tok = i; break; }
+                a += draw_weight(q, i);
+                if (a > target) { s_tok = i; break; }
             }
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        P.emitted[(size_t)b * (P.D + 1) + k] = s_tok;
-        // leave the workspace zeroed for the next call
-        for (int j = 0; j <= P.D; ++j) {
-            const int r1 = trow(P, b, j);
-            P.ws[r1].row_max = 0; P.ws[r1].row_z = 0; P.ws[r1].row_wx = 0;
-            if (j < P.D) {
-                const int r2 = drow(P, b, j);
-                P.ws[r2].row_max = 0; P.ws[r2].row_z = 0; P.ws[r2].row_wx = 0;
-            }
-        }
-    }
+    if (threadIdx.x == 0) P.emitted[(size_t)b * (P.D + 1) + acc] = s_tok;
 }
+
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace llima
 
@@ -283,7 +307,9 @@ using namespace llima;
 
 extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, int32_t V) {
     if (B <= 0 || D < 0 || V <= 0) return 0;
-    return (size_t)B * (2 * D + 1) * sizeof(VRowSlot);
+    const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
+    const size_t NR = (size_t)B * (2 * D + 1);
+    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + al256((size_t)B * S * 8);
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -293,7 +319,7 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
                                       size_t workspace_bytes, void* stream) {
     if (!target_logits || !u_resample || !accepted_len || !emitted) return LLIMA_E_INVAL;
     if (D > 0 && (!draft_logits || !draft_ids || !u_accept)) return LLIMA_E_INVAL;
-    if (B < 0 || D < 0 || V <= 0 || V > (1 << 22)) return LLIMA_E_INVAL;
+    if (B < 0 || D < 0 || D > VR_MAX_D || V <= 0 || V > (1 << 22)) return LLIMA_E_INVAL;
     if ((uintptr_t)target_logits % 16 || (D > 0 && (uintptr_t)draft_logits % 16) || V % 4)
         return LLIMA_E_INVAL;                  // rows are read with 16-byte loads
     if (B == 0) return LLIMA_OK;
@@ -306,11 +332,16 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.B = B; P.D = D; P.V = V;
     P.S = (V + VR_CHUNK - 1) / VR_CHUNK;
     P.NR = B * (2 * D + 1);
-    P.ws = (VRowSlot*)workspace;
+    char* w = (char*)workspace;
+    P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
+    P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
+    P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
+    P.res = (uint64_t*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
     hipLaunchKernelGGL(vr_rowmax, dim3(g12), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_rowsum, dim3(g12), dim3(LLIMA_WG), 0, st, P);
-    hipLaunchKernelGGL(vr_draw, dim3((uint32_t)B * (uint32_t)P.S), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.S), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }

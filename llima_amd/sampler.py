@@ -74,9 +74,9 @@ class SamplerConfig:
 
 
 class Workspace:
-    """Per-device zero-filled scratch buffers, grown on demand (the kernels
-    leave them zero-filled).  Allocation happens only when a call needs more
-    than any earlier call on that device."""
+    """Per-device scratch buffers, grown on demand.  The kernels keep no state
+    in them between calls, so one buffer serves calls of any shape; allocation
+    happens only when a call needs more than any earlier call on that device."""
     _bufs: dict = {}
 
     @classmethod
@@ -84,7 +84,7 @@ class Workspace:
         key = (device.index, kind)
         buf = cls._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
             cls._bufs[key] = buf
         return buf
 

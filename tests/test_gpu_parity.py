@@ -329,7 +329,7 @@ def test_verify_rejection_edges(gpu, oracle):
 
 def test_workspace_reuse_across_shapes(gpu, oracle):
     """One workspace buffer per entry point serves calls of any shape, in any
-    order (per-row workspace slots; control words left zero by every call)."""
+    order (the kernels keep no state in the workspace between calls)."""
     import llima_amd
     _say("workspace reuse across shapes")
     rng = np.random.default_rng(77)
