@@ -27,7 +27,8 @@
 
 namespace llima {
 
-// Workspace: [rows][S] chunk keys (uint64).  Nothing persists between calls.
+// Workspace: [rows][S] chunk keys (uint64) then [rows][S] flags (uint32).
+// Nothing persists between calls.
 #define ARGMAX_MIN_CHUNK 2048
 #define ARGMAX_MAX_GROUP 1024       // rows of one sequence / of one tree
 
@@ -39,6 +40,7 @@ struct ArgmaxParams {
     int32_t* out_ids;
     float* out_vals;
     uint64_t* keys;                // [rows][S]
+    uint32_t* flags;               // [rows][S]: chunk meets a split led by NaN
     int32_t B, V, S, split_dim, mode, vec_ok;
     // epilogues
     int32_t epi, D;                // chain: rows per sequence = D + 1
@@ -79,7 +81,11 @@ __device__ __forceinline__ int64_t split_begin(int s, int V, int sd, int mode) {
     return mode == LLIMA_ARGMAX_QUARTERS ? (int64_t)V * s / 4 : (int64_t)s * sd;
 }
 
-template <typename TL, int E>
+// VEC: rows 16-byte aligned and V a multiple of the values per load: every
+// chunk is read with 16-byte loads from clamped, always-valid addresses, the
+// out-of-row values are masked in registers, and all loads are in flight
+// before the first compare.
+template <typename TL, int E, bool VEC>
 __global__ __launch_bounds__(LLIMA_WG) void argmax_sweep(ArgmaxParams P) {
     constexpr int EPL = 16 / sizeof(TL);
     constexpr int NL = E / EPL;
@@ -94,72 +100,96 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_sweep(ArgmaxParams P) {
     const int V = P.V;
     const int c0 = (int)chunk * CHUNK;
     const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
-    const int sd = (P.split_dim <= 0 || P.split_dim >= V) ? V : P.split_dim;
 
+    llima_u32x4 q[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        if constexpr (VEC) {
+            const int ia = i0 < V ? i0 : V - EPL;
+            q[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+        } else {
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const int ia = i0 + e < V ? i0 + e : V - 1;
+                const float f = ld1<TL>(rowp, ia);
+                if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
+                else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+            }
+            q[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
     // Splits whose first value is NaN are invisible (argmax_bf16 starts its
-    // running maximum at values[0]).  Rare: detected per chunk, handled slowly.
+    // running maximum at values[0]).  Rare: flagged here, the row is then
+    // redone exactly by the finish kernel.
     if (threadIdx.x == 0) bad_splits = 0;
     __syncthreads();
     if (P.mode != LLIMA_ARGMAX_NEG_INF) {
+        const int sd = (P.split_dim <= 0 || P.split_dim >= V) ? V : P.split_dim;
         const int s_lo = split_of(c0, V, sd, P.mode), s_hi = split_of(c1 - 1, V, sd, P.mode);
         for (int s = s_lo + (int)threadIdx.x; s <= s_hi; s += LLIMA_WG) {
             const float f = ld1<TL>(rowp, split_begin(s, V, sd, P.mode));
             if (f != f) bad_splits = 1u;
         }
     }
-    __syncthreads();
-    const uint32_t bad = bad_splits;
 
     float best = -__builtin_inff();
     uint32_t bidx = 0xFFFFFFFFu;
-    if (bad == 0) {
 #pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-            float t[EPL];
-            if (P.vec_ok && i0 + EPL <= c1) {
-                const llima_u32x4 q = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
-                if constexpr (sizeof(TL) == 4) {
-                    t[0] = __uint_as_float(q.x); t[1] = __uint_as_float(q.y);
-                    t[2] = __uint_as_float(q.z); t[3] = __uint_as_float(q.w);
-                } else {
-                    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        float t[EPL];
+        const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+        if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        t[2 * e] = __uint_as_float(w4[e] << 16);
-                        t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-                    }
-                }
-            } else {
+            for (int e = 0; e < 4; ++e) t[e] = __uint_as_float(w4[e]);
+        } else {
 #pragma unroll
-                for (int e = 0; e < EPL; ++e)
-                    t[e] = (i0 + e < c1) ? ld1<TL>(rowp, i0 + e) : -__builtin_inff();
+            for (int e = 0; e < 4; ++e) {
+                t[2 * e] = __uint_as_float(w4[e] << 16);
+                t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
             }
+        }
 #pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                if (t[e] > best) { best = t[e]; bidx = (uint32_t)(i0 + e); }
-        }
-    } else {
-        // element-wise: skip values whose split starts with NaN
-        for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) {
-            const float f = ld1<TL>(rowp, split_begin(split_of(i, V, sd, P.mode), V, sd, P.mode));
-            if (f != f) continue;
-            const float x = ld1<TL>(rowp, i);
-            if (x > best) { best = x; bidx = (uint32_t)i; }
-        }
+        for (int e = 0; e < EPL; ++e)
+            if (t[e] > best && i0 + e < c1) { best = t[e]; bidx = (uint32_t)(i0 + e); }
     }
-    const uint64_t key = block_max_u64(pack_best(best, bidx), bs);
-    if (threadIdx.x == 0) P.keys[(size_t)row * P.S + chunk] = key;
+    const uint64_t key = block_max_u64(pack_best(best, bidx), bs);   // barrier: bad_splits final
+    if (threadIdx.x == 0) {
+        P.keys[(size_t)row * P.S + chunk] = key;
+        P.flags[(size_t)row * P.S + chunk] = bad_splits;
+    }
 }
 
 // Row result from its S chunk keys (one wavefront).  An all -inf row gives id 0.
+// A row with a NaN-led split is rescanned exactly by the wavefront.
 template <typename TL>
 __device__ __forceinline__ int32_t row_result(const ArgmaxParams& P, int row, float* val) {
     const uint64_t* k = P.keys + (size_t)row * P.S;
-    uint64_t best = 0;
-    for (int i = (int)lane_id(); i < P.S; i += 64) best = k[i] > best ? k[i] : best;
-    best = wave_max_u64(best);
+    const uint32_t* fl = P.flags + (size_t)row * P.S;
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    uint64_t best = 0;
+    uint32_t bad = 0;
+    for (int i = (int)lane_id(); i < P.S; i += 64) {
+        best = k[i] > best ? k[i] : best;
+        bad |= fl[i];
+    }
+    best = wave_max_u64(best);
+    bad = wave_max_u32(bad);
+    if (bad) {
+        const int V = P.V;
+        const int sd = (P.split_dim <= 0 || P.split_dim >= V) ? V : P.split_dim;
+        float bv = -__builtin_inff();
+        uint32_t bi = 0xFFFFFFFFu;
+        for (int i = (int)lane_id(); i < V; i += 64) {
+            const float f = ld1<TL>(rowp, split_begin(split_of(i, V, sd, P.mode), V, sd, P.mode));
+            if (f != f) continue;
+            const float x = ld1<TL>(rowp, i);
+            if (x > bv) { bv = x; bi = (uint32_t)i; }
+        }
+        best = wave_max_u64(pack_best(bv, bi));
+    }
     int32_t id = 0;
     float v = -__builtin_inff();
     if (best) { id = (int32_t)(~(uint32_t)best); v = ld1<TL>(rowp, id); }
@@ -232,6 +262,8 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_finish(ArgmaxParams P) {
     }
 }
 
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 struct ATile { int E, S; };
 static ATile argmax_tile(int B, int V, int dtype) {
     // 16 KB per workgroup streams best on MI355X; smaller when the grid is small.
@@ -243,8 +275,9 @@ static ATile argmax_tile(int B, int V, int dtype) {
 
 template <typename TL, int E>
 static hipError_t launch_argmax(const ArgmaxParams& P, hipStream_t st) {
-    hipLaunchKernelGGL((argmax_sweep<TL, E>), dim3((uint32_t)P.B * (uint32_t)P.S), dim3(LLIMA_WG),
-                       0, st, P);
+    const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
+    if (P.vec_ok) hipLaunchKernelGGL((argmax_sweep<TL, E, true>), g, b, 0, st, P);
+    else hipLaunchKernelGGL((argmax_sweep<TL, E, false>), g, b, 0, st, P);
     const uint32_t nfin = P.epi == EPI_NONE ? (uint32_t)(P.B + LLIMA_WAVES - 1) / LLIMA_WAVES
                         : P.epi == EPI_CHAIN ? (uint32_t)(P.B / (P.D + 1)) : 1u;
     hipLaunchKernelGGL((argmax_finish<TL>), dim3(nfin), dim3(LLIMA_WG), 0, st, P);
@@ -255,7 +288,9 @@ static int run_argmax(ArgmaxParams& P, int dtype, hipStream_t st) {
     const ATile t = argmax_tile(P.B, P.V, dtype);
     P.S = t.S;
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
-    P.vec_ok = ((uintptr_t)P.logits % 16 == 0) && ((P.row_stride * (int64_t)esz) % 16 == 0);
+    P.vec_ok = ((uintptr_t)P.logits % 16 == 0) && ((P.row_stride * (int64_t)esz) % 16 == 0) &&
+               (P.V % (int32_t)(16 / esz) == 0);
+    P.flags = (uint32_t*)((char*)P.keys + align256((size_t)P.B * t.S * sizeof(uint64_t)));
     hipError_t e;
     if (dtype == LLIMA_F32) {
         switch (t.E) {
@@ -274,7 +309,6 @@ static int run_argmax(ArgmaxParams& P, int dtype, hipStream_t st) {
     return e == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }
 
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace llima
 
@@ -283,7 +317,8 @@ using namespace llima;
 extern "C" size_t llima_argmax_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
     (void)dtype;
     if (B <= 0 || V <= 0) return 0;
-    return align256((size_t)B * ((V + ARGMAX_MIN_CHUNK - 1) / ARGMAX_MIN_CHUNK) * sizeof(uint64_t));
+    const size_t n = (size_t)B * ((V + ARGMAX_MIN_CHUNK - 1) / ARGMAX_MIN_CHUNK);
+    return align256(n * sizeof(uint64_t)) + align256(n * sizeof(uint32_t));
 }
 
 extern "C" int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_t V,

@@ -42,6 +42,7 @@ namespace llima {
 #define SAMPLE_EXC_CAP 512                         // distinct history ids per chunk
 #define SAMPLE_MIN_CHUNK 2048                      // 256 threads x E = 8
 #define SAMPLE_SEG 8192                            // full-row path segment
+#define SAMPLE_HBATCH 8                            // history ids per thread loaded up front
 
 #define HDR_OVERFLOW 1u
 #define HDR_FILTERED 2u
@@ -128,11 +129,14 @@ __device__ __forceinline__ float load_one<uint16_t>(const uint16_t* rowp, int i)
     return bf16_bits_to_f32(rowp[i]);
 }
 
-// Counts the row's history ids in [lo, lo + nslots*2) into an LDS table of
-// packed u16 counts; with exc, lists the distinct ids (first occurrence).
+// Counts the row's history ids in [lo, hi) into an LDS table of packed u16
+// counts.  With exc_id, lists the distinct ids (first occurrence wins the slot)
+// with their raw logits, fetched here so that the load overlaps the scan.
+template <typename TL>
 __device__ __forceinline__ void count_history(const SampleParams& P, int row, int hlen, int lo,
                                               int hi, uint32_t* table, int nwords,
-                                              int32_t* exc_id, uint32_t* n_exc) {
+                                              int32_t* exc_id, float* exc_raw, uint32_t* n_exc,
+                                              const TL* rowp) {
     for (int i = threadIdx.x; i < nwords; i += LLIMA_WG) table[i] = 0;
     __syncthreads();
     const int32_t* h = P.hist + (size_t)row * P.H_max;
@@ -144,7 +148,10 @@ __device__ __forceinline__ void count_history(const SampleParams& P, int row, in
             const uint32_t old = atomicAdd(&table[off >> 1], 1u << sh16);
             if (exc_id && ((old >> sh16) & 0xFFFFu) == 0) {
                 const uint32_t slot = atomicAdd(n_exc, 1u);
-                if (slot < SAMPLE_EXC_CAP) exc_id[slot] = id;
+                if (slot < SAMPLE_EXC_CAP) {
+                    exc_id[slot] = id;
+                    exc_raw[slot] = load_one<TL>(rowp, id);
+                }
             }
         }
     }
@@ -156,14 +163,17 @@ template <int CHUNK>
 struct SweepShared {
     uint32_t cnt[CHUNK / 2];
     int32_t exc_id[SAMPLE_EXC_CAP];
-    float exc_val[SAMPLE_EXC_CAP];
+    float exc_val[SAMPLE_EXC_CAP];           // raw, then penalised value
     uint64_t pre[SAMPLE_PRECAP];
     uint32_t n_exc, n_pre;
     uint32_t wave_bound[LLIMA_WAVES];
     BlockScratch bs;
 };
 
-template <typename TL, int E>
+// VEC: rows are 16-byte aligned and V is a multiple of the values per load, so
+// every chunk (also a row's partial last one) is read with 16-byte loads from
+// clamped, always-valid addresses and the out-of-row values masked in registers.
+template <typename TL, int E, bool VEC>
 __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
     constexpr int NL = E / EPL;                // loads per thread
@@ -181,32 +191,95 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     const int nw = (V + 31) >> 5;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
 
-    // ---- 1. issue the chunk's loads first
+    const RowCfg c = load_cfg(P, row);
+    const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+
+    // ---- 0. clear the chunk's history table
+    if (c.pen)
+        for (int i = threadIdx.x; i < CHUNK / 2; i += LLIMA_WG) sh.cnt[i] = 0;
+    if (threadIdx.x == 0) { sh.n_exc = 0; sh.n_pre = 0; }
+    __syncthreads();
+
+    // ---- 1. issue the loads, oldest first in the order they are consumed:
+    //         mask words, the first batch of history ids, then the chunk itself.
+    //         Every address is valid; nothing waits until all are in flight.
+    uint32_t mword[NL];
+    if (mrow) {
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+            mword[j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NL; ++j) mword[j] = 0xFFFFFFFFu;
+    }
+    // history ids: whether slot b holds a real id (j < hlen) is decided only
+    // when it is counted
+    int32_t hid[SAMPLE_HBATCH];
+    if (c.pen) {
+#pragma unroll
+        for (int b = 0; b < SAMPLE_HBATCH; ++b) {
+            const int j = (int)threadIdx.x + b * LLIMA_WG;
+            hid[b] = hrow[j < c.hlen ? j : 0];
+        }
+    }
     llima_u32x4 raw[NL];
-    uint32_t mbits[NL];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-        if (P.vec_ok && i0 + EPL <= c1) {
-            raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
+        if constexpr (VEC) {
+            const int ia = i0 < V ? i0 : V - EPL;
+            raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
         } else {
             uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                const float f = (i0 + e < c1) ? load_one<TL>(rowp, i0 + e) : NEG_INF;
+                const int ia = i0 + e < V ? i0 + e : V - 1;
+                const float f = load_one<TL>(rowp, ia);
                 if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
                 else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
             }
             raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
         }
-        mbits[j] = (mrow && i0 < c1) ? (mrow[i0 >> 5] >> (i0 & 31)) : 0xFFFFFFFFu;
     }
-    const RowCfg c = load_cfg(P, row);
 
-    // ---- 2. while they are in flight: the chunk's history counts
-    if (threadIdx.x == 0) { sh.n_exc = 0; sh.n_pre = 0; }
-    if (c.pen) count_history(P, row, c.hlen, c0, c1, sh.cnt, CHUNK / 2, sh.exc_id, &sh.n_exc);
-    else __syncthreads();
+    // ---- 2. while the chunk is in flight: count the history ids of the chunk;
+    //         distinct ids become exceptions
+    if (c.pen) {
+        auto count = [&](int32_t id) {
+            if (id >= c0 && id < c1) {
+                const uint32_t off = (uint32_t)(id - c0);
+                const uint32_t sh16 = (off & 1u) * 16u;
+                const uint32_t old = atomicAdd(&sh.cnt[off >> 1], 1u << sh16);
+                if (((old >> sh16) & 0xFFFFu) == 0) {
+                    const uint32_t slot = atomicAdd(&sh.n_exc, 1u);
+                    if (slot < SAMPLE_EXC_CAP) sh.exc_id[slot] = id;
+                }
+            }
+        };
+#pragma unroll
+        for (int b = 0; b < SAMPLE_HBATCH; ++b)
+            if ((int)threadIdx.x + b * LLIMA_WG < c.hlen) count(hid[b]);
+        for (int j = (int)threadIdx.x + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG)
+            count(hrow[j]);
+    }
+    __syncthreads();
+    // raw logits of the exceptions (issued now, consumed after the chunk)
+    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
+    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
+    float exc_raw[SAMPLE_EXC_CAP / LLIMA_WG];
+#pragma unroll
+    for (int q = 0; q < SAMPLE_EXC_CAP / LLIMA_WG; ++q) {
+        const uint32_t j = threadIdx.x + q * LLIMA_WG;
+        exc_raw[q] = j < n_exc_c ? load_one<TL>(rowp, sh.exc_id[j]) : 0.0f;
+    }
+    uint32_t mbits[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        mbits[j] = mword[j] >> (i0 & 31);
+    }
 
     // ---- 3. values after mask / NaN / history exclusion
     float v[E];
@@ -237,25 +310,28 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         for (int e = 0; e < EPL; ++e) {
             float x = t[e];
             const bool hist_hit = ((cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) != 0;
-            if (x != x || !((mbits[j] >> e) & 1u) || hist_hit) x = NEG_INF;
+            if (x != x || !((mbits[j] >> e) & 1u) || hist_hit || i0 + e >= c1) x = NEG_INF;
             v[j * EPL + e] = x;
         }
     }
 
     // ---- 4. exceptions: distinct history ids of this chunk, penalised exactly
-    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
-    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
     uint32_t flags = n_exc > SAMPLE_EXC_CAP ? HDR_OVERFLOW : 0u;
     float tmax = NEG_INF;
-    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-        const int id = sh.exc_id[j];
-        float l = load_one<TL>(rowp, id);
-        if (l != l) l = NEG_INF;
-        if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) l = NEG_INF;
-        l = penalize(l, table_count(sh.cnt, (uint32_t)(id - c0)), c);
-        sh.exc_val[j] = l;
-        tmax = l > tmax ? l : tmax;
+#pragma unroll
+    for (int q = 0; q < SAMPLE_EXC_CAP / LLIMA_WG; ++q) {
+        const uint32_t j = threadIdx.x + q * LLIMA_WG;
+        if (j < n_exc_c) {
+            const int id = sh.exc_id[j];
+            float l = exc_raw[q];
+            if (l != l) l = NEG_INF;
+            if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) l = NEG_INF;
+            l = penalize(l, table_count(sh.cnt, (uint32_t)(id - c0)), c);
+            sh.exc_val[j] = l;
+            tmax = l > tmax ? l : tmax;
+        }
     }
+    __syncthreads();
 
     ChunkHdr* hdr = P.hdr + (size_t)row * P.S + chunk;
     if (c.greedy) {
@@ -343,6 +419,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
 }
 
 // ================================================================== finish
+#define SMALL_K 256                                // brute-force path: one element per thread
+
 struct FinishShared {
     union {
         uint64_t cbuf[SAMPLE_FIN_CAP];         // gathered candidates
@@ -351,6 +429,9 @@ struct FinishShared {
     uint32_t hcnt[256];
     uint64_t hmass[256];
     uint32_t off[LLIMA_WG];
+    uint32_t kkey[SMALL_K], kid[SMALL_K];      // the top-k survivors (small path)
+    uint64_t kw[SMALL_K], kwf[SMALL_K];
+    uint32_t nk;
     uint32_t sel;
     uint64_t sel64, sel64b;
     BlockScratch bs;
@@ -358,46 +439,73 @@ struct FinishShared {
 
 // ------------------------------------------------------------------ radix selects
 // Each select runs over a set of (key, id, weight) elements presented by a
-// visitor; every thread visits its own elements.  Histograms live in LDS; the
-// boundary bin of each 8-bit digit is found with one workgroup scan.
+// visitor; every thread visits its own elements.  Digits are 8 bits wide and
+// start at the highest bit in which the visited keys differ (the bits above it
+// are common to all of them), so the first histogram already spreads the keys.
+struct Digits {
+    uint32_t prefix, pmask;   // fixed high bits of the selected key
+    int top;                  // top bit of the next digit (-1: done)
+};
 
-// k-th largest key (with multiplicity) among visited elements.
+__device__ __forceinline__ Digits digits_init(uint32_t kmin, uint32_t kmax) {
+    Digits d;
+    const uint32_t diff = kmax ^ kmin;
+    if (diff == 0) { d.prefix = kmax; d.pmask = 0xFFFFFFFFu; d.top = -1; return d; }
+    d.top = 31 - __builtin_clz(diff);
+    d.pmask = d.top == 31 ? 0u : ~((2u << d.top) - 1u);
+    d.prefix = kmax & d.pmask;
+    return d;
+}
+
+// k-th largest key (with multiplicity) among visited elements, all of whose
+// keys lie in [kmin, kmax].
 template <class Visit>
-__device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, FinishShared& sh) {
-    uint32_t prefix = 0, pmask = 0, rem = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
+__device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, uint32_t kmin,
+                                                    uint32_t kmax, FinishShared& sh) {
+    Digits d = digits_init(kmin, kmax);
+    uint32_t rem = k;
+    while (d.top >= 0) {
+        const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+        const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
         sh.hcnt[threadIdx.x] = 0;
         __syncthreads();
+        const uint32_t prefix = d.prefix, pmask = d.pmask;
         visit([&](uint32_t key, uint32_t, uint64_t) {
-            if ((key & pmask) == prefix) atomicAdd(&sh.hcnt[(key >> shift) & 255u], 1u);
+            if ((key & pmask) == prefix) atomicAdd(&sh.hcnt[(key >> lo) & bmask], 1u);
         });
         __syncthreads();
         const uint32_t bin = 255u - threadIdx.x;          // thread 0 <-> top bin
-        uint32_t c = sh.hcnt[bin], tot;
-        uint32_t above = block_excl_scan_u32(c, &tot, sh.bs);
+        const uint32_t c = sh.hcnt[bin];
+        uint32_t tot;
+        const uint32_t above = block_excl_scan_u32(c, &tot, sh.bs);
         if (above < rem && above + c >= rem) { sh.sel = bin; sh.sel64 = rem - above; }
         __syncthreads();
-        prefix |= sh.sel << shift;
-        pmask |= 255u << shift;
+        d.prefix |= sh.sel << lo;
+        d.pmask |= bmask << lo;
+        d.top = lo - 1;
         rem = (uint32_t)sh.sel64;
         __syncthreads();
     }
-    return prefix;
+    return d.prefix;
 }
 
 // Top-p boundary: the smallest key theta such that an element with key theta has
 // (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
 template <class Visit>
-__device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ, FinishShared& sh) {
-    uint32_t prefix = 0, pmask = 0;
+__device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ, uint32_t kmin,
+                                                     uint32_t kmax, FinishShared& sh) {
+    Digits d = digits_init(kmin, kmax);
     uint64_t acc = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
+    while (d.top >= 0) {
+        const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+        const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
         sh.hcnt[threadIdx.x] = 0;
         sh.hmass[threadIdx.x] = 0;
         __syncthreads();
+        const uint32_t prefix = d.prefix, pmask = d.pmask;
         visit([&](uint32_t key, uint32_t, uint64_t w) {
             if ((key & pmask) == prefix) {
-                const uint32_t b = (key >> shift) & 255u;
+                const uint32_t b = (key >> lo) & bmask;
                 atomicAdd(&sh.hcnt[b], 1u);
                 if (w) atomicAdd((unsigned long long*)&sh.hmass[b], (unsigned long long)w);
             }
@@ -414,27 +522,31 @@ __device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ,
         const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
         if (t == sel_t) { sh.sel = bin; sh.sel64 = above; }
         __syncthreads();
-        prefix |= sh.sel << shift;
-        pmask |= 255u << shift;
+        d.prefix |= sh.sel << lo;
+        d.pmask |= bmask << lo;
+        d.top = lo - 1;
         acc = sh.sel64;
         __syncthreads();
     }
-    return prefix;
+    return d.prefix;
 }
 
 // Draw: the smallest id whose ascending-id prefix mass exceeds target; also
-// returns that element's weight.  Ids are < 2^24.
+// returns that element's weight.  Ids are < V <= 2^24.
 template <class Visit>
-__device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target, uint64_t* w_out,
-                                                    FinishShared& sh) {
-    uint32_t prefix = 0, pmask = 0;
+__device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target, uint32_t V,
+                                                    uint64_t* w_out, FinishShared& sh) {
+    Digits d = digits_init(0u, V > 1 ? V - 1 : 1u);
     uint64_t acc = 0;
-    for (int shift = 16; shift >= 0; shift -= 8) {
+    while (d.top >= 0) {
+        const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+        const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
         sh.hmass[threadIdx.x] = 0;
         __syncthreads();
+        const uint32_t prefix = d.prefix, pmask = d.pmask;
         visit([&](uint32_t, uint32_t id, uint64_t w) {
             if (w && (id & pmask) == prefix)
-                atomicAdd((unsigned long long*)&sh.hmass[(id >> shift) & 255u], (unsigned long long)w);
+                atomicAdd((unsigned long long*)&sh.hmass[(id >> lo) & bmask], (unsigned long long)w);
         });
         __syncthreads();
         const uint32_t bin = threadIdx.x;
@@ -444,13 +556,14 @@ __device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target
             sh.sel = bin; sh.sel64 = below; sh.sel64b = m;
         }
         __syncthreads();
-        prefix |= sh.sel << shift;
-        pmask |= 255u << shift;
+        d.prefix |= sh.sel << lo;
+        d.pmask |= bmask << lo;
+        d.top = lo - 1;
         acc = sh.sel64;
         *w_out = sh.sel64b;
         __syncthreads();
     }
-    return prefix;
+    return d.prefix;
 }
 
 __device__ __forceinline__ void write_result(const SampleParams& P, int row, int32_t id, float prob) {
@@ -488,7 +601,9 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     auto for_each_x = [&](auto fn) {
         for (int lo = 0; lo < V; lo += SAMPLE_SEG) {
             const int hi = lo + SAMPLE_SEG < V ? lo + SAMPLE_SEG : V;
-            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2, nullptr, nullptr);
+            if (c.pen)
+                count_history<TL>(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2, nullptr, nullptr,
+                                  nullptr, rowp);
             for (int i = lo + threadIdx.x; i < hi; i += LLIMA_WG) {
                 float l = load_one<TL>(rowp, i);
                 if (l != l) l = -__builtin_inff();
@@ -518,13 +633,18 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         return;
     }
 
-    // Pass: maximum and number of finite values.
-    uint32_t kmax = 0, nfin = 0;
+    // Pass: maximum, minimum and number of finite values.
+    uint32_t kmax = 0, nkmin = 0, nfin = 0;
     for_each_x([&](float x, uint32_t) {
         const uint32_t k = f32_key(x);
-        if (k > LLIMA_KEY_NEG_INF) { nfin++; kmax = k > kmax ? k : kmax; }
+        if (k > LLIMA_KEY_NEG_INF) {
+            nfin++;
+            kmax = k > kmax ? k : kmax;
+            nkmin = ~k > nkmin ? ~k : nkmin;
+        }
     });
     kmax = block_max_u32(kmax, sh.bs);
+    const uint32_t kmin = ~block_max_u32(nkmin, sh.bs);
     nfin = block_sum_u32(nfin, sh.bs);
     if (nfin == 0) {
         if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
@@ -539,7 +659,8 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         });
     };
     uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
-    if (c.k > 0 && (uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, sh);
+    if (c.k > 0 && (uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, kmin, kmax, sh);
+    const uint32_t kmin_k = tau > kmin ? tau : kmin;
 
     auto visit_k = [&](auto fn) {
         for_each_x([&](float x, uint32_t id) {
@@ -553,7 +674,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         visit_k([&](uint32_t, uint32_t, uint64_t w) { Z += w; });
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc(visit_k, PZ, sh);
+        theta = select_topp_desc(visit_k, PZ, kmin_k, kmax, sh);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     auto visit_final = [&](auto fn) {
@@ -569,7 +690,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
         uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc(visit_final, target, &wtok, sh);
+        tok = (int32_t)select_draw_asc(visit_final, target, (uint32_t)V, &wtok, sh);
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
@@ -580,70 +701,65 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 }
 
 // ------------------------------------------------------------------ fast path
-// Sampling from the gathered candidates.  Returns false when they cannot be
-// proven to contain the kept set (the caller then runs the full-row path).
-__device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, const RowCfg& c,
-                                            uint32_t n, uint32_t flags, uint32_t bound_key,
-                                            FinishShared& sh) {
-    const float NEG_INF = -__builtin_inff();
+// The survivors of top-k held one per thread (at most SMALL_K): top-p, min-p
+// and the draw by direct sums over the LDS copy of the survivors.
+__device__ __forceinline__ void finish_small(const SampleParams& P, int row, const RowCfg& c,
+                                             uint32_t nk, uint32_t kmax, FinishShared& sh) {
+    const uint32_t t = threadIdx.x;
+    const bool mine = t < nk;
+    const uint32_t key = mine ? sh.kkey[t] : 0u;
+    const uint32_t id = mine ? sh.kid[t] : 0u;
+    const uint64_t w = mine ? sh.kw[t] : 0ull;
+    bool fin = mine;
+    if (c.p < 1.0f) {
+        const uint64_t Z = block_sum_u64(w, sh.bs);
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+        uint64_t above = 0;                       // mass strictly above this key
+        for (uint32_t j = 0; j < nk; ++j) above += sh.kkey[j] > key ? sh.kw[j] : 0ull;
+        fin = fin && ((((llima_u128)above << 32) < PZ) || key == kmax);
+    }
+    if (c.m > 0.0f) fin = fin && w >= (frac32(c.m) << 4);
+    if (mine) sh.kwf[t] = fin ? w : 0ull;
+    const uint64_t Zf = block_sum_u64(fin ? w : 0ull, sh.bs);   // barrier also publishes kwf
+    int32_t tok = -1;
+    if (Zf > 0 && fin && w > 0) {
+        const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+        uint64_t upto = 0;                        // mass of final ids <= this id
+        for (uint32_t j = 0; j < nk; ++j) upto += sh.kid[j] <= id ? sh.kwf[j] : 0ull;
+        if (upto - w <= target && target < upto) {
+            tok = (int32_t)id;
+            write_result(P, row, tok, (float)((double)w / (double)Zf));
+        }
+    }
+    if (Zf == 0 && t == 0) write_result(P, row, -1, 0.0f);
+    if (P.out_keep)
+        write_keep(P, row, [&](auto set) { if (fin) set(id); });
+}
+
+// Many survivors (top-k disabled, ties, k > SMALL_K): register-resident
+// candidates (slot j of thread t is candidate t + 256 j) and radix selects.
+__device__ __forceinline__ void finish_large(const SampleParams& P, int row, const RowCfg& c,
+                                             uint32_t n, uint32_t tau, uint32_t kmax,
+                                             FinishShared& sh) {
     uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
-    float xs[SAMPLE_SLOTS];
-    uint32_t kmax = 0;
+    uint64_t w[SAMPLE_SLOTS];
+    const float xmax = key_f32(kmax);
 #pragma unroll
     for (int j = 0; j < SAMPLE_SLOTS; ++j) {
         const uint32_t s = threadIdx.x + j * LLIMA_WG;
-        key[j] = 0; id[j] = 0; xs[j] = NEG_INF;
+        key[j] = 0; id[j] = 0; w[j] = 0;
         if (s < n) {
             const uint64_t q = sh.u.cbuf[s];
-            const float x = __uint_as_float((uint32_t)(q >> 32)) / c.T;
-            xs[j] = x;
-            key[j] = f32_key(x);
+            key[j] = (uint32_t)(q >> 32);
             id[j] = (uint32_t)q;
-            kmax = key[j] > kmax ? key[j] : kmax;
+            if (key[j] >= tau) w[j] = weight(key_f32(key[j]), xmax);
         }
     }
-    kmax = block_max_u32(kmax, sh.bs);
-    if (kmax <= LLIMA_KEY_NEG_INF) {
-        // Every candidate is -inf after the temperature (or there are none).
-        if (flags & HDR_FILTERED) return false;
-        if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
-        if (P.out_keep) write_keep(P, row, [&](auto) {});
-        return true;
-    }
-    const float xmax = key_f32(kmax);
-    auto visit_all = [&](auto fn) {
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j)
-            if (key[j] > LLIMA_KEY_NEG_INF) fn(key[j], id[j], 0ull);
-    };
-
-    // ---- top-k threshold, then the proof that the pre-filter kept every member:
-    // a value below a chunk's lowered bound g has x <= fl(g / T) < tau.
-    uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
-    if (c.k > 0) {
-        uint32_t nfin = 0;
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) nfin += key[j] > LLIMA_KEY_NEG_INF;
-        nfin = block_sum_u32(nfin, sh.bs);
-        if ((uint32_t)c.k <= nfin) tau = select_kth_desc(visit_all, (uint32_t)c.k, sh);
-        else if (flags & HDR_FILTERED) return false;
-        if (flags & HDR_FILTERED) {
-            const float gq = lower_bound_margin(key_f32(bound_key)) / c.T;
-            if (!(gq < key_f32(tau))) return false;
-        }
-    }
-
-    // ---- weights of the top-k survivors
-    uint64_t w[SAMPLE_SLOTS];
-#pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j)
-        w[j] = (key[j] > LLIMA_KEY_NEG_INF && key[j] >= tau) ? weight(xs[j], xmax) : 0ull;
     auto visit_k = [&](auto fn) {
 #pragma unroll
         for (int j = 0; j < SAMPLE_SLOTS; ++j)
-            if (key[j] > LLIMA_KEY_NEG_INF && key[j] >= tau) fn(key[j], id[j], w[j]);
+            if (key[j] >= tau) fn(key[j], id[j], w[j]);
     };
-
     uint32_t theta = 0;
     if (c.p < 1.0f) {
         uint64_t Z = 0;
@@ -651,7 +767,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
         for (int j = 0; j < SAMPLE_SLOTS; ++j) Z += w[j];
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc(visit_k, PZ, sh);
+        theta = select_topp_desc(visit_k, PZ, tau, kmax, sh);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     auto visit_final = [&](auto fn) {
@@ -667,7 +783,7 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
         uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc(visit_final, target, &wtok, sh);
+        tok = (int32_t)select_draw_asc(visit_final, target, (uint32_t)P.V, &wtok, sh);
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
@@ -675,6 +791,78 @@ __device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, cons
         write_keep(P, row, [&](auto set) {
             visit_final([&](uint32_t, uint32_t i, uint64_t) { set(i); });
         });
+}
+
+// Sampling from the gathered candidates (n of them in sh.u.cbuf).  Returns false
+// when they cannot be proven to contain the kept set (the caller then runs the
+// full-row path).
+__device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, const RowCfg& c,
+                                            uint32_t n, uint32_t flags, uint32_t bound_key,
+                                            FinishShared& sh) {
+    // ---- values after the temperature, as keys, in place: (key << 32 | id)
+    uint32_t kmax = 0, nkmin = 0, nfin = 0;
+    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
+        const uint64_t q = sh.u.cbuf[s];
+        const uint32_t k = f32_key(__uint_as_float((uint32_t)(q >> 32)) / c.T);
+        sh.u.cbuf[s] = ((uint64_t)k << 32) | (uint32_t)q;
+        if (k > LLIMA_KEY_NEG_INF) {
+            nfin++;
+            kmax = k > kmax ? k : kmax;
+            nkmin = ~k > nkmin ? ~k : nkmin;
+        }
+    }
+    kmax = block_max_u32(kmax, sh.bs);
+    const uint32_t kmin = ~block_max_u32(nkmin, sh.bs);
+    nfin = block_sum_u32(nfin, sh.bs);
+    if (nfin == 0) {
+        // Every candidate is -inf after the temperature (or there are none).
+        if (flags & HDR_FILTERED) return false;
+        if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
+        if (P.out_keep) write_keep(P, row, [&](auto) {});
+        return true;
+    }
+
+    // ---- top-k threshold, then the proof that the pre-filter kept every member:
+    // a value below a chunk's lowered bound g has x <= fl(g / T) < tau.
+    uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
+    if (c.k > 0) {
+        auto visit_fin = [&](auto fn) {
+            for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
+                const uint32_t k = (uint32_t)(sh.u.cbuf[s] >> 32);
+                if (k > LLIMA_KEY_NEG_INF) fn(k, 0u, 0ull);
+            }
+        };
+        if ((uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, kmin, kmax, sh);
+        else if (flags & HDR_FILTERED) return false;
+        if (flags & HDR_FILTERED) {
+            const float gq = lower_bound_margin(key_f32(bound_key)) / c.T;
+            if (!(gq < key_f32(tau))) return false;
+        }
+    }
+
+    // ---- survivors of top-k: one per thread when few
+    uint32_t cnt = 0;
+    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) cnt += (uint32_t)(sh.u.cbuf[s] >> 32) >= tau;
+    const uint32_t nk = block_sum_u32(cnt, sh.bs);
+    if (nk > SMALL_K) {
+        finish_large(P, row, c, n, tau, kmax, sh);
+        return true;
+    }
+    if (threadIdx.x == 0) sh.nk = 0;
+    __syncthreads();
+    const float xmax = key_f32(kmax);
+    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
+        const uint64_t q = sh.u.cbuf[s];
+        const uint32_t k = (uint32_t)(q >> 32);
+        if (k >= tau) {
+            const uint32_t slot = atomicAdd(&sh.nk, 1u);
+            sh.kkey[slot] = k;
+            sh.kid[slot] = (uint32_t)q;
+            sh.kw[slot] = weight(key_f32(k), xmax);
+        }
+    }
+    __syncthreads();
+    finish_small(P, row, c, nk, kmax, sh);
     return true;
 }
 
@@ -760,8 +948,9 @@ static int max_chunks(int V) { return (V + SAMPLE_MIN_CHUNK - 1) / SAMPLE_MIN_CH
 
 template <typename TL, int E>
 static void launch_sweep(const SampleParams& P, hipStream_t st) {
-    hipLaunchKernelGGL((sample_sweep<TL, E>), dim3((uint32_t)P.B * (uint32_t)P.S), dim3(LLIMA_WG),
-                       0, st, P);
+    const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
+    if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true>), g, b, 0, st, P);
+    else hipLaunchKernelGGL((sample_sweep<TL, E, false>), g, b, 0, st, P);
 }
 
 }  // namespace llima
@@ -812,7 +1001,8 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.V = V;
     P.H_max = history ? H_max : 0;
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
-    P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0);
+    P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0) &&
+               (V % (int32_t)(16 / esz) == 0);
     const int k_hint = cfg->top_k_rows ? 0 : cfg->top_k;
     const Tile t = choose_tile(B, V, dtype, (k_hint > 0 && k_hint < V) ? k_hint : 0);
     P.S = t.S;

@@ -69,19 +69,25 @@ __device__ __forceinline__ int drow(const VerifyParams& P, int b, int k) {
     return P.B * (P.D + 1) + b * P.D + k;
 }
 
-// Loads the chunk of 32 values per thread (16-byte loads, -inf past the end).
-__device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, float (&v)[VR_E]) {
+// Loads the chunk of 32 values per thread: 16-byte loads from clamped,
+// always-valid addresses (V is a multiple of 4), all in flight before the first
+// use; values past the end of the row become -inf.
+__device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, int V,
+                                           float (&v)[VR_E]) {
+    llima_u32x4 q[VR_E / 4];
 #pragma unroll
     for (int j = 0; j < VR_E / 4; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
-        if (i0 + 4 <= c1) {
-            const llima_u32x4 q = __builtin_nontemporal_load((const llima_u32x4*)(rowp + i0));
-            v[4 * j] = __uint_as_float(q.x); v[4 * j + 1] = __uint_as_float(q.y);
-            v[4 * j + 2] = __uint_as_float(q.z); v[4 * j + 3] = __uint_as_float(q.w);
-        } else {
+        const int ia = i0 < V ? i0 : V - 4;
+        q[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+    }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[4 * j + e] = i0 + e < c1 ? rowp[i0 + e] : -__builtin_inff();
-        }
+    for (int j = 0; j < VR_E / 4; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
+        const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[4 * j + e] = i0 + e < c1 ? __uint_as_float(w4[e]) : -__builtin_inff();
     }
 }
 
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
     const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     float v[VR_E];
-    load_chunk(row_ptr(P, r), c0, c1, v);
+    load_chunk(row_ptr(P, r), c0, c1, P.V, v);
     uint32_t m = 0;
 #pragma unroll
     for (int e = 0; e < VR_E; ++e) {
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
     float v[VR_E];
-    load_chunk(rowp, c0, c1, v);
+    load_chunk(rowp, c0, c1, P.V, v);
     if (threadIdx.x < 64) {
         const uint32_t* m = P.maxk + (size_t)r * P.S;
         uint32_t best = 0;
