@@ -244,48 +244,34 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         }
     }
 
-    // ---- 2. while the chunk is in flight: count the history ids of the chunk;
-    //         distinct ids become exceptions
+    // ---- 2. while the chunk is in flight: count the history ids of the chunk
     if (c.pen) {
-        auto count = [&](int32_t id) {
+#pragma unroll
+        for (int b = 0; b < SAMPLE_HBATCH; ++b) {
+            const int32_t id = hid[b];
+            if ((int)threadIdx.x + b * LLIMA_WG < c.hlen && id >= c0 && id < c1) {
+                const uint32_t off = (uint32_t)(id - c0);
+                atomicAdd(&sh.cnt[off >> 1], 1u << ((off & 1u) * 16u));
+            }
+        }
+        for (int j = (int)threadIdx.x + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
+            const int32_t id = hrow[j];
             if (id >= c0 && id < c1) {
                 const uint32_t off = (uint32_t)(id - c0);
-                const uint32_t sh16 = (off & 1u) * 16u;
-                const uint32_t old = atomicAdd(&sh.cnt[off >> 1], 1u << sh16);
-                if (((old >> sh16) & 0xFFFFu) == 0) {
-                    const uint32_t slot = atomicAdd(&sh.n_exc, 1u);
-                    if (slot < SAMPLE_EXC_CAP) sh.exc_id[slot] = id;
-                }
+                atomicAdd(&sh.cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
-        };
-#pragma unroll
-        for (int b = 0; b < SAMPLE_HBATCH; ++b)
-            if ((int)threadIdx.x + b * LLIMA_WG < c.hlen) count(hid[b]);
-        for (int j = (int)threadIdx.x + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG)
-            count(hrow[j]);
+        }
     }
     __syncthreads();
-    // raw logits of the exceptions (issued now, consumed after the chunk)
-    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
-    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
-    float exc_raw[SAMPLE_EXC_CAP / LLIMA_WG];
-#pragma unroll
-    for (int q = 0; q < SAMPLE_EXC_CAP / LLIMA_WG; ++q) {
-        const uint32_t j = threadIdx.x + q * LLIMA_WG;
-        exc_raw[q] = j < n_exc_c ? load_one<TL>(rowp, sh.exc_id[j]) : 0.0f;
-    }
-    uint32_t mbits[NL];
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-        mbits[j] = mword[j] >> (i0 & 31);
-    }
 
-    // ---- 3. values after mask / NaN / history exclusion
+    // ---- 3. values after mask / NaN; history values leave the stream as
+    //         exceptions (owner thread appends id and raw value), so that the
+    //         stream needs no division
     float v[E];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        const uint32_t mb = mword[j] >> (i0 & 31);
         float t[EPL];
         const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
         if constexpr (sizeof(TL) == 4) {
@@ -309,63 +295,65 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             float x = t[e];
-            const bool hist_hit = ((cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) != 0;
-            if (x != x || !((mbits[j] >> e) & 1u) || hist_hit || i0 + e >= c1) x = NEG_INF;
+            if (x != x || !((mb >> e) & 1u) || i0 + e >= c1) x = NEG_INF;
+            const uint32_t cnt = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+            if (cnt) {
+                const uint32_t slot = atomicAdd(&sh.n_exc, 1u);
+                if (slot < SAMPLE_EXC_CAP) {
+                    sh.exc_id[slot] = i0 + e;
+                    sh.exc_val[slot] = x;
+                }
+                x = NEG_INF;
+            }
             v[j * EPL + e] = x;
-        }
-    }
-
-    // ---- 4. exceptions: distinct history ids of this chunk, penalised exactly
-    uint32_t flags = n_exc > SAMPLE_EXC_CAP ? HDR_OVERFLOW : 0u;
-    float tmax = NEG_INF;
-#pragma unroll
-    for (int q = 0; q < SAMPLE_EXC_CAP / LLIMA_WG; ++q) {
-        const uint32_t j = threadIdx.x + q * LLIMA_WG;
-        if (j < n_exc_c) {
-            const int id = sh.exc_id[j];
-            float l = exc_raw[q];
-            if (l != l) l = NEG_INF;
-            if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) l = NEG_INF;
-            l = penalize(l, table_count(sh.cnt, (uint32_t)(id - c0)), c);
-            sh.exc_val[j] = l;
-            tmax = l > tmax ? l : tmax;
         }
     }
     __syncthreads();
 
+    // ---- 4. exceptions: distinct history ids of this chunk, penalised exactly
+    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
+    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
+    uint32_t flags = n_exc > SAMPLE_EXC_CAP ? HDR_OVERFLOW : 0u;
+    float tmax = NEG_INF;
+    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
+        const int id = sh.exc_id[j];
+        const float l = penalize(sh.exc_val[j], table_count(sh.cnt, (uint32_t)(id - c0)), c);
+        sh.exc_val[j] = l;
+        tmax = l > tmax ? l : tmax;
+    }
+
     ChunkHdr* hdr = P.hdr + (size_t)row * P.S + chunk;
     if (c.greedy) {
-        // ---- argmax: first index of the maximum
-        uint64_t best = 0;
+        // ---- argmax: first index of the maximum (values visited in index order)
+        float best = NEG_INF;
+        uint32_t bidx = 0xFFFFFFFFu;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
             const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const uint64_t kk = ((uint64_t)f32_key(v[j * EPL + e]) << 32) |
-                                    (uint64_t)(~(uint32_t)(i0 + e));
-                best = kk > best ? kk : best;
-            }
+            for (int e = 0; e < EPL; ++e)
+                if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
         }
+        uint64_t kb = best > NEG_INF ? (((uint64_t)f32_key(best) << 32) | (uint64_t)(~bidx)) : 0ull;
         for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-            const uint64_t kk = ((uint64_t)f32_key(sh.exc_val[j]) << 32) |
-                                (uint64_t)(~(uint32_t)sh.exc_id[j]);
-            best = kk > best ? kk : best;
+            const float x = sh.exc_val[j];
+            const uint64_t kk = x > NEG_INF ? (((uint64_t)f32_key(x) << 32) |
+                                               (uint64_t)(~(uint32_t)sh.exc_id[j])) : 0ull;
+            kb = kk > kb ? kk : kb;
         }
-        best = block_max_u64(best, sh.bs);
+        kb = block_max_u64(kb, sh.bs);
         if (threadIdx.x == 0) {
             hdr->count = 0;
             hdr->flags = flags;
             hdr->bound = 0;
-            hdr->greedy = best;
+            hdr->greedy = kb;
         }
         return;
     }
 
-    // ---- 5. pre-filter bound from lane maxima (any bound is safe: the finish
-    //         kernel proves completeness before trusting the candidates)
+    // ---- 5. pre-filter bound from lane maxima: every wave has >= r lanes whose
+    //         maximum is >= its bound, so the chunk has >= 4r >= k values >= t
     float g = NEG_INF;
-    uint32_t tb = 0;
     if (c.k > 0 && c.k <= 4 * 64) {
 #pragma unroll
         for (int e = 0; e < E; ++e) tmax = v[e] > tmax ? v[e] : tmax;
@@ -374,15 +362,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         const uint32_t wb = __shfl(sorted, (int)r - 1, 64);
         if (lane_id() == 0) sh.wave_bound[threadIdx.x >> 6] = wb;
         __syncthreads();
-        tb = sh.wave_bound[0];
+        uint32_t tb = sh.wave_bound[0];
 #pragma unroll
         for (int w = 1; w < LLIMA_WAVES; ++w) tb = sh.wave_bound[w] < tb ? sh.wave_bound[w] : tb;
-        if (tb > LLIMA_KEY_NEG_INF) {
-            g = lower_bound_margin(key_f32(tb));
-            flags |= HDR_FILTERED;
-        }
+        if (tb > LLIMA_KEY_NEG_INF) g = lower_bound_margin(key_f32(tb));
     }
-    // ---- 6. stage candidates in LDS, then copy them to the chunk's slot
+    // ---- 6. stage the values >= g in LDS
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
@@ -390,30 +375,64 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         for (int e = 0; e < EPL; ++e) {
             const float x = v[j * EPL + e];
             if (x > NEG_INF && x >= g) {
-                const uint32_t s = atomicAdd(&sh.n_pre, 1u);
-                if (s < SAMPLE_PRECAP)
-                    sh.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
+                const uint32_t s2 = atomicAdd(&sh.n_pre, 1u);
+                if (s2 < SAMPLE_PRECAP)
+                    sh.pre[s2] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
             }
         }
     }
     for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
         const float x = sh.exc_val[j];
         if (x > NEG_INF && x >= g) {
-            const uint32_t s = atomicAdd(&sh.n_pre, 1u);
-            if (s < SAMPLE_PRECAP)
-                sh.pre[s] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)sh.exc_id[j];
+            const uint32_t s2 = atomicAdd(&sh.n_pre, 1u);
+            if (s2 < SAMPLE_PRECAP)
+                sh.pre[s2] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)sh.exc_id[j];
         }
     }
     __syncthreads();
-    uint32_t n_pre = sh.n_pre;
-    const uint32_t cap = (uint32_t)P.share < SAMPLE_PRECAP ? (uint32_t)P.share : SAMPLE_PRECAP;
-    if (n_pre > cap) { flags |= HDR_OVERFLOW; n_pre = 0; }
+    const uint32_t n_pre = sh.n_pre;
+    if (n_pre > SAMPLE_PRECAP) flags |= HDR_OVERFLOW;
+    const uint32_t n_st = n_pre < SAMPLE_PRECAP ? n_pre : SAMPLE_PRECAP;
+
+    // ---- 7. the chunk's exact k-th largest value tau_c among the staged ones
+    //         (they hold every value >= g, hence the chunk's top k) by rank counting
+    float gout = NEG_INF;
+    uint32_t bound = 0;
+    if (c.k > 0 && n_st >= (uint32_t)c.k && !(flags & HDR_OVERFLOW)) {
+        uint32_t kt = 0;                                      // key of a tau_c candidate
+        for (uint32_t i = threadIdx.x; i < n_st; i += LLIMA_WG) {
+            const float xi = __uint_as_float((uint32_t)(sh.pre[i] >> 32));
+            uint32_t ge = 0;
+            for (uint32_t jj = 0; jj < n_st; ++jj)
+                ge += __uint_as_float((uint32_t)(sh.pre[jj] >> 32)) >= xi;
+            if (ge >= (uint32_t)c.k) { const uint32_t kk = f32_key(xi); kt = kk > kt ? kk : kt; }
+        }
+        bound = block_max_u32(kt, sh.bs);
+        gout = lower_bound_margin(key_f32(bound));
+        flags |= HDR_FILTERED;
+    }
+    // ---- 8. write the chunk's candidates (values >= gout) and its header
+    if (threadIdx.x == 0) sh.n_exc = 0;                      // reused as the output count
+    __syncthreads();
+    const uint32_t cap = (uint32_t)P.share;
     uint64_t* dst = P.cand + ((size_t)row * P.S + chunk) * P.share;
-    for (uint32_t j = threadIdx.x; j < n_pre; j += LLIMA_WG) dst[j] = sh.pre[j];
+    if (!(flags & HDR_OVERFLOW)) {
+        for (uint32_t i = threadIdx.x; i < n_st; i += LLIMA_WG) {
+            const uint64_t q = sh.pre[i];
+            if (__uint_as_float((uint32_t)(q >> 32)) >= gout) {
+                const uint32_t o = atomicAdd(&sh.n_exc, 1u);
+                if (o < cap) dst[o] = q;
+            }
+        }
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        hdr->count = n_pre;
+        uint32_t n_out = sh.n_exc;
+        if (n_out > cap) { flags |= HDR_OVERFLOW; }
+        if (flags & HDR_OVERFLOW) n_out = 0;
+        hdr->count = n_out;
         hdr->flags = flags;
-        hdr->bound = tb;
+        hdr->bound = bound;
         hdr->greedy = 0;
     }
 }
@@ -429,6 +448,7 @@ struct FinishShared {
     uint32_t hcnt[256];
     uint64_t hmass[256];
     uint32_t off[LLIMA_WG];
+    uint8_t cid[SAMPLE_FIN_CAP];               // candidate position -> chunk (S <= 256)
     uint32_t kkey[SMALL_K], kid[SMALL_K];      // the top-k survivors (small path)
     uint64_t kw[SMALL_K], kwf[SMALL_K];
     uint32_t nk;
@@ -901,25 +921,50 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
             done = true;
         }
     } else if (!(fl & HDR_OVERFLOW) && n <= SAMPLE_FIN_CAP) {
-        // ---- gather the candidates into LDS: chunk offsets by a block scan,
-        //      then one wave per chunk copies its slot
-        uint32_t base = 0;
-        for (int g0 = 0; g0 < P.S; g0 += LLIMA_WG) {
-            const int ch = g0 + (int)threadIdx.x;
+        // ---- gather the candidates into LDS
+        if (P.S <= LLIMA_WG) {
+            // chunk offsets by one block scan, a position -> chunk table, then
+            // every thread issues all of its loads before storing any
+            const int ch = (int)threadIdx.x;
             const uint32_t cnt = ch < P.S ? hdr[ch].count : 0u;
             uint32_t tot;
             const uint32_t ex = block_excl_scan_u32(cnt, &tot, sh.bs);
-            sh.off[threadIdx.x] = base + ex;
+            sh.off[threadIdx.x] = ex;
+            for (uint32_t i = 0; i < cnt; ++i) sh.cid[ex + i] = (uint8_t)ch;
             __syncthreads();
-            const int nch = P.S - g0 < LLIMA_WG ? P.S - g0 : LLIMA_WG;
-            for (int k = (int)(threadIdx.x >> 6); k < nch; k += LLIMA_WAVES) {
-                const uint32_t o = sh.off[k];
-                const uint32_t m = hdr[g0 + k].count;
-                const uint64_t* src = P.cand + ((size_t)row * P.S + g0 + k) * P.share;
-                for (uint32_t i = lane_id(); i < m; i += 64) sh.u.cbuf[o + i] = src[i];
+            uint64_t q[SAMPLE_SLOTS];
+#pragma unroll
+            for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+                const uint32_t f = threadIdx.x + j * LLIMA_WG;
+                const uint32_t cc = f < n ? sh.cid[f] : 0u;
+                const uint32_t o = f < n ? f - sh.off[cc] : 0u;
+                q[j] = P.cand[((size_t)row * P.S + cc) * P.share + o];
             }
-            base += tot;
+#pragma unroll
+            for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+                const uint32_t f = threadIdx.x + j * LLIMA_WG;
+                if (f < n) sh.u.cbuf[f] = q[j];
+            }
             __syncthreads();
+        } else {
+            uint32_t base = 0;
+            for (int g0 = 0; g0 < P.S; g0 += LLIMA_WG) {
+                const int ch = g0 + (int)threadIdx.x;
+                const uint32_t cnt = ch < P.S ? hdr[ch].count : 0u;
+                uint32_t tot;
+                const uint32_t ex = block_excl_scan_u32(cnt, &tot, sh.bs);
+                sh.off[threadIdx.x] = base + ex;
+                __syncthreads();
+                const int nch = P.S - g0 < LLIMA_WG ? P.S - g0 : LLIMA_WG;
+                for (int k = (int)(threadIdx.x >> 6); k < nch; k += LLIMA_WAVES) {
+                    const uint32_t o = sh.off[k];
+                    const uint32_t m = hdr[g0 + k].count;
+                    const uint64_t* src = P.cand + ((size_t)row * P.S + g0 + k) * P.share;
+                    for (uint32_t i = lane_id(); i < m; i += 64) sh.u.cbuf[o + i] = src[i];
+                }
+                base += tot;
+                __syncthreads();
+            }
         }
         done = finish_fast(P, row, c, n, fl, bound, sh);
     }
@@ -930,14 +975,13 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 struct Tile { int E; int S; };
 
 static Tile choose_tile(int B, int V, int dtype, int k) {
-    // Largest E first; shrink while the grid is small, but keep the row's
-    // candidate count (about 2k per chunk) well inside the finish capacity.
-    const int emax = dtype == LLIMA_F32 ? 32 : 64;
-    int E = emax;
+    // 16 KB of logits per workgroup; smaller chunks while the grid is small, as
+    // long as the row's candidates (about k per chunk) fit the finish.
+    int E = dtype == LLIMA_F32 ? 16 : 32;
     auto S_of = [&](int e) { return (V + LLIMA_WG * e - 1) / (LLIMA_WG * e); };
     while (E > 8) {
         if ((int64_t)B * S_of(E) >= 1024) break;
-        if (k > 0 && (int64_t)S_of(E / 2) * 2 * k > SAMPLE_FIN_CAP / 2) break;
+        if (k > 0 && (int64_t)S_of(E / 2) * k > SAMPLE_FIN_CAP / 2) break;
         E /= 2;
     }
     return {E, S_of(E)};
@@ -1011,19 +1055,13 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.cand = (uint64_t*)((char*)workspace + al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)));
     hipStream_t st = (hipStream_t)stream;
     if (dtype == LLIMA_F32) {
-        switch (t.E) {
-            case 8: launch_sweep<float, 8>(P, st); break;
-            case 16: launch_sweep<float, 16>(P, st); break;
-            default: launch_sweep<float, 32>(P, st); break;
-        }
+        if (t.E == 8) launch_sweep<float, 8>(P, st);
+        else launch_sweep<float, 16>(P, st);
         hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
-        switch (t.E) {
-            case 8: launch_sweep<uint16_t, 8>(P, st); break;
-            case 16: launch_sweep<uint16_t, 16>(P, st); break;
-            case 32: launch_sweep<uint16_t, 32>(P, st); break;
-            default: launch_sweep<uint16_t, 64>(P, st); break;
-        }
+        if (t.E == 8) launch_sweep<uint16_t, 8>(P, st);
+        else if (t.E == 16) launch_sweep<uint16_t, 16>(P, st);
+        else launch_sweep<uint16_t, 32>(P, st);
         hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
