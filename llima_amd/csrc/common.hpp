@@ -86,69 +86,121 @@ __device__ __forceinline__ uint64_t uniform32(float u) {
 }
 
 // ------------------------------------------------------------------ wave primitives
+// Cross-lane steps use DPP (row shifts, mirrors and the GFX9 row broadcasts),
+// which move data between lanes inside the VALU with no LDS round trip.
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Wave index as a uniform (scalar) value.
+__device__ __forceinline__ uint32_t wave_id() {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// Number of set bits of m below this lane.
+__device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ uint32_t readlane(uint32_t v, uint32_t l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
+    return ((uint64_t)readlane((uint32_t)(v >> 32), l) << 32) | readlane((uint32_t)v, l);
+}
+
+#define DPP_QUAD_XOR1 0xB1     // quad_perm [1,0,3,2]
+#define DPP_QUAD_XOR2 0x4E     // quad_perm [2,3,0,1]
+#define DPP_ROW_SHR(n) (0x110 + (n))
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_BCAST15 0x142  // lane 15 of each row -> the next row
+#define DPP_ROW_BCAST31 0x143  // lane 31 -> rows 2 and 3
+
+// DPP move: lanes of rows outside ROW_MASK (and, with BC, lanes whose source
+// is outside the row) receive old.
+template <int CTRL, int ROW_MASK, bool BC>
+__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xF, BC);
+}
+template <int CTRL, int ROW_MASK, bool BC>
+__device__ __forceinline__ uint64_t dpp64(uint64_t old, uint64_t v) {
+    const uint32_t lo = dpp32<CTRL, ROW_MASK, BC>((uint32_t)old, (uint32_t)v);
+    const uint32_t hi = dpp32<CTRL, ROW_MASK, BC>((uint32_t)(old >> 32), (uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+template <int CTRL, int ROW_MASK, bool BC>
+__device__ __forceinline__ uint32_t dppT(uint32_t old, uint32_t v) { return dpp32<CTRL, ROW_MASK, BC>(old, v); }
+template <int CTRL, int ROW_MASK, bool BC>
+__device__ __forceinline__ uint64_t dppT(uint64_t old, uint64_t v) { return dpp64<CTRL, ROW_MASK, BC>(old, v); }
+
+__device__ __forceinline__ uint32_t readlane63(uint32_t v) { return readlane(v, 63); }
+__device__ __forceinline__ uint64_t readlane63(uint64_t v) { return readlane64(v, 63); }
+
+// Reduction over the 64 lanes (op associative and commutative, identity its
+// neutral element); the result is uniform.
+template <typename T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, T identity, Op op) {
+    v = op(v, dppT<DPP_QUAD_XOR1, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_QUAD_XOR2, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_HALF_MIRROR, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_MIRROR, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_BCAST15, 0xA, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_BCAST31, 0xC, false>(identity, v));
+    return readlane63(v);
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = __shfl_xor(v, o, 64);
-        v = v > w ? v : w;
-    }
-    return v;
+    return wave_reduce<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
 }
-
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-    uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
-    return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    return wave_reduce<uint32_t>(v, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
 }
-
-__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
-    uint32_t lo = __shfl_up((uint32_t)v, o, 64);
-    uint32_t hi = __shfl_up((uint32_t)(v >> 32), o, 64);
-    return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+    return wave_reduce<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a | b; });
 }
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint64_t w = shfl_xor_u64(v, o);
-        v = v > w ? v : w;
-    }
-    return v;
-}
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
-    return v;
-}
-
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return wave_reduce<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    return wave_reduce<uint64_t>(v, 0ull, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+    return wave_reduce<uint64_t>(v, 0ull, [](uint64_t a, uint64_t b) { return a + b; });
 }
 
-// Inclusive prefix sum across the 64 lanes.
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-    const uint32_t l = lane_id();
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        uint64_t w = shfl_up_u64(v, o);
-        if (l >= (uint32_t)o) v += w;
-    }
-    return v;
-}
-
+// Inclusive prefix sums across the 64 lanes (Hillis-Steele inside each row of
+// 16 lanes, then the two row broadcasts).
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-    const uint32_t l = lane_id();
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        uint32_t w = __shfl_up(v, o, 64);
-        if (l >= (uint32_t)o) v += w;
-    }
+    v += dpp32<DPP_ROW_SHR(1), 0xF, true>(0u, v);
+    v += dpp32<DPP_ROW_SHR(2), 0xF, true>(0u, v);
+    v += dpp32<DPP_ROW_SHR(4), 0xF, true>(0u, v);
+    v += dpp32<DPP_ROW_SHR(8), 0xF, true>(0u, v);
+    v += dpp32<DPP_ROW_BCAST15, 0xA, false>(0u, v);
+    v += dpp32<DPP_ROW_BCAST31, 0xC, false>(0u, v);
     return v;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+    v += dpp64<DPP_ROW_SHR(1), 0xF, true>(0ull, v);
+    v += dpp64<DPP_ROW_SHR(2), 0xF, true>(0ull, v);
+    v += dpp64<DPP_ROW_SHR(4), 0xF, true>(0ull, v);
+    v += dpp64<DPP_ROW_SHR(8), 0xF, true>(0ull, v);
+    v += dpp64<DPP_ROW_BCAST15, 0xA, false>(0ull, v);
+    v += dpp64<DPP_ROW_BCAST31, 0xC, false>(0ull, v);
+    return v;
+}
+
+// The r-th largest (1-based, r <= 64) of one key per lane, with its bits below
+// lowbit cleared (so a value <= the exact one); keys of 0 never count, and the
+// result is 0 when fewer than r lanes hold a key.  One ballot per bit.
+__device__ __forceinline__ uint32_t wave_rth_largest(uint32_t key, uint32_t r, int lowbit) {
+    uint32_t t = 0;
+    for (int b = 31; b >= lowbit; --b) {
+        const uint32_t cand = t | (1u << b);
+        if ((uint32_t)__popcll(ballot(key >= cand)) >= r) t = cand;
+    }
+    return t;
 }
 
 // Descending bitonic sort of one uint32 per lane across a wavefront; returns

@@ -5,26 +5,29 @@
 // this part, device-scope cache maintenance and same-address atomics cost far
 // more than the whole sweep):
 //
-// sample_sweep: B x S workgroups; workgroup (row, chunk) streams a 256*E chunk
-//   of its row from HBM with 16-byte loads, issued before anything else, and
-//   keeps it in registers.  While the loads are in flight it counts the row's
-//   history ids that fall in the chunk in an LDS table (packed u16 counts);
-//   distinct ids become "exceptions" whose penalised value is computed apart, so
-//   the per-element work is a count != 0 test (no division in the stream).
-//   Masked (packed-uint32 grammar bitmask, LSB first), NaN and history values
-//   become -inf.  A lower bound t of the chunk's k-th largest value comes from
-//   the lane maxima (wavefront bitonic sort, min over the 4 waves) and every
-//   value >= t - |t| 2^-20 is written, with its id, to the chunk's own slot of
-//   the workspace together with a small header.
+// sample_sweep: B x S workgroups; workgroup (row, chunk) streams a 16 KB chunk
+//   of its row with 16-byte loads, all issued before anything waits, and keeps
+//   it in registers.  It counts the row's history ids that fall in the chunk in
+//   an LDS table (packed u16), then computes every value in registers: masked
+//   (packed-uint32 grammar bitmask, LSB first), NaN and out-of-row values become
+//   -inf and history values take the repetition / frequency / presence
+//   penalties.  A lower bound g of the chunk's k-th largest value comes from the
+//   lane maxima (a ballot search per wave for the ceil(k/4)-th largest, min over
+//   the 4 waves), and every value >= g - |g| 2^-20 is written, with its id, to
+//   the chunk's own workspace slot at offsets taken from ballots (no atomics),
+//   together with a small header.  The LDS footprint (8 KB for fp32) lets all
+//   workgroups of a B=64, V=128256 step be resident at once.
 //
-// sample_finish: one workgroup per row gathers the candidates into LDS, divides
-//   them by the temperature, proves that the bound could not have dropped a
-//   member of the top-k set (else falls back), and runs three radix selects over
-//   LDS histograms on register-resident candidates: top-k threshold (count),
-//   top-p threshold (fixed-point mass) and the draw (mass by ascending id).
-//   Rows that the candidates cannot serve (overflow, k beyond the fast path,
-//   top-k disabled without a mask, degenerate temperatures) are finished by the
-//   same workgroup with a full-row multi-pass version of the same selects.
+// sample_finish: one workgroup per row loads the headers and the candidates
+//   straight into registers (16 slots per thread), divides them by the
+//   temperature, drops those below the largest chunk bound, proves that no
+//   member of the top-k set can be missing (else falls back), and selects with
+//   LDS radix histograms whose scans use DPP: the top-k threshold (count), then,
+//   for up to 64 survivors, top-p / min-p / the draw by pairwise sums spread
+//   over the 4 waves, or otherwise the top-p threshold (fixed-point mass) and
+//   the draw (mass by ascending id).  Rows that the candidates cannot serve
+//   (overflow, top-k disabled without a mask, degenerate temperatures) are
+//   finished by the same workgroup with a full-row multi-pass version.
 //
 // The sampling semantics have no counterpart in the reference runtime, which
 // only ever takes the argmax (sima_lmm/devkit/cpp/utils.hpp:80-152,
@@ -38,11 +41,12 @@ namespace llima {
 #define SAMPLE_SLOTS 16                            // candidates per finishing thread
 #define SAMPLE_FIN_CAP (SAMPLE_SLOTS * LLIMA_WG)   // 4096
 #define SAMPLE_ROW_CAND 16384                      // candidate slots per row (all chunks)
-#define SAMPLE_PRECAP 1024                         // candidates staged in LDS per chunk
-#define SAMPLE_EXC_CAP 512                         // distinct history ids per chunk
-#define SAMPLE_MIN_CHUNK 2048                      // 256 threads x E = 8
+#define SAMPLE_MIN_CHUNK 4096                      // smallest chunk (fp32: 256 threads x 16)
 #define SAMPLE_SEG 8192                            // full-row path segment
 #define SAMPLE_HBATCH 8                            // history ids per thread loaded up front
+#define SAMPLE_K_BOUND 256                         // largest top-k the sweep bounds
+#define SAMPLE_BOUND_LOWBIT 12                     // key bits below this are not searched
+#define SAMPLE_SMALL 64                            // survivors handled one per lane
 
 #define HDR_OVERFLOW 1u
 #define HDR_FILTERED 2u
@@ -51,7 +55,7 @@ namespace llima {
 struct ChunkHdr {
     uint32_t count;      // candidates in this chunk's slot
     uint32_t flags;      // HDR_*
-    uint32_t bound;      // key of the pre-filter bound (when FILTERED)
+    uint32_t bound;      // key of the chunk bound (when FILTERED)
     uint32_t pad;
     uint64_t greedy;     // (key << 32 | ~index) of the chunk maximum
     uint64_t pad2;
@@ -72,6 +76,8 @@ struct SampleParams {
     uint64_t* cand;      // [B][S][share]  (value bits << 32 | id)
     int32_t B, V, H_max, S, share;
     int32_t vec_ok;
+    int32_t pre;         // candidate slots per chunk the finish loads up front
+    uint32_t pre_magic;  // f / pre == umulhi(f, pre_magic) for f < 4096
 };
 
 struct RowCfg {
@@ -93,7 +99,7 @@ __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
     r.beta = c.frequency_penalty_rows ? c.frequency_penalty_rows[row] : c.frequency_penalty;
     r.greedy = (c.greedy != 0) || !(r.T > 0.0f);
     int h = 0;
-    if (P.hist) {
+    if (P.H_max > 0) {
         h = P.hist_len ? P.hist_len[row] : P.H_max;
         h = h < 0 ? 0 : (h > P.H_max ? P.H_max : h);
     }
@@ -130,13 +136,9 @@ __device__ __forceinline__ float load_one<uint16_t>(const uint16_t* rowp, int i)
 }
 
 // Counts the row's history ids in [lo, hi) into an LDS table of packed u16
-// counts.  With exc_id, lists the distinct ids (first occurrence wins the slot)
-// with their raw logits, fetched here so that the load overlaps the scan.
-template <typename TL>
+// counts (full-row path).
 __device__ __forceinline__ void count_history(const SampleParams& P, int row, int hlen, int lo,
-                                              int hi, uint32_t* table, int nwords,
-                                              int32_t* exc_id, float* exc_raw, uint32_t* n_exc,
-                                              const TL* rowp) {
+                                              int hi, uint32_t* table, int nwords) {
     for (int i = threadIdx.x; i < nwords; i += LLIMA_WG) table[i] = 0;
     __syncthreads();
     const int32_t* h = P.hist + (size_t)row * P.H_max;
@@ -144,32 +146,13 @@ __device__ __forceinline__ void count_history(const SampleParams& P, int row, in
         const int32_t id = h[j];
         if (id >= lo && id < hi) {
             const uint32_t off = (uint32_t)(id - lo);
-            const uint32_t sh16 = (off & 1u) * 16u;
-            const uint32_t old = atomicAdd(&table[off >> 1], 1u << sh16);
-            if (exc_id && ((old >> sh16) & 0xFFFFu) == 0) {
-                const uint32_t slot = atomicAdd(n_exc, 1u);
-                if (slot < SAMPLE_EXC_CAP) {
-                    exc_id[slot] = id;
-                    exc_raw[slot] = load_one<TL>(rowp, id);
-                }
-            }
+            atomicAdd(&table[off >> 1], 1u << ((off & 1u) * 16u));
         }
     }
     __syncthreads();
 }
 
 // ================================================================== sweep
-template <int CHUNK>
-struct SweepShared {
-    uint32_t cnt[CHUNK / 2];
-    int32_t exc_id[SAMPLE_EXC_CAP];
-    float exc_val[SAMPLE_EXC_CAP];           // raw, then penalised value
-    uint64_t pre[SAMPLE_PRECAP];
-    uint32_t n_exc, n_pre;
-    uint32_t wave_bound[LLIMA_WAVES];
-    BlockScratch bs;
-};
-
 // VEC: rows are 16-byte aligned and V is a multiple of the values per load, so
 // every chunk (also a row's partial last one) is read with 16-byte loads from
 // clamped, always-valid addresses and the out-of-row values masked in registers.
@@ -178,56 +161,45 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
     constexpr int NL = E / EPL;                // loads per thread
     constexpr int CHUNK = LLIMA_WG * E;
-    __shared__ SweepShared<CHUNK> sh;
+    constexpr int CW = CHUNK / 2;              // history count words
+    __shared__ __align__(16) uint32_t cnt[CW];
+    __shared__ uint32_t xw[2][LLIMA_WAVES];
+    __shared__ uint64_t xg[LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
+    const int t = (int)threadIdx.x;
+    const uint32_t lane = lane_id(), wave = wave_id();
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
     const int c0 = (int)chunk * CHUNK;
     const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
-    const int nw = (V + 31) >> 5;
-    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
+    const int H = P.H_max;
+    const int32_t* hrow = P.hist + (size_t)row * H;
+    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
 
-    const RowCfg c = load_cfg(P, row);
-    const int32_t* hrow = P.hist + (size_t)row * P.H_max;
-
-    // ---- 0. clear the chunk's history table
-    if (c.pen)
-        for (int i = threadIdx.x; i < CHUNK / 2; i += LLIMA_WG) sh.cnt[i] = 0;
-    if (threadIdx.x == 0) { sh.n_exc = 0; sh.n_pre = 0; }
-    __syncthreads();
-
-    // ---- 1. issue the loads, oldest first in the order they are consumed:
-    //         mask words, the first batch of history ids, then the chunk itself.
-    //         Every address is valid; nothing waits until all are in flight.
-    uint32_t mword[NL];
-    if (mrow) {
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-            mword[j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < NL; ++j) mword[j] = 0xFFFFFFFFu;
-    }
-    // history ids: whether slot b holds a real id (j < hlen) is decided only
-    // when it is counted
+    // ---- 1. every load, issued before anything waits and in the order the
+    //         data is consumed: history ids, mask words, the chunk.  Only
+    //         kernel arguments decide them (the row's configuration is still
+    //         in flight); every address is valid.
     int32_t hid[SAMPLE_HBATCH];
-    if (c.pen) {
 #pragma unroll
-        for (int b = 0; b < SAMPLE_HBATCH; ++b) {
-            const int j = (int)threadIdx.x + b * LLIMA_WG;
-            hid[b] = hrow[j < c.hlen ? j : 0];
-        }
+    for (int b = 0; b < SAMPLE_HBATCH; ++b) {
+        const int j = t + b * LLIMA_WG;
+        hid[b] = (b * LLIMA_WG < H) ? hrow[j < H ? j : H - 1] : -1;
+    }
+    uint32_t mword[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+        mword[j] = mrow ? mrow[(i0 < V ? i0 : V - 1) >> 5] : 0xFFFFFFFFu;
     }
     llima_u32x4 raw[NL];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
         if constexpr (VEC) {
             const int ia = i0 < V ? i0 : V - EPL;
             raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
@@ -243,83 +215,73 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
         }
     }
+    const RowCfg c = load_cfg(P, row);
 
-    // ---- 2. while the chunk is in flight: count the history ids of the chunk
+    // ---- 2. history counts of the chunk
     if (c.pen) {
+        for (int i = t; i < CW / 4; i += LLIMA_WG) ((llima_u32x4*)cnt)[i] = llima_u32x4{0, 0, 0, 0};
+        __syncthreads();
 #pragma unroll
         for (int b = 0; b < SAMPLE_HBATCH; ++b) {
             const int32_t id = hid[b];
-            if ((int)threadIdx.x + b * LLIMA_WG < c.hlen && id >= c0 && id < c1) {
+            if (t + b * LLIMA_WG < c.hlen && id >= c0 && id < c1) {
                 const uint32_t off = (uint32_t)(id - c0);
-                atomicAdd(&sh.cnt[off >> 1], 1u << ((off & 1u) * 16u));
+                atomicAdd(&cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
         }
-        for (int j = (int)threadIdx.x + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
+        for (int j = t + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
             const int32_t id = hrow[j];
             if (id >= c0 && id < c1) {
                 const uint32_t off = (uint32_t)(id - c0);
-                atomicAdd(&sh.cnt[off >> 1], 1u << ((off & 1u) * 16u));
+                atomicAdd(&cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
 
-    // ---- 3. values after mask / NaN; history values leave the stream as
-    //         exceptions (owner thread appends id and raw value), so that the
-    //         stream needs no division
+    // ---- 3. values: mask / NaN / out of row -> -inf, history values penalised
     float v[E];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
         const uint32_t mb = mword[j] >> (i0 & 31);
-        float t[EPL];
+        float xs[EPL];
         const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
         if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t[e] = __uint_as_float(w4[e]);
+            for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                t[2 * e] = __uint_as_float(w4[e] << 16);
-                t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
+                xs[2 * e] = __uint_as_float(w4[e] << 16);
+                xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
             }
         }
         uint32_t cw[EPL / 2];
 #pragma unroll
         for (int e = 0; e < EPL / 2; ++e) cw[e] = 0;
-        if (c.pen && i0 < c1) {
-            const uint32_t off = (uint32_t)(i0 - c0);
-#pragma unroll
-            for (int e = 0; e < EPL / 2; ++e) cw[e] = sh.cnt[(off >> 1) + e];
+        if (c.pen) {
+            const uint32_t* cp = cnt + ((i0 - c0) >> 1);
+            if constexpr (EPL == 4) {
+                const uint2 w2 = *(const uint2*)cp;
+                cw[0] = w2.x; cw[1] = w2.y;
+            } else {
+                const llima_u32x4 wq = *(const llima_u32x4*)cp;
+                cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
+            }
         }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            float x = t[e];
-            if (x != x || !((mb >> e) & 1u) || i0 + e >= c1) x = NEG_INF;
-            const uint32_t cnt = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-            if (cnt) {
-                const uint32_t slot = atomicAdd(&sh.n_exc, 1u);
-                if (slot < SAMPLE_EXC_CAP) {
-                    sh.exc_id[slot] = i0 + e;
-                    sh.exc_val[slot] = x;
-                }
-                x = NEG_INF;
+            float x = xs[e];
+            const uint32_t inrow = VEC ? (uint32_t)(i0 < c1) : (uint32_t)(i0 + e < c1);
+            const uint32_t ok = ((mb >> e) & 1u) & inrow & (uint32_t)(x == x);
+            x = ok ? x : NEG_INF;
+            if (c.pen) {
+                const uint32_t cn = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+                if (cn) x = penalize(x, cn, c);
             }
             v[j * EPL + e] = x;
         }
-    }
-    __syncthreads();
-
-    // ---- 4. exceptions: distinct history ids of this chunk, penalised exactly
-    const uint32_t n_exc = c.pen ? sh.n_exc : 0u;
-    const uint32_t n_exc_c = n_exc < SAMPLE_EXC_CAP ? n_exc : SAMPLE_EXC_CAP;
-    uint32_t flags = n_exc > SAMPLE_EXC_CAP ? HDR_OVERFLOW : 0u;
-    float tmax = NEG_INF;
-    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-        const int id = sh.exc_id[j];
-        const float l = penalize(sh.exc_val[j], table_count(sh.cnt, (uint32_t)(id - c0)), c);
-        sh.exc_val[j] = l;
-        tmax = l > tmax ? l : tmax;
     }
 
     ChunkHdr* hdr = P.hdr + (size_t)row * P.S + chunk;
@@ -329,139 +291,114 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         uint32_t bidx = 0xFFFFFFFFu;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
 #pragma unroll
             for (int e = 0; e < EPL; ++e)
                 if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
         }
-        uint64_t kb = best > NEG_INF ? (((uint64_t)f32_key(best) << 32) | (uint64_t)(~bidx)) : 0ull;
-        for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-            const float x = sh.exc_val[j];
-            const uint64_t kk = x > NEG_INF ? (((uint64_t)f32_key(x) << 32) |
-                                               (uint64_t)(~(uint32_t)sh.exc_id[j])) : 0ull;
-            kb = kk > kb ? kk : kb;
-        }
-        kb = block_max_u64(kb, sh.bs);
-        if (threadIdx.x == 0) {
+        const uint32_t kb = best > NEG_INF ? f32_key(best) : 0u;
+        const uint32_t wk = wave_max_u32(kb);
+        const uint32_t wi = wave_max_u32((wk != 0 && kb == wk) ? ~bidx : 0u);
+        if (lane == 0) xg[wave] = wk ? (((uint64_t)wk << 32) | wi) : 0ull;
+        __syncthreads();
+        if (t == 0) {
+            uint64_t g = 0;
+#pragma unroll
+            for (int w = 0; w < LLIMA_WAVES; ++w) g = xg[w] > g ? xg[w] : g;
             hdr->count = 0;
-            hdr->flags = flags;
+            hdr->flags = 0;
             hdr->bound = 0;
-            hdr->greedy = kb;
+            hdr->greedy = g;
         }
         return;
     }
 
-    // ---- 5. pre-filter bound from lane maxima: every wave has >= r lanes whose
-    //         maximum is >= its bound, so the chunk has >= 4r >= k values >= t
-    float g = NEG_INF;
-    if (c.k > 0 && c.k <= 4 * 64) {
+    // ---- 4. chunk bound: every wave has >= r = ceil(k/4) lanes whose maximum
+    //         is >= its bound, so the chunk has >= 4r >= k values >= their min
+    uint32_t gkey = 0;
+    if (c.k > 0 && c.k <= SAMPLE_K_BOUND) {
+        float lm = NEG_INF;
 #pragma unroll
-        for (int e = 0; e < E; ++e) tmax = v[e] > tmax ? v[e] : tmax;
-        const uint32_t r = (uint32_t)(c.k + 3) >> 2;          // ceil(k/4) <= 64
-        const uint32_t sorted = wave_sort_desc(f32_key(tmax));
-        const uint32_t wb = __shfl(sorted, (int)r - 1, 64);
-        if (lane_id() == 0) sh.wave_bound[threadIdx.x >> 6] = wb;
+        for (int e = 0; e < E; ++e) lm = v[e] > lm ? v[e] : lm;
+        const uint32_t r = ((uint32_t)c.k + 3u) >> 2;
+        const uint32_t tw = wave_rth_largest(lm > NEG_INF ? f32_key(lm) : 0u, r, SAMPLE_BOUND_LOWBIT);
+        if (lane == 0) xw[0][wave] = tw;
         __syncthreads();
-        uint32_t tb = sh.wave_bound[0];
+        gkey = xw[0][0];
 #pragma unroll
-        for (int w = 1; w < LLIMA_WAVES; ++w) tb = sh.wave_bound[w] < tb ? sh.wave_bound[w] : tb;
-        if (tb > LLIMA_KEY_NEG_INF) g = lower_bound_margin(key_f32(tb));
+        for (int w = 1; w < LLIMA_WAVES; ++w) gkey = xw[0][w] < gkey ? xw[0][w] : gkey;
     }
-    // ---- 6. stage the values >= g in LDS
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const float x = v[j * EPL + e];
-            if (x > NEG_INF && x >= g) {
-                const uint32_t s2 = atomicAdd(&sh.n_pre, 1u);
-                if (s2 < SAMPLE_PRECAP)
-                    sh.pre[s2] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
-            }
-        }
+    float g = -__FLT_MAX__;                       // keeps every finite value
+    if (gkey) {
+        const float m = lower_bound_margin(key_f32(gkey));
+        g = m > -__FLT_MAX__ ? m : -__FLT_MAX__;
     }
-    for (uint32_t j = threadIdx.x; j < n_exc_c; j += LLIMA_WG) {
-        const float x = sh.exc_val[j];
-        if (x > NEG_INF && x >= g) {
-            const uint32_t s2 = atomicAdd(&sh.n_pre, 1u);
-            if (s2 < SAMPLE_PRECAP)
-                sh.pre[s2] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)sh.exc_id[j];
-        }
-    }
-    __syncthreads();
-    const uint32_t n_pre = sh.n_pre;
-    if (n_pre > SAMPLE_PRECAP) flags |= HDR_OVERFLOW;
-    const uint32_t n_st = n_pre < SAMPLE_PRECAP ? n_pre : SAMPLE_PRECAP;
 
-    // ---- 7. the chunk's exact k-th largest value tau_c among the staged ones
-    //         (they hold every value >= g, hence the chunk's top k) by rank counting
-    float gout = NEG_INF;
-    uint32_t bound = 0;
-    if (c.k > 0 && n_st >= (uint32_t)c.k && !(flags & HDR_OVERFLOW)) {
-        uint32_t kt = 0;                                      // key of a tau_c candidate
-        for (uint32_t i = threadIdx.x; i < n_st; i += LLIMA_WG) {
-            const float xi = __uint_as_float((uint32_t)(sh.pre[i] >> 32));
-            uint32_t ge = 0;
-            for (uint32_t jj = 0; jj < n_st; ++jj)
-                ge += __uint_as_float((uint32_t)(sh.pre[jj] >> 32)) >= xi;
-            if (ge >= (uint32_t)c.k) { const uint32_t kk = f32_key(xi); kt = kk > kt ? kk : kt; }
-        }
-        bound = block_max_u32(kt, sh.bs);
-        gout = lower_bound_margin(key_f32(bound));
-        flags |= HDR_FILTERED;
-    }
-    // ---- 8. write the chunk's candidates (values >= gout) and its header
-    if (threadIdx.x == 0) sh.n_exc = 0;                      // reused as the output count
+    // ---- 5. write the values >= g: count per wave, then ballot offsets
+    uint32_t wcount = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) wcount += (uint32_t)__popcll(ballot(v[e] >= g));
+    if (lane == 0) xw[1][wave] = wcount;
     __syncthreads();
+    uint32_t base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) {
+        const uint32_t n = xw[1][w];
+        base += (uint32_t)w < wave ? n : 0u;
+        total += n;
+    }
     const uint32_t cap = (uint32_t)P.share;
-    uint64_t* dst = P.cand + ((size_t)row * P.S + chunk) * P.share;
-    if (!(flags & HDR_OVERFLOW)) {
-        for (uint32_t i = threadIdx.x; i < n_st; i += LLIMA_WG) {
-            const uint64_t q = sh.pre[i];
-            if (__uint_as_float((uint32_t)(q >> 32)) >= gout) {
-                const uint32_t o = atomicAdd(&sh.n_exc, 1u);
-                if (o < cap) dst[o] = q;
+    if (total <= cap) {
+        uint64_t* dst = P.cand + ((size_t)row * P.S + chunk) * P.share;
+        uint32_t o = base;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float x = v[j * EPL + e];
+                const bool pr = x >= g;
+                const uint64_t m = ballot(pr);
+                if (m) {
+                    if (pr) dst[o + mbcnt(m)] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
+                    o += (uint32_t)__popcll(m);
+                }
             }
         }
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t n_out = sh.n_exc;
-        if (n_out > cap) { flags |= HDR_OVERFLOW; }
-        if (flags & HDR_OVERFLOW) n_out = 0;
-        hdr->count = n_out;
-        hdr->flags = flags;
-        hdr->bound = bound;
+    if (t == 0) {
+        hdr->count = total <= cap ? total : 0u;
+        hdr->flags = (total > cap ? HDR_OVERFLOW : 0u) | (gkey ? HDR_FILTERED : 0u);
+        hdr->bound = gkey;
         hdr->greedy = 0;
     }
 }
 
 // ================================================================== finish
-#define SMALL_K 256                                // brute-force path: one element per thread
-
 struct FinishShared {
     union {
-        uint64_t cbuf[SAMPLE_FIN_CAP];         // gathered candidates
+        uint64_t cbuf[SAMPLE_FIN_CAP];         // candidates gathered in chunk order
         uint32_t table[SAMPLE_SEG / 2];        // full-row path history counts
     } u;
-    uint32_t hcnt[256];
-    uint64_t hmass[256];
-    uint32_t off[LLIMA_WG];
-    uint8_t cid[SAMPLE_FIN_CAP];               // candidate position -> chunk (S <= 256)
-    uint32_t kkey[SMALL_K], kid[SMALL_K];      // the top-k survivors (small path)
-    uint64_t kw[SMALL_K], kwf[SMALL_K];
-    uint32_t nk;
-    uint32_t sel;
-    uint64_t sel64, sel64b;
+    uint32_t ccount[LLIMA_WG];                 // candidates per chunk
+    uint32_t hcnt[2][256];                     // radix histograms (double-buffered)
+    uint64_t hmass[2][256];
+    uint64_t above[256];
+    uint32_t skey[SAMPLE_SMALL], sid[SAMPLE_SMALL];
+    uint64_t part[2][LLIMA_WAVES][64];
+    uint32_t r32[8][LLIMA_WAVES];
+    uint64_t r64[2][LLIMA_WAVES];
+    uint32_t sel[2];
+    uint64_t sel64[2];
     BlockScratch bs;
 };
 
 // ------------------------------------------------------------------ radix selects
-// Each select runs over a set of (key, id, weight) elements presented by a
-// visitor; every thread visits its own elements.  Digits are 8 bits wide and
-// start at the highest bit in which the visited keys differ (the bits above it
-// are common to all of them), so the first histogram already spreads the keys.
+// Each select runs over register-resident elements (SAMPLE_SLOTS per thread,
+// key 0 = absent).  Digits are 8 bits wide and start at the highest bit in
+// which the keys differ (the bits above it are common to all of them).
+// hcnt[buf] and hmass[buf] are zero on entry and on return; every round clears
+// the other buffer for the next one, so a round needs three barriers.
 struct Digits {
     uint32_t prefix, pmask;   // fixed high bits of the selected key
     int top;                  // top bit of the next digit (-1: done)
@@ -477,111 +414,143 @@ __device__ __forceinline__ Digits digits_init(uint32_t kmin, uint32_t kmax) {
     return d;
 }
 
-// k-th largest key (with multiplicity) among visited elements, all of whose
-// keys lie in [kmin, kmax].
-template <class Visit>
-__device__ __forceinline__ uint32_t select_kth_desc(Visit visit, uint32_t k, uint32_t kmin,
-                                                    uint32_t kmax, FinishShared& sh) {
+// Exclusive prefix of v over the workgroup in thread order, given this wave's
+// inclusive scan inc; r is a per-wave LDS slot array.  Contains one barrier.
+__device__ __forceinline__ uint64_t wg_prefix_u64(uint64_t inc, uint64_t v, uint64_t* r) {
+    const uint32_t wave = wave_id();
+    if (lane_id() == 63) r[wave] = inc;
+    __syncthreads();
+    uint64_t before = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) before += (uint32_t)w < wave ? r[w] : 0ull;
+    return before + inc - v;
+}
+
+// k-th largest key (with multiplicity) among the elements, all of whose keys
+// lie in [kmin, kmax].
+__device__ __forceinline__ uint32_t fin_kth_desc(const uint32_t (&key)[SAMPLE_SLOTS], uint32_t k,
+                                                 uint32_t kmin, uint32_t kmax, FinishShared& sh,
+                                                 int& buf) {
     Digits d = digits_init(kmin, kmax);
     uint32_t rem = k;
+    const uint32_t t = threadIdx.x;
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        sh.hcnt[threadIdx.x] = 0;
+        uint32_t* hc = sh.hcnt[buf];
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j)
+            if (key[j] && (key[j] & d.pmask) == d.prefix) atomicAdd(&hc[(key[j] >> lo) & bmask], 1u);
         __syncthreads();
-        const uint32_t prefix = d.prefix, pmask = d.pmask;
-        visit([&](uint32_t key, uint32_t, uint64_t) {
-            if ((key & pmask) == prefix) atomicAdd(&sh.hcnt[(key >> lo) & bmask], 1u);
-        });
+        const uint32_t bin = 255u - t;                 // thread 0 <-> top bin
+        const uint32_t cn = hc[bin];
+        sh.hcnt[buf ^ 1][t] = 0;
+        sh.hmass[buf ^ 1][t] = 0;
+        const uint32_t inc = wave_incl_scan_u32(cn);
+        const uint32_t above = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
+        if (above < rem && above + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = rem - above; }
         __syncthreads();
-        const uint32_t bin = 255u - threadIdx.x;          // thread 0 <-> top bin
-        const uint32_t c = sh.hcnt[bin];
-        uint32_t tot;
-        const uint32_t above = block_excl_scan_u32(c, &tot, sh.bs);
-        if (above < rem && above + c >= rem) { sh.sel = bin; sh.sel64 = rem - above; }
-        __syncthreads();
-        d.prefix |= sh.sel << lo;
+        d.prefix |= sh.sel[0] << lo;
         d.pmask |= bmask << lo;
         d.top = lo - 1;
-        rem = (uint32_t)sh.sel64;
-        __syncthreads();
+        rem = sh.sel[1];
+        buf ^= 1;
     }
     return d.prefix;
 }
 
 // Top-p boundary: the smallest key theta such that an element with key theta has
 // (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
-template <class Visit>
-__device__ __forceinline__ uint32_t select_topp_desc(Visit visit, llima_u128 PZ, uint32_t kmin,
-                                                     uint32_t kmax, FinishShared& sh) {
+__device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[SAMPLE_SLOTS],
+                                                  const uint64_t (&w)[SAMPLE_SLOTS],
+                                                  llima_u128 PZ, uint32_t kmin, uint32_t kmax,
+                                                  FinishShared& sh, int& buf) {
     Digits d = digits_init(kmin, kmax);
     uint64_t acc = 0;
+    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        sh.hcnt[threadIdx.x] = 0;
-        sh.hmass[threadIdx.x] = 0;
-        __syncthreads();
-        const uint32_t prefix = d.prefix, pmask = d.pmask;
-        visit([&](uint32_t key, uint32_t, uint64_t w) {
-            if ((key & pmask) == prefix) {
-                const uint32_t b = (key >> lo) & bmask;
-                atomicAdd(&sh.hcnt[b], 1u);
-                if (w) atomicAdd((unsigned long long*)&sh.hmass[b], (unsigned long long)w);
+        uint32_t* hc = sh.hcnt[buf];
+        uint64_t* hm = sh.hmass[buf];
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+            if (key[j] && (key[j] & d.pmask) == d.prefix) {
+                const uint32_t b = (key[j] >> lo) & bmask;
+                atomicAdd(&hc[b], 1u);
+                if (w[j]) atomicAdd((unsigned long long*)&hm[b], (unsigned long long)w[j]);
             }
-        });
+        }
         __syncthreads();
-        const uint32_t t = threadIdx.x, bin = 255u - t;
-        const uint32_t c = sh.hcnt[bin];
-        uint64_t m = sh.hmass[bin], tot;
-        const uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
-        const bool cond = c > 0 && (((llima_u128)above << 32) < PZ);
-        // lowest qualifying bin = highest t; else the top non-empty bin = lowest t
-        const uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
-        const uint32_t top_nonempty = 255u - block_max_u32(c > 0 ? 255u - t : 0u, sh.bs);
-        const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
-        if (t == sel_t) { sh.sel = bin; sh.sel64 = above; }
+        const uint32_t bin = 255u - t;
+        const uint32_t cn = hc[bin];
+        const uint64_t m = hm[bin];
+        sh.hcnt[buf ^ 1][t] = 0;
+        sh.hmass[buf ^ 1][t] = 0;
+        const uint64_t inc = wave_incl_scan_u64(m);
+        const uint64_t above = acc + wg_prefix_u64(inc, m, sh.r64[0]);
+        const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
+        sh.above[t] = above;
+        const uint64_t bc = ballot(cond), bn = ballot(cn > 0);
+        if (lane == 0) {
+            sh.r32[1][wave] = bc ? 64u - (uint32_t)__builtin_clzll(bc) : 0u;    // highest lane + 1
+            sh.r32[2][wave] = bn ? (uint32_t)__builtin_ffsll((long long)bn) : 0u;   // lowest lane + 1
+        }
         __syncthreads();
-        d.prefix |= sh.sel << lo;
+        // the lowest qualifying bin (highest t); else the top non-empty bin (lowest t)
+        int sel_t = -1;
+#pragma unroll
+        for (int w2 = LLIMA_WAVES - 1; w2 >= 0; --w2)
+            if (sel_t < 0 && sh.r32[1][w2]) sel_t = w2 * 64 + (int)sh.r32[1][w2] - 1;
+        if (sel_t < 0) {
+#pragma unroll
+            for (int w2 = 0; w2 < LLIMA_WAVES; ++w2)
+                if (sel_t < 0 && sh.r32[2][w2]) sel_t = w2 * 64 + (int)sh.r32[2][w2] - 1;
+        }
+        if (sel_t < 0) sel_t = 0;
+        d.prefix |= (255u - (uint32_t)sel_t) << lo;
         d.pmask |= bmask << lo;
         d.top = lo - 1;
-        acc = sh.sel64;
-        __syncthreads();
+        acc = sh.above[sel_t];
+        buf ^= 1;
     }
     return d.prefix;
 }
 
-// Draw: the smallest id whose ascending-id prefix mass exceeds target; also
-// returns that element's weight.  Ids are < V <= 2^24.
-template <class Visit>
-__device__ __forceinline__ uint32_t select_draw_asc(Visit visit, uint64_t target, uint32_t V,
-                                                    uint64_t* w_out, FinishShared& sh) {
+// Draw: the smallest id whose ascending-id prefix mass exceeds target (< the
+// total mass); also returns that element's weight.  Ids are < V <= 2^24.
+__device__ __forceinline__ uint32_t fin_draw_asc(const uint32_t (&id)[SAMPLE_SLOTS],
+                                                 const uint64_t (&w)[SAMPLE_SLOTS], uint64_t target,
+                                                 uint32_t V, uint64_t* w_out, FinishShared& sh,
+                                                 int& buf) {
     Digits d = digits_init(0u, V > 1 ? V - 1 : 1u);
     uint64_t acc = 0;
+    const uint32_t t = threadIdx.x;
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        sh.hmass[threadIdx.x] = 0;
+        uint64_t* hm = sh.hmass[buf];
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j)
+            if (w[j] && (id[j] & d.pmask) == d.prefix)
+                atomicAdd((unsigned long long*)&hm[(id[j] >> lo) & bmask], (unsigned long long)w[j]);
         __syncthreads();
-        const uint32_t prefix = d.prefix, pmask = d.pmask;
-        visit([&](uint32_t, uint32_t id, uint64_t w) {
-            if (w && (id & pmask) == prefix)
-                atomicAdd((unsigned long long*)&sh.hmass[(id >> lo) & bmask], (unsigned long long)w);
-        });
-        __syncthreads();
-        const uint32_t bin = threadIdx.x;
-        uint64_t m = sh.hmass[bin], tot;
-        const uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
+        const uint32_t bin = t;
+        const uint64_t m = hm[bin];
+        sh.hcnt[buf ^ 1][t] = 0;
+        sh.hmass[buf ^ 1][t] = 0;
+        const uint64_t inc = wave_incl_scan_u64(m);
+        const uint64_t below = acc + wg_prefix_u64(inc, m, sh.r64[0]);
         if (m > 0 && below <= target && target < below + m) {
-            sh.sel = bin; sh.sel64 = below; sh.sel64b = m;
+            sh.sel[0] = bin; sh.sel64[0] = below; sh.sel64[1] = m;
         }
         __syncthreads();
-        d.prefix |= sh.sel << lo;
+        d.prefix |= sh.sel[0] << lo;
         d.pmask |= bmask << lo;
         d.top = lo - 1;
-        acc = sh.sel64;
-        *w_out = sh.sel64b;
-        __syncthreads();
+        acc = sh.sel64[0];
+        *w_out = sh.sel64[1];
+        buf ^= 1;
     }
     return d.prefix;
 }
@@ -610,7 +579,7 @@ __device__ __forceinline__ void write_keep(const SampleParams& P, int row, Visit
 // every pass (history table rebuilt per segment).
 template <typename TL>
 __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, const RowCfg& c,
-                                                FinishShared& sh) {
+                                             FinishShared& sh) {
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
     const int nw = (V + 31) >> 5;
@@ -621,9 +590,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     auto for_each_x = [&](auto fn) {
         for (int lo = 0; lo < V; lo += SAMPLE_SEG) {
             const int hi = lo + SAMPLE_SEG < V ? lo + SAMPLE_SEG : V;
-            if (c.pen)
-                count_history<TL>(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2, nullptr, nullptr,
-                                  nullptr, rowp);
+            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2);
             for (int i = lo + threadIdx.x; i < hi; i += LLIMA_WG) {
                 float l = load_one<TL>(rowp, i);
                 if (l != l) l = -__builtin_inff();
@@ -636,6 +603,37 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
             }
             __syncthreads();
         }
+    };
+    // Radix select over the row: histogram rounds that visit every element.
+    auto radix = [&](auto elem, uint32_t kmin, uint32_t kmax, auto pick) {
+        // elem(x, id, fn): calls fn(key, weight) for elements taking part
+        Digits d = digits_init(kmin, kmax);
+        uint64_t acc = 0;
+        uint32_t rem = 0;
+        while (d.top >= 0) {
+            const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+            const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
+            sh.hcnt[0][threadIdx.x] = 0;
+            sh.hmass[0][threadIdx.x] = 0;
+            __syncthreads();
+            const uint32_t prefix = d.prefix, pmask = d.pmask;
+            for_each_x([&](float x, uint32_t id) {
+                elem(x, id, [&](uint32_t key, uint64_t w) {
+                    if ((key & pmask) == prefix) {
+                        const uint32_t b = (key >> lo) & bmask;
+                        atomicAdd(&sh.hcnt[0][b], 1u);
+                        if (w) atomicAdd((unsigned long long*)&sh.hmass[0][b], (unsigned long long)w);
+                    }
+                });
+            });
+            __syncthreads();
+            const uint32_t sel = pick(lo, acc, rem);
+            d.prefix |= sel << lo;
+            d.pmask |= bmask << lo;
+            d.top = lo - 1;
+            __syncthreads();
+        }
+        return d.prefix;
     };
 
     if (c.greedy) {
@@ -672,217 +670,405 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         return;
     }
     const float xmax = key_f32(kmax);
-    auto visit_fin = [&](auto fn) {
-        for_each_x([&](float x, uint32_t id) {
-            const uint32_t k = f32_key(x);
-            if (k > LLIMA_KEY_NEG_INF) fn(k, id, 0ull);
-        });
-    };
-    uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
-    if (c.k > 0 && (uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, kmin, kmax, sh);
-    const uint32_t kmin_k = tau > kmin ? tau : kmin;
 
-    auto visit_k = [&](auto fn) {
-        for_each_x([&](float x, uint32_t id) {
-            const uint32_t k = f32_key(x);
-            if (k >= tau) fn(k, id, weight(x, xmax));
-        });
+    // top-k threshold
+    uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
+    if (c.k > 0 && (uint32_t)c.k <= nfin) {
+        uint32_t rem = (uint32_t)c.k;
+        tau = radix(
+            [&](float x, uint32_t, auto fn) {
+                const uint32_t k = f32_key(x);
+                if (k > LLIMA_KEY_NEG_INF) fn(k, 0ull);
+            },
+            kmin, kmax,
+            [&](int, uint64_t&, uint32_t&) {
+                const uint32_t bin = 255u - threadIdx.x;
+                const uint32_t cn = sh.hcnt[0][bin];
+                uint32_t tot;
+                const uint32_t above = block_excl_scan_u32(cn, &tot, sh.bs);
+                if (above < rem && above + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = rem - above; }
+                __syncthreads();
+                rem = sh.sel[1];
+                return sh.sel[0];
+            });
+    }
+    const uint32_t kmin_k = tau > kmin ? tau : kmin;
+    auto elem_k = [&](float x, uint32_t id, auto fn) {
+        const uint32_t k = f32_key(x);
+        if (k >= tau) fn(k, weight(x, xmax));
+        (void)id;
     };
+
+    // top-p threshold
     uint32_t theta = 0;
     if (c.p < 1.0f) {
         uint64_t Z = 0;
-        visit_k([&](uint32_t, uint32_t, uint64_t w) { Z += w; });
+        for_each_x([&](float x, uint32_t id) { elem_k(x, id, [&](uint32_t, uint64_t w) { Z += w; }); });
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc(visit_k, PZ, kmin_k, kmax, sh);
+        uint64_t acc = 0;
+        theta = radix(elem_k, kmin_k, kmax, [&](int, uint64_t&, uint32_t&) {
+            const uint32_t t = threadIdx.x, bin = 255u - t;
+            const uint32_t cn = sh.hcnt[0][bin];
+            uint64_t m = sh.hmass[0][bin], tot;
+            const uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
+            const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
+            const uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
+            const uint32_t top_nonempty = 255u - block_max_u32(cn > 0 ? 255u - t : 0u, sh.bs);
+            const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
+            if (t == sel_t) { sh.sel[0] = bin; sh.sel64[0] = above; }
+            __syncthreads();
+            acc = sh.sel64[0];
+            return sh.sel[0];
+        });
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
-    auto visit_final = [&](auto fn) {
-        visit_k([&](uint32_t k, uint32_t id, uint64_t w) {
-            if (k >= theta && w >= mthr) fn(k, id, w);
-        });
+    auto fin_elem = [&](float x, uint32_t id, auto fn) {
+        const uint32_t k = f32_key(x);
+        if (k >= tau && k >= theta) {
+            const uint64_t w = weight(x, xmax);
+            if (w >= mthr) fn(id, w);
+        }
     };
     uint64_t Zf = 0;
-    visit_final([&](uint32_t, uint32_t, uint64_t w) { Zf += w; });
+    for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t, uint64_t w) { Zf += w; }); });
     Zf = block_sum_u64(Zf, sh.bs);
     int32_t tok = -1;
     float prob = 0.0f;
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
-        uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc(visit_final, target, (uint32_t)V, &wtok, sh);
+        uint64_t acc = 0, wtok = 0;
+        tok = (int32_t)radix(
+            [&](float x, uint32_t id, auto fn) {
+                fin_elem(x, id, [&](uint32_t i, uint64_t w) { if (w) fn(i, w); });
+            },
+            0u, (uint32_t)(V > 1 ? V - 1 : 1),
+            [&](int, uint64_t&, uint32_t&) {
+                const uint32_t bin = threadIdx.x;
+                uint64_t m = sh.hmass[0][bin], tot;
+                const uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
+                if (m > 0 && below <= target && target < below + m) {
+                    sh.sel[0] = bin; sh.sel64[0] = below; sh.sel64[1] = m;
+                }
+                __syncthreads();
+                acc = sh.sel64[0];
+                wtok = sh.sel64[1];
+                return sh.sel[0];
+            });
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
-            visit_final([&](uint32_t, uint32_t id, uint64_t) { set(id); });
+            for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t i, uint64_t) { set(i); }); });
         });
 }
 
 // ------------------------------------------------------------------ fast path
-// The survivors of top-k held one per thread (at most SMALL_K): top-p, min-p
-// and the draw by direct sums over the LDS copy of the survivors.
-__device__ __forceinline__ void finish_small(const SampleParams& P, int row, const RowCfg& c,
-                                             uint32_t nk, uint32_t kmax, FinishShared& sh) {
-    const uint32_t t = threadIdx.x;
-    const bool mine = t < nk;
-    const uint32_t key = mine ? sh.kkey[t] : 0u;
-    const uint32_t id = mine ? sh.kid[t] : 0u;
-    const uint64_t w = mine ? sh.kw[t] : 0ull;
+// Up to 64 survivors of top-k, in skey/sid.  Every wave holds all of them, one
+// per lane; the pairwise sums (mass above a key, mass of ids up to an id) are
+// split over the 4 waves by the survivor they read.
+__device__ __forceinline__ void fin_small(const SampleParams& P, int row, const RowCfg& c,
+                                          uint32_t nk, uint32_t kmax, FinishShared& sh) {
+    const uint32_t lane = lane_id(), wave = wave_id();
+    const bool mine = lane < nk;
+    const uint32_t key = mine ? sh.skey[lane] : 0u;
+    const uint32_t id = mine ? sh.sid[lane] : 0u;
+    const uint64_t w = mine ? weight(key_f32(key), key_f32(kmax)) : 0ull;
+    const uint32_t j0 = wave * 16u;
     bool fin = mine;
     if (c.p < 1.0f) {
-        const uint64_t Z = block_sum_u64(w, sh.bs);
+        const uint64_t Z = wave_sum_u64(w);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        uint64_t above = 0;                       // mass strictly above this key
-        for (uint32_t j = 0; j < nk; ++j) above += sh.kkey[j] > key ? sh.kw[j] : 0ull;
+        uint64_t part = 0;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 16; ++jj) {
+            const uint32_t j = j0 + jj;
+            if (j < nk) {
+                const uint32_t kj = readlane(key, j);
+                const uint64_t wj = readlane64(w, j);
+                part += kj > key ? wj : 0ull;
+            }
+        }
+        sh.part[0][wave][lane] = part;
+        __syncthreads();
+        uint64_t above = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) above += sh.part[0][w2][lane];
         fin = fin && ((((llima_u128)above << 32) < PZ) || key == kmax);
     }
     if (c.m > 0.0f) fin = fin && w >= (frac32(c.m) << 4);
-    if (mine) sh.kwf[t] = fin ? w : 0ull;
-    const uint64_t Zf = block_sum_u64(fin ? w : 0ull, sh.bs);   // barrier also publishes kwf
-    int32_t tok = -1;
-    if (Zf > 0 && fin && w > 0) {
+    const uint64_t wf = fin ? w : 0ull;
+    const uint64_t Zf = wave_sum_u64(wf);            // the same in every wave
+    if (Zf == 0) {
+        if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
+    } else {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
-        uint64_t upto = 0;                        // mass of final ids <= this id
-        for (uint32_t j = 0; j < nk; ++j) upto += sh.kid[j] <= id ? sh.kwf[j] : 0ull;
-        if (upto - w <= target && target < upto) {
-            tok = (int32_t)id;
-            write_result(P, row, tok, (float)((double)w / (double)Zf));
+        uint64_t part = 0;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 16; ++jj) {
+            const uint32_t j = j0 + jj;
+            if (j < nk) {
+                const uint32_t ij = readlane(id, j);
+                const uint64_t wj = readlane64(wf, j);
+                part += ij <= id ? wj : 0ull;
+            }
         }
+        sh.part[1][wave][lane] = part;
+        __syncthreads();
+        uint64_t upto = 0;                            // mass of final ids <= this id
+#pragma unroll
+        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) upto += sh.part[1][w2][lane];
+        if (wave == 0 && wf > 0 && upto - wf <= target && target < upto)
+            write_result(P, row, (int32_t)id, (float)((double)wf / (double)Zf));
     }
-    if (Zf == 0 && t == 0) write_result(P, row, -1, 0.0f);
     if (P.out_keep)
-        write_keep(P, row, [&](auto set) { if (fin) set(id); });
+        write_keep(P, row, [&](auto set) { if (wave == 0 && fin) set(id); });
 }
 
-// Many survivors (top-k disabled, ties, k > SMALL_K): register-resident
-// candidates (slot j of thread t is candidate t + 256 j) and radix selects.
-__device__ __forceinline__ void finish_large(const SampleParams& P, int row, const RowCfg& c,
-                                             uint32_t n, uint32_t tau, uint32_t kmax,
-                                             FinishShared& sh) {
-    uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
+// Many survivors (top-k disabled, ties, k > 64): radix selects over the
+// register-resident candidates.
+__device__ __forceinline__ void fin_large(const SampleParams& P, int row, const RowCfg& c,
+                                          uint32_t (&key)[SAMPLE_SLOTS],
+                                          const uint32_t (&id)[SAMPLE_SLOTS], uint32_t tau,
+                                          uint32_t kmax, FinishShared& sh, int& buf) {
     uint64_t w[SAMPLE_SLOTS];
     const float xmax = key_f32(kmax);
+    uint64_t Z = 0;
 #pragma unroll
     for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        const uint32_t s = threadIdx.x + j * LLIMA_WG;
-        key[j] = 0; id[j] = 0; w[j] = 0;
-        if (s < n) {
-            const uint64_t q = sh.u.cbuf[s];
-            key[j] = (uint32_t)(q >> 32);
-            id[j] = (uint32_t)q;
-            if (key[j] >= tau) w[j] = weight(key_f32(key[j]), xmax);
-        }
+        if (key[j] < tau) key[j] = 0;
+        w[j] = key[j] ? weight(key_f32(key[j]), xmax) : 0ull;
+        Z += w[j];
     }
-    auto visit_k = [&](auto fn) {
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j)
-            if (key[j] >= tau) fn(key[j], id[j], w[j]);
-    };
     uint32_t theta = 0;
     if (c.p < 1.0f) {
-        uint64_t Z = 0;
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) Z += w[j];
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = select_topp_desc(visit_k, PZ, tau, kmax, sh);
+        theta = fin_topp_desc(key, w, PZ, tau, kmax, sh, buf);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
-    auto visit_final = [&](auto fn) {
-        visit_k([&](uint32_t k, uint32_t i, uint64_t ww) {
-            if (k >= theta && ww >= mthr) fn(k, i, ww);
-        });
-    };
+    uint32_t fmask = 0;
     uint64_t Zf = 0;
-    visit_final([&](uint32_t, uint32_t, uint64_t ww) { Zf += ww; });
+#pragma unroll
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        const bool f = key[j] && key[j] >= theta && w[j] >= mthr;
+        fmask |= f ? (1u << j) : 0u;
+        w[j] = f ? w[j] : 0ull;
+        Zf += w[j];
+    }
     Zf = block_sum_u64(Zf, sh.bs);
     int32_t tok = -1;
     float prob = 0.0f;
     if (Zf > 0) {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
         uint64_t wtok = 0;
-        tok = (int32_t)select_draw_asc(visit_final, target, (uint32_t)P.V, &wtok, sh);
+        tok = (int32_t)fin_draw_asc(id, w, target, (uint32_t)P.V, &wtok, sh, buf);
         prob = (float)((double)wtok / (double)Zf);
     }
     if (threadIdx.x == 0) write_result(P, row, tok, prob);
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
-            visit_final([&](uint32_t, uint32_t i, uint64_t) { set(i); });
+#pragma unroll
+            for (int j = 0; j < SAMPLE_SLOTS; ++j)
+                if ((fmask >> j) & 1u) set(id[j]);
         });
 }
 
-// Sampling from the gathered candidates (n of them in sh.u.cbuf).  Returns false
-// when they cannot be proven to contain the kept set (the caller then runs the
-// full-row path).
-__device__ __forceinline__ bool finish_fast(const SampleParams& P, int row, const RowCfg& c,
-                                            uint32_t n, uint32_t flags, uint32_t bound_key,
-                                            FinishShared& sh) {
-    // ---- values after the temperature, as keys, in place: (key << 32 | id)
-    uint32_t kmax = 0, nkmin = 0, nfin = 0;
-    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
-        const uint64_t q = sh.u.cbuf[s];
-        const uint32_t k = f32_key(__uint_as_float((uint32_t)(q >> 32)) / c.T);
-        sh.u.cbuf[s] = ((uint64_t)k << 32) | (uint32_t)q;
-        if (k > LLIMA_KEY_NEG_INF) {
-            nfin++;
-            kmax = k > kmax ? k : kmax;
-            nkmin = ~k > nkmin ? ~k : nkmin;
+// The finish from the sweep's candidates; false when the row needs the
+// full-row path.
+__device__ __forceinline__ bool fin_fast(const SampleParams& P, int row, const RowCfg& c,
+                                         FinishShared& sh) {
+    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
+    const int S = P.S;
+    const ChunkHdr* hdr = P.hdr + (size_t)row * S;
+    const bool direct = S <= LLIMA_WG;               // one header per thread
+
+    // ---- 1. loads: this thread's chunk header, then its candidate slots (the
+    //         first `pre` slots of every chunk, whatever their counts)
+    uint32_t h_count = 0, h_flags = 0, h_bound = 0;
+    uint64_t h_greedy = 0;
+    if (direct && (int)t < S) {
+        const ChunkHdr h = hdr[t];
+        h_count = h.count; h_flags = h.flags; h_bound = h.bound; h_greedy = h.greedy;
+    }
+    uint64_t q[SAMPLE_SLOTS];
+    const uint64_t* crow = P.cand + (size_t)row * S * P.share;
+    if (direct) {
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+            const uint32_t ch = __umulhi(f, P.pre_magic);
+            const bool in = ch < (uint32_t)S;
+            const uint32_t e = f - ch * (uint32_t)P.pre;
+            q[j] = crow[(size_t)(in ? ch : 0u) * P.share + (in ? e : 0u)];
         }
     }
-    kmax = block_max_u32(kmax, sh.bs);
-    const uint32_t kmin = ~block_max_u32(nkmin, sh.bs);
-    nfin = block_sum_u32(nfin, sh.bs);
-    if (nfin == 0) {
-        // Every candidate is -inf after the temperature (or there are none).
-        if (flags & HDR_FILTERED) return false;
-        if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
+    sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
+    sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
+
+    // ---- 2. merge the chunk headers
+    uint32_t fl = 0, bound = 0, n = 0, spill = 0;
+    uint64_t greedy = 0;
+    if (direct) {
+        sh.ccount[t] = h_count;
+        const uint32_t wfl = wave_or_u32(h_flags);
+        const uint32_t wb = wave_max_u32((h_flags & HDR_FILTERED) ? h_bound : 0u);
+        const uint32_t wn = wave_sum_u32(h_count);
+        const uint32_t wsp = wave_max_u32(h_count > (uint32_t)P.pre ? 1u : 0u);
+        const uint64_t wg = wave_max_u64(h_greedy);
+        if (lane == 0) {
+            sh.r32[0][wave] = wfl; sh.r32[1][wave] = wb; sh.r32[2][wave] = wn;
+            sh.r32[3][wave] = wsp; sh.r64[1][wave] = wg;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            fl |= sh.r32[0][w];
+            bound = sh.r32[1][w] > bound ? sh.r32[1][w] : bound;
+            n += sh.r32[2][w];
+            spill |= sh.r32[3][w];
+            greedy = sh.r64[1][w] > greedy ? sh.r64[1][w] : greedy;
+        }
+    } else {
+        uint32_t f2 = 0, b2 = 0;
+        uint64_t g2 = 0;
+        for (int ch = t; ch < S; ch += LLIMA_WG) {
+            const ChunkHdr h = hdr[ch];
+            f2 |= h.flags;
+            if (h.flags & HDR_FILTERED) b2 = h.bound > b2 ? h.bound : b2;
+            g2 = h.greedy > g2 ? h.greedy : g2;
+        }
+        fl = block_max_u32(f2 & HDR_OVERFLOW, sh.bs) | block_max_u32(f2 & HDR_FILTERED, sh.bs);
+        bound = block_max_u32(b2, sh.bs);
+        greedy = block_max_u64(g2, sh.bs);
+        fl |= HDR_OVERFLOW;                           // no direct gather: full-row path
+    }
+
+    if (c.greedy) {
+        if (!(fl & HDR_OVERFLOW)) {
+            const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
+            const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
+            if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+            if (P.out_keep)
+                write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
+            return true;
+        }
+        return false;
+    }
+    if ((fl & HDR_OVERFLOW) || n > SAMPLE_FIN_CAP) return false;
+
+    // ---- 3. which slots hold candidates; a chunk with more than `pre` of
+    //         them sends every row candidate through LDS in chunk order
+    uint32_t valid = 0;
+    if (!spill) {
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+            const uint32_t ch = __umulhi(f, P.pre_magic);
+            const uint32_t e = f - ch * (uint32_t)P.pre;
+            if (ch < (uint32_t)S && e < sh.ccount[ch < (uint32_t)S ? ch : 0u]) valid |= 1u << j;
+        }
+    } else {
+        const uint32_t cn = (int)t < S ? sh.ccount[t] : 0u;
+        const uint32_t inc = wave_incl_scan_u32(cn);
+        const uint32_t off = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
+        if ((int)t < S) sh.ccount[t] = off;           // own slot: read before by this thread only
+        __syncthreads();
+        for (int ch = (int)wave; ch < S; ch += LLIMA_WAVES) {
+            const uint32_t o = sh.ccount[ch];
+            const uint32_t m = hdr[ch].count;
+            const uint64_t* src = crow + (size_t)ch * P.share;
+            for (uint32_t i = lane; i < m; i += 64) sh.u.cbuf[o + i] = src[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+            if (f < n) { q[j] = sh.u.cbuf[f]; valid |= 1u << j; }
+        }
+    }
+
+    // ---- 4. keys of x / T; candidates below the largest chunk bound cannot be
+    //         in the top-k set (that chunk alone has k values at or above it)
+    const uint32_t kb = (fl & HDR_FILTERED) ? f32_key(key_f32(bound) / c.T) : 0u;
+    uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
+    uint32_t kmax = 0, nkmin = 0, nkeep = 0;
+#pragma unroll
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        const uint32_t k = f32_key(__uint_as_float((uint32_t)(q[j] >> 32)) / c.T);
+        const bool keep = ((valid >> j) & 1u) && k > LLIMA_KEY_NEG_INF && k >= kb;
+        key[j] = keep ? k : 0u;
+        id[j] = (uint32_t)q[j];
+        nkeep += keep ? 1u : 0u;
+        kmax = keep && k > kmax ? k : kmax;
+        nkmin = keep && ~k > nkmin ? ~k : nkmin;
+    }
+    {
+        const uint32_t a = wave_max_u32(kmax), b = wave_max_u32(nkmin), s = wave_sum_u32(nkeep);
+        if (lane == 0) { sh.r32[4][wave] = a; sh.r32[5][wave] = b; sh.r32[6][wave] = s; }
+        __syncthreads();
+        kmax = 0; nkmin = 0; nkeep = 0;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            kmax = sh.r32[4][w] > kmax ? sh.r32[4][w] : kmax;
+            nkmin = sh.r32[5][w] > nkmin ? sh.r32[5][w] : nkmin;
+            nkeep += sh.r32[6][w];
+        }
+    }
+    const uint32_t kmin = ~nkmin;
+    if (nkeep == 0) {
+        // every candidate is -inf (or there are none): nothing is admissible
+        if (fl & HDR_FILTERED) return false;
+        if (t == 0) write_result(P, row, -1, 0.0f);
         if (P.out_keep) write_keep(P, row, [&](auto) {});
         return true;
     }
 
-    // ---- top-k threshold, then the proof that the pre-filter kept every member:
-    // a value below a chunk's lowered bound g has x <= fl(g / T) < tau.
-    uint32_t tau = LLIMA_KEY_NEG_INF + 1u;
-    if (c.k > 0) {
-        auto visit_fin = [&](auto fn) {
-            for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
-                const uint32_t k = (uint32_t)(sh.u.cbuf[s] >> 32);
-                if (k > LLIMA_KEY_NEG_INF) fn(k, 0u, 0ull);
-            }
-        };
-        if ((uint32_t)c.k <= nfin) tau = select_kth_desc(visit_fin, (uint32_t)c.k, kmin, kmax, sh);
-        else if (flags & HDR_FILTERED) return false;
-        if (flags & HDR_FILTERED) {
-            const float gq = lower_bound_margin(key_f32(bound_key)) / c.T;
-            if (!(gq < key_f32(tau))) return false;
-        }
+    // ---- 5. top-k threshold, then the proof that the sweep kept every member:
+    //         a value below a chunk's lowered bound g has x <= fl(g / T) < tau
+    int buf = 0;
+    uint32_t tau = kmin;
+    if (c.k > 0 && (uint32_t)c.k < nkeep) tau = fin_kth_desc(key, (uint32_t)c.k, kmin, kmax, sh, buf);
+    else if (c.k > 0 && (uint32_t)c.k > nkeep && (fl & HDR_FILTERED)) return false;
+    if (fl & HDR_FILTERED) {
+        const float gq = lower_bound_margin(key_f32(bound)) / c.T;
+        if (!(gq < key_f32(tau))) return false;
     }
 
-    // ---- survivors of top-k: one per thread when few
-    uint32_t cnt = 0;
-    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) cnt += (uint32_t)(sh.u.cbuf[s] >> 32) >= tau;
-    const uint32_t nk = block_sum_u32(cnt, sh.bs);
-    if (nk > SMALL_K) {
-        finish_large(P, row, c, n, tau, kmax, sh);
+    // ---- 6. survivors: one per lane when few
+    uint64_t sm[SAMPLE_SLOTS];
+    uint32_t wn = 0;
+#pragma unroll
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        sm[j] = ballot(key[j] >= tau);
+        wn += (uint32_t)__popcll(sm[j]);
+    }
+    if (lane == 0) sh.r32[7][wave] = wn;
+    __syncthreads();
+    uint32_t nk = 0, o = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) {
+        o += (uint32_t)w < wave ? sh.r32[7][w] : 0u;
+        nk += sh.r32[7][w];
+    }
+    if (nk > SAMPLE_SMALL) {
+        fin_large(P, row, c, key, id, tau, kmax, sh, buf);
         return true;
     }
-    if (threadIdx.x == 0) sh.nk = 0;
-    __syncthreads();
-    const float xmax = key_f32(kmax);
-    for (uint32_t s = threadIdx.x; s < n; s += LLIMA_WG) {
-        const uint64_t q = sh.u.cbuf[s];
-        const uint32_t k = (uint32_t)(q >> 32);
-        if (k >= tau) {
-            const uint32_t slot = atomicAdd(&sh.nk, 1u);
-            sh.kkey[slot] = k;
-            sh.kid[slot] = (uint32_t)q;
-            sh.kw[slot] = weight(key_f32(k), xmax);
+#pragma unroll
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        if (sm[j]) {
+            if (key[j] >= tau) {
+                const uint32_t s = o + mbcnt(sm[j]);
+                sh.skey[s] = key[j];
+                sh.sid[s] = id[j];
+            }
+            o += (uint32_t)__popcll(sm[j]);
         }
     }
     __syncthreads();
-    finish_small(P, row, c, nk, kmax, sh);
+    fin_small(P, row, c, nk, kmax, sh);
     return true;
 }
 
@@ -891,102 +1077,10 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     __shared__ FinishShared sh;
     const int row = blockIdx.x;
     const RowCfg c = load_cfg(P, row);
-    const ChunkHdr* hdr = P.hdr + (size_t)row * P.S;
-
-    // ---- merge the chunk headers
-    uint32_t flags = 0, bound = 0, n = 0;
-    uint64_t greedy = 0;
-    for (int ch = threadIdx.x; ch < P.S; ch += LLIMA_WG) {
-        const ChunkHdr h = hdr[ch];
-        flags |= h.flags;
-        n += h.count;
-        if (h.flags & HDR_FILTERED) bound = h.bound > bound ? h.bound : bound;
-        greedy = h.greedy > greedy ? h.greedy : greedy;
-    }
-    // OR of flags through a max of the two flag bits
-    const uint32_t fl = block_max_u32(flags & HDR_OVERFLOW, sh.bs) |
-                        block_max_u32(flags & HDR_FILTERED, sh.bs);
-    bound = block_max_u32(bound, sh.bs);
-    n = block_sum_u32(n, sh.bs);
-
-    bool done = false;
-    if (c.greedy) {
-        greedy = block_max_u64(greedy, sh.bs);
-        if (!(fl & HDR_OVERFLOW)) {
-            const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
-            const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
-            if (threadIdx.x == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
-            if (P.out_keep)
-                write_keep(P, row, [&](auto set) { if (threadIdx.x == 0 && ok) set(tok); });
-            done = true;
-        }
-    } else if (!(fl & HDR_OVERFLOW) && n <= SAMPLE_FIN_CAP) {
-        // ---- gather the candidates into LDS
-        if (P.S <= LLIMA_WG) {
-            // chunk offsets by one block scan, a position -> chunk table, then
-            // every thread issues all of its loads before storing any
-            const int ch = (int)threadIdx.x;
-            const uint32_t cnt = ch < P.S ? hdr[ch].count : 0u;
-            uint32_t tot;
-            const uint32_t ex = block_excl_scan_u32(cnt, &tot, sh.bs);
-            sh.off[threadIdx.x] = ex;
-            for (uint32_t i = 0; i < cnt; ++i) sh.cid[ex + i] = (uint8_t)ch;
-            __syncthreads();
-            uint64_t q[SAMPLE_SLOTS];
-#pragma unroll
-            for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-                const uint32_t f = threadIdx.x + j * LLIMA_WG;
-                const uint32_t cc = f < n ? sh.cid[f] : 0u;
-                const uint32_t o = f < n ? f - sh.off[cc] : 0u;
-                q[j] = P.cand[((size_t)row * P.S + cc) * P.share + o];
-            }
-#pragma unroll
-            for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-                const uint32_t f = threadIdx.x + j * LLIMA_WG;
-                if (f < n) sh.u.cbuf[f] = q[j];
-            }
-            __syncthreads();
-        } else {
-            uint32_t base = 0;
-            for (int g0 = 0; g0 < P.S; g0 += LLIMA_WG) {
-                const int ch = g0 + (int)threadIdx.x;
-                const uint32_t cnt = ch < P.S ? hdr[ch].count : 0u;
-                uint32_t tot;
-                const uint32_t ex = block_excl_scan_u32(cnt, &tot, sh.bs);
-                sh.off[threadIdx.x] = base + ex;
-                __syncthreads();
-                const int nch = P.S - g0 < LLIMA_WG ? P.S - g0 : LLIMA_WG;
-                for (int k = (int)(threadIdx.x >> 6); k < nch; k += LLIMA_WAVES) {
-                    const uint32_t o = sh.off[k];
-                    const uint32_t m = hdr[g0 + k].count;
-                    const uint64_t* src = P.cand + ((size_t)row * P.S + g0 + k) * P.share;
-                    for (uint32_t i = lane_id(); i < m; i += 64) sh.u.cbuf[o + i] = src[i];
-                }
-                base += tot;
-                __syncthreads();
-            }
-        }
-        done = finish_fast(P, row, c, n, fl, bound, sh);
-    }
-    if (!done) finish_full_row<TL>(P, row, c, sh);
+    if (!fin_fast(P, row, c, sh)) finish_full_row<TL>(P, row, c, sh);
 }
 
 // ================================================================== host side
-struct Tile { int E; int S; };
-
-static Tile choose_tile(int B, int V, int dtype, int k) {
-    // 16 KB of logits per workgroup; smaller chunks while the grid is small, as
-    // long as the row's candidates (about k per chunk) fit the finish.
-    int E = dtype == LLIMA_F32 ? 16 : 32;
-    auto S_of = [&](int e) { return (V + LLIMA_WG * e - 1) / (LLIMA_WG * e); };
-    while (E > 8) {
-        if ((int64_t)B * S_of(E) >= 1024) break;
-        if (k > 0 && (int64_t)S_of(E / 2) * k > SAMPLE_FIN_CAP / 2) break;
-        E /= 2;
-    }
-    return {E, S_of(E)};
-}
-
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 static int max_chunks(int V) { return (V + SAMPLE_MIN_CHUNK - 1) / SAMPLE_MIN_CHUNK; }
 
@@ -1047,21 +1141,21 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
     P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0) &&
                (V % (int32_t)(16 / esz) == 0);
-    const int k_hint = cfg->top_k_rows ? 0 : cfg->top_k;
-    const Tile t = choose_tile(B, V, dtype, (k_hint > 0 && k_hint < V) ? k_hint : 0);
-    P.S = t.S;
-    P.share = SAMPLE_ROW_CAND / t.S;
+    // 16 KB of logits per workgroup: 4096 fp32 or 8192 bf16 values.
+    const int chunk = dtype == LLIMA_F32 ? 4096 : 8192;
+    P.S = (V + chunk - 1) / chunk;
+    P.share = SAMPLE_ROW_CAND / P.S;
+    P.pre = SAMPLE_FIN_CAP / P.S < P.share ? SAMPLE_FIN_CAP / P.S : P.share;
+    if (P.pre < 1) P.pre = 1;
+    P.pre_magic = P.pre > 1 ? (uint32_t)(0xFFFFFFFFull / (uint64_t)P.pre + 1ull) : 0xFFFFFFFFu;
     P.hdr = (ChunkHdr*)workspace;
     P.cand = (uint64_t*)((char*)workspace + al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)));
     hipStream_t st = (hipStream_t)stream;
     if (dtype == LLIMA_F32) {
-        if (t.E == 8) launch_sweep<float, 8>(P, st);
-        else launch_sweep<float, 16>(P, st);
+        launch_sweep<float, 16>(P, st);
         hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
-        if (t.E == 8) launch_sweep<uint16_t, 8>(P, st);
-        else if (t.E == 16) launch_sweep<uint16_t, 16>(P, st);
-        else launch_sweep<uint16_t, 32>(P, st);
+        launch_sweep<uint16_t, 32>(P, st);
         hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
