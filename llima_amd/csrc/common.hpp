@@ -63,12 +63,21 @@ __device__ __forceinline__ float exp_neg(float d) {
     return __builtin_ldexpf(p, (int)n);
 }
 
+// An integral float in [0, 2^40) as uint64 (exact; by its bits).
+__device__ __forceinline__ uint64_t f32_integral_to_u64(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const int ex = (int)(u >> 23) - 150;                // f = m * 2^ex, m the significand
+    const uint64_t m = (uint64_t)((u & 0x7FFFFFu) | 0x800000u);
+    const uint64_t r = ex >= 0 ? m << ex : m >> (-ex < 63 ? -ex : 63);
+    return u ? r : 0ull;
+}
+
 __device__ __forceinline__ uint64_t weight(float x, float xmax) {
     if (x == xmax) return LLIMA_W_ONE;
     float d = x - xmax;
     if (!(d >= -26.0f)) return 0;
     float e = exp_neg(d);
-    return (uint64_t)__builtin_rintf(__builtin_ldexpf(e, 36));
+    return f32_integral_to_u64(__builtin_rintf(__builtin_ldexpf(e, 36)));
 }
 
 // rint(v * 2^32) clamped to [0, 2^32].
@@ -101,6 +110,12 @@ __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_bal
 __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// base + number of set bits of m below this lane.
+__device__ __forceinline__ uint32_t mbcnt_add(uint64_t m, uint32_t base) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, base));
 }
 
 __device__ __forceinline__ uint32_t readlane(uint32_t v, uint32_t l) {

@@ -57,8 +57,9 @@ struct ChunkHdr {
     uint32_t flags;      // HDR_*
     uint32_t bound;      // key of the chunk bound (when FILTERED)
     uint32_t pad;
-    uint64_t greedy;     // (key << 32 | ~index) of the chunk maximum
-    uint64_t pad2;
+    uint32_t w[8];       // sampling rows: keys of the two largest lane maxima of
+                         // each wave (0: none); greedy rows: w[1]:w[0] =
+                         // (key << 32 | ~index) of the chunk maximum
 };
 
 struct SampleParams {
@@ -76,9 +77,13 @@ struct SampleParams {
     uint64_t* cand;      // [B][S][share]  (value bits << 32 | id)
     int32_t B, V, H_max, S, share;
     int32_t vec_ok;
-    int32_t pre;         // candidate slots per chunk the finish loads up front
-    uint32_t pre_magic;  // f / pre == umulhi(f, pre_magic) for f < 4096
+    int32_t lp, ls;      // log2 of pre (candidate slots per chunk the finish loads
+                         // up front) and of share (slots per chunk)
 };
+
+// Pads a chunk's first `pre` candidate slots behind its candidates: value -inf,
+// which no bound admits.
+#define SAMPLE_SENTINEL (0xFF800000ull << 32)
 
 struct RowCfg {
     float T, p, m, R, alpha, beta;
@@ -156,14 +161,20 @@ __device__ __forceinline__ void count_history(const SampleParams& P, int row, in
 // VEC: rows are 16-byte aligned and V is a multiple of the values per load, so
 // every chunk (also a row's partial last one) is read with 16-byte loads from
 // clamped, always-valid addresses and the out-of-row values masked in registers.
-template <typename TL, int E, bool VEC>
+template <bool B>
+struct Flag { static constexpr bool value = B; };
+
+// MASK: a grammar bitmask is given.  NaN values are never turned into -inf
+// here: every later use is an ordered comparison (x > best, x > lane max,
+// x >= bound), which a NaN fails, so a NaN is never selected.
+template <typename TL, int E, bool VEC, bool MASK>
 __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
     constexpr int NL = E / EPL;                // loads per thread
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr int CW = CHUNK / 2;              // history count words
     __shared__ __align__(16) uint32_t cnt[CW];
-    __shared__ uint32_t xw[2][LLIMA_WAVES];
+    __shared__ uint32_t xw[4][LLIMA_WAVES];
     __shared__ uint64_t xg[LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
@@ -191,10 +202,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         hid[b] = (b * LLIMA_WG < H) ? hrow[j < H ? j : H - 1] : -1;
     }
     uint32_t mword[NL];
+    if constexpr (MASK) {
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-        mword[j] = mrow ? mrow[(i0 < V ? i0 : V - 1) >> 5] : 0xFFFFFFFFu;
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+            mword[j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
+        }
     }
     llima_u32x4 raw[NL];
 #pragma unroll
@@ -239,48 +252,62 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         __syncthreads();
     }
 
-    // ---- 3. values: mask / NaN / out of row -> -inf, history values penalised
+    // ---- 3. values: masked and out-of-row -> -inf, history values penalised
     float v[E];
+    auto convert = [&](auto pen_tag) {
+        constexpr bool PEN = decltype(pen_tag)::value;
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-        const uint32_t mb = mword[j] >> (i0 & 31);
-        float xs[EPL];
-        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-        if constexpr (sizeof(TL) == 4) {
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+            float xs[EPL];
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+            if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                xs[2 * e] = __uint_as_float(w4[e] << 16);
-                xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-            }
-        }
-        uint32_t cw[EPL / 2];
-#pragma unroll
-        for (int e = 0; e < EPL / 2; ++e) cw[e] = 0;
-        if (c.pen) {
-            const uint32_t* cp = cnt + ((i0 - c0) >> 1);
-            if constexpr (EPL == 4) {
-                const uint2 w2 = *(const uint2*)cp;
-                cw[0] = w2.x; cw[1] = w2.y;
+                for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
             } else {
-                const llima_u32x4 wq = *(const llima_u32x4*)cp;
-                cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
-            }
-        }
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float x = xs[e];
-            const uint32_t inrow = VEC ? (uint32_t)(i0 < c1) : (uint32_t)(i0 + e < c1);
-            const uint32_t ok = ((mb >> e) & 1u) & inrow & (uint32_t)(x == x);
-            x = ok ? x : NEG_INF;
-            if (c.pen) {
-                const uint32_t cn = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-                if (cn) x = penalize(x, cn, c);
+                for (int e = 0; e < 4; ++e) {
+                    xs[2 * e] = __uint_as_float(w4[e] << 16);
+                    xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
+                }
             }
-            v[j * EPL + e] = x;
+            if constexpr (MASK) {
+                const uint32_t mb = mword[j] >> (i0 & 31);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) xs[e] = ((mb >> e) & 1u) ? xs[e] : NEG_INF;
+            }
+            if constexpr (PEN) {
+                uint32_t cw[EPL / 2];
+                const uint32_t* cp = cnt + ((i0 - c0) >> 1);
+                if constexpr (EPL == 4) {
+                    const uint2 w2 = *(const uint2*)cp;
+                    cw[0] = w2.x; cw[1] = w2.y;
+                } else {
+                    const llima_u32x4 wq = *(const llima_u32x4*)cp;
+                    cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
+                }
+#pragma unroll
+                for (int h = 0; h < EPL / 2; ++h) {
+                    if (cw[h]) {
+                        const uint32_t lo = cw[h] & 0xFFFFu, hi = cw[h] >> 16;
+                        if (lo) xs[2 * h] = penalize(xs[2 * h], lo, c);
+                        if (hi) xs[2 * h + 1] = penalize(xs[2 * h + 1], hi, c);
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) v[j * EPL + e] = xs[e];
+        }
+    };
+    if (c.pen) convert(Flag<true>{});
+    else convert(Flag<false>{});
+    if (c1 - c0 < CHUNK) {                         // the row's last, partial chunk
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+                if (i0 + e >= c1) v[j * EPL + e] = NEG_INF;
         }
     }
 
@@ -305,10 +332,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             uint64_t g = 0;
 #pragma unroll
             for (int w = 0; w < LLIMA_WAVES; ++w) g = xg[w] > g ? xg[w] : g;
-            hdr->count = 0;
-            hdr->flags = 0;
-            hdr->bound = 0;
-            hdr->greedy = g;
+            *(llima_u32x4*)hdr = llima_u32x4{0u, 0u, 0u, 0u};
+            *(llima_u32x4*)hdr->w = llima_u32x4{(uint32_t)g, (uint32_t)(g >> 32), 0u, 0u};
+            *(llima_u32x4*)(hdr->w + 4) = llima_u32x4{0u, 0u, 0u, 0u};
         }
         return;
     }
@@ -320,9 +346,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         float lm = NEG_INF;
 #pragma unroll
         for (int e = 0; e < E; ++e) lm = v[e] > lm ? v[e] : lm;
+        const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
         const uint32_t r = ((uint32_t)c.k + 3u) >> 2;
-        const uint32_t tw = wave_rth_largest(lm > NEG_INF ? f32_key(lm) : 0u, r, SAMPLE_BOUND_LOWBIT);
-        if (lane == 0) xw[0][wave] = tw;
+        const uint32_t tw = wave_rth_largest(lk, r, SAMPLE_BOUND_LOWBIT);
+        const uint32_t wm = wave_max_u32(lk);
+        const uint32_t wm2 = wave_max_u32(lk < wm ? lk : 0u);   // a lane other than the maximum's
+        if (lane == 0) { xw[0][wave] = tw; xw[2][wave] = wm; xw[3][wave] = wm2; }
         __syncthreads();
         gkey = xw[0][0];
 #pragma unroll
@@ -347,9 +376,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         base += (uint32_t)w < wave ? n : 0u;
         total += n;
     }
-    const uint32_t cap = (uint32_t)P.share;
+    const uint32_t cap = 1u << P.ls;
     if (total <= cap) {
-        uint64_t* dst = P.cand + ((size_t)row * P.S + chunk) * P.share;
+        uint64_t* dst = P.cand + (((size_t)row * P.S + chunk) << P.ls);
         uint32_t o = base;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
@@ -360,17 +389,21 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                 const bool pr = x >= g;
                 const uint64_t m = ballot(pr);
                 if (m) {
-                    if (pr) dst[o + mbcnt(m)] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
+                    if (pr) dst[mbcnt_add(m, o)] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
                     o += (uint32_t)__popcll(m);
                 }
             }
         }
+        for (uint32_t i = total + (uint32_t)t; i < (1u << P.lp); i += LLIMA_WG) dst[i] = SAMPLE_SENTINEL;
     }
     if (t == 0) {
-        hdr->count = total <= cap ? total : 0u;
-        hdr->flags = (total > cap ? HDR_OVERFLOW : 0u) | (gkey ? HDR_FILTERED : 0u);
-        hdr->bound = gkey;
-        hdr->greedy = 0;
+        *(llima_u32x4*)hdr = llima_u32x4{total <= cap ? total : 0u,
+                                         (total > cap ? HDR_OVERFLOW : 0u) | (gkey ? HDR_FILTERED : 0u),
+                                         gkey, 0u};
+        *(llima_u32x4*)hdr->w = gkey ? llima_u32x4{xw[2][0], xw[2][1], xw[2][2], xw[2][3]}
+                                     : llima_u32x4{0u, 0u, 0u, 0u};
+        *(llima_u32x4*)(hdr->w + 4) = gkey ? llima_u32x4{xw[3][0], xw[3][1], xw[3][2], xw[3][3]}
+                                           : llima_u32x4{0u, 0u, 0u, 0u};
     }
 }
 
@@ -380,12 +413,16 @@ struct FinishShared {
         uint64_t cbuf[SAMPLE_FIN_CAP];         // candidates gathered in chunk order
         uint32_t table[SAMPLE_SEG / 2];        // full-row path history counts
     } u;
-    uint32_t ccount[LLIMA_WG];                 // candidates per chunk
+    uint32_t wcnt[LLIMA_WAVES][LLIMA_WG];      // each wave's own copy of the chunk counts
+    uint32_t coff[LLIMA_WG];                   // chunk offsets (gather path)
+    uint64_t stage[LLIMA_WAVES][SAMPLE_SMALL]; // survivors of the bound, per wave
     uint32_t hcnt[2][256];                     // radix histograms (double-buffered)
     uint64_t hmass[2][256];
     uint64_t above[256];
-    uint32_t skey[SAMPLE_SMALL], sid[SAMPLE_SMALL];
     uint64_t part[2][LLIMA_WAVES][64];
+    llima_u32x4 sv[LLIMA_WAVES][64];           // each wave's copy of the survivors
+    uint32_t bh[LLIMA_WAVES][256];             // each wave's histogram of header values
+    uint32_t pc[LLIMA_WAVES][64];
     uint32_t r32[8][LLIMA_WAVES];
     uint64_t r64[2][LLIMA_WAVES];
     uint32_t sel[2];
@@ -765,37 +802,64 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 }
 
 // ------------------------------------------------------------------ fast path
-// Up to 64 survivors of top-k, in skey/sid.  Every wave holds all of them, one
-// per lane; the pairwise sums (mass above a key, mass of ids up to an id) are
-// split over the 4 waves by the survivor they read.
-__device__ __forceinline__ void fin_small(const SampleParams& P, int row, const RowCfg& c,
-                                          uint32_t nk, uint32_t kmax, FinishShared& sh) {
+// At most 64 candidates left by the bound, one per lane in every wave (lanes
+// >= nk and candidates that are -inf after the temperature hold key 0).  One
+// pairwise pass, split over the 4 waves by the candidate it reads (broadcast
+// LDS reads of the wave's own copy), gives each lane the number of keys above
+// and equal to its own and the mass above it: the top-k threshold is the key
+// of a lane with (above < k <= above + equal), and the top-p test uses the
+// mass above, which for a kept lane only counts kept lanes.  A second pass
+// gives the mass of final ids up to each id for the draw.  False when the
+// bound cannot be proven to keep the top-k set (full-row path).
+__device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const RowCfg& c,
+                                          uint32_t key, uint32_t id, uint32_t nk, uint32_t nfin,
+                                          uint32_t kmin, uint32_t kmax, uint32_t gthr,
+                                          FinishShared& sh) {
     const uint32_t lane = lane_id(), wave = wave_id();
-    const bool mine = lane < nk;
-    const uint32_t key = mine ? sh.skey[lane] : 0u;
-    const uint32_t id = mine ? sh.sid[lane] : 0u;
-    const uint64_t w = mine ? weight(key_f32(key), key_f32(kmax)) : 0ull;
+    const uint64_t w = key ? weight(key_f32(key), key_f32(kmax)) : 0ull;
     const uint32_t j0 = wave * 16u;
+    sh.sv[wave][lane] = llima_u32x4{key, id, (uint32_t)w, (uint32_t)(w >> 32)};
+    uint32_t gt = 0, eq = 0;
+    uint64_t above = 0;
+    // lanes >= nk hold key 0, weight 0: reading them changes nothing
+#pragma unroll
+    for (uint32_t jj = 0; jj < 16; ++jj) {
+        const llima_u32x4 o = sh.sv[wave][j0 + jj];
+        const uint64_t wj = ((uint64_t)o.w << 32) | o.z;
+        gt += o.x > key ? 1u : 0u;
+        eq += o.x == key ? 1u : 0u;
+        above += o.x > key ? wj : 0ull;
+    }
+    sh.part[0][wave][lane] = above;
+    sh.pc[wave][lane] = gt | (eq << 16);
+    __syncthreads();
+    above = 0; gt = 0; eq = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) {
+        above += sh.part[0][w2][lane];
+        const uint32_t g2 = sh.pc[w2][lane];
+        gt += g2 & 0xFFFFu;
+        eq += g2 >> 16;
+    }
+    uint32_t tau = kmin;
+    if (c.k > 0 && (uint32_t)c.k < nfin) {
+        const bool at = key != 0 && gt < (uint32_t)c.k && gt + eq >= (uint32_t)c.k;
+        tau = wave_max_u32(at ? key : 0u);
+    } else if (c.k > 0 && (uint32_t)c.k > nfin && gthr) {
+        return false;
+    }
+    // the proof that the bound dropped no member of the top-k set: a value
+    // below it has x <= fl(g / T) < tau
+    if (gthr && !(lower_bound_margin(key_f32(gthr)) / c.T < key_f32(tau))) return false;
+
+    const bool mine = key != 0 && key >= tau;
     bool fin = mine;
     if (c.p < 1.0f) {
-        const uint64_t Z = wave_sum_u64(w);
+        // (above << 32) < frac32(p) * Z  <=>  above < ceil(frac32(p) * Z / 2^32)
+        const uint64_t Z = wave_sum_u64(mine ? w : 0ull);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        uint64_t part = 0;
-#pragma unroll
-        for (uint32_t jj = 0; jj < 16; ++jj) {
-            const uint32_t j = j0 + jj;
-            if (j < nk) {
-                const uint32_t kj = readlane(key, j);
-                const uint64_t wj = readlane64(w, j);
-                part += kj > key ? wj : 0ull;
-            }
-        }
-        sh.part[0][wave][lane] = part;
-        __syncthreads();
-        uint64_t above = 0;
-#pragma unroll
-        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) above += sh.part[0][w2][lane];
-        fin = fin && ((((llima_u128)above << 32) < PZ) || key == kmax);
+        const uint64_t plim = (uint64_t)((PZ + 0xFFFFFFFFull) >> 32);
+        fin = fin && (above < plim || key == kmax);
     }
     if (c.m > 0.0f) fin = fin && w >= (frac32(c.m) << 4);
     const uint64_t wf = fin ? w : 0ull;
@@ -804,19 +868,16 @@ __device__ __forceinline__ void fin_small(const SampleParams& P, int row, const 
         if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
     } else {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
-        uint64_t part = 0;
+        sh.sv[wave][lane] = llima_u32x4{id, 0u, (uint32_t)wf, (uint32_t)(wf >> 32)};
+        uint64_t upto = 0;                            // mass of final ids <= this id
 #pragma unroll
         for (uint32_t jj = 0; jj < 16; ++jj) {
-            const uint32_t j = j0 + jj;
-            if (j < nk) {
-                const uint32_t ij = readlane(id, j);
-                const uint64_t wj = readlane64(wf, j);
-                part += ij <= id ? wj : 0ull;
-            }
+            const llima_u32x4 o = sh.sv[wave][j0 + jj];
+            upto += o.x <= id ? (((uint64_t)o.w << 32) | o.z) : 0ull;
         }
-        sh.part[1][wave][lane] = part;
+        sh.part[1][wave][lane] = upto;
         __syncthreads();
-        uint64_t upto = 0;                            // mass of final ids <= this id
+        upto = 0;
 #pragma unroll
         for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) upto += sh.part[1][w2][lane];
         if (wave == 0 && wf > 0 && upto - wf <= target && target < upto)
@@ -824,6 +885,7 @@ __device__ __forceinline__ void fin_small(const SampleParams& P, int row, const 
     }
     if (P.out_keep)
         write_keep(P, row, [&](auto set) { if (wave == 0 && fin) set(id); });
+    return true;
 }
 
 // Many survivors (top-k disabled, ties, k > 64): radix selects over the
@@ -875,129 +937,214 @@ __device__ __forceinline__ void fin_large(const SampleParams& P, int row, const 
         });
 }
 
-// The finish from the sweep's candidates; false when the row needs the
-// full-row path.
+// The row from the sweep's candidates; false when it needs the full-row path.
 __device__ __forceinline__ bool fin_fast(const SampleParams& P, int row, const RowCfg& c,
                                          FinishShared& sh) {
+    constexpr int HPL = 2;                           // chunk headers per lane (S <= 128)
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     const int S = P.S;
+    if (S > 64 * HPL) return false;
     const ChunkHdr* hdr = P.hdr + (size_t)row * S;
-    const bool direct = S <= LLIMA_WG;               // one header per thread
 
-    // ---- 1. loads: this thread's chunk header, then its candidate slots (the
-    //         first `pre` slots of every chunk, whatever their counts)
-    uint32_t h_count = 0, h_flags = 0, h_bound = 0;
-    uint64_t h_greedy = 0;
-    if (direct && (int)t < S) {
-        const ChunkHdr h = hdr[t];
-        h_count = h.count; h_flags = h.flags; h_bound = h.bound; h_greedy = h.greedy;
-    }
+    // ---- 1. loads, all issued before any is used: this thread's candidate
+    //         slots (the first `pre` slots of every chunk, whatever their
+    //         counts), then every header, read by every wave (lane l: chunks l
+    //         and l + 64)
     uint64_t q[SAMPLE_SLOTS];
-    const uint64_t* crow = P.cand + (size_t)row * S * P.share;
-    if (direct) {
+    const uint64_t* crow = P.cand + ((size_t)row * S << P.ls);
+    const uint32_t pmask = (1u << P.lp) - 1u;
 #pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-            const uint32_t ch = __umulhi(f, P.pre_magic);
-            const bool in = ch < (uint32_t)S;
-            const uint32_t e = f - ch * (uint32_t)P.pre;
-            q[j] = crow[(size_t)(in ? ch : 0u) * P.share + (in ? e : 0u)];
-        }
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        const uint32_t f = t + (uint32_t)j * LLIMA_WG;   // chunk f >> lp, slot f & pmask
+        const uint32_t ch = f >> P.lp;
+        q[j] = crow[ch < (uint32_t)S ? (ch << P.ls) + (f & pmask) : 0u];
+    }
+    llima_u32x4 ha[HPL], hb[HPL], hc[HPL];
+#pragma unroll
+    for (int i = 0; i < HPL; ++i) {
+        const int ch = (int)lane + 64 * i;
+        const llima_u32x4* hp = (const llima_u32x4*)(hdr + (ch < S ? ch : 0));
+        ha[i] = hp[0];
+        hb[i] = hp[1];
+        hc[i] = hp[2];
     }
     sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
     sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
 
-    // ---- 2. merge the chunk headers
-    uint32_t fl = 0, bound = 0, n = 0, spill = 0;
+    // ---- 2. header summary, computed by every wave (no barrier)
+    uint32_t fl = 0, bstar = 0, n = 0, spill = 0;
     uint64_t greedy = 0;
-    if (direct) {
-        sh.ccount[t] = h_count;
-        const uint32_t wfl = wave_or_u32(h_flags);
-        const uint32_t wb = wave_max_u32((h_flags & HDR_FILTERED) ? h_bound : 0u);
-        const uint32_t wn = wave_sum_u32(h_count);
-        const uint32_t wsp = wave_max_u32(h_count > (uint32_t)P.pre ? 1u : 0u);
-        const uint64_t wg = wave_max_u64(h_greedy);
-        if (lane == 0) {
-            sh.r32[0][wave] = wfl; sh.r32[1][wave] = wb; sh.r32[2][wave] = wn;
-            sh.r32[3][wave] = wsp; sh.r64[1][wave] = wg;
-        }
-        __syncthreads();
 #pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) {
-            fl |= sh.r32[0][w];
-            bound = sh.r32[1][w] > bound ? sh.r32[1][w] : bound;
-            n += sh.r32[2][w];
-            spill |= sh.r32[3][w];
-            greedy = sh.r64[1][w] > greedy ? sh.r64[1][w] : greedy;
+    for (int i = 0; i < HPL; ++i) {
+        if (i * 64 < S) {
+            const int ch = (int)lane + 64 * i;
+            if (ch < S) {
+                fl |= ha[i].y;
+                if (ha[i].y & HDR_FILTERED) bstar = ha[i].z > bstar ? ha[i].z : bstar;
+                n += ha[i].x;
+                spill |= ha[i].x > (1u << P.lp) ? 1u : 0u;
+                const uint64_t g = ((uint64_t)hb[i].y << 32) | hb[i].x;
+                greedy = g > greedy ? g : greedy;
+                sh.wcnt[wave][ch] = ha[i].x;
+            }
         }
-    } else {
-        uint32_t f2 = 0, b2 = 0;
-        uint64_t g2 = 0;
-        for (int ch = t; ch < S; ch += LLIMA_WG) {
-            const ChunkHdr h = hdr[ch];
-            f2 |= h.flags;
-            if (h.flags & HDR_FILTERED) b2 = h.bound > b2 ? h.bound : b2;
-            g2 = h.greedy > g2 ? h.greedy : g2;
-        }
-        fl = block_max_u32(f2 & HDR_OVERFLOW, sh.bs) | block_max_u32(f2 & HDR_FILTERED, sh.bs);
-        bound = block_max_u32(b2, sh.bs);
-        greedy = block_max_u64(g2, sh.bs);
-        fl |= HDR_OVERFLOW;                           // no direct gather: full-row path
     }
+    fl = wave_or_u32(fl);
+    bstar = wave_max_u32(bstar);
+    n = wave_sum_u32(n);
+    spill = wave_max_u32(spill);
+    greedy = wave_max_u64(greedy);
 
     if (c.greedy) {
-        if (!(fl & HDR_OVERFLOW)) {
-            const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
-            const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
-            if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
-            if (P.out_keep)
-                write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
-            return true;
-        }
-        return false;
+        if (fl & HDR_OVERFLOW) return false;
+        const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
+        const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
+        if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+        if (P.out_keep)
+            write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
+        return true;
     }
     if ((fl & HDR_OVERFLOW) || n > SAMPLE_FIN_CAP) return false;
 
-    // ---- 3. which slots hold candidates; a chunk with more than `pre` of
-    //         them sends every row candidate through LDS in chunk order
-    uint32_t valid = 0;
-    if (!spill) {
+    // ---- 3. bound on the top-k threshold: the largest chunk bound (that chunk
+    //         has k values at or above it), or the k-th largest of the lane
+    //         maxima in the headers (distinct values of the row), whichever is larger
+    uint32_t gthr = bstar;
+    if (c.k > 0 && 8 * S >= c.k) {
+        constexpr int NV = 8 * HPL;
+        uint32_t hv[NV];
+        uint32_t vmax = 0, vmin = 0xFFFFFFFFu, nz = 0;
 #pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-            const uint32_t ch = __umulhi(f, P.pre_magic);
-            const uint32_t e = f - ch * (uint32_t)P.pre;
-            if (ch < (uint32_t)S && e < sh.ccount[ch < (uint32_t)S ? ch : 0u]) valid |= 1u << j;
+        for (int i = 0; i < HPL; ++i) {
+            const bool in = (int)lane + 64 * i < S;
+            const uint32_t a[8] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w,
+                                   hc[i].x, hc[i].y, hc[i].z, hc[i].w};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t x = in ? a[u] : 0u;
+                hv[i * 8 + u] = x;
+                vmax = x > vmax ? x : vmax;
+                vmin = x && x < vmin ? x : vmin;
+                nz += x ? 1u : 0u;
+            }
         }
-    } else {
-        const uint32_t cn = (int)t < S ? sh.ccount[t] : 0u;
+        vmax = wave_max_u32(vmax);
+        vmin = wave_min_u32(vmin);
+        nz = wave_sum_u32(nz);
+        if (nz >= (uint32_t)c.k) {
+            // The lower edge of the histogram bin holding the k-th largest
+            // value (8-bit bins below the bits all the values share), with a
+            // histogram of its own in every wave: no barrier.
+            const uint32_t diff = vmax ^ vmin;
+            uint32_t tb = vmax;
+            if (diff) {
+                const int top = 31 - __builtin_clz(diff);
+                const int lo = top - 7 > 0 ? top - 7 : 0;
+                const uint32_t bmask = (2u << (top - lo)) - 1u;
+                const uint32_t prefix = top == 31 ? 0u : (vmax & ~((2u << top) - 1u));
+                uint32_t* bh = sh.bh[wave];
+                *(llima_u32x4*)(bh + 4 * lane) = llima_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int u = 0; u < NV; ++u)
+                    if (hv[u]) atomicAdd(&bh[(hv[u] >> lo) & bmask], 1u);
+                // lane l holds bins 255 - 4l (top) down to 252 - 4l
+                const llima_u32x4 b4 = *(const llima_u32x4*)(bh + 252 - 4 * lane);
+                const uint32_t s4 = b4.x + b4.y + b4.z + b4.w;
+                const uint32_t inc = wave_incl_scan_u32(s4);   // values in bins >= 252 - 4l
+                const uint64_t hit = ballot(inc >= (uint32_t)c.k);
+                const uint32_t L = (uint32_t)__builtin_ffsll((long long)hit) - 1u;
+                uint32_t acc = readlane(inc - s4, L);
+                const uint32_t q3 = readlane(b4.w, L), q2 = readlane(b4.z, L), q1 = readlane(b4.y, L);
+                uint32_t bin = 252u - 4u * L;
+                if (acc + q3 >= (uint32_t)c.k) bin = 255u - 4u * L;
+                else if (acc + q3 + q2 >= (uint32_t)c.k) bin = 254u - 4u * L;
+                else if (acc + q3 + q2 + q1 >= (uint32_t)c.k) bin = 253u - 4u * L;
+                tb = prefix | (bin << lo);
+            }
+            gthr = tb > gthr ? tb : gthr;
+        }
+    }
+    float gr = -__FLT_MAX__;
+    if (gthr) {
+        const float m = lower_bound_margin(key_f32(gthr));
+        gr = m > -__FLT_MAX__ ? m : -__FLT_MAX__;
+    }
+
+    // ---- 4. slots f < lim hold a candidate or the padding; a chunk with more
+    //         than `pre` candidates sends every candidate of the row through
+    //         LDS in chunk order
+    uint32_t lim = (uint32_t)S << P.lp;
+    if (spill) {
+        lim = SAMPLE_FIN_CAP;
+        const uint32_t cn = (int)t < S ? sh.wcnt[wave][t] : 0u;
         const uint32_t inc = wave_incl_scan_u32(cn);
         const uint32_t off = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
-        if ((int)t < S) sh.ccount[t] = off;           // own slot: read before by this thread only
+        if ((int)t < S) sh.coff[t] = off;
         __syncthreads();
         for (int ch = (int)wave; ch < S; ch += LLIMA_WAVES) {
-            const uint32_t o = sh.ccount[ch];
-            const uint32_t m = hdr[ch].count;
-            const uint64_t* src = crow + (size_t)ch * P.share;
+            const uint32_t o = sh.coff[ch];
+            const uint32_t m = sh.wcnt[wave][ch];
+            const uint64_t* src = crow + ((size_t)ch << P.ls);
             for (uint32_t i = lane; i < m; i += 64) sh.u.cbuf[o + i] = src[i];
         }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < SAMPLE_SLOTS; ++j) {
             const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-            if (f < n) { q[j] = sh.u.cbuf[f]; valid |= 1u << j; }
+            q[j] = f < n ? sh.u.cbuf[f] : SAMPLE_SENTINEL;
         }
     }
 
-    // ---- 4. keys of x / T; candidates below the largest chunk bound cannot be
-    //         in the top-k set (that chunk alone has k values at or above it)
-    const uint32_t kb = (fl & HDR_FILTERED) ? f32_key(key_f32(bound) / c.T) : 0u;
+    // ---- 5. candidates at or above the bound, staged per wave
+    uint32_t o = 0;
+#pragma unroll
+    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        const bool pass = t + (uint32_t)j * LLIMA_WG < lim &&
+                          __uint_as_float((uint32_t)(q[j] >> 32)) >= gr;
+        const uint64_t m = ballot(pass);
+        if (m) {
+            const uint32_t s2 = mbcnt_add(m, o);
+            if (pass && s2 < SAMPLE_SMALL) sh.stage[wave][s2] = q[j];
+            o += (uint32_t)__popcll(m);
+        }
+    }
+    if (lane == 0) sh.r32[0][wave] = o;
+    __syncthreads();
+    uint32_t wc[LLIMA_WAVES], nk0 = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) { wc[w] = sh.r32[0][w]; nk0 += wc[w]; }
+
+    if (nk0 <= SAMPLE_SMALL) {
+        // ---- 6a. every wave holds all survivors, one per lane
+        uint32_t key = 0, id = 0;
+        if (lane < nk0) {
+            uint32_t w = 0, idx = lane;
+            while (w < LLIMA_WAVES - 1 && idx >= wc[w]) { idx -= wc[w]; ++w; }
+            const uint64_t qq = sh.stage[w][idx];
+            const uint32_t k = f32_key(__uint_as_float((uint32_t)(qq >> 32)) / c.T);
+            key = k > LLIMA_KEY_NEG_INF ? k : 0u;
+            id = (uint32_t)qq;
+        }
+        const uint32_t nfin = (uint32_t)__popcll(ballot(key != 0));
+        if (nfin == 0) {
+            if (gthr) return false;
+            if (t == 0) write_result(P, row, -1, 0.0f);
+            if (P.out_keep) write_keep(P, row, [&](auto) {});
+            return true;
+        }
+        const uint32_t kmax = wave_max_u32(key);
+        const uint32_t kmin = wave_min_u32(key ? key : 0xFFFFFFFFu);
+        return fin_small(P, row, c, key, id, nk0, nfin, kmin, kmax, gthr, sh);
+    }
+
+    // ---- 6b. many survivors: keys in registers, radix selects
     uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
     uint32_t kmax = 0, nkmin = 0, nkeep = 0;
 #pragma unroll
     for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        const uint32_t k = f32_key(__uint_as_float((uint32_t)(q[j] >> 32)) / c.T);
-        const bool keep = ((valid >> j) & 1u) && k > LLIMA_KEY_NEG_INF && k >= kb;
+        const float x = __uint_as_float((uint32_t)(q[j] >> 32));
+        const uint32_t k = f32_key(x / c.T);
+        const bool keep = t + (uint32_t)j * LLIMA_WG < lim && x >= gr && k > LLIMA_KEY_NEG_INF;
         key[j] = keep ? k : 0u;
         id[j] = (uint32_t)q[j];
         nkeep += keep ? 1u : 0u;
@@ -1005,8 +1152,8 @@ __device__ __forceinline__ bool fin_fast(const SampleParams& P, int row, const R
         nkmin = keep && ~k > nkmin ? ~k : nkmin;
     }
     {
-        const uint32_t a = wave_max_u32(kmax), b = wave_max_u32(nkmin), s = wave_sum_u32(nkeep);
-        if (lane == 0) { sh.r32[4][wave] = a; sh.r32[5][wave] = b; sh.r32[6][wave] = s; }
+        const uint32_t a = wave_max_u32(kmax), b = wave_max_u32(nkmin), s2 = wave_sum_u32(nkeep);
+        if (lane == 0) { sh.r32[4][wave] = a; sh.r32[5][wave] = b; sh.r32[6][wave] = s2; }
         __syncthreads();
         kmax = 0; nkmin = 0; nkeep = 0;
 #pragma unroll
@@ -1016,59 +1163,14 @@ __device__ __forceinline__ bool fin_fast(const SampleParams& P, int row, const R
             nkeep += sh.r32[6][w];
         }
     }
+    if (nkeep == 0) return false;                    // cannot happen with nk0 > 64 finite
     const uint32_t kmin = ~nkmin;
-    if (nkeep == 0) {
-        // every candidate is -inf (or there are none): nothing is admissible
-        if (fl & HDR_FILTERED) return false;
-        if (t == 0) write_result(P, row, -1, 0.0f);
-        if (P.out_keep) write_keep(P, row, [&](auto) {});
-        return true;
-    }
-
-    // ---- 5. top-k threshold, then the proof that the sweep kept every member:
-    //         a value below a chunk's lowered bound g has x <= fl(g / T) < tau
     int buf = 0;
     uint32_t tau = kmin;
     if (c.k > 0 && (uint32_t)c.k < nkeep) tau = fin_kth_desc(key, (uint32_t)c.k, kmin, kmax, sh, buf);
-    else if (c.k > 0 && (uint32_t)c.k > nkeep && (fl & HDR_FILTERED)) return false;
-    if (fl & HDR_FILTERED) {
-        const float gq = lower_bound_margin(key_f32(bound)) / c.T;
-        if (!(gq < key_f32(tau))) return false;
-    }
-
-    // ---- 6. survivors: one per lane when few
-    uint64_t sm[SAMPLE_SLOTS];
-    uint32_t wn = 0;
-#pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        sm[j] = ballot(key[j] >= tau);
-        wn += (uint32_t)__popcll(sm[j]);
-    }
-    if (lane == 0) sh.r32[7][wave] = wn;
-    __syncthreads();
-    uint32_t nk = 0, o = 0;
-#pragma unroll
-    for (int w = 0; w < LLIMA_WAVES; ++w) {
-        o += (uint32_t)w < wave ? sh.r32[7][w] : 0u;
-        nk += sh.r32[7][w];
-    }
-    if (nk > SAMPLE_SMALL) {
-        fin_large(P, row, c, key, id, tau, kmax, sh, buf);
-        return true;
-    }
-#pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        if (sm[j]) {
-            if (key[j] >= tau) {
-                const uint32_t s = o + mbcnt(sm[j]);
-                sh.skey[s] = key[j];
-                sh.sid[s] = id[j];
-            }
-            o += (uint32_t)__popcll(sm[j]);
-        }
-    }
-    __syncthreads();
-    fin_small(P, row, c, nk, kmax, sh);
+    else if (c.k > 0 && (uint32_t)c.k > nkeep && gthr) return false;
+    if (gthr && !(lower_bound_margin(key_f32(gthr)) / c.T < key_f32(tau))) return false;
+    fin_large(P, row, c, key, id, tau, kmax, sh, buf);
     return true;
 }
 
@@ -1087,8 +1189,13 @@ static int max_chunks(int V) { return (V + SAMPLE_MIN_CHUNK - 1) / SAMPLE_MIN_CH
 template <typename TL, int E>
 static void launch_sweep(const SampleParams& P, hipStream_t st) {
     const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
-    if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true>), g, b, 0, st, P);
-    else hipLaunchKernelGGL((sample_sweep<TL, E, false>), g, b, 0, st, P);
+    if (P.bitmask) {
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true, true>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, E, false, true>), g, b, 0, st, P);
+    } else {
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true, false>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, E, false, false>), g, b, 0, st, P);
+    }
 }
 
 }  // namespace llima
@@ -1144,10 +1251,11 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     // 16 KB of logits per workgroup: 4096 fp32 or 8192 bf16 values.
     const int chunk = dtype == LLIMA_F32 ? 4096 : 8192;
     P.S = (V + chunk - 1) / chunk;
-    P.share = SAMPLE_ROW_CAND / P.S;
-    P.pre = SAMPLE_FIN_CAP / P.S < P.share ? SAMPLE_FIN_CAP / P.S : P.share;
-    if (P.pre < 1) P.pre = 1;
-    P.pre_magic = P.pre > 1 ? (uint32_t)(0xFFFFFFFFull / (uint64_t)P.pre + 1ull) : 0xFFFFFFFFu;
+    // powers of two: share = slots per chunk, pre = slots per chunk the finish
+    // reads up front (S * pre <= 4096 = one slot per finishing thread x 16)
+    auto floor_log2 = [](int x) { int l = 0; while ((2 << l) <= x) ++l; return l; };
+    P.ls = floor_log2(SAMPLE_ROW_CAND / P.S);
+    P.lp = floor_log2(SAMPLE_FIN_CAP / P.S);
     P.hdr = (ChunkHdr*)workspace;
     P.cand = (uint64_t*)((char*)workspace + al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)));
     hipStream_t st = (hipStream_t)stream;
