@@ -101,7 +101,7 @@ def main():
         rows = B
         unit_rows = "sequences/s"
         dtype = "f32"
-        kernel_names = ["vr_rowmax", "vr_rowsum", "vr_draw"]
+        kernel_names = ["vr_rowmax", "vr_rowsum", "vr_drawsum", "vr_final"]
         config = {"workload": "speculative", "B": B, "draft_len": D, "V": V}
     else:
         lg = w["logits"]
@@ -150,7 +150,7 @@ def main():
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16" if is_bf16 else "f32"
-        kernel_names = ["sample_kernel"]
+        kernel_names = ["sample_sweep", "sample_finish"]
         config = {"workload": name, "B": B, "V": V, "history": H,
                   "logits_dtype": "bf16" if is_bf16 else "fp32"}
         config.update({k: v for k, v in cfgd.items()})
