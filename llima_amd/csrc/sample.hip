@@ -1,33 +1,41 @@
 // sample.hip -- fused penalty / temperature / mask / top-k / top-p / min-p /
 // inverse-CDF sampling over [B, V] logits rows on MI355X (gfx950).
 //
-// Two launches per step, with no atomics or fences between workgroups (on
-// this part, device-scope cache maintenance and same-address atomics cost far
-// more than the whole sweep):
+// Two launches per step, with no atomics or fences between workgroups (a
+// device-scope release costs an L2 write-back per workgroup on this part, and
+// same-address atomics from thousands of workgroups serialise):
 //
-// sample_sweep: B x S workgroups; workgroup (row, chunk) streams a 16 KB chunk
-//   of its row with 16-byte loads, all issued before anything waits, and keeps
-//   it in registers.  It counts the row's history ids that fall in the chunk in
-//   an LDS table (packed u16), then computes every value in registers: masked
-//   (packed-uint32 grammar bitmask, LSB first), NaN and out-of-row values become
-//   -inf and history values take the repetition / frequency / presence
-//   penalties.  A lower bound g of the chunk's k-th largest value comes from the
-//   lane maxima (a ballot search per wave for the ceil(k/4)-th largest, min over
-//   the 4 waves), and every value >= g - |g| 2^-20 is written, with its id, to
-//   the chunk's own workspace slot at offsets taken from ballots (no atomics),
-//   together with a small header.  The LDS footprint (8 KB for fp32) lets all
-//   workgroups of a B=64, V=128256 step be resident at once.
+// sample_sweep: B x S workgroups; workgroup (row, chunk) owns 16 KB of one row
+//   (4096 fp32 or 8192 bf16 values).  At 5 TB/s an fp32 value arrives every
+//   ~0.8 ps, which leaves a few VALU operations per value: the sweep does one
+//   max per value (the lane maxima), picks the chunk bound g from them with a
+//   per-wave ballot search, and tests values against g only in the few lanes
+//   whose maximum reaches it.  Values >= g are written, with their ids and in
+//   id order, to the chunk's own workspace region behind a 16-byte header:
+//     top-k rows    g = the r-th largest of the 256 lane maxima (r ~ 16), a
+//                   lower bound of the chunk's r-th largest value;
+//     other rows    g = chunk max - 27 T when values of zero weight cannot
+//                   matter, else every finite value;
+//     greedy rows   only the chunk's (maximum, first index) in the header.
+//   Penalties: when they can only lower a value (repetition >= 1, presence
+//   and frequency >= 0) on top-k rows, the sweep selects on the raw values
+//   (a penalised value never exceeds its raw value, so the bound argument
+//   holds) and the finish penalises the candidates only.  Otherwise the sweep
+//   builds the chunk's history counts in LDS, with the history ids loaded
+//   ahead of the chunk so that they are counted while it is in flight, and
+//   penalises in registers.
 //
-// sample_finish: one workgroup per row loads the headers and the candidates
-//   straight into registers (16 slots per thread), divides them by the
-//   temperature, drops those below the largest chunk bound, proves that no
-//   member of the top-k set can be missing (else falls back), and selects with
-//   LDS radix histograms whose scans use DPP: the top-k threshold (count), then,
-//   for up to 64 survivors, top-p / min-p / the draw by pairwise sums spread
-//   over the 4 waves, or otherwise the top-p threshold (fixed-point mass) and
-//   the draw (mass by ascending id).  Rows that the candidates cannot serve
-//   (overflow, top-k disabled without a mask, degenerate temperatures) are
-//   finished by the same workgroup with a full-row multi-pass version.
+// sample_finish: one workgroup per row.  One round of 16-byte loads covers the
+//   header and the first slots of every chunk region; the candidates are
+//   gathered into LDS in id order and spread over the threads (4 or 16 per
+//   thread).  Lazy penalties count the row's history ids against an LDS hash
+//   of the candidate ids.  After division by T, histogram rounds narrow the
+//   top-k boundary until at most 64 values remain above it; those are ranked
+//   pairwise (exact tau, top-p mass, min-p, the draw) split over the 4 waves.
+//   The result stands only if the bounds provably lost nothing: tau must
+//   exceed every chunk's fl(g / T), or, without top-k, every skipped value
+//   must have weight 0.  Otherwise an exact multi-pass scan of the whole row
+//   finishes it.
 //
 // The sampling semantics have no counterpart in the reference runtime, which
 // only ever takes the argmax (sima_lmm/devkit/cpp/utils.hpp:80-152,
@@ -38,30 +46,26 @@
 
 namespace llima {
 
-#define SAMPLE_SLOTS 16                            // candidates per finishing thread
-#define SAMPLE_FIN_CAP (SAMPLE_SLOTS * LLIMA_WG)   // 4096
-#define SAMPLE_ROW_CAND 16384                      // candidate slots per row (all chunks)
-#define SAMPLE_MIN_CHUNK 4096                      // smallest chunk (fp32: 256 threads x 16)
-#define SAMPLE_SEG 8192                            // full-row path segment
-#define SAMPLE_HBATCH 8                            // history ids per thread loaded up front
-#define SAMPLE_K_BOUND 256                         // largest top-k the sweep bounds
-#define SAMPLE_BOUND_LOWBIT 12                     // key bits below this are not searched
-#define SAMPLE_SMALL 64                            // survivors handled one per lane
+#define SMP_REGION 512                             // u64 slots per chunk region (4 KB)
+#define SMP_HDR 1                                  // header slots at the start of a region
+#define SMP_CAP (SMP_REGION - SMP_HDR)             // candidates a chunk can hand over
+#define SMP_FIN_CAP 4096                           // candidates per row the finish holds
+#define SMP_MAX_S 256                              // chunks per row the finish can gather
+#define SMP_HBATCH 8                               // history ids per thread loaded up front
+#define SMP_BOUND_LOWBIT 12                        // key bits below this are not searched
+#define SMP_SMALL 64                               // survivors handled one per lane
+#define SMP_SEG 8192                               // full-row path segment
+#define SMP_HASH 4096                              // lazy-penalty hash slots
 
-#define HDR_OVERFLOW 1u
-#define HDR_FILTERED 2u
+#define HF_OVERFLOW 1u
 
-// Written by every sweep workgroup (no state survives a call).
-struct ChunkHdr {
-    uint32_t count;      // candidates in this chunk's slot
-    uint32_t flags;      // HDR_*
-    uint32_t bound;      // key of the chunk bound (when FILTERED)
-    uint32_t pad;
-    uint32_t w[8];       // sampling rows: keys of the two largest lane maxima of
-                         // each wave (0: none); greedy rows: w[1]:w[0] =
-                         // (key << 32 | ~index) of the chunk maximum
-};
-
+// Chunk region: slot 0 is the header, low 32 bits: candidates written |
+// flags << 16; high 32 bits: the bound g (float bits): every finite value >= g
+// was written (-inf: all).  Candidates follow from slot 1 as (value bits << 32
+// | id) in id order; the slots the finish reads in its first round (pre_slots)
+// that hold no candidate carry SMP_SENTINEL.  Greedy rows: slot 1 holds
+// (key << 32 | ~index) of the chunk maximum.
+#define SMP_SENTINEL (0xFF800000ull << 32)         // value -inf: never a candidate
 struct SampleParams {
     const void* logits;
     int64_t row_stride;
@@ -73,45 +77,64 @@ struct SampleParams {
     int32_t* out_ids;
     float* out_probs;
     uint32_t* out_keep;
-    ChunkHdr* hdr;       // [B][S]
-    uint64_t* cand;      // [B][S][share]  (value bits << 32 | id)
-    int32_t B, V, H_max, S, share;
+    uint64_t* ws;        // [B][S][SMP_REGION]
+    int32_t B, V, H_max, S;
+    int32_t lgs;         // log2 of S rounded up to a power of two (finish gather)
     int32_t vec_ok;
-    int32_t lp, ls;      // log2 of pre (candidate slots per chunk the finish loads
-                         // up front) and of share (slots per chunk)
+    int32_t lazy;        // penalties are applied by the finish (see llima_sample)
 };
-
-// Pads a chunk's first `pre` candidate slots behind its candidates: value -inf,
-// which no bound admits.
-#define SAMPLE_SENTINEL (0xFF800000ull << 32)
 
 struct RowCfg {
     float T, p, m, R, alpha, beta;
-    int32_t k;
+    int32_t k;           // 0: top-k disabled
     bool greedy, pen;
     int32_t hlen;
 };
 
+// The per-row value when the array is given, else the broadcast scalar (passed
+// by value: selecting between a pointer into the kernel arguments and one
+// into global memory would force the arguments into private memory).
+template <typename T>
+__device__ __forceinline__ T row_or(const T* rows, T scalar, int row) {
+    return rows ? __builtin_nontemporal_load(rows + row) : scalar;
+}
+
 __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
     const llima_sampler_config& c = P.cfg;
     RowCfg r;
-    r.T = c.temperature_rows ? c.temperature_rows[row] : c.temperature;
-    r.k = c.top_k_rows ? c.top_k_rows[row] : c.top_k;
-    r.p = c.top_p_rows ? c.top_p_rows[row] : c.top_p;
-    r.m = c.min_p_rows ? c.min_p_rows[row] : c.min_p;
-    r.R = c.repetition_penalty_rows ? c.repetition_penalty_rows[row] : c.repetition_penalty;
-    r.alpha = c.presence_penalty_rows ? c.presence_penalty_rows[row] : c.presence_penalty;
-    r.beta = c.frequency_penalty_rows ? c.frequency_penalty_rows[row] : c.frequency_penalty;
+    r.T = row_or(c.temperature_rows, c.temperature, row);
+    r.k = row_or(c.top_k_rows, c.top_k, row);
+    r.p = row_or(c.top_p_rows, c.top_p, row);
+    r.m = row_or(c.min_p_rows, c.min_p, row);
+    r.R = row_or(c.repetition_penalty_rows, c.repetition_penalty, row);
+    r.alpha = row_or(c.presence_penalty_rows, c.presence_penalty, row);
+    r.beta = row_or(c.frequency_penalty_rows, c.frequency_penalty, row);
     r.greedy = (c.greedy != 0) || !(r.T > 0.0f);
     int h = 0;
     if (P.H_max > 0) {
-        h = P.hist_len ? P.hist_len[row] : P.H_max;
+        h = row_or(P.hist_len, (int32_t)P.H_max, row);
         h = h < 0 ? 0 : (h > P.H_max ? P.H_max : h);
     }
     r.hlen = h;
     r.pen = h > 0 && (r.R != 1.0f || r.alpha != 0.0f || r.beta != 0.0f);
-    if (!(r.k > 0 && r.k < P.V)) r.k = 0;             // disabled
+    if (!(r.k > 0 && r.k < P.V)) r.k = 0;
     return r;
+}
+
+// Values of weight 0 can be left out of the candidates when they cannot be in
+// the reported kept set: top-p drops them (all positive mass lies above them),
+// min-p with a positive threshold drops them, and without a kept-set output
+// they never affect the draw.
+__device__ __forceinline__ bool zero_weight_irrelevant(const SampleParams& P, const RowCfg& c) {
+    return P.out_keep == nullptr || c.p < 1.0f || (c.m > 0.0f && frac32(c.m) > 0);
+}
+
+// Lane maxima ranked for the top-k chunk bound: enough that a chunk rarely
+// holds more of the row's top-k values than this.
+__device__ __forceinline__ uint32_t bound_rank(int k, int S) {
+    int r = (4 * k + S - 1) / S + 8;
+    r = r < 16 ? 16 : (r > 64 ? 64 : r);
+    return (uint32_t)(k < r ? k : r);
 }
 
 // HF RepetitionPenalty (score < 0 ? score * p : score / p), then OpenAI
@@ -119,12 +142,6 @@ __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
 __device__ __forceinline__ float penalize(float l, uint32_t c, const RowCfg& cfg) {
     l = (l < 0.0f) ? l * cfg.R : l / cfg.R;
     return (l - cfg.beta * (float)c) - cfg.alpha;
-}
-
-// The pre-filter bound lowered by a relative 2^-20, so that no value whose
-// quotient by T can round onto the bound's quotient is filtered out.
-__device__ __forceinline__ float lower_bound_margin(float t) {
-    return t - __builtin_fabsf(t) * 0x1p-20f;
 }
 
 __device__ __forceinline__ uint32_t table_count(const uint32_t* table, uint32_t off) {
@@ -140,41 +157,34 @@ __device__ __forceinline__ float load_one<uint16_t>(const uint16_t* rowp, int i)
     return bf16_bits_to_f32(rowp[i]);
 }
 
-// Counts the row's history ids in [lo, hi) into an LDS table of packed u16
-// counts (full-row path).
-__device__ __forceinline__ void count_history(const SampleParams& P, int row, int hlen, int lo,
-                                              int hi, uint32_t* table, int nwords) {
-    for (int i = threadIdx.x; i < nwords; i += LLIMA_WG) table[i] = 0;
-    __syncthreads();
-    const int32_t* h = P.hist + (size_t)row * P.H_max;
-    for (int j = threadIdx.x; j < hlen; j += LLIMA_WG) {
-        const int32_t id = h[j];
-        if (id >= lo && id < hi) {
-            const uint32_t off = (uint32_t)(id - lo);
-            atomicAdd(&table[off >> 1], 1u << ((off & 1u) * 16u));
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ uint64_t* region_of(const SampleParams& P, uint32_t row, uint32_t chunk) {
+    return P.ws + ((size_t)row * (uint32_t)P.S + chunk) * SMP_REGION;
+}
+
+// Slots of every region the finish reads in its first round: 8 per thread,
+// 256 >> lgs threads per chunk.
+__device__ __forceinline__ uint32_t pre_slots(const SampleParams& P) {
+    const uint32_t n = (uint32_t)(LLIMA_WG >> P.lgs) * 8u;
+    return n < SMP_REGION ? n : SMP_REGION;
 }
 
 // ================================================================== sweep
 // VEC: rows are 16-byte aligned and V is a multiple of the values per load, so
 // every chunk (also a row's partial last one) is read with 16-byte loads from
 // clamped, always-valid addresses and the out-of-row values masked in registers.
-template <bool B>
-struct Flag { static constexpr bool value = B; };
-
-// MASK: a grammar bitmask is given.  NaN values are never turned into -inf
-// here: every later use is an ordered comparison (x > best, x > lane max,
-// x >= bound), which a NaN fails, so a NaN is never selected.
-template <typename TL, int E, bool VEC, bool MASK>
+// MASK: a grammar bitmask is given.  NaN values stay NaN here: every later use
+// is an ordered comparison or a max that ignores NaN, so a NaN is never selected.
+template <typename TL, bool VEC, bool MASK>
 __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
-    constexpr int NL = E / EPL;                // loads per thread
+    constexpr int NL = 4;                      // 16-byte loads per thread
+    constexpr int E = NL * EPL;                // values per thread
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr int CW = CHUNK / 2;              // history count words
     __shared__ __align__(16) uint32_t cnt[CW];
-    __shared__ uint32_t xw[4][LLIMA_WAVES];
+    __shared__ uint32_t xa[LLIMA_WAVES];
+    __shared__ uint32_t xs[66];                    // staged lane maxima: count, keys, result
+    __shared__ uint32_t xc[NL][LLIMA_WAVES];
     __shared__ uint64_t xg[LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
@@ -187,20 +197,22 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     const int V = P.V;
     const int c0 = (int)chunk * CHUNK;
     const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
-    const int H = P.H_max;
-    const int32_t* hrow = P.hist + (size_t)row * H;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
+    const int H = P.H_max;
+    const bool eager = H > 0 && !P.lazy;
 
-    // ---- 1. every load, issued before anything waits and in the order the
-    //         data is consumed: history ids, mask words, the chunk.  Only
-    //         kernel arguments decide them (the row's configuration is still
-    //         in flight); every address is valid.
-    int32_t hid[SAMPLE_HBATCH];
+    // ---- 1. loads, in the order their data is used, all before the first
+    //         wait: history ids (rows penalised here), mask words, the chunk
+    int32_t hid[SMP_HBATCH];
+    if (eager) {
+        const int32_t* hrow = P.hist + (size_t)row * H;
 #pragma unroll
-    for (int b = 0; b < SAMPLE_HBATCH; ++b) {
-        const int j = t + b * LLIMA_WG;
-        hid[b] = (b * LLIMA_WG < H) ? hrow[j < H ? j : H - 1] : -1;
+        for (int b = 0; b < SMP_HBATCH; ++b) {
+            const int j = t + b * LLIMA_WG;
+            hid[b] = hrow[j < H ? j : H - 1];
+        }
     }
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t mword[NL];
     if constexpr (MASK) {
 #pragma unroll
@@ -228,21 +240,25 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     const RowCfg c = load_cfg(P, row);
+    const bool pen_here = eager && c.pen;
 
-    // ---- 2. history counts of the chunk
-    if (c.pen) {
+    // ---- 2. history counts of the chunk (waits for the history ids only)
+    if (pen_here) {
+#pragma unroll
         for (int i = t; i < CW / 4; i += LLIMA_WG) ((llima_u32x4*)cnt)[i] = llima_u32x4{0, 0, 0, 0};
         __syncthreads();
 #pragma unroll
-        for (int b = 0; b < SAMPLE_HBATCH; ++b) {
+        for (int b = 0; b < SMP_HBATCH; ++b) {
             const int32_t id = hid[b];
             if (t + b * LLIMA_WG < c.hlen && id >= c0 && id < c1) {
                 const uint32_t off = (uint32_t)(id - c0);
                 atomicAdd(&cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
         }
-        for (int j = t + SAMPLE_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
+        const int32_t* hrow = P.hist + (size_t)row * H;
+        for (int j = t + SMP_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
             const int32_t id = hrow[j];
             if (id >= c0 && id < c1) {
                 const uint32_t off = (uint32_t)(id - c0);
@@ -252,56 +268,52 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         __syncthreads();
     }
 
-    // ---- 3. values: masked and out-of-row -> -inf, history values penalised
+    // ---- 3. values: masked -> -inf, history values penalised (here), values
+    //         past the row -> -inf (the last chunk only)
     float v[E];
-    auto convert = [&](auto pen_tag) {
-        constexpr bool PEN = decltype(pen_tag)::value;
 #pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-            float xs[EPL];
-            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-            if constexpr (sizeof(TL) == 4) {
+    for (int j = 0; j < NL; ++j) {
+        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+        float xs[EPL];
+        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+        if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
-            } else {
+            for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
+        } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    xs[2 * e] = __uint_as_float(w4[e] << 16);
-                    xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-                }
+            for (int e = 0; e < 4; ++e) {
+                xs[2 * e] = __uint_as_float(w4[e] << 16);
+                xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
             }
-            if constexpr (MASK) {
-                const uint32_t mb = mword[j] >> (i0 & 31);
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) xs[e] = ((mb >> e) & 1u) ? xs[e] : NEG_INF;
-            }
-            if constexpr (PEN) {
-                uint32_t cw[EPL / 2];
-                const uint32_t* cp = cnt + ((i0 - c0) >> 1);
-                if constexpr (EPL == 4) {
-                    const uint2 w2 = *(const uint2*)cp;
-                    cw[0] = w2.x; cw[1] = w2.y;
-                } else {
-                    const llima_u32x4 wq = *(const llima_u32x4*)cp;
-                    cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
-                }
-#pragma unroll
-                for (int h = 0; h < EPL / 2; ++h) {
-                    if (cw[h]) {
-                        const uint32_t lo = cw[h] & 0xFFFFu, hi = cw[h] >> 16;
-                        if (lo) xs[2 * h] = penalize(xs[2 * h], lo, c);
-                        if (hi) xs[2 * h + 1] = penalize(xs[2 * h + 1], hi, c);
-                    }
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) v[j * EPL + e] = xs[e];
         }
-    };
-    if (c.pen) convert(Flag<true>{});
-    else convert(Flag<false>{});
-    if (c1 - c0 < CHUNK) {                         // the row's last, partial chunk
+        if constexpr (MASK) {
+            const uint32_t mb = mword[j] >> (i0 & 31);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) xs[e] = ((mb >> e) & 1u) ? xs[e] : NEG_INF;
+        }
+        if (pen_here) {
+            uint32_t cw[EPL / 2];
+            const uint32_t* cp = cnt + ((i0 - c0) >> 1);
+            if constexpr (EPL == 4) {
+                const uint2 w2 = *(const uint2*)cp;
+                cw[0] = w2.x; cw[1] = w2.y;
+            } else {
+                const llima_u32x4 wq = *(const llima_u32x4*)cp;
+                cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
+            }
+#pragma unroll
+            for (int h = 0; h < EPL / 2; ++h) {
+                if (cw[h]) {
+                    const uint32_t lo = cw[h] & 0xFFFFu, hi = cw[h] >> 16;
+                    if (lo) xs[2 * h] = penalize(xs[2 * h], lo, c);
+                    if (hi) xs[2 * h + 1] = penalize(xs[2 * h + 1], hi, c);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[j * EPL + e] = xs[e];
+    }
+    if (c1 - c0 < CHUNK) {
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
             const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
@@ -311,11 +323,11 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         }
     }
 
-    ChunkHdr* hdr = P.hdr + (size_t)row * P.S + chunk;
+    uint64_t* reg = region_of(P, row, chunk);
     if (c.greedy) {
         // ---- argmax: first index of the maximum (values visited in index order)
         float best = NEG_INF;
-        uint32_t bidx = 0xFFFFFFFFu;
+        uint32_t bidx = 0;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
             const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
@@ -323,119 +335,174 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             for (int e = 0; e < EPL; ++e)
                 if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
         }
-        const uint32_t kb = best > NEG_INF ? f32_key(best) : 0u;
-        const uint32_t wk = wave_max_u32(kb);
-        const uint32_t wi = wave_max_u32((wk != 0 && kb == wk) ? ~bidx : 0u);
-        if (lane == 0) xg[wave] = wk ? (((uint64_t)wk << 32) | wi) : 0ull;
+        const uint64_t kk = best > NEG_INF ? (((uint64_t)f32_key(best) << 32) | (uint32_t)~bidx) : 0ull;
+        const uint64_t wk = wave_max_u64(kk);
+        if (lane == 0) xg[wave] = wk;
         __syncthreads();
         if (t == 0) {
             uint64_t g = 0;
 #pragma unroll
             for (int w = 0; w < LLIMA_WAVES; ++w) g = xg[w] > g ? xg[w] : g;
-            *(llima_u32x4*)hdr = llima_u32x4{0u, 0u, 0u, 0u};
-            *(llima_u32x4*)hdr->w = llima_u32x4{(uint32_t)g, (uint32_t)(g >> 32), 0u, 0u};
-            *(llima_u32x4*)(hdr->w + 4) = llima_u32x4{0u, 0u, 0u, 0u};
+            *(llima_u32x4*)reg = llima_u32x4{0u, __float_as_uint(NEG_INF), (uint32_t)g,
+                                             (uint32_t)(g >> 32)};
         }
         return;
     }
 
-    // ---- 4. chunk bound: every wave has >= r = ceil(k/4) lanes whose maximum
-    //         is >= its bound, so the chunk has >= 4r >= k values >= their min
-    uint32_t gkey = 0;
-    if (c.k > 0 && c.k <= SAMPLE_K_BOUND) {
-        float lm = NEG_INF;
+    // ---- 4. lane maxima (a NaN is ignored by the max) and the chunk bound g
+    float lm = v[0];
 #pragma unroll
-        for (int e = 0; e < E; ++e) lm = v[e] > lm ? v[e] : lm;
-        const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
-        const uint32_t r = ((uint32_t)c.k + 3u) >> 2;
-        const uint32_t tw = wave_rth_largest(lk, r, SAMPLE_BOUND_LOWBIT);
-        const uint32_t wm = wave_max_u32(lk);
-        const uint32_t wm2 = wave_max_u32(lk < wm ? lk : 0u);   // a lane other than the maximum's
-        if (lane == 0) { xw[0][wave] = tw; xw[2][wave] = wm; xw[3][wave] = wm2; }
+    for (int e = 1; e < E; ++e) lm = __builtin_fmaxf(lm, v[e]);
+    const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
+    float g = NEG_INF;
+    if (c.k > 0) {
+        // r lanes of one wave hold maxima >= that wave's r-th largest lane
+        // maximum (low key bits cleared: a lower value), so the chunk's r-th
+        // largest value is at least the largest of the four.
+        // Then the lane maxima at or above that (they include the chunk's r
+        // largest) are staged in LDS and, when at most 64, one wave finds the
+        // chunk's r-th largest lane maximum itself: about r values pass it.
+        const uint32_t r = bound_rank(c.k, P.S);
+        const uint32_t bw = wave_rth_largest(lk, r, SMP_BOUND_LOWBIT);
+        if (lane == 0) xa[wave] = bw;
+        if (t == 0) xs[0] = 0;
         __syncthreads();
-        gkey = xw[0][0];
+        uint32_t gk = 0;
 #pragma unroll
-        for (int w = 1; w < LLIMA_WAVES; ++w) gkey = xw[0][w] < gkey ? xw[0][w] : gkey;
+        for (int w = 0; w < LLIMA_WAVES; ++w) gk = xa[w] > gk ? xa[w] : gk;
+        if (gk) {
+            if (lk >= gk) {
+                const uint32_t o = atomicAdd(&xs[0], 1u);
+                if (o < 64u) xs[1 + o] = lk;
+            }
+            __syncthreads();
+            const uint32_t ns = xs[0];
+            if (ns <= 64u) {
+                if (wave == 0) {
+                    const uint32_t key = lane < ns ? xs[1 + lane] : 0u;
+                    const uint32_t g2k = wave_rth_largest(key, r, SMP_BOUND_LOWBIT);
+                    if (lane == 0) xs[65] = g2k;
+                }
+                __syncthreads();
+                const uint32_t g2k = xs[65];
+                gk = g2k > gk ? g2k : gk;
+            }
+            g = key_f32(gk);
+        }
+    } else if (zero_weight_irrelevant(P, c)) {
+        // values this far below the chunk maximum have weight 0 (checked exactly
+        // by the finish against the row maximum)
+        const uint32_t wm = wave_max_u32(lk);
+        if (lane == 0) xa[wave] = wm;
+        __syncthreads();
+        uint32_t mk = 0;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) mk = xa[w] > mk ? xa[w] : mk;
+        if (mk) {
+            const float gm = key_f32(mk) - 27.0f * c.T;
+            g = gm == gm ? gm : NEG_INF;
+        }
     }
-    float g = -__FLT_MAX__;                       // keeps every finite value
-    if (gkey) {
-        const float m = lower_bound_margin(key_f32(gkey));
-        g = m > -__FLT_MAX__ ? m : -__FLT_MAX__;
-    }
+    // the smallest finite float stands for -inf: -inf and NaN never pass
+    const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
 
-    // ---- 5. write the values >= g: count per wave, then ballot offsets
-    uint32_t wcount = 0;
+    // ---- 5. write the values >= g in id order: per load j, lane counts, wave
+    //         scans (two counts packed per u32), then the waves in order.  Only
+    //         lanes whose maximum reaches g test their values.
+    uint32_t pm[NL];
 #pragma unroll
-    for (int e = 0; e < E; ++e) wcount += (uint32_t)__popcll(ballot(v[e] >= g));
-    if (lane == 0) xw[1][wave] = wcount;
-    __syncthreads();
-    uint32_t base = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < LLIMA_WAVES; ++w) {
-        const uint32_t n = xw[1][w];
-        base += (uint32_t)w < wave ? n : 0u;
-        total += n;
-    }
-    const uint32_t cap = 1u << P.ls;
-    if (total <= cap) {
-        uint64_t* dst = P.cand + (((size_t)row * P.S + chunk) << P.ls);
-        uint32_t o = base;
+    for (int j = 0; j < NL; ++j) pm[j] = 0;
+    if (lm >= g2) {
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+            uint32_t m = 0;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float x = v[j * EPL + e];
-                const bool pr = x >= g;
-                const uint64_t m = ballot(pr);
-                if (m) {
-                    if (pr) dst[mbcnt_add(m, o)] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(i0 + e);
-                    o += (uint32_t)__popcll(m);
+            for (int e = 0; e < EPL; ++e) m |= v[j * EPL + e] >= g2 ? (1u << e) : 0u;
+            pm[j] = m;
+        }
+    }
+    const uint32_t a01 = (uint32_t)__popc(pm[0]) | ((uint32_t)__popc(pm[1]) << 16);
+    const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
+    const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
+    const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
+    if (lane == 0) {
+        xc[0][wave] = t01 & 0xFFFFu; xc[1][wave] = t01 >> 16;
+        xc[2][wave] = t23 & 0xFFFFu; xc[3][wave] = t23 >> 16;
+    }
+    __syncthreads();
+    uint32_t base[NL], total = 0;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        uint32_t before = 0;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            const uint32_t n = xc[j][w];
+            before += (uint32_t)w < wave ? n : 0u;
+        }
+        base[j] = total + before;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) total += xc[j][w];
+    }
+    const bool fits = total <= SMP_CAP;
+    if (fits && lm >= g2) {
+        const uint32_t e01 = i01 - a01, e23 = i23 - a23;
+        const uint32_t lx[NL] = {e01 & 0xFFFFu, e01 >> 16, e23 & 0xFFFFu, e23 >> 16};
+        uint64_t* dst = reg + SMP_HDR;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            if (pm[j]) {
+                const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+                uint32_t o = base[j] + lx[j];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    if ((pm[j] >> e) & 1u) {
+                        dst[o] = ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
+                        ++o;
+                    }
                 }
             }
         }
-        for (uint32_t i = total + (uint32_t)t; i < (1u << P.lp); i += LLIMA_WG) dst[i] = SAMPLE_SENTINEL;
     }
-    if (t == 0) {
-        *(llima_u32x4*)hdr = llima_u32x4{total <= cap ? total : 0u,
-                                         (total > cap ? HDR_OVERFLOW : 0u) | (gkey ? HDR_FILTERED : 0u),
-                                         gkey, 0u};
-        *(llima_u32x4*)hdr->w = gkey ? llima_u32x4{xw[2][0], xw[2][1], xw[2][2], xw[2][3]}
-                                     : llima_u32x4{0u, 0u, 0u, 0u};
-        *(llima_u32x4*)(hdr->w + 4) = gkey ? llima_u32x4{xw[3][0], xw[3][1], xw[3][2], xw[3][3]}
-                                           : llima_u32x4{0u, 0u, 0u, 0u};
+    if (fits) {
+        const uint32_t pre = pre_slots(P);
+        for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
     }
+    if (t == 0)
+        *(uint64_t*)reg = ((uint64_t)__float_as_uint(g) << 32) | (fits ? total : (HF_OVERFLOW << 16));
 }
 
 // ================================================================== finish
-struct FinishShared {
+struct FinShared {
     union {
-        uint64_t cbuf[SAMPLE_FIN_CAP];         // candidates gathered in chunk order
-        uint32_t table[SAMPLE_SEG / 2];        // full-row path history counts
+        uint64_t cand[SMP_FIN_CAP + SMP_FIN_CAP / 16];   // element f at f + f / 16
+        uint32_t table[SMP_SEG / 2];                     // full-row path history counts
+        struct {
+            uint32_t key[SMP_HASH];                      // candidate id + 1, 0 = empty
+            uint32_t cnt[SMP_HASH];                      // history occurrences
+        } hash;
     } u;
-    uint32_t wcnt[LLIMA_WAVES][LLIMA_WG];      // each wave's own copy of the chunk counts
-    uint32_t coff[LLIMA_WG];                   // chunk offsets (gather path)
-    uint64_t stage[LLIMA_WAVES][SAMPLE_SMALL]; // survivors of the bound, per wave
-    uint32_t hcnt[2][256];                     // radix histograms (double-buffered)
+    uint32_t ccount[SMP_MAX_S];
+    uint32_t coff[SMP_MAX_S];
+    uint32_t hcnt[2][256];
     uint64_t hmass[2][256];
-    uint64_t above[256];
+    llima_u32x4 sv[2 * SMP_SMALL];
+    llima_u32x4 sv2[LLIMA_WAVES][2 * SMP_SMALL];
+    uint32_t pc[2][LLIMA_WAVES][64];
     uint64_t part[2][LLIMA_WAVES][64];
-    llima_u32x4 sv[LLIMA_WAVES][64];           // each wave's copy of the survivors
-    uint32_t bh[LLIMA_WAVES][256];             // each wave's histogram of header values
-    uint32_t pc[LLIMA_WAVES][64];
+    uint64_t part2[2][LLIMA_WAVES][64];
+    uint64_t r64[4][LLIMA_WAVES];
     uint32_t r32[8][LLIMA_WAVES];
-    uint64_t r64[2][LLIMA_WAVES];
-    uint32_t sel[2];
+    uint32_t sel[4];
     uint64_t sel64[2];
+    uint32_t hflags, hgkey, hn;
+    uint64_t hgreedy;
+    uint32_t hk[2 * SMP_SMALL];                      // survivor ids + 1 (lazy penalties)
+    uint32_t hc[2 * SMP_SMALL];                      // their history occurrences
     BlockScratch bs;
 };
 
-// ------------------------------------------------------------------ radix selects
-// Each select runs over register-resident elements (SAMPLE_SLOTS per thread,
-// key 0 = absent).  Digits are 8 bits wide and start at the highest bit in
-// which the keys differ (the bits above it are common to all of them).
-// hcnt[buf] and hmass[buf] are zero on entry and on return; every round clears
-// the other buffer for the next one, so a round needs three barriers.
+// ------------------------------------------------------------------ radix helpers
+// Digits are 8 bits wide and start at the highest bit in which the keys differ.
 struct Digits {
     uint32_t prefix, pmask;   // fixed high bits of the selected key
     int top;                  // top bit of the next digit (-1: done)
@@ -463,55 +530,23 @@ __device__ __forceinline__ uint64_t wg_prefix_u64(uint64_t inc, uint64_t v, uint
     return before + inc - v;
 }
 
-// k-th largest key (with multiplicity) among the elements, all of whose keys
-// lie in [kmin, kmax].
-__device__ __forceinline__ uint32_t fin_kth_desc(const uint32_t (&key)[SAMPLE_SLOTS], uint32_t k,
-                                                 uint32_t kmin, uint32_t kmax, FinishShared& sh,
-                                                 int& buf) {
-    Digits d = digits_init(kmin, kmax);
-    uint32_t rem = k;
-    const uint32_t t = threadIdx.x;
-    while (d.top >= 0) {
-        const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
-        const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        uint32_t* hc = sh.hcnt[buf];
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j)
-            if (key[j] && (key[j] & d.pmask) == d.prefix) atomicAdd(&hc[(key[j] >> lo) & bmask], 1u);
-        __syncthreads();
-        const uint32_t bin = 255u - t;                 // thread 0 <-> top bin
-        const uint32_t cn = hc[bin];
-        sh.hcnt[buf ^ 1][t] = 0;
-        sh.hmass[buf ^ 1][t] = 0;
-        const uint32_t inc = wave_incl_scan_u32(cn);
-        const uint32_t above = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
-        if (above < rem && above + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = rem - above; }
-        __syncthreads();
-        d.prefix |= sh.sel[0] << lo;
-        d.pmask |= bmask << lo;
-        d.top = lo - 1;
-        rem = sh.sel[1];
-        buf ^= 1;
-    }
-    return d.prefix;
-}
-
-// Top-p boundary: the smallest key theta such that an element with key theta has
-// (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
-__device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[SAMPLE_SLOTS],
-                                                  const uint64_t (&w)[SAMPLE_SLOTS],
-                                                  llima_u128 PZ, uint32_t kmin, uint32_t kmax,
-                                                  FinishShared& sh, int& buf) {
+// Top-p boundary: the smallest key theta such that an element with key theta
+// has (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
+// hcnt / hmass are zero on entry and on return.
+template <int EPT>
+__device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
+                                  llima_u128 PZ, uint32_t kmin, uint32_t kmax, FinShared& sh) {
     Digits d = digits_init(kmin, kmax);
     uint64_t acc = 0;
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
+    int buf = 0;
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
         uint32_t* hc = sh.hcnt[buf];
         uint64_t* hm = sh.hmass[buf];
 #pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+        for (int j = 0; j < EPT; ++j) {
             if (key[j] && (key[j] & d.pmask) == d.prefix) {
                 const uint32_t b = (key[j] >> lo) & bmask;
                 atomicAdd(&hc[b], 1u);
@@ -527,7 +562,6 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[SAMPLE_S
         const uint64_t inc = wave_incl_scan_u64(m);
         const uint64_t above = acc + wg_prefix_u64(inc, m, sh.r64[0]);
         const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
-        sh.above[t] = above;
         const uint64_t bc = ballot(cond), bn = ballot(cn > 0);
         if (lane == 0) {
             sh.r32[1][wave] = bc ? 64u - (uint32_t)__builtin_clzll(bc) : 0u;    // highest lane + 1
@@ -545,50 +579,17 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[SAMPLE_S
                 if (sel_t < 0 && sh.r32[2][w2]) sel_t = w2 * 64 + (int)sh.r32[2][w2] - 1;
         }
         if (sel_t < 0) sel_t = 0;
+        if ((int)t == sel_t) sh.sel64[0] = above;
+        __syncthreads();
         d.prefix |= (255u - (uint32_t)sel_t) << lo;
         d.pmask |= bmask << lo;
         d.top = lo - 1;
-        acc = sh.above[sel_t];
-        buf ^= 1;
-    }
-    return d.prefix;
-}
-
-// Draw: the smallest id whose ascending-id prefix mass exceeds target (< the
-// total mass); also returns that element's weight.  Ids are < V <= 2^24.
-__device__ __forceinline__ uint32_t fin_draw_asc(const uint32_t (&id)[SAMPLE_SLOTS],
-                                                 const uint64_t (&w)[SAMPLE_SLOTS], uint64_t target,
-                                                 uint32_t V, uint64_t* w_out, FinishShared& sh,
-                                                 int& buf) {
-    Digits d = digits_init(0u, V > 1 ? V - 1 : 1u);
-    uint64_t acc = 0;
-    const uint32_t t = threadIdx.x;
-    while (d.top >= 0) {
-        const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
-        const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        uint64_t* hm = sh.hmass[buf];
-#pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j)
-            if (w[j] && (id[j] & d.pmask) == d.prefix)
-                atomicAdd((unsigned long long*)&hm[(id[j] >> lo) & bmask], (unsigned long long)w[j]);
-        __syncthreads();
-        const uint32_t bin = t;
-        const uint64_t m = hm[bin];
-        sh.hcnt[buf ^ 1][t] = 0;
-        sh.hmass[buf ^ 1][t] = 0;
-        const uint64_t inc = wave_incl_scan_u64(m);
-        const uint64_t below = acc + wg_prefix_u64(inc, m, sh.r64[0]);
-        if (m > 0 && below <= target && target < below + m) {
-            sh.sel[0] = bin; sh.sel64[0] = below; sh.sel64[1] = m;
-        }
-        __syncthreads();
-        d.prefix |= sh.sel[0] << lo;
-        d.pmask |= bmask << lo;
-        d.top = lo - 1;
         acc = sh.sel64[0];
-        *w_out = sh.sel64[1];
+        hc[t] = 0;
+        hm[t] = 0;
         buf ^= 1;
     }
+    __syncthreads();
     return d.prefix;
 }
 
@@ -611,23 +612,38 @@ __device__ __forceinline__ void write_keep(const SampleParams& P, int row, Visit
     __syncthreads();
 }
 
+// Counts the row's history ids in [lo, hi) into an LDS table of packed u16
+// counts (full-row path).
+__device__ __forceinline__ void count_history(const SampleParams& P, int row, int hlen, int lo,
+                                              int hi, uint32_t* table, int nwords) {
+    for (int i = threadIdx.x; i < nwords; i += LLIMA_WG) table[i] = 0;
+    __syncthreads();
+    const int32_t* h = P.hist + (size_t)row * P.H_max;
+    for (int j = threadIdx.x; j < hlen; j += LLIMA_WG) {
+        const int32_t id = h[j];
+        if (id >= lo && id < hi) {
+            const uint32_t off = (uint32_t)(id - lo);
+            atomicAdd(&table[off >> 1], 1u << ((off & 1u) * 16u));
+        }
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------------ full-row path
 // Exact multi-pass selection by one workgroup; recomputes x for the whole row on
 // every pass (history table rebuilt per segment).
 template <typename TL>
-__device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, const RowCfg& c,
-                                             FinishShared& sh) {
+__device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, const RowCfg& c, FinShared& sh) {
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
     const int nw = (V + 31) >> 5;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
     uint32_t* table = sh.u.table;
     __syncthreads();
-    // fn(x, id) for every element of the row.
     auto for_each_x = [&](auto fn) {
-        for (int lo = 0; lo < V; lo += SAMPLE_SEG) {
-            const int hi = lo + SAMPLE_SEG < V ? lo + SAMPLE_SEG : V;
-            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SAMPLE_SEG / 2);
+        for (int lo = 0; lo < V; lo += SMP_SEG) {
+            const int hi = lo + SMP_SEG < V ? lo + SMP_SEG : V;
+            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SMP_SEG / 2);
             for (int i = lo + threadIdx.x; i < hi; i += LLIMA_WG) {
                 float l = load_one<TL>(rowp, i);
                 if (l != l) l = -__builtin_inff();
@@ -643,7 +659,6 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     };
     // Radix select over the row: histogram rounds that visit every element.
     auto radix = [&](auto elem, uint32_t kmin, uint32_t kmax, auto pick) {
-        // elem(x, id, fn): calls fn(key, weight) for elements taking part
         Digits d = digits_init(kmin, kmax);
         uint64_t acc = 0;
         uint32_t rem = 0;
@@ -801,104 +816,363 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         });
 }
 
-// ------------------------------------------------------------------ fast path
-// At most 64 candidates left by the bound, one per lane in every wave (lanes
-// >= nk and candidates that are -inf after the temperature hold key 0).  One
-// pairwise pass, split over the 4 waves by the candidate it reads (broadcast
-// LDS reads of the wave's own copy), gives each lane the number of keys above
-// and equal to its own and the mass above it: the top-k threshold is the key
-// of a lane with (above < k <= above + equal), and the top-p test uses the
-// mass above, which for a kept lane only counts kept lanes.  A second pass
-// gives the mass of final ids up to each id for the draw.  False when the
-// bound cannot be proven to keep the top-k set (full-row path).
-__device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const RowCfg& c,
-                                          uint32_t key, uint32_t id, uint32_t nk, uint32_t nfin,
-                                          uint32_t kmin, uint32_t kmax, uint32_t gthr,
-                                          FinishShared& sh) {
+// ------------------------------------------------------------------ small path
+// At most 64 NPL candidates, staged in sv[0, ns) as {key, id, w lo, w hi},
+// that contain every value of the top-k set (all values >= tau, ties
+// included).  Every wave holds all of them (lane l: candidates l and, with
+// NPL = 2, l + 64); pairwise passes split over the 4 waves by the candidate
+// they read (broadcast LDS reads) rank them: tau is the key of the candidate
+// with (above < k <= above + equal), and the top-p test uses the mass strictly
+// above.  The draw is a scan when sv is in id order (id_sorted), else a second
+// pairwise pass (mass of final ids up to each id).  Returns false, before
+// writing anything, when tau does not exceed tcut (a key no value left out of
+// sv can reach).
+template <int NPL>
+__device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const RowCfg& c, uint32_t ns,
+                          uint32_t kmax, uint32_t tcut, llima_u32x4* sv, bool id_sorted,
+                          FinShared& sh) {
+    constexpr uint32_t PER = 16u * NPL;              // candidates each wave reads
     const uint32_t lane = lane_id(), wave = wave_id();
-    const uint64_t w = key ? weight(key_f32(key), key_f32(kmax)) : 0ull;
-    const uint32_t j0 = wave * 16u;
-    sh.sv[wave][lane] = llima_u32x4{key, id, (uint32_t)w, (uint32_t)(w >> 32)};
-    uint32_t gt = 0, eq = 0;
-    uint64_t above = 0;
-    // lanes >= nk hold key 0, weight 0: reading them changes nothing
+    uint32_t key[NPL], id[NPL];
+    uint64_t w[NPL];
 #pragma unroll
-    for (uint32_t jj = 0; jj < 16; ++jj) {
-        const llima_u32x4 o = sh.sv[wave][j0 + jj];
+    for (int e = 0; e < NPL; ++e) {
+        const uint32_t i = (uint32_t)e * 64u + lane;
+        const llima_u32x4 me = i < ns ? sv[i] : llima_u32x4{0u, 0u, 0u, 0u};
+        key[e] = me.x; id[e] = me.y;
+        w[e] = ((uint64_t)me.w << 32) | me.z;
+    }
+    const uint32_t j0 = wave * PER;
+    uint32_t gt[NPL], eq[NPL];
+    uint64_t above[NPL], same[NPL];
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) { gt[e] = 0; eq[e] = 0; above[e] = 0; same[e] = 0; }
+#pragma unroll
+    for (uint32_t jj = 0; jj < PER; ++jj) {
+        const llima_u32x4 o = sv[j0 + jj];
+        const bool in = j0 + jj < ns;
         const uint64_t wj = ((uint64_t)o.w << 32) | o.z;
-        gt += o.x > key ? 1u : 0u;
-        eq += o.x == key ? 1u : 0u;
-        above += o.x > key ? wj : 0ull;
-    }
-    sh.part[0][wave][lane] = above;
-    sh.pc[wave][lane] = gt | (eq << 16);
-    __syncthreads();
-    above = 0; gt = 0; eq = 0;
 #pragma unroll
-    for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) {
-        above += sh.part[0][w2][lane];
-        const uint32_t g2 = sh.pc[w2][lane];
-        gt += g2 & 0xFFFFu;
-        eq += g2 >> 16;
+        for (int e = 0; e < NPL; ++e) {
+            gt[e] += in && o.x > key[e] ? 1u : 0u;
+            eq[e] += in && o.x == key[e] ? 1u : 0u;
+            above[e] += in && o.x > key[e] ? wj : 0ull;
+            same[e] += in && o.x == key[e] ? wj : 0ull;
+        }
     }
-    uint32_t tau = kmin;
-    if (c.k > 0 && (uint32_t)c.k < nfin) {
-        const bool at = key != 0 && gt < (uint32_t)c.k && gt + eq >= (uint32_t)c.k;
-        tau = wave_max_u32(at ? key : 0u);
-    } else if (c.k > 0 && (uint32_t)c.k > nfin && gthr) {
-        return false;
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        sh.part[e][wave][lane] = above[e];
+        sh.part2[e][wave][lane] = same[e];
+        sh.pc[e][wave][lane] = gt[e] | (eq[e] << 16);
     }
-    // the proof that the bound dropped no member of the top-k set: a value
-    // below it has x <= fl(g / T) < tau
-    if (gthr && !(lower_bound_margin(key_f32(gthr)) / c.T < key_f32(tau))) return false;
+    __syncthreads();
+    // tau: the key of a candidate with gt < k <= gt + eq; Z (the mass kept by
+    // top-k) = mass above tau + mass equal to it, read off that candidate
+    uint32_t tk = 0;
+    uint64_t zt = 0;
+    const bool has_k = c.k > 0 && (uint32_t)c.k <= ns;
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        above[e] = 0; same[e] = 0; gt[e] = 0; eq[e] = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) {
+            above[e] += sh.part[e][w2][lane];
+            same[e] += sh.part2[e][w2][lane];
+            const uint32_t g2 = sh.pc[e][w2][lane];
+            gt[e] += g2 & 0xFFFFu;
+            eq[e] += g2 >> 16;
+        }
+        const uint32_t i = (uint32_t)e * 64u + lane;
+        const bool at = has_k && i < ns && gt[e] < (uint32_t)c.k && gt[e] + eq[e] >= (uint32_t)c.k;
+        if (at && key[e] > tk) { tk = key[e]; zt = above[e] + same[e]; }
+    }
+    uint32_t tau = 1u;
+    uint64_t Zk = 0;                                  // valid when has_k
+    if (has_k) {
+        tau = wave_max_u32(tk);
+        const uint64_t hit = ballot(tk == tau && tau != 0u);
+        const uint32_t L = hit ? (uint32_t)__builtin_ffsll((long long)hit) - 1u : 0u;
+        Zk = readlane64(zt, L);
+    }
+    if (c.k > 0 && tcut && !(tau > tcut)) return false;   // uniform: every wave has tau
 
-    const bool mine = key != 0 && key >= tau;
-    bool fin = mine;
+    bool fin[NPL];
+    uint64_t zk = 0;
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        fin[e] = (uint32_t)e * 64u + lane < ns && key[e] != 0u && key[e] >= tau;
+        zk += fin[e] ? w[e] : 0ull;
+    }
     if (c.p < 1.0f) {
         // (above << 32) < frac32(p) * Z  <=>  above < ceil(frac32(p) * Z / 2^32)
-        const uint64_t Z = wave_sum_u64(mine ? w : 0ull);
+        const uint64_t Z = has_k ? Zk : wave_sum_u64(zk);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
         const uint64_t plim = (uint64_t)((PZ + 0xFFFFFFFFull) >> 32);
-        fin = fin && (above < plim || key == kmax);
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) fin[e] = fin[e] && (above[e] < plim || key[e] == kmax);
     }
-    if (c.m > 0.0f) fin = fin && w >= (frac32(c.m) << 4);
-    const uint64_t wf = fin ? w : 0ull;
-    const uint64_t Zf = wave_sum_u64(wf);            // the same in every wave
-    if (Zf == 0) {
-        if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
-    } else {
-        const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
-        sh.sv[wave][lane] = llima_u32x4{id, 0u, (uint32_t)wf, (uint32_t)(wf >> 32)};
-        uint64_t upto = 0;                            // mass of final ids <= this id
+    if (c.m > 0.0f) {
+        const uint64_t mthr = frac32(c.m) << 4;
 #pragma unroll
-        for (uint32_t jj = 0; jj < 16; ++jj) {
-            const llima_u32x4 o = sh.sv[wave][j0 + jj];
-            upto += o.x <= id ? (((uint64_t)o.w << 32) | o.z) : 0ull;
+        for (int e = 0; e < NPL; ++e) fin[e] = fin[e] && w[e] >= mthr;
+    }
+    uint64_t wf[NPL];
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) wf[e] = fin[e] ? w[e] : 0ull;
+    if (id_sorted) {
+        // element order (e, lane) is id order: the draw is a scan
+        uint64_t upto[NPL], Zf = 0;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+            upto[e] = wave_incl_scan_u64(wf[e]) + Zf;
+            Zf = readlane63(upto[e]);
         }
-        sh.part[1][wave][lane] = upto;
-        __syncthreads();
-        upto = 0;
+        if (Zf == 0) {
+            if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
+        } else {
+            const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
 #pragma unroll
-        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) upto += sh.part[1][w2][lane];
-        if (wave == 0 && wf > 0 && upto - wf <= target && target < upto)
-            write_result(P, row, (int32_t)id, (float)((double)wf / (double)Zf));
+            for (int e = 0; e < NPL; ++e)
+                if (wave == 0 && wf[e] > 0 && upto[e] - wf[e] <= target && target < upto[e])
+                    write_result(P, row, (int32_t)id[e], (float)((double)wf[e] / (double)Zf));
+        }
+    } else {
+        uint64_t zl = 0;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) zl += wf[e];
+        const uint64_t Zf = wave_sum_u64(zl);        // the same in every wave
+        __syncthreads();                              // every wave has read sv and part
+        if (Zf == 0) {
+            if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
+        } else {
+            const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+            if (wave == 0) {
+#pragma unroll
+                for (int e = 0; e < NPL; ++e)
+                    sv[(uint32_t)e * 64u + lane] = llima_u32x4{id[e], 0u, (uint32_t)wf[e], (uint32_t)(wf[e] >> 32)};
+            }
+            __syncthreads();
+            uint64_t upto[NPL];
+#pragma unroll
+            for (int e = 0; e < NPL; ++e) upto[e] = 0;
+#pragma unroll
+            for (uint32_t jj = 0; jj < PER; ++jj) {
+                const llima_u32x4 o = sv[j0 + jj];
+                const uint64_t wj = ((uint64_t)o.w << 32) | o.z;
+#pragma unroll
+                for (int e = 0; e < NPL; ++e) upto[e] += o.x <= id[e] ? wj : 0ull;   // wf 0 past ns
+            }
+#pragma unroll
+            for (int e = 0; e < NPL; ++e) sh.part[e][wave][lane] = upto[e];
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < NPL; ++e) {
+                uint64_t u = 0;
+#pragma unroll
+                for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) u += sh.part[e][w2][lane];
+                if (wave == 0 && wf[e] > 0 && u - wf[e] <= target && target < u)
+                    write_result(P, row, (int32_t)id[e], (float)((double)wf[e] / (double)Zf));
+            }
+        }
     }
     if (P.out_keep)
-        write_keep(P, row, [&](auto set) { if (wave == 0 && fin) set(id); });
+        write_keep(P, row, [&](auto set) {
+#pragma unroll
+            for (int e = 0; e < NPL; ++e)
+                if (wave == 0 && fin[e]) set(id[e]);
+        });
     return true;
 }
 
-// Many survivors (top-k disabled, ties, k > 64): radix selects over the
-// register-resident candidates.
-__device__ __forceinline__ void fin_large(const SampleParams& P, int row, const RowCfg& c,
-                                          uint32_t (&key)[SAMPLE_SLOTS],
-                                          const uint32_t (&id)[SAMPLE_SLOTS], uint32_t tau,
-                                          uint32_t kmax, FinishShared& sh, int& buf) {
-    uint64_t w[SAMPLE_SLOTS];
+// ------------------------------------------------------------------ fast path
+__device__ __forceinline__ uint32_t hash_slot(uint32_t id) {
+    return (id * 2654435761u) >> (32 - 12);         // SMP_HASH = 4096 slots
+}
+
+// Candidates f = t + 256 j (j < EPT) of the N gathered in sh.u.cand (id
+// order).  False when the row needs the full-row path (nothing written yet).
+template <int EPT>
+__device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const RowCfg& c, uint32_t N,
+                          uint32_t gkey, const int32_t (&hid)[SMP_HBATCH], FinShared& sh) {
+    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
+    float x[EPT];
+    uint32_t id[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+        x[j] = -__builtin_inff();
+        id[j] = 0;
+        if (f < N) {
+            const uint64_t q = sh.u.cand[f + (f >> 4)];
+            x[j] = __uint_as_float((uint32_t)(q >> 32));
+            id[j] = (uint32_t)q;
+        }
+    }
+
+    // ---- lazy penalties: history ids counted against a hash of the candidate ids
+    if (P.lazy && c.pen) {
+        if (N > SMP_HASH / 2) return false;
+        __syncthreads();                              // sh.u.cand is read
+        for (uint32_t i = t; i < SMP_HASH / 4; i += LLIMA_WG) {
+            ((llima_u32x4*)sh.u.hash.key)[i] = llima_u32x4{0u, 0u, 0u, 0u};
+            ((llima_u32x4*)sh.u.hash.cnt)[i] = llima_u32x4{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();
+        uint32_t slot[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            slot[j] = 0;
+            if (t + (uint32_t)j * LLIMA_WG < N) {
+                uint32_t h = hash_slot(id[j]);
+                for (int p = 0; p < SMP_HASH; ++p) {
+                    const uint32_t prev = atomicCAS(&sh.u.hash.key[h], 0u, id[j] + 1u);
+                    if (prev == 0u) break;
+                    h = (h + 1u) & (SMP_HASH - 1u);
+                }
+                slot[j] = h;
+            }
+        }
+        __syncthreads();
+        auto count_id = [&](int32_t hv) {
+            if (hv < 0 || hv >= P.V) return;
+            uint32_t h = hash_slot((uint32_t)hv);
+            for (int p = 0; p < SMP_HASH; ++p) {
+                const uint32_t kk = sh.u.hash.key[h];
+                if (kk == (uint32_t)hv + 1u) { atomicAdd(&sh.u.hash.cnt[h], 1u); return; }
+                if (kk == 0u) return;
+                h = (h + 1u) & (SMP_HASH - 1u);
+            }
+        };
+#pragma unroll
+        for (int b = 0; b < SMP_HBATCH; ++b)
+            if ((int)t + b * LLIMA_WG < c.hlen) count_id(hid[b]);
+        const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+        for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) count_id(hrow[i]);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            if (t + (uint32_t)j * LLIMA_WG < N) {
+                const uint32_t cn = sh.u.hash.cnt[slot[j]];
+                if (cn) x[j] = penalize(x[j], cn, c);
+            }
+        }
+    }
+
+    // ---- keys of x / T (0: absent or -inf), row maximum and minimum, count
+    uint32_t key[EPT];
+    uint32_t kmx = 0, nkmn = 0, nf = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        key[j] = 0;
+        if (t + (uint32_t)j * LLIMA_WG < N) {
+            const uint32_t k = f32_key(x[j] / c.T);
+            key[j] = k > LLIMA_KEY_NEG_INF ? k : 0u;
+        }
+        kmx = key[j] > kmx ? key[j] : kmx;
+        nkmn = key[j] && ~key[j] > nkmn ? ~key[j] : nkmn;
+        nf += key[j] ? 1u : 0u;
+    }
+    {
+        const uint32_t a = wave_max_u32(kmx), b = wave_max_u32(nkmn), s2 = wave_sum_u32(nf);
+        if (lane == 0) { sh.r32[0][wave] = a; sh.r32[1][wave] = b; sh.r32[2][wave] = s2; }
+        sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
+        sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
+        __syncthreads();
+        kmx = 0; nkmn = 0; nf = 0;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            kmx = sh.r32[0][w] > kmx ? sh.r32[0][w] : kmx;
+            nkmn = sh.r32[1][w] > nkmn ? sh.r32[1][w] : nkmn;
+            nf += sh.r32[2][w];
+        }
+        __syncthreads();
+    }
+    const uint32_t kmax = kmx, kmin = ~nkmn;
+    if (nf == 0) {
+        if (gkey) return false;                      // skipped values may be finite
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        if (P.out_keep) write_keep(P, row, [&](auto) {});
+        return true;
+    }
     const float xmax = key_f32(kmax);
+
+    // ---- lower edge of the top-k boundary: histogram rounds until at most 64
+    //      values are at or above it (or the k-th largest key itself is known)
+    uint32_t lowkey = 1u;
+    bool exact = true;                               // lowkey is tau itself
+    if (c.k > 0) {
+        if (nf < (uint32_t)c.k) {
+            if (gkey) return false;                  // values left out could count
+        } else {
+            Digits d = digits_init(kmin, kmax);
+            uint32_t rem = (uint32_t)c.k, above_all = 0;
+            lowkey = d.prefix;
+            exact = d.top < 0;
+            int buf = 0;
+            while (d.top >= 0) {
+                const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+                const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
+                uint32_t* hc = sh.hcnt[buf];
+#pragma unroll
+                for (int j = 0; j < EPT; ++j)
+                    if (key[j] && (key[j] & d.pmask) == d.prefix) atomicAdd(&hc[(key[j] >> lo) & bmask], 1u);
+                __syncthreads();
+                const uint32_t bin = 255u - t;                 // thread 0 <-> top bin
+                const uint32_t cn = hc[bin];
+                sh.hcnt[buf ^ 1][t] = 0;
+                const uint32_t inc = wave_incl_scan_u32(cn);
+                const uint32_t ab = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
+                if (ab < rem && ab + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = ab; sh.sel[2] = cn; }
+                __syncthreads();
+                const uint32_t sb = sh.sel[0], sab = sh.sel[1], scn = sh.sel[2];
+                hc[t] = 0;
+                buf ^= 1;
+                d.prefix |= sb << lo;
+                d.pmask |= bmask << lo;
+                d.top = lo - 1;
+                rem -= sab;
+                above_all += sab;
+                lowkey = d.prefix;
+                exact = d.top < 0;
+                if (above_all + scn <= SMP_SMALL) break;
+            }
+            __syncthreads();
+        }
+    } else if (gkey) {
+        // without top-k every skipped value must have weight 0 (and not matter)
+        const float dg = key_f32(gkey) - xmax;
+        if (dg >= -26.0f || !zero_weight_irrelevant(P, c)) return false;
+    }
+    if (c.k > 0 && exact && gkey && !(lowkey > gkey)) return false;
+
+    // ---- values at or above lowkey: at most 64 -> pairwise small path
+    uint32_t ns = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) ns += key[j] && key[j] >= lowkey ? 1u : 0u;
+    uint32_t nst;
+    const uint32_t so = block_excl_scan_u32(ns, &nst, sh.bs);
+    if (nst <= SMP_SMALL) {
+        uint32_t o = so;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            if (key[j] && key[j] >= lowkey) {
+                const uint64_t w = weight(key_f32(key[j]), xmax);
+                sh.sv[o] = llima_u32x4{key[j], id[j], (uint32_t)w, (uint32_t)(w >> 32)};
+                ++o;
+            }
+        }
+        __syncthreads();
+        return fin_small<1>(P, row, c, nst, kmax, c.k > 0 ? gkey : 0u, sh.sv, false, sh);
+    }
+    // more than 64 remain only when lowkey is tau (ties) or there is no top-k
+
+    // ---- many survivors: weights, top-p radix, min-p, draw by a scan in id order
+    const uint32_t tau = lowkey;
+    uint64_t w[EPT];
     uint64_t Z = 0;
 #pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+    for (int j = 0; j < EPT; ++j) {
         if (key[j] < tau) key[j] = 0;
         w[j] = key[j] ? weight(key_f32(key[j]), xmax) : 0ull;
         Z += w[j];
@@ -907,294 +1181,431 @@ __device__ __forceinline__ void fin_large(const SampleParams& P, int row, const 
     if (c.p < 1.0f) {
         Z = block_sum_u64(Z, sh.bs);
         const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = fin_topp_desc(key, w, PZ, tau, kmax, sh, buf);
+        theta = fin_topp_desc<EPT>(key, w, PZ, tau > kmin ? tau : kmin, kmax, sh);
     }
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     uint32_t fmask = 0;
-    uint64_t Zf = 0;
 #pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
+    for (int j = 0; j < EPT; ++j) {
         const bool f = key[j] && key[j] >= theta && w[j] >= mthr;
         fmask |= f ? (1u << j) : 0u;
         w[j] = f ? w[j] : 0ull;
-        Zf += w[j];
     }
-    Zf = block_sum_u64(Zf, sh.bs);
-    int32_t tok = -1;
-    float prob = 0.0f;
-    if (Zf > 0) {
+    // final weights into LDS in id order, then 16 consecutive ids per thread
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+        if (f < N) sh.u.cand[f + (f >> 4)] = w[j];
+    }
+    __syncthreads();
+    uint64_t ws[16], mysum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t f = t * 16u + (uint32_t)j;
+        ws[j] = f < N ? sh.u.cand[f + (f >> 4)] : 0ull;
+        mysum += ws[j];
+    }
+    uint64_t Zf;
+    const uint64_t before = block_excl_scan_u64(mysum, &Zf, sh.bs);
+    if (Zf == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+    } else {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
-        uint64_t wtok = 0;
-        tok = (int32_t)fin_draw_asc(id, w, target, (uint32_t)P.V, &wtok, sh, buf);
-        prob = (float)((double)wtok / (double)Zf);
+        if (mysum > 0 && before <= target && target < before + mysum) {
+            uint64_t acc = before;
+            int jt = -1;
+            uint64_t wt = 0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (jt < 0 && ws[j] && acc <= target && target < acc + ws[j]) { jt = j; wt = ws[j]; }
+                acc += ws[j];
+            }
+            const uint32_t f = t * 16u + (uint32_t)jt;
+            sh.sel[3] = f;
+            sh.sel64[1] = wt;
+        }
     }
-    if (threadIdx.x == 0) write_result(P, row, tok, prob);
+    __syncthreads();
+    if (Zf > 0) {
+        // element f lives in thread f % 256, slot f / 256, which holds its id
+        const uint32_t ftok = sh.sel[3];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (t + (uint32_t)j * LLIMA_WG == ftok)
+                write_result(P, row, (int32_t)id[j], (float)((double)sh.sel64[1] / (double)Zf));
+    }
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
 #pragma unroll
-            for (int j = 0; j < SAMPLE_SLOTS; ++j)
+            for (int j = 0; j < EPT; ++j)
                 if ((fmask >> j) & 1u) set(id[j]);
         });
+    return true;
 }
 
-// The row from the sweep's candidates; false when it needs the full-row path.
-__device__ __forceinline__ bool fin_fast(const SampleParams& P, int row, const RowCfg& c,
-                                         FinishShared& sh) {
-    constexpr int HPL = 2;                           // chunk headers per lane (S <= 128)
+// ------------------------------------------------------------------ direct path
+// Survivors (at most 64), staged in sh.sv[0, ns) as {raw value bits, id}: the
+// candidates at or above the raw key lowkey (1: every candidate).  Every wave
+// holds all of them (lane l: survivor l).  Lazy rows take their penalties here
+// (history ids counted against a hash of the survivor ids); then x / T, the
+// weights and the pairwise passes of fin_small.  Returns false, before
+// writing anything, when the result cannot be proven: tau must exceed the
+// chunk bounds (gkey) and, when lowkey cut candidates off, fl(lowkey / T) (a
+// value below lowkey, penalised or not, is at most that).
+__device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, const RowCfg& c, uint32_t ns,
+                              uint32_t lowkey, uint32_t gkey, const int32_t (&hid)[SMP_HBATCH],
+                              FinShared& sh) {
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
-    const int S = P.S;
-    if (S > 64 * HPL) return false;
-    const ChunkHdr* hdr = P.hdr + (size_t)row * S;
-
-    // ---- 1. loads, all issued before any is used: this thread's candidate
-    //         slots (the first `pre` slots of every chunk, whatever their
-    //         counts), then every header, read by every wave (lane l: chunks l
-    //         and l + 64)
-    uint64_t q[SAMPLE_SLOTS];
-    const uint64_t* crow = P.cand + ((size_t)row * S << P.ls);
-    const uint32_t pmask = (1u << P.lp) - 1u;
+    float x[2];
+    uint32_t id[2];
 #pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        const uint32_t f = t + (uint32_t)j * LLIMA_WG;   // chunk f >> lp, slot f & pmask
-        const uint32_t ch = f >> P.lp;
-        q[j] = crow[ch < (uint32_t)S ? (ch << P.ls) + (f & pmask) : 0u];
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t i = (uint32_t)e * 64u + lane;
+        const llima_u32x4 me = i < ns ? sh.sv[i] : llima_u32x4{0u, 0u, 0u, 0u};
+        x[e] = i < ns ? key_f32(me.x) : -__builtin_inff();
+        id[e] = me.y;
     }
-    llima_u32x4 ha[HPL], hb[HPL], hc[HPL];
+    if (P.lazy && c.pen) {
+        // a hashed bitmap of the survivor ids (sh.u.hash.key, zeroed by the
+        // caller) rules out almost every history id with one LDS read; a hit
+        // is resolved by binary search among the survivors (id order)
+        uint32_t* bm = sh.u.hash.key;
+        auto bit_of = [](uint32_t v) { return (v * 2654435761u) >> 15; };   // 2^17 bits
+        if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < HPL; ++i) {
-        const int ch = (int)lane + 64 * i;
-        const llima_u32x4* hp = (const llima_u32x4*)(hdr + (ch < S ? ch : 0));
-        ha[i] = hp[0];
-        hb[i] = hp[1];
-        hc[i] = hp[2];
-    }
-    sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
-    sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
-
-    // ---- 2. header summary, computed by every wave (no barrier)
-    uint32_t fl = 0, bstar = 0, n = 0, spill = 0;
-    uint64_t greedy = 0;
+            for (int e = 0; e < 2; ++e) {
+                if ((uint32_t)e * 64u + lane < ns) {
+                    const uint32_t h = bit_of(id[e]);
+                    atomicOr(&bm[h >> 5], 1u << (h & 31u));
+                }
+            }
+        }
+        __syncthreads();
+        auto count_id = [&](int32_t hv) {
+            if (hv < 0 || hv >= P.V) return;
+            const uint32_t h = bit_of((uint32_t)hv);
+            if (!((bm[h >> 5] >> (h & 31u)) & 1u)) return;
+            uint32_t lo = 0, hi = ns;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (sh.sv[mid].y < (uint32_t)hv) lo = mid + 1; else hi = mid;
+            }
+            if (lo < ns && sh.sv[lo].y == (uint32_t)hv) atomicAdd(&sh.hc[lo], 1u);
+        };
 #pragma unroll
-    for (int i = 0; i < HPL; ++i) {
-        if (i * 64 < S) {
-            const int ch = (int)lane + 64 * i;
-            if (ch < S) {
-                fl |= ha[i].y;
-                if (ha[i].y & HDR_FILTERED) bstar = ha[i].z > bstar ? ha[i].z : bstar;
-                n += ha[i].x;
-                spill |= ha[i].x > (1u << P.lp) ? 1u : 0u;
-                const uint64_t g = ((uint64_t)hb[i].y << 32) | hb[i].x;
-                greedy = g > greedy ? g : greedy;
-                sh.wcnt[wave][ch] = ha[i].x;
+        for (int b = 0; b < SMP_HBATCH; ++b)
+            if ((int)t + b * LLIMA_WG < c.hlen) count_id(hid[b]);
+        const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+        for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) count_id(hrow[i]);
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t i = (uint32_t)e * 64u + lane;
+            if (i < ns) {
+                const uint32_t cn = sh.hc[i];
+                if (cn) x[e] = penalize(x[e], cn, c);
             }
         }
     }
-    fl = wave_or_u32(fl);
-    bstar = wave_max_u32(bstar);
-    n = wave_sum_u32(n);
-    spill = wave_max_u32(spill);
-    greedy = wave_max_u64(greedy);
-
-    if (c.greedy) {
-        if (fl & HDR_OVERFLOW) return false;
-        const bool ok = (uint32_t)(greedy >> 32) > LLIMA_KEY_NEG_INF;
-        const uint32_t tok = ok ? ~(uint32_t)greedy : 0xFFFFFFFFu;
-        if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
-        if (P.out_keep)
-            write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
+    // every wave: temperature, keys and weights of the survivors -> its own
+    // copy sh.sv2[wave] (no barrier before the pairwise passes)
+    uint32_t key[2], kmax = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const float xt = x[e] / c.T;
+        key[e] = (uint32_t)e * 64u + lane < ns && xt > -__builtin_inff() ? f32_key(xt) : 0u;
+        kmax = key[e] > kmax ? key[e] : kmax;
+    }
+    kmax = wave_max_u32(kmax);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint64_t w = key[e] ? weight(key_f32(key[e]), key_f32(kmax)) : 0ull;
+        sh.sv2[wave][(uint32_t)e * 64u + lane] = llima_u32x4{key[e], id[e], (uint32_t)w, (uint32_t)(w >> 32)};
+    }
+    __builtin_amdgcn_wave_barrier();                 // the wave's LDS writes precede its reads
+    if (kmax == 0u) {
+        if (gkey || lowkey > 1u) return false;
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        if (P.out_keep) write_keep(P, row, [&](auto) {});
         return true;
     }
-    if ((fl & HDR_OVERFLOW) || n > SAMPLE_FIN_CAP) return false;
+    uint32_t tcut = 0;
+    if (c.k > 0) {
+        tcut = gkey;
+        if (lowkey > 1u) {
+            const uint32_t kl = f32_key(key_f32(lowkey) / c.T);
+            tcut = kl > tcut ? kl : tcut;
+        }
+    }
+    return ns <= SMP_SMALL ? fin_small<1>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh)
+                           : fin_small<2>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh);
+}
 
-    // ---- 3. bound on the top-k threshold: the largest chunk bound (that chunk
-    //         has k values at or above it), or the k-th largest of the lane
-    //         maxima in the headers (distinct values of the row), whichever is larger
-    uint32_t gthr = bstar;
-    if (c.k > 0 && 8 * S >= c.k) {
-        constexpr int NV = 8 * HPL;
-        uint32_t hv[NV];
-        uint32_t vmax = 0, vmin = 0xFFFFFFFFu, nz = 0;
+// Candidates straight from the first-round loads: thread t holds the 8 slots
+// [8 part, 8 part + 8) of its chunk's region, so slot order over the threads
+// is id order.  kr: raw keys (0 = no candidate), idv: ids.  Finds the lower
+// edge lowkey of the top-k boundary on the raw values with histogram rounds
+// until at most 64 candidates remain at or above it, stages them and hands
+// over to fin_survivors.  False when the row needs another path.
+__device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const RowCfg& c, const uint32_t (&kr)[8],
+                           const uint32_t (&idv)[8], uint32_t N, uint32_t kmin, uint32_t kmax,
+                           uint32_t gkey, const int32_t (&hid)[SMP_HBATCH], FinShared& sh) {
+    const uint32_t t = threadIdx.x;
+    if (N == 0) {
+        if (gkey) return false;
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        if (P.out_keep) write_keep(P, row, [&](auto) {});
+        return true;
+    }
+    if (P.lazy && c.pen) {
 #pragma unroll
-        for (int i = 0; i < HPL; ++i) {
-            const bool in = (int)lane + 64 * i < S;
-            const uint32_t a[8] = {hb[i].x, hb[i].y, hb[i].z, hb[i].w,
-                                   hc[i].x, hc[i].y, hc[i].z, hc[i].w};
+        for (int i = 0; i < SMP_HASH / 4 / LLIMA_WG; ++i)
+            ((llima_u32x4*)sh.u.hash.key)[t + i * LLIMA_WG] = llima_u32x4{0u, 0u, 0u, 0u};
+    }
+    uint32_t lowkey = 1u;
+    if (c.k > 0) {
+        if (N < (uint32_t)c.k) {
+            if (gkey) return false;                  // values left out could count
+        } else {
+            Digits d = digits_init(kmin, kmax);
+            // lazy penalties can push values of the top-k below their raw rank:
+            // keep a margin of candidates below the k-th largest raw value
+            const uint32_t kk = (uint32_t)c.k;
+            const uint32_t margin = !(P.lazy && c.pen) ? 0u
+                                  : kk + 10u <= SMP_SMALL ? 10u
+                                  : kk < 2u * SMP_SMALL ? min(32u, 2u * SMP_SMALL - kk) : 0u;
+            uint32_t rem = min(N, (uint32_t)c.k + margin), above_all = 0;
+            lowkey = d.prefix;
+            int buf = 0;
+            while (d.top >= 0) {
+                const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
+                const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
+                uint32_t* hc = sh.hcnt[buf];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t x = in ? a[u] : 0u;
-                hv[i * 8 + u] = x;
-                vmax = x > vmax ? x : vmax;
-                vmin = x && x < vmin ? x : vmin;
-                nz += x ? 1u : 0u;
+                for (int j = 0; j < 8; ++j)
+                    if (kr[j] && (kr[j] & d.pmask) == d.prefix) atomicAdd(&hc[(kr[j] >> lo) & bmask], 1u);
+                __syncthreads();
+                const uint32_t bin = 255u - t;                 // thread 0 <-> top bin
+                const uint32_t cn = hc[bin];
+                sh.hcnt[buf ^ 1][t] = 0;
+                const uint32_t inc = wave_incl_scan_u32(cn);
+                const uint32_t ab = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
+                if (ab < rem && ab + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = ab; sh.sel[2] = cn; }
+                __syncthreads();
+                const uint32_t sb = sh.sel[0], sab = sh.sel[1], scn = sh.sel[2];
+                hc[t] = 0;
+                buf ^= 1;
+                d.prefix |= sb << lo;
+                d.pmask |= bmask << lo;
+                d.top = lo - 1;
+                rem -= sab;
+                above_all += sab;
+                lowkey = d.prefix;
+                if (above_all + scn <= 2 * SMP_SMALL) break;
             }
+            __syncthreads();
         }
-        vmax = wave_max_u32(vmax);
-        vmin = wave_min_u32(vmin);
-        nz = wave_sum_u32(nz);
-        if (nz >= (uint32_t)c.k) {
-            // The lower edge of the histogram bin holding the k-th largest
-            // value (8-bit bins below the bits all the values share), with a
-            // histogram of its own in every wave: no barrier.
-            const uint32_t diff = vmax ^ vmin;
-            uint32_t tb = vmax;
-            if (diff) {
-                const int top = 31 - __builtin_clz(diff);
-                const int lo = top - 7 > 0 ? top - 7 : 0;
-                const uint32_t bmask = (2u << (top - lo)) - 1u;
-                const uint32_t prefix = top == 31 ? 0u : (vmax & ~((2u << top) - 1u));
-                uint32_t* bh = sh.bh[wave];
-                *(llima_u32x4*)(bh + 4 * lane) = llima_u32x4{0u, 0u, 0u, 0u};
+    } else if (gkey) {
+        // without top-k every skipped value must have weight 0 (and not matter)
+        const float dg = key_f32(gkey) - key_f32(kmax) / c.T;
+        if (dg >= -26.0f || !zero_weight_irrelevant(P, c)) return false;
+    }
+    uint32_t ns = 0;
 #pragma unroll
-                for (int u = 0; u < NV; ++u)
-                    if (hv[u]) atomicAdd(&bh[(hv[u] >> lo) & bmask], 1u);
-                // lane l holds bins 255 - 4l (top) down to 252 - 4l
-                const llima_u32x4 b4 = *(const llima_u32x4*)(bh + 252 - 4 * lane);
-                const uint32_t s4 = b4.x + b4.y + b4.z + b4.w;
-                const uint32_t inc = wave_incl_scan_u32(s4);   // values in bins >= 252 - 4l
-                const uint64_t hit = ballot(inc >= (uint32_t)c.k);
-                const uint32_t L = (uint32_t)__builtin_ffsll((long long)hit) - 1u;
-                uint32_t acc = readlane(inc - s4, L);
-                const uint32_t q3 = readlane(b4.w, L), q2 = readlane(b4.z, L), q1 = readlane(b4.y, L);
-                uint32_t bin = 252u - 4u * L;
-                if (acc + q3 >= (uint32_t)c.k) bin = 255u - 4u * L;
-                else if (acc + q3 + q2 >= (uint32_t)c.k) bin = 254u - 4u * L;
-                else if (acc + q3 + q2 + q1 >= (uint32_t)c.k) bin = 253u - 4u * L;
-                tb = prefix | (bin << lo);
-            }
-            gthr = tb > gthr ? tb : gthr;
-        }
-    }
-    float gr = -__FLT_MAX__;
-    if (gthr) {
-        const float m = lower_bound_margin(key_f32(gthr));
-        gr = m > -__FLT_MAX__ ? m : -__FLT_MAX__;
-    }
-
-    // ---- 4. slots f < lim hold a candidate or the padding; a chunk with more
-    //         than `pre` candidates sends every candidate of the row through
-    //         LDS in chunk order
-    uint32_t lim = (uint32_t)S << P.lp;
-    if (spill) {
-        lim = SAMPLE_FIN_CAP;
-        const uint32_t cn = (int)t < S ? sh.wcnt[wave][t] : 0u;
-        const uint32_t inc = wave_incl_scan_u32(cn);
-        const uint32_t off = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
-        if ((int)t < S) sh.coff[t] = off;
-        __syncthreads();
-        for (int ch = (int)wave; ch < S; ch += LLIMA_WAVES) {
-            const uint32_t o = sh.coff[ch];
-            const uint32_t m = sh.wcnt[wave][ch];
-            const uint64_t* src = crow + ((size_t)ch << P.ls);
-            for (uint32_t i = lane; i < m; i += 64) sh.u.cbuf[o + i] = src[i];
-        }
-        __syncthreads();
+    for (int j = 0; j < 8; ++j) ns += kr[j] && kr[j] >= lowkey ? 1u : 0u;
+    uint32_t nst;
+    const uint32_t so = block_excl_scan_u32(ns, &nst, sh.bs);
+    if (nst > 2 * SMP_SMALL) return false;
+    uint32_t o = so;
 #pragma unroll
-        for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-            const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-            q[j] = f < n ? sh.u.cbuf[f] : SAMPLE_SENTINEL;
+    for (int j = 0; j < 8; ++j) {
+        if (kr[j] && kr[j] >= lowkey) {
+            sh.sv[o] = llima_u32x4{kr[j], idv[j], 0u, 0u};
+            ++o;
         }
     }
-
-    // ---- 5. candidates at or above the bound, staged per wave
-    uint32_t o = 0;
-#pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        const bool pass = t + (uint32_t)j * LLIMA_WG < lim &&
-                          __uint_as_float((uint32_t)(q[j] >> 32)) >= gr;
-        const uint64_t m = ballot(pass);
-        if (m) {
-            const uint32_t s2 = mbcnt_add(m, o);
-            if (pass && s2 < SAMPLE_SMALL) sh.stage[wave][s2] = q[j];
-            o += (uint32_t)__popcll(m);
-        }
-    }
-    if (lane == 0) sh.r32[0][wave] = o;
+    if (t < 2 * SMP_SMALL) { sh.hk[t] = 0; sh.hc[t] = 0; }
     __syncthreads();
-    uint32_t wc[LLIMA_WAVES], nk0 = 0;
-#pragma unroll
-    for (int w = 0; w < LLIMA_WAVES; ++w) { wc[w] = sh.r32[0][w]; nk0 += wc[w]; }
-
-    if (nk0 <= SAMPLE_SMALL) {
-        // ---- 6a. every wave holds all survivors, one per lane
-        uint32_t key = 0, id = 0;
-        if (lane < nk0) {
-            uint32_t w = 0, idx = lane;
-            while (w < LLIMA_WAVES - 1 && idx >= wc[w]) { idx -= wc[w]; ++w; }
-            const uint64_t qq = sh.stage[w][idx];
-            const uint32_t k = f32_key(__uint_as_float((uint32_t)(qq >> 32)) / c.T);
-            key = k > LLIMA_KEY_NEG_INF ? k : 0u;
-            id = (uint32_t)qq;
-        }
-        const uint32_t nfin = (uint32_t)__popcll(ballot(key != 0));
-        if (nfin == 0) {
-            if (gthr) return false;
-            if (t == 0) write_result(P, row, -1, 0.0f);
-            if (P.out_keep) write_keep(P, row, [&](auto) {});
-            return true;
-        }
-        const uint32_t kmax = wave_max_u32(key);
-        const uint32_t kmin = wave_min_u32(key ? key : 0xFFFFFFFFu);
-        return fin_small(P, row, c, key, id, nk0, nfin, kmin, kmax, gthr, sh);
-    }
-
-    // ---- 6b. many survivors: keys in registers, radix selects
-    uint32_t key[SAMPLE_SLOTS], id[SAMPLE_SLOTS];
-    uint32_t kmax = 0, nkmin = 0, nkeep = 0;
-#pragma unroll
-    for (int j = 0; j < SAMPLE_SLOTS; ++j) {
-        const float x = __uint_as_float((uint32_t)(q[j] >> 32));
-        const uint32_t k = f32_key(x / c.T);
-        const bool keep = t + (uint32_t)j * LLIMA_WG < lim && x >= gr && k > LLIMA_KEY_NEG_INF;
-        key[j] = keep ? k : 0u;
-        id[j] = (uint32_t)q[j];
-        nkeep += keep ? 1u : 0u;
-        kmax = keep && k > kmax ? k : kmax;
-        nkmin = keep && ~k > nkmin ? ~k : nkmin;
-    }
-    {
-        const uint32_t a = wave_max_u32(kmax), b = wave_max_u32(nkmin), s2 = wave_sum_u32(nkeep);
-        if (lane == 0) { sh.r32[4][wave] = a; sh.r32[5][wave] = b; sh.r32[6][wave] = s2; }
-        __syncthreads();
-        kmax = 0; nkmin = 0; nkeep = 0;
-#pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) {
-            kmax = sh.r32[4][w] > kmax ? sh.r32[4][w] : kmax;
-            nkmin = sh.r32[5][w] > nkmin ? sh.r32[5][w] : nkmin;
-            nkeep += sh.r32[6][w];
-        }
-    }
-    if (nkeep == 0) return false;                    // cannot happen with nk0 > 64 finite
-    const uint32_t kmin = ~nkmin;
-    int buf = 0;
-    uint32_t tau = kmin;
-    if (c.k > 0 && (uint32_t)c.k < nkeep) tau = fin_kth_desc(key, (uint32_t)c.k, kmin, kmax, sh, buf);
-    else if (c.k > 0 && (uint32_t)c.k > nkeep && gthr) return false;
-    if (gthr && !(lower_bound_margin(key_f32(gthr)) / c.T < key_f32(tau))) return false;
-    fin_large(P, row, c, key, id, tau, kmax, sh, buf);
-    return true;
+    return fin_survivors(P, row, c, nst, lowkey, gkey, hid, sh);
 }
 
 template <typename TL>
 __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
-    __shared__ FinishShared sh;
+    __shared__ FinShared sh;
     const int row = blockIdx.x;
     const RowCfg c = load_cfg(P, row);
-    if (!fin_fast(P, row, c, sh)) finish_full_row<TL>(P, row, c, sh);
+    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
+    const int S = P.S;
+    bool done = false;
+    if (S <= SMP_MAX_S) {
+        // ---- 1. one round of loads: thread t reads 64 bytes (8 slots) of chunk
+        //         t >> (8 - lgs), part t & (tpc - 1) (part 0 starts with the
+        //         header); then the history ids when the penalties are applied here
+        const int sh8 = 8 - P.lgs;
+        const uint32_t tpc = 1u << sh8;
+        const uint32_t ch = t >> sh8, pt = t & (tpc - 1u);
+        const bool mine = (int)ch < S && pt * 8u < SMP_REGION;
+        const uint64_t* reg = P.ws + ((size_t)row * S + (mine ? ch : 0u)) * SMP_REGION + (mine ? pt * 8u : 0u);
+        llima_u32x4 q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ((const llima_u32x4*)reg)[i];
+        int32_t hid[SMP_HBATCH];
+        if (P.lazy && c.pen) {
+            const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+#pragma unroll
+            for (int b = 0; b < SMP_HBATCH; ++b) {
+                const int j = (int)t + b * LLIMA_WG;
+                hid[b] = hrow[j < c.hlen ? j : c.hlen - 1];
+            }
+        }
+
+        // ---- 2. this thread's slots as candidates (raw keys; padding and the
+        //         header are none) and the header facts, reduced over the row
+        const uint32_t pre = pre_slots(P);
+        const bool hdr = mine && pt == 0;
+        uint32_t kr[8], idv[8];
+        uint32_t kmx = 0, nkmn = 0, n = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t hi = h ? q[i].w : q[i].y, lo = h ? q[i].z : q[i].x;
+                const bool valid = mine && !c.greedy && !(hdr && i == 0 && h == 0) &&
+                                   hi != (uint32_t)(SMP_SENTINEL >> 32);
+                const uint32_t k = valid ? f32_key(__uint_as_float(hi)) : 0u;
+                kr[2 * i + h] = k;
+                idv[2 * i + h] = lo;
+                kmx = k > kmx ? k : kmx;
+                nkmn = k && ~k > nkmn ? ~k : nkmn;
+                n += k ? 1u : 0u;
+            }
+        }
+        uint32_t ovf = 0, gk = 0;
+        uint64_t gr = 0;
+        if (hdr) {
+            const uint32_t flags = q[0].x >> 16;
+            const uint32_t count = (flags & HF_OVERFLOW) ? 0u : (q[0].x & 0xFFFFu);
+            ovf = (flags & HF_OVERFLOW) ? 2u : (SMP_HDR + count > pre ? 1u : 0u);
+            const float g = __uint_as_float(q[0].y);
+            if (!c.greedy && g > -__builtin_inff()) {
+                const float gt = g / c.T;
+                gk = gt == gt ? f32_key(gt) : 0xFFFFFFFFu;
+            }
+            gr = ((uint64_t)q[0].w << 32) | q[0].z;
+            sh.ccount[ch] = count;
+        }
+        {
+            const uint32_t a = wave_max_u32(kmx), b = wave_max_u32(nkmn), s2 = wave_sum_u32(n);
+            const uint32_t o2 = wave_max_u32(ovf), g2 = wave_max_u32(gk);
+            const uint64_t gg = c.greedy ? wave_max_u64(gr) : 0ull;
+            if (lane == 0) {
+                sh.r32[0][wave] = a; sh.r32[1][wave] = b; sh.r32[2][wave] = s2;
+                sh.r32[3][wave] = o2; sh.r32[4][wave] = g2; sh.r64[1][wave] = gg;
+            }
+            sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
+            sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
+            __syncthreads();
+        }
+        uint32_t kmax = 0, nkmin = 0, N = 0, ov = 0, gkey = 0;
+        uint64_t best = 0;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            kmax = sh.r32[0][w] > kmax ? sh.r32[0][w] : kmax;
+            nkmin = sh.r32[1][w] > nkmin ? sh.r32[1][w] : nkmin;
+            N += sh.r32[2][w];
+            ov = sh.r32[3][w] > ov ? sh.r32[3][w] : ov;
+            gkey = sh.r32[4][w] > gkey ? sh.r32[4][w] : gkey;
+            best = sh.r64[1][w] > best ? sh.r64[1][w] : best;
+        }
+
+        if (c.greedy) {
+            const bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
+            const uint32_t tok = ok ? ~(uint32_t)best : 0xFFFFFFFFu;
+            if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+            if (P.out_keep)
+                write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
+            done = true;
+        } else if (ov == 0u) {
+            done = fin_direct(P, row, c, kr, idv, N, ~nkmin, kmax, gkey, hid, sh);
+        }
+        if (!done && ov < 2u) {
+            // ---- 3. gather: candidates into LDS in id order (element f at f + f / 16)
+            __syncthreads();
+            if (wave == 0) {
+                // exclusive scan of the counts: lane l owns chunks 4l .. 4l+3
+                uint32_t cc[4], s4 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int cix = (int)lane * 4 + i;
+                    cc[i] = cix < S ? sh.ccount[cix] : 0u;
+                    s4 += cc[i];
+                }
+                const uint32_t inc = wave_incl_scan_u32(s4);
+                uint32_t o = inc - s4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int cix = (int)lane * 4 + i;
+                    if (cix < S) sh.coff[cix] = o;
+                    o += cc[i];
+                }
+                if (lane == 63) sh.hn = inc;
+            }
+            __syncthreads();
+            const uint32_t NG = sh.hn;
+            if (NG <= SMP_FIN_CAP) {
+                const uint32_t pre_c = pre - SMP_HDR;      // candidates read in 1.
+                if (mine) {
+                    const uint32_t n_c = sh.ccount[ch], o_c = sh.coff[ch];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int s = (int)(pt * 8u) + 2 * i + h - SMP_HDR;   // candidate index
+                            if (s >= 0 && (uint32_t)s < n_c) {
+                                const uint32_t f = o_c + (uint32_t)s;
+                                const uint64_t val = h ? (((uint64_t)q[i].w << 32) | q[i].z)
+                                                       : (((uint64_t)q[i].y << 32) | q[i].x);
+                                sh.u.cand[f + (f >> 4)] = val;
+                            }
+                        }
+                    }
+                }
+                // chunks with more candidates than the first round covered
+                for (int cc = (int)wave; cc < S; cc += LLIMA_WAVES) {
+                    const uint32_t n_c = sh.ccount[cc];
+                    if (n_c > pre_c) {
+                        const uint32_t o_c = sh.coff[cc];
+                        const uint64_t* src = P.ws + ((size_t)row * S + cc) * SMP_REGION + SMP_HDR;
+                        for (uint32_t s = pre_c + lane; s < n_c; s += 64) {
+                            const uint32_t f = o_c + s;
+                            sh.u.cand[f + (f >> 4)] = src[s];
+                        }
+                    }
+                }
+                sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
+                sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
+                __syncthreads();
+                done = NG <= 4u * LLIMA_WG ? fin_elems<4>(P, row, c, NG, gkey, hid, sh)
+                                           : fin_elems<16>(P, row, c, NG, gkey, hid, sh);
+            }
+        }
+    }
+    if (!done) finish_full_row<TL>(P, row, c, sh);
 }
 
 // ================================================================== host side
-static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
-static int max_chunks(int V) { return (V + SAMPLE_MIN_CHUNK - 1) / SAMPLE_MIN_CHUNK; }
+static int chunk_values(int dtype) { return dtype == LLIMA_F32 ? 4096 : 8192; }
 
-template <typename TL, int E>
+template <typename TL>
 static void launch_sweep(const SampleParams& P, hipStream_t st) {
     const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
     if (P.bitmask) {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true, true>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, E, false, true>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, true>), g, b, 0, st, P);
     } else {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, E, true, false>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, E, false, false>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, false>), g, b, 0, st, P);
     }
 }
 
@@ -1203,10 +1614,9 @@ static void launch_sweep(const SampleParams& P, hipStream_t st) {
 using namespace llima;
 
 extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
-    (void)dtype;
-    if (B <= 0 || V <= 0) return 0;
-    return al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)) +
-           (size_t)B * SAMPLE_ROW_CAND * sizeof(uint64_t);
+    if (B <= 0 || V <= 0 || (dtype != LLIMA_F32 && dtype != LLIMA_BF16)) return 0;
+    const size_t S = (size_t)((V + chunk_values(dtype) - 1) / chunk_values(dtype));
+    return (size_t)B * S * SMP_REGION * sizeof(uint64_t);
 }
 
 extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V,
@@ -1220,7 +1630,8 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     if (B < 0 || V <= 0 || V > (1 << 24) || row_stride < V) return LLIMA_E_INVAL;
     if (history && (H_max < 0 || H_max >= 65536)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
-    if (!workspace || workspace_bytes < llima_sample_workspace_bytes(B, V, dtype))
+    if (!workspace || workspace_bytes < llima_sample_workspace_bytes(B, V, dtype) ||
+        ((uintptr_t)workspace & 15u))
         return LLIMA_E_WORKSPACE;
     if (!cfg->greedy && !cfg->temperature_rows) {
         if (!(cfg->temperature >= 0.0f) || __builtin_isinf(cfg->temperature)) return LLIMA_E_INVAL;
@@ -1242,28 +1653,32 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.out_ids = out_ids;
     P.out_probs = out_probs;
     P.out_keep = out_keep;
+    P.ws = (uint64_t*)workspace;
     P.B = B;
     P.V = V;
     P.H_max = history ? H_max : 0;
+    const int chunk = chunk_values(dtype);
+    P.S = (V + chunk - 1) / chunk;
+    int lgs = 0;
+    while ((1 << lgs) < P.S && lgs < 8) ++lgs;
+    P.lgs = lgs;
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
     P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0) &&
                (V % (int32_t)(16 / esz) == 0);
-    // 16 KB of logits per workgroup: 4096 fp32 or 8192 bf16 values.
-    const int chunk = dtype == LLIMA_F32 ? 4096 : 8192;
-    P.S = (V + chunk - 1) / chunk;
-    // powers of two: share = slots per chunk, pre = slots per chunk the finish
-    // reads up front (S * pre <= 4096 = one slot per finishing thread x 16)
-    auto floor_log2 = [](int x) { int l = 0; while ((2 << l) <= x) ++l; return l; };
-    P.ls = floor_log2(SAMPLE_ROW_CAND / P.S);
-    P.lp = floor_log2(SAMPLE_FIN_CAP / P.S);
-    P.hdr = (ChunkHdr*)workspace;
-    P.cand = (uint64_t*)((char*)workspace + al256((size_t)B * max_chunks(V) * sizeof(ChunkHdr)));
+    // The finish applies the penalties (to the candidates only) when every row
+    // samples with top-k and the penalties can only lower a value: repetition
+    // >= 1, presence and frequency >= 0 (one broadcast configuration).
+    const bool rows_cfg = cfg->temperature_rows || cfg->top_k_rows || cfg->repetition_penalty_rows ||
+                          cfg->presence_penalty_rows || cfg->frequency_penalty_rows;
+    P.lazy = P.H_max > 0 && !rows_cfg && !cfg->greedy && cfg->temperature > 0.0f &&
+             cfg->top_k > 0 && cfg->top_k < V && cfg->repetition_penalty >= 1.0f &&
+             cfg->presence_penalty >= 0.0f && cfg->frequency_penalty >= 0.0f;
     hipStream_t st = (hipStream_t)stream;
     if (dtype == LLIMA_F32) {
-        launch_sweep<float, 16>(P, st);
+        launch_sweep<float>(P, st);
         hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
-        launch_sweep<uint16_t, 32>(P, st);
+        launch_sweep<uint16_t>(P, st);
         hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
