@@ -86,6 +86,7 @@ struct SampleParams {
 
 struct RowCfg {
     float T, p, m, R, alpha, beta;
+    float u;             // the row's uniform (loaded up front: it ends the finish)
     int32_t k;           // 0: top-k disabled
     bool greedy, pen;
     int32_t hlen;
@@ -109,6 +110,7 @@ __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
     r.R = row_or(c.repetition_penalty_rows, c.repetition_penalty, row);
     r.alpha = row_or(c.presence_penalty_rows, c.presence_penalty, row);
     r.beta = row_or(c.frequency_penalty_rows, c.frequency_penalty, row);
+    r.u = P.uniforms[row];
     r.greedy = (c.greedy != 0) || !(r.T > 0.0f);
     int h = 0;
     if (P.H_max > 0) {
@@ -788,7 +790,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     int32_t tok = -1;
     float prob = 0.0f;
     if (Zf > 0) {
-        const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+        const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
         uint64_t acc = 0, wtok = 0;
         tok = (int32_t)radix(
             [&](float x, uint32_t id, auto fn) {
@@ -827,7 +829,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 // pairwise pass (mass of final ids up to each id).  Returns false, before
 // writing anything, when tau does not exceed tcut (a key no value left out of
 // sv can reach).
-template <int NPL>
+template <int NPL, bool padded>
 __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const RowCfg& c, uint32_t ns,
                           uint32_t kmax, uint32_t tcut, llima_u32x4* sv, bool id_sorted,
                           FinShared& sh) {
@@ -847,17 +849,24 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
     uint64_t above[NPL], same[NPL];
 #pragma unroll
     for (int e = 0; e < NPL; ++e) { gt[e] = 0; eq[e] = 0; above[e] = 0; same[e] = 0; }
+    // every read first (one LDS latency), then the comparisons.  Entries past
+    // ns are zero (key 0, weight 0) when padded, and then need no bound check.
+    llima_u32x4 ov[PER];
+#pragma unroll
+    for (uint32_t jj = 0; jj < PER; ++jj) ov[jj] = sv[j0 + jj];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (uint32_t jj = 0; jj < PER; ++jj) {
-        const llima_u32x4 o = sv[j0 + jj];
-        const bool in = j0 + jj < ns;
+        const llima_u32x4 o = ov[jj];
+        const bool in = padded || j0 + jj < ns;
         const uint64_t wj = ((uint64_t)o.w << 32) | o.z;
 #pragma unroll
         for (int e = 0; e < NPL; ++e) {
-            gt[e] += in && o.x > key[e] ? 1u : 0u;
-            eq[e] += in && o.x == key[e] ? 1u : 0u;
-            above[e] += in && o.x > key[e] ? wj : 0ull;
-            same[e] += in && o.x == key[e] ? wj : 0ull;
+            const bool g = in && o.x > key[e], q = in && o.x == key[e];
+            gt[e] += g ? 1u : 0u;
+            eq[e] += q ? 1u : 0u;
+            above[e] += g ? wj : 0ull;
+            same[e] += q ? wj : 0ull;
         }
     }
 #pragma unroll
@@ -931,7 +940,7 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
         if (Zf == 0) {
             if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
         } else {
-            const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+            const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
 #pragma unroll
             for (int e = 0; e < NPL; ++e)
                 if (wave == 0 && wf[e] > 0 && upto[e] - wf[e] <= target && target < upto[e])
@@ -946,7 +955,7 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
         if (Zf == 0) {
             if (threadIdx.x == 0) write_result(P, row, -1, 0.0f);
         } else {
-            const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+            const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
             if (wave == 0) {
 #pragma unroll
                 for (int e = 0; e < NPL; ++e)
@@ -1163,7 +1172,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
             }
         }
         __syncthreads();
-        return fin_small<1>(P, row, c, nst, kmax, c.k > 0 ? gkey : 0u, sh.sv, false, sh);
+        return fin_small<1, false>(P, row, c, nst, kmax, c.k > 0 ? gkey : 0u, sh.sv, false, sh);
     }
     // more than 64 remain only when lowkey is tau (ties) or there is no top-k
 
@@ -1211,7 +1220,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     if (Zf == 0) {
         if (t == 0) write_result(P, row, -1, 0.0f);
     } else {
-        const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.uniforms[row]) * Zf) >> 32);
+        const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
         if (mysum > 0 && before <= target && target < before + mysum) {
             uint64_t acc = before;
             int jt = -1;
@@ -1282,10 +1291,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             }
         }
         __syncthreads();
-        auto count_id = [&](int32_t hv) {
-            if (hv < 0 || hv >= P.V) return;
-            const uint32_t h = bit_of((uint32_t)hv);
-            if (!((bm[h >> 5] >> (h & 31u)) & 1u)) return;
+        auto resolve = [&](int32_t hv) {               // hv passed the bitmap
             uint32_t lo = 0, hi = ns;
             while (lo < hi) {
                 const uint32_t mid = (lo + hi) >> 1;
@@ -1293,11 +1299,25 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             }
             if (lo < ns && sh.sv[lo].y == (uint32_t)hv) atomicAdd(&sh.hc[lo], 1u);
         };
+        // all bitmap reads first, then the (rare) hits
+        uint32_t bits[SMP_HBATCH];
+#pragma unroll
+        for (int b = 0; b < SMP_HBATCH; ++b) {
+            const int32_t hv = hid[b];
+            const bool ok = (int)t + b * LLIMA_WG < c.hlen && hv >= 0 && hv < P.V;
+            const uint32_t h = bit_of((uint32_t)hv);
+            bits[b] = ok ? (bm[h >> 5] >> (h & 31u)) & 1u : 0u;
+        }
 #pragma unroll
         for (int b = 0; b < SMP_HBATCH; ++b)
-            if ((int)t + b * LLIMA_WG < c.hlen) count_id(hid[b]);
+            if (bits[b]) resolve(hid[b]);
         const int32_t* hrow = P.hist + (size_t)row * P.H_max;
-        for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) count_id(hrow[i]);
+        for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) {
+            const int32_t hv = hrow[i];
+            if (hv < 0 || hv >= P.V) continue;
+            const uint32_t h = bit_of((uint32_t)hv);
+            if ((bm[h >> 5] >> (h & 31u)) & 1u) resolve(hv);
+        }
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -1338,8 +1358,8 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             tcut = kl > tcut ? kl : tcut;
         }
     }
-    return ns <= SMP_SMALL ? fin_small<1>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh)
-                           : fin_small<2>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh);
+    return ns <= SMP_SMALL ? fin_small<1, true>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh)
+                           : fin_small<2, true>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh);
 }
 
 // Candidates straight from the first-round loads: thread t holds the 8 slots
