@@ -44,8 +44,11 @@ __device__ __forceinline__ float key_f32(uint32_t k) {
 // exp(d), d <= 0: Cody-Waite reduction e^d = 2^n e^r with a degree-7 Taylor
 // polynomial for e^r, |r| <= ln2/2.  Only IEEE-exact operations (mul, rint,
 // fma, ldexp) so the result is reproducible bit for bit on the host.
-__device__ __forceinline__ float exp_neg(float d) {
-    if (!(d >= -26.0f)) return 0.0f;
+// Written with selects only (no early return): the finish kernels run it on
+// one wave per SIMD, where a branch costs more than the arithmetic it skips.
+__device__ __forceinline__ float exp_neg(float d0) {
+    const bool in = d0 >= -26.0f;                       // false for NaN
+    const float d = in ? d0 : -26.0f;
     const float kLog2e = 1.44269502162933349609375f;
     const float kLn2Hi = 0.693145751953125f;
     const float kLn2Lo = 1.428606765330187045e-06f;
@@ -60,7 +63,7 @@ __device__ __forceinline__ float exp_neg(float d) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    return in ? __builtin_ldexpf(p, (int)n) : 0.0f;
 }
 
 // An integral float in [0, 2^40) as uint64 (exact; by its bits).
@@ -73,11 +76,9 @@ __device__ __forceinline__ uint64_t f32_integral_to_u64(float f) {
 }
 
 __device__ __forceinline__ uint64_t weight(float x, float xmax) {
-    if (x == xmax) return LLIMA_W_ONE;
-    float d = x - xmax;
-    if (!(d >= -26.0f)) return 0;
-    float e = exp_neg(d);
-    return f32_integral_to_u64(__builtin_rintf(__builtin_ldexpf(e, 36)));
+    const float d = x - xmax;
+    const uint64_t w = f32_integral_to_u64(__builtin_rintf(__builtin_ldexpf(exp_neg(d), 36)));
+    return x == xmax ? LLIMA_W_ONE : (d >= -26.0f ? w : 0ull);
 }
 
 // rint(v * 2^32) clamped to [0, 2^32].

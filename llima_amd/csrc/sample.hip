@@ -12,8 +12,8 @@
 //   per-wave ballot search, and tests values against g only in the few lanes
 //   whose maximum reaches it.  Values >= g are written, with their ids and in
 //   id order, to the chunk's own workspace region behind a 16-byte header:
-//     top-k rows    g = the r-th largest of the 256 lane maxima (r ~ 16), a
-//                   lower bound of the chunk's r-th largest value;
+//     top-k rows    g = the largest of the four waves' r-th largest lane
+//                   maxima (r ~ 8): about 20-30 values pass it;
 //     other rows    g = chunk max - 27 T when values of zero weight cannot
 //                   matter, else every finite value;
 //     greedy rows   only the chunk's (maximum, first index) in the header.
@@ -82,6 +82,7 @@ struct SampleParams {
     int32_t lgs;         // log2 of S rounded up to a power of two (finish gather)
     int32_t vec_ok;
     int32_t lazy;        // penalties are applied by the finish (see llima_sample)
+    int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
 };
 
 struct RowCfg {
@@ -131,11 +132,12 @@ __device__ __forceinline__ bool zero_weight_irrelevant(const SampleParams& P, co
     return P.out_keep == nullptr || c.p < 1.0f || (c.m > 0.0f && frac32(c.m) > 0);
 }
 
-// Lane maxima ranked for the top-k chunk bound: enough that a chunk rarely
-// holds more of the row's top-k values than this.
-__device__ __forceinline__ uint32_t bound_rank(int k, int S) {
-    int r = (4 * k + S - 1) / S + 8;
-    r = r < 16 ? 16 : (r > 64 ? 64 : r);
+// Lane maxima ranked, per wave, for the top-k chunk bound: a wave (1024 fp32
+// or 2048 bf16 values) rarely holds this many of the row's top-k values (about
+// k / (4 S) on average).  Also used on the host for a broadcast top-k.
+__host__ __device__ inline uint32_t bound_rank(int k, int S) {
+    int r = (k + S - 1) / S + 6;
+    r = r < 8 ? 8 : (r > 64 ? 64 : r);
     return (uint32_t)(k < r ? k : r);
 }
 
@@ -176,35 +178,39 @@ __device__ __forceinline__ uint32_t pre_slots(const SampleParams& P) {
 // clamped, always-valid addresses and the out-of-row values masked in registers.
 // MASK: a grammar bitmask is given.  NaN values stay NaN here: every later use
 // is an ordered comparison or a max that ignores NaN, so a NaN is never selected.
-template <typename TL, bool VEC, bool MASK>
+// SC: chunks per workgroup (consecutive chunks of one row).  Chunk cc + 1 is
+// requested once chunk cc has arrived and before it is processed, so the
+// processing overlaps the next transfer (with every load of the grid issued at
+// once, each chunk completes only when the last of all requests does).
+template <typename TL, bool VEC, bool MASK, int SC>
 __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int EPL = 16 / sizeof(TL);       // values per 16-byte load
-    constexpr int NL = 4;                      // 16-byte loads per thread
-    constexpr int E = NL * EPL;                // values per thread
+    constexpr int NL = 4;                      // 16-byte loads per thread and chunk
+    constexpr int E = NL * EPL;                // values per thread and chunk
     constexpr int CHUNK = LLIMA_WG * E;
-    constexpr int CW = CHUNK / 2;              // history count words
+    constexpr int CW = SC * CHUNK / 2;         // history count words (the group)
     __shared__ __align__(16) uint32_t cnt[CW];
-    __shared__ uint32_t xa[LLIMA_WAVES];
-    __shared__ uint32_t xs[66];                    // staged lane maxima: count, keys, result
-    __shared__ uint32_t xc[NL][LLIMA_WAVES];
-    __shared__ uint64_t xg[LLIMA_WAVES];
+    __shared__ uint32_t xa[SC][LLIMA_WAVES];
+    __shared__ uint32_t xc[SC][NL][LLIMA_WAVES];
+    __shared__ uint64_t xg[SC][LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
-    uint32_t row, chunk;
-    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
+    const uint32_t G = ((uint32_t)P.S + SC - 1) / SC;   // chunk groups per row
+    uint32_t row, grp;
+    map_row_chunk(blockIdx.x, (uint32_t)P.B, G, &row, &grp);
     if (row >= (uint32_t)P.B) return;
     const int t = (int)threadIdx.x;
     const uint32_t lane = lane_id(), wave = wave_id();
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
-    const int c0 = (int)chunk * CHUNK;
-    const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
+    const int g0 = (int)grp * SC * CHUNK;                      // first id of the group
+    const int g1 = g0 + SC * CHUNK < V ? g0 + SC * CHUNK : V;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
     const int H = P.H_max;
     const bool eager = H > 0 && !P.lazy;
 
     // ---- 1. loads, in the order their data is used, all before the first
-    //         wait: history ids (rows penalised here), mask words, the chunk
+    //         wait: history ids (rows penalised here), mask words, the chunks
     int32_t hid[SMP_HBATCH];
     if (eager) {
         const int32_t* hrow = P.hist + (size_t)row * H;
@@ -215,38 +221,41 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t mword[NL];
-    if constexpr (MASK) {
+    uint32_t mword[SC][NL];
+    llima_u32x4 raw[SC][NL];
+    auto issue = [&](int cc) {                  // mask words and values of chunk cc
+        if constexpr (MASK) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+                const int i0 = g0 + cc * CHUNK + j * (LLIMA_WG * EPL) + t * EPL;
+                mword[cc][j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-            mword[j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
-        }
-    }
-    llima_u32x4 raw[NL];
+            const int i0 = g0 + cc * CHUNK + j * (LLIMA_WG * EPL) + t * EPL;
+            if constexpr (VEC) {
+                const int ia = i0 < V ? i0 : V - EPL;
+                raw[cc][j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+            } else {
+                uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-        if constexpr (VEC) {
-            const int ia = i0 < V ? i0 : V - EPL;
-            raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
-        } else {
-            uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int ia = i0 + e < V ? i0 + e : V - 1;
-                const float f = load_one<TL>(rowp, ia);
-                if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
-                else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+                for (int e = 0; e < EPL; ++e) {
+                    const int ia = i0 + e < V ? i0 + e : V - 1;
+                    const float f = load_one<TL>(rowp, ia);
+                    if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
+                    else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+                }
+                raw[cc][j] = llima_u32x4{w[0], w[1], w[2], w[3]};
             }
-            raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
         }
-    }
+    };
+    issue(0);
     __builtin_amdgcn_sched_barrier(0);
     const RowCfg c = load_cfg(P, row);
     const bool pen_here = eager && c.pen;
 
-    // ---- 2. history counts of the chunk (waits for the history ids only)
+    // ---- 2. history counts of the group (waits for the history ids only)
     if (pen_here) {
 #pragma unroll
         for (int i = t; i < CW / 4; i += LLIMA_WG) ((llima_u32x4*)cnt)[i] = llima_u32x4{0, 0, 0, 0};
@@ -254,223 +263,221 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
 #pragma unroll
         for (int b = 0; b < SMP_HBATCH; ++b) {
             const int32_t id = hid[b];
-            if (t + b * LLIMA_WG < c.hlen && id >= c0 && id < c1) {
-                const uint32_t off = (uint32_t)(id - c0);
+            if (t + b * LLIMA_WG < c.hlen && id >= g0 && id < g1) {
+                const uint32_t off = (uint32_t)(id - g0);
                 atomicAdd(&cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
         }
         const int32_t* hrow = P.hist + (size_t)row * H;
         for (int j = t + SMP_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
             const int32_t id = hrow[j];
-            if (id >= c0 && id < c1) {
-                const uint32_t off = (uint32_t)(id - c0);
+            if (id >= g0 && id < g1) {
+                const uint32_t off = (uint32_t)(id - g0);
                 atomicAdd(&cnt[off >> 1], 1u << ((off & 1u) * 16u));
             }
         }
         __syncthreads();
     }
+    const uint32_t rank = P.cfg.top_k_rows ? bound_rank(c.k, P.S) : (uint32_t)P.rank;
 
-    // ---- 3. values: masked -> -inf, history values penalised (here), values
-    //         past the row -> -inf (the last chunk only)
-    float v[E];
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-        float xs[EPL];
-        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-        if constexpr (sizeof(TL) == 4) {
+    for (int cc = 0; cc < SC; ++cc) {
+        const uint32_t chunk = grp * SC + (uint32_t)cc;
+        if (chunk >= (uint32_t)P.S) break;
+        const int c0 = g0 + cc * CHUNK;
+        const int c1 = c0 + CHUNK < V ? c0 + CHUNK : V;
+
+        // ---- 3. values: masked -> -inf, history values penalised (here),
+        //         values past the row -> -inf (the last chunk only)
+        float v[E];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xs[e] = __uint_as_float(w4[e]);
-        } else {
+        for (int j = 0; j < NL; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+            float xv[EPL];
+            const uint32_t w4[4] = {raw[cc][j].x, raw[cc][j].y, raw[cc][j].z, raw[cc][j].w};
+            if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                xs[2 * e] = __uint_as_float(w4[e] << 16);
-                xs[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-            }
-        }
-        if constexpr (MASK) {
-            const uint32_t mb = mword[j] >> (i0 & 31);
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) xs[e] = ((mb >> e) & 1u) ? xs[e] : NEG_INF;
-        }
-        if (pen_here) {
-            uint32_t cw[EPL / 2];
-            const uint32_t* cp = cnt + ((i0 - c0) >> 1);
-            if constexpr (EPL == 4) {
-                const uint2 w2 = *(const uint2*)cp;
-                cw[0] = w2.x; cw[1] = w2.y;
+                for (int e = 0; e < 4; ++e) xv[e] = __uint_as_float(w4[e]);
             } else {
-                const llima_u32x4 wq = *(const llima_u32x4*)cp;
-                cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
-            }
 #pragma unroll
-            for (int h = 0; h < EPL / 2; ++h) {
-                if (cw[h]) {
-                    const uint32_t lo = cw[h] & 0xFFFFu, hi = cw[h] >> 16;
-                    if (lo) xs[2 * h] = penalize(xs[2 * h], lo, c);
-                    if (hi) xs[2 * h + 1] = penalize(xs[2 * h + 1], hi, c);
+                for (int e = 0; e < 4; ++e) {
+                    xv[2 * e] = __uint_as_float(w4[e] << 16);
+                    xv[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
                 }
             }
-        }
+            if constexpr (MASK) {
+                const uint32_t mb = mword[cc][j] >> (i0 & 31);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) v[j * EPL + e] = xs[e];
-    }
-    if (c1 - c0 < CHUNK) {
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                if (i0 + e >= c1) v[j * EPL + e] = NEG_INF;
-        }
-    }
-
-    uint64_t* reg = region_of(P, row, chunk);
-    if (c.greedy) {
-        // ---- argmax: first index of the maximum (values visited in index order)
-        float best = NEG_INF;
-        uint32_t bidx = 0;
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
-        }
-        const uint64_t kk = best > NEG_INF ? (((uint64_t)f32_key(best) << 32) | (uint32_t)~bidx) : 0ull;
-        const uint64_t wk = wave_max_u64(kk);
-        if (lane == 0) xg[wave] = wk;
-        __syncthreads();
-        if (t == 0) {
-            uint64_t g = 0;
-#pragma unroll
-            for (int w = 0; w < LLIMA_WAVES; ++w) g = xg[w] > g ? xg[w] : g;
-            *(llima_u32x4*)reg = llima_u32x4{0u, __float_as_uint(NEG_INF), (uint32_t)g,
-                                             (uint32_t)(g >> 32)};
-        }
-        return;
-    }
-
-    // ---- 4. lane maxima (a NaN is ignored by the max) and the chunk bound g
-    float lm = v[0];
-#pragma unroll
-    for (int e = 1; e < E; ++e) lm = __builtin_fmaxf(lm, v[e]);
-    const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
-    float g = NEG_INF;
-    if (c.k > 0) {
-        // r lanes of one wave hold maxima >= that wave's r-th largest lane
-        // maximum (low key bits cleared: a lower value), so the chunk's r-th
-        // largest value is at least the largest of the four.
-        // Then the lane maxima at or above that (they include the chunk's r
-        // largest) are staged in LDS and, when at most 64, one wave finds the
-        // chunk's r-th largest lane maximum itself: about r values pass it.
-        const uint32_t r = bound_rank(c.k, P.S);
-        const uint32_t bw = wave_rth_largest(lk, r, SMP_BOUND_LOWBIT);
-        if (lane == 0) xa[wave] = bw;
-        if (t == 0) xs[0] = 0;
-        __syncthreads();
-        uint32_t gk = 0;
-#pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) gk = xa[w] > gk ? xa[w] : gk;
-        if (gk) {
-            if (lk >= gk) {
-                const uint32_t o = atomicAdd(&xs[0], 1u);
-                if (o < 64u) xs[1 + o] = lk;
+                for (int e = 0; e < EPL; ++e) xv[e] = ((mb >> e) & 1u) ? xv[e] : NEG_INF;
             }
-            __syncthreads();
-            const uint32_t ns = xs[0];
-            if (ns <= 64u) {
-                if (wave == 0) {
-                    const uint32_t key = lane < ns ? xs[1 + lane] : 0u;
-                    const uint32_t g2k = wave_rth_largest(key, r, SMP_BOUND_LOWBIT);
-                    if (lane == 0) xs[65] = g2k;
+            if (pen_here) {
+                uint32_t cw[EPL / 2];
+                const uint32_t* cp = cnt + ((i0 - g0) >> 1);
+                if constexpr (EPL == 4) {
+                    const uint2 w2 = *(const uint2*)cp;
+                    cw[0] = w2.x; cw[1] = w2.y;
+                } else {
+                    const llima_u32x4 wq = *(const llima_u32x4*)cp;
+                    cw[0] = wq.x; cw[1] = wq.y; cw[2] = wq.z; cw[3] = wq.w;
                 }
-                __syncthreads();
-                const uint32_t g2k = xs[65];
-                gk = g2k > gk ? g2k : gk;
+#pragma unroll
+                for (int h = 0; h < EPL / 2; ++h) {
+                    if (cw[h]) {
+                        const uint32_t lo = cw[h] & 0xFFFFu, hi = cw[h] >> 16;
+                        if (lo) xv[2 * h] = penalize(xv[2 * h], lo, c);
+                        if (hi) xv[2 * h + 1] = penalize(xv[2 * h + 1], hi, c);
+                    }
+                }
             }
-            g = key_f32(gk);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) v[j * EPL + e] = xv[e];
         }
-    } else if (zero_weight_irrelevant(P, c)) {
-        // values this far below the chunk maximum have weight 0 (checked exactly
-        // by the finish against the row maximum)
-        const uint32_t wm = wave_max_u32(lk);
-        if (lane == 0) xa[wave] = wm;
-        __syncthreads();
-        uint32_t mk = 0;
+        if (c1 - c0 < CHUNK) {
 #pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) mk = xa[w] > mk ? xa[w] : mk;
-        if (mk) {
-            const float gm = key_f32(mk) - 27.0f * c.T;
-            g = gm == gm ? gm : NEG_INF;
-        }
-    }
-    // the smallest finite float stands for -inf: -inf and NaN never pass
-    const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
-
-    // ---- 5. write the values >= g in id order: per load j, lane counts, wave
-    //         scans (two counts packed per u32), then the waves in order.  Only
-    //         lanes whose maximum reaches g test their values.
-    uint32_t pm[NL];
-#pragma unroll
-    for (int j = 0; j < NL; ++j) pm[j] = 0;
-    if (lm >= g2) {
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            uint32_t m = 0;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) m |= v[j * EPL + e] >= g2 ? (1u << e) : 0u;
-            pm[j] = m;
-        }
-    }
-    const uint32_t a01 = (uint32_t)__popc(pm[0]) | ((uint32_t)__popc(pm[1]) << 16);
-    const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
-    const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
-    const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
-    if (lane == 0) {
-        xc[0][wave] = t01 & 0xFFFFu; xc[1][wave] = t01 >> 16;
-        xc[2][wave] = t23 & 0xFFFFu; xc[3][wave] = t23 >> 16;
-    }
-    __syncthreads();
-    uint32_t base[NL], total = 0;
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        uint32_t before = 0;
-#pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) {
-            const uint32_t n = xc[j][w];
-            before += (uint32_t)w < wave ? n : 0u;
-        }
-        base[j] = total + before;
-#pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) total += xc[j][w];
-    }
-    const bool fits = total <= SMP_CAP;
-    if (fits && lm >= g2) {
-        const uint32_t e01 = i01 - a01, e23 = i23 - a23;
-        const uint32_t lx[NL] = {e01 & 0xFFFFu, e01 >> 16, e23 & 0xFFFFu, e23 >> 16};
-        uint64_t* dst = reg + SMP_HDR;
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            if (pm[j]) {
+            for (int j = 0; j < NL; ++j) {
                 const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-                uint32_t o = base[j] + lx[j];
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    if ((pm[j] >> e) & 1u) {
-                        dst[o] = ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
-                        ++o;
+                for (int e = 0; e < EPL; ++e)
+                    if (i0 + e >= c1) v[j * EPL + e] = NEG_INF;
+            }
+        }
+        // lane maximum (a NaN is ignored by the max): it reads every value, so
+        // chunk cc is in when it is done; then the next chunk is requested
+        // before this one is worked on (unconditionally: addresses past the row
+        // are clamped, and loads behind a branch make the next use wait)
+        float lm = v[0];
+#pragma unroll
+        for (int e = 1; e < E; ++e) lm = __builtin_fmaxf(lm, v[e]);
+        if (cc + 1 < SC) {
+            asm volatile("" ::"v"(lm) : "memory");   // lm computed here, loads stay below
+            issue(cc + 1);
+        }
+
+        uint64_t* reg = region_of(P, row, chunk);
+        if (c.greedy) {
+            // ---- argmax: first index of the maximum (values visited in index order)
+            float best = NEG_INF;
+            uint32_t bidx = 0;
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+                const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
+            }
+            const uint64_t kk = best > NEG_INF ? (((uint64_t)f32_key(best) << 32) | (uint32_t)~bidx) : 0ull;
+            const uint64_t wk = wave_max_u64(kk);
+            if (lane == 0) xg[cc][wave] = wk;
+            __syncthreads();
+            if (t == 0) {
+                uint64_t g = 0;
+#pragma unroll
+                for (int w = 0; w < LLIMA_WAVES; ++w) g = xg[cc][w] > g ? xg[cc][w] : g;
+                *(llima_u32x4*)reg = llima_u32x4{0u, __float_as_uint(NEG_INF), (uint32_t)g,
+                                                 (uint32_t)(g >> 32)};
+            }
+            continue;
+        }
+
+        // ---- 4. the chunk bound g
+        const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
+        float g = NEG_INF;
+        if (c.k > 0) {
+            // g = the largest of the four waves' r-th largest lane maxima (low
+            // key bits cleared: a lower value).  Any g is correct, since every
+            // value >= g is written and the finish checks that its top-k
+            // boundary lies above g; a smaller g costs candidates, a larger
+            // one the finish's fast path (when one wave holds r of the row's
+            // top-k values).  One wave-level search, no second pass: this runs
+            // after the chunk's data arrived, on the kernel's critical path.
+            const uint32_t bw = wave_rth_largest(lk, rank, SMP_BOUND_LOWBIT);
+            if (lane == 0) xa[cc][wave] = bw;
+            __syncthreads();
+            uint32_t gk = 0;
+#pragma unroll
+            for (int w = 0; w < LLIMA_WAVES; ++w) gk = xa[cc][w] > gk ? xa[cc][w] : gk;
+            if (gk) g = key_f32(gk);
+        } else if (zero_weight_irrelevant(P, c)) {
+            // values this far below the chunk maximum have weight 0 (checked
+            // exactly by the finish against the row maximum)
+            const uint32_t wm = wave_max_u32(lk);
+            if (lane == 0) xa[cc][wave] = wm;
+            __syncthreads();
+            uint32_t mk = 0;
+#pragma unroll
+            for (int w = 0; w < LLIMA_WAVES; ++w) mk = xa[cc][w] > mk ? xa[cc][w] : mk;
+            if (mk) {
+                const float gm = key_f32(mk) - 27.0f * c.T;
+                g = gm == gm ? gm : NEG_INF;
+            }
+        }
+        // the smallest finite float stands for -inf: -inf and NaN never pass
+        const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
+
+        // ---- 5. write the values >= g in id order: per load j, lane counts,
+        //         wave scans (two counts packed per u32), then the waves in
+        //         order.  Only lanes whose maximum reaches g test their values.
+        uint32_t pm[NL];
+#pragma unroll
+        for (int j = 0; j < NL; ++j) pm[j] = 0;
+        if (lm >= g2) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) m |= v[j * EPL + e] >= g2 ? (1u << e) : 0u;
+                pm[j] = m;
+            }
+        }
+        const uint32_t a01 = (uint32_t)__popc(pm[0]) | ((uint32_t)__popc(pm[1]) << 16);
+        const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
+        const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
+        const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
+        if (lane == 0) {
+            xc[cc][0][wave] = t01 & 0xFFFFu; xc[cc][1][wave] = t01 >> 16;
+            xc[cc][2][wave] = t23 & 0xFFFFu; xc[cc][3][wave] = t23 >> 16;
+        }
+        __syncthreads();
+        uint32_t base[NL], total = 0;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            uint32_t before = 0;
+#pragma unroll
+            for (int w = 0; w < LLIMA_WAVES; ++w) {
+                const uint32_t n = xc[cc][j][w];
+                before += (uint32_t)w < wave ? n : 0u;
+            }
+            base[j] = total + before;
+#pragma unroll
+            for (int w = 0; w < LLIMA_WAVES; ++w) total += xc[cc][j][w];
+        }
+        const bool fits = total <= SMP_CAP;
+        if (fits && lm >= g2) {
+            const uint32_t e01 = i01 - a01, e23 = i23 - a23;
+            const uint32_t lx[NL] = {e01 & 0xFFFFu, e01 >> 16, e23 & 0xFFFFu, e23 >> 16};
+            uint64_t* dst = reg + SMP_HDR;
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+                if (pm[j]) {
+                    const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+                    uint32_t o = base[j] + lx[j];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        if ((pm[j] >> e) & 1u) {
+                            dst[o] = ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
+                            ++o;
+                        }
                     }
                 }
             }
         }
+        if (fits) {
+            const uint32_t pre = pre_slots(P);
+            for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
+        }
+        if (t == 0)
+            *(uint64_t*)reg = ((uint64_t)__float_as_uint(g) << 32) | (fits ? total : (HF_OVERFLOW << 16));
     }
-    if (fits) {
-        const uint32_t pre = pre_slots(P);
-        for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
-    }
-    if (t == 0)
-        *(uint64_t*)reg = ((uint64_t)__float_as_uint(g) << 32) | (fits ? total : (HF_OVERFLOW << 16));
 }
 
 // ================================================================== finish
@@ -485,9 +492,9 @@ struct FinShared {
     } u;
     uint32_t ccount[SMP_MAX_S];
     uint32_t coff[SMP_MAX_S];
-    uint32_t hcnt[2][256];
+    uint32_t hcnt[3][256 + 64];                      // + a spare bin per lane
     uint64_t hmass[2][256];
-    llima_u32x4 sv[2 * SMP_SMALL];
+    llima_u32x4 sv[2 * SMP_SMALL + 64];              // + a spare slot per lane
     llima_u32x4 sv2[LLIMA_WAVES][2 * SMP_SMALL];
     uint32_t pc[2][LLIMA_WAVES][64];
     uint64_t part[2][LLIMA_WAVES][64];
@@ -498,8 +505,7 @@ struct FinShared {
     uint64_t sel64[2];
     uint32_t hflags, hgkey, hn;
     uint64_t hgreedy;
-    uint32_t hk[2 * SMP_SMALL];                      // survivor ids + 1 (lazy penalties)
-    uint32_t hc[2 * SMP_SMALL];                      // their history occurrences
+    uint32_t hc[LLIMA_WG];                           // survivors' history occurrences
     BlockScratch bs;
 };
 
@@ -1271,61 +1277,82 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const uint32_t i = (uint32_t)e * 64u + lane;
-        const llima_u32x4 me = i < ns ? sh.sv[i] : llima_u32x4{0u, 0u, 0u, 0u};
+        const llima_u32x4 me = sh.sv[i];                // sv holds 2 * SMP_SMALL + 64 slots
         x[e] = i < ns ? key_f32(me.x) : -__builtin_inff();
-        id[e] = me.y;
+        id[e] = i < ns ? me.y : 0u;
     }
     if (P.lazy && c.pen) {
-        // a hashed bitmap of the survivor ids (sh.u.hash.key, zeroed by the
-        // caller) rules out almost every history id with one LDS read; a hit
-        // is resolved by binary search among the survivors (id order)
-        uint32_t* bm = sh.u.hash.key;
-        auto bit_of = [](uint32_t v) { return (v * 2654435761u) >> 15; };   // 2^17 bits
+        // an LDS hash of the survivor ids in buckets of 4 slots (sh.u.hash.key:
+        // id + 1, zeroed by the caller; sh.u.hash.cnt: the survivor's index).
+        // A bucket spills into the next one only when full, so one 16-byte
+        // read settles almost every history id: a free slot without a match
+        // means absent.
+        uint32_t* hkey = sh.u.hash.key;
+        uint32_t* hidx = sh.u.hash.cnt;
+        const llima_u32x4* hb4 = (const llima_u32x4*)hkey;
+        auto bucket_of = [](uint32_t v) { return (v * 2654435761u) >> (32 - 10); };   // SMP_HASH / 4
         if (wave == 0) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                if ((uint32_t)e * 64u + lane < ns) {
-                    const uint32_t h = bit_of(id[e]);
-                    atomicOr(&bm[h >> 5], 1u << (h & 31u));
+                const uint32_t i = (uint32_t)e * 64u + lane;
+                if (i < ns) {
+                    uint32_t b = bucket_of(id[e]);
+                    for (;;) {
+                        uint32_t s = 0;
+                        while (s < 4u && atomicCAS(&hkey[4u * b + s], 0u, id[e] + 1u) != 0u) ++s;
+                        if (s < 4u) { hidx[4u * b + s] = i; break; }
+                        b = (b + 1u) & (SMP_HASH / 4u - 1u);
+                    }
                 }
             }
         }
         __syncthreads();
-        auto resolve = [&](int32_t hv) {               // hv passed the bitmap
-            uint32_t lo = 0, hi = ns;
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (sh.sv[mid].y < (uint32_t)hv) lo = mid + 1; else hi = mid;
+        auto probe = [&](uint32_t v, uint32_t b, llima_u32x4 q) {   // v = id + 1, q = bucket b
+            for (;;) {
+                const int s = q.x == v ? 0 : q.y == v ? 1 : q.z == v ? 2 : q.w == v ? 3 : -1;
+                if (s >= 0) { atomicAdd(&sh.hc[hidx[4u * b + (uint32_t)s]], 1u); return; }
+                if (!(q.x && q.y && q.z && q.w)) return;
+                b = (b + 1u) & (SMP_HASH / 4u - 1u);
+                q = hb4[b];
             }
-            if (lo < ns && sh.sv[lo].y == (uint32_t)hv) atomicAdd(&sh.hc[lo], 1u);
         };
-        // all bitmap reads first, then the (rare) hits
-        uint32_t bits[SMP_HBATCH];
+        // all bucket reads first, then the (rare) hits and full buckets
+        uint32_t hb[SMP_HBATCH];
+        llima_u32x4 hq[SMP_HBATCH];
+#pragma unroll
+        for (int b = 0; b < SMP_HBATCH; ++b) {
+            hb[b] = bucket_of((uint32_t)hid[b]);
+            hq[b] = hb4[hb[b]];
+        }
+        uint32_t need = 0;
 #pragma unroll
         for (int b = 0; b < SMP_HBATCH; ++b) {
             const int32_t hv = hid[b];
-            const bool ok = (int)t + b * LLIMA_WG < c.hlen && hv >= 0 && hv < P.V;
-            const uint32_t h = bit_of((uint32_t)hv);
-            bits[b] = ok ? (bm[h >> 5] >> (h & 31u)) & 1u : 0u;
+            const bool ok = ((int)t + b * LLIMA_WG < c.hlen) & (hv >= 0) & (hv < P.V);
+            const uint32_t v = (uint32_t)hv + 1u;
+            const llima_u32x4 q = hq[b];
+            const bool m = (q.x == v) | (q.y == v) | (q.z == v) | (q.w == v);
+            const bool full = (q.x != 0u) & (q.y != 0u) & (q.z != 0u) & (q.w != 0u);
+            need |= (ok & (m | full)) ? 1u << b : 0u;
         }
+        if (need) {
 #pragma unroll
-        for (int b = 0; b < SMP_HBATCH; ++b)
-            if (bits[b]) resolve(hid[b]);
+            for (int b = 0; b < SMP_HBATCH; ++b)
+                if ((need >> b) & 1u) probe((uint32_t)hid[b] + 1u, hb[b], hq[b]);
+        }
         const int32_t* hrow = P.hist + (size_t)row * P.H_max;
         for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) {
             const int32_t hv = hrow[i];
             if (hv < 0 || hv >= P.V) continue;
-            const uint32_t h = bit_of((uint32_t)hv);
-            if ((bm[h >> 5] >> (h & 31u)) & 1u) resolve(hv);
+            const uint32_t b = bucket_of((uint32_t)hv);
+            probe((uint32_t)hv + 1u, b, hb4[b]);
         }
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const uint32_t i = (uint32_t)e * 64u + lane;
-            if (i < ns) {
-                const uint32_t cn = sh.hc[i];
-                if (cn) x[e] = penalize(x[e], cn, c);
-            }
+            const uint32_t cn = sh.hc[(uint32_t)e * 64u + lane];    // 0 past ns
+            const float xp = penalize(x[e], cn, c);
+            x[e] = cn ? xp : x[e];
         }
     }
     // every wave: temperature, keys and weights of the survivors -> its own
@@ -1340,7 +1367,8 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
     kmax = wave_max_u32(kmax);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-        const uint64_t w = key[e] ? weight(key_f32(key[e]), key_f32(kmax)) : 0ull;
+        const uint64_t w0 = weight(key_f32(key[e]), key_f32(kmax));
+        const uint64_t w = key[e] ? w0 : 0ull;
         sh.sv2[wave][(uint32_t)e * 64u + lane] = llima_u32x4{key[e], id[e], (uint32_t)w, (uint32_t)(w >> 32)};
     }
     __builtin_amdgcn_wave_barrier();                 // the wave's LDS writes precede its reads
@@ -1397,25 +1425,45 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                                   : kk < 2u * SMP_SMALL ? min(32u, 2u * SMP_SMALL - kk) : 0u;
             uint32_t rem = min(N, (uint32_t)c.k + margin), above_all = 0;
             lowkey = d.prefix;
-            int buf = 0;
+            // round r counts into hcnt[r % 3] (rounds 0 and 1 zeroed by the
+            // caller); after its barrier every wave scans all 256 bins itself
+            // and zeroes hcnt[(r + 2) % 3], which every wave has finished
+            // reading (round r - 1) and nobody counts into before round r + 2
+            uint32_t buf = 0;
             while (d.top >= 0) {
                 const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
                 const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
                 uint32_t* hc = sh.hcnt[buf];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (kr[j] && (kr[j] & d.pmask) == d.prefix) atomicAdd(&hc[(kr[j] >> lo) & bmask], 1u);
+                for (int j = 0; j < 8; ++j) {
+                    const bool in = (kr[j] != 0u) & ((kr[j] & d.pmask) == d.prefix);
+                    atomicAdd(&hc[in ? (kr[j] >> lo) & bmask : 256u + lane_id()], 1u);
+                }
                 __syncthreads();
-                const uint32_t bin = 255u - t;                 // thread 0 <-> top bin
-                const uint32_t cn = hc[bin];
-                sh.hcnt[buf ^ 1][t] = 0;
-                const uint32_t inc = wave_incl_scan_u32(cn);
-                const uint32_t ab = (uint32_t)wg_prefix_u64(inc, cn, sh.r64[0]);
-                if (ab < rem && ab + cn >= rem) { sh.sel[0] = bin; sh.sel[1] = ab; sh.sel[2] = cn; }
-                __syncthreads();
-                const uint32_t sb = sh.sel[0], sab = sh.sel[1], scn = sh.sel[2];
-                hc[t] = 0;
-                buf ^= 1;
+                // lane l: bins 255 - 4l down to 252 - 4l (.w .z .y .x)
+                const llima_u32x4 c4 = ((const llima_u32x4*)hc)[63u - lane_id()];
+                const uint32_t nxt = buf == 0u ? 2u : buf - 1u;
+                sh.hcnt[nxt][t] = 0;
+                const uint32_t s4 = c4.x + c4.y + c4.z + c4.w;
+                uint32_t ab = wave_incl_scan_u32(s4) - s4;
+                const uint32_t top = 255u - 4u * lane_id();
+                const uint32_t cs[4] = {c4.w, c4.z, c4.y, c4.x};
+                uint32_t mb = 0, mab = 0, mcn = 0;
+                bool hit = false;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool h = ab < rem && ab + cs[i] >= rem;
+                    mb = h ? top - (uint32_t)i : mb;
+                    mab = h ? ab : mab;
+                    mcn = h ? cs[i] : mcn;
+                    hit = hit || h;
+                    ab += cs[i];
+                }
+                const uint64_t hm = ballot(hit);
+                if (hm == 0) return false;               // cannot happen: the bins hold rem
+                const uint32_t L = (uint32_t)__builtin_ffsll((long long)hm) - 1u;
+                const uint32_t sb = readlane(mb, L), sab = readlane(mab, L), scn = readlane(mcn, L);
+                buf = buf == 2u ? 0u : buf + 1u;
                 d.prefix |= sb << lo;
                 d.pmask |= bmask << lo;
                 d.top = lo - 1;
@@ -1424,7 +1472,6 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                 lowkey = d.prefix;
                 if (above_all + scn <= 2 * SMP_SMALL) break;
             }
-            __syncthreads();
         }
     } else if (gkey) {
         // without top-k every skipped value must have weight 0 (and not matter)
@@ -1434,18 +1481,28 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
     uint32_t ns = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ns += kr[j] && kr[j] >= lowkey ? 1u : 0u;
-    uint32_t nst;
-    const uint32_t so = block_excl_scan_u32(ns, &nst, sh.bs);
+    // exclusive scan of the counts over the workgroup (sh.bs.w32 is not
+    // written again before the barrier below)
+    const uint32_t inc = wave_incl_scan_u32(ns);
+    const uint32_t wave = wave_id();
+    if (lane_id() == 63) sh.bs.w32[wave] = inc;
+    __syncthreads();
+    uint32_t nst = 0, before = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) {
+        const uint32_t n = sh.bs.w32[w];
+        before += (uint32_t)w < wave ? n : 0u;
+        nst += n;
+    }
     if (nst > 2 * SMP_SMALL) return false;
-    uint32_t o = so;
+    uint32_t o = before + inc - ns;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        if (kr[j] && kr[j] >= lowkey) {
-            sh.sv[o] = llima_u32x4{kr[j], idv[j], 0u, 0u};
-            ++o;
-        }
+        const bool in = (kr[j] != 0u) & (kr[j] >= lowkey);
+        sh.sv[in ? o : 2u * SMP_SMALL + lane_id()] = llima_u32x4{kr[j], idv[j], 0u, 0u};
+        o += in ? 1u : 0u;
     }
-    if (t < 2 * SMP_SMALL) { sh.hk[t] = 0; sh.hc[t] = 0; }
+    sh.hc[t] = 0;
     __syncthreads();
     return fin_survivors(P, row, c, nst, lowkey, gkey, hid, sh);
 }
@@ -1470,20 +1527,27 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         llima_u32x4 q[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[i] = ((const llima_u32x4*)reg)[i];
+        // issued on every row (from the workspace when unused): loads behind a
+        // branch would make the first use of q wait for them as well
         int32_t hid[SMP_HBATCH];
-        if (P.lazy && c.pen) {
-            const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+        {
+            const bool lp = P.lazy && c.pen;
+            const int32_t* hrow = lp ? P.hist + (size_t)row * P.H_max : (const int32_t*)P.ws;
+            const int hl = lp ? c.hlen : LLIMA_WG * SMP_HBATCH;
 #pragma unroll
             for (int b = 0; b < SMP_HBATCH; ++b) {
                 const int j = (int)t + b * LLIMA_WG;
-                hid[b] = hrow[j < c.hlen ? j : c.hlen - 1];
+                hid[b] = hrow[j < hl ? j : hl - 1];
             }
         }
 
         // ---- 2. this thread's slots as candidates (raw keys; padding and the
         //         header are none) and the header facts, reduced over the row
+        // (selects and bitwise logic throughout: one wave per SIMD runs this,
+        // so every branch is paid in full)
         const uint32_t pre = pre_slots(P);
-        const bool hdr = mine && pt == 0;
+        const bool hdr = mine & (pt == 0u);
+        const bool live = mine & !c.greedy;
         uint32_t kr[8], idv[8];
         uint32_t kmx = 0, nkmn = 0, n = 0;
 #pragma unroll
@@ -1491,30 +1555,24 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t hi = h ? q[i].w : q[i].y, lo = h ? q[i].z : q[i].x;
-                const bool valid = mine && !c.greedy && !(hdr && i == 0 && h == 0) &&
-                                   hi != (uint32_t)(SMP_SENTINEL >> 32);
+                const bool valid = live & (hi != (uint32_t)(SMP_SENTINEL >> 32)) & ((i | h) != 0 || !hdr);
                 const uint32_t k = valid ? f32_key(__uint_as_float(hi)) : 0u;
                 kr[2 * i + h] = k;
                 idv[2 * i + h] = lo;
                 kmx = k > kmx ? k : kmx;
-                nkmn = k && ~k > nkmn ? ~k : nkmn;
+                const uint32_t nk = k ? ~k : 0u;
+                nkmn = nk > nkmn ? nk : nkmn;
                 n += k ? 1u : 0u;
             }
         }
-        uint32_t ovf = 0, gk = 0;
-        uint64_t gr = 0;
-        if (hdr) {
-            const uint32_t flags = q[0].x >> 16;
-            const uint32_t count = (flags & HF_OVERFLOW) ? 0u : (q[0].x & 0xFFFFu);
-            ovf = (flags & HF_OVERFLOW) ? 2u : (SMP_HDR + count > pre ? 1u : 0u);
-            const float g = __uint_as_float(q[0].y);
-            if (!c.greedy && g > -__builtin_inff()) {
-                const float gt = g / c.T;
-                gk = gt == gt ? f32_key(gt) : 0xFFFFFFFFu;
-            }
-            gr = ((uint64_t)q[0].w << 32) | q[0].z;
-            sh.ccount[ch] = count;
-        }
+        const uint32_t flags = q[0].x >> 16;
+        const uint32_t count = (flags & HF_OVERFLOW) ? 0u : (q[0].x & 0xFFFFu);
+        const uint32_t ovf = !hdr ? 0u : (flags & HF_OVERFLOW) ? 2u : (SMP_HDR + count > pre ? 1u : 0u);
+        const float g0 = __uint_as_float(q[0].y);
+        const float gt0 = g0 / c.T;
+        const uint32_t gk = (hdr & !c.greedy & (g0 > -__builtin_inff())) ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
+        const uint64_t gr = hdr ? ((uint64_t)q[0].w << 32) | q[0].z : 0ull;
+        if (hdr) sh.ccount[ch] = count;
         {
             const uint32_t a = wave_max_u32(kmx), b = wave_max_u32(nkmn), s2 = wave_sum_u32(n);
             const uint32_t o2 = wave_max_u32(ovf), g2 = wave_max_u32(gk);
@@ -1617,15 +1675,18 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 // ================================================================== host side
 static int chunk_values(int dtype) { return dtype == LLIMA_F32 ? 4096 : 8192; }
 
+#define SMP_SWEEP_SC 1                             // chunks per sweep workgroup
+
 template <typename TL>
 static void launch_sweep(const SampleParams& P, hipStream_t st) {
-    const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
+    constexpr int SC = SMP_SWEEP_SC;
+    const dim3 g((uint32_t)P.B * (uint32_t)((P.S + SC - 1) / SC)), b(LLIMA_WG);
     if (P.bitmask) {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, false, true>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true, SC>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, true, SC>), g, b, 0, st, P);
     } else {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, false, false>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false, SC>), g, b, 0, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, false, SC>), g, b, 0, st, P);
     }
 }
 
@@ -1682,6 +1743,10 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     int lgs = 0;
     while ((1 << lgs) < P.S && lgs < 8) ++lgs;
     P.lgs = lgs;
+    {
+        const int k = cfg->top_k;
+        P.rank = (k > 0 && k < V) ? (int32_t)bound_rank(k, P.S) : 0;
+    }
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
     P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0) &&
                (V % (int32_t)(16 / esz) == 0);

@@ -219,6 +219,44 @@ def test_sample_per_row_configs(gpu, oracle):
     _sample_both(gpu, oracle, x, u, None, history=hist, cfg_rows=rows)
 
 
+def test_sample_lazy_penalty_hits(gpu, oracle):
+    """Penalties applied to the finish's survivors only (repetition >= 1,
+    presence and frequency >= 0, broadcast top-k): history ids that are
+    survivors, hot ids repeated hundreds of times, and survivors that share one
+    bucket of the finish's 4-slot id hash (1024 buckets, Fibonacci hashing)."""
+    _say("sample lazy penalty hits")
+    rng = np.random.default_rng(77)
+    B, V, H = 6, 128256, 2048
+    x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(4.0)).astype(np.float32)
+    ids = np.arange(V, dtype=np.uint64)
+    bucket = (((ids * 2654435761) & 0xFFFFFFFF) >> 22).astype(np.int64)
+    hist = rng.integers(0, V, size=(B, H)).astype(np.int32)
+    # row 0: 14 survivors in one bucket (chains into the next buckets), each in the history
+    same = np.flatnonzero(bucket == bucket[12345])[:14]
+    x[0, same] = np.float32(18.0) + np.arange(14, dtype=np.float32) * np.float32(0.25)
+    hist[0, :14 * 20] = np.repeat(same, 20)
+    # row 1: the history is the row's 60 largest values, repeated
+    top = np.argsort(-x[1])[:60]
+    hist[1] = np.resize(top, H)
+    # row 2: the row maximum repeated 2000 times
+    hist[2, :2000] = int(np.argmax(x[2]))
+    # row 3: two buckets' worth of survivors, counts 1..n
+    b2 = np.flatnonzero(bucket == bucket[999])[:9]
+    x[3, b2] = np.float32(17.0) + np.arange(9, dtype=np.float32) * np.float32(0.1)
+    hist[3, :45] = np.concatenate([np.full(i + 1, v) for i, v in enumerate(b2)])
+    # row 4: ids out of range and a short history length
+    hist[4, :100] = -3
+    hist[4, 100:200] = V + 7
+    hl = np.full(B, H, dtype=np.int32)
+    hl[4] = 700
+    u = rng.random(B).astype(np.float32)
+    cfg = dict(temperature=0.8, top_k=50, top_p=0.95, min_p=0.05, repetition_penalty=1.15,
+               presence_penalty=0.5, frequency_penalty=0.3)
+    _sample_both(gpu, oracle, x, u, cfg, history=hist, hist_len=hl)
+    cfg2 = dict(temperature=1.1, top_k=20, repetition_penalty=3.0, frequency_penalty=2.0)
+    _sample_both(gpu, oracle, x, u, cfg2, history=hist, hist_len=hl)
+
+
 def test_sample_repeatable_and_workspace_reset(gpu, oracle):
     """Back-to-back calls sharing one workspace give identical results."""
     import llima_amd
