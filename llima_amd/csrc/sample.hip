@@ -1279,74 +1279,59 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
         const uint32_t i = (uint32_t)e * 64u + lane;
         const llima_u32x4 me = sh.sv[i];                // sv holds 2 * SMP_SMALL + 64 slots
         x[e] = i < ns ? key_f32(me.x) : -__builtin_inff();
-        id[e] = i < ns ? me.y : 0u;
+        id[e] = i < ns ? me.y : 0xFFFFFFFFu;            // matches no history id
     }
     if (P.lazy && c.pen) {
-        // an LDS hash of the survivor ids in buckets of 4 slots (sh.u.hash.key:
-        // id + 1, zeroed by the caller; sh.u.hash.cnt: the survivor's index).
-        // A bucket spills into the next one only when full, so one 16-byte
-        // read settles almost every history id: a free slot without a match
-        // means absent.
-        uint32_t* hkey = sh.u.hash.key;
-        uint32_t* hidx = sh.u.hash.cnt;
-        const llima_u32x4* hb4 = (const llima_u32x4*)hkey;
-        auto bucket_of = [](uint32_t v) { return (v * 2654435761u) >> (32 - 10); };   // SMP_HASH / 4
+        // A bitmap of the survivor ids (2^16 bits in sh.u.hash.key, zeroed by
+        // the caller) passes a history id with one LDS read; the few that pass
+        // (the survivors' own occurrences and about 0.1 % false hits) are
+        // broadcast one distinct id per wave at a time and counted by the lanes
+        // holding the survivors (every wave holds them all), together with the
+        // wave's other copies of that id.
+        uint32_t* bm = sh.u.hash.key;
+        auto bit_of = [](uint32_t v) { return (v * 2654435761u) >> 16; };
         if (wave == 0) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const uint32_t i = (uint32_t)e * 64u + lane;
-                if (i < ns) {
-                    uint32_t b = bucket_of(id[e]);
-                    for (;;) {
-                        uint32_t s = 0;
-                        while (s < 4u && atomicCAS(&hkey[4u * b + s], 0u, id[e] + 1u) != 0u) ++s;
-                        if (s < 4u) { hidx[4u * b + s] = i; break; }
-                        b = (b + 1u) & (SMP_HASH / 4u - 1u);
-                    }
-                }
+                const uint32_t h = bit_of(id[e]);
+                if ((uint32_t)e * 64u + lane < ns) atomicOr(&bm[h >> 5], 1u << (h & 31u));
             }
         }
         __syncthreads();
-        auto probe = [&](uint32_t v, uint32_t b, llima_u32x4 q) {   // v = id + 1, q = bucket b
-            for (;;) {
-                const int s = q.x == v ? 0 : q.y == v ? 1 : q.z == v ? 2 : q.w == v ? 3 : -1;
-                if (s >= 0) { atomicAdd(&sh.hc[hidx[4u * b + (uint32_t)s]], 1u); return; }
-                if (!(q.x && q.y && q.z && q.w)) return;
-                b = (b + 1u) & (SMP_HASH / 4u - 1u);
-                q = hb4[b];
+        uint32_t cn[2] = {0u, 0u};
+        // hv: this lane's history id; inlen: lanes whose entry lies before hlen
+        auto count_pass = [&](uint32_t hv, uint64_t m, uint64_t inlen) {   // m: lanes that passed
+            while (m) {
+                const uint32_t L = (uint32_t)__builtin_ctzll(m);
+                const uint32_t u = readlane(hv, L);
+                const uint64_t same = ballot(hv == u) & inlen;
+                m &= ~same;
+                const uint32_t k = (uint32_t)__popcll(same);
+#pragma unroll
+                for (int e = 0; e < 2; ++e) cn[e] += id[e] == u ? k : 0u;
             }
         };
-        // all bucket reads first, then the (rare) hits and full buckets
-        uint32_t hb[SMP_HBATCH];
-        llima_u32x4 hq[SMP_HBATCH];
+        uint32_t bw[SMP_HBATCH];                         // every bitmap read first
+#pragma unroll
+        for (int b = 0; b < SMP_HBATCH; ++b) bw[b] = bm[bit_of((uint32_t)hid[b]) >> 5];
 #pragma unroll
         for (int b = 0; b < SMP_HBATCH; ++b) {
-            hb[b] = bucket_of((uint32_t)hid[b]);
-            hq[b] = hb4[hb[b]];
-        }
-        uint32_t need = 0;
-#pragma unroll
-        for (int b = 0; b < SMP_HBATCH; ++b) {
-            const int32_t hv = hid[b];
-            const bool ok = ((int)t + b * LLIMA_WG < c.hlen) & (hv >= 0) & (hv < P.V);
-            const uint32_t v = (uint32_t)hv + 1u;
-            const llima_u32x4 q = hq[b];
-            const bool m = (q.x == v) | (q.y == v) | (q.z == v) | (q.w == v);
-            const bool full = (q.x != 0u) & (q.y != 0u) & (q.z != 0u) & (q.w != 0u);
-            need |= (ok & (m | full)) ? 1u << b : 0u;
-        }
-        if (need) {
-#pragma unroll
-            for (int b = 0; b < SMP_HBATCH; ++b)
-                if ((need >> b) & 1u) probe((uint32_t)hid[b] + 1u, hb[b], hq[b]);
+            const uint64_t inlen = ballot((int)t + b * LLIMA_WG < c.hlen);
+            const uint64_t m = ballot((bw[b] >> (bit_of((uint32_t)hid[b]) & 31u)) & 1u) & inlen;
+            count_pass((uint32_t)hid[b], m, inlen);
         }
         const int32_t* hrow = P.hist + (size_t)row * P.H_max;
-        for (int i = (int)t + SMP_HBATCH * LLIMA_WG; i < c.hlen; i += LLIMA_WG) {
-            const int32_t hv = hrow[i];
-            if (hv < 0 || hv >= P.V) continue;
-            const uint32_t b = bucket_of((uint32_t)hv);
-            probe((uint32_t)hv + 1u, b, hb4[b]);
+        for (int base = SMP_HBATCH * LLIMA_WG; base < c.hlen; base += LLIMA_WG) {
+            const int i = base + (int)t;
+            const uint32_t hv = i < c.hlen ? (uint32_t)hrow[i] : 0u;
+            const uint32_t h = bit_of(hv);
+            const uint64_t inlen = ballot(i < c.hlen);
+            count_pass(hv, ballot((bm[h >> 5] >> (h & 31u)) & 1u) & inlen, inlen);
         }
+        // ids outside [0, V) match no survivor
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (cn[e]) atomicAdd(&sh.hc[(uint32_t)e * 64u + lane], cn[e]);
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -1408,7 +1393,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
     }
     if (P.lazy && c.pen) {
 #pragma unroll
-        for (int i = 0; i < SMP_HASH / 4 / LLIMA_WG; ++i)
+        for (int i = 0; i < 2; ++i)                          // the 2^16-bit id bitmap
             ((llima_u32x4*)sh.u.hash.key)[t + i * LLIMA_WG] = llima_u32x4{0u, 0u, 0u, 0u};
     }
     uint32_t lowkey = 1u;
@@ -1424,6 +1409,9 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                                   : kk + 10u <= SMP_SMALL ? 10u
                                   : kk < 2u * SMP_SMALL ? min(32u, 2u * SMP_SMALL - kk) : 0u;
             uint32_t rem = min(N, (uint32_t)c.k + margin), above_all = 0;
+            // survivors wanted: at least rem, at most cap (one per lane when
+            // rem allows it: the pairwise ranking costs the square)
+            const uint32_t cap = rem <= SMP_SMALL ? SMP_SMALL : 2u * SMP_SMALL;
             lowkey = d.prefix;
             // round r counts into hcnt[r % 3] (rounds 0 and 1 zeroed by the
             // caller); after its barrier every wave scans all 256 bins itself
@@ -1448,8 +1436,10 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                 uint32_t ab = wave_incl_scan_u32(s4) - s4;
                 const uint32_t top = 255u - 4u * lane_id();
                 const uint32_t cs[4] = {c4.w, c4.z, c4.y, c4.x};
-                uint32_t mb = 0, mab = 0, mcn = 0;
-                bool hit = false;
+                // mb: the bin holding the rem-th key; fb: the lowest bin such
+                // that it and the bins above hold at most cap - above_all keys
+                uint32_t mb = 0, mab = 0, mcn = 0, fb = 0, fcum = 0;
+                bool hit = false, fit = false;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool h = ab < rem && ab + cs[i] >= rem;
@@ -1457,20 +1447,31 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                     mab = h ? ab : mab;
                     mcn = h ? cs[i] : mcn;
                     hit = hit || h;
+                    const bool f = above_all + ab + cs[i] <= cap;
+                    fb = f ? top - (uint32_t)i : fb;
+                    fcum = f ? ab + cs[i] : fcum;
+                    fit = fit || f;
                     ab += cs[i];
                 }
-                const uint64_t hm = ballot(hit);
+                const uint64_t hm = ballot(hit), fm = ballot(fit);
                 if (hm == 0) return false;               // cannot happen: the bins hold rem
+                buf = buf == 2u ? 0u : buf + 1u;
+                if (fm) {
+                    const uint32_t F = 63u - (uint32_t)__builtin_clzll(fm);
+                    if (readlane(fcum, F) >= rem) {      // cap keys or fewer, rem or more
+                        lowkey = d.prefix | (readlane(fb, F) << lo);
+                        break;
+                    }
+                }
                 const uint32_t L = (uint32_t)__builtin_ffsll((long long)hm) - 1u;
                 const uint32_t sb = readlane(mb, L), sab = readlane(mab, L), scn = readlane(mcn, L);
-                buf = buf == 2u ? 0u : buf + 1u;
                 d.prefix |= sb << lo;
                 d.pmask |= bmask << lo;
                 d.top = lo - 1;
                 rem -= sab;
                 above_all += sab;
                 lowkey = d.prefix;
-                if (above_all + scn <= 2 * SMP_SMALL) break;
+                if (cap > SMP_SMALL && above_all + scn <= cap) break;
             }
         }
     } else if (gkey) {
