@@ -52,7 +52,7 @@ namespace llima {
 #define SMP_FIN_CAP 4096                           // candidates per row the finish holds
 #define SMP_MAX_S 256                              // chunks per row the finish can gather
 #define SMP_HBATCH 8                               // history ids per thread loaded up front
-#define SMP_BOUND_LOWBIT 12                        // key bits below this are not searched
+#define SMP_BOUND_LOWBIT 16                        // key bits below this are not searched
 #define SMP_SMALL 64                               // survivors handled one per lane
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
