@@ -10,10 +10,14 @@ one batch.  Inputs rotate over >= 1 GiB of distinct device buffers so that the
 timed region starts.
 
 Prints ONE JSON line.  value = sampled rows/s (whole job), ms_per_step from a
-HIP-graph replay of K steps bracketed by synchronisation; roofline.achieved =
-algorithmic bytes per launch / mean kernel duration from per-launch HIP events
-on the launch stream; cpu_baseline = the CPU oracle on a bounded sample of the
-same workload on this host.
+HIP-graph replay of K steps bracketed by synchronisation and timed with HIP
+events on the launch stream.  One step is one entry-point call (for the sampler
+its two kernels, sweep and finish), so roofline.achieved = algorithmic bytes per
+step / ms_per_step; eager_call_us is the mean of per-call HIP events without the
+graph (host launch gaps included).  roofline.traffic = HBM bytes per step from
+the committed rocprofv3 counter runs (profiles/traffic.json), when measured for
+this workload.  cpu_baseline = the CPU oracle on a bounded sample of the same
+workload on this host.
 """
 from __future__ import annotations
 
@@ -213,7 +217,14 @@ def main():
     total_ms = ev0.elapsed_time(ev1)
     ms_per_step = total_ms / K
 
-    achieved = alg_bytes / (launch_ms * 1e-3) / 1e9
+    achieved = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    traffic = None
+    try:
+        with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "traffic.json")) as f:
+            traffic = json.load(f).get(name, {}).get("bytes_per_step")
+    except (OSError, ValueError):
+        pass
     result = {
         "metric": METRIC,
         "value": rows / (ms_per_step * 1e-3),
@@ -237,11 +248,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "kernel": kernel_names,
-            "algorithmic_bytes_per_launch": int(alg_bytes),
-            "mean_launch_us": launch_ms * 1e3,
-            "median_launch_us": float(np.median(per_launch_ms)) * 1e3,
+            "algorithmic_bytes_per_step": int(alg_bytes),
+            "eager_call_us": launch_ms * 1e3,
+            "eager_call_median_us": float(np.median(per_launch_ms)) * 1e3,
         },
     }
     if not args.no_cpu_baseline:
