@@ -1403,10 +1403,13 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
         } else {
             Digits d = digits_init(kmin, kmax);
             // lazy penalties can push values of the top-k below their raw rank:
-            // keep a margin of candidates below the k-th largest raw value
+            // keep a margin of candidates below the k-th largest raw value (the
+            // row falls back when more survivors than that drop below the rest;
+            // a random history holds about one in a thousand ids, and a wider
+            // margin narrows the window the first round can stop in)
             const uint32_t kk = (uint32_t)c.k;
             const uint32_t margin = !(P.lazy && c.pen) ? 0u
-                                  : kk + 10u <= SMP_SMALL ? 10u
+                                  : kk + 6u <= SMP_SMALL ? 6u
                                   : kk < 2u * SMP_SMALL ? min(32u, 2u * SMP_SMALL - kk) : 0u;
             uint32_t rem = min(N, (uint32_t)c.k + margin), above_all = 0;
             // survivors wanted: at least rem, at most cap (one per lane when
