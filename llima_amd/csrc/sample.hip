@@ -54,6 +54,7 @@ namespace llima {
 #define SMP_HBATCH 8                               // history ids per thread loaded up front
 #define SMP_BOUND_LOWBIT 16                        // key bits below this are not searched
 #define SMP_SMALL 64                               // survivors handled one per lane
+#define SMP_WCAP 128                               // candidates a sweep wave can stage
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
 
@@ -189,9 +190,11 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int E = NL * EPL;                // values per thread and chunk
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr int CW = SC * CHUNK / 2;         // history count words (the group)
+    constexpr int WS = CHUNK / LLIMA_WAVES;    // ids per wave and chunk
     __shared__ __align__(16) uint32_t cnt[CW];
     __shared__ uint32_t xa[SC][LLIMA_WAVES];
-    __shared__ uint32_t xc[SC][NL][LLIMA_WAVES];
+    __shared__ uint32_t xn[SC][LLIMA_WAVES];              // candidates per wave
+    __shared__ uint64_t xst[SC][LLIMA_WAVES][SMP_WCAP + 64];   // staged candidates (+ a spare slot per lane)
     __shared__ uint64_t xg[SC][LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
@@ -201,6 +204,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     if (row >= (uint32_t)P.B) return;
     const int t = (int)threadIdx.x;
     const uint32_t lane = lane_id(), wave = wave_id();
+    // wave w of a chunk owns its ids [w WS, (w + 1) WS); load j of lane l covers
+    // EPL ids at j 64 EPL + l EPL of that slice (1 KB contiguous per wave load)
+    const int lofs = (int)wave * WS + (int)lane * EPL;
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
     const int V = P.V;
     const int g0 = (int)grp * SC * CHUNK;                      // first id of the group
@@ -227,13 +233,13 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         if constexpr (MASK) {
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
-                const int i0 = g0 + cc * CHUNK + j * (LLIMA_WG * EPL) + t * EPL;
+                const int i0 = g0 + cc * CHUNK + j * (64 * EPL) + lofs;
                 mword[cc][j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
             }
         }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int i0 = g0 + cc * CHUNK + j * (LLIMA_WG * EPL) + t * EPL;
+            const int i0 = g0 + cc * CHUNK + j * (64 * EPL) + lofs;
             if constexpr (VEC) {
                 const int ia = i0 < V ? i0 : V - EPL;
                 raw[cc][j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
@@ -292,7 +298,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         float v[E];
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+            const int i0 = c0 + j * (64 * EPL) + lofs;
             float xv[EPL];
             const uint32_t w4[4] = {raw[cc][j].x, raw[cc][j].y, raw[cc][j].z, raw[cc][j].w};
             if constexpr (sizeof(TL) == 4) {
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         if (c1 - c0 < CHUNK) {
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
-                const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+                const int i0 = c0 + j * (64 * EPL) + lofs;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e)
                     if (i0 + e >= c1) v[j * EPL + e] = NEG_INF;
@@ -360,7 +366,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             uint32_t bidx = 0;
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
-                const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
+                const int i0 = c0 + j * (64 * EPL) + lofs;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e)
                     if (v[j * EPL + e] > best) { best = v[j * EPL + e]; bidx = (uint32_t)(i0 + e); }
@@ -414,9 +420,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         // the smallest finite float stands for -inf: -inf and NaN never pass
         const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
 
-        // ---- 5. write the values >= g in id order: per load j, lane counts,
-        //         wave scans (two counts packed per u32), then the waves in
-        //         order.  Only lanes whose maximum reaches g test their values.
+        // ---- 5. the values >= g in id order.  Each wave stages its own in LDS
+        //         (order load j, lane, value: id order inside the wave's slice;
+        //         offsets from two packed wave scans, writes to a spare slot per
+        //         lane instead of branches), then, after the one barrier, copies
+        //         its run to the region behind the runs of the waves before it.
+        //         Only lanes whose maximum reaches g test their values.
         uint32_t pm[NL];
 #pragma unroll
         for (int j = 0; j < NL; ++j) pm[j] = 0;
@@ -433,45 +442,40 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
         const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
         const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
-        if (lane == 0) {
-            xc[cc][0][wave] = t01 & 0xFFFFu; xc[cc][1][wave] = t01 >> 16;
-            xc[cc][2][wave] = t23 & 0xFFFFu; xc[cc][3][wave] = t23 >> 16;
-        }
-        __syncthreads();
-        uint32_t base[NL], total = 0;
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            uint32_t before = 0;
-#pragma unroll
-            for (int w = 0; w < LLIMA_WAVES; ++w) {
-                const uint32_t n = xc[cc][j][w];
-                before += (uint32_t)w < wave ? n : 0u;
-            }
-            base[j] = total + before;
-#pragma unroll
-            for (int w = 0; w < LLIMA_WAVES; ++w) total += xc[cc][j][w];
-        }
-        const bool fits = total <= SMP_CAP;
-        if (fits && lm >= g2) {
+        const uint32_t T0 = t01 & 0xFFFFu, T1 = t01 >> 16, T2 = t23 & 0xFFFFu, T3 = t23 >> 16;
+        const uint32_t nw = T0 + T1 + T2 + T3;
+        uint64_t* stg = xst[cc][wave];
+        if (nw <= SMP_WCAP && lm >= g2) {
             const uint32_t e01 = i01 - a01, e23 = i23 - a23;
-            const uint32_t lx[NL] = {e01 & 0xFFFFu, e01 >> 16, e23 & 0xFFFFu, e23 >> 16};
-            uint64_t* dst = reg + SMP_HDR;
+            const uint32_t start[NL] = {e01 & 0xFFFFu, T0 + (e01 >> 16), T0 + T1 + (e23 & 0xFFFFu),
+                                        T0 + T1 + T2 + (e23 >> 16)};
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
-                if (pm[j]) {
-                    const int i0 = c0 + j * (LLIMA_WG * EPL) + t * EPL;
-                    uint32_t o = base[j] + lx[j];
+                const int i0 = c0 + j * (64 * EPL) + lofs;
+                uint32_t o = start[j];
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) {
-                        if ((pm[j] >> e) & 1u) {
-                            dst[o] = ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
-                            ++o;
-                        }
-                    }
+                for (int e = 0; e < EPL; ++e) {
+                    const bool in = (pm[j] >> e) & 1u;
+                    stg[in ? o : SMP_WCAP + lane] =
+                        ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
+                    o += in ? 1u : 0u;
                 }
             }
         }
+        if (lane == 0) xn[cc][wave] = nw;
+        __syncthreads();
+        uint32_t off = 0, total = 0;
+        bool wfit = true;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            const uint32_t n = xn[cc][w];
+            off += (uint32_t)w < wave ? n : 0u;
+            total += n;
+            wfit = wfit && n <= SMP_WCAP;
+        }
+        const bool fits = wfit && total <= SMP_CAP;
         if (fits) {
+            for (uint32_t i = lane; i < nw; i += 64) reg[SMP_HDR + off + i] = stg[i];
             const uint32_t pre = pre_slots(P);
             for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
         }
