@@ -219,6 +219,30 @@ __device__ __forceinline__ uint32_t wave_rth_largest(uint32_t key, uint32_t r, i
     return t;
 }
 
+// The same value as wave_rth_largest(key, r, lowbit) for lowbit <= 23, with
+// fewer serial steps in the common case: the key's top 9 bits (sign and
+// exponent of the float) are taken from the wave maximum's bucket or the one
+// below it (two independent ballots), leaving the mantissa bits 22..lowbit.
+// Anything else takes the full search.
+__device__ __forceinline__ uint32_t wave_rth_largest_exp(uint32_t key, uint32_t r, int lowbit) {
+    const uint32_t e1 = wave_max_u32(key) & 0xFF800000u;
+    if (e1 >= 0x00800000u) {
+        const uint32_t e0 = e1 - 0x00800000u;
+        const uint32_t n1 = (uint32_t)__popcll(ballot(key >= e1));
+        const uint32_t n0 = (uint32_t)__popcll(ballot(key >= e0));
+        if (n0 >= r) {
+            uint32_t t = n1 >= r ? e1 : e0;
+#pragma unroll
+            for (int b = 22; b >= lowbit; --b) {
+                const uint32_t cand = t | (1u << b);
+                if ((uint32_t)__popcll(ballot(key >= cand)) >= r) t = cand;
+            }
+            return t;
+        }
+    }
+    return wave_rth_largest(key, r, lowbit);
+}
+
 // Descending bitonic sort of one uint32 per lane across a wavefront; returns
 // this lane's element of the sorted sequence (lane 0 holds the largest).
 __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {

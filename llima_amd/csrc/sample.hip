@@ -396,7 +396,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             // one the finish's fast path (when one wave holds r of the row's
             // top-k values).  One wave-level search, no second pass: this runs
             // after the chunk's data arrived, on the kernel's critical path.
-            const uint32_t bw = wave_rth_largest(lk, rank, SMP_BOUND_LOWBIT);
+            const uint32_t bw = wave_rth_largest_exp(lk, rank, SMP_BOUND_LOWBIT);
             if (lane == 0) xa[cc][wave] = bw;
             __syncthreads();
             uint32_t gk = 0;
