@@ -62,11 +62,12 @@ namespace llima {
 
 // Chunk region: slot 0 is the header, low 32 bits: candidates written |
 // flags << 16; high 32 bits: the bound g (float bits): every finite value >= g
-// was written (-inf: all).  Candidates follow from slot 1 as (value bits << 32
-// | id) in id order; the slots the finish reads in its first round (pre_slots)
-// that hold no candidate carry SMP_SENTINEL.  Greedy rows: slot 1 holds
-// (key << 32 | ~index) of the chunk maximum.
-#define SMP_SENTINEL (0xFF800000ull << 32)         // value -inf: never a candidate
+// was written (-inf: all).  Candidates follow from slot 1 as (key << 32 | id)
+// in id order (the key of a finite value is never 0); the slots the finish
+// reads in its first round (pre_slots) that hold no candidate carry
+// SMP_SENTINEL, key 0.  Greedy rows: slot 1 holds (key << 32 | ~index) of the
+// chunk maximum.
+#define SMP_SENTINEL 0ull                          // key 0: no candidate
 struct SampleParams {
     const void* logits;
     int64_t row_stride;
@@ -475,7 +476,11 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         }
         const bool fits = wfit && total <= SMP_CAP;
         if (fits) {
-            for (uint32_t i = lane; i < nw; i += 64) reg[SMP_HDR + off + i] = stg[i];
+            for (uint32_t i = lane; i < nw; i += 64) {         // staged as value bits, written as keys
+                const uint64_t sv = stg[i];
+                reg[SMP_HDR + off + i] = ((uint64_t)f32_key(__uint_as_float((uint32_t)(sv >> 32))) << 32) |
+                                         (uint32_t)sv;
+            }
             const uint32_t pre = pre_slots(P);
             for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
         }
@@ -1024,7 +1029,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         id[j] = 0;
         if (f < N) {
             const uint64_t q = sh.u.cand[f + (f >> 4)];
-            x[j] = __uint_as_float((uint32_t)(q >> 32));
+            x[j] = key_f32((uint32_t)(q >> 32));
             id[j] = (uint32_t)q;
         }
     }
@@ -1563,8 +1568,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t hi = h ? q[i].w : q[i].y, lo = h ? q[i].z : q[i].x;
-                const bool valid = live & (hi != (uint32_t)(SMP_SENTINEL >> 32)) & ((i | h) != 0 || !hdr);
-                const uint32_t k = valid ? f32_key(__uint_as_float(hi)) : 0u;
+                const bool valid = live & ((i | h) != 0 || !hdr);   // slot 0 of a region is the header
+                const uint32_t k = valid ? hi : 0u;                  // sentinels hold key 0
                 kr[2 * i + h] = k;
                 idv[2 * i + h] = lo;
                 kmx = k > kmx ? k : kmx;
