@@ -446,10 +446,10 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         const uint32_t T0 = t01 & 0xFFFFu, T1 = t01 >> 16, T2 = t23 & 0xFFFFu, T3 = t23 >> 16;
         const uint32_t nw = T0 + T1 + T2 + T3;
         uint64_t* stg = xst[cc][wave];
+        const uint32_t e01 = i01 - a01, e23 = i23 - a23;
+        const uint32_t start[NL] = {e01 & 0xFFFFu, T0 + (e01 >> 16), T0 + T1 + (e23 & 0xFFFFu),
+                                    T0 + T1 + T2 + (e23 >> 16)};   // this lane's first slot per load
         if (nw <= SMP_WCAP && lm >= g2) {
-            const uint32_t e01 = i01 - a01, e23 = i23 - a23;
-            const uint32_t start[NL] = {e01 & 0xFFFFu, T0 + (e01 >> 16), T0 + T1 + (e23 & 0xFFFFu),
-                                        T0 + T1 + T2 + (e23 >> 16)};
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
                 const int i0 = c0 + j * (64 * EPL) + lofs;
@@ -466,20 +466,35 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         if (lane == 0) xn[cc][wave] = nw;
         __syncthreads();
         uint32_t off = 0, total = 0;
-        bool wfit = true;
 #pragma unroll
         for (int w = 0; w < LLIMA_WAVES; ++w) {
             const uint32_t n = xn[cc][w];
             off += (uint32_t)w < wave ? n : 0u;
             total += n;
-            wfit = wfit && n <= SMP_WCAP;
         }
-        const bool fits = wfit && total <= SMP_CAP;
+        const bool fits = total <= SMP_CAP;
         if (fits) {
-            for (uint32_t i = lane; i < nw; i += 64) {         // staged as value bits, written as keys
-                const uint64_t sv = stg[i];
-                reg[SMP_HDR + off + i] = ((uint64_t)f32_key(__uint_as_float((uint32_t)(sv >> 32))) << 32) |
-                                         (uint32_t)sv;
+            if (nw <= SMP_WCAP) {
+                for (uint32_t i = lane; i < nw; i += 64) {     // staged as value bits, written as keys
+                    const uint64_t sv = stg[i];
+                    reg[SMP_HDR + off + i] =
+                        ((uint64_t)f32_key(__uint_as_float((uint32_t)(sv >> 32))) << 32) | (uint32_t)sv;
+                }
+            } else if (lm >= g2) {
+                // more than the staging holds (dense rows such as grammar-masked
+                // ones without top-k): straight from the registers
+#pragma unroll
+                for (int j = 0; j < NL; ++j) {
+                    const int i0 = c0 + j * (64 * EPL) + lofs;
+                    uint32_t o = SMP_HDR + off + start[j];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        if ((pm[j] >> e) & 1u) {
+                            reg[o] = ((uint64_t)f32_key(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
+                            ++o;
+                        }
+                    }
+                }
             }
             const uint32_t pre = pre_slots(P);
             for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
