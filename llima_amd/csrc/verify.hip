@@ -19,11 +19,13 @@
 // workspace slots; a later launch reads them):
 //   vr_rowmax   per (row, chunk) maximum key
 //   vr_rowsum   per (row, chunk) sum of W, and W at each row's draft token
-//   vr_drawsum  per (sequence, chunk): the acceptance scan (recomputed from the
-//               sums by every workgroup of the sequence), then the chunk's sum
-//               of residual weights when a draft was rejected
-//   vr_final    per sequence: acceptance, emitted drafts, the chunk holding the
-//               draw target, and the scan of that chunk for the token.
+//   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
+//               the sums by every workgroup of the sequence), then, for every
+//               group of 32 ids of the draw row, the sum of the residual
+//               weights and the sum of the plain target weights
+//   vr_final    per sequence: acceptance, emitted drafts, the group holding the
+//               draw target (a block scan over the group sums), and the token
+//               inside it (one wave, one id per lane).
 // Pass 2 re-reads the rows right after pass 1; at these sizes they are still
 // resident in the 256 MB Infinity Cache.
 #include "common.hpp"
@@ -34,6 +36,9 @@ namespace llima {
 #define VR_E 32
 #define VR_CHUNK (LLIMA_WG * VR_E)
 #define VR_MAX_D 255
+#define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup
+#define VR_G 32                      // ids per draw group (4 threads of vr_drawsum)
+#define VR_GB 16                     // group sums a vr_final thread loads at once
 
 struct VerifyParams {
     const float* tgt;
@@ -46,8 +51,9 @@ struct VerifyParams {
     uint32_t* maxk;      // [NR][S]
     uint64_t* sums;      // [NR][S]
     uint64_t* wx;        // [NR]
-    uint64_t* res;       // [B][S]
-    int32_t B, D, V, S, NR;
+    uint64_t* gres;      // [B][NG] residual weight per group of VR_G ids
+    uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
+    int32_t B, D, V, S, NR, NG, SD;
 };
 
 // Row r: target rows first ([B][D+1]), then draft rows ([B][D]).
@@ -148,43 +154,57 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
 struct SeqShared {
     uint64_t z[2 * VR_MAX_D + 1];      // Z of target rows 0..D then draft rows 0..D-1
     uint32_t m[2 * VR_MAX_D + 1];      // maximum keys, same order
+    uint8_t ok[VR_MAX_D];              // draft k passes its acceptance test
     int32_t acc;
     BlockScratch bs;
 };
 
-// Z and maximum of every row of sequence b (one wavefront per row), then the
-// acceptance scan.  Returns the number of accepted drafts (same in every thread).
+// Z and maximum of every row of sequence b, then the acceptance scan.  Every
+// input is requested at once (the per-chunk sums are combined with LDS
+// atomics) and the D acceptance tests run in parallel, one per thread: the
+// only serial part is the first failing test, found in LDS.  Returns the
+// number of accepted drafts (same in every thread).
 __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShared& sh) {
-    const int nr = 2 * P.D + 1;
-    for (int q = (int)(threadIdx.x >> 6); q < nr; q += LLIMA_WAVES) {
+    const int nr = 2 * P.D + 1, t = (int)threadIdx.x;
+    for (int q = t; q < nr; q += LLIMA_WG) { sh.z[q] = 0; sh.m[q] = 0; }
+    __syncthreads();
+    for (int i = t; i < nr * P.S; i += LLIMA_WG) {
+        const int q = i / P.S, c = i - q * P.S;
         const int r = q <= P.D ? trow(P, b, q) : drow(P, b, q - P.D - 1);
-        uint64_t z = 0;
-        uint32_t m = 0;
-        for (int i = (int)lane_id(); i < P.S; i += 64) {
-            z += P.sums[(size_t)r * P.S + i];
-            const uint32_t mk = P.maxk[(size_t)r * P.S + i];
-            m = mk > m ? mk : m;
-        }
-        z = wave_sum_u64(z);
-        m = wave_max_u32(m);
-        if (lane_id() == 0) { sh.z[q] = z; sh.m[q] = m; }
+        atomicAdd((unsigned long long*)&sh.z[q], (unsigned long long)P.sums[(size_t)r * P.S + c]);
+        atomicMax(&sh.m[q], P.maxk[(size_t)r * P.S + c]);
+    }
+    // per draft: W at the draft token in the target and the draft row
+    int x = -1;
+    uint64_t wt = 0, wd = 0;
+    float ua = 0.0f;
+    if (t < P.D) {
+        x = P.draft_ids[b * P.D + t];
+        wt = P.wx[trow(P, b, t)];
+        wd = P.wx[drow(P, b, t)];
+        ua = P.u_accept[b * P.D + t];
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (; acc < P.D; ++acc) {
-            const int x = P.draft_ids[b * P.D + acc];
-            const uint64_t zt = sh.z[acc], zd = sh.z[P.D + 1 + acc];
-            bool ok = false;
-            if (x >= 0 && x < P.V && zt > 0) {
-                const uint64_t wt = P.wx[trow(P, b, acc)], wd = P.wx[drow(P, b, acc)];
-                const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
-                const llima_u128 rhs = (llima_u128)uniform32(P.u_accept[b * P.D + acc]) *
-                                       ((llima_u128)wd * zt);
-                ok = lhs >= rhs;
-            }
-            if (!ok) break;
+    for (int k = t; k < P.D; k += LLIMA_WG) {
+        if (k != t) {                                   // D > LLIMA_WG: the rest one by one
+            x = P.draft_ids[b * P.D + k];
+            wt = P.wx[trow(P, b, k)];
+            wd = P.wx[drow(P, b, k)];
+            ua = P.u_accept[b * P.D + k];
         }
+        const uint64_t zt = sh.z[k], zd = sh.z[P.D + 1 + k];
+        bool ok = false;
+        if (x >= 0 && x < P.V && zt > 0) {
+            const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
+            const llima_u128 rhs = (llima_u128)uniform32(ua) * ((llima_u128)wd * zt);
+            ok = lhs >= rhs;
+        }
+        sh.ok[k] = ok ? 1 : 0;
+    }
+    __syncthreads();
+    if (t == 0) {
+        int acc = 0;
+        while (acc < P.D && sh.ok[acc]) ++acc;
         sh.acc = acc;
     }
     __syncthreads();
@@ -221,88 +241,126 @@ __device__ __forceinline__ DrawCtx draw_ctx(const VerifyParams& P, int b, int ac
     return q;
 }
 
-__device__ __forceinline__ uint64_t draw_weight(const DrawCtx& q, int i) {
-    const uint64_t wt = row_weight(q.t[i], q.mt);
-    if (!q.residual) return wt;
-    const uint64_t wd = row_weight(q.d[i], q.md);
+
+// Residual weight of one id from its target and draft values.
+__device__ __forceinline__ uint64_t residual_weight(const DrawCtx& q, uint64_t wt, float xd) {
+    const uint64_t wd = row_weight(xd, q.md);
     const llima_u128 a = (llima_u128)wt * q.zd, c = (llima_u128)wd * q.zt;
     return a > c ? (uint64_t)((a - c) >> q.shift) : 0ull;
 }
 
+// 8 consecutive values from id i0 (a multiple of 8): two 16-byte loads from
+// clamped addresses; values past the row are -inf.
+__device__ __forceinline__ void load8(const float* rowp, int i0, int V, float (&x)[8]) {
+    const int ia = i0 < V ? i0 : V - 4, ib = i0 + 4 < V ? i0 + 4 : V - 4;
+    const llima_u32x4 a = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+    const llima_u32x4 b = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ib));
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = i0 + e < V ? __uint_as_float(w[e]) : -__builtin_inff();
+}
+
+__device__ __forceinline__ uint64_t quad_sum_u64(uint64_t v) {
+    v += dpp64<DPP_QUAD_XOR1, 0xF, false>(0ull, v);
+    v += dpp64<DPP_QUAD_XOR2, 0xF, false>(0ull, v);
+    return v;
+}
+
 __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
     __shared__ SeqShared sh;
-    const int b = blockIdx.x / P.S, c = blockIdx.x % P.S;
+    const int b = blockIdx.x / P.SD, c = blockIdx.x % P.SD;
     const int acc = accept_scan(P, b, sh);
-    if (acc >= P.D) return;                          // bonus draw: no residual
-    const DrawCtx q = draw_ctx(P, b, acc, sh);
-    const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
-    uint64_t s = 0;
-    for (int i = c0 + (int)threadIdx.x; i < c1; i += LLIMA_WG) s += draw_weight(q, i);
-    s = block_sum_u64(s, sh.bs);
-    if (threadIdx.x == 0) P.res[(size_t)b * P.S + c] = s;
+    const DrawCtx q = draw_ctx(P, b, acc, sh);       // residual iff a draft was rejected
+    const int i0 = c * VR_DCHUNK + (int)threadIdx.x * 8;
+    float xt[8], xd[8];
+    load8(q.t, i0, P.V, xt);
+    if (q.residual) load8(q.d, i0, P.V, xd);
+    uint64_t st = 0, sr = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint64_t wt = row_weight(xt[e], q.mt);
+        st += wt;
+        if (q.residual) sr += residual_weight(q, wt, xd[e]);
+    }
+    st = quad_sum_u64(st);                            // 4 threads = one group of 32 ids
+    sr = quad_sum_u64(sr);
+    const int g = i0 / VR_G;
+    if ((threadIdx.x & 3u) == 0u && g < P.NG) {
+        P.gtgt[(size_t)b * P.NG + g] = st;
+        P.gres[(size_t)b * P.NG + g] = sr;
+    }
 }
 
 __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     __shared__ SeqShared sh;
-    __shared__ int32_t s_chunk, s_tok;
-    __shared__ uint64_t s_before, s_target;
-    __shared__ bool s_residual;
+    __shared__ int32_t s_group, s_tok;
+    __shared__ uint64_t s_before;
     const int b = blockIdx.x;
+    const uint32_t t = threadIdx.x;
     const int acc = accept_scan(P, b, sh);
     DrawCtx q = draw_ctx(P, b, acc, sh);
-    const int rt = trow(P, b, acc);
-    if (threadIdx.x == 0) {
+    if (t == 0) {
         int32_t* em = P.emitted + (size_t)b * (P.D + 1);
         for (int j = 0; j < acc; ++j) em[j] = P.draft_ids[b * P.D + j];
         for (int j = acc; j <= P.D; ++j) em[j] = -1;
         P.accepted_len[b] = acc;
-        // locate the chunk that holds the draw target
-        const uint64_t* sums = P.res + (size_t)b * P.S;
-        uint64_t total = 0;
-        bool residual = q.residual;
-        if (residual) {
-            for (int j = 0; j < P.S; ++j) total += sums[j];
-            if (total == 0) residual = false;          // p_t == p_d: draw from p_t
-        }
-        if (!residual) {
-            sums = P.sums + (size_t)rt * P.S;
-            total = q.zt;
-        }
-        int32_t chunk = -1;
-        uint64_t before = 0, target = 0;
-        if (total > 0) {
-            target = (uint64_t)(((llima_u128)uniform32(P.u_resample[b]) * total) >> 32);
-            for (int j = 0; j < P.S; ++j) {
-                const uint64_t sj = sums[j];
-                if (before + sj > target) { chunk = j; break; }
-                before += sj;
-            }
-        }
-        s_chunk = chunk; s_before = before; s_target = target; s_residual = residual;
+        s_group = -1;
         s_tok = -1;
     }
-    __syncthreads();
-    const int chunk = s_chunk;
-    if (chunk >= 0) {
-        q.residual = s_residual;
-        const int c0 = chunk * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
-        // thread t owns the contiguous ids [c0 + t*VR_E, c0 + (t+1)*VR_E)
-        const int lo = c0 + (int)threadIdx.x * VR_E;
-        const int hi = lo + VR_E < c1 ? lo + VR_E : c1;
-        uint64_t sub = 0;
-        for (int i = lo; i < hi; ++i) sub += draw_weight(q, i);
-        uint64_t tot;
-        uint64_t a = s_before + block_excl_scan_u64(sub, &tot, sh.bs);
-        const uint64_t target = s_target;
-        if (sub > 0 && a <= target && target < a + sub) {
-            for (int i = lo; i < hi; ++i) {
-                a += draw_weight(q, i);
-                if (a > target) { s_tok = i; break; }
+    // thread t owns the groups [t GPT, (t + 1) GPT), read VR_GB at a time with
+    // every load of a batch in flight together
+    const int NG = P.NG, GPT = (NG + LLIMA_WG - 1) / LLIMA_WG;
+    const int g0 = (int)t * GPT, g1 = g0 + GPT < NG ? g0 + GPT : NG;
+    const uint64_t* gr = P.gres + (size_t)b * NG;
+    const uint64_t* gt = P.gtgt + (size_t)b * NG;
+    auto range_sum = [&](const uint64_t* a) {
+        uint64_t sum = 0;
+        for (int gb = g0; gb < g1; gb += VR_GB) {
+            uint64_t v[VR_GB];
+#pragma unroll
+            for (int j = 0; j < VR_GB; ++j) v[j] = gb + j < g1 ? a[gb + j] : 0ull;
+#pragma unroll
+            for (int j = 0; j < VR_GB; ++j) sum += v[j];
+        }
+        return sum;
+    };
+    if (q.residual) {
+        if (block_sum_u64(range_sum(gr), sh.bs) == 0) q.residual = false;   // p_t == p_d: draw from p_t
+    }
+    const uint64_t* sums = q.residual ? gr : gt;
+    const uint64_t s = range_sum(sums);
+    uint64_t total;
+    const uint64_t before = block_excl_scan_u64(s, &total, sh.bs);
+    const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.u_resample[b]) * total) >> 32);
+    if (total > 0 && s > 0 && before <= target && target < before + s) {
+        uint64_t a = before;
+        bool found = false;
+        for (int gb = g0; gb < g1 && !found; gb += VR_GB) {
+            uint64_t v[VR_GB];
+#pragma unroll
+            for (int j = 0; j < VR_GB; ++j) v[j] = gb + j < g1 ? sums[gb + j] : 0ull;
+#pragma unroll
+            for (int j = 0; j < VR_GB; ++j) {
+                if (!found && a + v[j] > target) { s_group = gb + j; s_before = a; found = true; }
+                a += found ? 0ull : v[j];
             }
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) P.emitted[(size_t)b * (P.D + 1) + acc] = s_tok;
+    const int grp = s_group;
+    if (grp >= 0 && t < 64) {
+        // one id per lane: the group's weights, scanned in id order
+        const int i = grp * VR_G + (int)t;
+        uint64_t w = 0;
+        if (t < VR_G && i < P.V) {
+            const uint64_t wt = row_weight(q.t[i], q.mt);
+            w = q.residual ? residual_weight(q, wt, q.d[i]) : wt;
+        }
+        const uint64_t inc = s_before + wave_incl_scan_u64(w);
+        if (w > 0 && inc - w <= target && target < inc) s_tok = i;
+    }
+    __syncthreads();
+    if (t == 0) P.emitted[(size_t)b * (P.D + 1) + acc] = s_tok;
 }
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -315,7 +373,8 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
     if (B <= 0 || D < 0 || V <= 0) return 0;
     const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
     const size_t NR = (size_t)B * (2 * D + 1);
-    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + al256((size_t)B * S * 8);
+    const size_t NG = (size_t)(V + VR_G - 1) / VR_G;
+    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * NG * 8);
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -338,16 +397,19 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.B = B; P.D = D; P.V = V;
     P.S = (V + VR_CHUNK - 1) / VR_CHUNK;
     P.NR = B * (2 * D + 1);
+    P.NG = (V + VR_G - 1) / VR_G;
+    P.SD = (V + VR_DCHUNK - 1) / VR_DCHUNK;
     char* w = (char*)workspace;
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
     P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
-    P.res = (uint64_t*)w;
+    P.gres = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
+    P.gtgt = (uint64_t*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
     hipLaunchKernelGGL(vr_rowmax, dim3(g12), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_rowsum, dim3(g12), dim3(LLIMA_WG), 0, st, P);
-    hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.S), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }
