@@ -192,7 +192,10 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr int CW = SC * CHUNK / 2;         // history count words (the group)
     constexpr int WS = CHUNK / LLIMA_WAVES;    // ids per wave and chunk
-    __shared__ __align__(16) uint32_t cnt[CW];
+    // history counts of the group, two 16-bit counts per word: dynamic LDS,
+    // sized by the launch only when the sweep applies the penalties itself
+    // (otherwise 0 bytes, which keeps the workgroups' LDS small)
+    extern __shared__ __align__(16) uint32_t cnt[];
     __shared__ uint32_t xa[SC][LLIMA_WAVES];
     __shared__ uint32_t xn[SC][LLIMA_WAVES];              // candidates per wave
     __shared__ uint64_t xst[SC][LLIMA_WAVES][SMP_WCAP + 64];   // staged candidates (+ a spare slot per lane)
@@ -1709,12 +1712,14 @@ template <typename TL>
 static void launch_sweep(const SampleParams& P, hipStream_t st) {
     constexpr int SC = SMP_SWEEP_SC;
     const dim3 g((uint32_t)P.B * (uint32_t)((P.S + SC - 1) / SC)), b(LLIMA_WG);
+    // the history count table (dynamic LDS) only when the sweep penalises
+    const size_t cnt_bytes = (P.H_max > 0 && !P.lazy) ? (size_t)SC * (16 / sizeof(TL)) * 4 * LLIMA_WG / 2 * 4 : 0;
     if (P.bitmask) {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true, SC>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, false, true, SC>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true, SC>), g, b, cnt_bytes, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, true, SC>), g, b, cnt_bytes, st, P);
     } else {
-        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false, SC>), g, b, 0, st, P);
-        else hipLaunchKernelGGL((sample_sweep<TL, false, false, SC>), g, b, 0, st, P);
+        if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false, SC>), g, b, cnt_bytes, st, P);
+        else hipLaunchKernelGGL((sample_sweep<TL, false, false, SC>), g, b, cnt_bytes, st, P);
     }
 }
 
