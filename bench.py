@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="batched_penalties",
                     choices=["batched_penalties", "single_row", "constrained",
-                             "large_vocab_bf16", "large_vocab_bf16_greedy", "speculative"])
+                             "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
+                             "speculative"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -70,7 +71,8 @@ def main():
 
     name = args.workload
     greedy_variant = name.endswith("_greedy")
-    gen = wl.WORKLOADS["large_vocab_bf16" if greedy_variant else name]
+    argmax_only = name == "argmax_bf16"          # llima_argmax on the same rows
+    gen = wl.WORKLOADS["large_vocab_bf16" if (greedy_variant or argmax_only) else name]
     w = gen()
     t0 = time.time()
 
@@ -143,21 +145,32 @@ def main():
         cref = ctypes.byref(cfg)
         hp = None if hist is None else hist.data_ptr()
         mp = None if mask is None else mask.data_ptr()
-        for x in bufs:
-            launches.append(lambda sp, x=x: check(L.llima_sample(
-                x.data_ptr(), dt, B, V, V, hp, None, H, mp, u.data_ptr(), cref,
-                out_ids.data_ptr(), out_p.data_ptr(), None, ws.data_ptr(), nws, sp),
-                "llima_sample"))
-        alg_bytes = lg.nbytes + (0 if hist is None else hist.numel() * 4) + \
-            (0 if mask is None else mask.numel() * 4) + u.numel() * 4 + out_ids.numel() * 4 + \
-            out_p.numel() * 4
+        if argmax_only:
+            nwa = L.llima_argmax_workspace_bytes(B, V, dt)
+            wsa = torch.zeros(max(nwa, 1), dtype=torch.uint8, device=dev)
+            for x in bufs:
+                launches.append(lambda sp, x=x: check(L.llima_argmax(
+                    x.data_ptr(), dt, B, V, V, 0, _lib.ARGMAX_SPLIT_FIRST, out_ids.data_ptr(), None,
+                    wsa.data_ptr(), nwa, sp), "llima_argmax"))
+            alg_bytes = lg.nbytes + out_ids.numel() * 4
+            kernel_names = ["argmax_sweep", "argmax_finish"]
+            config = {"workload": name, "B": B, "V": V, "logits_dtype": "bf16" if is_bf16 else "fp32"}
+        else:
+            for x in bufs:
+                launches.append(lambda sp, x=x: check(L.llima_sample(
+                    x.data_ptr(), dt, B, V, V, hp, None, H, mp, u.data_ptr(), cref,
+                    out_ids.data_ptr(), out_p.data_ptr(), None, ws.data_ptr(), nws, sp),
+                    "llima_sample"))
+            alg_bytes = lg.nbytes + (0 if hist is None else hist.numel() * 4) + \
+                (0 if mask is None else mask.numel() * 4) + u.numel() * 4 + out_ids.numel() * 4 + \
+                out_p.numel() * 4
+            kernel_names = ["sample_sweep", "sample_finish"]
+            config = {"workload": name, "B": B, "V": V, "history": H,
+                      "logits_dtype": "bf16" if is_bf16 else "fp32"}
+            config.update({k: v for k, v in cfgd.items()})
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16" if is_bf16 else "f32"
-        kernel_names = ["sample_sweep", "sample_finish"]
-        config = {"workload": name, "B": B, "V": V, "history": H,
-                  "logits_dtype": "bf16" if is_bf16 else "fp32"}
-        config.update({k: v for k, v in cfgd.items()})
     torch.cuda.synchronize()
     setup_s = time.time() - t0
 
@@ -280,12 +293,19 @@ def cpu_baseline(name, w, seconds, greedy_variant):
         unit = "sequences/s"
         sample = f"{reps} x verify_rejection over the full [16,8,128256] batch"
     else:
-        cfg = orc.SamplerConfig(greedy=True) if greedy_variant else orc.SamplerConfig(**w["cfg"])
         lg = w["logits"]
-        while time.time() < t_end or reps == 0:
-            orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])
-            n_rows += lg.shape[0]
-            reps += 1
+        if name == "argmax_bf16":
+            # the same rows through the oracle's argmax (the reference's rule)
+            while time.time() < t_end or reps == 0:
+                orc.argmax(lg)
+                n_rows += lg.shape[0]
+                reps += 1
+        else:
+            cfg = orc.SamplerConfig(greedy=True) if greedy_variant else orc.SamplerConfig(**w["cfg"])
+            while time.time() < t_end or reps == 0:
+                orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])
+                n_rows += lg.shape[0]
+                reps += 1
         unit = "rows/s"
         sample = f"{reps} x the full {list(lg.shape)} batch"
     dt = time.time() - t0
