@@ -520,7 +520,7 @@ struct FinShared {
     uint32_t ccount[SMP_MAX_S];
     uint32_t coff[SMP_MAX_S];
     uint32_t hcnt[3][256 + 64];                      // + a spare bin per lane
-    uint64_t hmass[2][256];
+    uint64_t hmass[3][256 + 64];                     // + a spare bin per lane
     llima_u32x4 sv[2 * SMP_SMALL + 64];              // + a spare slot per lane
     llima_u32x4 sv2[LLIMA_WAVES][2 * SMP_SMALL];
     uint32_t pc[2][LLIMA_WAVES][64];
@@ -567,14 +567,17 @@ __device__ __forceinline__ uint64_t wg_prefix_u64(uint64_t inc, uint64_t v, uint
 
 // Top-p boundary: the smallest key theta such that an element with key theta
 // has (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
-// hcnt / hmass are zero on entry and on return.
+// Radix rounds over 8-bit digits with one barrier each: round r counts into
+// buffer r % 3 (buffers 0 and 1 zero on entry; non-members count into a spare
+// bin per lane), then every wave scans all 256 bins itself and zeroes buffer
+// (r + 2) % 3.  Stops early when the selected bin holds one key.
 template <int EPT>
 __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
                                   llima_u128 PZ, uint32_t kmin, uint32_t kmax, FinShared& sh) {
     Digits d = digits_init(kmin, kmax);
     uint64_t acc = 0;
-    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
-    int buf = 0;
+    const uint32_t t = threadIdx.x, lane = lane_id();
+    uint32_t buf = 0;
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
@@ -582,47 +585,68 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
         uint64_t* hm = sh.hmass[buf];
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
-            if (key[j] && (key[j] & d.pmask) == d.prefix) {
-                const uint32_t b = (key[j] >> lo) & bmask;
-                atomicAdd(&hc[b], 1u);
-                if (w[j]) atomicAdd((unsigned long long*)&hm[b], (unsigned long long)w[j]);
-            }
+            const bool in = (key[j] != 0u) & ((key[j] & d.pmask) == d.prefix);
+            const uint32_t b = in ? (key[j] >> lo) & bmask : 256u + lane;
+            atomicAdd(&hc[b], 1u);
+            atomicAdd((unsigned long long*)&hm[b], (unsigned long long)w[j]);
         }
         __syncthreads();
-        const uint32_t bin = 255u - t;
-        const uint32_t cn = hc[bin];
-        const uint64_t m = hm[bin];
-        sh.hcnt[buf ^ 1][t] = 0;
-        sh.hmass[buf ^ 1][t] = 0;
-        const uint64_t inc = wave_incl_scan_u64(m);
-        const uint64_t above = acc + wg_prefix_u64(inc, m, sh.r64[0]);
-        const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
-        const uint64_t bc = ballot(cond), bn = ballot(cn > 0);
-        if (lane == 0) {
-            sh.r32[1][wave] = bc ? 64u - (uint32_t)__builtin_clzll(bc) : 0u;    // highest lane + 1
-            sh.r32[2][wave] = bn ? (uint32_t)__builtin_ffsll((long long)bn) : 0u;   // lowest lane + 1
-        }
-        __syncthreads();
-        // the lowest qualifying bin (highest t); else the top non-empty bin (lowest t)
-        int sel_t = -1;
+        // lane l: bins 255 - 4l down to 252 - 4l
+        const llima_u32x4 c4 = ((const llima_u32x4*)hc)[63u - lane];
+        const uint32_t cs[4] = {c4.w, c4.z, c4.y, c4.x};
+        uint64_t ms[4];
 #pragma unroll
-        for (int w2 = LLIMA_WAVES - 1; w2 >= 0; --w2)
-            if (sel_t < 0 && sh.r32[1][w2]) sel_t = w2 * 64 + (int)sh.r32[1][w2] - 1;
-        if (sel_t < 0) {
+        for (int i = 0; i < 4; ++i) ms[i] = hm[255u - 4u * lane - (uint32_t)i];
+        const uint32_t nxt = buf == 0u ? 2u : buf - 1u;
+        sh.hcnt[nxt][t] = 0;
+        sh.hmass[nxt][t] = 0;
+        const uint64_t m4 = ms[0] + ms[1] + ms[2] + ms[3];
+        uint64_t ab = acc + wave_incl_scan_u64(m4) - m4;           // mass above the lane's top bin
+        // last qualifying bin of the lane (lowest key), first non-empty bin
+        int qi = -1, ni = -1;
+        uint64_t qab = 0, nab = 0;
+        uint32_t qcn = 0, ncn = 0;
 #pragma unroll
-            for (int w2 = 0; w2 < LLIMA_WAVES; ++w2)
-                if (sel_t < 0 && sh.r32[2][w2]) sel_t = w2 * 64 + (int)sh.r32[2][w2] - 1;
+        for (int i = 0; i < 4; ++i) {
+            const bool ne = cs[i] > 0u;
+            const bool q = ne && (((llima_u128)ab << 32) < PZ);
+            qi = q ? i : qi; qab = q ? ab : qab; qcn = q ? cs[i] : qcn;
+            const bool first = ne && ni < 0;
+            ni = first ? i : ni; nab = first ? ab : nab; ncn = first ? cs[i] : ncn;
+            ab += ms[i];
         }
-        if (sel_t < 0) sel_t = 0;
-        if ((int)t == sel_t) sh.sel64[0] = above;
-        __syncthreads();
-        d.prefix |= (255u - (uint32_t)sel_t) << lo;
+        const uint64_t bq = ballot(qi >= 0), bn = ballot(ni >= 0);
+        uint32_t L, sel;
+        uint64_t sab;
+        uint32_t scn;
+        if (bq) {                                   // the lowest qualifying bin: highest lane
+            L = 63u - (uint32_t)__builtin_clzll(bq);
+            sel = 255u - 4u * L - (uint32_t)readlane((uint32_t)qi, L);
+            sab = readlane64(qab, L);
+            scn = readlane(qcn, L);
+        } else {                                    // else the top non-empty bin: lowest lane
+            L = bn ? (uint32_t)__builtin_ffsll((long long)bn) - 1u : 0u;
+            sel = bn ? 255u - 4u * L - (uint32_t)readlane((uint32_t)ni, L) : 255u;
+            sab = bn ? readlane64(nab, L) : acc;
+            scn = bn ? readlane(ncn, L) : 0u;
+        }
+        d.prefix |= sel << lo;
         d.pmask |= bmask << lo;
         d.top = lo - 1;
-        acc = sh.sel64[0];
-        hc[t] = 0;
-        hm[t] = 0;
-        buf ^= 1;
+        acc = sab;
+        buf = buf == 2u ? 0u : buf + 1u;
+        if (scn == 1u && d.top >= 0) {
+            // one key left in the selected bin: later rounds would select it
+            // digit by digit (its mass above is the same at every level), so it
+            // is theta
+            uint32_t kk = 0;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                const bool in = (key[j] != 0u) & ((key[j] & d.pmask) == d.prefix);
+                kk = in && key[j] > kk ? key[j] : kk;
+            }
+            return block_max_u32(kk, sh.bs);
+        }
     }
     __syncthreads();
     return d.prefix;
@@ -1108,7 +1132,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     for (int j = 0; j < EPT; ++j) {
         key[j] = 0;
         if (t + (uint32_t)j * LLIMA_WG < N) {
-            const uint32_t k = f32_key(x[j] / c.T);
+            const uint32_t k = f32_key(c.T == 1.0f ? x[j] : x[j] / c.T);   // x / 1 is x
             key[j] = k > LLIMA_KEY_NEG_INF ? k : 0u;
         }
         kmx = key[j] > kmx ? key[j] : kmx;
@@ -1638,7 +1662,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         } else if (ov == 0u) {
             done = fin_direct(P, row, c, kr, idv, N, ~nkmin, kmax, gkey, hid, sh);
         }
-        if (!done && ov < 2u) {
+        // the gather and full-row paths are cold: their code is placed after
+        // the direct path's, which then streams through the instruction cache
+        if (__builtin_expect(!done && ov < 2u, 0)) {
             // ---- 3. gather: candidates into LDS in id order (element f at f + f / 16)
             __syncthreads();
             if (wave == 0) {
@@ -1663,7 +1689,6 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
             __syncthreads();
             const uint32_t NG = sh.hn;
             if (NG <= SMP_FIN_CAP) {
-                const uint32_t pre_c = pre - SMP_HDR;      // candidates read in 1.
                 if (mine) {
                     const uint32_t n_c = sh.ccount[ch], o_c = sh.coff[ch];
 #pragma unroll
@@ -1681,6 +1706,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
                     }
                 }
                 // chunks with more candidates than the first round covered
+                const uint32_t pre_c = pre - SMP_HDR;
                 for (int cc = (int)wave; cc < S; cc += LLIMA_WAVES) {
                     const uint32_t n_c = sh.ccount[cc];
                     if (n_c > pre_c) {
@@ -1700,7 +1726,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
             }
         }
     }
-    if (!done) finish_full_row<TL>(P, row, c, sh);
+    if (__builtin_expect(!done, 0)) finish_full_row<TL>(P, row, c, sh);
 }
 
 // ================================================================== host side
