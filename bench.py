@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--workload", default="batched_penalties",
                     choices=["batched_penalties", "single_row", "constrained",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
-                             "speculative"])
+                             "speculative", "score_bf16", "mtp_masked_argmax"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -109,6 +109,49 @@ def main():
         dtype = "f32"
         kernel_names = ["vr_rowmax", "vr_rowsum", "vr_drawsum", "vr_final"]
         config = {"workload": "speculative", "B": B, "draft_len": D, "V": V}
+    elif name in ("score_bf16", "mtp_masked_argmax"):
+        lg = w["logits"]
+        B, V = lg.shape
+        dt = _lib.LLIMA_BF16
+        per = lg.nbytes
+        nbuf = max(2, int(np.ceil(args.rotate_gib * 2**30 / per)))
+        g = torch.Generator(device=dev)
+        g.manual_seed(2001)
+        bufs = [torch.from_numpy(lg.view(np.int16)).to(dev).view(torch.bfloat16)]
+        for i in range(1, nbuf):
+            x = torch.randn((B, V), generator=g, device=dev) * 5.0
+            bufs.append((30.0 * torch.tanh(x / 30.0)).to(torch.bfloat16).contiguous())
+        rows = B
+        unit_rows = "rows/s"
+        dtype = "bf16"
+        if name == "score_bf16":
+            tg = torch.from_numpy(w["targets"]).to(dev)
+            lp = torch.empty(B, dtype=torch.float64, device=dev)
+            gr = torch.empty(B, dtype=torch.int32, device=dev)
+            nws = L.llima_score_logits_workspace_bytes(B, V, dt)
+            ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+            for x in bufs:
+                launches.append(lambda sp, x=x: check(L.llima_score_logits(
+                    x.data_ptr(), dt, B, V, V, tg.data_ptr(), lp.data_ptr(), gr.data_ptr(),
+                    ws.data_ptr(), nws, sp), "llima_score_logits"))
+            alg_bytes = lg.nbytes + B * (4 + 8 + 4)
+            kernel_names = ["score_sweep", "score_finish"]
+            config = {"workload": name, "B": B, "V": V, "logits_dtype": "bf16"}
+        else:
+            C, k = w["centroids"].shape[1], w["top_k"]
+            cent = torch.from_numpy(w["centroids"].view(np.int16)).to(dev)
+            order = torch.from_numpy(w["ordering"].view(np.int32)).to(dev)
+            ids_o = torch.empty(B, dtype=torch.int32, device=dev)
+            st_o = torch.empty(B, dtype=torch.int32, device=dev)
+            for x in bufs:
+                launches.append(lambda sp, x=x: check(L.llima_mtp_masked_argmax(
+                    cent.data_ptr(), C, C, order.data_ptr(), k, x.data_ptr(), dt, B, V, V,
+                    ids_o.data_ptr(), st_o.data_ptr(), None, sp), "llima_mtp_masked_argmax"))
+            # centroid row, the selected ordering runs and their logits, the outputs
+            alg_bytes = B * (C * 2 + k * (V // C) * (4 + 2) + 4 + 4)
+            kernel_names = ["mtp_masked_argmax"]
+            config = {"workload": name, "B": B, "V": V, "centroids": C, "top_k": k,
+                      "logits_dtype": "bf16"}
     else:
         lg = w["logits"]
         B, V = lg.shape
@@ -292,6 +335,21 @@ def cpu_baseline(name, w, seconds, greedy_variant):
             reps += 1
         unit = "sequences/s"
         sample = f"{reps} x verify_rejection over the full [16,8,128256] batch"
+    elif name in ("score_bf16", "mtp_masked_argmax"):
+        # one row per call, as the reference's functions (single thread)
+        threads = 1
+        lg = w["logits"]
+        while time.time() < t_end or reps == 0:
+            r = reps % lg.shape[0]
+            if name == "score_bf16":
+                orc.score_logits(lg[r], int(w["targets"][r]))
+            else:
+                cand = orc.select_candidate_tokens(w["centroids"][r], w["ordering"], w["top_k"])
+                orc.masked_argmax(lg[r], cand)
+            n_rows += 1
+            reps += 1
+        unit = "rows/s"
+        sample = f"{reps} rows of the {list(lg.shape)} batch, one call per row"
     else:
         lg = w["logits"]
         if name == "argmax_bf16":

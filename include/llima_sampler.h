@@ -39,6 +39,11 @@
  *   llima_verify_rejection <- no reference counterpart (the reference verifies
  *                            drafts greedily, eagle_helpers.hpp:153-195); the
  *                            greedy limit equals resolve_draft_tokens.
+ *   llima_score_logits    <- score_logits             sima_lmm/devkit/cpp/language_model.cpp:29-62
+ *   llima_mtp_masked_argmax <- select_candidate_tokens
+ *                            sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:113-167,
+ *                            _argmax_gemma4_mtp_masked_row
+ *                            sima_lmm/devkit/cpp/language_model_gemma4_mtp.cpp:31-97
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -158,6 +163,41 @@ int llima_verify_rejection(const float* target_logits, const float* draft_logits
                            const float* u_accept, const float* u_resample,
                            int32_t* accepted_len, int32_t* emitted, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* Log-likelihood of B target tokens: replaces score_logits
+ * (sima_lmm/devkit/cpp/language_model.cpp:29-62), one row per call there.
+ * targets [B] int32 (device).  out_logprob[B] (double) = x_t - (max + log sum
+ * exp(x - max)); NaN when the row holds a NaN or its maximum is infinite (as
+ * the reference's double sum).  out_is_greedy[B] = 1 when the target is the
+ * first maximum, else 0; a target outside [0, V) (the reference throws
+ * std::runtime_error) gives LLIMA_E_RANGE there and a NaN log-probability. */
+size_t llima_score_logits_workspace_bytes(int32_t B, int32_t V, int32_t dtype);
+int llima_score_logits(const void* logits, int32_t dtype, int32_t B, int32_t V,
+                       int64_t row_stride, const int32_t* targets, double* out_logprob,
+                       int32_t* out_is_greedy, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Gemma4 MTP masked argmax of B rows: replaces select_candidate_tokens
+ * (sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:113-167) and
+ * LanguageModel::_argmax_gemma4_mtp_masked_row
+ * (sima_lmm/devkit/cpp/language_model_gemma4_mtp.cpp:31-97).
+ * centroid_logits: bf16 [B][centroid_stride] (C used, C <= 8192);
+ * token_ordering: [V] token ids, V / C per centroid; the top_k centroids by
+ * (value desc, index asc) give the candidate tokens, and out_ids[B] receives
+ * the candidate with the greatest logit (lowest token id on equal values; NaN
+ * never selected).  logits may be NULL (selection only).  out_candidates
+ * (nullable, [B][top_k * V / C]) receives the candidates in the reference's
+ * order (centroid rank, then ordering position).  out_status (nullable, [B]):
+ * LLIMA_OK, LLIMA_E_RANGE for an ordering entry >= V among the candidates, or
+ * LLIMA_E_INVAL when no candidate has a non-NaN logit (both are
+ * std::runtime_error in the reference); out_ids is then -1.  Returns
+ * LLIMA_E_INVAL when V is not a multiple of C or top_k is outside [1, C]
+ * (the reference's own checks).  Needs no workspace. */
+int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_stride, int32_t C,
+                            const uint32_t* token_ordering, int32_t top_k, const void* logits,
+                            int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
+                            int32_t* out_ids, int32_t* out_status, uint32_t* out_candidates,
+                            void* stream);
 
 const char* llima_status_string(int status);
 int llima_abi_version(void);

@@ -12,6 +12,9 @@ the buffers handed to it (inputs must already be on the GPU).
   evaluate_posterior / verify_tree    eagle_helpers.hpp:153-195, language_model_eagle3.cpp:530-567
   sample(...)                         the sampler stages (no reference counterpart)
   verify_rejection(...)               stochastic draft verification (no reference counterpart)
+  score_logits(logits, target)        language_model.cpp:29-62
+  select_candidate_tokens(...)        gemma4_mtp_helpers.cpp:113-167
+  argmax_gemma4_mtp_masked_row(s)     language_model_gemma4_mtp.cpp:31-97
 
 Errors: the reference throws std::invalid_argument / std::runtime_error; here
 ValueError / RuntimeError are raised for the same conditions.
@@ -30,7 +33,8 @@ from ._lib import check, lib
 __all__ = [
     "SamplerConfig", "argmax", "argmax_bf16", "calc_next_token_id", "argmax_lm_head_rows",
     "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
-    "Workspace",
+    "Workspace", "score_logits", "select_candidate_tokens", "argmax_gemma4_mtp_masked_rows",
+    "argmax_gemma4_mtp_masked_row",
 ]
 
 
@@ -311,3 +315,115 @@ def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
                                        em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
           "llima_verify_rejection")
     return acc, em
+
+
+def score_logits(logits: torch.Tensor, target):
+    """score_logits (language_model.cpp:29-62): the log-softmax of the target
+    token and whether the target is the (first) argmax.
+
+    logits [V] with an int target -> (logprob float, is_greedy bool), raising
+    RuntimeError for a target outside the vocabulary as the reference does;
+    logits [B, V] with int targets [B] -> (float64 [B], bool [B]) tensors."""
+    single = logits.dim() == 1
+    x = _rows2d(logits)
+    B, V = x.shape
+    dev = x.device
+    if single:
+        t = int(target)
+        if t < 0 or t >= V:
+            raise RuntimeError(f"Target token id {t} is outside logits vocabulary size {V}")
+        tg = torch.full((1,), t, dtype=torch.int32, device=dev)
+    else:
+        tg = torch.as_tensor(target).to(device=dev, dtype=torch.int32).contiguous().reshape(-1)
+        if tg.numel() != B:
+            raise ValueError("one target per row is required")
+    _on_gpu(x, tg)
+    lp = torch.empty(B, dtype=torch.float64, device=dev)
+    gr = torch.empty(B, dtype=torch.int32, device=dev)
+    dt = _dtype_code(x)
+    ws = Workspace.get(dev, "score", lib().llima_score_logits_workspace_bytes(B, V, dt))
+    check(lib().llima_score_logits(x.data_ptr(), dt, B, V, x.stride(0), tg.data_ptr(),
+                                   lp.data_ptr(), gr.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   _stream(dev)), "llima_score_logits")
+    if single:
+        return float(lp[0]), bool(gr[0] == 1)
+    if bool((gr < 0).any()):
+        raise RuntimeError(f"a target token id is outside logits vocabulary size {V}")
+    return lp, gr == 1
+
+
+def _mtp_args(centroid_logits: torch.Tensor, token_ordering, top_k: int):
+    c = centroid_logits
+    if c.dim() == 1:
+        c = c.unsqueeze(0)
+    if c.dtype != torch.bfloat16 or c.dim() != 2:
+        raise ValueError("centroid_logits must be bfloat16 [C] or [B, C]")
+    if c.stride(-1) != 1:
+        c = c.contiguous()
+    o = torch.as_tensor(token_ordering)
+    if o.dtype == torch.int64:
+        o = (o & 0xFFFFFFFF).to(torch.int32)         # uint32 bit patterns
+    o = o.to(device=c.device, dtype=torch.int32).contiguous().reshape(-1)
+    C, V = c.shape[1], o.numel()
+    # the reference's own argument checks (gemma4_mtp_helpers.cpp:118-128)
+    if C == 0 or V == 0 or V % C != 0:
+        raise RuntimeError("Gemma4 masked lm_head vocabulary must divide evenly across centroids")
+    if top_k <= 0 or top_k > C:
+        raise RuntimeError("Invalid Gemma4 masked lm_head centroid top-k")
+    if C > 8192:
+        raise ValueError("at most 8192 centroids per row")
+    _on_gpu(c, o)
+    return c, o, C, V
+
+
+def _mtp_status(st: torch.Tensor):
+    s = st.tolist()
+    if any(v == _lib.LLIMA_E_RANGE for v in s):
+        raise RuntimeError("Gemma4 token_ordering contains an out-of-range token ID")
+    if any(v == _lib.LLIMA_E_INVAL for v in s):
+        raise RuntimeError("Gemma4 masked lm_head selected no token")
+
+
+def select_candidate_tokens(centroid_logits: torch.Tensor, token_ordering, top_k_centroids: int):
+    """select_candidate_tokens (gemma4_mtp_helpers.cpp:113-167): the tokens of
+    the top_k centroids by (value desc, index asc), in that order.  One row [C]
+    -> list of ints; rows [B, C] -> int32 [B, top_k * V / C]."""
+    c, o, C, V = _mtp_args(centroid_logits, token_ordering, int(top_k_centroids))
+    B, k = c.shape[0], int(top_k_centroids)
+    cand = torch.empty((B, k * (V // C)), dtype=torch.int32, device=c.device)
+    st = torch.empty(B, dtype=torch.int32, device=c.device)
+    check(lib().llima_mtp_masked_argmax(c.data_ptr(), c.stride(0), C, o.data_ptr(), k, None,
+                                        _lib.LLIMA_BF16, B, V, V, None, st.data_ptr(),
+                                        cand.data_ptr(), _stream(c.device)),
+          "llima_mtp_masked_argmax")
+    _mtp_status(st)
+    return cand[0].tolist() if centroid_logits.dim() == 1 else cand
+
+
+def argmax_gemma4_mtp_masked_rows(centroid_logits: torch.Tensor, token_ordering, top_k: int,
+                                  logits: torch.Tensor):
+    """_argmax_gemma4_mtp_masked_row (language_model_gemma4_mtp.cpp:31-97) over
+    B rows: the candidate token (select_candidate_tokens) with the greatest
+    logit, the lowest token id on equal values.  centroid_logits bf16 [B, C],
+    token_ordering [V], logits [B, V] -> int32 [B]."""
+    c, o, C, V = _mtp_args(centroid_logits, token_ordering, int(top_k))
+    x = _rows2d(logits)
+    if x.shape[0] != c.shape[0] or x.shape[1] != V:
+        raise ValueError("logits must be [B, V] with V = len(token_ordering)")
+    _on_gpu(x)
+    B = x.shape[0]
+    ids = torch.empty(B, dtype=torch.int32, device=x.device)
+    st = torch.empty(B, dtype=torch.int32, device=x.device)
+    check(lib().llima_mtp_masked_argmax(c.data_ptr(), c.stride(0), C, o.data_ptr(), int(top_k),
+                                        x.data_ptr(), _dtype_code(x), B, V, x.stride(0),
+                                        ids.data_ptr(), st.data_ptr(), None, _stream(x.device)),
+          "llima_mtp_masked_argmax")
+    _mtp_status(st)
+    return ids
+
+
+def argmax_gemma4_mtp_masked_row(centroid_logits: torch.Tensor, token_ordering, top_k: int,
+                                 logits: torch.Tensor) -> int:
+    """One row of argmax_gemma4_mtp_masked_rows: centroid_logits [C], logits [V]."""
+    return int(argmax_gemma4_mtp_masked_rows(centroid_logits.reshape(1, -1), token_ordering,
+                                             top_k, logits.reshape(1, -1))[0])

@@ -136,10 +136,34 @@ def large_vocab_bf16(B=256, V=262144, H=512, seed=1005):
                 bitmask=None, cfg=cfg)
 
 
+def score_bf16(B=256, V=262144, seed=1006):
+    """Log-likelihood scoring (score_logits) of B target ids over the bf16
+    Gemma-head rows of large_vocab_bf16 (same logits, seeded targets)."""
+    w = large_vocab_bf16(B=B, V=V, H=1)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    targets = rng.integers(0, V, size=B, dtype=np.int32)
+    return dict(name="score_bf16", logits=w["logits"], targets=targets)
+
+
+def mtp_masked_argmax(B=16, C=2048, V=262144, top_k=32, seed=1007):
+    """Gemma4 MTP drafting: B rows of bf16 centroid logits [B, C] (2048 centroids,
+    top-32, the reference's defaults: vlm_config.py:780-781), a seeded token
+    ordering (a permutation of V) and bf16 N(0, 5^2) soft-capped logits [B, V]."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cent = f32_to_bf16_bits(_normal(rng, (B, C), 2.0))
+    ordering = rng.permutation(V).astype(np.uint32)
+    x = _normal(rng, (B, V), 5.0)
+    x = (np.float32(30.0) * np.tanh(x / np.float32(30.0))).astype(np.float32)
+    return dict(name="mtp_masked_argmax", logits=f32_to_bf16_bits(x), centroids=cent,
+                ordering=ordering, top_k=top_k)
+
+
 WORKLOADS = {
     "single_row": single_row,
     "batched_penalties": batched_penalties,
     "constrained": constrained,
     "speculative": speculative,
     "large_vocab_bf16": large_vocab_bf16,
+    "score_bf16": score_bf16,
+    "mtp_masked_argmax": mtp_masked_argmax,
 }

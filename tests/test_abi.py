@@ -18,7 +18,8 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ["llima_argmax", "llima_sample", "llima_verify_greedy", "llima_verify_tree",
-              "llima_verify_rejection", "llima_workspace_init"]:
+              "llima_verify_rejection", "llima_workspace_init", "llima_score_logits",
+              "llima_mtp_masked_argmax"]:
         assert n in names
 
 
@@ -45,6 +46,17 @@ def test_host_only_entry_points():
     assert L.llima_verify_rejection(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 1, (1 << 22) + 4,
                                     ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                     ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == -1
+    p = ctypes.c_void_p(16)
+    assert L.llima_score_logits(None, 0, 1, 10, 10, p, p, p, p, 1 << 20, None) == -1
+    assert L.llima_score_logits(p, 0, 1, 10, 10, p, p, p, None, 0, None) == -4
+    assert L.llima_score_logits_workspace_bytes(256, 262144, 1) > 0
+    # the reference's own checks: V a multiple of C, top_k in [1, C]
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 2, p, 1, 1, 10, 10, p, p, None, None) == -1
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 5, p, 1, 1, 8, 8, p, p, None, None) == -1
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 0, p, 1, 1, 8, 8, p, p, None, None) == -1
+    assert L.llima_mtp_masked_argmax(p, 9000, 9000, p, 1, p, 1, 1, 9000, 9000, p, p, None,
+                                     None) == -1              # beyond 8192 centroids
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, None, 1, 1, 8, 8, None, p, None, None) == -1
 
 
 def test_config_struct_layout_matches_header():

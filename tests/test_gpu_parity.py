@@ -390,3 +390,144 @@ def test_workspace_reuse_across_shapes(gpu, oracle):
         acc, em = llima_amd.verify_greedy(_t(tgt, gpu), _t(dr, gpu))
         eacc, eem = oracle.verify_greedy(tgt, dr)
         assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
+
+
+# ----------------------------------------------------------------- score_logits
+# Tolerance: the reference sums exp(x - max) in double; the kernel's terms are
+# fp32 exp2 values accumulated in double, so the log-probability agrees to about
+# 1e-6 (asserted: 1e-5 absolute, the fp32 probability tolerance).  The argmax
+# flag, NaN and infinity outcomes are exact.
+SCORE_TOL = 1e-5
+
+
+def _score_check(got_lp, got_g, x, targets, oracle):
+    for r, t in enumerate(targets):
+        elp, eg = oracle.score_logits(x[r], int(t))
+        g = float(got_lp[r])
+        if np.isnan(elp):
+            assert np.isnan(g), (r, t, g)
+        elif np.isinf(elp):
+            assert g == elp, (r, t, g, elp)
+        else:
+            assert abs(g - elp) <= SCORE_TOL, (r, t, g, elp)
+        assert bool(got_g[r]) == eg, (r, t)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,V", [(1, 1), (3, 7), (4, 5003), (8, 128256), (2, 262144)])
+def test_score_logits_parity(gpu, oracle, dtype, B, V):
+    import torch
+    import llima_amd
+    _say("score_logits", dtype, B, V)
+    rng = np.random.default_rng(B * 7 + V)
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    x[:, rng.integers(0, V, size=3)] = x.max() + 1          # ties at the maximum
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    xf = x if dtype == "f32" else wl.bf16_bits_to_f32(x)
+    am = np.argmax(xf, axis=1)
+    for targets in [am, rng.integers(0, V, size=B)]:
+        lp, g = llima_amd.score_logits(_t(x, gpu), torch.from_numpy(targets.astype(np.int32)))
+        _score_check(_np(lp), _np(g), x, targets, oracle)
+
+
+def test_score_logits_edges(gpu, oracle):
+    import torch
+    import llima_amd
+    _say("score_logits edges")
+    V = 10000
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 2, (8, V)).astype(np.float32)
+    x[0, 77] = np.nan                      # any NaN -> NaN
+    x[1, :] = -np.inf                      # all -inf -> NaN, argmax 0
+    x[2, 5] = np.inf                       # infinite maximum -> NaN
+    x[3, 9] = -np.inf                      # -inf target -> -inf
+    x[4, :] = 1.5                          # all equal: argmax 0
+    x[5, 4096:8192] = -np.inf              # a whole chunk of -inf
+    x[6, :] = np.nan
+    targets = np.array([3, 0, 5, 9, 0, 100, 1, 9999], np.int32)
+    lp, g = llima_amd.score_logits(_t(x, gpu), torch.from_numpy(targets))
+    _score_check(_np(lp), _np(g), x, targets, oracle)
+    # strided rows
+    xs = _t(x, gpu)[2:8, 7:9007]
+    lp, g = llima_amd.score_logits(xs, torch.from_numpy(targets[2:8] % 9000))
+    _score_check(_np(lp), _np(g), x[2:8, 7:9007], targets[2:8] % 9000, oracle)
+    # one row, the reference's signature
+    lp1, g1 = llima_amd.score_logits(_t(x[3], gpu), 9)
+    assert lp1 == -np.inf and not g1
+    with pytest.raises(RuntimeError):
+        llima_amd.score_logits(_t(x[3], gpu), V)
+    with pytest.raises(RuntimeError):
+        llima_amd.score_logits(_t(x[:2], gpu), torch.tensor([0, V], dtype=torch.int32))
+
+
+# ----------------------------------------------------------------- Gemma4 MTP masked argmax
+def _mtp_expected(oracle, cent_bits, ordering, k, x):
+    cand = oracle.select_candidate_tokens(cent_bits, ordering, k)
+    return cand, oracle.masked_argmax(x, cand)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,C,V,k", [(4, 2048, 262144, 32), (3, 16, 64, 5), (2, 100, 1000, 100),
+                                     (5, 8192, 65536, 7), (1, 1, 9, 1)])
+def test_mtp_masked_argmax_parity(gpu, oracle, dtype, B, C, V, k):
+    import llima_amd
+    _say("mtp masked argmax", dtype, B, C, V, k)
+    rng = np.random.default_rng(C + V + k)
+    cent = wl.f32_to_bf16_bits(rng.integers(-20, 21, size=(B, C)).astype(np.float32) * 0.5)  # ties
+    ordering = rng.permutation(V).astype(np.uint32)
+    x = rng.integers(-40, 41, size=(B, V)).astype(np.float32) * np.float32(0.25)              # ties
+    x[0, rng.integers(0, V, size=V // 3)] = -np.inf
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    ids = llima_amd.argmax_gemma4_mtp_masked_rows(_t(cent, gpu), _t(ordering, gpu), k, _t(x, gpu))
+    cands = llima_amd.select_candidate_tokens(_t(cent, gpu), _t(ordering, gpu), k)
+    for r in range(B):
+        ec, eid = _mtp_expected(oracle, cent[r], ordering, k, x[r])
+        assert _np(cands[r]).astype(np.uint32).tolist() == ec.tolist(), r
+        assert int(_np(ids)[r]) == eid, r
+
+
+def test_mtp_masked_argmax_reference_vectors_and_errors(gpu, oracle):
+    import json
+    import os
+    import torch
+    import llima_amd
+    _say("mtp reference vectors")
+    path = os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")
+    v = json.load(open(path))
+    for case in v["select_candidate_tokens"]:
+        c = wl.f32_to_bf16_bits(np.array(case["centroid_logits"], np.float32))
+        got = llima_amd.select_candidate_tokens(_t(c, gpu), _t(np.array(case["token_ordering"],
+                                                                        np.uint32), gpu),
+                                                case["top_k"])
+        assert got == case["expected"]
+    for case in v["select_candidate_tokens_errors"]:
+        c = wl.f32_to_bf16_bits(np.array(case["centroid_logits"], np.float32))
+        with pytest.raises(RuntimeError):
+            llima_amd.select_candidate_tokens(_t(c, gpu), _t(np.array(case["token_ordering"],
+                                                                      np.uint32), gpu),
+                                              case["top_k"])
+    # no candidate with a number -> the reference's "selected no token"
+    cent = wl.f32_to_bf16_bits(np.array([1, 3, 2, 0], np.float32))
+    order = np.arange(8, dtype=np.uint32)
+    x = np.zeros(8, np.float32)
+    x[2:4] = np.nan
+    with pytest.raises(RuntimeError):
+        llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(order, gpu), 1, _t(x, gpu))
+    x[3] = -np.inf                                           # -inf is a candidate value
+    assert llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(order, gpu), 1,
+                                                  _t(x, gpu)) == 3
+    x[:] = 7.0                                               # equal values -> lowest token id
+    assert llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(order, gpu), 4,
+                                                  _t(x, gpu)) == 0
+    bad = order.copy()
+    bad[5] = 8                                               # out-of-range id in a selected run
+    with pytest.raises(RuntimeError):
+        llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(bad, gpu), 3, _t(x, gpu))
+    bad = order.copy()
+    bad[7] = 0xFFFFFFFF                                      # in an unselected run: ignored
+    assert llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(bad, gpu), 3,
+                                                  _t(x, gpu)) == 0
+    with pytest.raises(RuntimeError):
+        llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(order, gpu), 5, _t(x, gpu))

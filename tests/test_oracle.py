@@ -171,6 +171,26 @@ def test_score_logits_against_scipy(oracle):
         oracle.score_logits(x, 4096)
 
 
+def test_score_logits_nan_and_infinities(oracle):
+    """The double sum of exp(x - max) is NaN with a NaN value (exp(NaN)), with an
+    infinite maximum (inf - inf) and with an all -inf row (-inf - -inf); a -inf
+    target under a finite maximum has log-probability -inf."""
+    x = np.array([0.5, 2.0, -1.0, 2.0], np.float32)
+    lp, g = oracle.score_logits(x, 3)
+    assert abs(lp - (2.0 - (2.0 + np.log(np.exp(-1.5) + 2 + np.exp(-3.0))))) < 1e-15
+    assert not g                                    # the first maximum is index 1
+    assert oracle.score_logits(x, 1)[1]
+    y = x.copy(); y[2] = np.nan
+    assert np.isnan(oracle.score_logits(y, 1)[0])
+    y = x.copy(); y[0] = np.inf
+    assert np.isnan(oracle.score_logits(y, 0)[0]) and oracle.score_logits(y, 0)[1]
+    y = np.full(4, -np.inf, np.float32)
+    lp, g = oracle.score_logits(y, 0)
+    assert np.isnan(lp) and g
+    y = x.copy(); y[2] = -np.inf
+    assert oracle.score_logits(y, 2)[0] == -np.inf
+
+
 def test_masked_argmax(oracle):
     row = np.array([0, 5, 3, 5, 9, 1], np.float32)
     assert oracle.masked_argmax(row, [3, 1, 2]) == 1       # equal value -> lower token id
