@@ -90,8 +90,8 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_sweep(ArgmaxParams P) {
     constexpr int EPL = 16 / sizeof(TL);
     constexpr int NL = E / EPL;
     constexpr int CHUNK = LLIMA_WG * E;
-    __shared__ BlockScratch bs;
     __shared__ uint32_t bad_splits;
+    __shared__ uint32_t wmax[LLIMA_WAVES], wfi[LLIMA_WAVES];
 
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
@@ -134,30 +134,49 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_sweep(ArgmaxParams P) {
         }
     }
 
-    float best = -__builtin_inff();
-    uint32_t bidx = 0xFFFFFFFFu;
+    // the chunk maximum first (one max per value; values past the row are
+    // -inf), then its first index, searched only by the threads that hold it
+    float t[NL * EPL];
+    const bool full = c1 - c0 == CHUNK;
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-        float t[EPL];
         const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
-        if constexpr (sizeof(TL) == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t[e] = __uint_as_float(w4[e]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                t[2 * e] = __uint_as_float(w4[e] << 16);
-                t[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
-            }
+        for (int e = 0; e < EPL; ++e) {
+            float f;
+            if constexpr (sizeof(TL) == 4) f = __uint_as_float(w4[e]);
+            else f = __uint_as_float((e & 1) ? (w4[e >> 1] & 0xFFFF0000u) : (w4[e >> 1] << 16));
+            t[j * EPL + e] = full || i0 + e < c1 ? f : -__builtin_inff();
         }
-#pragma unroll
-        for (int e = 0; e < EPL; ++e)
-            if (t[e] > best && i0 + e < c1) { best = t[e]; bidx = (uint32_t)(i0 + e); }
     }
-    const uint64_t key = block_max_u64(pack_best(best, bidx), bs);   // barrier: bad_splits final
+    float mt = -__builtin_inff();                  // fmaxf ignores NaN: a NaN never wins
+#pragma unroll
+    for (int e = 0; e < NL * EPL; ++e) mt = __builtin_fmaxf(mt, t[e]);
+    const uint32_t km = wave_max_u32(mt > -__builtin_inff() ? f32_key(mt) : 0u);
+    if (lane_id() == 0) wmax[threadIdx.x >> 6] = km;
+    __syncthreads();                               // also: bad_splits final
+    uint32_t kc = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) kc = wmax[w] > kc ? wmax[w] : kc;
+    const float mc = kc ? key_f32(kc) : -__builtin_inff();
+    uint32_t fi = 0xFFFFFFFFu;
+    if (kc && mt == mc) {
+#pragma unroll
+        for (int j = NL - 1; j >= 0; --j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+#pragma unroll
+            for (int e = EPL - 1; e >= 0; --e) fi = t[j * EPL + e] == mc ? (uint32_t)(i0 + e) : fi;
+        }
+    }
+    fi = wave_min_u32(fi);
+    if (lane_id() == 0) wfi[threadIdx.x >> 6] = fi;
+    __syncthreads();
     if (threadIdx.x == 0) {
-        P.keys[(size_t)row * P.S + chunk] = key;
+        uint32_t first = 0xFFFFFFFFu;
+#pragma unroll
+        for (int w = 0; w < LLIMA_WAVES; ++w) first = wfi[w] < first ? wfi[w] : first;
+        P.keys[(size_t)row * P.S + chunk] = kc ? (((uint64_t)kc << 32) | (uint32_t)~first) : 0ull;
         P.flags[(size_t)row * P.S + chunk] = bad_splits;
     }
 }

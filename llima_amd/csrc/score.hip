@@ -61,25 +61,14 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
         }));
 }
 
-__device__ __forceinline__ double block_sum_f64(double v, double* w) {
-    v = wave_sum_f64(v);
-    if (lane_id() == 0) w[wave_id()] = v;
-    __syncthreads();
-    double t = 0.0;
-#pragma unroll
-    for (int i = 0; i < LLIMA_WAVES; ++i) t += w[i];
-    return t;
-}
-
 template <typename TL, int E, bool VEC>
 __global__ __launch_bounds__(LLIMA_WG) void score_sweep(ScoreParams P) {
     constexpr int EPL = 16 / sizeof(TL);
     constexpr int NL = E / EPL;
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr float LOG2E = 1.44269504088896340736f;
-    __shared__ BlockScratch bs;
     __shared__ double wsum[LLIMA_WAVES];
-    __shared__ uint32_t wnan[LLIMA_WAVES];
+    __shared__ uint32_t wmax[LLIMA_WAVES], wfi[LLIMA_WAVES], wnan[LLIMA_WAVES];
 
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
@@ -122,18 +111,11 @@ __global__ __launch_bounds__(LLIMA_WG) void score_sweep(ScoreParams P) {
             x[j * EPL + e] = i0 + e < c1 ? f : -__builtin_inff();
         }
     }
-    // per thread: its maximum m_t (fmaxf ignores NaN), the first index holding
-    // it, and s_t = sum of exp(x - m_t) (NaN when a value is NaN or m_t = +inf)
+    // per thread: its maximum m_t (fmaxf ignores NaN) and s_t = sum of
+    // exp(x - m_t) (NaN when a value is NaN or m_t = +inf)
     float mt = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < E; ++e) mt = __builtin_fmaxf(mt, x[e]);
-    uint32_t bidx = 0;
-#pragma unroll
-    for (int j = NL - 1; j >= 0; --j) {
-        const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
-#pragma unroll
-        for (int e = EPL - 1; e >= 0; --e) bidx = x[j * EPL + e] == mt ? (uint32_t)(i0 + e) : bidx;
-    }
     float s = 0.0f;
     uint32_t nan = 0;
     if (mt > -__builtin_inff()) {
@@ -143,21 +125,44 @@ __global__ __launch_bounds__(LLIMA_WG) void score_sweep(ScoreParams P) {
 #pragma unroll
         for (int e = 0; e < E; ++e) nan |= x[e] != x[e] ? 1u : 0u;    // NaN beside -inf only
     }
-    const uint64_t pk = mt > -__builtin_inff() ? (((uint64_t)f32_key(mt) << 32) | (uint32_t)~bidx) : 0ull;
-    const uint64_t key = block_max_u64(pk, bs);
-    const float mc = key ? key_f32((uint32_t)(key >> 32)) : -__builtin_inff();
+    // the chunk maximum m_c (one barrier: every thread reads the four waves')
+    const uint32_t km = wave_max_u32(mt > -__builtin_inff() ? f32_key(mt) : 0u);
+    if (lane_id() == 0) wmax[wave_id()] = km;
+    __syncthreads();
+    uint32_t kc = 0;
+#pragma unroll
+    for (int w = 0; w < LLIMA_WAVES; ++w) kc = wmax[w] > kc ? wmax[w] : kc;
+    const float mc = kc ? key_f32(kc) : -__builtin_inff();
+    // its first index: only threads whose maximum is m_c search their values
+    uint32_t fi = 0xFFFFFFFFu;
+    if (kc && mt == mc) {
+#pragma unroll
+        for (int j = NL - 1; j >= 0; --j) {
+            const int i0 = c0 + j * (LLIMA_WG * EPL) + (int)threadIdx.x * EPL;
+#pragma unroll
+            for (int e = EPL - 1; e >= 0; --e) fi = x[j * EPL + e] == mc ? (uint32_t)(i0 + e) : fi;
+        }
+    }
     // s_c = sum_t s_t exp(m_t - m_c); a NaN s_t (a NaN value, or an infinite
     // maximum) makes s_c NaN, which the finish reads as "NaN result"
     const float f = mt > -__builtin_inff() ? s * __builtin_amdgcn_exp2f((mt - mc) * LOG2E) : 0.0f;
+    const double ws = wave_sum_f64((double)f);
+    fi = wave_min_u32(fi);
     nan = wave_max_u32(nan);
-    if (lane_id() == 0) wnan[wave_id()] = nan;
-    const double tot = block_sum_f64((double)f, wsum);           // barrier: wnan visible
+    if (lane_id() == 0) { wsum[wave_id()] = ws; wfi[wave_id()] = fi; wnan[wave_id()] = nan; }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t n = tot != tot ? 1u : 0u;
+        double tot = 0.0;
+        uint32_t n = 0, first = 0xFFFFFFFFu;
 #pragma unroll
-        for (int w = 0; w < LLIMA_WAVES; ++w) n |= wnan[w];
+        for (int w = 0; w < LLIMA_WAVES; ++w) {
+            tot += wsum[w];
+            n |= wnan[w];
+            first = wfi[w] < first ? wfi[w] : first;
+        }
+        n |= tot != tot ? 1u : 0u;
         const size_t o = (size_t)row * P.S + chunk;
-        P.keys[o] = key;
+        P.keys[o] = kc ? (((uint64_t)kc << 32) | (uint32_t)~first) : 0ull;
         P.sums[o] = tot;
         P.flags[o] = n;
     }
