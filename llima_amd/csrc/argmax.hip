@@ -188,6 +188,8 @@ __device__ __forceinline__ int32_t row_result(const ArgmaxParams& P, int row, fl
     const uint64_t* k = P.keys + (size_t)row * P.S;
     const uint32_t* fl = P.flags + (size_t)row * P.S;
     const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    // QUARTERS: merged from (values[0], 0), read now (independent of the keys)
+    const float v0 = P.mode == LLIMA_ARGMAX_QUARTERS ? ld1<TL>(rowp, 0) : 0.0f;
     uint64_t best = 0;
     uint32_t bad = 0;
     for (int i = (int)lane_id(); i < P.S; i += 64) {
@@ -196,6 +198,9 @@ __device__ __forceinline__ int32_t row_result(const ArgmaxParams& P, int row, fl
     }
     best = wave_max_u64(best);
     bad = wave_max_u32(bad);
+    // the value is the key's; the key maps -0 to +0, so a zero is read back
+    float v = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
+    if (best && v == 0.0f) v = ld1<TL>(rowp, (int64_t)(~(uint32_t)best));
     if (bad) {
         const int V = P.V;
         const int sd = (P.split_dim <= 0 || P.split_dim >= V) ? V : P.split_dim;
@@ -208,15 +213,10 @@ __device__ __forceinline__ int32_t row_result(const ArgmaxParams& P, int row, fl
             if (x > bv) { bv = x; bi = (uint32_t)i; }
         }
         best = wave_max_u64(pack_best(bv, bi));
+        v = best ? ld1<TL>(rowp, (int64_t)(~(uint32_t)best)) : -__builtin_inff();
     }
-    int32_t id = 0;
-    float v = -__builtin_inff();
-    if (best) { id = (int32_t)(~(uint32_t)best); v = ld1<TL>(rowp, id); }
-    if (P.mode == LLIMA_ARGMAX_QUARTERS) {
-        // merged from (values[0], 0): a NaN there is kept
-        const float v0 = ld1<TL>(rowp, 0);
-        if (v0 != v0) { id = 0; v = v0; }
-    }
+    int32_t id = best ? (int32_t)(~(uint32_t)best) : 0;
+    if (P.mode == LLIMA_ARGMAX_QUARTERS && v0 != v0) { id = 0; v = v0; }   // a NaN there is kept
     *val = v;
     return id;
 }

@@ -62,13 +62,16 @@ def test_argmax_nan_split_rules(gpu, oracle):
     x[5, 7] = np.inf; x[5, 9] = np.inf
     x[6, 3] = np.nan; x[6, 10] = 1e30
     x[7, 10000] = np.nan; x[7, 12000] = 77         # NaN at the start of split 2
+    x[8, :] = -1; x[8, 10] = -0.0; x[8, 20] = 0.0  # maximum -0 first: its sign is reported
+    x[9, :] = -1; x[9, 10] = 0.0; x[9, 11] = -0.0
     for split in [0, 5000, 4096, 1]:
         for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters")]:
             ids, vals = llima_amd.argmax(_t(x, gpu), split_dim=split, mode=mname)
             eids, evals = oracle.argmax(x, split_dim=split, mode=mode)
             assert (_np(ids) == eids).all(), (split, mname, _np(ids), eids)
             g, e = _np(vals), evals
-            assert ((g == e) | (np.isnan(g) & np.isnan(e))).all(), (split, mname)
+            assert ((g.view(np.uint32) == e.view(np.uint32)) | (np.isnan(g) & np.isnan(e))).all(), \
+                (split, mname)
 
 
 def test_argmax_strided_rows(gpu, oracle):
