@@ -55,6 +55,7 @@ namespace llima {
 #define SMP_BOUND_LOWBIT 16                        // key bits below this are not searched
 #define SMP_SMALL 64                               // survivors handled one per lane
 #define SMP_WCAP 128                               // candidates a sweep wave can stage
+#define SMP_SPARSE 16                              // lanes above the bound for a sparse sweep wave
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
 
@@ -199,6 +200,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     __shared__ uint32_t xa[SC][LLIMA_WAVES];
     __shared__ uint32_t xn[SC][LLIMA_WAVES];              // candidates per wave
     __shared__ uint64_t xst[SC][LLIMA_WAVES][SMP_WCAP + 64];   // staged candidates (+ a spare slot per lane)
+    __shared__ __align__(16) float xv[SC][LLIMA_WAVES][NL * SMP_SPARSE * EPL];   // sparse waves' parked values
+    __shared__ uint32_t xl[SC][LLIMA_WAVES][SMP_SPARSE];                        // ... and their lanes
     __shared__ uint64_t xg[SC][LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
@@ -424,45 +427,94 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         // the smallest finite float stands for -inf: -inf and NaN never pass
         const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
 
-        // ---- 5. the values >= g in id order.  Each wave stages its own in LDS
-        //         (order load j, lane, value: id order inside the wave's slice;
-        //         offsets from two packed wave scans, writes to a spare slot per
-        //         lane instead of branches), then, after the one barrier, copies
-        //         its run to the region behind the runs of the waves before it.
-        //         Only lanes whose maximum reaches g test their values.
-        uint32_t pm[NL];
-#pragma unroll
-        for (int j = 0; j < NL; ++j) pm[j] = 0;
-        if (lm >= g2) {
-#pragma unroll
-            for (int j = 0; j < NL; ++j) {
-                uint32_t m = 0;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) m |= v[j * EPL + e] >= g2 ? (1u << e) : 0u;
-                pm[j] = m;
-            }
-        }
-        const uint32_t a01 = (uint32_t)__popc(pm[0]) | ((uint32_t)__popc(pm[1]) << 16);
-        const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
-        const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
-        const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
-        const uint32_t T0 = t01 & 0xFFFFu, T1 = t01 >> 16, T2 = t23 & 0xFFFFu, T3 = t23 >> 16;
-        const uint32_t nw = T0 + T1 + T2 + T3;
+        // ---- 5. the values >= g in id order (load j, lane, value: id order
+        //         inside the wave's slice).  Each wave stages its own in LDS,
+        //         then, after the one barrier, copies its run to the region
+        //         behind the runs of the waves before it.
+        //         Sparse bf16 waves (32 values a lane, few lanes hold a value
+        //         >= g: every top-k row): those lanes park their values in LDS
+        //         in id order and all 64 lanes then test 64 of them per step
+        //         (ballot + mbcnt place them), so the cost follows the lanes
+        //         that matter.  (fp32 waves, 16 values a lane, are faster on
+        //         the dense path: its tail is the shorter chain.)
+        //         Dense waves: per-lane bit masks, two packed wave scans for
+        //         the offsets, writes to a spare slot per lane instead of
+        //         branches.
         uint64_t* stg = xst[cc][wave];
-        const uint32_t e01 = i01 - a01, e23 = i23 - a23;
-        const uint32_t start[NL] = {e01 & 0xFFFFu, T0 + (e01 >> 16), T0 + T1 + (e23 & 0xFFFFu),
-                                    T0 + T1 + T2 + (e23 >> 16)};   // this lane's first slot per load
-        if (nw <= SMP_WCAP && lm >= g2) {
+        const uint64_t qm = ballot(lm >= g2);
+        const uint32_t nq = (uint32_t)__popcll(qm);
+        const bool sparse = sizeof(TL) == 2 && nq <= SMP_SPARSE;   // uniform in the wave
+        float* xw = &xv[cc][wave][0];
+        auto sparse_pass = [&](auto put) {
+            uint32_t base = 0;
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
-                const int i0 = c0 + j * (64 * EPL) + lofs;
-                uint32_t o = start[j];
+                for (uint32_t k0 = 0; k0 < nq * EPL; k0 += 64) {
+                    const uint32_t k = k0 + lane;              // value e = k % EPL of rank k / EPL
+                    const bool valid = k < nq * EPL;
+                    const float f = xw[j * SMP_SPARSE * EPL + (valid ? k : 0u)];
+                    const bool in = valid && f >= g2;
+                    const uint64_t b = ballot(in);
+                    if (in) {
+                        const uint32_t L = xl[cc][wave][k / EPL];
+                        const uint32_t id = (uint32_t)(c0 + j * (64 * EPL) + (int)wave * WS) + L * EPL + k % EPL;
+                        put(base + mbcnt(b), ((uint64_t)__float_as_uint(f) << 32) | id);
+                    }
+                    base += (uint32_t)__popcll(b);
+                }
+            }
+            return base;
+        };
+        uint32_t pm[NL] = {0, 0, 0, 0}, start[NL] = {0, 0, 0, 0};
+        uint32_t nw;
+        if (sparse) {
+            if (lm >= g2) {
+                const uint32_t qr = mbcnt(qm);
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    const bool in = (pm[j] >> e) & 1u;
-                    stg[in ? o : SMP_WCAP + lane] =
-                        ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
-                    o += in ? 1u : 0u;
+                for (int j = 0; j < NL; ++j) {
+#pragma unroll
+                    for (int h = 0; h < EPL / 4; ++h)
+                        *(llima_u32x4*)&xw[j * SMP_SPARSE * EPL + qr * EPL + 4 * h] =
+                            llima_u32x4{__float_as_uint(v[j * EPL + 4 * h]), __float_as_uint(v[j * EPL + 4 * h + 1]),
+                                        __float_as_uint(v[j * EPL + 4 * h + 2]), __float_as_uint(v[j * EPL + 4 * h + 3])};
+                }
+                xl[cc][wave][qr] = lane;
+            }
+            __builtin_amdgcn_wave_barrier();                  // the wave's LDS writes precede its reads
+            nw = sparse_pass([&](uint32_t pos, uint64_t val) { if (pos < SMP_WCAP) stg[pos] = val; });
+        } else {
+            if (lm >= g2) {
+#pragma unroll
+                for (int j = 0; j < NL; ++j) {
+                    uint32_t m = 0;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) m |= v[j * EPL + e] >= g2 ? (1u << e) : 0u;
+                    pm[j] = m;
+                }
+            }
+            const uint32_t a01 = (uint32_t)__popc(pm[0]) | ((uint32_t)__popc(pm[1]) << 16);
+            const uint32_t a23 = (uint32_t)__popc(pm[2]) | ((uint32_t)__popc(pm[3]) << 16);
+            const uint32_t i01 = wave_incl_scan_u32(a01), i23 = wave_incl_scan_u32(a23);
+            const uint32_t t01 = readlane63(i01), t23 = readlane63(i23);
+            const uint32_t T0 = t01 & 0xFFFFu, T1 = t01 >> 16, T2 = t23 & 0xFFFFu, T3 = t23 >> 16;
+            nw = T0 + T1 + T2 + T3;
+            const uint32_t e01 = i01 - a01, e23 = i23 - a23;
+            start[0] = e01 & 0xFFFFu;                          // this lane's first slot per load
+            start[1] = T0 + (e01 >> 16);
+            start[2] = T0 + T1 + (e23 & 0xFFFFu);
+            start[3] = T0 + T1 + T2 + (e23 >> 16);
+            if (nw <= SMP_WCAP && lm >= g2) {
+#pragma unroll
+                for (int j = 0; j < NL; ++j) {
+                    const int i0 = c0 + j * (64 * EPL) + lofs;
+                    uint32_t o = start[j];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        const bool in = (pm[j] >> e) & 1u;
+                        stg[in ? o : SMP_WCAP + lane] =
+                            ((uint64_t)__float_as_uint(v[j * EPL + e]) << 32) | (uint32_t)(i0 + e);
+                        o += in ? 1u : 0u;
+                    }
                 }
             }
         }
@@ -483,6 +535,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                     reg[SMP_HDR + off + i] =
                         ((uint64_t)f32_key(__uint_as_float((uint32_t)(sv >> 32))) << 32) | (uint32_t)sv;
                 }
+            } else if (sparse) {
+                // more than the staging holds: the sparse pass again, to the region
+                sparse_pass([&](uint32_t pos, uint64_t val) {
+                    reg[SMP_HDR + off + pos] =
+                        ((uint64_t)f32_key(__uint_as_float((uint32_t)(val >> 32))) << 32) | (uint32_t)val;
+                });
             } else if (lm >= g2) {
                 // more than the staging holds (dense rows such as grammar-masked
                 // ones without top-k): straight from the registers
