@@ -431,38 +431,46 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         //         inside the wave's slice).  Each wave stages its own in LDS,
         //         then, after the one barrier, copies its run to the region
         //         behind the runs of the waves before it.
-        //         Sparse bf16 waves (32 values a lane, few lanes hold a value
-        //         >= g: every top-k row): those lanes park their values in LDS
-        //         in id order and all 64 lanes then test 64 of them per step
-        //         (ballot + mbcnt place them), so the cost follows the lanes
-        //         that matter.  (fp32 waves, 16 values a lane, are faster on
-        //         the dense path: its tail is the shorter chain.)
+        //         Sparse waves (at most 16 lanes hold a value >= g: every top-k
+        //         row): those lanes park their values in LDS in id order and
+        //         all 64 lanes then test 64 of them per step (ballot + mbcnt
+        //         place them), so the cost follows the lanes that matter.
         //         Dense waves: per-lane bit masks, two packed wave scans for
         //         the offsets, writes to a spare slot per lane instead of
         //         branches.
         uint64_t* stg = xst[cc][wave];
         const uint64_t qm = ballot(lm >= g2);
         const uint32_t nq = (uint32_t)__popcll(qm);
-        const bool sparse = sizeof(TL) == 2 && nq <= SMP_SPARSE;   // uniform in the wave
+        const bool sparse = nq <= SMP_SPARSE;                 // uniform in the wave
         float* xw = &xv[cc][wave][0];
+        constexpr int SR = (SMP_SPARSE * EPL + 63) / 64;      // steps per load
         auto sparse_pass = [&](auto put) {
+            // every LDS read first (one latency), then the tests and writes
+            float f[NL][SR];
+            uint32_t L[NL][SR];
+#pragma unroll
+            for (int j = 0; j < NL; ++j)
+#pragma unroll
+                for (int r = 0; r < SR; ++r) {
+                    const uint32_t k = (uint32_t)r * 64u + lane;     // value k % EPL of rank k / EPL
+                    const bool valid = k < nq * EPL;
+                    f[j][r] = xw[j * SMP_SPARSE * EPL + (valid ? k : 0u)];
+                    L[j][r] = xl[cc][wave][valid ? k / EPL : 0u];
+                }
             uint32_t base = 0;
 #pragma unroll
-            for (int j = 0; j < NL; ++j) {
-                for (uint32_t k0 = 0; k0 < nq * EPL; k0 += 64) {
-                    const uint32_t k = k0 + lane;              // value e = k % EPL of rank k / EPL
-                    const bool valid = k < nq * EPL;
-                    const float f = xw[j * SMP_SPARSE * EPL + (valid ? k : 0u)];
-                    const bool in = valid && f >= g2;
+            for (int j = 0; j < NL; ++j)
+#pragma unroll
+                for (int r = 0; r < SR; ++r) {
+                    const uint32_t k = (uint32_t)r * 64u + lane;
+                    const bool in = k < nq * EPL && f[j][r] >= g2;
                     const uint64_t b = ballot(in);
                     if (in) {
-                        const uint32_t L = xl[cc][wave][k / EPL];
-                        const uint32_t id = (uint32_t)(c0 + j * (64 * EPL) + (int)wave * WS) + L * EPL + k % EPL;
-                        put(base + mbcnt(b), ((uint64_t)__float_as_uint(f) << 32) | id);
+                        const uint32_t id = (uint32_t)(c0 + j * (64 * EPL) + (int)wave * WS) + L[j][r] * EPL + k % EPL;
+                        put(base + mbcnt(b), ((uint64_t)__float_as_uint(f[j][r]) << 32) | id);
                     }
                     base += (uint32_t)__popcll(b);
                 }
-            }
             return base;
         };
         uint32_t pm[NL] = {0, 0, 0, 0}, start[NL] = {0, 0, 0, 0};

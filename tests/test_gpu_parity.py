@@ -207,19 +207,24 @@ def test_sample_masks_and_edges(gpu, oracle):
             assert gi[0] == -1
 
 
-def test_sample_sparse_waves(gpu, oracle):
-    """bf16 sweep waves with few lanes above the chunk bound take the sparse
-    path; with more candidates than a wave stages (12 lanes x 32 values kept)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_sparse_waves(gpu, oracle, dtype):
+    """Sweep waves with few lanes above the chunk bound take the sparse path;
+    with more candidates than a wave stages (12 lanes x all their values kept)
     it writes them to the region directly."""
-    _say("sample sparse sweep waves")
+    _say("sample sparse sweep waves", dtype)
     rng = np.random.default_rng(33)
     B, V = 4, 16384
+    epl = 4 if dtype == "f32" else 8                              # values per 16-byte load
+    ws = 1024 if dtype == "f32" else 2048                         # ids per wave slice
     x = np.full((B, V), -100.0, np.float32)
-    ids = np.array([j * 512 + l * 8 + e for j in range(4) for l in range(12) for e in range(8)])
+    ids = np.array([j * 64 * epl + l * epl + e for j in range(4) for l in range(12)
+                    for e in range(epl)])
     x[:, ids] = rng.normal(0, 1, (B, ids.size)).astype(np.float32)
-    x[1, ids + 2048] = rng.normal(0, 1, ids.size)                  # the next wave's slice too
+    x[1, ids + ws] = rng.normal(0, 1, ids.size)                   # the next wave's slice too
     x[2, ids[:40]] = rng.normal(5, 1, 40)                         # a few lanes dominate
-    x = wl.f32_to_bf16_bits(x)
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
     u = rng.random(B).astype(np.float32)
     for cfgd in [dict(temperature=1.0, top_p=0.9), dict(temperature=1.0, min_p=0.01),
                  dict(temperature=0.7, top_k=20, top_p=0.95), dict(temperature=1.0, top_k=3)]:
