@@ -103,6 +103,32 @@ __device__ __forceinline__ uint64_t row_weight(float x, uint32_t mkey) {
     return weight(x, key_f32(mkey));
 }
 
+// weight(x, xmax) as the integral float it converts (W < 2^37, exact in
+// fp32): sums of at most 2^16 of them are exact in double, so the row sums skip
+// the per-value float -> uint64 conversion.  exp_neg's steps with two folds
+// that leave every result unchanged: d is clamped at -26 (NaN included) with no
+// select after, since rint(e^-26 2^36) = rint(0.35) = 0; and the two scalings
+// are one, 2^(n+36) (n >= -38 keeps every intermediate normal).
+__device__ __forceinline__ float weight_f(float x, float xmax) {
+    const float d = __builtin_fmaxf(x - xmax, -26.0f);   // fmaxf(NaN, -26) = -26
+    const float kLog2e = 1.44269502162933349609375f;
+    const float kLn2Hi = 0.693145751953125f;
+    const float kLn2Lo = 1.428606765330187045e-06f;
+    const float n = __builtin_rintf(d * kLog2e);
+    float r = __builtin_fmaf(n, -kLn2Hi, d);
+    r = __builtin_fmaf(n, -kLn2Lo, r);
+    float p = 1.98412698412698412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float w = __builtin_rintf(__builtin_ldexpf(p, (int)n + 36));
+    return x == xmax ? 68719476736.0f : w;             // 2^36 (also for an infinite maximum)
+}
+
 __global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
     __shared__ BlockScratch bs;
     const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
@@ -137,8 +163,13 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     __syncthreads();
     const uint32_t mkey = s_mkey;
     uint64_t s = 0;
+    if (mkey > LLIMA_KEY_NEG_INF) {
+        const float xm = key_f32(mkey);
+        double sd = 0.0;                                 // exact: 32 terms below 2^37
 #pragma unroll
-    for (int e = 0; e < VR_E; ++e) s += row_weight(v[e], mkey);
+        for (int e = 0; e < VR_E; ++e) sd += (double)weight_f(v[e], xm);
+        s = (uint64_t)sd;
+    }
     s = block_sum_u64(s, bs);
     if (threadIdx.x == 0) {
         P.sums[(size_t)r * P.S + c] = s;
