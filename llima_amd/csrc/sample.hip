@@ -55,7 +55,7 @@ namespace llima {
 #define SMP_BOUND_LOWBIT 16                        // key bits below this are not searched
 #define SMP_SMALL 64                               // survivors handled one per lane
 #define SMP_WCAP 128                               // candidates a sweep wave can stage
-#define SMP_SPARSE 16                              // lanes above the bound for a sparse sweep wave
+#define SMP_SPARSE 12                              // lanes above the bound for a sparse sweep wave
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
 
@@ -199,9 +199,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     extern __shared__ __align__(16) uint32_t cnt[];
     __shared__ uint32_t xa[SC][LLIMA_WAVES];
     __shared__ uint32_t xn[SC][LLIMA_WAVES];              // candidates per wave
-    __shared__ uint64_t xst[SC][LLIMA_WAVES][SMP_WCAP + 64];   // staged candidates (+ a spare slot per lane)
-    __shared__ __align__(16) float xv[SC][LLIMA_WAVES][NL * SMP_SPARSE * EPL];   // sparse waves' parked values
-    __shared__ uint32_t xl[SC][LLIMA_WAVES][SMP_SPARSE];                        // ... and their lanes
+    // a wave's staged candidates (+ a spare slot per lane) or, for a sparse
+    // wave, first its parked values: the same 1.5 KB (the sweep's LDS size
+    // sets how fast its workgroups are dispatched)
+    __shared__ __align__(16) uint64_t xst[SC][LLIMA_WAVES][SMP_WCAP + 64];
+    __shared__ uint32_t xl[SC][LLIMA_WAVES][SMP_SPARSE];     // a sparse wave's parking lanes
+    static_assert(NL * SMP_SPARSE * EPL * 4 <= (SMP_WCAP + 64) * 8, "parked values exceed the staging");
     __shared__ uint64_t xg[SC][LLIMA_WAVES];
     const float NEG_INF = -__builtin_inff();
 
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         //         inside the wave's slice).  Each wave stages its own in LDS,
         //         then, after the one barrier, copies its run to the region
         //         behind the runs of the waves before it.
-        //         Sparse waves (at most 16 lanes hold a value >= g: every top-k
+        //         Sparse waves (at most 12 lanes hold a value >= g: every top-k
         //         row): those lanes park their values in LDS in id order and
         //         all 64 lanes then test 64 of them per step (ballot + mbcnt
         //         place them), so the cost follows the lanes that matter.
@@ -442,9 +445,12 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         const uint64_t qm = ballot(lm >= g2);
         const uint32_t nq = (uint32_t)__popcll(qm);
         const bool sparse = nq <= SMP_SPARSE;                 // uniform in the wave
-        float* xw = &xv[cc][wave][0];
+        float* xw = (float*)stg;                              // parked values
         constexpr int SR = (SMP_SPARSE * EPL + 63) / 64;      // steps per load
-        auto sparse_pass = [&](auto put) {
+        // staging: writes only when the wave's candidates fit (its parked
+        // values, all read by then, are overwritten); else nothing, and the
+        // pass runs again after the barrier with the region as destination
+        auto sparse_pass = [&](auto put, bool staging) {
             // every LDS read first (one latency), then the tests and writes
             float f[NL][SR];
             uint32_t L[NL][SR];
@@ -457,21 +463,30 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                     f[j][r] = xw[j * SMP_SPARSE * EPL + (valid ? k : 0u)];
                     L[j][r] = xl[cc][wave][valid ? k / EPL : 0u];
                 }
-            uint32_t base = 0;
+            uint64_t b[NL][SR];
+            uint32_t tot = 0;
 #pragma unroll
             for (int j = 0; j < NL; ++j)
 #pragma unroll
                 for (int r = 0; r < SR; ++r) {
-                    const uint32_t k = (uint32_t)r * 64u + lane;
-                    const bool in = k < nq * EPL && f[j][r] >= g2;
-                    const uint64_t b = ballot(in);
-                    if (in) {
-                        const uint32_t id = (uint32_t)(c0 + j * (64 * EPL) + (int)wave * WS) + L[j][r] * EPL + k % EPL;
-                        put(base + mbcnt(b), ((uint64_t)__float_as_uint(f[j][r]) << 32) | id);
-                    }
-                    base += (uint32_t)__popcll(b);
+                    b[j][r] = ballot((uint32_t)r * 64u + lane < nq * EPL && f[j][r] >= g2);
+                    tot += (uint32_t)__popcll(b[j][r]);
                 }
-            return base;
+            if (!staging || tot <= SMP_WCAP) {
+                uint32_t base = 0;
+#pragma unroll
+                for (int j = 0; j < NL; ++j)
+#pragma unroll
+                    for (int r = 0; r < SR; ++r) {
+                        if ((b[j][r] >> lane) & 1ull) {
+                            const uint32_t k = (uint32_t)r * 64u + lane;
+                            const uint32_t id = (uint32_t)(c0 + j * (64 * EPL) + (int)wave * WS) + L[j][r] * EPL + k % EPL;
+                            put(base + mbcnt(b[j][r]), ((uint64_t)__float_as_uint(f[j][r]) << 32) | id);
+                        }
+                        base += (uint32_t)__popcll(b[j][r]);
+                    }
+            }
+            return tot;
         };
         uint32_t pm[NL] = {0, 0, 0, 0}, start[NL] = {0, 0, 0, 0};
         uint32_t nw;
@@ -489,7 +504,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                 xl[cc][wave][qr] = lane;
             }
             __builtin_amdgcn_wave_barrier();                  // the wave's LDS writes precede its reads
-            nw = sparse_pass([&](uint32_t pos, uint64_t val) { if (pos < SMP_WCAP) stg[pos] = val; });
+            nw = sparse_pass([&](uint32_t pos, uint64_t val) { stg[pos] = val; }, true);
         } else {
             if (lm >= g2) {
 #pragma unroll
@@ -548,7 +563,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                 sparse_pass([&](uint32_t pos, uint64_t val) {
                     reg[SMP_HDR + off + pos] =
                         ((uint64_t)f32_key(__uint_as_float((uint32_t)(val >> 32))) << 32) | (uint32_t)val;
-                });
+                }, false);
             } else if (lm >= g2) {
                 // more than the staging holds (dense rows such as grammar-masked
                 // ones without top-k): straight from the registers
