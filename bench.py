@@ -143,13 +143,16 @@ def main():
             order = torch.from_numpy(w["ordering"].view(np.int32)).to(dev)
             ids_o = torch.empty(B, dtype=torch.int32, device=dev)
             st_o = torch.empty(B, dtype=torch.int32, device=dev)
+            nws = L.llima_mtp_masked_argmax_workspace_bytes(B)
+            ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
             for x in bufs:
                 launches.append(lambda sp, x=x: check(L.llima_mtp_masked_argmax(
                     cent.data_ptr(), C, C, order.data_ptr(), k, x.data_ptr(), dt, B, V, V,
-                    ids_o.data_ptr(), st_o.data_ptr(), None, sp), "llima_mtp_masked_argmax"))
+                    ids_o.data_ptr(), st_o.data_ptr(), None, ws.data_ptr(), nws, sp),
+                    "llima_mtp_masked_argmax"))
             # centroid row, the selected ordering runs and their logits, the outputs
             alg_bytes = B * (C * 2 + k * (V // C) * (4 + 2) + 4 + 4)
-            kernel_names = ["mtp_masked_argmax"]
+            kernel_names = ["mtp_select_gather", "mtp_combine"]
             config = {"workload": name, "B": B, "V": V, "centroids": C, "top_k": k,
                       "logits_dtype": "bf16"}
     else:

@@ -192,12 +192,13 @@ int llima_score_logits(const void* logits, int32_t dtype, int32_t B, int32_t V,
  * LLIMA_E_INVAL when no candidate has a non-NaN logit (both are
  * std::runtime_error in the reference); out_ids is then -1.  Returns
  * LLIMA_E_INVAL when V is not a multiple of C or top_k is outside [1, C]
- * (the reference's own checks).  Needs no workspace. */
+ * (the reference's own checks). */
+size_t llima_mtp_masked_argmax_workspace_bytes(int32_t B);
 int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_stride, int32_t C,
                             const uint32_t* token_ordering, int32_t top_k, const void* logits,
                             int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
                             int32_t* out_ids, int32_t* out_status, uint32_t* out_candidates,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 const char* llima_status_string(int status);
 int llima_abi_version(void);

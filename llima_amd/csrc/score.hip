@@ -19,7 +19,8 @@
 // agrees to about 1e-6 absolute; the argmax, the greedy flag and every NaN /
 // infinity outcome are exact.
 //
-// Masked argmax: one workgroup per row.  The top_k centroids by (value desc,
+// Masked argmax: G workgroups per row, then one wavefront per row combines
+// their maxima.  The top_k centroids by (value desc,
 // index asc) are found as a set by an 8-bit radix select on the value keys in
 // LDS (plus an index-order scan of the ties at the boundary when only some of
 // them are in); their tokens (the token_ordering runs of the selected
@@ -236,6 +237,8 @@ static hipError_t launch_score(const ScoreParams& P, hipStream_t st) {
 // ============================================================ masked argmax
 #define MTP_MAX_C 8192             // centroids per row held in LDS
 #define MTP_GB 16                  // candidates per thread with loads in flight together
+#define MTP_MAX_G 16               // workgroups sharing one row's candidates
+#define MTP_SHARE 512              // candidates per workgroup (at least)
 
 struct MtpParams {
     const uint16_t* centroids;     // bf16 [B][c_stride]
@@ -246,21 +249,27 @@ struct MtpParams {
     int32_t* out_ids;              // [B] or null
     int32_t* out_status;           // [B] or null
     uint32_t* out_cand;            // [B][k * per] or null
-    int32_t B, V, C, k, per;
+    uint64_t* pkeys;               // [B][G] best (value key, ~token) of each share
+    uint32_t* pbad;                // [B][G] 1: an ordering entry >= V in the share
+    int32_t B, V, C, k, per, G;
 };
 
 struct MtpShared {
     uint32_t ck[MTP_MAX_C];        // centroid value keys (16 bits), NaN -> 0
     uint32_t sel[MTP_MAX_C];       // selected centroids, index order
     uint32_t hist[256];
-    uint32_t digit, need, ties, nsel, bad;
+    uint32_t digit, need, ties, bad;
     BlockScratch bs;
 };
 
+// Workgroup (row, part): the centroid selection of the row (every part of the
+// row repeats it: a few microseconds of latency, no traffic to speak of), then
+// share `part` of the row's candidates: the gathers of one row are spread over
+// G workgroups, since one CU pulls one scattered cache line per candidate.
 template <typename TL>
-__global__ __launch_bounds__(LLIMA_WG) void mtp_masked_argmax(MtpParams P) {
+__global__ __launch_bounds__(LLIMA_WG) void mtp_select_gather(MtpParams P) {
     __shared__ MtpShared sh;
-    const int row = (int)blockIdx.x;
+    const int row = (int)blockIdx.x / P.G, part = (int)blockIdx.x % P.G;
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     const int C = P.C;
     const uint16_t* crow = P.centroids + (size_t)row * P.c_stride;
@@ -314,25 +323,35 @@ __global__ __launch_bounds__(LLIMA_WG) void mtp_masked_argmax(MtpParams P) {
     }
     const uint32_t tau = prefix;
     // ---- the selected centroids (keys above tau, then the first `need` with
-    //      key tau by index) into sh.sel in any order: the argmax does not
-    //      depend on it and the candidate list orders by rank
-    if (t == 0) sh.nsel = 0;
-    __syncthreads();
-    if (need == sh.ties) {                          // every tie is in (the usual case)
-        for (int i = (int)t; i < C; i += LLIMA_WG)
-            if (sh.ck[i] >= tau) sh.sel[atomicAdd(&sh.nsel, 1u)] = (uint32_t)i;
-    } else {
-        // ties in index order: thread t owns a contiguous index range
-        const int per_t = (C + LLIMA_WG - 1) / LLIMA_WG;
-        const int i0 = (int)t * per_t, i1 = i0 + per_t < C ? i0 + per_t : C;
-        uint32_t neq = 0, teq;
-        for (int i = i0; i < i1; ++i) neq += sh.ck[i] == tau ? 1u : 0u;
-        uint32_t eqb = block_excl_scan_u32(neq, &teq, sh.bs);   // ties before this range
+    //      key tau by index) into sh.sel in index order: every workgroup of
+    //      the row builds the same list, and each takes its share of it
+    const int per_t = (C + LLIMA_WG - 1) / LLIMA_WG;           // thread t: a contiguous index range
+    const int i0 = (int)t * per_t, i1 = i0 + per_t < C ? i0 + per_t : C;
+    uint32_t neq = 0, nsl = 0;
+    for (int i = i0; i < i1; ++i) {
+        const uint32_t kk = sh.ck[i];
+        neq += kk == tau ? 1u : 0u;
+        nsl += kk > tau ? 1u : 0u;
+    }
+    const bool all_ties = need == sh.ties;                      // the usual case
+    uint32_t teq = 0, tsel;
+    uint32_t eqb = all_ties ? 0u : block_excl_scan_u32(neq, &teq, sh.bs);   // ties before this range
+    uint32_t ns2 = nsl;
+    if (!all_ties) {
+        uint32_t e2 = eqb;
         for (int i = i0; i < i1; ++i) {
-            const uint32_t kk = sh.ck[i];
-            if (kk > tau || (kk == tau && eqb < need)) sh.sel[atomicAdd(&sh.nsel, 1u)] = (uint32_t)i;
-            eqb += kk == tau ? 1u : 0u;
+            const bool tie = sh.ck[i] == tau;
+            ns2 += tie && e2 < need ? 1u : 0u;
+            e2 += tie ? 1u : 0u;
         }
+    } else {
+        ns2 += neq;
+    }
+    uint32_t o = block_excl_scan_u32(ns2, &tsel, sh.bs);          // tsel == k
+    for (int i = i0; i < i1; ++i) {
+        const uint32_t kk = sh.ck[i];
+        if (kk > tau || (kk == tau && (all_ties || eqb < need))) sh.sel[o++] = (uint32_t)i;
+        eqb += kk == tau ? 1u : 0u;
     }
     __syncthreads();
     // ---- candidates: the ordering runs of the selected centroids; their rank
@@ -343,17 +362,19 @@ __global__ __launch_bounds__(LLIMA_WG) void mtp_masked_argmax(MtpParams P) {
     const TL* rowp = P.logits ? (const TL*)P.logits + (size_t)row * P.row_stride : nullptr;
     uint32_t* cand = P.out_cand ? P.out_cand + (size_t)row * ncand : nullptr;
     const float inv_per = 1.0f / (float)per;
+    const int share = (ncand + P.G - 1) / P.G;
+    const int jlo = part * share, jhi = jlo + share < ncand ? jlo + share : ncand;
     uint64_t best = 0;
     uint32_t bad = 0;
-    // candidate j = t + 256 m of a batch: centroid rank r = j / per (fp32
+    // candidate j = jlo + t + 256 m of a batch: centroid rank r = j / per (fp32
     // quotient, exact after one correction since j < 2^24), position off
-    for (int j0 = 0; j0 < ncand; j0 += MTP_GB * LLIMA_WG) {
+    for (int j0 = jlo; j0 < jhi; j0 += MTP_GB * LLIMA_WG) {
         uint32_t tok[MTP_GB], cr[MTP_GB], co[MTP_GB];
         bool ok[MTP_GB];
 #pragma unroll
         for (int m = 0; m < MTP_GB; ++m) {             // every ordering load first
             const int j = j0 + m * LLIMA_WG + (int)t;
-            ok[m] = j < ncand;
+            ok[m] = j < jhi;
             int r = (int)((float)j * inv_per);
             int off = j - r * per;
             r = off < 0 ? r - 1 : (off >= per ? r + 1 : r);
@@ -391,10 +412,23 @@ __global__ __launch_bounds__(LLIMA_WG) void mtp_masked_argmax(MtpParams P) {
     if (bad) sh.bad = 1;                              // benign race: every writer stores 1
     best = block_max_u64(best, sh.bs);                // barrier: sh.bad final
     if (t != 0) return;
+    P.pkeys[(size_t)row * P.G + part] = best;
+    P.pbad[(size_t)row * P.G + part] = sh.bad;
+}
+
+// One wavefront per row: the shares' maxima and error flags combined.
+__global__ __launch_bounds__(LLIMA_WG) void mtp_combine(MtpParams P) {
+    const int row = (int)blockIdx.x * LLIMA_WAVES + (int)wave_id();
+    if (row >= P.B) return;
+    const uint32_t lane = lane_id();
+    const bool in = (int)lane < P.G;
+    const uint64_t kb = wave_max_u64(in ? P.pkeys[(size_t)row * P.G + lane] : 0ull);
+    const uint32_t bad = wave_max_u32(in ? P.pbad[(size_t)row * P.G + lane] : 0u);
+    if (lane != 0) return;
     int32_t id = -1, st = LLIMA_OK;
-    if (sh.bad) st = LLIMA_E_RANGE;                   // out-of-range token id in the ordering
-    else if (rowp && best == 0) st = LLIMA_E_INVAL;   // no candidate value (all NaN)
-    else if (rowp) id = (int32_t)~(uint32_t)best;
+    if (bad) st = LLIMA_E_RANGE;                      // out-of-range token id in the ordering
+    else if (P.logits && kb == 0) st = LLIMA_E_INVAL; // no candidate value (all NaN)
+    else if (P.logits) id = (int32_t)~(uint32_t)kb;
     if (P.out_ids) P.out_ids[row] = id;
     if (P.out_status) P.out_status[row] = st;
 }
@@ -453,11 +487,18 @@ extern "C" int llima_score_logits(const void* logits, int32_t dtype, int32_t B, 
     return e == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }
 
+extern "C" size_t llima_mtp_masked_argmax_workspace_bytes(int32_t B) {
+    if (B <= 0) return 0;
+    return sc_align256((size_t)B * MTP_MAX_G * sizeof(uint64_t)) +
+           sc_align256((size_t)B * MTP_MAX_G * sizeof(uint32_t));
+}
+
 extern "C" int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_stride,
                                        int32_t C, const uint32_t* token_ordering, int32_t top_k,
                                        const void* logits, int32_t dtype, int32_t B, int32_t V,
                                        int64_t row_stride, int32_t* out_ids, int32_t* out_status,
-                                       uint32_t* out_candidates, void* stream) {
+                                       uint32_t* out_candidates, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
     if (!centroid_logits || !token_ordering) return LLIMA_E_INVAL;
     if (B < 0 || V <= 0 || C <= 0 || C > MTP_MAX_C || centroid_stride < C) return LLIMA_E_INVAL;
     if (V % C != 0) return LLIMA_E_INVAL;                 // gemma4_mtp_helpers.cpp:118-125
@@ -470,6 +511,8 @@ extern "C" int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t 
         return LLIMA_E_INVAL;                             // nothing to compute
     }
     if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_mtp_masked_argmax_workspace_bytes(B))
+        return LLIMA_E_WORKSPACE;
     MtpParams P = {};
     P.centroids = centroid_logits;
     P.c_stride = centroid_stride;
@@ -480,10 +523,15 @@ extern "C" int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t 
     P.out_status = out_status;
     P.out_cand = out_candidates;
     P.B = B; P.V = V; P.C = C; P.k = top_k; P.per = V / C;
+    const int64_t ncand = (int64_t)top_k * (V / C);
+    const int64_t g = (ncand + MTP_SHARE - 1) / MTP_SHARE;
+    P.G = (int32_t)(g < 1 ? 1 : (g > MTP_MAX_G ? MTP_MAX_G : g));
+    P.pkeys = (uint64_t*)workspace;
+    P.pbad = (uint32_t*)((char*)workspace + sc_align256((size_t)B * MTP_MAX_G * sizeof(uint64_t)));
     const hipStream_t st = (hipStream_t)stream;
-    if (logits && dtype == LLIMA_F32)
-        hipLaunchKernelGGL(mtp_masked_argmax<float>, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
-    else
-        hipLaunchKernelGGL(mtp_masked_argmax<uint16_t>, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    const dim3 grid((uint32_t)B * (uint32_t)P.G), blk(LLIMA_WG);
+    if (logits && dtype == LLIMA_F32) hipLaunchKernelGGL(mtp_select_gather<float>, grid, blk, 0, st, P);
+    else hipLaunchKernelGGL(mtp_select_gather<uint16_t>, grid, blk, 0, st, P);
+    hipLaunchKernelGGL(mtp_combine, dim3((uint32_t)(B + LLIMA_WAVES - 1) / LLIMA_WAVES), blk, 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }

@@ -392,9 +392,11 @@ def select_candidate_tokens(centroid_logits: torch.Tensor, token_ordering, top_k
     B, k = c.shape[0], int(top_k_centroids)
     cand = torch.empty((B, k * (V // C)), dtype=torch.int32, device=c.device)
     st = torch.empty(B, dtype=torch.int32, device=c.device)
+    ws = Workspace.get(c.device, "mtp", lib().llima_mtp_masked_argmax_workspace_bytes(B))
     check(lib().llima_mtp_masked_argmax(c.data_ptr(), c.stride(0), C, o.data_ptr(), k, None,
                                         _lib.LLIMA_BF16, B, V, V, None, st.data_ptr(),
-                                        cand.data_ptr(), _stream(c.device)),
+                                        cand.data_ptr(), ws.data_ptr(), ws.numel(),
+                                        _stream(c.device)),
           "llima_mtp_masked_argmax")
     _mtp_status(st)
     return cand[0].tolist() if centroid_logits.dim() == 1 else cand
@@ -414,9 +416,11 @@ def argmax_gemma4_mtp_masked_rows(centroid_logits: torch.Tensor, token_ordering,
     B = x.shape[0]
     ids = torch.empty(B, dtype=torch.int32, device=x.device)
     st = torch.empty(B, dtype=torch.int32, device=x.device)
+    ws = Workspace.get(x.device, "mtp", lib().llima_mtp_masked_argmax_workspace_bytes(B))
     check(lib().llima_mtp_masked_argmax(c.data_ptr(), c.stride(0), C, o.data_ptr(), int(top_k),
                                         x.data_ptr(), _dtype_code(x), B, V, x.stride(0),
-                                        ids.data_ptr(), st.data_ptr(), None, _stream(x.device)),
+                                        ids.data_ptr(), st.data_ptr(), None, ws.data_ptr(),
+                                        ws.numel(), _stream(x.device)),
           "llima_mtp_masked_argmax")
     _mtp_status(st)
     return ids

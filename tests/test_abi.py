@@ -51,12 +51,18 @@ def test_host_only_entry_points():
     assert L.llima_score_logits(p, 0, 1, 10, 10, p, p, p, None, 0, None) == -4
     assert L.llima_score_logits_workspace_bytes(256, 262144, 1) > 0
     # the reference's own checks: V a multiple of C, top_k in [1, C]
-    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 2, p, 1, 1, 10, 10, p, p, None, None) == -1
-    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 5, p, 1, 1, 8, 8, p, p, None, None) == -1
-    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 0, p, 1, 1, 8, 8, p, p, None, None) == -1
-    assert L.llima_mtp_masked_argmax(p, 9000, 9000, p, 1, p, 1, 1, 9000, 9000, p, p, None,
-                                     None) == -1              # beyond 8192 centroids
-    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, None, 1, 1, 8, 8, None, p, None, None) == -1
+    wsb = L.llima_mtp_masked_argmax_workspace_bytes(1)
+    assert wsb > 0
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 2, p, 1, 1, 10, 10, p, p, None, p, wsb,
+                                     None) == -1
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 5, p, 1, 1, 8, 8, p, p, None, p, wsb, None) == -1
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 0, p, 1, 1, 8, 8, p, p, None, p, wsb, None) == -1
+    assert L.llima_mtp_masked_argmax(p, 9000, 9000, p, 1, p, 1, 1, 9000, 9000, p, p, None, p,
+                                     wsb, None) == -1         # beyond 8192 centroids
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, None, 1, 1, 8, 8, None, p, None, p, wsb,
+                                     None) == -1
+    assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, p, 1, 1, 8, 8, p, p, None, None, 0,
+                                     None) == -4              # no workspace
 
 
 def test_config_struct_layout_matches_header():
