@@ -238,7 +238,7 @@ static hipError_t launch_score(const ScoreParams& P, hipStream_t st) {
 #define MTP_MAX_C 8192             // centroids per row held in LDS
 #define MTP_GB 16                  // candidates per thread with loads in flight together
 #define MTP_MAX_G 16               // workgroups sharing one row's candidates
-#define MTP_SHARE 512              // candidates per workgroup (at least)
+#define MTP_SHARE 256              // candidates per workgroup (at least)
 
 struct MtpParams {
     const uint16_t* centroids;     // bf16 [B][c_stride]
