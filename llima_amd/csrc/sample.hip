@@ -1145,16 +1145,14 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     float x[EPT];
     uint32_t id[EPT];
+    // every read at once from a clamped slot, the element past N made -inf
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-        x[j] = -__builtin_inff();
-        id[j] = 0;
-        if (f < N) {
-            const uint64_t q = sh.u.cand[f + (f >> 4)];
-            x[j] = key_f32((uint32_t)(q >> 32));
-            id[j] = (uint32_t)q;
-        }
+        const uint32_t fc = f < N ? f : 0u;
+        const uint64_t q = sh.u.cand[fc + (fc >> 4)];
+        x[j] = f < N ? key_f32((uint32_t)(q >> 32)) : -__builtin_inff();
+        id[j] = (uint32_t)q;
     }
 
     // ---- lazy penalties: history ids counted against a hash of the candidate ids
@@ -1206,16 +1204,20 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         }
     }
 
-    // ---- keys of x / T (0: absent or -inf), row maximum and minimum, count
+    // ---- keys of x / T (0: absent or -inf; past N x is -inf), row maximum
+    //      and minimum, count.  x / 1 is x: no division at temperature 1.
     uint32_t key[EPT];
     uint32_t kmx = 0, nkmn = 0, nf = 0;
+    if (c.T == 1.0f) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) key[j] = f32_key(x[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) key[j] = f32_key(x[j] / c.T);
+    }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        key[j] = 0;
-        if (t + (uint32_t)j * LLIMA_WG < N) {
-            const uint32_t k = f32_key(c.T == 1.0f ? x[j] : x[j] / c.T);   // x / 1 is x
-            key[j] = k > LLIMA_KEY_NEG_INF ? k : 0u;
-        }
+        key[j] = key[j] > LLIMA_KEY_NEG_INF ? key[j] : 0u;
         kmx = key[j] > kmx ? key[j] : kmx;
         nkmn = key[j] && ~key[j] > nkmn ? ~key[j] : nkmn;
         nf += key[j] ? 1u : 0u;
