@@ -1322,8 +1322,9 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     uint64_t Z = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        if (key[j] < tau) key[j] = 0;
-        w[j] = key[j] ? weight(key_f32(key[j]), xmax) : 0ull;
+        key[j] = key[j] < tau ? 0u : key[j];
+        const uint64_t wj = weight(key_f32(key[j]), xmax);   // no branch: key 0 is NaN, weight 0
+        w[j] = key[j] ? wj : 0ull;
         Z += w[j];
     }
     uint32_t theta = 0;
@@ -1340,19 +1341,23 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         fmask |= f ? (1u << j) : 0u;
         w[j] = f ? w[j] : 0ull;
     }
-    // final weights into LDS in id order, then 16 consecutive ids per thread
+    // final weights into LDS in id order (every slot below EPT * 256 <=
+    // SMP_FIN_CAP: elements past N hold weight 0), then 16 consecutive ids per
+    // thread (those past EPT * 256 are 0)
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-        if (f < N) sh.u.cand[f + (f >> 4)] = w[j];
+        sh.u.cand[f + (f >> 4)] = w[j];
     }
     __syncthreads();
     uint64_t ws[16], mysum = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const uint32_t f = t * 16u + (uint32_t)j;
-        ws[j] = f < N ? sh.u.cand[f + (f >> 4)] : 0ull;
+        const uint32_t fc = f < EPT * LLIMA_WG ? f : 0u;
+        const uint64_t v = sh.u.cand[fc + (fc >> 4)];
+        ws[j] = f < EPT * LLIMA_WG ? v : 0ull;
         mysum += ws[j];
     }
     uint64_t Zf;
