@@ -662,24 +662,26 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
     while (d.top >= 0) {
         const int lo = d.top - 7 > 0 ? d.top - 7 : 0;
         const uint32_t bmask = (1u << (d.top - lo + 1)) - 1u;
-        uint32_t* hc = sh.hcnt[buf];
         uint64_t* hm = sh.hmass[buf];
+        // one 64-bit atomic per value: (mass << 13) + count (W <= 2^36 and at
+        // most 4096 values: mass < 2^49, count < 2^13)
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             const bool in = (key[j] != 0u) & ((key[j] & d.pmask) == d.prefix);
             const uint32_t b = in ? (key[j] >> lo) & bmask : 256u + lane;
-            atomicAdd(&hc[b], 1u);
-            atomicAdd((unsigned long long*)&hm[b], (unsigned long long)w[j]);
+            atomicAdd((unsigned long long*)&hm[b], (unsigned long long)((w[j] << 13) | 1ull));
         }
         __syncthreads();
         // lane l: bins 255 - 4l down to 252 - 4l
-        const llima_u32x4 c4 = ((const llima_u32x4*)hc)[63u - lane];
-        const uint32_t cs[4] = {c4.w, c4.z, c4.y, c4.x};
+        uint32_t cs[4];
         uint64_t ms[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ms[i] = hm[255u - 4u * lane - (uint32_t)i];
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t v = hm[255u - 4u * lane - (uint32_t)i];
+            cs[i] = (uint32_t)(v & 0x1FFFu);
+            ms[i] = v >> 13;
+        }
         const uint32_t nxt = buf == 0u ? 2u : buf - 1u;
-        sh.hcnt[nxt][t] = 0;
         sh.hmass[nxt][t] = 0;
         const uint64_t m4 = ms[0] + ms[1] + ms[2] + ms[3];
         uint64_t ab = acc + wave_incl_scan_u64(m4) - m4;           // mass above the lane's top bin
