@@ -193,6 +193,55 @@ def test_sample_configs(gpu, oracle, ci, dtype):
     _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl)
 
 
+def _random_cfg(rng):
+    d = {}
+    if rng.random() < 0.1:
+        d["greedy"] = True
+    d["temperature"] = float(rng.choice([1.0, 0.7, 1.3, 0.05, 3.0]))
+    if rng.random() < 0.75:
+        d["top_k"] = int(rng.choice([1, 5, 20, 40, 50, 64, 65, 100, 300]))
+    if rng.random() < 0.6:
+        d["top_p"] = float(rng.choice([0.5, 0.9, 0.95, 0.99]))
+    if rng.random() < 0.3:
+        d["min_p"] = float(rng.choice([0.01, 0.05, 0.2]))
+    if rng.random() < 0.5:
+        d["repetition_penalty"] = float(rng.choice([1.05, 1.15, 0.9]))
+        d["presence_penalty"] = float(rng.choice([0.0, 0.5, -0.3]))
+        d["frequency_penalty"] = float(rng.choice([0.0, 0.3]))
+    return d
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_sample_random_configs(gpu, oracle, seed):
+    """Seeded random shapes, dtypes, configs, histories and masks."""
+    rng = np.random.default_rng(5000 + seed)
+    B = int(rng.integers(1, 7))
+    V = int(rng.choice([37, 1000, 4096, 8192, 30001, 65536, 128256]))
+    dtype = "bf16" if rng.random() < 0.5 else "f32"
+    sigma = float(rng.choice([1.0, 3.0, 5.0]))
+    x = rng.normal(0, sigma, (B, V)).astype(np.float32)
+    if rng.random() < 0.3:
+        x = np.round(x * 2) / 2                              # ties
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    hist = hl = None
+    if rng.random() < 0.6:
+        H = int(rng.choice([16, 300, 2048]))
+        hist = rng.integers(-3, V + 3, size=(B, H)).astype(np.int32)
+        if rng.random() < 0.5:
+            hist[:, : H // 4] = rng.integers(0, min(V, 64), size=(B, H // 4))   # hot ids
+        hl = rng.integers(0, H + 1, size=B).astype(np.int32)
+    mask = None
+    if rng.random() < 0.3:
+        nw = (V + 31) // 32
+        mask = (rng.random((B, nw)) < rng.choice([0.02, 0.5, 0.98])).astype(np.uint32) * np.uint32(0xFFFFFFFF)
+        mask ^= rng.integers(0, 2**32, size=(B, nw), dtype=np.uint64).astype(np.uint32) & np.uint32(0x0F0F0F0F)
+    u = rng.random(B).astype(np.float32)
+    cfgd = _random_cfg(rng)
+    _say("sample random", seed, B, V, dtype, cfgd, "hist" if hist is not None else "", "mask" if mask is not None else "")
+    _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl, mask=mask)
+
+
 def test_sample_masks_and_edges(gpu, oracle):
     _say("sample masks/edges")
     rng = np.random.default_rng(21)
