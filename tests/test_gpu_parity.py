@@ -418,6 +418,31 @@ def test_verify_rejection_parity(gpu, oracle, B, D, V):
     assert (_np(em) == eem).all()
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_verify_rejection_random(gpu, oracle, seed):
+    """Seeded random shapes; drafts either sampled, forced equal to the target
+    argmax (long acceptance runs) or random ids (early rejection)."""
+    import llima_amd
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 9))
+    D = int(rng.integers(0, 9))
+    V = int(rng.choice([4, 100, 4096, 32000, 128256]))
+    _say("verify_rejection random", seed, B, D, V)
+    w = wl.speculative(B=B, D=D, V=V, seed=8000 + seed)
+    ids = w["draft_ids"]
+    mode = seed % 3
+    if mode == 1 and D > 0:
+        ids = w["target"][:, :D].argmax(-1).astype(np.int32)
+    elif mode == 2 and D > 0:
+        ids = rng.integers(0, V, size=(B, D)).astype(np.int32)
+    acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu), _t(ids, gpu),
+                                         _t(w["u_accept"], gpu), _t(w["u_resample"], gpu))
+    eacc, eem = oracle.verify_rejection(w["target"], w["draft"], ids, w["u_accept"],
+                                        w["u_resample"])
+    assert (_np(acc) == eacc).all(), (_np(acc), eacc)
+    assert (_np(em) == eem).all()
+
+
 def test_verify_rejection_edges(gpu, oracle):
     import llima_amd
     _say("verify_rejection edges")
