@@ -193,6 +193,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     constexpr int CHUNK = LLIMA_WG * E;
     constexpr int CW = SC * CHUNK / 2;         // history count words (the group)
     constexpr int WS = CHUNK / LLIMA_WAVES;    // ids per wave and chunk
+    // lanes of a sparse wave: 8 for bf16 (64 parked values per load: one step), 12 for fp32
+    constexpr int SPL = sizeof(TL) == 2 ? 8 : SMP_SPARSE;
     // history counts of the group, two 16-bit counts per word: dynamic LDS,
     // sized by the launch only when the sweep applies the penalties itself
     // (otherwise 0 bytes, which keeps the workgroups' LDS small)
@@ -434,7 +436,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         //         inside the wave's slice).  Each wave stages its own in LDS,
         //         then, after the one barrier, copies its run to the region
         //         behind the runs of the waves before it.
-        //         Sparse waves (at most 12 lanes hold a value >= g: every top-k
+        //         Sparse waves (at most SPL lanes hold a value >= g: every top-k
         //         row): those lanes park their values in LDS in id order and
         //         all 64 lanes then test 64 of them per step (ballot + mbcnt
         //         place them), so the cost follows the lanes that matter.
@@ -444,9 +446,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
         uint64_t* stg = xst[cc][wave];
         const uint64_t qm = ballot(lm >= g2);
         const uint32_t nq = (uint32_t)__popcll(qm);
-        const bool sparse = nq <= SMP_SPARSE;                 // uniform in the wave
+        const bool sparse = nq <= (uint32_t)SPL;              // uniform in the wave
         float* xw = (float*)stg;                              // parked values
-        constexpr int SR = (SMP_SPARSE * EPL + 63) / 64;      // steps per load
+        constexpr int SR = (SPL * EPL + 63) / 64;             // steps per load
         // staging: writes only when the wave's candidates fit (its parked
         // values, all read by then, are overwritten); else nothing, and the
         // pass runs again after the barrier with the region as destination
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                 for (int r = 0; r < SR; ++r) {
                     const uint32_t k = (uint32_t)r * 64u + lane;     // value k % EPL of rank k / EPL
                     const bool valid = k < nq * EPL;
-                    f[j][r] = xw[j * SMP_SPARSE * EPL + (valid ? k : 0u)];
+                    f[j][r] = xw[j * SPL * EPL + (valid ? k : 0u)];
                     L[j][r] = xl[cc][wave][valid ? k / EPL : 0u];
                 }
             uint64_t b[NL][SR];
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
                 for (int j = 0; j < NL; ++j) {
 #pragma unroll
                     for (int h = 0; h < EPL / 4; ++h)
-                        *(llima_u32x4*)&xw[j * SMP_SPARSE * EPL + qr * EPL + 4 * h] =
+                        *(llima_u32x4*)&xw[j * SPL * EPL + qr * EPL + 4 * h] =
                             llima_u32x4{__float_as_uint(v[j * EPL + 4 * h]), __float_as_uint(v[j * EPL + 4 * h + 1]),
                                         __float_as_uint(v[j * EPL + 4 * h + 2]), __float_as_uint(v[j * EPL + 4 * h + 3])};
                 }

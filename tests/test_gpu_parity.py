@@ -258,16 +258,17 @@ def test_sample_masks_and_edges(gpu, oracle):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_sample_sparse_waves(gpu, oracle, dtype):
-    """Sweep waves with few lanes above the chunk bound take the sparse path;
-    with more candidates than a wave stages (12 lanes x all their values kept)
-    it writes them to the region directly."""
+    """Sweep waves with few lanes above the chunk bound take the sparse path
+    (at most 12 lanes for fp32, 8 for bf16); with more candidates than a wave
+    stages (those lanes' values all kept) it writes them to the region directly."""
     _say("sample sparse sweep waves", dtype)
     rng = np.random.default_rng(33)
     B, V = 4, 16384
     epl = 4 if dtype == "f32" else 8                              # values per 16-byte load
     ws = 1024 if dtype == "f32" else 2048                         # ids per wave slice
     x = np.full((B, V), -100.0, np.float32)
-    ids = np.array([j * 64 * epl + l * epl + e for j in range(4) for l in range(12)
+    lanes = 12 if dtype == "f32" else 8
+    ids = np.array([j * 64 * epl + l * epl + e for j in range(4) for l in range(lanes)
                     for e in range(epl)])
     x[:, ids] = rng.normal(0, 1, (B, ids.size)).astype(np.float32)
     x[1, ids + ws] = rng.normal(0, 1, ids.size)                   # the next wave's slice too
