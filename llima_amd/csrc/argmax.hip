@@ -226,8 +226,8 @@ __global__ __launch_bounds__(LLIMA_WG) void argmax_finish(ArgmaxParams P) {
     __shared__ int32_t tok[ARGMAX_MAX_GROUP];
     const int wave = (int)(threadIdx.x >> 6);
     if (P.epi == EPI_NONE) {
-        const int row = (int)blockIdx.x * LLIMA_WAVES + wave;
-        if (row >= P.B) return;
+        const int row = finish_row(blockIdx.x, (uint32_t)wave, (uint32_t)P.B);
+        if (row < 0) return;
         float v;
         const int32_t id = row_result<TL>(P, row, &v);
         if (lane_id() == 0) {
@@ -297,7 +297,7 @@ static hipError_t launch_argmax(const ArgmaxParams& P, hipStream_t st) {
     const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
     if (P.vec_ok) hipLaunchKernelGGL((argmax_sweep<TL, E, true>), g, b, 0, st, P);
     else hipLaunchKernelGGL((argmax_sweep<TL, E, false>), g, b, 0, st, P);
-    const uint32_t nfin = P.epi == EPI_NONE ? (uint32_t)(P.B + LLIMA_WAVES - 1) / LLIMA_WAVES
+    const uint32_t nfin = P.epi == EPI_NONE ? finish_row_blocks((uint32_t)P.B)
                         : P.epi == EPI_CHAIN ? (uint32_t)(P.B / (P.D + 1)) : 1u;
     hipLaunchKernelGGL((argmax_finish<TL>), dim3(nfin), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError();

@@ -369,4 +369,19 @@ __device__ __forceinline__ void map_row_chunk(uint32_t w, uint32_t B, uint32_t S
     }
 }
 
+// Finish kernels with one wavefront per row: (workgroup, wave) -> row, and the
+// workgroup count.  With B a multiple of 8 the sweep put row r's chunks on XCD
+// r % 8 (map_row_chunk); workgroup w runs on XCD w % 8 and takes rows of that
+// XCD, so the chunk results it reads are in its own L2.  Rows past B: -1.
+__device__ __forceinline__ int finish_row(uint32_t blk, uint32_t wave, uint32_t B) {
+    uint32_t r;
+    if ((B & 7u) == 0) r = (blk & 7u) + 8u * ((blk >> 3) * LLIMA_WAVES + wave);
+    else r = blk * LLIMA_WAVES + wave;
+    return r < B ? (int)r : -1;
+}
+inline uint32_t finish_row_blocks(uint32_t B) {
+    return (B & 7u) == 0 ? 8u * ((B + 8u * LLIMA_WAVES - 1u) / (8u * LLIMA_WAVES))
+                         : (B + LLIMA_WAVES - 1u) / LLIMA_WAVES;
+}
+
 }  // namespace llima

@@ -172,8 +172,8 @@ __global__ __launch_bounds__(LLIMA_WG) void score_sweep(ScoreParams P) {
 // One wavefront per row: M, S and the log-probability at the target.
 template <typename TL>
 __global__ __launch_bounds__(LLIMA_WG) void score_finish(ScoreParams P) {
-    const int row = (int)blockIdx.x * LLIMA_WAVES + (int)wave_id();
-    if (row >= P.B) return;
+    const int row = finish_row(blockIdx.x, wave_id(), (uint32_t)P.B);
+    if (row < 0) return;
     const uint32_t lane = lane_id();
     const uint64_t* k = P.keys + (size_t)row * P.S;
     const double* sm = P.sums + (size_t)row * P.S;
@@ -229,7 +229,7 @@ static hipError_t launch_score(const ScoreParams& P, hipStream_t st) {
     const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
     if (P.vec_ok) hipLaunchKernelGGL((score_sweep<TL, E, true>), g, b, 0, st, P);
     else hipLaunchKernelGGL((score_sweep<TL, E, false>), g, b, 0, st, P);
-    hipLaunchKernelGGL((score_finish<TL>), dim3((uint32_t)(P.B + LLIMA_WAVES - 1) / LLIMA_WAVES),
+    hipLaunchKernelGGL((score_finish<TL>), dim3(finish_row_blocks((uint32_t)P.B)),
                        dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError();
 }
