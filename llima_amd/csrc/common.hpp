@@ -113,12 +113,6 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// base + number of set bits of m below this lane.
-__device__ __forceinline__ uint32_t mbcnt_add(uint64_t m, uint32_t base) {
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, base));
-}
-
 __device__ __forceinline__ uint32_t readlane(uint32_t v, uint32_t l) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
 }
@@ -172,9 +166,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return wave_reduce<uint32_t>(v, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
-}
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-    return wave_reduce<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a | b; });
 }
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     return wave_reduce<uint32_t>(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
@@ -241,25 +232,6 @@ __device__ __forceinline__ uint32_t wave_rth_largest_exp(uint32_t key, uint32_t 
         }
     }
     return wave_rth_largest(key, r, lowbit);
-}
-
-// Descending bitonic sort of one uint32 per lane across a wavefront; returns
-// this lane's element of the sorted sequence (lane 0 holds the largest).
-__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
-    const uint32_t l = lane_id();
-#pragma unroll
-    for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            uint32_t w = __shfl_xor(v, stride, 64);
-            bool desc = (l & size) == 0;          // direction of this bitonic block
-            bool lower = (l & stride) == 0;       // this lane keeps the max if desc
-            bool take_max = (lower == desc);
-            uint32_t mx = v > w ? v : w, mn = v > w ? w : v;
-            v = take_max ? mx : mn;
-        }
-    }
-    return v;
 }
 
 // ------------------------------------------------------------------ block primitives
