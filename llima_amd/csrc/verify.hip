@@ -188,6 +188,7 @@ struct SeqShared {
     uint8_t ok[VR_MAX_D];              // draft k passes its acceptance test
     int32_t acc;
     BlockScratch bs;
+    uint64_t w2[2][LLIMA_WAVES];       // two scans at once
 };
 
 // Z and maximum of every row of sequence b, then the acceptance scan.  Every
@@ -328,6 +329,21 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     __shared__ uint64_t s_before;
     const int b = blockIdx.x;
     const uint32_t t = threadIdx.x;
+    // thread t owns the groups [t GPT, (t + 1) GPT): both arrays (residual and
+    // plain target sums) are read once and scanned together (the residual
+    // total decides which one the draw uses); the first VR_GB of each are
+    // requested before the acceptance scan, which they do not depend on
+    const int NG = P.NG, GPT = (NG + LLIMA_WG - 1) / LLIMA_WG;
+    const int g0 = (int)t * GPT, g1 = g0 + GPT < NG ? g0 + GPT : NG;
+    const uint64_t* gr = P.gres + (size_t)b * NG;
+    const uint64_t* gt = P.gtgt + (size_t)b * NG;
+    uint64_t vr0[VR_GB], vt0[VR_GB];
+#pragma unroll
+    for (int j = 0; j < VR_GB; ++j) {
+        const int gi = g0 + j < g1 ? g0 + j : 0;
+        vr0[j] = gr[gi];
+        vt0[j] = gt[gi];
+    }
     const int acc = accept_scan(P, b, sh);
     DrawCtx q = draw_ctx(P, b, acc, sh);
     if (t == 0) {
@@ -338,30 +354,44 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
         s_group = -1;
         s_tok = -1;
     }
-    // thread t owns the groups [t GPT, (t + 1) GPT), read VR_GB at a time with
-    // every load of a batch in flight together
-    const int NG = P.NG, GPT = (NG + LLIMA_WG - 1) / LLIMA_WG;
-    const int g0 = (int)t * GPT, g1 = g0 + GPT < NG ? g0 + GPT : NG;
-    const uint64_t* gr = P.gres + (size_t)b * NG;
-    const uint64_t* gt = P.gtgt + (size_t)b * NG;
-    auto range_sum = [&](const uint64_t* a) {
-        uint64_t sum = 0;
-        for (int gb = g0; gb < g1; gb += VR_GB) {
-            uint64_t v[VR_GB];
+    uint64_t sr = 0, st = 0;
 #pragma unroll
-            for (int j = 0; j < VR_GB; ++j) v[j] = gb + j < g1 ? a[gb + j] : 0ull;
-#pragma unroll
-            for (int j = 0; j < VR_GB; ++j) sum += v[j];
-        }
-        return sum;
-    };
-    if (q.residual) {
-        if (block_sum_u64(range_sum(gr), sh.bs) == 0) q.residual = false;   // p_t == p_d: draw from p_t
+    for (int j = 0; j < VR_GB; ++j) {
+        sr += g0 + j < g1 ? vr0[j] : 0ull;
+        st += g0 + j < g1 ? vt0[j] : 0ull;
     }
+    for (int gb = g0 + VR_GB; gb < g1; gb += VR_GB) {
+        uint64_t vr[VR_GB], vt[VR_GB];
+#pragma unroll
+        for (int j = 0; j < VR_GB; ++j) {
+            const int gi = gb + j < g1 ? gb + j : g0;
+            vr[j] = gr[gi];
+            vt[j] = gt[gi];
+        }
+#pragma unroll
+        for (int j = 0; j < VR_GB; ++j) {
+            sr += gb + j < g1 ? vr[j] : 0ull;
+            st += gb + j < g1 ? vt[j] : 0ull;
+        }
+    }
+    // exclusive scans of both sums over the workgroup, and their totals
+    const uint64_t ir = wave_incl_scan_u64(sr), it = wave_incl_scan_u64(st);
+    const uint32_t wv = t >> 6;
+    if (lane_id() == 63) { sh.w2[0][wv] = ir; sh.w2[1][wv] = it; }
+    __syncthreads();
+    uint64_t br = 0, bt = 0, tr = 0, tt = 0;
+#pragma unroll
+    for (int i = 0; i < LLIMA_WAVES; ++i) {
+        br += (uint32_t)i < wv ? sh.w2[0][i] : 0ull;
+        bt += (uint32_t)i < wv ? sh.w2[1][i] : 0ull;
+        tr += sh.w2[0][i];
+        tt += sh.w2[1][i];
+    }
+    if (q.residual && tr == 0) q.residual = false;          // p_t == p_d: draw from p_t
     const uint64_t* sums = q.residual ? gr : gt;
-    const uint64_t s = range_sum(sums);
-    uint64_t total;
-    const uint64_t before = block_excl_scan_u64(s, &total, sh.bs);
+    const uint64_t s = q.residual ? sr : st;
+    const uint64_t before = q.residual ? br + ir - sr : bt + it - st;
+    const uint64_t total = q.residual ? tr : tt;
     const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.u_resample[b]) * total) >> 32);
     if (total > 0 && s > 0 && before <= target && target < before + s) {
         uint64_t a = before;
