@@ -77,7 +77,7 @@ __device__ __forceinline__ int drow(const VerifyParams& P, int b, int k) {
 
 // Loads the chunk of 32 values per thread: 16-byte loads from clamped,
 // always-valid addresses (V is a multiple of 4), all in flight before the first
-// use; values past the end of the row become -inf.
+// use; in a row's last, partial chunk the values past the end become -inf.
 __device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, int V,
                                            float (&v)[VR_E]) {
     llima_u32x4 q[VR_E / 4];
@@ -89,11 +89,18 @@ __device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, in
     }
 #pragma unroll
     for (int j = 0; j < VR_E / 4; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
         const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            v[4 * j + e] = i0 + e < c1 ? __uint_as_float(w4[e]) : -__builtin_inff();
+        for (int e = 0; e < 4; ++e) v[4 * j + e] = __uint_as_float(w4[e]);
+    }
+    if (c1 - c0 < VR_CHUNK) {
+#pragma unroll
+        for (int j = 0; j < VR_E / 4; ++j) {
+            const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[4 * j + e] = i0 + e < c1 ? v[4 * j + e] : -__builtin_inff();
+        }
     }
 }
 
@@ -103,12 +110,18 @@ __device__ __forceinline__ uint64_t row_weight(float x, uint32_t mkey) {
     return weight(x, key_f32(mkey));
 }
 
-// weight(x, xmax) as the integral float it converts (W < 2^37, exact in
-// fp32): sums of at most 2^16 of them are exact in double, so the row sums skip
-// the per-value float -> uint64 conversion.  exp_neg's steps with two folds
-// that leave every result unchanged: d is clamped at -26 (NaN included) with no
-// select after, since rint(e^-26 2^36) = rint(0.35) = 0; and the two scalings
-// are one, 2^(n+36) (n >= -38 keeps every intermediate normal).
+// weight(x, xmax) for a finite xmax, as the integral float it converts
+// (W < 2^37, exact in fp32): sums of at most 2^16 of them are exact in double,
+// so the row sums skip the per-value float -> uint64 conversion.  exp_neg's
+// steps with three folds that leave every result unchanged:
+//   * d is clamped at -26 (NaN included) with no select after, since
+//     rint(e^-26 2^36) = rint(0.35) = 0;
+//   * the factor 2^36 is in the polynomial's coefficients: scaling every
+//     coefficient by a power of two scales every rounded step by it (the
+//     smallest, 2^36/5040, is far from the subnormals), and p 2^36 2^n with
+//     n >= -38 stays normal, so ldexp(p 2^36, n) = ldexp(ldexp(p, n), 36);
+//   * x == xmax needs no select: d = 0 gives n = 0, r = 0 and p = 2^36 exactly.
+#define VR_TWO36 68719476736.0f
 __device__ __forceinline__ float weight_f(float x, float xmax) {
     const float d = __builtin_fmaxf(x - xmax, -26.0f);   // fmaxf(NaN, -26) = -26
     const float kLog2e = 1.44269502162933349609375f;
@@ -117,16 +130,15 @@ __device__ __forceinline__ float weight_f(float x, float xmax) {
     const float n = __builtin_rintf(d * kLog2e);
     float r = __builtin_fmaf(n, -kLn2Hi, d);
     r = __builtin_fmaf(n, -kLn2Lo, r);
-    float p = 1.98412698412698412698e-04f;
-    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f);
-    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f);
-    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f);
-    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f);
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    const float w = __builtin_rintf(__builtin_ldexpf(p, (int)n + 36));
-    return x == xmax ? 68719476736.0f : w;             // 2^36 (also for an infinite maximum)
+    float p = 1.98412698412698412698e-04f * VR_TWO36;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f * VR_TWO36);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f * VR_TWO36);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f * VR_TWO36);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f * VR_TWO36);
+    p = __builtin_fmaf(p, r, 0.5f * VR_TWO36);
+    p = __builtin_fmaf(p, r, VR_TWO36);
+    p = __builtin_fmaf(p, r, VR_TWO36);
+    return __builtin_rintf(__builtin_ldexpf(p, (int)n));
 }
 
 __global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
@@ -166,8 +178,13 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     if (mkey > LLIMA_KEY_NEG_INF) {
         const float xm = key_f32(mkey);
         double sd = 0.0;                                 // exact: 32 terms below 2^37
+        if (xm == __builtin_inff()) {                    // W = 2^36 at every +inf, else 0
 #pragma unroll
-        for (int e = 0; e < VR_E; ++e) sd += (double)weight_f(v[e], xm);
+            for (int e = 0; e < VR_E; ++e) sd += v[e] == xm ? (double)VR_TWO36 : 0.0;
+        } else {
+#pragma unroll
+            for (int e = 0; e < VR_E; ++e) sd += (double)weight_f(v[e], xm);
+        }
         s = (uint64_t)sd;
     }
     s = block_sum_u64(s, bs);

@@ -455,6 +455,9 @@ def test_verify_rejection_edges(gpu, oracle):
     drf[2, 0, :] = -np.inf; drf[2, 0, 5] = 0.0            # one-hot draft row
     tgt[3, 1, :] = -np.inf                                  # degenerate target row
     tgt[4, 0, 100:200] = np.nan
+    tgt[0, 4, [7, 2999]] = np.inf                           # +inf maxima: W = 2^36 at each
+    drf[5, 1, 11] = np.inf
+    tgt[5, 1, 11] = np.inf
     ids = rng.integers(0, V, (B, D)).astype(np.int32)
     ids[5, 2] = V + 10                                      # out-of-range draft id
     ids[2, 0] = 5
