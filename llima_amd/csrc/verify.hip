@@ -15,10 +15,13 @@
 // sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111); with one-hot distributions
 // this reduces to that rule.
 //
-// Four launches, no atomics or fences between workgroups (each writes its own
-// workspace slots; a later launch reads them):
-//   vr_rowmax   per (row, chunk) maximum key
-//   vr_rowsum   per (row, chunk) sum of W, and W at each row's draft token
+// Four launches:
+//   vr_clear    marks every chunk-maximum slot unpublished (0: every key of a
+//               value, -inf included, is above 0)
+//   vr_rowpass  per (row, chunk of 8192 ids), one read of the rows: the chunk's
+//               maximum key, published in its slot; once every chunk of the row
+//               has published, the sum of W over the chunk (from the values
+//               still in registers), and W at the row's draft token
 //   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
 //               the sums by every workgroup of the sequence), then, for every
 //               group of 32 ids of the draw row, the sum of the residual
@@ -26,8 +29,15 @@
 //   vr_final    per sequence: acceptance, emitted drafts, the group holding the
 //               draw target (a block scan over the group sums), and the token
 //               inside it (one wave, one id per lane).
-// Pass 2 re-reads the rows right after pass 1; at these sizes they are still
-// resident in the 256 MB Infinity Cache.
+// vr_rowpass workgroups wait for the other chunks of their row, which the
+// dispatcher normally starts alongside them (a row's chunks are consecutive
+// workgroups).  The wait never depends on that: a workgroup that has polled
+// VR_HELP_AFTER times reads the lowest unpublished chunk of its row itself and
+// publishes its maximum (the value the chunk's own workgroup publishes too),
+// so every wait ends after at most VR_HELP_AFTER + S polls, whatever the order
+// and residency of the workgroups.  Slots are written and polled with
+// device-scope atomics (the chunks of a row may run on different XCDs, whose
+// L2 caches are not coherent with each other).
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -39,6 +49,7 @@ namespace llima {
 #define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup
 #define VR_G 32                      // ids per draw group (4 threads of vr_drawsum)
 #define VR_GB 16                     // group sums a vr_final thread loads at once
+#define VR_HELP_AFTER 64             // polls (~1 us each) before a waiter reads a late chunk itself
 
 struct VerifyParams {
     const float* tgt;
@@ -141,38 +152,71 @@ __device__ __forceinline__ float weight_f(float x, float xmax) {
     return __builtin_rintf(__builtin_ldexpf(p, (int)n));
 }
 
-__global__ __launch_bounds__(LLIMA_WG) void vr_rowmax(VerifyParams P) {
-    __shared__ BlockScratch bs;
-    const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
-    const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
-    float v[VR_E];
-    load_chunk(row_ptr(P, r), c0, c1, P.V, v);
-    uint32_t m = 0;
-#pragma unroll
-    for (int e = 0; e < VR_E; ++e) {
-        const uint32_t k = v[e] == v[e] ? f32_key(v[e]) : 0u;   // NaN never counts
-        m = k > m ? k : m;
-    }
-    m = block_max_u32(m, bs);
-    if (threadIdx.x == 0) P.maxk[(size_t)r * P.S + c] = m;
+__global__ __launch_bounds__(LLIMA_WG) void vr_clear(VerifyParams P) {
+    const int n = P.NR * P.S;
+    for (int i = (int)(blockIdx.x * LLIMA_WG + threadIdx.x); i < n; i += (int)(gridDim.x * LLIMA_WG))
+        P.maxk[i] = 0;
 }
 
-__global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
+// Maximum key of chunk c of a row (every thread gets it), read in quarters.
+__device__ __forceinline__ uint32_t chunk_max_key(const float* rowp, int c, int V, BlockScratch& bs) {
+    const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < V ? c0 + VR_CHUNK : V;
+    float m = -__builtin_inff();
+#pragma unroll 1
+    for (int j = 0; j < VR_E / 4; ++j) {                // 4 registers: the waiter's own chunk stays live
+        const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
+        const int ia = i0 < V ? i0 : V - 4;
+        const llima_u32x4 q = *(const llima_u32x4*)(rowp + ia);
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = __uint_as_float(w4[e]);
+            m = i0 + e < c1 && x > m ? x : m;
+        }
+    }
+    return block_max_u32(f32_key(m), bs);
+}
+
+__global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
     __shared__ BlockScratch bs;
     __shared__ uint32_t s_mkey;
-    const int r = blockIdx.x / P.S, c = blockIdx.x % P.S;
+    __shared__ int32_t s_miss;
+    const int r = (int)blockIdx.x / P.S, c = (int)blockIdx.x - r * P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
     float v[VR_E];
     load_chunk(rowp, c0, c1, P.V, v);
-    if (threadIdx.x < 64) {
-        const uint32_t* m = P.maxk + (size_t)r * P.S;
-        uint32_t best = 0;
-        for (int i = (int)threadIdx.x; i < P.S; i += 64) best = m[i] > best ? m[i] : best;
-        best = wave_max_u32(best);
-        if (threadIdx.x == 0) s_mkey = best;
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < VR_E; ++e) m = v[e] > m ? v[e] : m;   // NaN never counts
+    const uint32_t k = block_max_u32(f32_key(m), bs);          // >= f32_key(-inf) > 0
+    uint32_t* slot = P.maxk + (size_t)r * P.S;
+    if (threadIdx.x == 0) __hip_atomic_store(&slot[c], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the row maximum: wave 0 polls the row's slots until all are published
+    for (int round = 0;; ++round) {
+        if (threadIdx.x < 64) {
+            uint32_t best = 0, miss = 0xFFFFFFFFu;
+            for (int i = (int)threadIdx.x; i < P.S; i += 64) {
+                const uint32_t x = __hip_atomic_load(&slot[i], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                if (x == 0) miss = (uint32_t)i < miss ? (uint32_t)i : miss;
+                best = x > best ? x : best;
+            }
+            best = wave_max_u32(best);
+            miss = wave_min_u32(miss);
+            if (threadIdx.x == 0) { s_mkey = best; s_miss = (int32_t)miss; }
+            if (miss != 0xFFFFFFFFu && round < VR_HELP_AFTER) __builtin_amdgcn_s_sleep(8);
+        }
+        __syncthreads();
+        const int miss = s_miss;
+        if (miss < 0) break;                                    // every chunk published
+        if (round >= VR_HELP_AFTER) {                           // a late chunk: read it here
+            const uint32_t km = chunk_max_key(rowp, miss, P.V, bs);
+            if (threadIdx.x == 0)
+                __hip_atomic_store(&slot[miss], km, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
     }
-    __syncthreads();
     const uint32_t mkey = s_mkey;
     uint64_t s = 0;
     if (mkey > LLIMA_KEY_NEG_INF) {
@@ -190,9 +234,9 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowsum(VerifyParams P) {
     s = block_sum_u64(s, bs);
     if (threadIdx.x == 0) {
         P.sums[(size_t)r * P.S + c] = s;
-        const int b = seq_of(P, r), k = pos_of(P, r);
-        if (k < P.D) {
-            const int x = P.draft_ids[b * P.D + k];
+        const int b = seq_of(P, r), kk = pos_of(P, r);
+        if (kk < P.D) {
+            const int x = P.draft_ids[b * P.D + kk];
             if (x >= c0 && x < c1) P.wx[r] = row_weight(rowp[x], mkey);
         }
     }
@@ -485,8 +529,9 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.gtgt = (uint64_t*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
-    hipLaunchKernelGGL(vr_rowmax, dim3(g12), dim3(LLIMA_WG), 0, st, P);
-    hipLaunchKernelGGL(vr_rowsum, dim3(g12), dim3(LLIMA_WG), 0, st, P);
+    const uint32_t gc = (g12 + LLIMA_WG - 1) / LLIMA_WG;
+    hipLaunchKernelGGL(vr_clear, dim3(gc < 64 ? gc : 64), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_rowpass, dim3(g12), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
