@@ -25,10 +25,12 @@
 //   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
 //               the sums by every workgroup of the sequence), then, for every
 //               group of 32 ids of the draw row, the sum of the residual
-//               weights and the sum of the plain target weights
-//   vr_final    per sequence: acceptance, emitted drafts, the group holding the
-//               draw target (a block scan over the group sums), and the token
-//               inside it (one wave, one id per lane).
+//               weights and the sum of the plain target weights.  Workgroup 0
+//               of a sequence also writes accepted_len, the emitted drafts and
+//               the draw context for vr_final
+//   vr_final    per sequence: the group holding the draw target (a block scan
+//               over the group sums), and the token inside it (one wave, one id
+//               per lane).
 // vr_rowpass workgroups wait for the other chunks of their row, which the
 // dispatcher normally starts alongside them (a row's chunks are consecutive
 // workgroups).  The wait never depends on that: a workgroup that has polled
@@ -51,6 +53,14 @@ namespace llima {
 #define VR_GB 16                     // group sums a vr_final thread loads at once
 #define VR_HELP_AFTER 64             // polls (~1 us each) before a waiter reads a late chunk itself
 
+// Draw context of a sequence: what vr_final needs of its acceptance step.
+struct SeqCtx {
+    uint64_t zt, zd;     // Z of the draw's target row, and of its draft row (residual draw)
+    uint32_t mt, md;     // their maximum keys
+    int32_t acc;         // accepted drafts: the draw uses target row acc
+    int32_t shift;       // residual scaling
+};
+
 struct VerifyParams {
     const float* tgt;
     const float* drf;
@@ -64,6 +74,7 @@ struct VerifyParams {
     uint64_t* wx;        // [NR]
     uint64_t* gres;      // [B][NG] residual weight per group of VR_G ids
     uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
+    SeqCtx* ctx;         // [B]
     int32_t B, D, V, S, NR, NG, SD;
 };
 
@@ -249,7 +260,6 @@ struct SeqShared {
     uint8_t ok[VR_MAX_D];              // draft k passes its acceptance test
     int32_t acc;
     BlockScratch bs;
-    uint64_t w2[2][LLIMA_WAVES];       // two scans at once
 };
 
 // Z and maximum of every row of sequence b, then the acceptance scan.  Every
@@ -364,6 +374,18 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
     const int b = blockIdx.x / P.SD, c = blockIdx.x % P.SD;
     const int acc = accept_scan(P, b, sh);
     const DrawCtx q = draw_ctx(P, b, acc, sh);       // residual iff a draft was rejected
+    if (c == 0) {
+        const int t = (int)threadIdx.x;
+        if (t == 0) {
+            SeqCtx x;
+            x.zt = q.zt; x.zd = q.zd; x.mt = q.mt; x.md = q.md;
+            x.acc = acc; x.shift = q.shift;
+            P.ctx[b] = x;
+            P.accepted_len[b] = acc;
+        }
+        if (t <= P.D)                                  // vr_final writes the drawn token at acc
+            P.emitted[(size_t)b * (P.D + 1) + t] = t < acc ? P.draft_ids[b * P.D + t] : -1;
+    }
     const int i0 = c * VR_DCHUNK + (int)threadIdx.x * 8;
     float xt[8], xd[8];
     load8(q.t, i0, P.V, xt);
@@ -385,15 +407,14 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
 }
 
 __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
-    __shared__ SeqShared sh;
+    __shared__ uint64_t s_w2[2][LLIMA_WAVES];          // two scans at once
     __shared__ int32_t s_group, s_tok;
     __shared__ uint64_t s_before;
     const int b = blockIdx.x;
     const uint32_t t = threadIdx.x;
     // thread t owns the groups [t GPT, (t + 1) GPT): both arrays (residual and
     // plain target sums) are read once and scanned together (the residual
-    // total decides which one the draw uses); the first VR_GB of each are
-    // requested before the acceptance scan, which they do not depend on
+    // total decides which one the draw uses)
     const int NG = P.NG, GPT = (NG + LLIMA_WG - 1) / LLIMA_WG;
     const int g0 = (int)t * GPT, g1 = g0 + GPT < NG ? g0 + GPT : NG;
     const uint64_t* gr = P.gres + (size_t)b * NG;
@@ -405,13 +426,14 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
         vr0[j] = gr[gi];
         vt0[j] = gt[gi];
     }
-    const int acc = accept_scan(P, b, sh);
-    DrawCtx q = draw_ctx(P, b, acc, sh);
+    const SeqCtx x = P.ctx[b];
+    const int acc = x.acc;
+    DrawCtx q;
+    q.residual = acc < P.D;
+    q.t = row_ptr(P, trow(P, b, acc));
+    q.d = q.residual ? row_ptr(P, drow(P, b, acc)) : nullptr;
+    q.mt = x.mt; q.md = x.md; q.zt = x.zt; q.zd = x.zd; q.shift = x.shift;
     if (t == 0) {
-        int32_t* em = P.emitted + (size_t)b * (P.D + 1);
-        for (int j = 0; j < acc; ++j) em[j] = P.draft_ids[b * P.D + j];
-        for (int j = acc; j <= P.D; ++j) em[j] = -1;
-        P.accepted_len[b] = acc;
         s_group = -1;
         s_tok = -1;
     }
@@ -438,15 +460,15 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     // exclusive scans of both sums over the workgroup, and their totals
     const uint64_t ir = wave_incl_scan_u64(sr), it = wave_incl_scan_u64(st);
     const uint32_t wv = t >> 6;
-    if (lane_id() == 63) { sh.w2[0][wv] = ir; sh.w2[1][wv] = it; }
+    if (lane_id() == 63) { s_w2[0][wv] = ir; s_w2[1][wv] = it; }
     __syncthreads();
     uint64_t br = 0, bt = 0, tr = 0, tt = 0;
 #pragma unroll
     for (int i = 0; i < LLIMA_WAVES; ++i) {
-        br += (uint32_t)i < wv ? sh.w2[0][i] : 0ull;
-        bt += (uint32_t)i < wv ? sh.w2[1][i] : 0ull;
-        tr += sh.w2[0][i];
-        tt += sh.w2[1][i];
+        br += (uint32_t)i < wv ? s_w2[0][i] : 0ull;
+        bt += (uint32_t)i < wv ? s_w2[1][i] : 0ull;
+        tr += s_w2[0][i];
+        tt += s_w2[1][i];
     }
     if (q.residual && tr == 0) q.residual = false;          // p_t == p_d: draw from p_t
     const uint64_t* sums = q.residual ? gr : gt;
@@ -496,7 +518,8 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
     const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
     const size_t NR = (size_t)B * (2 * D + 1);
     const size_t NG = (size_t)(V + VR_G - 1) / VR_G;
-    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * NG * 8);
+    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * NG * 8) +
+           al256((size_t)B * sizeof(SeqCtx));
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -526,7 +549,8 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
     P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
     P.gres = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
-    P.gtgt = (uint64_t*)w;
+    P.gtgt = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
+    P.ctx = (SeqCtx*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
     const uint32_t gc = (g12 + LLIMA_WG - 1) / LLIMA_WG;
