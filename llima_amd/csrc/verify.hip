@@ -34,12 +34,16 @@
 // vr_rowpass workgroups wait for the other chunks of their row, which the
 // dispatcher normally starts alongside them (a row's chunks are consecutive
 // workgroups).  The wait never depends on that: a workgroup that has polled
-// VR_HELP_AFTER times reads the lowest unpublished chunk of its row itself and
+// help_after times reads the lowest unpublished chunk of its row itself and
 // publishes its maximum (the value the chunk's own workgroup publishes too),
-// so every wait ends after at most VR_HELP_AFTER + S polls, whatever the order
+// so every wait ends after at most help_after + S polls, whatever the order
 // and residency of the workgroups.  Slots are written and polled with
 // device-scope atomics (the chunks of a row may run on different XCDs, whose
-// L2 caches are not coherent with each other).
+// L2 caches are not coherent with each other).  help_after is VR_HELP_AFTER
+// unless the environment variable LLIMA_VERIFY_HELP_AFTER gives another count
+// (0 makes every waiter read its row's late chunks itself: a test setting).
+#include <cstdlib>
+
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -76,6 +80,7 @@ struct VerifyParams {
     uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
     SeqCtx* ctx;         // [B]
     int32_t B, D, V, S, NR, NG, SD;
+    int32_t help_after;  // polls before a waiter reads a late chunk itself
 };
 
 // Row r: target rows first ([B][D+1]), then draft rows ([B][D]).
@@ -216,12 +221,12 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
             best = wave_max_u32(best);
             miss = wave_min_u32(miss);
             if (threadIdx.x == 0) { s_mkey = best; s_miss = (int32_t)miss; }
-            if (miss != 0xFFFFFFFFu && round < VR_HELP_AFTER) __builtin_amdgcn_s_sleep(8);
+            if (miss != 0xFFFFFFFFu && round < P.help_after) __builtin_amdgcn_s_sleep(8);
         }
         __syncthreads();
         const int miss = s_miss;
         if (miss < 0) break;                                    // every chunk published
-        if (round >= VR_HELP_AFTER) {                           // a late chunk: read it here
+        if (round >= P.help_after) {                            // a late chunk: read it here
             const uint32_t km = chunk_max_key(rowp, miss, P.V, bs);
             if (threadIdx.x == 0)
                 __hip_atomic_store(&slot[miss], km, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -544,6 +549,11 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.NR = B * (2 * D + 1);
     P.NG = (V + VR_G - 1) / VR_G;
     P.SD = (V + VR_DCHUNK - 1) / VR_DCHUNK;
+    P.help_after = VR_HELP_AFTER;
+    if (const char* e = std::getenv("LLIMA_VERIFY_HELP_AFTER")) {
+        const long h = std::strtol(e, nullptr, 10);
+        P.help_after = h < 0 ? 0 : h > (1L << 20) ? (1 << 20) : (int32_t)h;
+    }
     char* w = (char*)workspace;
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);

@@ -470,6 +470,24 @@ def test_verify_rejection_edges(gpu, oracle):
     assert eacc[0] == D                                     # identical rows accept every draft
 
 
+@pytest.mark.parametrize("B,D,V", [(16, 7, 128256), (3, 2, 70000), (2, 0, 9000)])
+def test_verify_rejection_help_path(gpu, oracle, monkeypatch, B, D, V):
+    """LLIMA_VERIFY_HELP_AFTER=0: a row-pass workgroup that finds one of its
+    row's chunk maxima unpublished reads that chunk itself at once, so the path
+    that bounds every wait runs on most rows; the results are unchanged."""
+    import llima_amd
+    _say("verify_rejection help path", B, D, V)
+    monkeypatch.setenv("LLIMA_VERIFY_HELP_AFTER", "0")
+    w = wl.speculative(B=B, D=D, V=V, seed=61 + V)
+    acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
+                                         _t(w["draft_ids"], gpu), _t(w["u_accept"], gpu),
+                                         _t(w["u_resample"], gpu))
+    eacc, eem = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
+                                        w["u_resample"])
+    assert (_np(acc) == eacc).all(), (_np(acc), eacc)
+    assert (_np(em) == eem).all()
+
+
 def test_workspace_reuse_across_shapes(gpu, oracle):
     """One workspace buffer per entry point serves calls of any shape, in any
     order (the kernels keep no state in the workspace between calls)."""
