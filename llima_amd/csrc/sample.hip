@@ -649,16 +649,20 @@ __device__ __forceinline__ uint64_t wg_prefix_u64(uint64_t inc, uint64_t v, uint
 }
 
 // Top-p boundary: the smallest key theta such that an element with key theta
-// has (mass strictly above) * 2^32 < PZ; when none has (PZ == 0) the top key.
-// Radix rounds over 8-bit digits with one barrier each: round r counts into
-// buffer r % 3 (buffers 0 and 1 zero on entry; non-members count into a spare
-// bin per lane), then every wave scans all 256 bins itself and zeroes buffer
-// (r + 2) % 3.  Stops early when the selected bin holds one key.
+// has (mass strictly above) * 2^32 < p32 * Z, Z the mass of every element
+// (every nonzero key lies in [kmin, kmax]); when none has (p32 == 0) the top
+// key.  Radix rounds over 8-bit digits with one barrier each: round r counts
+// into buffer r % 3 (buffers 0 and 1 zero on entry; non-members count into a
+// spare bin per lane), then every wave scans all 256 bins itself and zeroes
+// buffer (r + 2) % 3.  Round 0 holds every element, so its total is Z.  Stops
+// early when the selected bin holds one key.
 template <int EPT>
 __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
-                                  llima_u128 PZ, uint32_t kmin, uint32_t kmax, FinShared& sh) {
+                                  uint64_t p32, uint32_t kmin, uint32_t kmax, FinShared& sh) {
     Digits d = digits_init(kmin, kmax);
     uint64_t acc = 0;
+    llima_u128 PZ = 0;
+    bool first = true;
     const uint32_t t = threadIdx.x, lane = lane_id();
     uint32_t buf = 0;
     while (d.top >= 0) {
@@ -686,7 +690,10 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
         const uint32_t nxt = buf == 0u ? 2u : buf - 1u;
         sh.hmass[nxt][t] = 0;
         const uint64_t m4 = ms[0] + ms[1] + ms[2] + ms[3];
-        uint64_t ab = acc + wave_incl_scan_u64(m4) - m4;           // mass above the lane's top bin
+        const uint64_t inc = wave_incl_scan_u64(m4);
+        if (first) PZ = (llima_u128)p32 * readlane63(inc);          // p32 * Z
+        first = false;
+        uint64_t ab = acc + inc - m4;                               // mass above the lane's top bin
         // last qualifying bin of the lane (lowest key), first non-empty bin
         int qi = -1, ni = -1;
         uint64_t qab = 0, nab = 0;
@@ -1323,20 +1330,14 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     // ---- many survivors: weights, top-p radix, min-p, draw by a scan in id order
     const uint32_t tau = lowkey;
     uint64_t w[EPT];
-    uint64_t Z = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         key[j] = key[j] < tau ? 0u : key[j];
         const uint64_t wj = weight(key_f32(key[j]), xmax);   // no branch: key 0 is NaN, weight 0
         w[j] = key[j] ? wj : 0ull;
-        Z += w[j];
     }
     uint32_t theta = 0;
-    if (c.p < 1.0f) {
-        Z = block_sum_u64(Z, sh.bs);
-        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        theta = fin_topp_desc<EPT>(key, w, PZ, tau > kmin ? tau : kmin, kmax, sh);
-    }
+    if (c.p < 1.0f) theta = fin_topp_desc<EPT>(key, w, frac32(c.p), tau > kmin ? tau : kmin, kmax, sh);
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     uint32_t fmask = 0;
 #pragma unroll
