@@ -488,6 +488,63 @@ def test_verify_rejection_help_path(gpu, oracle, monkeypatch, B, D, V):
     assert (_np(em) == eem).all()
 
 
+def test_workspace_garbage(gpu, oracle):
+    """Every entry point gives the same results on a workspace that holds
+    arbitrary bytes (all ones, then random): nothing in it is read before the
+    call wrote it (the rejection row pass marks its own slots unpublished
+    first)."""
+    import torch
+    import llima_amd
+    from llima_amd.sampler import Workspace
+    _say("workspace garbage")
+    rng = np.random.default_rng(99)
+    x = rng.normal(0, 3, (4, 30000)).astype(np.float32)
+    h = rng.integers(0, 30000, size=(4, 200)).astype(np.int32)
+    u = rng.random(4).astype(np.float32)
+    cw = wl.constrained(B=2, V=20000, runs=40, seed=5)
+    xb = wl.f32_to_bf16_bits(rng.normal(0, 4, (3, 70000)).astype(np.float32))
+    sp = wl.speculative(B=3, D=4, V=30000, seed=6)
+    tr = rng.normal(0, 3, (6, 9000)).astype(np.float32)
+    ri = np.array([[0, 1, 3], [0, 2, -1]], np.int32)
+    cand = rng.integers(0, 9000, size=(2, 3)).astype(np.int32)
+    cent = wl.f32_to_bf16_bits(rng.normal(0, 2, (2, 512)).astype(np.float32))
+    order = rng.permutation(65536).astype(np.uint32)
+    xm = wl.f32_to_bf16_bits(rng.normal(0, 2, (2, 65536)).astype(np.float32))
+
+    def run_all():
+        out = []
+        cfg = llima_amd.SamplerConfig(temperature=0.8, top_k=40, top_p=0.9, min_p=0.02,
+                                      repetition_penalty=1.2, presence_penalty=0.3,
+                                      frequency_penalty=0.2)
+        out += [_np(t) for t in llima_amd.sample(_t(x, gpu), _t(u, gpu), cfg, history=_t(h, gpu))]
+        out += [_np(t) for t in llima_amd.sample(_t(cw["logits"], gpu), _t(cw["uniforms"], gpu),
+                                                  llima_amd.SamplerConfig(**cw["cfg"]),
+                                                  bitmask=_t(cw["bitmask"], gpu))]
+        out += [_np(t) for t in llima_amd.argmax(_t(xb, gpu))]
+        out += [_np(t) for t in llima_amd.verify_greedy(_t(sp["target"], gpu),
+                                                         _t(sp["draft_ids"], gpu))]
+        out += [_np(t) for t in llima_amd.verify_rejection(
+            _t(sp["target"], gpu), _t(sp["draft"], gpu), _t(sp["draft_ids"], gpu),
+            _t(sp["u_accept"], gpu), _t(sp["u_resample"], gpu))]
+        out += [np.array(llima_amd.verify_tree(_t(tr, gpu), _t(ri, gpu), _t(cand, gpu)))]
+        out += [_np(t) for t in llima_amd.score_logits(
+            _t(xb, gpu), torch.from_numpy(np.array([5, 7, 9], np.int32)))]
+        out += [_np(llima_amd.argmax_gemma4_mtp_masked_rows(_t(cent, gpu), _t(order, gpu), 8,
+                                                             _t(xm, gpu)))]
+        return out
+
+    ref = run_all()
+    for fill in ("ones", "random"):
+        for buf in Workspace._bufs.values():
+            if fill == "ones":
+                buf.fill_(255)
+            else:
+                buf.copy_(torch.randint(0, 256, buf.shape, dtype=torch.uint8, device=buf.device))
+        got = run_all()
+        for i, (a, b) in enumerate(zip(ref, got)):
+            assert np.array_equal(a, b, equal_nan=True), (fill, i)
+
+
 def test_workspace_reuse_across_shapes(gpu, oracle):
     """One workspace buffer per entry point serves calls of any shape, in any
     order (the kernels keep no state in the workspace between calls)."""
