@@ -711,3 +711,84 @@ def test_mtp_masked_argmax_reference_vectors_and_errors(gpu, oracle):
                                                   _t(x, gpu)) == 0
     with pytest.raises(RuntimeError):
         llima_amd.argmax_gemma4_mtp_masked_row(_t(cent, gpu), _t(order, gpu), 5, _t(x, gpu))
+
+
+# ----------------------------------------------------------------- maximum sizes
+def test_sample_maximum_sizes(gpu, oracle):
+    """V = 2^24, the largest llima_sample takes: 4096 fp32 (2048 bf16) chunks a
+    row, more than the finish gathers, so every row takes the exact full-row
+    path; with a 65535-id history, the largest H_max."""
+    _say("sample maximum sizes")
+    rng = np.random.default_rng(11)
+    V = 1 << 24
+    x = rng.normal(0, 3, (2, V)).astype(np.float32)
+    h = rng.integers(0, V, size=(2, 65535)).astype(np.int32)
+    h[:, :4000] = np.argsort(x, axis=1)[:, -4000:]          # the top of each row repeated
+    u = rng.random(2).astype(np.float32)
+    _sample_both(gpu, oracle, x, u, dict(temperature=0.9, top_k=40, top_p=0.9,
+                                         repetition_penalty=1.2, presence_penalty=0.2), history=h)
+    xb = wl.f32_to_bf16_bits(x[:1])
+    _sample_both(gpu, oracle, xb, u[:1], dict(temperature=1.0, top_k=64, top_p=0.95, min_p=0.01),
+                 history=h[:1])
+
+
+def test_argmax_and_verify_greedy_maximum_sizes(gpu, oracle):
+    """Rows longer than 2^24 ids (argmax has no vocabulary limit): the index
+    part of the 64-bit keys and the split arithmetic past 2^24."""
+    import llima_amd
+    _say("argmax maximum sizes")
+    rng = np.random.default_rng(12)
+    V = (1 << 24) + 1003
+    x = rng.integers(-40, 41, size=(2, V)).astype(np.float32) * np.float32(0.25)
+    x[0, V - 1] = 100.0                                      # the last id
+    x[1, [(1 << 24) + 5, (1 << 24) + 7]] = 100.0             # ties past 2^24
+    for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters")]:
+        ids, vals = llima_amd.argmax(_t(x, gpu), split_dim=(1 << 22) + 1, mode=mname)
+        eids, evals = oracle.argmax(x, split_dim=(1 << 22) + 1, mode=mode)
+        assert (_np(ids) == eids).all(), (mname, _np(ids), eids)
+        assert (_np(vals).view(np.uint32) == evals.view(np.uint32)).all()
+    t = x.reshape(1, 2, V)
+    dr = np.array([[V - 1]], np.int32)
+    acc, em = llima_amd.verify_greedy(_t(t, gpu), _t(dr, gpu))
+    eacc, eem = oracle.verify_greedy(t, dr)
+    assert (_np(acc) == eacc).all() and (_np(em) == eem).all()
+
+
+def test_verify_rejection_maximum_sizes(gpu, oracle):
+    """V = 2^22, the largest llima_verify_rejection takes: 512 chunks a row
+    (the row pass polls 8 slots a lane), 2048 draw workgroups per sequence."""
+    import llima_amd
+    _say("verify_rejection maximum sizes")
+    w = wl.speculative(B=2, D=2, V=1 << 22, seed=13)
+    for ids in [w["draft_ids"], w["target"][:, :2].argmax(-1).astype(np.int32)]:
+        acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
+                                             _t(ids, gpu), _t(w["u_accept"], gpu),
+                                             _t(w["u_resample"], gpu))
+        eacc, eem = oracle.verify_rejection(w["target"], w["draft"], ids, w["u_accept"],
+                                            w["u_resample"])
+        assert (_np(acc) == eacc).all(), (_np(acc), eacc)
+        assert (_np(em) == eem).all()
+
+
+def test_score_and_mtp_maximum_sizes(gpu, oracle):
+    """score_logits over rows longer than 2^24 ids; the MTP masked argmax at
+    C = 8192 centroids and the largest V below 2^24 that C divides (65504
+    candidates a row)."""
+    import torch
+    import llima_amd
+    _say("score / mtp maximum sizes")
+    rng = np.random.default_rng(14)
+    V = (1 << 24) + 5
+    x = rng.normal(0, 3, (2, V)).astype(np.float32)
+    x[1, V - 2] = x[1].max() + 1
+    targets = np.array([V - 1, V - 2], np.int32)
+    lp, g = llima_amd.score_logits(_t(x, gpu), torch.from_numpy(targets))
+    _score_check(_np(lp), _np(g), x, targets, oracle)
+    C, k = 8192, 32
+    Vm = (1 << 24) - C
+    cent = wl.f32_to_bf16_bits(rng.integers(-20, 21, size=(1, C)).astype(np.float32) * 0.5)
+    ordering = rng.permutation(Vm).astype(np.uint32)
+    xm = wl.f32_to_bf16_bits(rng.normal(0, 2, (1, Vm)).astype(np.float32))
+    ids = llima_amd.argmax_gemma4_mtp_masked_rows(_t(cent, gpu), _t(ordering, gpu), k, _t(xm, gpu))
+    ec, eid = _mtp_expected(oracle, cent[0], ordering, k, xm[0])
+    assert int(_np(ids)[0]) == eid
