@@ -67,6 +67,9 @@ enum {
 
 enum { LLIMA_F32 = 0, LLIMA_BF16 = 1 };
 
+/* A call with B = 0 rows (or sequences) launches nothing and returns LLIMA_OK
+ * once its sizes and modes are valid; its per-row buffers may then be null. */
+
 /* argmax modes (NaN and split handling of the reference variants):
  *  SPLIT_FIRST: per split of split_dim values, argmax_bf16 semantics (start at
  *               the split's first value, strict '>': a NaN first value hides

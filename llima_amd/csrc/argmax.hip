@@ -344,7 +344,7 @@ extern "C" int llima_argmax(const void* logits, int32_t dtype, int32_t B, int32_
                             int64_t row_stride, int32_t split_dim, int32_t mode,
                             int32_t* out_ids, float* out_vals, void* workspace,
                             size_t workspace_bytes, void* stream) {
-    if (!logits || !out_ids) return LLIMA_E_INVAL;
+    if (B > 0 && (!logits || !out_ids)) return LLIMA_E_INVAL;   // B = 0: empty buffers may be null
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
     if (B < 0 || V <= 0 || row_stride < V) return LLIMA_E_INVAL;
     if (mode < LLIMA_ARGMAX_SPLIT_FIRST || mode > LLIMA_ARGMAX_QUARTERS) return LLIMA_E_INVAL;
@@ -372,7 +372,8 @@ extern "C" int llima_verify_greedy(const void* target_logits, int32_t dtype, int
                                    int32_t V, const int32_t* draft_ids, int32_t* accepted_len,
                                    int32_t* emitted, void* workspace, size_t workspace_bytes,
                                    void* stream) {
-    if (!target_logits || !accepted_len || !emitted || (D > 0 && !draft_ids)) return LLIMA_E_INVAL;
+    if (B > 0 && (!target_logits || !accepted_len || !emitted || (D > 0 && !draft_ids)))
+        return LLIMA_E_INVAL;
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
     if (B < 0 || D < 0 || D + 1 > ARGMAX_MAX_GROUP || V <= 0) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;

@@ -1858,7 +1858,7 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
                             const float* uniforms, const llima_sampler_config* cfg,
                             int32_t* out_ids, float* out_probs, uint32_t* out_keep,
                             void* workspace, size_t workspace_bytes, void* stream) {
-    if (!logits || !cfg || !out_ids || !uniforms) return LLIMA_E_INVAL;
+    if (!cfg || (B > 0 && (!logits || !out_ids || !uniforms))) return LLIMA_E_INVAL;
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
     if (B < 0 || V <= 0 || V > (1 << 24) || row_stride < V) return LLIMA_E_INVAL;
     if (history && (H_max < 0 || H_max >= 65536)) return LLIMA_E_INVAL;

@@ -449,7 +449,7 @@ extern "C" int llima_score_logits(const void* logits, int32_t dtype, int32_t B, 
                                   int64_t row_stride, const int32_t* targets, double* out_logprob,
                                   int32_t* out_is_greedy, void* workspace, size_t workspace_bytes,
                                   void* stream) {
-    if (!logits || !targets || !out_logprob || !out_is_greedy) return LLIMA_E_INVAL;
+    if (B > 0 && (!logits || !targets || !out_logprob || !out_is_greedy)) return LLIMA_E_INVAL;
     if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
     if (B < 0 || V <= 0 || row_stride < V) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
@@ -499,15 +499,15 @@ extern "C" int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t 
                                        int64_t row_stride, int32_t* out_ids, int32_t* out_status,
                                        uint32_t* out_candidates, void* workspace,
                                        size_t workspace_bytes, void* stream) {
-    if (!centroid_logits || !token_ordering) return LLIMA_E_INVAL;
+    if (!token_ordering || (B > 0 && !centroid_logits)) return LLIMA_E_INVAL;
     if (B < 0 || V <= 0 || C <= 0 || C > MTP_MAX_C || centroid_stride < C) return LLIMA_E_INVAL;
     if (V % C != 0) return LLIMA_E_INVAL;                 // gemma4_mtp_helpers.cpp:118-125
     if (V >= (1 << 24)) return LLIMA_E_INVAL;             // candidate indices stay exact in fp32
     if (top_k <= 0 || top_k > C) return LLIMA_E_INVAL;    // gemma4_mtp_helpers.cpp:126-128
     if (logits) {
         if (dtype != LLIMA_F32 && dtype != LLIMA_BF16) return LLIMA_E_INVAL;
-        if (row_stride < V || !out_ids) return LLIMA_E_INVAL;
-    } else if (!out_candidates) {
+        if (row_stride < V || (B > 0 && !out_ids)) return LLIMA_E_INVAL;
+    } else if (!out_candidates && B > 0) {
         return LLIMA_E_INVAL;                             // nothing to compute
     }
     if (B == 0) return LLIMA_OK;

@@ -532,8 +532,8 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
                                       const float* u_accept, const float* u_resample,
                                       int32_t* accepted_len, int32_t* emitted, void* workspace,
                                       size_t workspace_bytes, void* stream) {
-    if (!target_logits || !u_resample || !accepted_len || !emitted) return LLIMA_E_INVAL;
-    if (D > 0 && (!draft_logits || !draft_ids || !u_accept)) return LLIMA_E_INVAL;
+    if (B > 0 && (!target_logits || !u_resample || !accepted_len || !emitted)) return LLIMA_E_INVAL;
+    if (B > 0 && D > 0 && (!draft_logits || !draft_ids || !u_accept)) return LLIMA_E_INVAL;
     if (B < 0 || D < 0 || D > VR_MAX_D || V <= 0 || V > (1 << 22)) return LLIMA_E_INVAL;
     if ((uintptr_t)target_logits % 16 || (D > 0 && (uintptr_t)draft_logits % 16) || V % 4)
         return LLIMA_E_INVAL;                  // rows are read with 16-byte loads

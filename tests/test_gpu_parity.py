@@ -488,6 +488,41 @@ def test_verify_rejection_help_path(gpu, oracle, monkeypatch, B, D, V):
     assert (_np(em) == eem).all()
 
 
+def test_empty_batches(gpu, oracle):
+    """B = 0 rows (an empty server step) is a no-op on every entry point, with
+    empty outputs; an empty row (V = 0) raises as the reference's argmax_bf16
+    does (utils.hpp:85-87)."""
+    import torch
+    import llima_amd
+    _say("empty batches")
+    V = 1000
+    x = torch.empty((0, V), dtype=torch.float32, device=gpu)
+    ids, vals = llima_amd.argmax(x)
+    assert ids.numel() == 0 and vals.numel() == 0
+    ids, probs = llima_amd.sample(x, torch.empty(0, device=gpu),
+                                  llima_amd.SamplerConfig(temperature=0.7, top_k=5),
+                                  history=torch.empty((0, 4), dtype=torch.int32, device=gpu))
+    assert ids.numel() == 0 and probs.numel() == 0
+    t = torch.empty((0, 3, V), dtype=torch.float32, device=gpu)
+    acc, em = llima_amd.verify_greedy(t, torch.empty((0, 2), dtype=torch.int32, device=gpu))
+    assert acc.numel() == 0 and tuple(em.shape) == (0, 3)
+    acc, em = llima_amd.verify_rejection(t, torch.empty((0, 2, V), device=gpu),
+                                         torch.empty((0, 2), dtype=torch.int32, device=gpu),
+                                         torch.empty((0, 2), device=gpu),
+                                         torch.empty(0, device=gpu))
+    assert acc.numel() == 0 and tuple(em.shape) == (0, 3)
+    lp, g = llima_amd.score_logits(x, torch.empty(0, dtype=torch.int32))
+    assert lp.numel() == 0 and g.numel() == 0
+    cent = torch.empty((0, 8), dtype=torch.bfloat16, device=gpu)
+    order = torch.arange(V, dtype=torch.int32, device=gpu)
+    ids = llima_amd.argmax_gemma4_mtp_masked_rows(cent, order, 2,
+                                                  torch.empty((0, V), dtype=torch.bfloat16,
+                                                              device=gpu))
+    assert ids.numel() == 0
+    with pytest.raises(ValueError):
+        llima_amd.argmax_bf16(torch.empty(0, dtype=torch.bfloat16, device=gpu))
+
+
 def test_workspace_garbage(gpu, oracle):
     """Every entry point gives the same results on a workspace that holds
     arbitrary bytes (all ones, then random): nothing in it is read before the
