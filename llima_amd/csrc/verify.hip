@@ -174,12 +174,13 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_clear(VerifyParams P) {
         P.maxk[i] = 0;
 }
 
-// Maximum key of chunk c of a row (every thread gets it), read in quarters.
+// Maximum key of chunk c of a row (every thread gets it), read one 16-byte
+// load per thread at a time.
 __device__ __forceinline__ uint32_t chunk_max_key(const float* rowp, int c, int V, BlockScratch& bs) {
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < V ? c0 + VR_CHUNK : V;
     float m = -__builtin_inff();
 #pragma unroll 1
-    for (int j = 0; j < VR_E / 4; ++j) {                // 4 registers: the waiter's own chunk stays live
+    for (int j = 0; j < VR_E / 4; ++j) {                // few registers: the waiter's own chunk stays live
         const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
         const int ia = i0 < V ? i0 : V - 4;
         const llima_u32x4 q = *(const llima_u32x4*)(rowp + ia);
