@@ -44,6 +44,10 @@
  *                            sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:113-167,
  *                            _argmax_gemma4_mtp_masked_row
  *                            sima_lmm/devkit/cpp/language_model_gemma4_mtp.cpp:31-97
+ *   llima_lm_head_argmax  <- the in-graph LM head + softcap + argmax
+ *                            sima_lmm/model/language_part_base.py:171-180,
+ *                            sima_lmm/model/model_graph.py:601, 868-870, whose
+ *                            int32 the host reads at language_model.cpp:1607-1609
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -202,6 +206,20 @@ int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_st
                             int32_t dtype, int32_t B, int32_t V, int64_t row_stride,
                             int32_t* out_ids, int32_t* out_status, uint32_t* out_candidates,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* LM head with a fused softcap and argmax, for decode-sized batches: for each
+ * of B hidden rows (bf16 [B][H], 16-byte aligned) and V vocab rows of the
+ * weight (bf16 [V][H], the nn.Linear layout, 16-byte aligned),
+ *   logit = softcap * tanh(s / softcap)  (s when softcap <= 0),
+ *   s = sum_h hidden[b][h] * weight[v][h]  in fp32;
+ * out_ids[B] = first index of the maximum logit (NaN never wins; a row with
+ * no non-NaN logit gives 0), out_vals[B] (nullable) its value, out_logits
+ * (nullable, fp32 [B][V]) every logit.  H <= 4096 and H % 8 == 0.  The
+ * weights are read once per 8 hidden rows (H <= 2048) or 4 (H <= 4096). */
+size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V);
+int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
+                         float softcap, int32_t* out_ids, float* out_vals, float* out_logits,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 const char* llima_status_string(int status);
 int llima_abi_version(void);

@@ -40,6 +40,9 @@ SIGNATURES = {
     "llima_mtp_masked_argmax_workspace_bytes": (_sz, [_i32]),
     "llima_mtp_masked_argmax": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _i32, _i32, _i32,
                                                _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "llima_lm_head_argmax_workspace_bytes": (_sz, [_i32, _i32]),
+    "llima_lm_head_argmax": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _vp, _vp,
+                                            _vp, _vp, _sz, _vp]),
     "llima_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "llima_abi_version": (ctypes.c_int, []),
 }

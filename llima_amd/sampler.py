@@ -431,3 +431,31 @@ def argmax_gemma4_mtp_masked_row(centroid_logits: torch.Tensor, token_ordering, 
     """One row of argmax_gemma4_mtp_masked_rows: centroid_logits [C], logits [V]."""
     return int(argmax_gemma4_mtp_masked_rows(centroid_logits.reshape(1, -1), token_ordering,
                                              top_k, logits.reshape(1, -1))[0])
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 0.0,
+                   return_logits: bool = False):
+    """LM head + softcap + argmax, as the reference's graph computes them before
+    the host reads one int32 (language_part_base.py:171-180,
+    language_model.cpp:1607-1609): hidden bf16 [B, H] (or [H]), weight bf16
+    [V, H] -> (ids int32 [B], values float32 [B]) and, if return_logits, the
+    fp32 logits [B, V]."""
+    x = hidden.reshape(1, -1) if hidden.dim() == 1 else hidden
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("lm_head_argmax takes bf16 hidden states and weights")
+    x = x.contiguous()
+    w = weight.contiguous()
+    B, H = x.shape
+    if w.dim() != 2 or w.shape[1] != H:
+        raise ValueError("weight must be [V, H]")
+    V = w.shape[0]
+    dev = w.device
+    _on_gpu(x, w)
+    ids = torch.empty(B, dtype=torch.int32, device=dev)
+    vals = torch.empty(B, dtype=torch.float32, device=dev)
+    logits = torch.empty((B, V), dtype=torch.float32, device=dev) if return_logits else None
+    ws = Workspace.get(dev, "lm_head", lib().llima_lm_head_argmax_workspace_bytes(B, V))
+    check(lib().llima_lm_head_argmax(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap),
+                                     ids.data_ptr(), vals.data_ptr(), _ptr(logits), ws.data_ptr(),
+                                     ws.numel(), _stream(dev)), "llima_lm_head_argmax")
+    return (ids, vals, logits) if return_logits else (ids, vals)

@@ -827,3 +827,67 @@ def test_score_and_mtp_maximum_sizes(gpu, oracle):
     ids = llima_amd.argmax_gemma4_mtp_masked_rows(_t(cent, gpu), _t(ordering, gpu), k, _t(xm, gpu))
     ec, eid = _mtp_expected(oracle, cent[0], ordering, k, xm[0])
     assert int(_np(ids)[0]) == eid
+
+
+# ----------------------------------------------------------------- LM head
+# Tolerance: each logit is a sum of H fp32 products of bf16 values, in an
+# order the float64 reference does not follow: |logit - ref| <= 1e-5 *
+# sum_h |x_h w_h| + 1e-6, plus 4e-6 |ref| for the softcap's tanhf (x -> cap
+# tanh(x / cap) is 1-Lipschitz).  The argmax is exact with respect to the
+# kernel's own logits: the first index of their maximum, NaN never wins.
+def _lm_head_check(ids, vals, logits, x, w, cap):
+    xf = wl.bf16_bits_to_f32(x).astype(np.float64)
+    wf = wl.bf16_bits_to_f32(w).astype(np.float64)
+    s = xf @ wf.T
+    ref = cap * np.tanh(s / cap) if cap > 0 else s
+    bound = 1e-5 * (np.abs(xf) @ np.abs(wf).T) + 1e-6 + 4e-6 * np.abs(ref)
+    fin = np.isfinite(ref)
+    assert (np.abs(logits - ref)[fin] <= bound[fin]).all(), np.abs(logits - ref)[fin].max()
+    for b in range(x.shape[0]):
+        row = logits[b]
+        ok = ~np.isnan(row)
+        if not ok.any():
+            assert ids[b] == 0 and np.isnan(vals[b])
+            continue
+        m = row[ok].max()
+        assert ids[b] == int(np.flatnonzero(ok & (row == m))[0]), b
+        assert vals[b] == m
+
+
+@pytest.mark.parametrize("B,H,V,cap", [(1, 4096, 128256, 0.0), (3, 1536, 262144, 30.0),
+                                       (8, 2048, 50000, 0.0), (11, 512, 1000, 30.0),
+                                       (5, 8, 7, 0.0), (4, 4096, 3001, 0.0)])
+def test_lm_head_argmax_parity(gpu, B, H, V, cap):
+    import llima_amd
+    _say("lm head", B, H, V, cap)
+    rng = np.random.default_rng(B * 31 + H + V)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 1.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    ids, vals, logits = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap,
+                                                 return_logits=True)
+    _lm_head_check(_np(ids), _np(vals), _np(logits), x, w, cap)
+    ids2, vals2 = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap)
+    assert (_np(ids2) == _np(ids)).all() and (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
+
+
+def test_lm_head_argmax_ties_and_nan(gpu):
+    """Equal vocab rows tie: the lower index wins; a NaN logit never wins; a
+    row whose logits are all NaN gives id 0 and a NaN value."""
+    import llima_amd
+    _say("lm head ties / nan")
+    rng = np.random.default_rng(5)
+    B, H, V = 3, 256, 5000
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    wf = rng.normal(0, 0.05, (V, H)).astype(np.float32)
+    wf[4000] = wl.bf16_bits_to_f32(x[0]) * 0.5               # the maximum of row 0 ...
+    wf[1234] = wf[4000]                                      # ... tied at a lower index
+    wf[17, 3] = np.nan                                       # a NaN logit in every row
+    w = wl.f32_to_bf16_bits(wf)
+    xn = x.copy()
+    xn[2] = wl.f32_to_bf16_bits(np.full(H, np.nan, np.float32))   # row 2: all NaN
+    ids, vals, logits = llima_amd.lm_head_argmax(_t(xn, gpu), _t(w, gpu), return_logits=True)
+    ids, vals, logits = _np(ids), _np(vals), _np(logits)
+    assert ids[0] == 1234
+    assert np.isnan(logits[1, 17]) and ids[1] != 17
+    assert ids[2] == 0 and np.isnan(vals[2])
+    _lm_head_check(ids[:2], vals[:2], logits[:2], x[:2], w, 0.0)
