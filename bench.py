@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--workload", default="batched_penalties",
                     choices=["batched_penalties", "single_row", "constrained",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
-                             "speculative", "score_bf16", "mtp_masked_argmax"])
+                             "speculative", "score_bf16", "mtp_masked_argmax",
+                             "lm_head_argmax"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -77,7 +78,32 @@ def main():
     t0 = time.time()
 
     launches = []          # one callable per rotated input, taking a stream pointer
-    if name == "speculative":
+    data_note = None
+    if name == "lm_head_argmax":
+        B, H, V = w["B"], w["H"], w["V"]
+        g = torch.Generator(device=dev)
+        g.manual_seed(w["seed"])
+        weight = (torch.randn((V, H), generator=g, device=dev) * (1.0 / H ** 0.5)).to(torch.bfloat16)
+        hid = [torch.from_numpy(w["hidden"].view(np.int16)).to(dev).view(torch.bfloat16)]
+        hid += [torch.randn((B, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(7)]
+        ids_o = torch.empty(B, dtype=torch.int32, device=dev)
+        vals_o = torch.empty(B, dtype=torch.float32, device=dev)
+        nws = L.llima_lm_head_argmax_workspace_bytes(B, V)
+        ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+        for x in hid:
+            launches.append(lambda sp, x=x: check(L.llima_lm_head_argmax(
+                x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, ids_o.data_ptr(),
+                vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
+        per = weight.numel() * 2
+        alg_bytes = V * H * 2 + B * H * 2 + B * 8
+        rows = B
+        unit_rows = "rows/s"
+        dtype = "bf16"
+        kernel_names = ["lmh_rows", "lmh_finish"]
+        config = {"workload": name, "B": B, "H": H, "V": V, "weight": "bf16 [V, H]"}
+        data_note = ("synthetic (seeded; one bf16 [%d, %d] weight, %.2f GiB, above the 256 MB "
+                     "Infinity Cache; 8 rotating hidden rows)" % (V, H, per / 2**30))
+    elif name == "speculative":
         B, D, V = w["target"].shape[0], w["target"].shape[1] - 1, w["target"].shape[2]
         per = w["target"].nbytes + w["draft"].nbytes
         nbuf = max(2, int(np.ceil(args.rotate_gib * 2**30 / per)))
@@ -297,7 +323,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
-        "data": "synthetic (seeded; inputs rotate over %d device buffers, %.2f GiB)" % (
+        "data": data_note or "synthetic (seeded; inputs rotate over %d device buffers, %.2f GiB)" % (
             len(launches), len(launches) * per / 2**30),
         "config": config,
         "timing": "graph replay" if graph is not None else "eager launches",
@@ -330,6 +356,24 @@ def cpu_baseline(name, w, seconds, greedy_variant):
     t_end = time.time() + seconds
     n_rows, reps = 0, 0
     t0 = time.time()
+    if name == "lm_head_argmax":
+        # numpy float32 matrix-vector products + argmax over a 16384-row slice
+        # of a weight of the same shape, scaled to the full vocabulary
+        rng = np.random.default_rng(w["seed"])
+        nv = 16384
+        wt = (rng.standard_normal((nv, w["H"]), dtype=np.float32) * np.float32(w["H"] ** -0.5))
+        xs = np.ascontiguousarray(w["hidden"].astype(np.uint32) << 16).view(np.float32)
+        t0 = time.time()
+        while time.time() < t_end or reps == 0:
+            np.argmax(xs @ wt.T, axis=1)
+            reps += 1
+        dt = time.time() - t0
+        full = dt * (w["V"] / nv) / reps                     # seconds per full-vocabulary call
+        return {"value": w["B"] / full, "unit": "rows/s", "cores": threads, "kind": "port",
+                "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + argmax (a %d-row slice of "
+                          "the vocabulary, scaled by V / %d), %.1f s" % (
+                              reps, w["B"], w["H"], nv, w["H"], nv, nv, dt),
+                "cpu": _cpu_model()}
     if name == "speculative":
         while time.time() < t_end or reps == 0:
             orc.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],

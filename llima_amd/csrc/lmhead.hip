@@ -19,7 +19,7 @@
 // the current row is summed), sums each hidden row's products in fp32 (per
 // lane in h order, then across the wave), applies the softcap, optionally
 // writes the logits, and keeps per hidden row the 64-bit key
-// (value key << 32 | ~v) of its best vocab row.  lmh_finish: one wavefront per
+// (value key << 32 | ~v) of its best vocab row.  lmh_finish: one workgroup per
 // hidden row reduces the waves' keys.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
@@ -135,16 +135,29 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
     }
 }
 
-// One wavefront per hidden row: the greatest key over the waves.  A row with
-// no non-NaN logit gives id 0 and a NaN value.
+// One workgroup per hidden row: the greatest key over the waves (16 loads per
+// thread in flight at a time).  A row with no non-NaN logit gives id 0 and a
+// NaN value.
 __global__ __launch_bounds__(LLIMA_WG) void lmh_finish(LmhParams P) {
-    const int b = (int)blockIdx.x * LLIMA_WAVES + (int)(threadIdx.x >> 6);
-    if (b >= P.B) return;
+    __shared__ BlockScratch bs;
+    const int b = (int)blockIdx.x;
     const uint64_t* k = P.keys + (size_t)b * P.NW;
     uint64_t best = 0;
-    for (int i = (int)lane_id(); i < P.NW; i += 64) best = k[i] > best ? k[i] : best;
-    best = wave_max_u64(best);
-    if (lane_id() == 0) {
+    for (int i0 = 0; i0 < P.NW; i0 += LLIMA_WG * 16) {
+        uint64_t kv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = i0 + j * LLIMA_WG + (int)threadIdx.x;
+            kv[j] = k[i < P.NW ? i : 0];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool in = i0 + j * LLIMA_WG + (int)threadIdx.x < P.NW;
+            best = in && kv[j] > best ? kv[j] : best;
+        }
+    }
+    best = block_max_u64(best, bs);
+    if (threadIdx.x == 0) {
         P.out_ids[b] = best ? (int32_t)~(uint32_t)best : 0;
         if (P.out_vals) P.out_vals[b] = best ? key_f32((uint32_t)(best >> 32)) : __builtin_nanf("");
     }
@@ -209,7 +222,6 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
             default: hipLaunchKernelGGL(lmh_rows<1>, g, blk, 0, st, P, b0, nb); break;
         }
     }
-    hipLaunchKernelGGL(lmh_finish, dim3(((uint32_t)B + LLIMA_WAVES - 1) / LLIMA_WAVES),
-                       dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }

@@ -158,6 +158,16 @@ def mtp_masked_argmax(B=16, C=2048, V=262144, top_k=32, seed=1007):
                 ordering=ordering, top_k=top_k)
 
 
+def lm_head_argmax(B=1, H=4096, V=128256, seed=1008):
+    """LM head + argmax at decode: B bf16 hidden rows of width H = 4096 against a
+    bf16 [V, H] weight with V = 128256 (a Llama-3-8B head, 1.05 GB).  The weight,
+    N(0, 1/H), is generated on the device from the seed (torch), the hidden rows
+    ~ N(0, 1) here."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    hidden = f32_to_bf16_bits(_normal(rng, (B, H), 1.0))
+    return dict(name="lm_head_argmax", hidden=hidden, B=B, H=H, V=V, seed=seed)
+
+
 WORKLOADS = {
     "single_row": single_row,
     "batched_penalties": batched_penalties,
@@ -166,4 +176,5 @@ WORKLOADS = {
     "large_vocab_bf16": large_vocab_bf16,
     "score_bf16": score_bf16,
     "mtp_masked_argmax": mtp_masked_argmax,
+    "lm_head_argmax": lm_head_argmax,
 }
