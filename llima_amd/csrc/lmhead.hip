@@ -135,6 +135,130 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
     }
 }
 
+// ------------------------------------------------------------------ MFMA path
+// Batches of 16 rows and more: v_mfma_f32_32x32x8_bf16 tiles, the weight read
+// once per 64 hidden rows.  A wave owns 128 vocab rows (4 tiles of 32) and the
+// pass's 64 hidden rows (2 tiles of 32): 8 accumulators of 32x32 fp32.
+// Operand layout of the instruction: lane l supplies row (A) or column (B)
+// l % 32 and 4 values of k; accumulator element i of lane l is C[i % 4 +
+// 8 (i / 4) + 4 (l / 32)][l % 32].  Step s takes ids k = 32 s .. 32 s + 31: lane
+// half g reads 8 + 8 of them with two 16-byte loads, [32 s + 8 g, + 8) and
+// [32 s + 16 + 8 g, + 8), and feeds them to 4 MFMAs, 4 ids each.  Every id of the
+// step is used exactly once, with the same assignment for both operands, so the
+// sum over k is complete; its order is not the GEMV path's.
+typedef short lmh_s4 __attribute__((ext_vector_type(4)));
+typedef float lmh_acc __attribute__((ext_vector_type(16)));
+#define LMH_NT 4                       // 32-column vocab tiles per wave
+#define LMH_MB 64                      // hidden rows per pass
+
+__device__ __forceinline__ lmh_s4 lmh_half(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(lmh_s4, (uint64_t)a | ((uint64_t)b << 32));
+}
+
+__device__ __forceinline__ uint64_t lmh_key(float s, int n, int V) {
+    return s == s && n < V ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)n : 0ull;
+}
+
+// Greatest 64-bit value over the 32 lanes of this lane's half-wave.
+__device__ __forceinline__ uint64_t half_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(LLIMA_WG) void lmh_mfma(LmhParams P, int b0, int nb) {
+    const int lane = (int)lane_id(), g = lane >> 5, r = lane & 31;
+    const int wv = (int)blockIdx.x * LLIMA_WAVES + (int)(threadIdx.x >> 6);
+    const int n0 = wv * (32 * LMH_NT);
+    const int H = P.H, V = P.V;
+    const uint16_t* xa[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = mt * 32 + r;                          // rows past nb read row b0
+        xa[mt] = P.hidden + (size_t)(b0 + (m < nb ? m : 0)) * H + 8 * g;
+    }
+    const uint16_t* wb[LMH_NT];
+#pragma unroll
+    for (int nt = 0; nt < LMH_NT; ++nt) {
+        const int n = n0 + nt * 32 + r;                     // rows past V read row V - 1
+        wb[nt] = P.weight + (size_t)(n < V ? n : V - 1) * H + 8 * g;
+    }
+    lmh_acc acc[2][LMH_NT];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < LMH_NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.0f;
+    llima_u32x4 qa[2][2], qb[LMH_NT][2], na[2][2], nq[LMH_NT][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) qa[mt][u] = *(const llima_u32x4*)(xa[mt] + 16 * u);
+#pragma unroll
+        for (int nt = 0; nt < LMH_NT; ++nt)
+            qb[nt][u] = __builtin_nontemporal_load((const llima_u32x4*)(wb[nt] + 16 * u));
+    }
+    for (int k0 = 0; k0 < H; k0 += 32) {
+        const int k1 = k0 + 32 < H ? k0 + 32 : k0;          // the last step requests itself again
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) na[mt][u] = *(const llima_u32x4*)(xa[mt] + k1 + 16 * u);
+#pragma unroll
+            for (int nt = 0; nt < LMH_NT; ++nt)
+                nq[nt][u] = __builtin_nontemporal_load((const llima_u32x4*)(wb[nt] + k1 + 16 * u));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const lmh_s4 a = h ? lmh_half(qa[mt][u].z, qa[mt][u].w) : lmh_half(qa[mt][u].x, qa[mt][u].y);
+#pragma unroll
+                    for (int nt = 0; nt < LMH_NT; ++nt) {
+                        const lmh_s4 b = h ? lmh_half(qb[nt][u].z, qb[nt][u].w) : lmh_half(qb[nt][u].x, qb[nt][u].y);
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, acc[mt][nt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) qa[mt][u] = na[mt][u];
+#pragma unroll
+            for (int nt = 0; nt < LMH_NT; ++nt) qb[nt][u] = nq[nt][u];
+        }
+    }
+    // epilogue: softcap, logits, and per hidden row the greatest key of the 128 columns
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
+            uint64_t best = 0;
+#pragma unroll
+            for (int nt = 0; nt < LMH_NT; ++nt) {
+                const int n = n0 + nt * 32 + r;
+                float v = acc[mt][nt][i];
+                if (P.cap > 0.0f) v = P.cap * tanhf(v / P.cap);
+                if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
+                const uint64_t k = lmh_key(v, n, V);
+                best = k > best ? k : best;
+            }
+            best = half_max_u64(best);
+            if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
+        }
+    }
+}
+
 // One workgroup per hidden row: the greatest key over the waves (16 loads per
 // thread in flight at a time).  A row with no non-NaN logit gives id 0 and a
 // NaN value.
@@ -184,9 +308,16 @@ static int lmh_rows_per_pass(int H) {
 
 using namespace llima;
 
+// Waves of the MFMA kernel: one per 128 vocab rows, whole workgroups.
+static int lmh_mfma_waves(int V) {
+    const int w = (V + 32 * LMH_NT - 1) / (32 * LMH_NT);
+    return (w + LLIMA_WAVES - 1) / LLIMA_WAVES * LLIMA_WAVES;
+}
+
 extern "C" size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V) {
     if (B <= 0 || V <= 0) return 0;
-    return lmh_align256((size_t)B * lmh_waves(V) * sizeof(uint64_t));
+    const int nw = lmh_waves(V) > lmh_mfma_waves(V) ? lmh_waves(V) : lmh_mfma_waves(V);
+    return lmh_align256((size_t)B * nw * sizeof(uint64_t));
 }
 
 extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H,
@@ -211,6 +342,16 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.NW = lmh_waves(V);
     P.cap = softcap;
     hipStream_t st = (hipStream_t)stream;
+    if (B >= 16 && H % 32 == 0) {                      // wide batch: MFMA tiles
+        P.NW = lmh_mfma_waves(V);
+        const dim3 gm((uint32_t)(P.NW / LLIMA_WAVES)), bm(LLIMA_WG);
+        for (int b0 = 0; b0 < B; b0 += LMH_MB) {
+            const int nb = B - b0 < LMH_MB ? B - b0 : LMH_MB;
+            hipLaunchKernelGGL(lmh_mfma, gm, bm, 0, st, P, b0, nb);
+        }
+        hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+        return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+    }
     const int nbp = lmh_rows_per_pass(H);
     const dim3 g((uint32_t)((P.NW + LMH_WAVES - 1) / LMH_WAVES)), blk(LMH_WG);
     for (int b0 = 0; b0 < B; b0 += nbp) {
