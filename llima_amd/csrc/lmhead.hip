@@ -11,7 +11,8 @@
 // 868-870); the host reads back one int32 (sima_lmm/devkit/cpp/language_model.cpp:1607-1609).
 //
 // At decode batch sizes the product is bound by reading the weights (V H 2
-// bytes, read once per pass); an MFMA tiling pays off only for wide batches.
+// bytes, read once per pass of up to 8 hidden rows); batches of 16 rows and
+// more take the MFMA tiling further down (one pass per 64 rows).
 //
 // lmh_rows: 512-thread workgroups; the pass's hidden rows (NB of them) are
 // staged in LDS as fp32; each wave streams whole vocab rows (lane l holds ids
