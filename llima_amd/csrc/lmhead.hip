@@ -138,23 +138,15 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
 
 // ------------------------------------------------------------------ MFMA path
 // Batches of 16 rows and more: v_mfma_f32_32x32x8_bf16 tiles, the weight read
-// once per 64 hidden rows.  A wave owns 128 vocab rows (4 tiles of 32) and the
-// pass's 64 hidden rows (2 tiles of 32): 8 accumulators of 32x32 fp32.
-// Operand layout of the instruction: lane l supplies row (A) or column (B)
-// l % 32 and 4 values of k; accumulator element i of lane l is C[i % 4 +
-// 8 (i / 4) + 4 (l / 32)][l % 32].  Step s takes ids k = 32 s .. 32 s + 31: lane
-// half g reads 8 + 8 of them with two 16-byte loads, [32 s + 8 g, + 8) and
-// [32 s + 16 + 8 g, + 8), and feeds them to 4 MFMAs, 4 ids each.  Every id of the
-// step is used exactly once, with the same assignment for both operands, so the
-// sum over k is complete; its order is not the GEMV path's.
+// once per 64 hidden rows.  Operand layout of the instruction (checked on the
+// GPU): lane l supplies row (A) or column (B) l % 32 and 4 values of k;
+// accumulator element i of lane l is C[i % 4 + 8 (i / 4) + 4 (l / 32)][l % 32].
+// Step j of a 64-id chunk gives lane half g the ids 8 j + 4 g .. 8 j + 4 g + 3,
+// the same for both operands, so every id of the chunk is used once; the order
+// of the fp32 sum over k is not the GEMV path's.
 typedef short lmh_s4 __attribute__((ext_vector_type(4)));
 typedef float lmh_acc __attribute__((ext_vector_type(16)));
-#define LMH_NT 4                       // 32-column vocab tiles per wave
 #define LMH_MB 64                      // hidden rows per pass
-
-__device__ __forceinline__ lmh_s4 lmh_half(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(lmh_s4, (uint64_t)a | ((uint64_t)b << 32));
-}
 
 __device__ __forceinline__ uint64_t lmh_key(float s, int n, int V) {
     return s == s && n < V ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)n : 0ull;
@@ -172,89 +164,94 @@ __device__ __forceinline__ uint64_t half_max_u64(uint64_t v) {
     return v;
 }
 
+// Workgroup tile: 128 vocab rows (one 32-row tile per wave) x the pass's 64
+// hidden rows; k in chunks of 64 ids (128 bytes of a row), each chunk read with
+// coalesced 16-byte loads (8 threads per row: whole 128-byte lines) into LDS
+// rows padded to LMH_LDSR bytes, double-buffered with one barrier per chunk;
+// the next chunk's loads are in flight while the current one feeds the MFMAs.
+#define LMH_KC 64
+#define LMH_LDSR 136                   // bytes per staged row: 128 + 8 (2-way banks at most)
+#define LMH_WR 128                     // vocab rows per workgroup
+
 __global__ __launch_bounds__(LLIMA_WG) void lmh_mfma(LmhParams P, int b0, int nb) {
-    const int lane = (int)lane_id(), g = lane >> 5, r = lane & 31;
-    const int wv = (int)blockIdx.x * LLIMA_WAVES + (int)(threadIdx.x >> 6);
-    const int n0 = wv * (32 * LMH_NT);
-    const int H = P.H, V = P.V;
-    const uint16_t* xa[2];
+    __shared__ __align__(16) uint8_t lw[2][LMH_WR * LMH_LDSR];
+    __shared__ __align__(16) uint8_t lx[2][LMH_MB * LMH_LDSR];
+    const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r = lane & 31;
+    const int n0 = (int)blockIdx.x * LMH_WR;
+    const int H = P.H, V = P.V, nch = H / LMH_KC;
+    // global -> LDS mapping: thread t, row (t >> 3) + 32 q, 16-byte piece t & 7
+    const int pr = t >> 3, pc = t & 7;
+    const uint16_t* gw[4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = mt * 32 + r;                          // rows past nb read row b0
-        xa[mt] = P.hidden + (size_t)(b0 + (m < nb ? m : 0)) * H + 8 * g;
+    for (int q = 0; q < 4; ++q) {
+        const int n = n0 + pr + 32 * q;                      // rows past V read row V - 1
+        gw[q] = P.weight + (size_t)(n < V ? n : V - 1) * H + pc * 8;
     }
-    const uint16_t* wb[LMH_NT];
+    const uint16_t* gx[2];
 #pragma unroll
-    for (int nt = 0; nt < LMH_NT; ++nt) {
-        const int n = n0 + nt * 32 + r;                     // rows past V read row V - 1
-        wb[nt] = P.weight + (size_t)(n < V ? n : V - 1) * H + 8 * g;
+    for (int q = 0; q < 2; ++q) {
+        const int m = pr + 32 * q;                           // rows past nb read row b0
+        gx[q] = P.hidden + (size_t)(b0 + (m < nb ? m : 0)) * H + pc * 8;
     }
-    lmh_acc acc[2][LMH_NT];
+    llima_u32x4 rw[4], rx[2];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rw[q] = __builtin_nontemporal_load((const llima_u32x4*)(gw[q] + c * LMH_KC));
+#pragma unroll
+        for (int q = 0; q < 2; ++q) rx[q] = *(const llima_u32x4*)(gx[q] + c * LMH_KC);
+    };
+    auto stage = [&](int buf) {                              // 8-byte LDS writes (rows are 8-aligned)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint64_t* d = (uint64_t*)(lw[buf] + (pr + 32 * q) * LMH_LDSR + pc * 16);
+            d[0] = (uint64_t)rw[q].x | ((uint64_t)rw[q].y << 32);
+            d[1] = (uint64_t)rw[q].z | ((uint64_t)rw[q].w << 32);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            uint64_t* d = (uint64_t*)(lx[buf] + (pr + 32 * q) * LMH_LDSR + pc * 16);
+            d[0] = (uint64_t)rx[q].x | ((uint64_t)rx[q].y << 32);
+            d[1] = (uint64_t)rx[q].z | ((uint64_t)rx[q].w << 32);
+        }
+    };
+    lmh_acc acc[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < LMH_NT; ++nt)
+        for (int i = 0; i < 16; ++i) acc[mt][i] = 0.0f;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < nch) fetch(c + 1);
+        // 8 MFMA steps of 8 ids: lane half g supplies ids 8 j + 4 g .. + 3 of the chunk
+        const uint8_t* wrow = lw[buf] + (wave * 32 + r) * LMH_LDSR + 8 * g;
+        const uint8_t* x0 = lx[buf] + r * LMH_LDSR + 8 * g;
+        const uint8_t* x1 = lx[buf] + (32 + r) * LMH_LDSR + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.0f;
-    llima_u32x4 qa[2][2], qb[LMH_NT][2], na[2][2], nq[LMH_NT][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) qa[mt][u] = *(const llima_u32x4*)(xa[mt] + 16 * u);
-#pragma unroll
-        for (int nt = 0; nt < LMH_NT; ++nt)
-            qb[nt][u] = __builtin_nontemporal_load((const llima_u32x4*)(wb[nt] + 16 * u));
+        for (int j = 0; j < 8; ++j) {
+            const lmh_s4 bo = *(const lmh_s4*)(wrow + 16 * j);
+            const lmh_s4 a0 = *(const lmh_s4*)(x0 + 16 * j);
+            const lmh_s4 a1 = *(const lmh_s4*)(x1 + 16 * j);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a0, bo, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a1, bo, acc[1], 0, 0, 0);
+        }
+        if (c + 1 < nch) stage(buf ^ 1);                    // its last readers passed the previous barrier
+        __syncthreads();
     }
-    for (int k0 = 0; k0 < H; k0 += 32) {
-        const int k1 = k0 + 32 < H ? k0 + 32 : k0;          // the last step requests itself again
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) na[mt][u] = *(const llima_u32x4*)(xa[mt] + k1 + 16 * u);
-#pragma unroll
-            for (int nt = 0; nt < LMH_NT; ++nt)
-                nq[nt][u] = __builtin_nontemporal_load((const llima_u32x4*)(wb[nt] + k1 + 16 * u));
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    const lmh_s4 a = h ? lmh_half(qa[mt][u].z, qa[mt][u].w) : lmh_half(qa[mt][u].x, qa[mt][u].y);
-#pragma unroll
-                    for (int nt = 0; nt < LMH_NT; ++nt) {
-                        const lmh_s4 b = h ? lmh_half(qb[nt][u].z, qb[nt][u].w) : lmh_half(qb[nt][u].x, qb[nt][u].y);
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, acc[mt][nt], 0, 0, 0);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) qa[mt][u] = na[mt][u];
-#pragma unroll
-            for (int nt = 0; nt < LMH_NT; ++nt) qb[nt][u] = nq[nt][u];
-        }
-    }
-    // epilogue: softcap, logits, and per hidden row the greatest key of the 128 columns
+    // epilogue: softcap, logits, and per hidden row the greatest key of the wave's 32 columns
+    const int wv = (int)blockIdx.x * LLIMA_WAVES + wave;
+    const int n = n0 + wave * 32 + r;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-            uint64_t best = 0;
-#pragma unroll
-            for (int nt = 0; nt < LMH_NT; ++nt) {
-                const int n = n0 + nt * 32 + r;
-                float v = acc[mt][nt][i];
-                if (P.cap > 0.0f) v = P.cap * tanhf(v / P.cap);
-                if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
-                const uint64_t k = lmh_key(v, n, V);
-                best = k > best ? k : best;
-            }
-            best = half_max_u64(best);
+            float v = acc[mt][i];
+            if (P.cap > 0.0f) v = P.cap * tanhf(v / P.cap);
+            if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
+            const uint64_t best = half_max_u64(lmh_key(v, n, V));
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
         }
     }
@@ -309,10 +306,9 @@ static int lmh_rows_per_pass(int H) {
 
 using namespace llima;
 
-// Waves of the MFMA kernel: one per 128 vocab rows, whole workgroups.
+// Waves of the MFMA kernel: one per 32 vocab rows, whole workgroups.
 static int lmh_mfma_waves(int V) {
-    const int w = (V + 32 * LMH_NT - 1) / (32 * LMH_NT);
-    return (w + LLIMA_WAVES - 1) / LLIMA_WAVES * LLIMA_WAVES;
+    return (V + LMH_WR - 1) / LMH_WR * LLIMA_WAVES;
 }
 
 extern "C" size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V) {
@@ -343,7 +339,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.NW = lmh_waves(V);
     P.cap = softcap;
     hipStream_t st = (hipStream_t)stream;
-    if (B >= 16 && H % 32 == 0) {                      // wide batch: MFMA tiles
+    if (B >= 16 && H % LMH_KC == 0) {                  // wide batch: MFMA tiles
         P.NW = lmh_mfma_waves(V);
         const dim3 gm((uint32_t)(P.NW / LLIMA_WAVES)), bm(LLIMA_WG);
         for (int b0 = 0; b0 < B; b0 += LMH_MB) {
