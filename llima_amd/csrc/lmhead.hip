@@ -11,8 +11,9 @@
 // 868-870); the host reads back one int32 (sima_lmm/devkit/cpp/language_model.cpp:1607-1609).
 //
 // At decode batch sizes the product is bound by reading the weights (V H 2
-// bytes, read once per pass of up to 8 hidden rows); batches of 16 rows and
-// more take the MFMA tiling further down (one pass per 64 rows).
+// bytes, read once per pass of up to 8 hidden rows); batches that would need
+// more than one such pass take the MFMA tiling further down (one pass per 64
+// rows).
 //
 // lmh_rows: 512-thread workgroups; the pass's hidden rows (NB of them) are
 // staged in LDS as fp32; each wave streams whole vocab rows (lane l holds ids
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
 }
 
 // ------------------------------------------------------------------ MFMA path
-// Batches of 16 rows and more: v_mfma_f32_32x32x8_bf16 tiles, the weight read
+// Batches wider than one GEMV pass: v_mfma_f32_32x32x8_bf16 tiles, the weight read
 // once per 64 hidden rows.  Operand layout of the instruction (checked on the
 // GPU): lane l supplies row (A) or column (B) l % 32 and 4 values of k;
 // accumulator element i of lane l is C[i % 4 + 8 (i / 4) + 4 (l / 32)][l % 32].
@@ -339,7 +340,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.NW = lmh_waves(V);
     P.cap = softcap;
     hipStream_t st = (hipStream_t)stream;
-    if (B >= 16 && H % LMH_KC == 0) {                  // wide batch: MFMA tiles
+    if (B > lmh_rows_per_pass(H) && H % LMH_KC == 0) {   // more than one GEMV pass: MFMA tiles
         P.NW = lmh_mfma_waves(V);
         const dim3 gm((uint32_t)(P.NW / LLIMA_WAVES)), bm(LLIMA_WG);
         for (int b0 = 0; b0 < B; b0 += LMH_MB) {
