@@ -43,7 +43,7 @@ def parse():
                     choices=["batched_penalties", "single_row", "constrained",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
-                             "lm_head_argmax"])
+                             "lm_head_argmax", "lm_head_argmax_b64"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -79,7 +79,7 @@ def main():
 
     launches = []          # one callable per rotated input, taking a stream pointer
     data_note = None
-    if name == "lm_head_argmax":
+    if name.startswith("lm_head_argmax"):
         B, H, V = w["B"], w["H"], w["V"]
         g = torch.Generator(device=dev)
         g.manual_seed(w["seed"])
@@ -99,7 +99,7 @@ def main():
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16"
-        kernel_names = ["lmh_rows", "lmh_finish"]
+        kernel_names = ["lmh_mfma" if B > 4 else "lmh_rows", "lmh_finish"]
         config = {"workload": name, "B": B, "H": H, "V": V, "weight": "bf16 [V, H]"}
         data_note = ("synthetic (seeded; one bf16 [%d, %d] weight, %.2f GiB, above the 256 MB "
                      "Infinity Cache; 8 rotating hidden rows)" % (V, H, per / 2**30))
@@ -356,7 +356,7 @@ def cpu_baseline(name, w, seconds, greedy_variant):
     t_end = time.time() + seconds
     n_rows, reps = 0, 0
     t0 = time.time()
-    if name == "lm_head_argmax":
+    if name.startswith("lm_head_argmax"):
         # numpy float32 matrix-vector products + argmax over a 16384-row slice
         # of a weight of the same shape, scaled to the full vocabulary
         rng = np.random.default_rng(w["seed"])

@@ -177,4 +177,5 @@ WORKLOADS = {
     "score_bf16": score_bf16,
     "mtp_masked_argmax": mtp_masked_argmax,
     "lm_head_argmax": lm_head_argmax,
+    "lm_head_argmax_b64": lambda: dict(lm_head_argmax(B=64), name="lm_head_argmax_b64"),
 }
