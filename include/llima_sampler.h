@@ -214,10 +214,10 @@ int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_st
  *   s = sum_h hidden[b][h] * weight[v][h]  in fp32;
  * out_ids[B] = first index of the maximum logit (NaN never wins; a row with
  * no non-NaN logit gives 0), out_vals[B] (nullable) its value, out_logits
- * (nullable, fp32 [B][V]) every logit.  H <= 4096 and H % 8 == 0.  The
- * weights are read once per 8 hidden rows (H <= 2048) or 4 (H <= 4096);
- * wider batches with H % 64 == 0 use MFMA tiles that read them once per 64
- * rows. */
+ * (nullable, fp32 [B][V]) every logit.  H % 8 == 0, and H <= 4096 unless
+ * H % 64 == 0 (then H <= 65536).  The weights are read once per 8 hidden rows
+ * (H <= 2048) or 4 (H <= 4096); wider batches, and rows wider than 4096, use
+ * MFMA tiles that read them once per 64 rows (H % 64 == 0). */
 size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V);
 int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
                          float softcap, int32_t* out_ids, float* out_vals, float* out_logits,

@@ -322,7 +322,8 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
                                     int32_t V, float softcap, int32_t* out_ids, float* out_vals,
                                     float* out_logits, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-    if (B < 0 || H <= 0 || V <= 0 || H > LMH_MAX_H || H % 8 != 0) return LLIMA_E_INVAL;
+    if (B < 0 || H <= 0 || V <= 0 || H % 8 != 0) return LLIMA_E_INVAL;
+    if (H > LMH_MAX_H && (H > 65536 || H % LMH_KC != 0)) return LLIMA_E_INVAL;   // MFMA path only
     if (!weight || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
     if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
     if ((uintptr_t)weight % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
@@ -340,7 +341,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.NW = lmh_waves(V);
     P.cap = softcap;
     hipStream_t st = (hipStream_t)stream;
-    if (B > lmh_rows_per_pass(H) && H % LMH_KC == 0) {   // more than one GEMV pass: MFMA tiles
+    if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
         P.NW = lmh_mfma_waves(V);
         const dim3 gm((uint32_t)(P.NW / LLIMA_WAVES)), bm(LLIMA_WG);
         for (int b0 = 0; b0 < B; b0 += LMH_MB) {
