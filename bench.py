@@ -17,7 +17,13 @@ step / ms_per_step; eager_call_us is the mean of per-call HIP events without the
 graph (host launch gaps included).  roofline.traffic = HBM bytes per step from
 the committed rocprofv3 counter runs (profiles/traffic.json), when measured for
 this workload.  cpu_baseline = the CPU oracle on a bounded sample of the same
-workload on this host.
+workload on this host (for the LM-head workloads, numpy float32 products on a
+slice of the vocabulary, scaled to the whole).
+
+--workload selects the other configurations: single_row, constrained,
+large_vocab_bf16(_greedy), argmax_bf16, speculative, score_bf16,
+mtp_masked_argmax, and lm_head_argmax / lm_head_argmax_b64 (the LM head with
+its argmax at B = 1 and B = 64).
 """
 from __future__ import annotations
 
