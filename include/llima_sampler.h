@@ -66,7 +66,8 @@ enum {
     LLIMA_E_INVAL = -1,      /* bad argument: size, dtype, config value */
     LLIMA_E_RANGE = -2,      /* id or length out of range */
     LLIMA_E_HIP = -3,        /* the HIP runtime reported an error at launch */
-    LLIMA_E_WORKSPACE = -4   /* workspace missing or too small */
+    LLIMA_E_WORKSPACE = -4,  /* workspace missing or too small */
+    LLIMA_E_SCRATCH = -5     /* the call needs more than the static scratch holds */
 };
 
 enum { LLIMA_F32 = 0, LLIMA_BF16 = 1 };
@@ -140,6 +141,24 @@ int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_
                  const uint32_t* bitmask, const float* uniforms,
                  const llima_sampler_config* cfg, int32_t* out_ids, float* out_probs,
                  uint32_t* out_keep, void* workspace, size_t workspace_bytes, void* stream);
+
+/* llima_sample without a workspace argument.  No counterpart in the reference:
+ * it serves callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  The workspace
+ * is a static device array of llima_sample_noalloc_max_bytes() (32 MiB) bytes
+ * per GPU, allocated when the library is loaded on that GPU and held until the
+ * process ends; the call allocates nothing.  Calls whose
+ * llima_sample_workspace_bytes(B, V, dtype) exceed it return LLIMA_E_SCRATCH
+ * (e.g. B*ceil(V/4096) <= 8192 for fp32 rows, B*ceil(V/8192) <= 8192 for bf16).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or different host threads without ordering) race.
+ * Results are those of llima_sample on the same inputs. */
+size_t llima_sample_noalloc_max_bytes(void);
+int llima_sample_noalloc(const void* logits, int32_t dtype, int32_t B, int32_t V,
+                         int64_t row_stride, const int32_t* history, const int32_t* history_len,
+                         int32_t H_max, const uint32_t* bitmask, const float* uniforms,
+                         const llima_sampler_config* cfg, int32_t* out_ids, float* out_probs,
+                         uint32_t* out_keep, void* stream);
 
 /* Greedy chain verification of B sequences with D draft tokens each.
  * target_logits: [B][D+1][V]; draft_ids: [B][D].  accepted_len[B] = length of

@@ -12,6 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllima_sampler.so")
 
 LLIMA_OK, LLIMA_E_INVAL, LLIMA_E_RANGE, LLIMA_E_HIP, LLIMA_E_WORKSPACE = 0, -1, -2, -3, -4
+LLIMA_E_SCRATCH = -5
 LLIMA_F32, LLIMA_BF16 = 0, 1
 ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS = 0, 1, 2
 
@@ -25,6 +26,9 @@ SIGNATURES = {
     "llima_sample_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_sample": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _vp, _sz, _vp]),
+    "llima_sample_noalloc_max_bytes": (_sz, []),
+    "llima_sample_noalloc": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _i32, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _vp]),
     "llima_verify_greedy_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "llima_verify_greedy": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _sz,
                                            _vp]),

@@ -41,6 +41,8 @@
 // only ever takes the argmax (sima_lmm/devkit/cpp/utils.hpp:80-152,
 // sima_lmm/devkit/cpp/language_model.cpp:3689-3714); greedy rows follow that
 // argmax (first index of the maximum) over the masked, penalised row.
+#include <mutex>
+
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -1919,4 +1921,58 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
         hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+// ================================================================== no-alloc variant
+// llima_sample_noalloc: llima_sample with its workspace in a static device
+// array instead of a caller buffer, for callers that cannot allocate (code under
+// HIP graph capture, serving loops that forbid hipMalloc).  The array is
+// allocated on each GPU when the library's code object is loaded there and is
+// held until the process ends.  Its name is a host-side stand-in, not a device
+// address: host code uses only the address hipGetSymbolAddress returns, looked
+// up once per device with that device current and kept in g_scratch_dev.
+// The sampler keeps no state in its workspace between calls (every slot a call
+// reads is written earlier in the same call), so nothing needs clearing; calls
+// that overlap on one GPU share the array and race.
+#define LLIMA_SAMPLE_SCRATCH_BYTES ((size_t)32 << 20)
+#define LLIMA_SCRATCH_MAX_DEVICES 64
+
+static __device__ __align__(256) uint64_t scratch[LLIMA_SAMPLE_SCRATCH_BYTES / sizeof(uint64_t)];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[LLIMA_SCRATCH_MAX_DEVICES];   // guarded by g_scratch_mu
+
+static int scratch_of_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= LLIMA_SCRATCH_MAX_DEVICES)
+        return LLIMA_E_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LLIMA_E_HIP;
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return LLIMA_OK;
+}
+
+extern "C" size_t llima_sample_noalloc_max_bytes(void) { return LLIMA_SAMPLE_SCRATCH_BYTES; }
+
+extern "C" int llima_sample_noalloc(const void* logits, int32_t dtype, int32_t B, int32_t V,
+                                    int64_t row_stride, const int32_t* history,
+                                    const int32_t* history_len, int32_t H_max,
+                                    const uint32_t* bitmask, const float* uniforms,
+                                    const llima_sampler_config* cfg, int32_t* out_ids,
+                                    float* out_probs, uint32_t* out_keep, void* stream) {
+    const size_t need = llima_sample_workspace_bytes(B, V, dtype);
+    if (B <= 0 || need == 0)   // an empty call, or sizes llima_sample rejects: nothing is launched
+        return llima_sample(logits, dtype, B, V, row_stride, history, history_len, H_max, bitmask,
+                            uniforms, cfg, out_ids, out_probs, out_keep, nullptr, 0, stream);
+    if (need > LLIMA_SAMPLE_SCRATCH_BYTES) return LLIMA_E_SCRATCH;
+    void* ws = nullptr;
+    const int rc = scratch_of_current_device(&ws);
+    if (rc != LLIMA_OK) return rc;
+    return llima_sample(logits, dtype, B, V, row_stride, history, history_len, H_max, bitmask,
+                        uniforms, cfg, out_ids, out_probs, out_keep, ws,
+                        LLIMA_SAMPLE_SCRATCH_BYTES, stream);
 }
