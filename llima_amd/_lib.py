@@ -14,15 +14,17 @@ LIB_PATH = os.path.join(HERE, "libllima_sampler.so")
 LLIMA_OK, LLIMA_E_INVAL, LLIMA_E_RANGE, LLIMA_E_HIP, LLIMA_E_WORKSPACE = 0, -1, -2, -3, -4
 LLIMA_E_SCRATCH = -5
 LLIMA_F32, LLIMA_BF16 = 0, 1
-ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS = 0, 1, 2
+ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS, ARGMAX_LOWEST = 0, 1, 2, 3
+MAX_SPLITS = 16
 
 # name -> (restype, argtypes) for every entry point of include/llima_sampler.h
 _vp, _sz, _i32, _i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
 SIGNATURES = {
-    "llima_workspace_init": (ctypes.c_int, [_vp, _sz, _vp]),
     "llima_argmax_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_argmax": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _sz,
                                     _vp]),
+    "llima_argmax_splits": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                           _sz, _vp]),
     "llima_sample_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_sample": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _i32, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _vp, _sz, _vp]),
@@ -30,14 +32,18 @@ SIGNATURES = {
     "llima_sample_noalloc": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _i32, _vp, _vp,
                                             _vp, _vp, _vp, _vp, _vp]),
     "llima_verify_greedy_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
-    "llima_verify_greedy": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _sz,
-                                           _vp]),
+    "llima_verify_greedy": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                           _vp, _sz, _vp]),
+    "llima_verify_greedy_splits": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
+                                                  _vp, _vp, _vp, _sz, _vp]),
     "llima_verify_tree_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_verify_tree": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _i32, _i32, _vp, _vp,
                                          _sz, _vp]),
     "llima_verify_rejection_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_verify_rejection": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                               _vp, _sz, _vp]),
+    "llima_verify_rejection_ex": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                                 _vp, _i32, _vp, _vp, _sz, _vp]),
     "llima_score_logits_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_score_logits": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),

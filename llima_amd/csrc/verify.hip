@@ -40,10 +40,10 @@
 // and residency of the workgroups.  Slots are written and polled with
 // device-scope atomics (the chunks of a row may run on different XCDs, whose
 // L2 caches are not coherent with each other).  help_after is VR_HELP_AFTER
-// unless the environment variable LLIMA_VERIFY_HELP_AFTER gives another count
-// (0 makes every waiter read its row's late chunks itself: a test setting).
-#include <cstdlib>
-
+// unless llima_verify_rejection_ex gives another count (0 makes every waiter
+// read its row's late chunks itself); with ~1 us per poll, a row whose chunks
+// are held back (e.g. by kernels of other streams occupying the CUs) delays
+// its waiters by at most about help_after us before they read those chunks.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -81,6 +81,7 @@ struct VerifyParams {
     SeqCtx* ctx;         // [B]
     int32_t B, D, V, S, NR, NG, SD;
     int32_t help_after;  // polls before a waiter reads a late chunk itself
+    uint32_t* help_count;  // nullable: chunks read by waiters (cleared by vr_clear)
 };
 
 // Row r: target rows first ([B][D+1]), then draft rows ([B][D]).
@@ -172,6 +173,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_clear(VerifyParams P) {
     const int n = P.NR * P.S;
     for (int i = (int)(blockIdx.x * LLIMA_WG + threadIdx.x); i < n; i += (int)(gridDim.x * LLIMA_WG))
         P.maxk[i] = 0;
+    if (P.help_count && blockIdx.x == 0 && threadIdx.x == 0) *P.help_count = 0;
 }
 
 // Maximum key of chunk c of a row (every thread gets it), read one 16-byte
@@ -229,8 +231,12 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
         if (miss < 0) break;                                    // every chunk published
         if (round >= P.help_after) {                            // a late chunk: read it here
             const uint32_t km = chunk_max_key(rowp, miss, P.V, bs);
-            if (threadIdx.x == 0)
+            if (threadIdx.x == 0) {
                 __hip_atomic_store(&slot[miss], km, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (P.help_count)
+                    __hip_atomic_fetch_add(P.help_count, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         __syncthreads();
     }
@@ -528,16 +534,18 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
            al256((size_t)B * sizeof(SeqCtx));
 }
 
-extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
-                                      int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
-                                      const float* u_accept, const float* u_resample,
-                                      int32_t* accepted_len, int32_t* emitted, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
+extern "C" int llima_verify_rejection_ex(const float* target_logits, const float* draft_logits,
+                                         int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
+                                         const float* u_accept, const float* u_resample,
+                                         int32_t* accepted_len, int32_t* emitted,
+                                         int32_t help_after, uint32_t* help_count,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
     if (B > 0 && (!target_logits || !u_resample || !accepted_len || !emitted)) return LLIMA_E_INVAL;
     if (B > 0 && D > 0 && (!draft_logits || !draft_ids || !u_accept)) return LLIMA_E_INVAL;
     if (B < 0 || D < 0 || D > VR_MAX_D || V <= 0 || V > (1 << 22)) return LLIMA_E_INVAL;
     if ((uintptr_t)target_logits % 16 || (D > 0 && (uintptr_t)draft_logits % 16) || V % 4)
         return LLIMA_E_INVAL;                  // rows are read with 16-byte loads
+    if (help_after > (1 << 20)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_verify_rejection_workspace_bytes(B, D, V))
         return LLIMA_E_WORKSPACE;
@@ -550,11 +558,8 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.NR = B * (2 * D + 1);
     P.NG = (V + VR_G - 1) / VR_G;
     P.SD = (V + VR_DCHUNK - 1) / VR_DCHUNK;
-    P.help_after = VR_HELP_AFTER;
-    if (const char* e = std::getenv("LLIMA_VERIFY_HELP_AFTER")) {
-        const long h = std::strtol(e, nullptr, 10);
-        P.help_after = h < 0 ? 0 : h > (1L << 20) ? (1 << 20) : (int32_t)h;
-    }
+    P.help_after = help_after < 0 ? VR_HELP_AFTER : help_after;
+    P.help_count = help_count;
     char* w = (char*)workspace;
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
@@ -570,4 +575,14 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
+                                      int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
+                                      const float* u_accept, const float* u_resample,
+                                      int32_t* accepted_len, int32_t* emitted, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    return llima_verify_rejection_ex(target_logits, draft_logits, B, D, V, draft_ids, u_accept,
+                                     u_resample, accepted_len, emitted, -1, nullptr, workspace,
+                                     workspace_bytes, stream);
 }

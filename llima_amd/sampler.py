@@ -8,6 +8,7 @@ the buffers handed to it (inputs must already be on the GPU).
   argmax_bf16(values)                 utils.hpp:80-152
   calc_next_token_id(logits)          language_model.cpp:3689-3714
   argmax_lm_head_rows(rows, drafts)   language_model.cpp:3636-3687
+  spec_path_argmax(logits, row)       language_model.cpp:1518-1611
   resolve_draft_tokens(...)           gemma4_mtp_helpers.cpp:81-111 (via verify_greedy)
   evaluate_posterior / verify_tree    eagle_helpers.hpp:153-195, language_model_eagle3.cpp:530-567
   sample(...)                         the sampler stages (no reference counterpart)
@@ -32,6 +33,7 @@ from ._lib import check, lib
 
 __all__ = [
     "SamplerConfig", "argmax", "argmax_bf16", "calc_next_token_id", "argmax_lm_head_rows",
+    "spec_path_argmax",
     "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
     "Workspace", "score_logits", "select_candidate_tokens", "argmax_gemma4_mtp_masked_rows",
     "argmax_gemma4_mtp_masked_row",
@@ -78,17 +80,23 @@ class SamplerConfig:
 
 
 class Workspace:
-    """Per-device scratch buffers, grown on demand.  The kernels keep no state
-    in them between calls, so one buffer serves calls of any shape; allocation
-    happens only when a call needs more than any earlier call on that device."""
+    """Scratch buffers per (device, current stream, entry point), grown on
+    demand.  The kernels keep no state in them between calls, so one buffer
+    serves calls of any shape; allocation happens only when a call needs more
+    than any earlier call on that stream.  Calls on one stream are ordered, so
+    they may share a buffer; each stream has its own, so calls on different
+    streams never race on scratch, and a buffer is allocated on (and returned
+    to torch's caching allocator under) the stream that uses it."""
     _bufs: dict = {}
 
     @classmethod
     def get(cls, device: torch.device, kind: str, nbytes: int) -> torch.Tensor:
-        key = (device.index, kind)
+        stream = torch.cuda.current_stream(device)
+        key = (device.index, stream.cuda_stream, kind)
         buf = cls._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
             cls._bufs[key] = buf
         return buf
 
@@ -126,16 +134,54 @@ def _rows2d(logits: torch.Tensor) -> torch.Tensor:
 
 
 MODES = {"split_first": _lib.ARGMAX_SPLIT_FIRST, "neg_inf": _lib.ARGMAX_NEG_INF,
-         "quarters": _lib.ARGMAX_QUARTERS}
+         "quarters": _lib.ARGMAX_QUARTERS, "lowest": _lib.ARGMAX_LOWEST}
 
 
-def argmax(logits: torch.Tensor, split_dim: int = 0, mode: str = "split_first"):
+def _split_arrays(splits):
+    """Host arrays describing split buffers [..., w_i] (last dim contiguous):
+    (pointers, widths, row strides, rows, V, dtype code, keep-alive list)."""
+    if not 1 <= len(splits) <= _lib.MAX_SPLITS:
+        raise ValueError(f"1..{_lib.MAX_SPLITS} split buffers are supported")
+    xs = []
+    for t in splits:
+        t = t.reshape(-1, t.shape[-1])
+        if t.stride(-1) != 1:
+            t = t.contiguous()
+        xs.append(t)
+    rows, dt = xs[0].shape[0], _dtype_code(xs[0])
+    for t in xs:
+        if t.shape[0] != rows or _dtype_code(t) != dt or t.device != xs[0].device:
+            raise ValueError("split buffers must share rows, dtype and device")
+    _on_gpu(*xs)
+    n = len(xs)
+    ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in xs])
+    widths = (ctypes.c_int32 * n)(*[t.shape[1] for t in xs])
+    strides = (ctypes.c_int64 * n)(*[t.stride(0) for t in xs])
+    return ptrs, widths, strides, rows, sum(t.shape[1] for t in xs), dt, xs
+
+
+def argmax(logits, split_dim: int = 0, mode: str = "split_first"):
     """Greedy selection over [B, V] rows -> (ids int32 [B], values float32 [B]).
 
+    logits: one [B, V] tensor, or a list of split buffers [B, w_i] holding
+    consecutive vocabulary ranges (the reference's n{N}_lm_split{i} buffers,
+    language_model.cpp:3584-3613), each buffer then being a split.
     mode "split_first": per split of split_dim values, argmax_bf16 semantics
     (utils.hpp:80-152) merged as _argmax_lm_head_row (language_model.cpp:3616-3633);
     "neg_inf": the EAGLE3 verify scan (language_model_eagle3.cpp:486-522);
-    "quarters": _calc_next_token_id's four-way split (language_model.cpp:3689-3714)."""
+    "quarters": _calc_next_token_id's four-way split (language_model.cpp:3689-3714);
+    "lowest": the speculative path's multi-split scan from bf16 lowest()
+    (language_model.cpp:1556-1575)."""
+    if isinstance(logits, (list, tuple)):
+        ptrs, widths, strides, B, V, dt, keep = _split_arrays(logits)
+        dev = keep[0].device
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        vals = torch.empty(B, dtype=torch.float32, device=dev)
+        ws = Workspace.get(dev, "argmax", lib().llima_argmax_workspace_bytes(B, V, dt))
+        check(lib().llima_argmax_splits(ptrs, widths, strides, len(keep), dt, B, MODES[mode],
+                                        ids.data_ptr(), vals.data_ptr(), ws.data_ptr(),
+                                        ws.numel(), _stream(dev)), "llima_argmax_splits")
+        return ids, vals
     x = _rows2d(logits)
     _on_gpu(x)
     B, V = x.shape
@@ -165,14 +211,32 @@ def calc_next_token_id(logits: torch.Tensor) -> int:
     return int(ids[0])
 
 
-def argmax_lm_head_rows(rows: torch.Tensor, expected_draft_tokens, split_dim: int = 0):
+def spec_path_argmax(logits, row: int) -> int:
+    """The speculative path's next token in run_model_once
+    (language_model.cpp:1518-1611): row `row` of one [N, V] buffer is scanned
+    from its first value (argmax_bf16); split buffers [N, w_i] are scanned in
+    order from bf16 lowest() with a strict '>'."""
+    if isinstance(logits, (list, tuple)) and len(logits) > 1:
+        ids, _ = argmax([t[row:row + 1] for t in logits], mode="lowest")
+    else:
+        x = logits[0] if isinstance(logits, (list, tuple)) else logits
+        ids, _ = argmax(x[row:row + 1], mode="split_first")
+    return int(ids[0])
+
+
+def argmax_lm_head_rows(rows, expected_draft_tokens, split_dim: int = 0):
     """_argmax_lm_head_rows (language_model.cpp:3636-3687): per-row argmax of the
     first len(expected)+1 rows, truncated after the first row whose argmax differs
-    from the expected draft token."""
+    from the expected draft token.  rows: [N, V] (splits of split_dim values)
+    or the list of split buffers [N, w_i]."""
     n = len(expected_draft_tokens) + 1
-    if n > rows.shape[0]:
-        raise RuntimeError(f"Requested {n} lm_head rows from n{rows.shape[0]} output")
-    ids, _ = argmax(rows[:n], split_dim=split_dim)
+    nrows = rows[0].shape[0] if isinstance(rows, (list, tuple)) else rows.shape[0]
+    if n > nrows:
+        raise RuntimeError(f"Requested {n} lm_head rows from n{nrows} output")
+    if isinstance(rows, (list, tuple)):
+        ids, _ = argmax([t[:n] for t in rows])
+    else:
+        ids, _ = argmax(rows[:n], split_dim=split_dim)
     ids = ids.tolist()
     out = []
     for r, t in enumerate(ids):
@@ -229,24 +293,42 @@ def sample(logits: torch.Tensor, uniforms: torch.Tensor, config: SamplerConfig,
     return (ids, probs, keep) if return_keep else (ids, probs)
 
 
-def verify_greedy(target_logits: torch.Tensor, draft_ids: torch.Tensor):
-    """Greedy chain verification: target_logits [B, D+1, V], draft_ids [B, D] ->
-    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded)."""
-    t = target_logits.contiguous()
-    if t.dim() != 3:
-        raise ValueError("target_logits must be [B, D+1, V]")
-    B, D1, V = t.shape
+def verify_greedy(target_logits, draft_ids: torch.Tensor, split_dim: int = 0,
+                  mode: str = "split_first"):
+    """Greedy chain verification: target_logits [B, D+1, V] (or a list of split
+    buffers [B, D+1, w_i]), draft_ids [B, D] -> (accepted_len int32 [B],
+    emitted int32 [B, D+1], -1 padded).  Each target row's argmax follows
+    split_dim and mode as argmax (the default with the head's split_dim is
+    _argmax_lm_head_rows, language_model.cpp:3636-3687)."""
+    if isinstance(target_logits, (list, tuple)):
+        if target_logits[0].dim() != 3:
+            raise ValueError("split target buffers must be [B, D+1, w_i]")
+        B, D1 = target_logits[0].shape[:2]
+        ptrs, widths, strides, _, V, dt, keep = _split_arrays(target_logits)
+        dev = keep[0].device
+    else:
+        t = target_logits.contiguous()
+        if t.dim() != 3:
+            raise ValueError("target_logits must be [B, D+1, V]")
+        B, D1, V = t.shape
+        dt = _dtype_code(t)
+        dev = t.device
+        _on_gpu(t)
     D = D1 - 1
-    dev = t.device
     d = draft_ids.to(device=dev, dtype=torch.int32).contiguous().reshape(B, D)
-    _on_gpu(t, d)
+    _on_gpu(d)
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     em = torch.empty((B, D1), dtype=torch.int32, device=dev)
-    dt = _dtype_code(t)
     ws = Workspace.get(dev, "verify_greedy", lib().llima_verify_greedy_workspace_bytes(B, D, V, dt))
-    check(lib().llima_verify_greedy(t.data_ptr(), dt, B, D, V, d.data_ptr(), acc.data_ptr(),
-                                    em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
-          "llima_verify_greedy")
+    if isinstance(target_logits, (list, tuple)):
+        check(lib().llima_verify_greedy_splits(ptrs, widths, strides, len(keep), dt, B, D,
+                                               MODES[mode], d.data_ptr(), acc.data_ptr(),
+                                               em.data_ptr(), ws.data_ptr(), ws.numel(),
+                                               _stream(dev)), "llima_verify_greedy_splits")
+    else:
+        check(lib().llima_verify_greedy(t.data_ptr(), dt, B, D, V, split_dim, MODES[mode],
+                                        d.data_ptr(), acc.data_ptr(), em.data_ptr(), ws.data_ptr(),
+                                        ws.numel(), _stream(dev)), "llima_verify_greedy")
     return acc, em
 
 
@@ -290,10 +372,15 @@ def verify_tree(tree_logits: torch.Tensor, retrieve_indices: torch.Tensor,
 
 
 def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
-                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_resample: torch.Tensor):
+                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_resample: torch.Tensor,
+                     help_after: Optional[int] = None, help_count: Optional[torch.Tensor] = None):
     """Stochastic verification: target [B, D+1, V] and draft [B, D, V] fp32
     logits, draft ids [B, D], uniforms u_accept [B, D] and u_resample [B] ->
-    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded)."""
+    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded).
+    help_after: polls (~1 us each) before a row-pass workgroup reads a late
+    chunk of its row itself (None: the library default); help_count (an int32
+    device tensor of one element, optional) receives how many chunks were read
+    that way.  The results do not depend on either."""
     t = target_logits.contiguous()
     dl = draft_logits.contiguous()
     if t.dtype != torch.float32 or dl.dtype != torch.float32:
@@ -306,13 +393,15 @@ def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
     ids = draft_ids.to(device=dev, dtype=torch.int32).contiguous()
     ua = u_accept.to(device=dev, dtype=torch.float32).contiguous()
     ur = u_resample.to(device=dev, dtype=torch.float32).contiguous()
-    _on_gpu(t, dl, ids, ua, ur)
+    _on_gpu(t, dl, ids, ua, ur, help_count)
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     em = torch.empty((B, D1), dtype=torch.int32, device=dev)
     ws = Workspace.get(dev, "verify_rejection", lib().llima_verify_rejection_workspace_bytes(B, D, V))
-    check(lib().llima_verify_rejection(t.data_ptr(), dl.data_ptr(), B, D, V, ids.data_ptr(),
-                                       ua.data_ptr(), ur.data_ptr(), acc.data_ptr(),
-                                       em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+    check(lib().llima_verify_rejection_ex(t.data_ptr(), dl.data_ptr(), B, D, V, ids.data_ptr(),
+                                          ua.data_ptr(), ur.data_ptr(), acc.data_ptr(),
+                                          em.data_ptr(), -1 if help_after is None else help_after,
+                                          _ptr(help_count), ws.data_ptr(), ws.numel(),
+                                          _stream(dev)),
           "llima_verify_rejection")
     return acc, em
 

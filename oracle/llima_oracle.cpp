@@ -130,6 +130,11 @@ static inline int bitlen128(u128 v) {
 //         wins and an all -inf/NaN row yields id 0 (language_model_eagle3.cpp:486-522).
 // mode 2: four parts [V*p/4, V*(p+1)/4), each argmax_bf16, merged from
 //         (values[0], 0) with the same rule (language_model.cpp:3689-3714).
+// mode 3: best starts at bf16 lowest() with index 0, strict '>' over every
+//         split in order (the speculative path's multi-split scan,
+//         language_model.cpp:1556-1575).
+static const float ORC_BF16_LOWEST = -3.38953139e38f;   // bf16 0xFF7F
+
 static void argmax_split(const void* row, int dtype, int64_t begin, int64_t size,
                          float* best_v, int64_t* best_i) {
     float best = load_logit(row, dtype, begin);
@@ -142,48 +147,78 @@ static void argmax_split(const void* row, int dtype, int64_t begin, int64_t size
     *best_i = begin + idx;
 }
 
-int orc_argmax(const void* logits, int dtype, int B, int V, int64_t row_stride,
-               int split_dim, int mode, int32_t* out_ids, float* out_vals) {
+// One row; mode 0 splits start at bounds[0..nb-1] (bounds[0] == 0, increasing).
+static void argmax_row(const void* row, int dtype, int V, const int64_t* bounds, int nb,
+                       int mode, float* out_v, int64_t* out_i) {
+    float bv;
+    int64_t bi = 0;
+    if (mode == 1 || mode == 3) {
+        bv = mode == 1 ? -std::numeric_limits<float>::infinity() : ORC_BF16_LOWEST;
+        for (int64_t i = 0; i < V; ++i) {
+            float v = load_logit(row, dtype, i);
+            if (v > bv) { bv = v; bi = i; }
+        }
+    } else if (mode == 0) {
+        bv = -std::numeric_limits<float>::infinity();
+        for (int s = 0; s < nb; ++s) {
+            int64_t begin = bounds[s], end = s + 1 < nb ? bounds[s + 1] : V;
+            float v; int64_t i;
+            argmax_split(row, dtype, begin, end - begin, &v, &i);
+            if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+        }
+    } else {
+        bv = load_logit(row, dtype, 0);
+        for (int p = 0; p < 4; ++p) {
+            int64_t begin = (int64_t)V * p / 4, end = (int64_t)V * (p + 1) / 4;
+            if (end <= begin) continue;
+            float v; int64_t i;
+            argmax_split(row, dtype, begin, end - begin, &v, &i);
+            if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+        }
+    }
+    *out_v = bv;
+    *out_i = bi;
+}
+
+static bool valid_bounds(const int64_t* bounds, int nb, int V) {
+    if (nb < 1 || bounds[0] != 0) return false;
+    for (int s = 1; s < nb; ++s)
+        if (bounds[s] <= bounds[s - 1] || bounds[s] >= V) return false;
+    return true;
+}
+
+// Split starts given explicitly (mode 0); modes 1-3 ignore them.
+int orc_argmax_bounds(const void* logits, int dtype, int B, int V, int64_t row_stride,
+                      const int64_t* bounds, int nb, int mode, int32_t* out_ids,
+                      float* out_vals) {
     if (B < 0 || V <= 0 || (dtype != 0 && dtype != 1)) return ORC_E_INVAL;
-    if (mode < 0 || mode > 2) return ORC_E_INVAL;
+    if (mode < 0 || mode > 3 || !valid_bounds(bounds, nb, V)) return ORC_E_INVAL;
     const size_t esz = dtype == 0 ? 4 : 2;
 #pragma omp parallel for schedule(static)
     for (int b = 0; b < B; ++b) {
         const void* row = (const char*)logits + (size_t)b * row_stride * esz;
         float bv;
         int64_t bi;
-        if (mode == 1) {
-            bv = -std::numeric_limits<float>::infinity();
-            bi = 0;
-            for (int64_t i = 0; i < V; ++i) {
-                float v = load_logit(row, dtype, i);
-                if (v > bv) { bv = v; bi = i; }
-            }
-        } else if (mode == 0) {
-            int sd = (split_dim <= 0 || split_dim >= V) ? V : split_dim;
-            bv = -std::numeric_limits<float>::infinity();
-            bi = 0;
-            for (int64_t s = 0; s < V; s += sd) {
-                int64_t size = std::min<int64_t>(sd, V - s);
-                float v; int64_t i;
-                argmax_split(row, dtype, s, size, &v, &i);
-                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-            }
-        } else {
-            bv = load_logit(row, dtype, 0);
-            bi = 0;
-            for (int p = 0; p < 4; ++p) {
-                int64_t begin = (int64_t)V * p / 4, end = (int64_t)V * (p + 1) / 4;
-                if (end <= begin) continue;
-                float v; int64_t i;
-                argmax_split(row, dtype, begin, end - begin, &v, &i);
-                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-            }
-        }
+        argmax_row(row, dtype, V, bounds, nb, mode, &bv, &bi);
         out_ids[b] = (int32_t)bi;
         if (out_vals) out_vals[b] = bv;
     }
     return ORC_OK;
+}
+
+static std::vector<int64_t> uniform_bounds(int V, int split_dim) {
+    const int sd = (split_dim <= 0 || split_dim >= V) ? V : split_dim;
+    std::vector<int64_t> b;
+    for (int64_t s = 0; s < V; s += sd) b.push_back(s);
+    return b;
+}
+
+int orc_argmax(const void* logits, int dtype, int B, int V, int64_t row_stride,
+               int split_dim, int mode, int32_t* out_ids, float* out_vals) {
+    if (V <= 0) return ORC_E_INVAL;
+    const std::vector<int64_t> b = uniform_bounds(V, split_dim);
+    return orc_argmax_bounds(logits, dtype, B, V, row_stride, b.data(), (int)b.size(), mode,
+                             out_ids, out_vals);
 }
 
 // ---------------------------------------------------------------- sampler
@@ -370,10 +405,12 @@ int orc_resolve_draft_tokens(const int32_t* drafts, int D, const int32_t* target
 }
 
 int orc_verify_greedy(const void* target_logits, int dtype, int B, int D, int V,
-                      const int32_t* draft_ids, int32_t* accepted_len, int32_t* emitted) {
+                      const int64_t* bounds, int nb, int mode, const int32_t* draft_ids,
+                      int32_t* accepted_len, int32_t* emitted) {
     if (B < 0 || D < 0 || V <= 0) return ORC_E_INVAL;
     std::vector<int32_t> tgt((size_t)B * (D + 1));
-    int rc = orc_argmax(target_logits, dtype, B * (D + 1), V, V, 0, 0, tgt.data(), nullptr);
+    int rc = orc_argmax_bounds(target_logits, dtype, B * (D + 1), V, V, bounds, nb, mode,
+                               tgt.data(), nullptr);
     if (rc) return rc;
     for (int b = 0; b < B; ++b) {
         std::vector<int32_t> em(D + 1), fl(D + 1);

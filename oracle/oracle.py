@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
 
 F32, BF16 = 0, 1
-ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS = 0, 1, 2
+ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS, ARGMAX_LOWEST = 0, 1, 2, 3
 
 
 def build() -> str:
@@ -95,16 +95,26 @@ def weight(x: float, xmax: float) -> int:
     return int(lib().orc_weight(float(x), float(xmax)))
 
 
-def argmax(logits, split_dim: int = 0, mode: int = ARGMAX_SPLIT_FIRST):
+def _bounds(V, split_dim, bounds):
+    if bounds is None:
+        sd = V if split_dim <= 0 or split_dim >= V else split_dim
+        bounds = range(0, V, sd)
+    return np.ascontiguousarray(list(bounds), np.int64)
+
+
+def argmax(logits, split_dim: int = 0, mode: int = ARGMAX_SPLIT_FIRST, bounds=None):
     """argmax_bf16 / _argmax_lm_head_row semantics (utils.hpp:80-152,
-    language_model.cpp:3616-3633, 3689-3714, language_model_eagle3.cpp:486-522)."""
+    language_model.cpp:3616-3633, 3689-3714, language_model_eagle3.cpp:486-522,
+    the spec path's multi-split scan language_model.cpp:1556-1575 as mode 3).
+    bounds: explicit split starts (mode 0) instead of split_dim."""
     x, dt = _logits(logits)
     x2 = x.reshape(-1, x.shape[-1])
     B, V = x2.shape
+    bd = _bounds(V, split_dim, bounds)
     ids = np.empty(B, np.int32)
     vals = np.empty(B, np.float32)
-    rc = lib().orc_argmax(_ptr(x2), dt, B, V, ctypes.c_int64(V), split_dim, mode,
-                          _ptr(ids), _ptr(vals))
+    rc = lib().orc_argmax_bounds(_ptr(x2), dt, B, V, ctypes.c_int64(V), _ptr(bd), len(bd), mode,
+                                 _ptr(ids), _ptr(vals))
     if rc:
         raise ValueError(f"orc_argmax rc={rc}")
     return ids.reshape(x.shape[:-1]), vals.reshape(x.shape[:-1])
@@ -160,13 +170,18 @@ def resolve_draft_tokens(drafts, targets):
     return [(int(em[i]), bool(fl[i])) for i in range(n.value)]
 
 
-def verify_greedy(target_logits, draft_ids):
+def verify_greedy(target_logits, draft_ids, split_dim: int = 0, mode: int = ARGMAX_SPLIT_FIRST,
+                  bounds=None):
+    """Per-row argmax (as argmax) of [B, D+1, V] target rows, then
+    resolve_draft_tokens per sequence -> (accepted_len [B], emitted [B, D+1])."""
     x, dt = _logits(target_logits)
     B, D1, V = x.shape
+    bd = _bounds(V, split_dim, bounds)
     d = np.ascontiguousarray(draft_ids, np.int32).reshape(B, D1 - 1)
     acc = np.empty(B, np.int32)
     em = np.empty((B, D1), np.int32)
-    rc = lib().orc_verify_greedy(_ptr(x), dt, B, D1 - 1, V, _ptr(d), _ptr(acc), _ptr(em))
+    rc = lib().orc_verify_greedy(_ptr(x), dt, B, D1 - 1, V, _ptr(bd), len(bd), mode, _ptr(d),
+                                 _ptr(acc), _ptr(em))
     if rc:
         raise ValueError(f"orc_verify_greedy rc={rc}")
     return acc, em

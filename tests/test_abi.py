@@ -18,7 +18,7 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ["llima_argmax", "llima_sample", "llima_verify_greedy", "llima_verify_tree",
-              "llima_verify_rejection", "llima_workspace_init", "llima_score_logits",
+              "llima_verify_rejection", "llima_verify_rejection_ex", "llima_score_logits",
               "llima_mtp_masked_argmax"]:
         assert n in names
 
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 def test_host_only_entry_points():
     from llima_amd._lib import lib
     L = lib()
-    assert L.llima_abi_version() == 1
+    assert L.llima_abi_version() == 2
     assert L.llima_status_string(-4).decode() == "workspace missing or too small"
     assert L.llima_sample_workspace_bytes(64, 128256, 0) > 0
     assert L.llima_argmax_workspace_bytes(0, 10, 0) == 0
@@ -47,6 +47,20 @@ def test_host_only_entry_points():
                                     ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                     ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == -1
     p = ctypes.c_void_p(16)
+    # split buffers: QUARTERS is refused, as are more than 16 splits and empty splits
+    ptrs = (ctypes.c_void_p * 17)(*([16] * 17))
+    widths = (ctypes.c_int32 * 17)(*([64] * 17))
+    assert L.llima_argmax_splits(ptrs, widths, None, 2, 0, 1, 2, p, None, p, 1 << 20, None) == -1
+    assert L.llima_argmax_splits(ptrs, widths, None, 17, 0, 1, 0, p, None, p, 1 << 20, None) == -1
+    assert L.llima_argmax_splits(ptrs, widths, None, 0, 0, 1, 0, p, None, p, 1 << 20, None) == -1
+    zero = (ctypes.c_int32 * 2)(64, 0)
+    assert L.llima_argmax_splits(ptrs, zero, None, 2, 0, 1, 0, p, None, p, 1 << 20, None) == -1
+    assert L.llima_argmax_splits(ptrs, widths, None, 2, 0, 1, 3, p, None, None, 0, None) == -4
+    assert L.llima_verify_greedy_splits(ptrs, widths, None, 2, 0, 1, 2, 2, p, p, p, p, 1 << 20,
+                                        None) == -1
+    assert L.llima_verify_greedy(p, 0, 1, 2, 64, 0, 4, p, p, p, p, 1 << 20, None) == -1
+    assert L.llima_sample_noalloc(p, 0, 4096, 128256, 128256, None, None, 0, None, p,
+                                  ctypes.byref(_lib_cfg()), p, None, None, None) == -5
     assert L.llima_score_logits(None, 0, 1, 10, 10, p, p, p, p, 1 << 20, None) == -1
     assert L.llima_score_logits(p, 0, 1, 10, 10, p, p, p, None, 0, None) == -4
     assert L.llima_score_logits_workspace_bytes(256, 262144, 1) > 0
@@ -63,6 +77,13 @@ def test_host_only_entry_points():
                                      None) == -1
     assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, p, 1, 1, 8, 8, p, p, None, None, 0,
                                      None) == -4              # no workspace
+
+
+def _lib_cfg():
+    from llima_amd._lib import SamplerConfigC
+    c = SamplerConfigC()
+    c.temperature, c.repetition_penalty = 1.0, 1.0
+    return c
 
 
 def test_config_struct_layout_matches_header():

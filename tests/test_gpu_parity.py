@@ -41,7 +41,7 @@ def test_argmax_parity(gpu, oracle, dtype, B, V):
     x = rng.integers(-50, 51, size=(B, V)).astype(np.float32) * np.float32(0.25)  # ties
     if dtype == "bf16":
         x = wl.f32_to_bf16_bits(x)
-    for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters")]:
+    for mode, mname in [(0, "split_first"), (1, "neg_inf"), (2, "quarters"), (3, "lowest")]:
         ids, vals = llima_amd.argmax(_t(x, gpu), mode=mname)
         eids, evals = oracle.argmax(x, mode=mode)
         assert (_np(ids) == eids).all(), mname
@@ -471,21 +471,55 @@ def test_verify_rejection_edges(gpu, oracle):
 
 
 @pytest.mark.parametrize("B,D,V", [(16, 7, 128256), (3, 2, 70000), (2, 0, 9000)])
-def test_verify_rejection_help_path(gpu, oracle, monkeypatch, B, D, V):
-    """LLIMA_VERIFY_HELP_AFTER=0: a row-pass workgroup that finds one of its
-    row's chunk maxima unpublished reads that chunk itself at once, so the path
-    that bounds every wait runs on most rows; the results are unchanged."""
+def test_verify_rejection_help_path(gpu, oracle, B, D, V):
+    """help_after = 0: a row-pass workgroup that finds one of its row's chunk
+    maxima unpublished reads that chunk itself at once, so the path that bounds
+    every wait runs; the device counter shows it did, and the results are
+    unchanged."""
+    import torch
     import llima_amd
     _say("verify_rejection help path", B, D, V)
-    monkeypatch.setenv("LLIMA_VERIFY_HELP_AFTER", "0")
     w = wl.speculative(B=B, D=D, V=V, seed=61 + V)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=gpu)
     acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
                                          _t(w["draft_ids"], gpu), _t(w["u_accept"], gpu),
-                                         _t(w["u_resample"], gpu))
+                                         _t(w["u_resample"], gpu), help_after=0, help_count=cnt)
     eacc, eem = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
                                         w["u_resample"])
     assert (_np(acc) == eacc).all(), (_np(acc), eacc)
     assert (_np(em) == eem).all()
+    n = int(_np(cnt)[0])
+    _say("help-path chunk reads", n)
+    assert n >= 0
+    if B * (2 * D + 1) >= 64:
+        # hundreds of rows of 16 chunks: some waiter polls before a partner publishes
+        assert n > 0
+
+
+def test_two_streams_use_separate_workspaces(gpu, oracle):
+    """Two sampling calls on two streams with no synchronisation between them
+    (each stream gets its own scratch), both checked against the oracle."""
+    import torch
+    import llima_amd
+    _say("two streams")
+    wa = wl.batched_penalties(B=32, V=128256, H=2048)
+    wb = wl.large_vocab_bf16(B=32, V=262144, H=512)
+    xa, ua, ha = _t(wa["logits"], gpu), _t(wa["uniforms"], gpu), _t(wa["history"], gpu)
+    xb, ub, hb = _t(wb["logits"], gpu), _t(wb["uniforms"], gpu), _t(wb["history"], gpu)
+    torch.cuda.synchronize(gpu)
+    sa, sb = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    outs = {}
+    for rep in range(3):
+        with torch.cuda.stream(sa):
+            outs["a"] = llima_amd.sample(xa, ua, llima_amd.SamplerConfig(**wa["cfg"]), history=ha)
+        with torch.cuda.stream(sb):
+            outs["b"] = llima_amd.sample(xb, ub, llima_amd.SamplerConfig(**wb["cfg"]), history=hb)
+    torch.cuda.synchronize(gpu)
+    from oracle.oracle import SamplerConfig as OC
+    for k, w in (("a", wa), ("b", wb)):
+        eids, eprobs = oracle.sample(w["logits"], w["uniforms"], OC(**w["cfg"]), history=w["history"])
+        assert (_np(outs[k][0]) == eids).all(), k
+        assert (_np(outs[k][1]).view(np.uint32) == eprobs.view(np.uint32)).all(), k
 
 
 def test_empty_batches(gpu, oracle):

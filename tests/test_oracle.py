@@ -81,9 +81,73 @@ def test_argmax_reference_nan_and_split_rules(oracle):
     row8 = np.array([1, 2, nan, 9, 3, 4, 5, 6], np.float32)
     assert oracle.argmax(row8[None], mode=2)[0][0] == 7
     # all -inf -> 0 in every mode; ties -> lowest index
-    for m in (0, 1, 2):
+    for m in (0, 1, 2, 3):
         assert oracle.argmax(np.full((1, 5), -inf, np.float32), mode=m)[0][0] == 0
         assert oracle.argmax(np.array([[1, 5, 5, 2]], np.float32), mode=m)[0][0] == 1
+    # the spec path's multi-split scan starts at bf16 lowest() (language_model.cpp:1556-1575):
+    # a maximum equal to lowest() never wins, one just above it does
+    low = np.float32(-3.38953139e38)
+    assert wl.bf16_bits_to_f32(np.array([0xFF7F], np.uint16))[0] == low
+    row = np.array([[-inf, nan, low, -inf]], np.float32)
+    assert oracle.argmax(row, mode=3)[0][0] == 0
+    assert oracle.argmax(row, mode=1)[0][0] == 2 and oracle.argmax(row, mode=0)[0][0] == 2
+    row = np.array([[low, -inf, np.float32(-3.3e38), nan]], np.float32)
+    assert oracle.argmax(row, mode=3)[0][0] == 2
+
+
+def _literal_lm_head_row(row, starts):
+    """_argmax_lm_head_row over split views (language_model.cpp:3616-3633), each
+    split by argmax_bf16's loop (utils.hpp:140-151), written as plain loops."""
+    best_value, best_index = -math.inf, 0
+    V = len(row)
+    for k, begin in enumerate(starts):
+        end = starts[k + 1] if k + 1 < len(starts) else V
+        best, off = float(row[begin]), 0
+        for i in range(1, end - begin):
+            if float(row[begin + i]) > best:
+                best, off = float(row[begin + i]), i
+        index = begin + off
+        if best > best_value or (best == best_value and index < best_index):
+            best_value, best_index = best, index
+    return best_index
+
+
+def _literal_spec_multi_split(row):
+    """The speculative path's multi-split scan (language_model.cpp:1556-1575)."""
+    best_val, best_idx = float(np.float32(-3.38953139e38)), 0
+    for j, v in enumerate(row):
+        if float(v) > best_val:
+            best_val, best_idx = float(v), j
+    return best_idx
+
+
+def test_argmax_split_bounds_against_literal_restatement(oracle):
+    """Explicit split starts (uneven splits, NaN at split starts, -inf, lowest())
+    against plain-loop restatements of the two reference scans."""
+    rng = np.random.default_rng(23)
+    low = np.float32(-3.38953139e38)
+    for trial in range(60):
+        V = int(rng.integers(2, 90))
+        nb = int(rng.integers(1, min(V, 6) + 1))
+        starts = sorted(set([0] + list(rng.choice(np.arange(1, V), size=nb - 1, replace=False))))
+        x = rng.integers(-3, 4, size=(4, V)).astype(np.float32)
+        pool = np.array([np.nan, -np.inf, low, np.inf], np.float32)
+        for b in range(4):
+            hit = rng.random(V) < 0.2
+            x[b, hit] = pool[rng.integers(0, 4, size=hit.sum())]
+            if rng.random() < 0.5:
+                x[b, starts[int(rng.integers(0, len(starts)))]] = np.nan
+        if trial % 2:
+            x = wl.bf16_bits_to_f32(wl.f32_to_bf16_bits(x))
+        ids0 = oracle.argmax(x, mode=0, bounds=starts)[0]
+        ids3 = oracle.argmax(x, mode=3, bounds=starts)[0]
+        for b in range(4):
+            assert ids0[b] == _literal_lm_head_row(x[b], starts), (x[b], starts)
+            assert ids3[b] == _literal_spec_multi_split(x[b]), x[b]
+        # uniform split_dim == the same explicit starts
+        sd = int(rng.integers(1, V + 1))
+        assert (oracle.argmax(x, split_dim=sd)[0] ==
+                oracle.argmax(x, bounds=list(range(0, V, sd)))[0]).all()
 
 
 # ----------------------------------------------------------------- reference vectors
