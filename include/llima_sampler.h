@@ -46,6 +46,13 @@
  *                            sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:113-167,
  *                            _argmax_gemma4_mtp_masked_row
  *                            sima_lmm/devkit/cpp/language_model_gemma4_mtp.cpp:31-97
+ *   llima_topk            <- topk<T>                  sima_lmm/devkit/cpp/utils.hpp:216-281
+ *   llima_eagle3_tree_*   <- topk_generate's selection steps (topk, logsoftmax,
+ *                            cumulative scores, tree mask, position ids,
+ *                            retrieve indices, searchsorted)
+ *                            sima_lmm/devkit/cpp/language_model_eagle3.cpp:808-1164,
+ *                            sima_lmm/devkit/cpp/utils.hpp:283-301,
+ *                            sima_lmm/devkit/cpp/eagle_helpers.hpp:197-214
  *   llima_lm_head_argmax  <- the in-graph LM head + softcap + argmax
  *                            sima_lmm/model/language_part_base.py:171-180,
  *                            sima_lmm/model/model_graph.py:601, 868-870, whose
@@ -288,6 +295,48 @@ size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V);
 int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
                          float softcap, int32_t* out_ids, float* out_vals, float* out_logits,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
+ * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):
+ * a min-heap of the first k values, replaced at the root only by strictly
+ * greater values, output by a selection sort of the heap -- the same indices in
+ * the same order, ties included.  k in [1, 32], cols >= k.  out_idx [rows][k]
+ * int32, out_vals [rows][k] fp32 (bf16 values widened exactly).  No workspace. */
+int llima_topk(const void* x, int32_t dtype, int32_t rows, int32_t cols, int64_t row_stride,
+               int32_t k, int32_t* out_idx, float* out_vals, void* stream);
+
+/* EAGLE3 draft tree (the selection side of topk_generate,
+ * sima_lmm/devkit/cpp/language_model_eagle3.cpp:808-1164).  The caller runs the
+ * draft model between the calls; `tree` is a caller-owned device buffer of
+ * llima_eagle3_tree_bytes(K, depth) bytes holding the tree from begin to finish
+ * (K = the draft's top-k, 1..32; depth = levels, 1..16; the reference uses K = 5,
+ * depth 4).  d2t: int32 [Vd] draft-to-target offsets (token = id + d2t[id]).
+ *   begin:  the root row [Vd]: its top K ids (topk), their log-softmax (the
+ *           level's scores), out_input_ids [K] = their tokens.
+ *   grow:   level = 1 .. depth-1, logits [K][Vd] (row stride row_stride): each
+ *           row's top K and log-softmax plus that row's score, the best K of the
+ *           K*K cumulative scores (topk); out_input_ids [K] their tokens,
+ *           out_parent_rows [K] (nullable) their rows, out_mask (nullable,
+ *           fp32 [K][K*(level+1)]) the draft attention mask for the next level.
+ *   finish: after the depth-1 grow calls: the best total_tokens (1..32) node
+ *           scores; out_tokens [N] (N = total_tokens + 1: sample_token, then the
+ *           survivors' tokens in node order), out_tree_mask fp32 [N][N],
+ *           out_position_ids [N], out_retrieve [N][N] (leaf paths from the
+ *           root, -1 padded), out_dims [2] = {leaf paths, columns used}.
+ * log-softmax uses exp and log rounded once from double (the correctly rounded
+ * values; the reference's C library expf/logf agree on all but rare arguments). */
+size_t llima_eagle3_tree_bytes(int32_t K, int32_t depth);
+int llima_eagle3_tree_begin(const void* logits, int32_t dtype, int32_t Vd, const int32_t* d2t,
+                            int32_t K, int32_t depth, void* tree, size_t tree_bytes,
+                            int32_t* out_input_ids, void* stream);
+int llima_eagle3_tree_grow(const void* logits, int32_t dtype, int32_t Vd, int64_t row_stride,
+                           const int32_t* d2t, int32_t K, int32_t depth, int32_t level,
+                           void* tree, size_t tree_bytes, int32_t* out_input_ids,
+                           int32_t* out_parent_rows, float* out_mask, void* stream);
+int llima_eagle3_tree_finish(void* tree, size_t tree_bytes, int32_t K, int32_t depth,
+                             int32_t total_tokens, int32_t sample_token, int32_t* out_tokens,
+                             float* out_tree_mask, int32_t* out_position_ids,
+                             int32_t* out_retrieve, int32_t* out_dims, void* stream);
 
 const char* llima_status_string(int status);
 int llima_abi_version(void);

@@ -53,6 +53,14 @@ SIGNATURES = {
     "llima_lm_head_argmax_workspace_bytes": (_sz, [_i32, _i32]),
     "llima_lm_head_argmax": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _vp, _vp,
                                             _vp, _vp, _sz, _vp]),
+    "llima_topk": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _i32, _vp, _vp, _vp]),
+    "llima_eagle3_tree_bytes": (_sz, [_i32, _i32]),
+    "llima_eagle3_tree_begin": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp,
+                                               _vp]),
+    "llima_eagle3_tree_grow": (ctypes.c_int, [_vp, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp,
+                                              _sz, _vp, _vp, _vp, _vp]),
+    "llima_eagle3_tree_finish": (ctypes.c_int, [_vp, _sz, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                                _vp, _vp, _vp]),
     "llima_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "llima_abi_version": (ctypes.c_int, []),
 }

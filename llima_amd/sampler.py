@@ -16,6 +16,8 @@ the buffers handed to it (inputs must already be on the GPU).
   score_logits(logits, target)        language_model.cpp:29-62
   select_candidate_tokens(...)        gemma4_mtp_helpers.cpp:113-167
   argmax_gemma4_mtp_masked_row(s)     language_model_gemma4_mtp.cpp:31-97
+  topk(x, k)                          utils.hpp:216-281
+  Eagle3DraftTree                     language_model_eagle3.cpp:808-1164 (topk_generate's selection)
 
 Errors: the reference throws std::invalid_argument / std::runtime_error; here
 ValueError / RuntimeError are raised for the same conditions.
@@ -36,7 +38,7 @@ __all__ = [
     "spec_path_argmax",
     "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
     "Workspace", "score_logits", "select_candidate_tokens", "argmax_gemma4_mtp_masked_rows",
-    "argmax_gemma4_mtp_masked_row",
+    "argmax_gemma4_mtp_masked_row", "topk", "Eagle3DraftTree",
 ]
 
 
@@ -548,3 +550,102 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 
                                      ids.data_ptr(), vals.data_ptr(), _ptr(logits), ws.data_ptr(),
                                      ws.numel(), _stream(dev)), "llima_lm_head_argmax")
     return (ids, vals, logits) if return_logits else (ids, vals)
+
+
+def topk(x: torch.Tensor, k: int):
+    """topk<T> (utils.hpp:216-281) over the rows of x ([cols] or [rows, cols],
+    fp32 or bf16) -> (indices int32 [rows, k], values float32 [rows, k]) in the
+    reference heap's output order, ties included.  k in [1, 32]."""
+    single = x.dim() == 1
+    a = _rows2d(x)
+    _on_gpu(a)
+    rows, cols = a.shape
+    if not 1 <= k <= 32:
+        raise RuntimeError("topk: k out of supported range [1, 32]")
+    if cols < k:
+        raise ValueError("topk needs at least k values per row")
+    idx = torch.empty((rows, k), dtype=torch.int32, device=a.device)
+    val = torch.empty((rows, k), dtype=torch.float32, device=a.device)
+    check(lib().llima_topk(a.data_ptr(), _dtype_code(a), rows, cols, a.stride(0), k,
+                           idx.data_ptr(), val.data_ptr(), _stream(a.device)), "llima_topk")
+    return (idx[0], val[0]) if single else (idx, val)
+
+
+class Eagle3DraftTree:
+    """The selection side of the EAGLE3 draft tree (topk_generate,
+    language_model_eagle3.cpp:808-1164) on the GPU.  The draft model runs
+    between the calls:
+
+        tree = Eagle3DraftTree(d2t, topk=5, depth=4)
+        ids = tree.begin(root_logits)              # [Vd] -> first draft inputs [K]
+        for level in range(1, depth):
+            ids, parent_rows, mask = tree.grow(draft_logits)   # [K, Vd]
+        out = tree.finish(total_tokens=15, sample_token=tok)
+
+    finish returns the draft tokens [N], tree mask [N, N], position ids [N]
+    and retrieve indices [leaves, columns] (N = total_tokens + 1)."""
+
+    def __init__(self, d2t: torch.Tensor, topk: int = 5, depth: int = 4):
+        self.d2t = d2t.to(dtype=torch.int32).contiguous()
+        _on_gpu(self.d2t)
+        self.K, self.depth = int(topk), int(depth)
+        nb = lib().llima_eagle3_tree_bytes(self.K, self.depth)
+        if nb == 0:
+            raise ValueError("topk must be 1..32 and depth 1..16 (at most 16384 nodes)")
+        self.dev = self.d2t.device
+        self.state = torch.empty(nb, dtype=torch.uint8, device=self.dev)
+        self.level = 0
+
+    def _logits(self, x, rows):
+        a = _rows2d(x)
+        _on_gpu(a)
+        if a.shape[0] != rows:
+            raise ValueError(f"expected {rows} logits rows, got {a.shape[0]}")
+        if a.shape[1] > self.d2t.numel():
+            raise ValueError("d2t must hold an offset for every draft id")
+        return a
+
+    def begin(self, root_logits: torch.Tensor) -> torch.Tensor:
+        a = self._logits(root_logits.reshape(1, -1), 1)
+        ids = torch.empty(self.K, dtype=torch.int32, device=self.dev)
+        check(lib().llima_eagle3_tree_begin(a.data_ptr(), _dtype_code(a), a.shape[1],
+                                            self.d2t.data_ptr(), self.K, self.depth,
+                                            self.state.data_ptr(), self.state.numel(),
+                                            ids.data_ptr(), _stream(self.dev)),
+              "llima_eagle3_tree_begin")
+        self.level = 1
+        return ids
+
+    def grow(self, logits: torch.Tensor):
+        if not 1 <= self.level < self.depth:
+            raise RuntimeError("grow: begin first, and at most depth - 1 levels")
+        a = self._logits(logits, self.K)
+        ids = torch.empty(self.K, dtype=torch.int32, device=self.dev)
+        prow = torch.empty(self.K, dtype=torch.int32, device=self.dev)
+        mask = torch.empty((self.K, self.K * (self.level + 1)), dtype=torch.float32,
+                           device=self.dev)
+        check(lib().llima_eagle3_tree_grow(a.data_ptr(), _dtype_code(a), a.shape[1], a.stride(0),
+                                           self.d2t.data_ptr(), self.K, self.depth, self.level,
+                                           self.state.data_ptr(), self.state.numel(),
+                                           ids.data_ptr(), prow.data_ptr(), mask.data_ptr(),
+                                           _stream(self.dev)), "llima_eagle3_tree_grow")
+        self.level += 1
+        return ids, prow, mask
+
+    def finish(self, total_tokens: int, sample_token: int):
+        if self.level != self.depth:
+            raise RuntimeError("finish: grow depth - 1 levels first")
+        N = int(total_tokens) + 1
+        tok = torch.empty(N, dtype=torch.int32, device=self.dev)
+        tmask = torch.empty((N, N), dtype=torch.float32, device=self.dev)
+        pos = torch.empty(N, dtype=torch.int32, device=self.dev)
+        ret = torch.empty((N, N), dtype=torch.int32, device=self.dev)
+        dims = torch.empty(2, dtype=torch.int32, device=self.dev)
+        check(lib().llima_eagle3_tree_finish(self.state.data_ptr(), self.state.numel(), self.K,
+                                             self.depth, int(total_tokens), int(sample_token),
+                                             tok.data_ptr(), tmask.data_ptr(), pos.data_ptr(),
+                                             ret.data_ptr(), dims.data_ptr(), _stream(self.dev)),
+              "llima_eagle3_tree_finish")
+        leaves, cols = dims.tolist()
+        return dict(tokens=tok, tree_mask=tmask, position_ids=pos,
+                    retrieve=ret[:leaves, :cols])

@@ -430,19 +430,17 @@ int orc_verify_greedy(const void* target_logits, int dtype, int B, int D, int V,
 int orc_evaluate_posterior(const int32_t* next_ids, const int32_t* candidates, int n_paths,
                            int L, int32_t* best, int32_t* accept_len, int32_t* bonus) {
     if (n_paths <= 0 || L <= 0) return ORC_E_INVAL;
-    int32_t max_acc = 0, best_c = 0;
-    for (int c = 0; c < n_paths; ++c) {
-        int32_t acc = 0;
-        for (int i = 0; i + 1 < L; ++i) {
-            int32_t arg = next_ids[c * L + i], nxt = candidates[c * L + i + 1];
-            if (nxt < 0 || arg != nxt) break;
-            ++acc;
-        }
-        if (acc > max_acc) { max_acc = acc; best_c = c; }
+    int32_t win_path = 0, win_len = 0;
+    for (int p = 0; p < n_paths; ++p) {
+        const int32_t* tgt = next_ids + (size_t)p * L;     // target token after position i
+        const int32_t* cnd = candidates + (size_t)p * L;   // the path's token at position i
+        int32_t len = 0;
+        while (len + 1 < L && cnd[len + 1] >= 0 && tgt[len] == cnd[len + 1]) ++len;
+        if (len > win_len) { win_len = len; win_path = p; }
     }
-    *best = best_c;
-    *accept_len = max_acc;
-    *bonus = next_ids[best_c * L + max_acc];
+    *best = win_path;
+    *accept_len = win_len;
+    *bonus = next_ids[(size_t)win_path * L + win_len];
     return ORC_OK;
 }
 
@@ -605,6 +603,228 @@ int orc_score_logits(const void* row, int dtype, int V, int32_t target, double* 
     for (int i = 0; i < V; ++i) s += std::exp((double)load_logit(row, dtype, i) - mx);
     *logprob = (double)load_logit(row, dtype, target) - (mx + std::log(s));
     *is_greedy_out = am == target;
+    return ORC_OK;
+}
+
+// ---------------------------------------------------------------- EAGLE3 draft tree
+// topk<T> (utils.hpp:216-281) on one row: a min-heap of the first k values
+// (heapified from the last parent down), a later value replaces the root only
+// when it is strictly greater, and sifts down to the smaller child (the right
+// one only when the left one is strictly greater; a parent equal to its
+// smaller child stays).  The output is a selection sort of the heap array:
+// position a takes the first strictly greatest remaining entry, whose slot
+// then receives entry a.  k in [1, 32] and cols >= k.
+}  // extern "C"
+
+template <typename Get>
+static void heap_topk(Get get, int64_t cols, int k, int32_t* out_idx, float* out_val) {
+    float hv[32];
+    int32_t hi[32];
+    for (int j = 0; j < k; ++j) { hv[j] = get(j); hi[j] = j; }
+    auto sift = [&](int node) {
+        for (;;) {
+            int c = 2 * node + 1;
+            if (c >= k) return;
+            if (c + 1 < k && hv[c] > hv[c + 1]) ++c;
+            if (!(hv[node] > hv[c])) return;
+            std::swap(hv[node], hv[c]);
+            std::swap(hi[node], hi[c]);
+            node = c;
+        }
+    };
+    for (int j = k / 2 - 1; j >= 0; --j) sift(j);
+    for (int64_t j = k; j < cols; ++j) {
+        const float v = get(j);
+        if (v > hv[0]) { hv[0] = v; hi[0] = (int32_t)j; sift(0); }
+    }
+    for (int a = 0; a < k; ++a) {
+        int m = a;
+        for (int b = a + 1; b < k; ++b)
+            if (hv[b] > hv[m]) m = b;
+        out_val[a] = hv[m];
+        out_idx[a] = hi[m];
+        hv[m] = hv[a];
+        hi[m] = hi[a];
+    }
+}
+
+extern "C" {
+
+int orc_topk(const void* x, int dtype, int rows, int64_t cols, int64_t row_stride, int k,
+             int32_t* out_idx, float* out_val) {
+    if (rows < 0 || k < 1 || k > 32 || cols < k || (dtype != 0 && dtype != 1)) return ORC_E_INVAL;
+    const size_t esz = dtype == 0 ? 4 : 2;
+    for (int r = 0; r < rows; ++r) {
+        const void* row = (const char*)x + (size_t)r * row_stride * esz;
+        heap_topk([&](int64_t i) { return load_logit(row, dtype, i); }, cols, k,
+                  out_idx + (size_t)r * k, out_val + (size_t)r * k);
+    }
+    return ORC_OK;
+}
+
+// logsoftmax<T> (utils.hpp:283-301) in float: the maximum, a running float sum
+// of exp(v - max) in index order, then v - (log(sum) + max).  cr = 0 uses the
+// C library's expf/logf as the reference does; cr = 1 uses exp and log of the
+// float argument in double rounded once to float (correctly rounded but for
+// double-rounding cases of probability ~2^-29), the arithmetic of the HIP path.
+static inline float orc_expf(float x, int cr) { return cr ? (float)std::exp((double)x) : std::exp(x); }
+static inline float orc_logf(float x, int cr) { return cr ? (float)std::log((double)x) : std::log(x); }
+
+int orc_logsoftmax(const float* v, int n, int cr, float* out) {
+    if (n <= 0) return ORC_E_INVAL;
+    float mx = -std::numeric_limits<float>::infinity();
+    for (int i = 0; i < n; ++i) mx = std::max(mx, v[i]);
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i) sum += orc_expf(v[i] - mx, cr);
+    const float shift = orc_logf(sum, cr) + mx;
+    for (int i = 0; i < n; ++i) out[i] = v[i] - shift;
+    return ORC_OK;
+}
+
+// searchsorted (eagle_helpers.hpp:197-214), left side: the first position whose
+// element is not less than q.
+static int32_t lower_pos(const int32_t* sorted, int n, int32_t q) {
+    return (int32_t)(std::lower_bound(sorted, sorted + n, q) - sorted);
+}
+
+// The selection side of the EAGLE3 draft tree (topk_generate,
+// language_model_eagle3.cpp:808-1164), given the draft logits of every level
+// (the draft model's forward passes between levels are the caller's):
+//   level 0: the top K ids of the root row, their log-softmax as the node
+//            scores, their d2t-mapped tokens, parent group 0;
+//   level i = 1 .. depth-1: the top K ids of each of the K rows, each row's
+//            log-softmax plus that row's score from the previous level (K*K
+//            cumulative scores and tokens appended to the node lists); the
+//            parent group of the level is (0, .., K-1) + 1 + K*K*max(0, i-2)
+//            + (i > 1 ? K : 0) -- the reference's loop declares a new
+//            topk_cs_index (:953) that hides the one its parent groups read
+//            (:867, :906-908), so those stay 0 .. K-1; the best K cumulative
+//            scores become the next scores, their rows (flat / K) the parent
+//            rows, their mapped tokens the next input ids, and the draft
+//            attention mask gains those rows of itself plus an identity block;
+//   finish:  the best total_tokens node scores, their positions sorted; the
+//            tokens there behind sample_token; each survivor's parent group
+//            entry (position / K) minus 1 located among the sorted positions
+//            (0 for the root group), + 1 -> mask_index; the tree mask is the
+//            identity plus column 0 with each row OR-ed with its parent row in
+//            order; position ids = row sums - 1; one retrieve row per node that
+//            is nobody's parent, walked back to the root.
+// logits are bf16 (dtype 1) or fp32 (0); level_logits holds depth-1 blocks of
+// [K][Vd].  Outputs: inputs [depth][K] (input ids after the root and after
+// each level), prow [depth-1][K] (parent rows), masks [depth-1][K][K*depth]
+// (the attention mask after each level, K*(i+2) columns used, rest 0),
+// tokens [N], mask [N][N], pos [N], retrieve [N][N] (-1 padded), dims =
+// {leaf rows, retrieve columns}, with N = total_tokens + 1.
+int orc_eagle3_tree(const void* root_logits, const void* level_logits, int dtype, int Vd,
+                    const int32_t* d2t, int K, int depth, int total_tokens, int32_t sample_token,
+                    int cr, int32_t* inputs, int32_t* prow, float* masks, int32_t* tokens,
+                    float* mask, int32_t* pos, int32_t* retrieve, int32_t* dims) {
+    if (K < 1 || K > 32 || depth < 1 || Vd < K || total_tokens < 1 || total_tokens > 32)
+        return ORC_E_INVAL;
+    const int n_nodes = K + (depth - 1) * K * K;
+    if (total_tokens > n_nodes) return ORC_E_INVAL;
+    const size_t esz = dtype == 0 ? 4 : 2;
+    auto map_tok = [&](int32_t draft_id) { return (int32_t)(draft_id + d2t[draft_id]); };
+    std::vector<float> node_score;
+    std::vector<int32_t> node_tok, parent_flat;
+    std::vector<float> cur(K);
+    std::vector<int32_t> idx(K * K), tmp_i(K);
+    std::vector<float> val(K * K), lp(K);
+    // level 0
+    heap_topk([&](int64_t i) { return load_logit(root_logits, dtype, i); }, Vd, K, idx.data(),
+              val.data());
+    orc_logsoftmax(val.data(), K, cr, cur.data());
+    for (int j = 0; j < K; ++j) {
+        node_score.push_back(cur[j]);
+        node_tok.push_back(map_tok(idx[j]));
+        inputs[j] = map_tok(idx[j]);
+    }
+    parent_flat.push_back(0);
+    // draft attention mask: K rows, starts as the K x K identity
+    const int mcols = K * depth;
+    std::vector<float> am((size_t)K * mcols, 0.0f);
+    for (int r = 0; r < K; ++r) am[(size_t)r * mcols + r] = 1.0f;
+    int acols = K;
+    for (int lv = 1; lv < depth; ++lv) {
+        const int i = lv - 1;                               // the reference's loop counter
+        const int32_t base = 1 + K * K * std::max(0, i - 1) + (i > 0 ? K : 0);
+        for (int j = 0; j < K; ++j) parent_flat.push_back(j + base);
+        const char* blk = (const char*)level_logits + (size_t)i * K * Vd * esz;
+        std::vector<float> cu((size_t)K * K);
+        for (int r = 0; r < K; ++r) {
+            const void* row = blk + (size_t)r * Vd * esz;
+            heap_topk([&](int64_t q) { return load_logit(row, dtype, q); }, Vd, K,
+                      idx.data() + (size_t)r * K, val.data() + (size_t)r * K);
+            orc_logsoftmax(val.data() + (size_t)r * K, K, cr, lp.data());
+            for (int j = 0; j < K; ++j) cu[(size_t)r * K + j] = lp[j] + cur[r];
+        }
+        std::vector<int32_t> best(K);
+        std::vector<float> bestv(K);
+        heap_topk([&](int64_t q) { return cu[q]; }, (int64_t)K * K, K, best.data(), bestv.data());
+        for (int j = 0; j < K; ++j) {
+            cur[j] = bestv[j];
+            prow[(size_t)i * K + j] = best[j] / K;
+            inputs[(size_t)lv * K + j] = map_tok(idx[best[j]]);
+        }
+        for (int q = 0; q < K * K; ++q) {
+            node_score.push_back(cu[q]);
+            node_tok.push_back(map_tok(idx[q]));
+        }
+        std::vector<float> nm((size_t)K * mcols, 0.0f);
+        for (int r = 0; r < K; ++r) {
+            const int src = best[r] / K;
+            for (int c = 0; c < acols; ++c) nm[(size_t)r * mcols + c] = am[(size_t)src * mcols + c];
+            nm[(size_t)r * mcols + acols + r] = 1.0f;
+        }
+        acols += K;
+        am.swap(nm);
+        std::copy(am.begin(), am.end(), masks + (size_t)i * K * mcols);
+    }
+    // finish
+    std::vector<int32_t> sel(total_tokens);
+    std::vector<float> selv(total_tokens);
+    heap_topk([&](int64_t q) { return node_score[q]; }, n_nodes, total_tokens, sel.data(),
+              selv.data());
+    std::sort(sel.begin(), sel.end());
+    const int N = total_tokens + 1;
+    tokens[0] = sample_token;
+    std::vector<int32_t> up(total_tokens);                 // mask_index
+    for (int q = 0; q < total_tokens; ++q) {
+        tokens[q + 1] = node_tok[sel[q]];
+        const int32_t par = parent_flat[sel[q] / K];
+        up[q] = (par == 0 ? -1 : lower_pos(sel.data(), total_tokens, par - 1)) + 1;
+    }
+    std::vector<int> tm((size_t)N * N, 0);
+    for (int r = 0; r < N; ++r) { tm[(size_t)r * N + r] = 1; tm[(size_t)r * N] = 1; }
+    for (int q = 0; q < total_tokens; ++q)
+        for (int c = 0; c < N; ++c) tm[(size_t)(q + 1) * N + c] |= tm[(size_t)up[q] * N + c];
+    int maxpos = 0;
+    for (int r = 0; r < N; ++r) {
+        int sum = 0;
+        for (int c = 0; c < N; ++c) { sum += tm[(size_t)r * N + c]; mask[(size_t)r * N + c] = (float)tm[(size_t)r * N + c]; }
+        pos[r] = sum - 1;
+        maxpos = std::max(maxpos, pos[r]);
+    }
+    const int rcols = maxpos + 1;
+    std::vector<char> is_parent(N, 0);
+    for (int q = 0; q < total_tokens; ++q) is_parent[up[q]] = 1;
+    int n_parent = 0;
+    for (int r = 0; r < N; ++r) n_parent += is_parent[r];
+    const int leaves = total_tokens - (n_parent - 1);
+    for (int q = 0; q < N * N; ++q) retrieve[q] = -1;
+    int row = 0;
+    for (int node = 0; node < N; ++node) {
+        if (is_parent[node]) continue;
+        if (row >= leaves) return ORC_E_RANGE;              // cannot happen: see dims
+        int at = node;
+        for (int j = pos[node]; j >= 0; --j) {
+            retrieve[(size_t)row * N + j] = at;
+            if (at > 0) at = up[at - 1];
+        }
+        ++row;
+    }
+    dims[0] = leaves;
+    dims[1] = rcols;
     return ORC_OK;
 }
 

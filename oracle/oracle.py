@@ -279,3 +279,64 @@ def f32_to_bf16_bits(x):
 
 def bf16_bits_to_f32(h):
     return (np.ascontiguousarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def topk(x, k: int):
+    """topk<T> (utils.hpp:216-281): heap top-k per row -> (indices int32
+    [rows, k], values float32 [rows, k]) in the heap's output order."""
+    a, dt = _logits(x)
+    a2 = a.reshape(-1, a.shape[-1])
+    rows, cols = a2.shape
+    idx = np.empty((rows, k), np.int32)
+    val = np.empty((rows, k), np.float32)
+    rc = lib().orc_topk(_ptr(a2), dt, rows, ctypes.c_int64(cols), ctypes.c_int64(cols), k,
+                        _ptr(idx), _ptr(val))
+    if rc:
+        raise ValueError(f"orc_topk rc={rc}")
+    return idx.reshape(a.shape[:-1] + (k,)), val.reshape(a.shape[:-1] + (k,))
+
+
+def logsoftmax(values, cr: bool = False):
+    """logsoftmax<T> (utils.hpp:283-301) in float; cr selects exp/log rounded
+    once from double (the HIP path's arithmetic) instead of the C library's."""
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    out = np.empty_like(v)
+    rc = lib().orc_logsoftmax(_ptr(v), len(v), int(cr), _ptr(out))
+    if rc:
+        raise ValueError(f"orc_logsoftmax rc={rc}")
+    return out
+
+
+def eagle3_tree(root_logits, level_logits, d2t, K: int, depth: int, total_tokens: int,
+                sample_token: int, cr: bool = True):
+    """The selection side of the EAGLE3 draft tree (language_model_eagle3.cpp:
+    808-1164).  root_logits [Vd], level_logits [depth-1, K, Vd] (float32 or
+    bf16 bits), d2t int32 [Vd].  Returns a dict of the per-level input ids and
+    parent rows, the draft masks, and the final tokens, tree mask, position
+    ids and retrieve indices."""
+    r, dt = _logits(root_logits)
+    Vd = r.shape[-1]
+    if depth > 1:
+        lv, dt2 = _logits(level_logits)
+        assert dt2 == dt and lv.shape == (depth - 1, K, Vd)
+    else:
+        lv = np.zeros((1, K, Vd), r.dtype)
+    d = np.ascontiguousarray(d2t, np.int32)
+    N = total_tokens + 1
+    inputs = np.zeros((depth, K), np.int32)
+    prow = np.zeros((max(depth - 1, 1), K), np.int32)
+    masks = np.zeros((max(depth - 1, 1), K, K * depth), np.float32)
+    tokens = np.zeros(N, np.int32)
+    mask = np.zeros((N, N), np.float32)
+    pos = np.zeros(N, np.int32)
+    retrieve = np.zeros((N, N), np.int32)
+    dims = np.zeros(2, np.int32)
+    rc = lib().orc_eagle3_tree(_ptr(r), _ptr(lv), dt, Vd, _ptr(d), K, depth, total_tokens,
+                               int(sample_token), int(cr), _ptr(inputs), _ptr(prow), _ptr(masks),
+                               _ptr(tokens), _ptr(mask), _ptr(pos), _ptr(retrieve), _ptr(dims))
+    if rc:
+        raise ValueError(f"orc_eagle3_tree rc={rc}")
+    leaves, rcols = int(dims[0]), int(dims[1])
+    return dict(inputs=inputs, parent_rows=prow[:depth - 1], masks=masks[:depth - 1],
+                tokens=tokens, tree_mask=mask, position_ids=pos,
+                retrieve=retrieve[:leaves, :rcols])
