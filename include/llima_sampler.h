@@ -53,6 +53,10 @@
  *                            sima_lmm/devkit/cpp/language_model_eagle3.cpp:808-1164,
  *                            sima_lmm/devkit/cpp/utils.hpp:283-301,
  *                            sima_lmm/devkit/cpp/eagle_helpers.hpp:197-214
+ *   llima_stop_check      <- the decode loop's stop-token check
+ *                            sima_lmm/devkit/cpp/language_model.cpp:643-671,
+ *                            language_model_dflash.cpp:570-579,
+ *                            language_model_gemma4_mtp.cpp:940-956
  *   llima_lm_head_argmax  <- the in-graph LM head + softcap + argmax
  *                            sima_lmm/model/language_part_base.py:171-180,
  *                            sima_lmm/model/model_graph.py:601, 868-870, whose
@@ -283,18 +287,22 @@ int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_st
 /* LM head with a fused softcap and argmax, for decode-sized batches: for each
  * of B hidden rows (bf16 [B][H], 16-byte aligned) and V vocab rows of the
  * weight (bf16 [V][H], the nn.Linear layout, 16-byte aligned),
- *   logit = softcap * tanh(s / softcap)  (s when softcap <= 0),
- *   s = sum_h hidden[b][h] * weight[v][h]  in fp32;
- * out_ids[B] = first index of the maximum logit (NaN never wins; a row with
- * no non-NaN logit gives 0), out_vals[B] (nullable) its value, out_logits
- * (nullable, fp32 [B][V]) every logit.  H % 8 == 0, and H <= 4096 unless
- * H % 64 == 0 (then H <= 65536).  The weights are read once per 8 hidden rows
- * (H <= 2048) or 4 (H <= 4096); wider batches, and rows wider than 4096, use
- * MFMA tiles that read them once per 64 rows (H % 64 == 0). */
+ *   logit = round(softcap * tanh(s / softcap))  (s when softcap <= 0),
+ *   s = sum_h hidden[b][h] * weight[v][h]  in fp32,
+ * where round is to the nearest bf16 (ties to even) for logit_dtype
+ * LLIMA_BF16 -- the precision of the reference's executed graphs
+ * (sima_lmm/model/model_graph.py:30-45), so logits equal in bf16 tie and the
+ * lower index wins -- and none for LLIMA_F32.  out_ids[B] = first index of the
+ * maximum logit (NaN never wins; a row with no non-NaN logit gives 0),
+ * out_vals[B] (nullable) its value, out_logits (nullable, fp32 [B][V]) every
+ * logit.  H % 8 == 0, and H <= 4096 unless H % 64 == 0 (then H <= 65536).  The
+ * weights are read once per 8 hidden rows (H <= 2048) or 4 (H <= 4096); wider
+ * batches, and rows wider than 4096, use MFMA tiles that read them once per 64
+ * rows (H % 64 == 0). */
 size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V);
 int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
-                         float softcap, int32_t* out_ids, float* out_vals, float* out_logits,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         float softcap, int32_t logit_dtype, int32_t* out_ids, float* out_vals,
+                         float* out_logits, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
  * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):
@@ -337,6 +345,19 @@ int llima_eagle3_tree_finish(void* tree, size_t tree_bytes, int32_t K, int32_t d
                              int32_t total_tokens, int32_t sample_token, int32_t* out_tokens,
                              float* out_tree_mask, int32_t* out_position_ids,
                              int32_t* out_retrieve, int32_t* out_dims, void* stream);
+
+/* Stop-token check of B sequences' newly emitted tokens [B][M] (count[B]
+ * valid per sequence, nullable: all M), as the reference's decode loops do it:
+ * the run is cut at room[b] tokens (the cache space left; nullable: no cap) and
+ * after its first token in the stop set, which is kept.  stop_mask: the stop
+ * set as a bitmask over V ids ([ceil(V/32)] uint32, bit id & 31 of word id >> 5,
+ * LSB first); ids outside [0, V) never stop.  out_keep[B]: tokens to keep;
+ * out_status[B] (nullable): LLIMA_STOP_TOKEN when a stop token ended the run,
+ * else LLIMA_STOP_CACHE_FULL when room cut it, else LLIMA_STOP_NONE. */
+enum { LLIMA_STOP_NONE = 0, LLIMA_STOP_TOKEN = 1, LLIMA_STOP_CACHE_FULL = 2 };
+int llima_stop_check(const int32_t* tokens, const int32_t* count, int32_t B, int32_t M,
+                     const uint32_t* stop_mask, int32_t V, const int32_t* room,
+                     int32_t* out_keep, int32_t* out_status, void* stream);
 
 const char* llima_status_string(int status);
 int llima_abi_version(void);

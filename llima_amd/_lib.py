@@ -16,6 +16,7 @@ LLIMA_E_SCRATCH = -5
 LLIMA_F32, LLIMA_BF16 = 0, 1
 ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS, ARGMAX_LOWEST = 0, 1, 2, 3
 MAX_SPLITS = 16
+STOP_NONE, STOP_TOKEN, STOP_CACHE_FULL = 0, 1, 2
 
 # name -> (restype, argtypes) for every entry point of include/llima_sampler.h
 _vp, _sz, _i32, _i64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int64
@@ -51,8 +52,8 @@ SIGNATURES = {
     "llima_mtp_masked_argmax": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _i32, _i32, _i32,
                                                _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "llima_lm_head_argmax_workspace_bytes": (_sz, [_i32, _i32]),
-    "llima_lm_head_argmax": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _vp, _vp,
-                                            _vp, _vp, _sz, _vp]),
+    "llima_lm_head_argmax": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _i32, _vp,
+                                            _vp, _vp, _vp, _sz, _vp]),
     "llima_topk": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _i32, _vp, _vp, _vp]),
     "llima_eagle3_tree_bytes": (_sz, [_i32, _i32]),
     "llima_eagle3_tree_begin": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp,
@@ -61,6 +62,7 @@ SIGNATURES = {
                                               _sz, _vp, _vp, _vp, _vp]),
     "llima_eagle3_tree_finish": (ctypes.c_int, [_vp, _sz, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
                                                 _vp, _vp, _vp]),
+    "llima_stop_check": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp]),
     "llima_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "llima_abi_version": (ctypes.c_int, []),
 }

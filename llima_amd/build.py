@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libllima_sampler.so")
-SOURCES = ["argmax.hip", "sample.hip", "verify.hip", "score.hip", "lmhead.hip", "tree.hip"]
+SOURCES = ["argmax.hip", "sample.hip", "verify.hip", "score.hip", "lmhead.hip", "tree.hip", "stop.hip"]
 ARCH = os.environ.get("LLIMA_OFFLOAD_ARCH", "gfx950")
 
 

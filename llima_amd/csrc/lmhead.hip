@@ -43,7 +43,21 @@ struct LmhParams {
     float* out_vals;                   // or null
     int32_t B, H, V, NW;
     float cap;
+    int32_t round_bf16;                // logits rounded to bf16 before the argmax
 };
+
+// The logit as the argmax sees it: softcapped, then (round_bf16) rounded to
+// the nearest bf16, ties to even (NaN stays NaN), the precision of the
+// reference's executed graphs (model_graph.py:30-45), in which equal bf16
+// logits tie and the lower index wins.
+__device__ __forceinline__ float lmh_logit(float s, const LmhParams& P) {
+    if (P.cap > 0.0f) s = P.cap * tanhf(s / P.cap);
+    if (P.round_bf16 && s == s) {
+        const uint32_t u = __float_as_uint(s);
+        s = __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+    }
+    return s;
+}
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
     return __uint_as_float(wave_reduce<uint32_t>(
@@ -120,8 +134,7 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float s = wave_sum_f32(acc[b]);
-            if (P.cap > 0.0f) s = P.cap * tanhf(s / P.cap);
+            const float s = lmh_logit(wave_sum_f32(acc[b]), P);
             if (b < nb && P.out_logits && lane == 0) P.out_logits[(size_t)(b0 + b) * P.V + v] = s;
             const uint64_t key = s == s ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)v : 0ull;
             best[b] = key > best[b] ? key : best[b];
@@ -249,8 +262,7 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_mfma(LmhParams P, int b0, int nb
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-            float v = acc[mt][i];
-            if (P.cap > 0.0f) v = P.cap * tanhf(v / P.cap);
+            const float v = lmh_logit(acc[mt][i], P);
             if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
             const uint64_t best = half_max_u64(lmh_key(v, n, V));
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
@@ -319,13 +331,14 @@ extern "C" size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V) {
 }
 
 extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H,
-                                    int32_t V, float softcap, int32_t* out_ids, float* out_vals,
-                                    float* out_logits, void* workspace, size_t workspace_bytes,
-                                    void* stream) {
+                                    int32_t V, float softcap, int32_t logit_dtype,
+                                    int32_t* out_ids, float* out_vals, float* out_logits,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
     if (B < 0 || H <= 0 || V <= 0 || H % 8 != 0) return LLIMA_E_INVAL;
     if (H > LMH_MAX_H && (H > 65536 || H % LMH_KC != 0)) return LLIMA_E_INVAL;   // MFMA path only
     if (!weight || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
     if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
+    if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
     if ((uintptr_t)weight % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_lm_head_argmax_workspace_bytes(B, V))
@@ -340,6 +353,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.B = B; P.H = H; P.V = V;
     P.NW = lmh_waves(V);
     P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
     hipStream_t st = (hipStream_t)stream;
     if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
         P.NW = lmh_mfma_waves(V);
@@ -351,7 +365,9 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
         hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
         return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
     }
-    const int nbp = lmh_rows_per_pass(H);
+    // rows per pass: what H allows, but no more than the batch fills
+    int nbp = lmh_rows_per_pass(H);
+    while (nbp > 1 && nbp / 2 >= B) nbp /= 2;
     const dim3 g((uint32_t)((P.NW + LMH_WAVES - 1) / LMH_WAVES)), blk(LMH_WG);
     for (int b0 = 0; b0 < B; b0 += nbp) {
         const int nb = B - b0 < nbp ? B - b0 : nbp;

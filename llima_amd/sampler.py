@@ -17,6 +17,7 @@ the buffers handed to it (inputs must already be on the GPU).
   select_candidate_tokens(...)        gemma4_mtp_helpers.cpp:113-167
   argmax_gemma4_mtp_masked_row(s)     language_model_gemma4_mtp.cpp:31-97
   topk(x, k)                          utils.hpp:216-281
+  stop_check(tokens, stop_mask, V)    language_model.cpp:643-671 (the decode loops' stop rule)
   Eagle3DraftTree                     language_model_eagle3.cpp:808-1164 (topk_generate's selection)
 
 Errors: the reference throws std::invalid_argument / std::runtime_error; here
@@ -26,6 +27,8 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
+
+import numpy as np
 from typing import Optional
 
 import torch
@@ -38,7 +41,7 @@ __all__ = [
     "spec_path_argmax",
     "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
     "Workspace", "score_logits", "select_candidate_tokens", "argmax_gemma4_mtp_masked_rows",
-    "argmax_gemma4_mtp_masked_row", "topk", "Eagle3DraftTree",
+    "argmax_gemma4_mtp_masked_row", "topk", "Eagle3DraftTree", "stop_mask", "stop_check",
 ]
 
 
@@ -525,15 +528,19 @@ def argmax_gemma4_mtp_masked_row(centroid_logits: torch.Tensor, token_ordering, 
 
 
 def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 0.0,
-                   return_logits: bool = False):
+                   return_logits: bool = False, logit_dtype: str = "bf16"):
     """LM head + softcap + argmax, as the reference's graph computes them before
     the host reads one int32 (language_part_base.py:171-180,
     language_model.cpp:1607-1609): hidden bf16 [B, H] (or [H]), weight bf16
     [V, H] -> (ids int32 [B], values float32 [B]) and, if return_logits, the
-    fp32 logits [B, V]."""
+    float32 logits [B, V].  logit_dtype "bf16" rounds each logit to bf16
+    before the argmax, as the reference's bf16 graphs produce them (equal bf16
+    logits tie, the lower index wins); "f32" keeps the fp32 sums."""
     x = hidden.reshape(1, -1) if hidden.dim() == 1 else hidden
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise ValueError("lm_head_argmax takes bf16 hidden states and weights")
+    if logit_dtype not in ("bf16", "f32"):
+        raise ValueError("logit_dtype must be 'bf16' or 'f32'")
     x = x.contiguous()
     w = weight.contiguous()
     B, H = x.shape
@@ -546,7 +553,8 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 
     vals = torch.empty(B, dtype=torch.float32, device=dev)
     logits = torch.empty((B, V), dtype=torch.float32, device=dev) if return_logits else None
     ws = Workspace.get(dev, "lm_head", lib().llima_lm_head_argmax_workspace_bytes(B, V))
-    check(lib().llima_lm_head_argmax(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap),
+    ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
+    check(lib().llima_lm_head_argmax(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap), ld,
                                      ids.data_ptr(), vals.data_ptr(), _ptr(logits), ws.data_ptr(),
                                      ws.numel(), _stream(dev)), "llima_lm_head_argmax")
     return (ids, vals, logits) if return_logits else (ids, vals)
@@ -649,3 +657,41 @@ class Eagle3DraftTree:
         leaves, cols = dims.tolist()
         return dict(tokens=tok, tree_mask=tmask, position_ids=pos,
                     retrieve=ret[:leaves, :cols])
+
+
+def stop_mask(stop_token_ids, V: int, device) -> torch.Tensor:
+    """The stop set as the [ceil(V/32)] bitmask llima_stop_check reads (ids
+    outside [0, V) are dropped: they never stop)."""
+    words = np.zeros((V + 31) // 32, np.uint32)
+    for t in stop_token_ids:
+        t = int(t)
+        if 0 <= t < V:
+            words[t >> 5] |= np.uint32(1 << (t & 31))
+    return torch.from_numpy(words.view(np.int32)).to(device)
+
+
+def stop_check(tokens: torch.Tensor, stop: torch.Tensor, V: int,
+               count: Optional[torch.Tensor] = None, room: Optional[torch.Tensor] = None):
+    """The decode loops' stop rule (language_model.cpp:643-671,
+    language_model_dflash.cpp:570-579, language_model_gemma4_mtp.cpp:940-956)
+    on emitted tokens [B, M] (count [B] valid each, room [B] cache space left)
+    with the stop set as the bitmask of stop_mask -> (keep int32 [B],
+    status int32 [B]: STOP_NONE / STOP_TOKEN / STOP_CACHE_FULL)."""
+    t = tokens.to(dtype=torch.int32)
+    if t.dim() == 1:
+        t = t.unsqueeze(1)
+    t = t.contiguous()
+    B, M = t.shape
+    dev = t.device
+    c = None if count is None else count.to(device=dev, dtype=torch.int32).contiguous()
+    r = None if room is None else room.to(device=dev, dtype=torch.int32).contiguous()
+    m = stop.to(device=dev).contiguous()
+    if m.numel() != (V + 31) // 32:
+        raise ValueError("the stop mask must hold ceil(V / 32) words")
+    _on_gpu(t, c, r, m)
+    keep = torch.empty(B, dtype=torch.int32, device=dev)
+    status = torch.empty(B, dtype=torch.int32, device=dev)
+    check(lib().llima_stop_check(t.data_ptr(), _ptr(c), B, M, m.data_ptr(), V, _ptr(r),
+                                 keep.data_ptr(), status.data_ptr(), _stream(dev)),
+          "llima_stop_check")
+    return keep, status

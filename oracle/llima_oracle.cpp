@@ -47,6 +47,8 @@
 #include <numeric>
 #include <vector>
 
+#include <omp.h>
+
 typedef unsigned __int128 u128;
 
 extern "C" {
@@ -827,5 +829,65 @@ int orc_eagle3_tree(const void* root_logits, const void* level_logits, int dtype
     dims[1] = rcols;
     return ORC_OK;
 }
+
+// The decode loops' stop rule (language_model.cpp:643-671, language_model_dflash.cpp:
+// 570-579, language_model_gemma4_mtp.cpp:940-956): the emitted run, cut at the
+// cache room, ends after its first token in the stop set (kept).  status: 0
+// none, 1 stop token, 2 cut by the room.
+int orc_stop_check(const int32_t* tokens, const int32_t* count, int B, int M,
+                   const int32_t* stop_ids, int n_stop, const int32_t* room, int32_t* keep,
+                   int32_t* status) {
+    if (B < 0 || M < 0) return ORC_E_INVAL;
+    std::vector<int32_t> st(stop_ids, stop_ids + n_stop);
+    std::sort(st.begin(), st.end());
+    for (int b = 0; b < B; ++b) {
+        int n = count ? std::min(std::max(count[b], 0), M) : M;
+        int s = 0;
+        if (room && std::max(room[b], 0) < n) { n = std::max(room[b], 0); s = 2; }
+        int k = n;
+        for (int i = 0; i < n; ++i) {
+            if (std::binary_search(st.begin(), st.end(), tokens[(size_t)b * M + i])) {
+                k = i + 1;
+                s = 1;
+                break;
+            }
+        }
+        keep[b] = k;
+        status[b] = s;
+    }
+    return ORC_OK;
+}
+
+// _calc_next_token_id (language_model.cpp:3689-3714) in the reference's own
+// shape, for the CPU baseline of the greedy workloads: four OpenMP threads per
+// row, each the scalar argmax_bf16 loop (utils.hpp:140-151, the path on x86)
+// over a quarter, merged in a critical section from (values[0], 0).
+int orc_calc_next_token_id_omp4(const void* row, int dtype, int V, int32_t* out) {
+    if (V <= 0) return ORC_E_INVAL;
+    float best_value = load_logit(row, dtype, 0);
+    int64_t best_index = 0;
+#pragma omp parallel for num_threads(4)
+    for (int part = 0; part < 4; ++part) {
+        const int64_t begin = (int64_t)V * part / 4, end = (int64_t)V * (part + 1) / 4;
+        if (end > begin) {
+            float v;
+            int64_t i;
+            argmax_split(row, dtype, begin, end - begin, &v, &i);
+#pragma omp critical
+            {
+                if (v > best_value || (v == best_value && i < best_index)) {
+                    best_value = v;
+                    best_index = i;
+                }
+            }
+        }
+    }
+    *out = (int32_t)best_index;
+    return ORC_OK;
+}
+
+// Threads of the oracle's OpenMP loops over rows (the CPU baseline's 1-thread
+// and many-thread figures).
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 }  // extern "C"

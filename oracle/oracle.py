@@ -340,3 +340,35 @@ def eagle3_tree(root_logits, level_logits, d2t, K: int, depth: int, total_tokens
     return dict(inputs=inputs, parent_rows=prow[:depth - 1], masks=masks[:depth - 1],
                 tokens=tokens, tree_mask=mask, position_ids=pos,
                 retrieve=retrieve[:leaves, :rcols])
+
+
+def stop_check(tokens, stop_ids, count=None, room=None):
+    """The decode loops' stop rule -> (keep [B], status [B]: 0 none, 1 stop
+    token, 2 cut by the cache room)."""
+    t = np.ascontiguousarray(tokens, np.int32)
+    B, M = t.shape
+    st = np.ascontiguousarray(list(stop_ids), np.int32)
+    c = None if count is None else np.ascontiguousarray(count, np.int32)
+    r = None if room is None else np.ascontiguousarray(room, np.int32)
+    keep = np.empty(B, np.int32)
+    status = np.empty(B, np.int32)
+    rc = lib().orc_stop_check(_ptr(t), _ptr(c), B, M, _ptr(st), len(st), _ptr(r), _ptr(keep),
+                              _ptr(status))
+    if rc:
+        raise ValueError(f"orc_stop_check rc={rc}")
+    return keep, status
+
+
+def calc_next_token_id_omp4(row) -> int:
+    """_calc_next_token_id (language_model.cpp:3689-3714) with its four OpenMP
+    threads (CPU baseline of the greedy workloads)."""
+    x, dt = _logits(np.ascontiguousarray(row).reshape(-1))
+    out = ctypes.c_int32()
+    rc = lib().orc_calc_next_token_id_omp4(_ptr(x), dt, len(x), ctypes.byref(out))
+    if rc:
+        raise ValueError(f"orc_calc_next_token_id_omp4 rc={rc}")
+    return int(out.value)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))

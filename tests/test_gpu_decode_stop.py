@@ -1,0 +1,29 @@
+"""GPU parity of the decode loop's stop-token check (language_model.cpp:643-671,
+language_model_dflash.cpp:570-579, language_model_gemma4_mtp.cpp:940-956)
+against the oracle: kept counts and stop reasons bit for bit."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_stop_check_parity(gpu, oracle):
+    import torch
+    import llima_amd
+    print("[gpu-case] stop check", flush=True)
+    rng = np.random.default_rng(12)
+    V = 128256
+    stop = [128001, 128008, 128009, 7, 0]
+    for B, M in [(1, 1), (64, 1), (16, 8), (300, 16), (5, 0)]:
+        toks = rng.integers(-2, V + 3, size=(B, M)).astype(np.int32)
+        hit = rng.random((B, M)) < 0.08
+        toks[hit] = rng.choice(stop, hit.sum())
+        count = rng.integers(0, M + 2, B).astype(np.int32)
+        room = rng.integers(-1, M + 3, B).astype(np.int32)
+        mask = llima_amd.stop_mask(stop, V, gpu)
+        t = torch.from_numpy(toks).to(gpu)
+        for c, r in ((None, None), (count, None), (count, room)):
+            keep, status = llima_amd.stop_check(t, mask, V, None if c is None else torch.from_numpy(c),
+                                                None if r is None else torch.from_numpy(r))
+            ek, es = oracle.stop_check(toks, stop, count=c, room=r)
+            assert (keep.cpu().numpy() == ek).all() and (status.cpu().numpy() == es).all(), (B, M)

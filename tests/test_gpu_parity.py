@@ -871,13 +871,20 @@ def test_score_and_mtp_maximum_sizes(gpu, oracle):
 # so |logit - ref| <= (H/4 + 70) 2^-24 sum_h |x_h w_h| + 1e-6, plus 4e-6 |ref|
 # for the softcap's tanhf (x -> cap tanh(x / cap) is 1-Lipschitz).  The argmax is exact with respect to the
 # kernel's own logits: the first index of their maximum, NaN never wins.
-def _lm_head_check(ids, vals, logits, x, w, cap):
+def _lm_head_check(ids, vals, logits, x, w, cap, bf16=True):
+    """Logits against a float64 product of the same bf16 values: the fp32 sum's
+    error bound, plus half a bf16 ulp (2^-8 relative) when the logits are
+    rounded to bf16 (then they must be bf16 values); the argmax exact with
+    respect to the logits returned (first index, NaN never wins)."""
     xf = wl.bf16_bits_to_f32(x).astype(np.float64)
     wf = wl.bf16_bits_to_f32(w).astype(np.float64)
     s = xf @ wf.T
     ref = cap * np.tanh(s / cap) if cap > 0 else s
     H = x.shape[1]
     bound = (H / 4 + 70) * 2.0**-24 * (np.abs(xf) @ np.abs(wf).T) + 1e-6 + 4e-6 * np.abs(ref)
+    if bf16:
+        bound = bound * (1 + 2.0**-8) + 2.0**-8 * np.abs(ref)
+        assert ((logits.view(np.uint32) & 0xFFFF) == 0).all()
     fin = np.isfinite(ref)
     assert (np.abs(logits - ref)[fin] <= bound[fin]).all(), np.abs(logits - ref)[fin].max()
     for b in range(x.shape[0]):
@@ -904,11 +911,13 @@ def test_lm_head_argmax_parity(gpu, B, H, V, cap):
     rng = np.random.default_rng(B * 31 + H + V)
     x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
     w = wl.f32_to_bf16_bits(rng.normal(0, 1.0 / np.sqrt(H), (V, H)).astype(np.float32))
-    ids, vals, logits = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap,
-                                                 return_logits=True)
-    _lm_head_check(_np(ids), _np(vals), _np(logits), x, w, cap)
-    ids2, vals2 = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap)
-    assert (_np(ids2) == _np(ids)).all() and (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
+    for ld in ("bf16", "f32"):
+        ids, vals, logits = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap,
+                                                     return_logits=True, logit_dtype=ld)
+        _lm_head_check(_np(ids), _np(vals), _np(logits), x, w, cap, bf16=ld == "bf16")
+        ids2, vals2 = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap, logit_dtype=ld)
+        assert (_np(ids2) == _np(ids)).all()
+        assert (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
 
 
 def test_lm_head_argmax_ties_and_nan(gpu):
@@ -932,3 +941,33 @@ def test_lm_head_argmax_ties_and_nan(gpu):
     assert np.isnan(logits[1, 17]) and ids[1] != 17
     assert ids[2] == 0 and np.isnan(vals[2])
     _lm_head_check(ids[:2], vals[:2], logits[:2], x[:2], w, 0.0)
+
+
+def test_lm_head_argmax_bf16_ties(gpu):
+    """Two vocab rows whose fp32 logits differ but round to the same bf16
+    value: with bf16 logits (the reference's precision) the lower index wins;
+    with fp32 logits the larger sum wins."""
+    import llima_amd
+    _say("lm head bf16 ties")
+    rng = np.random.default_rng(8)
+    B, H, V = 2, 512, 4096
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    xf = wl.bf16_bits_to_f32(x).astype(np.float64)
+    wf = wl.bf16_bits_to_f32(wl.f32_to_bf16_bits(rng.normal(0, 0.02, (V, H)).astype(np.float32)))
+    top = wl.bf16_bits_to_f32(wl.f32_to_bf16_bits((wl.bf16_bits_to_f32(x[0]) * 0.05)))
+    wf[3000] = top                                           # row 0's maximum ...
+    wf[700] = top                                            # ... and a copy at a lower index
+    j = int(np.argmax(np.abs(xf[0])))
+    sign = 1.0 if xf[0, j] > 0 else -1.0
+    bits = wl.f32_to_bf16_bits(wf[3000:3001])
+    bits[0, j] = bits[0, j] + (1 if (sign > 0) == (wf[3000, j] >= 0) else -1)   # one bf16 ulp up
+    wf[3000] = wl.bf16_bits_to_f32(bits)[0]
+    w = wl.f32_to_bf16_bits(wf)
+    s = xf @ wl.bf16_bits_to_f32(w).astype(np.float64).T
+    assert s[0, 3000] > s[0, 700]
+    r = wl.bf16_bits_to_f32(wl.f32_to_bf16_bits(s[0, [700, 3000]].astype(np.float32)))
+    assert r[0] == r[1] and s[0].argmax() in (700, 3000)   # equal in bf16
+    ids_b, _ = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), logit_dtype="bf16")
+    ids_f, _ = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), logit_dtype="f32")
+    assert int(_np(ids_b)[0]) == 700
+    assert int(_np(ids_f)[0]) == 3000

@@ -454,3 +454,30 @@ def test_rejection_output_distribution_is_target(oracle):
     wts = np.repeat(pd, G * G) / (G * G)
     dist = np.array([wts[first == i].sum() for i in range(V)])
     assert np.abs(dist - pt).max() < 4.0 / G
+
+
+# ----------------------------------------------------------------- decode-loop stop rule
+def test_stop_check_reference_rule(oracle):
+    """language_model.cpp:656 (one token, kept and stopping),
+    language_model_dflash.cpp:570-579 (a run cut at the room, then after its
+    first stop token), hand-derived."""
+    stop = [2, 128001, 128009]
+    toks = np.array([[5, 7, 2, 9], [128009, 1, 1, 1], [4, 4, 4, 4], [4, 4, 2, 4], [-1, 3, 2, 0]],
+                    np.int32)
+    keep, status = oracle.stop_check(toks, stop)
+    assert list(keep) == [3, 1, 4, 3, 3] and list(status) == [1, 1, 0, 1, 1]
+    keep, status = oracle.stop_check(toks, stop, count=[4, 4, 2, 1, 4], room=[2, 9, 9, 9, 0])
+    assert list(keep) == [2, 1, 2, 1, 0] and list(status) == [2, 1, 0, 0, 2]
+
+
+def test_calc_next_token_id_omp4_matches_quarters_rule(oracle):
+    """The 4-thread restatement used as the greedy CPU baseline gives the
+    quarters rule's ids (language_model.cpp:3689-3714), NaN at a quarter start
+    included."""
+    rng = np.random.default_rng(1)
+    for V in [7, 151936, 262144]:
+        for rep in range(4):
+            x = wl.f32_to_bf16_bits(rng.integers(-5, 6, V).astype(np.float32))
+            if rep % 2:
+                x[V // 4] = 0x7FC0
+            assert oracle.calc_next_token_id_omp4(x) == oracle.argmax(x[None], mode=2)[0][0]
