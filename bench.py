@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many plain launches (for rocprofv3 counter runs)")
     return ap.parse_args()
@@ -98,7 +98,7 @@ def main():
         ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
         for x in hid:
             launches.append(lambda sp, x=x: check(L.llima_lm_head_argmax(
-                x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, ids_o.data_ptr(),
+                x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, ids_o.data_ptr(),
                 vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
         per = weight.numel() * 2
         alg_bytes = V * H * 2 + B * H * 2 + B * 8
@@ -212,6 +212,13 @@ def main():
         mask = None if w["bitmask"] is None else \
             torch.from_numpy(w["bitmask"].view(np.int32)).to(dev)
         u = torch.from_numpy(w["uniforms"]).to(dev)
+        # histories, masks and uniforms rotate with the logits (their own
+        # buffers per step, so no step finds them in a cache)
+        hists = [hist] + [None if hist is None else torch.roll(hist, i, 0).contiguous()
+                          for i in range(1, nbuf)]
+        masks = [mask] + [None if mask is None else torch.roll(mask, i, 0).contiguous()
+                          for i in range(1, nbuf)]
+        us = [u] + [torch.rand(u.shape, generator=g, device=dev) for _ in range(1, nbuf)]
         cfgd = dict(w["cfg"])
         if greedy_variant:
             cfgd = dict(greedy=True)
@@ -221,8 +228,6 @@ def main():
         nws = L.llima_sample_workspace_bytes(B, V, dt)
         ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
         cref = ctypes.byref(cfg)
-        hp = None if hist is None else hist.data_ptr()
-        mp = None if mask is None else mask.data_ptr()
         if argmax_only:
             nwa = L.llima_argmax_workspace_bytes(B, V, dt)
             wsa = torch.zeros(max(nwa, 1), dtype=torch.uint8, device=dev)
@@ -234,9 +239,10 @@ def main():
             kernel_names = ["argmax_sweep", "argmax_finish"]
             config = {"workload": name, "B": B, "V": V, "logits_dtype": "bf16" if is_bf16 else "fp32"}
         else:
-            for x in bufs:
-                launches.append(lambda sp, x=x: check(L.llima_sample(
-                    x.data_ptr(), dt, B, V, V, hp, None, H, mp, u.data_ptr(), cref,
+            for x, hh, mm, uu in zip(bufs, hists, masks, us):
+                launches.append(lambda sp, x=x, hh=hh, mm=mm, uu=uu: check(L.llima_sample(
+                    x.data_ptr(), dt, B, V, V, None if hh is None else hh.data_ptr(), None, H,
+                    None if mm is None else mm.data_ptr(), uu.data_ptr(), cref,
                     out_ids.data_ptr(), out_p.data_ptr(), None, ws.data_ptr(), nws, sp),
                     "llima_sample"))
             alg_bytes = lg.nbytes + (0 if hist is None else hist.numel() * 4) + \
@@ -353,15 +359,29 @@ def main():
 
 
 def cpu_baseline(name, w, seconds, greedy_variant):
-    """The CPU oracle (oracle/llima_oracle.cpp, OpenMP over rows) timed on a
-    bounded sample of the same workload on this host."""
+    """The CPU oracle (oracle/llima_oracle.cpp, built -O3 for x86-64-v3, OpenMP
+    over rows) timed on bounded samples of the same workload on this host, at
+    1 thread and at OMP_NUM_THREADS threads (the host's CPU share; every
+    core otherwise).  The greedy workloads run the reference's own shape: one
+    row at a time with four threads (_calc_next_token_id,
+    language_model.cpp:3689-3714).  `value` is the many-thread figure."""
     from oracle import oracle as orc
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
-    os.environ["OMP_NUM_THREADS"] = str(threads)
+    nproc = os.cpu_count() or 1
+    many = int(os.environ.get("OMP_NUM_THREADS", "0")) or nproc
     orc.lib()
-    t_end = time.time() + seconds
-    n_rows, reps = 0, 0
-    t0 = time.time()
+    leg = seconds / 2
+
+    def timed(fn, threads):
+        orc.set_threads(threads)
+        t0 = time.time()
+        n = reps = 0
+        while time.time() < t0 + leg or reps == 0:
+            n += fn()
+            reps += 1
+        return n / (time.time() - t0), reps, time.time() - t0
+
+    info = {"kind": "port", "cpu": _cpu_model(), "nproc": nproc,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
     if name.startswith("lm_head_argmax"):
         # numpy float32 matrix-vector products + argmax over a 16384-row slice
         # of a weight of the same shape, scaled to the full vocabulary
@@ -370,61 +390,89 @@ def cpu_baseline(name, w, seconds, greedy_variant):
         wt = (rng.standard_normal((nv, w["H"]), dtype=np.float32) * np.float32(w["H"] ** -0.5))
         xs = np.ascontiguousarray(w["hidden"].astype(np.uint32) << 16).view(np.float32)
         t0 = time.time()
-        while time.time() < t_end or reps == 0:
+        reps = 0
+        while time.time() < t0 + seconds or reps == 0:
             np.argmax(xs @ wt.T, axis=1)
             reps += 1
         dt = time.time() - t0
         full = dt * (w["V"] / nv) / reps                     # seconds per full-vocabulary call
-        return {"value": w["B"] / full, "unit": "rows/s", "cores": threads, "kind": "port",
-                "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + argmax (a %d-row slice of "
-                          "the vocabulary, scaled by V / %d), %.1f s" % (
-                              reps, w["B"], w["H"], nv, w["H"], nv, nv, dt),
-                "cpu": _cpu_model()}
+        info.update({"value": w["B"] / full, "unit": "rows/s", "cores": many,
+                     "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + argmax (a %d-row slice "
+                               "of the vocabulary, scaled by V / %d), %.1f s" % (
+                                   reps, w["B"], w["H"], nv, w["H"], nv, nv, dt)})
+        return info
     if name == "speculative":
-        while time.time() < t_end or reps == 0:
+        unit = "sequences/s"
+        B = w["target"].shape[0]
+
+        def fn():
             orc.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
                                  w["u_resample"])
-            n_rows += w["target"].shape[0]
-            reps += 1
-        unit = "sequences/s"
-        sample = f"{reps} x verify_rejection over the full [16,8,128256] batch"
+            return B
+        what = "verify_rejection over the full [16,8,128256] batch"
+        one_row = False
     elif name in ("score_bf16", "mtp_masked_argmax"):
-        # one row per call, as the reference's functions (single thread)
-        threads = 1
+        unit = "rows/s"
         lg = w["logits"]
-        while time.time() < t_end or reps == 0:
-            r = reps % lg.shape[0]
+        state = {"r": 0}
+
+        def fn():                        # one row per call, as the reference's functions
+            r = state["r"] % lg.shape[0]
+            state["r"] += 1
             if name == "score_bf16":
                 orc.score_logits(lg[r], int(w["targets"][r]))
             else:
                 cand = orc.select_candidate_tokens(w["centroids"][r], w["ordering"], w["top_k"])
                 orc.masked_argmax(lg[r], cand)
-            n_rows += 1
-            reps += 1
+            return 1
+        what = f"rows of the {list(lg.shape)} batch, one call per row"
+        one_row = True
+    elif name == "argmax_bf16" or greedy_variant:
         unit = "rows/s"
-        sample = f"{reps} rows of the {list(lg.shape)} batch, one call per row"
-    else:
         lg = w["logits"]
-        if name == "argmax_bf16":
-            # the same rows through the oracle's argmax (the reference's rule)
-            while time.time() < t_end or reps == 0:
-                orc.argmax(lg)
-                n_rows += lg.shape[0]
-                reps += 1
-        else:
-            cfg = orc.SamplerConfig(greedy=True) if greedy_variant else orc.SamplerConfig(**w["cfg"])
-            while time.time() < t_end or reps == 0:
-                orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])
-                n_rows += lg.shape[0]
-                reps += 1
+        state = {"r": 0}
+
+        def fn():                        # _calc_next_token_id: one row, four threads
+            r = state["r"] % lg.shape[0]
+            state["r"] += 1
+            orc.calc_next_token_id_omp4(lg[r])
+            return 1
+        what = f"rows of the {list(lg.shape)} batch, one _calc_next_token_id call (4 threads) per row"
+        one_row = True
+    else:
         unit = "rows/s"
-        sample = f"{reps} x the full {list(lg.shape)} batch"
-    dt = time.time() - t0
-    return {"value": n_rows / dt, "unit": unit, "cores": threads, "kind": "port",
-            "sample": sample + f", {dt:.1f} s", "cpu": _cpu_model()}
+        lg = w["logits"]
+        cfg = orc.SamplerConfig(**w["cfg"])
+
+        def fn():
+            orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])
+            return lg.shape[0]
+        what = f"the full {list(lg.shape)} batch"
+        one_row = False
+    if one_row:
+        v, reps, dt = timed(fn, 1)
+        info.update({"value": v, "unit": unit, "cores": 4 if "4 threads" in what else 1,
+                     "sample": f"{reps} {what}, {dt:.1f} s"})
+        return info
+    v1, r1, d1 = timed(fn, 1)
+    vm, rm, dm = timed(fn, many)
+    info.update({"value": vm, "unit": unit, "cores": many,
+                 "sample": f"{rm} x {what} at {many} threads, {dm:.1f} s",
+                 "single_thread": {"value": v1, "unit": unit, "cores": 1,
+                                   "sample": f"{r1} x {what}, {d1:.1f} s"}})
+    return info
 
 
 def _cpu_model():
+    """lscpu's model name (the /proc/cpuinfo line as a fallback)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:

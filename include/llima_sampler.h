@@ -225,7 +225,12 @@ int llima_verify_tree(const void* tree_logits, int32_t dtype, int32_t K, int32_t
  * D drafts: target_logits [B][D+1][V] fp32, draft_logits [B][D][V] fp32,
  * draft_ids [B][D], u_accept [B][D], u_resample [B].  Accept draft k iff
  * p_t(x_k) >= u_k * p_d(x_k); at the first rejection resample from
- * max(0, p_t - p_d); after D acceptances draw a bonus token from p_t[D]. */
+ * max(0, p_t - p_d); after D acceptances draw a bonus token from p_t[D].
+ * Probabilities are fixed-point softmax weights built per chunk of 8192 ids
+ * (W_i = rint(exp(x_i - m_c) 2^36) * rint(exp(m_c - M) 2^27), m_c the chunk's
+ * maximum, M the row's), so each row is read once with no wait between
+ * workgroups; the draws use W_i >> 32.  V % 4 == 0, V <= 2^22, D <= 255, rows
+ * 16-byte aligned. */
 size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, int32_t V);
 int llima_verify_rejection(const float* target_logits, const float* draft_logits, int32_t B,
                            int32_t D, int32_t V, const int32_t* draft_ids,
@@ -233,20 +238,6 @@ int llima_verify_rejection(const float* target_logits, const float* draft_logits
                            int32_t* accepted_len, int32_t* emitted, void* workspace,
                            size_t workspace_bytes, void* stream);
 
-/* llima_verify_rejection with the bound on the row pass's cross-workgroup wait
- * exposed: a workgroup waiting for the maxima of its row's other chunks reads
- * a chunk that is still unpublished after help_after polls (~1 us each) itself,
- * so a verification whose workgroups are held back (e.g. by kernels of other
- * streams occupying the CUs) is delayed by at most ~help_after us per wait.
- * help_after < 0 selects the default (64); 0 makes every waiter read late
- * chunks at once.  help_count (nullable, device uint32) receives how many
- * chunks waiters read themselves.  Results do not depend on help_after. */
-int llima_verify_rejection_ex(const float* target_logits, const float* draft_logits, int32_t B,
-                              int32_t D, int32_t V, const int32_t* draft_ids,
-                              const float* u_accept, const float* u_resample,
-                              int32_t* accepted_len, int32_t* emitted, int32_t help_after,
-                              uint32_t* help_count, void* workspace, size_t workspace_bytes,
-                              void* stream);
 
 /* Log-likelihood of B target tokens: replaces score_logits
  * (sima_lmm/devkit/cpp/language_model.cpp:29-62), one row per call there.

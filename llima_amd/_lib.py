@@ -43,8 +43,6 @@ SIGNATURES = {
     "llima_verify_rejection_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_verify_rejection": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                               _vp, _sz, _vp]),
-    "llima_verify_rejection_ex": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
-                                                 _vp, _i32, _vp, _vp, _sz, _vp]),
     "llima_score_logits_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "llima_score_logits": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),

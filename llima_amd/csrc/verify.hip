@@ -3,66 +3,58 @@
 //
 // Inputs: target logits [B][D+1][V] and draft logits [B][D][V] (fp32), the D
 // draft ids of each sequence, uniforms u_accept[B][D] and u_resample[B].
-// Probabilities are fixed-point softmax weights W = rint(exp(x - max) * 2^36)
-// with Z = sum W per row (exact uint64 sums), so every decision below is
-// integer arithmetic and identical to the CPU restatement:
-//   accept draft k  iff  W_t(x) * Z_d * 2^32 >= U32(u_k) * W_d(x) * Z_t
-//   residual        R_i = max(0, W_t,i * Z_d - W_d,i * Z_t) >> shift,
-//                   shift = max(0, bitlen(Z_t) + bitlen(Z_d) - 63)
+// Probabilities are fixed-point softmax weights built per chunk of 8192 ids:
+// chunk c of a row has its maximum m_c, the row its maximum M, and
+//   w_i = rint(exp(x_i - m_c) 2^36),  F_c = rint(exp(m_c - M) 2^27),
+//   W_i = w_i F_c,  Z = sum_c F_c sum_{i in c} w_i  (exact, 128-bit),
+// so every chunk's sum needs only the chunk's own maximum: the row pass reads
+// each row once and no workgroup waits for another.  Decisions:
+//   accept draft k  iff  W_t(x) Z_d >= u_k W_d(x) Z_t      (IEEE double)
+//   draws           on W~_i = W_i >> 32 (below 2^31); the residual at a
+//                   rejection is R_i = max(0, W~_t,i z_d - W~_d,i z_t) >> 21 with
+//                   z = Z >> 27 shifted (the same shift for both rows) to 32
+//                   bits, so every product is one 32 x 32 -> 64-bit multiply;
 //   draw            smallest id whose ascending prefix of weights exceeds
 //                   (U32(u) * total) >> 32.
 // The reference verifies drafts greedily (sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195,
 // sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111); with one-hot distributions
 // this reduces to that rule.
 //
-// Four launches:
-//   vr_clear    marks every chunk-maximum slot unpublished (0: every key of a
-//               value, -inf included, is above 0)
+// Three launches:
 //   vr_rowpass  per (row, chunk of 8192 ids), one read of the rows: the chunk's
-//               maximum key, published in its slot; once every chunk of the row
-//               has published, the sum of W over the chunk (from the values
-//               still in registers), and W at the row's draft token
+//               maximum key, the sum of w over the chunk, and w at the row's
+//               draft token
 //   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
-//               the sums by every workgroup of the sequence), then, for every
-//               group of 32 ids of the draw row, the sum of the residual
-//               weights and the sum of the plain target weights.  Workgroup 0
-//               of a sequence also writes accepted_len, the emitted drafts and
-//               the draw context for vr_final
+//               the chunk maxima and sums by every workgroup of the sequence),
+//               then, for every group of 32 ids of the draw row, the sum of the
+//               residual weights and the sum of the plain target weights.
+//               Workgroup 0 of a sequence also writes accepted_len, the emitted
+//               drafts and the draw context for vr_final
 //   vr_final    per sequence: the group holding the draw target (a block scan
 //               over the group sums), and the token inside it (one wave, one id
 //               per lane).
-// vr_rowpass workgroups wait for the other chunks of their row, which the
-// dispatcher normally starts alongside them (a row's chunks are consecutive
-// workgroups).  The wait never depends on that: a workgroup that has polled
-// help_after times reads the lowest unpublished chunk of its row itself and
-// publishes its maximum (the value the chunk's own workgroup publishes too),
-// so every wait ends after at most help_after + S polls, whatever the order
-// and residency of the workgroups.  Slots are written and polled with
-// device-scope atomics (the chunks of a row may run on different XCDs, whose
-// L2 caches are not coherent with each other).  help_after is VR_HELP_AFTER
-// unless llima_verify_rejection_ex gives another count (0 makes every waiter
-// read its row's late chunks itself); with ~1 us per poll, a row whose chunks
-// are held back (e.g. by kernels of other streams occupying the CUs) delays
-// its waiters by at most about help_after us before they read those chunks.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
 namespace llima {
 
 #define VR_E 32
-#define VR_CHUNK (LLIMA_WG * VR_E)
+#define VR_CHUNK (LLIMA_WG * VR_E)   // 8192 ids: the chunk of the weights' definition
+#define VR_CSHIFT 13                 // log2(VR_CHUNK)
 #define VR_MAX_D 255
-#define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup
+#define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup (inside one chunk)
 #define VR_G 32                      // ids per draw group (4 threads of vr_drawsum)
 #define VR_GB 16                     // group sums a vr_final thread loads at once
-#define VR_HELP_AFTER 64             // polls (~1 us each) before a waiter reads a late chunk itself
+#define VR_FBITS 27                  // chunk factor F_c = rint(exp(m_c - M) 2^27)
+#define VR_ZBITS 32                  // width of the residual's normalizers
+#define VR_RSHIFT 21                 // residual scaling (sums below 2^64 for V <= 2^22)
 
 // Draw context of a sequence: what vr_final needs of its acceptance step.
 struct SeqCtx {
-    uint64_t zt, zd;     // Z of the draw's target row, and of its draft row (residual draw)
-    uint32_t mt, md;     // their maximum keys
+    uint32_t zt, zd;     // the residual's normalizers (32-bit z of the two draw rows)
+    uint32_t Mt, Md;     // maximum keys of the draw's target and draft rows
     int32_t acc;         // accepted drafts: the draw uses target row acc
-    int32_t shift;       // residual scaling
+    int32_t residual;    // a draft was rejected: the draw is from the residual
 };
 
 struct VerifyParams {
@@ -73,15 +65,13 @@ struct VerifyParams {
     const float* u_resample;
     int32_t* accepted_len;
     int32_t* emitted;
-    uint32_t* maxk;      // [NR][S]
-    uint64_t* sums;      // [NR][S]
-    uint64_t* wx;        // [NR]
+    uint32_t* maxk;      // [NR][S] chunk maximum keys
+    uint64_t* sums;      // [NR][S] chunk sums of w
+    uint64_t* wx;        // [NR] w at the row's draft token (relative to its chunk)
     uint64_t* gres;      // [B][NG] residual weight per group of VR_G ids
     uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
     SeqCtx* ctx;         // [B]
     int32_t B, D, V, S, NR, NG, SD;
-    int32_t help_after;  // polls before a waiter reads a late chunk itself
-    uint32_t* help_count;  // nullable: chunks read by waiters (cleared by vr_clear)
 };
 
 // Row r: target rows first ([B][D+1]), then draft rows ([B][D]).
@@ -132,15 +122,25 @@ __device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, in
     }
 }
 
-// Weight of a value given its row maximum key (0 when the row has no value).
-__device__ __forceinline__ uint64_t row_weight(float x, uint32_t mkey) {
+// w of a value given its chunk's maximum key (0 when the chunk has no value).
+__device__ __forceinline__ uint64_t chunk_weight(float x, uint32_t mkey) {
     if (mkey <= LLIMA_KEY_NEG_INF) return 0;
     return weight(x, key_f32(mkey));
 }
 
+// F_c = rint(exp(m_c - M) 2^27): 2^27 for the maximum's chunks, 0 for a chunk
+// with no value or one more than 26 below the maximum.
+__device__ __forceinline__ uint32_t chunk_factor(uint32_t mck, uint32_t Mk) {
+    if (mck <= LLIMA_KEY_NEG_INF) return 0;
+    if (mck == Mk) return 1u << VR_FBITS;
+    const float d = key_f32(mck) - key_f32(Mk);
+    if (!(d >= -26.0f)) return 0;
+    return (uint32_t)__builtin_rintf(__builtin_ldexpf(exp_neg(d), VR_FBITS));
+}
+
 // weight(x, xmax) for a finite xmax, as the integral float it converts
 // (W < 2^37, exact in fp32): sums of at most 2^16 of them are exact in double,
-// so the row sums skip the per-value float -> uint64 conversion.  exp_neg's
+// so the chunk sums skip the per-value float -> uint64 conversion.  exp_neg's
 // steps with three folds that leave every result unchanged:
 //   * d is clamped at -26 (NaN included) with no select after, since
 //     rint(e^-26 2^36) = rint(0.35) = 0;
@@ -169,37 +169,11 @@ __device__ __forceinline__ float weight_f(float x, float xmax) {
     return __builtin_rintf(__builtin_ldexpf(p, (int)n));
 }
 
-__global__ __launch_bounds__(LLIMA_WG) void vr_clear(VerifyParams P) {
-    const int n = P.NR * P.S;
-    for (int i = (int)(blockIdx.x * LLIMA_WG + threadIdx.x); i < n; i += (int)(gridDim.x * LLIMA_WG))
-        P.maxk[i] = 0;
-    if (P.help_count && blockIdx.x == 0 && threadIdx.x == 0) *P.help_count = 0;
-}
-
-// Maximum key of chunk c of a row (every thread gets it), read one 16-byte
-// load per thread at a time.
-__device__ __forceinline__ uint32_t chunk_max_key(const float* rowp, int c, int V, BlockScratch& bs) {
-    const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < V ? c0 + VR_CHUNK : V;
-    float m = -__builtin_inff();
-#pragma unroll 1
-    for (int j = 0; j < VR_E / 4; ++j) {                // few registers: the waiter's own chunk stays live
-        const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
-        const int ia = i0 < V ? i0 : V - 4;
-        const llima_u32x4 q = *(const llima_u32x4*)(rowp + ia);
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float x = __uint_as_float(w4[e]);
-            m = i0 + e < c1 && x > m ? x : m;
-        }
-    }
-    return block_max_u32(f32_key(m), bs);
-}
-
+// ------------------------------------------------------------------ row pass
+// One workgroup per (row, chunk): the chunk's maximum, its sum of w (relative to
+// that maximum) and w at the row's draft token when it lies in the chunk.
 __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
     __shared__ BlockScratch bs;
-    __shared__ uint32_t s_mkey;
-    __shared__ int32_t s_miss;
     const int r = (int)blockIdx.x / P.S, c = (int)blockIdx.x - r * P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
@@ -208,44 +182,12 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
     float m = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < VR_E; ++e) m = v[e] > m ? v[e] : m;   // NaN never counts
-    const uint32_t k = block_max_u32(f32_key(m), bs);          // >= f32_key(-inf) > 0
-    uint32_t* slot = P.maxk + (size_t)r * P.S;
-    if (threadIdx.x == 0) __hip_atomic_store(&slot[c], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the row maximum: wave 0 polls the row's slots until all are published
-    for (int round = 0;; ++round) {
-        if (threadIdx.x < 64) {
-            uint32_t best = 0, miss = 0xFFFFFFFFu;
-            for (int i = (int)threadIdx.x; i < P.S; i += 64) {
-                const uint32_t x = __hip_atomic_load(&slot[i], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                if (x == 0) miss = (uint32_t)i < miss ? (uint32_t)i : miss;
-                best = x > best ? x : best;
-            }
-            best = wave_max_u32(best);
-            miss = wave_min_u32(miss);
-            if (threadIdx.x == 0) { s_mkey = best; s_miss = (int32_t)miss; }
-            if (miss != 0xFFFFFFFFu && round < P.help_after) __builtin_amdgcn_s_sleep(8);
-        }
-        __syncthreads();
-        const int miss = s_miss;
-        if (miss < 0) break;                                    // every chunk published
-        if (round >= P.help_after) {                            // a late chunk: read it here
-            const uint32_t km = chunk_max_key(rowp, miss, P.V, bs);
-            if (threadIdx.x == 0) {
-                __hip_atomic_store(&slot[miss], km, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (P.help_count)
-                    __hip_atomic_fetch_add(P.help_count, 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        __syncthreads();
-    }
-    const uint32_t mkey = s_mkey;
+    const uint32_t mkey = block_max_u32(f32_key(m), bs);       // >= f32_key(-inf) > 0
     uint64_t s = 0;
     if (mkey > LLIMA_KEY_NEG_INF) {
         const float xm = key_f32(mkey);
         double sd = 0.0;                                 // exact: 32 terms below 2^37
-        if (xm == __builtin_inff()) {                    // W = 2^36 at every +inf, else 0
+        if (xm == __builtin_inff()) {                    // w = 2^36 at every +inf, else 0
 #pragma unroll
             for (int e = 0; e < VR_E; ++e) sd += v[e] == xm ? (double)VR_TWO36 : 0.0;
         } else {
@@ -256,40 +198,76 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
     }
     s = block_sum_u64(s, bs);
     if (threadIdx.x == 0) {
+        P.maxk[(size_t)r * P.S + c] = mkey;
         P.sums[(size_t)r * P.S + c] = s;
         const int b = seq_of(P, r), kk = pos_of(P, r);
         if (kk < P.D) {
             const int x = P.draft_ids[b * P.D + kk];
-            if (x >= c0 && x < c1) P.wx[r] = row_weight(rowp[x], mkey);
+            if (x >= c0 && x < c1) P.wx[r] = chunk_weight(rowp[x], mkey);
         }
     }
 }
 
 // ------------------------------------------------------------------ acceptance
+#define VR_SEQ_ITEMS 4               // (row, chunk) items of a sequence a thread holds
+#define VR_MK_LDS (VR_SEQ_ITEMS * LLIMA_WG)
+
 struct SeqShared {
-    uint64_t z[2 * VR_MAX_D + 1];      // Z of target rows 0..D then draft rows 0..D-1
-    uint32_t m[2 * VR_MAX_D + 1];      // maximum keys, same order
-    uint8_t ok[VR_MAX_D];              // draft k passes its acceptance test
+    uint32_t M[2 * VR_MAX_D + 1];          // maximum keys of target rows 0..D, then draft rows
+    unsigned long long zl[2 * VR_MAX_D + 1][3];   // Z in 26-bit limbs
+    uint32_t mk[VR_MK_LDS];                // chunk maxima [row q][chunk] (when they fit)
+    uint8_t ok[VR_MAX_D];                  // draft k passes its acceptance test
     int32_t acc;
     BlockScratch bs;
 };
 
-// Z and maximum of every row of sequence b, then the acceptance scan.  Every
-// input is requested at once (the per-chunk sums are combined with LDS
-// atomics) and the D acceptance tests run in parallel, one per thread: the
-// only serial part is the first failing test, found in LDS.  Returns the
-// number of accepted drafts (same in every thread).
+__device__ __forceinline__ int row_of(const VerifyParams& P, int b, int q) {
+    return q <= P.D ? trow(P, b, q) : drow(P, b, q - P.D - 1);
+}
+
+__device__ __forceinline__ llima_u128 limbs_z(const unsigned long long (&l)[3]) {
+    return (llima_u128)l[0] + ((llima_u128)l[1] << 26) + ((llima_u128)l[2] << 52);
+}
+
+__device__ __forceinline__ double u128_to_double(llima_u128 z) {
+    return (double)(uint64_t)(z >> 64) * 18446744073709551616.0 + (double)(uint64_t)z;
+}
+
+__device__ __forceinline__ int bitlen64(uint64_t z) { return z ? 64 - __clzll((long long)z) : 0; }
+
+// Chunk maximum of row q (of the sequence), chunk c: from LDS when the
+// sequence's maxima fit there (accept_scan staged them), else from memory.
+__device__ __forceinline__ uint32_t seq_maxk(const VerifyParams& P, int b, int q, int c,
+                                             const SeqShared& sh) {
+    const int n = (2 * P.D + 1) * P.S;
+    return n <= VR_MK_LDS ? sh.mk[q * P.S + c] : P.maxk[(size_t)row_of(P, b, q) * P.S + c];
+}
+
+// M and Z of every row of sequence b, then the acceptance scan.  Every input is
+// requested at once (up to VR_SEQ_ITEMS (row, chunk) items per thread, held in
+// registers): the chunk maxima combine with LDS atomics, then each chunk's
+// F_c S_c (below 2^77) is added to its row's Z in three 26-bit limbs, which sum
+// exactly.  The D acceptance tests run in parallel, one per thread; the only
+// serial part is the first failing test, found in LDS.  Returns the number of
+// accepted drafts (same in every thread).
 __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShared& sh) {
-    const int nr = 2 * P.D + 1, t = (int)threadIdx.x;
-    for (int q = t; q < nr; q += LLIMA_WG) { sh.z[q] = 0; sh.m[q] = 0; }
-    __syncthreads();
-    for (int i = t; i < nr * P.S; i += LLIMA_WG) {
-        const int q = i / P.S, c = i - q * P.S;
-        const int r = q <= P.D ? trow(P, b, q) : drow(P, b, q - P.D - 1);
-        atomicAdd((unsigned long long*)&sh.z[q], (unsigned long long)P.sums[(size_t)r * P.S + c]);
-        atomicMax(&sh.m[q], P.maxk[(size_t)r * P.S + c]);
+    const int nr = 2 * P.D + 1, t = (int)threadIdx.x, n = nr * P.S;
+    for (int q = t; q < nr; q += LLIMA_WG) {
+        sh.M[q] = 0;
+        sh.zl[q][0] = 0; sh.zl[q][1] = 0; sh.zl[q][2] = 0;
     }
-    // per draft: W at the draft token in the target and the draft row
+    uint32_t km[VR_SEQ_ITEMS];
+    uint64_t sm[VR_SEQ_ITEMS];
+#pragma unroll
+    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+        const int i = t + j * LLIMA_WG;
+        const int ic = i < n ? i : 0;
+        const int q = ic / P.S, c = ic - q * P.S;
+        const size_t rc = (size_t)row_of(P, b, q) * P.S + c;
+        km[j] = P.maxk[rc];
+        sm[j] = P.sums[rc];
+    }
+    // per draft: w at the draft token in the target and the draft row
     int x = -1;
     uint64_t wt = 0, wd = 0;
     float ua = 0.0f;
@@ -299,6 +277,33 @@ __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShar
         wd = P.wx[drow(P, b, t)];
         ua = P.u_accept[b * P.D + t];
     }
+    __syncthreads();                                   // M and zl zeroed
+#pragma unroll
+    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+        const int i = t + j * LLIMA_WG;
+        if (i < n) {
+            atomicMax(&sh.M[i / P.S], km[j]);
+            if (n <= VR_MK_LDS) sh.mk[i] = km[j];
+        }
+    }
+    for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG)  // sequences with more items than that
+        atomicMax(&sh.M[i / P.S], P.maxk[(size_t)row_of(P, b, i / P.S) * P.S + i % P.S]);
+    __syncthreads();
+    auto add_z = [&](int q, uint32_t kk, uint64_t ss) {
+        const llima_u128 fs = (llima_u128)ss * chunk_factor(kk, sh.M[q]);
+        atomicAdd(&sh.zl[q][0], (unsigned long long)(fs & 0x3FFFFFFull));
+        atomicAdd(&sh.zl[q][1], (unsigned long long)((fs >> 26) & 0x3FFFFFFull));
+        atomicAdd(&sh.zl[q][2], (unsigned long long)(fs >> 52));
+    };
+#pragma unroll
+    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+        const int i = t + j * LLIMA_WG;
+        if (i < n) add_z(i / P.S, km[j], sm[j]);
+    }
+    for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG) {
+        const size_t rc = (size_t)row_of(P, b, i / P.S) * P.S + i % P.S;
+        add_z(i / P.S, P.maxk[rc], P.sums[rc]);
+    }
     __syncthreads();
     for (int k = t; k < P.D; k += LLIMA_WG) {
         if (k != t) {                                   // D > LLIMA_WG: the rest one by one
@@ -307,11 +312,15 @@ __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShar
             wd = P.wx[drow(P, b, k)];
             ua = P.u_accept[b * P.D + k];
         }
-        const uint64_t zt = sh.z[k], zd = sh.z[P.D + 1 + k];
+        const llima_u128 zt = limbs_z(sh.zl[k]), zd = limbs_z(sh.zl[P.D + 1 + k]);
         bool ok = false;
         if (x >= 0 && x < P.V && zt > 0) {
-            const llima_u128 lhs = ((llima_u128)wt * zd) << 32;
-            const llima_u128 rhs = (llima_u128)uniform32(ua) * ((llima_u128)wd * zt);
+            const int cx = x >> VR_CSHIFT;
+            const uint64_t Wt = wt * chunk_factor(seq_maxk(P, b, k, cx, sh), sh.M[k]);
+            const uint64_t Wd = wd * chunk_factor(seq_maxk(P, b, P.D + 1 + k, cx, sh),
+                                                  sh.M[P.D + 1 + k]);
+            const double lhs = (double)Wt * u128_to_double(zd);
+            const double rhs = (double)ua * (double)Wd * u128_to_double(zt);
             ok = lhs >= rhs;
         }
         sh.ok[k] = ok ? 1 : 0;
@@ -326,15 +335,14 @@ __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShar
     return sh.acc;
 }
 
-__device__ __forceinline__ int bitlen64(uint64_t z) { return z ? 64 - __clzll((long long)z) : 0; }
-
+// The draw of a sequence: its rows and the scalars of its weights.
 struct DrawCtx {
     bool residual;
     const float* t;
     const float* d;
-    uint32_t mt, md;
-    uint64_t zt, zd;
-    int shift;
+    int rt, rd;              // row indices (for the chunk maxima)
+    uint32_t Mt, Md;         // row maximum keys
+    uint32_t zt, zd;         // residual normalizers
 };
 
 __device__ __forceinline__ DrawCtx draw_ctx(const VerifyParams& P, int b, int acc,
@@ -342,26 +350,55 @@ __device__ __forceinline__ DrawCtx draw_ctx(const VerifyParams& P, int b, int ac
     DrawCtx q;
     q.residual = acc < P.D;
     const int k = acc;                                 // target row of the draw
-    q.t = row_ptr(P, trow(P, b, k));
-    q.mt = sh.m[k];
-    q.zt = sh.z[k];
-    q.d = nullptr; q.md = 0; q.zd = 0; q.shift = 0;
+    q.rt = trow(P, b, k);
+    q.t = row_ptr(P, q.rt);
+    q.Mt = sh.M[k];
+    q.d = nullptr; q.rd = 0; q.Md = 0; q.zt = 0; q.zd = 0;
     if (q.residual) {
-        q.d = row_ptr(P, drow(P, b, k));
-        q.md = sh.m[P.D + 1 + k];
-        q.zd = sh.z[P.D + 1 + k];
-        const int s = bitlen64(q.zt) + bitlen64(q.zd) - 63;
-        q.shift = s > 0 ? s : 0;
+        q.rd = drow(P, b, k);
+        q.d = row_ptr(P, q.rd);
+        q.Md = sh.M[P.D + 1 + k];
+        const uint64_t ht = (uint64_t)(limbs_z(sh.zl[k]) >> VR_FBITS);
+        const uint64_t hd = (uint64_t)(limbs_z(sh.zl[P.D + 1 + k]) >> VR_FBITS);
+        const int bt = bitlen64(ht), bd = bitlen64(hd);
+        const int s = (bt > bd ? bt : bd) - VR_ZBITS;
+        q.zt = (uint32_t)(s > 0 ? ht >> s : ht);
+        q.zd = (uint32_t)(s > 0 ? hd >> s : hd);
     }
     return q;
 }
 
+// What the draw weights of one chunk of a draw row need: the chunk's maximum
+// (finite; 0 for a chunk with no value, whose factor is 0), whether it is +inf,
+// and F_c 2^-32.
+struct DrawChunk {
+    float xm;
+    bool inf;
+    double fs;
+};
 
-// Residual weight of one id from its target and draft values.
-__device__ __forceinline__ uint64_t residual_weight(const DrawCtx& q, uint64_t wt, float xd) {
-    const uint64_t wd = row_weight(xd, q.md);
-    const llima_u128 a = (llima_u128)wt * q.zd, c = (llima_u128)wd * q.zt;
-    return a > c ? (uint64_t)((a - c) >> q.shift) : 0ull;
+__device__ __forceinline__ DrawChunk draw_chunk(uint32_t mck, uint32_t Mk) {
+    DrawChunk c;
+    const float m = key_f32(mck);
+    c.inf = m == __builtin_inff();
+    c.xm = mck > LLIMA_KEY_NEG_INF && !c.inf ? m : 0.0f;
+    c.fs = (double)chunk_factor(mck, Mk) * 0x1p-32;
+    return c;
+}
+
+// W~ = (w F) >> 32 of a value of the chunk.  w is an integral float below 2^37
+// (24 significant bits at most) and F is below 2^28, so w F 2^-32 is exact in
+// double and the conversion to uint32 truncates it.  In a chunk whose maximum
+// is +inf, w is 2^36 at the +inf values and 0 elsewhere.
+__device__ __forceinline__ uint32_t draw_weight(float x, const DrawChunk& c) {
+    const float w = c.inf ? (x == __builtin_inff() ? VR_TWO36 : 0.0f) : weight_f(x, c.xm);
+    return (uint32_t)((double)w * c.fs);
+}
+
+// Residual weight of one id from its W~ values: each product below 2^63.
+__device__ __forceinline__ uint64_t residual_weight(const DrawCtx& q, uint32_t wt, uint32_t wd) {
+    const uint64_t a = (uint64_t)wt * q.zd, c = (uint64_t)wd * q.zt;
+    return a > c ? (a - c) >> VR_RSHIFT : 0ull;
 }
 
 // 8 consecutive values from id i0 (a multiple of 8): two 16-byte loads from
@@ -390,14 +427,18 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
         const int t = (int)threadIdx.x;
         if (t == 0) {
             SeqCtx x;
-            x.zt = q.zt; x.zd = q.zd; x.mt = q.mt; x.md = q.md;
-            x.acc = acc; x.shift = q.shift;
+            x.zt = q.zt; x.zd = q.zd; x.Mt = q.Mt; x.Md = q.Md;
+            x.acc = acc; x.residual = q.residual ? 1 : 0;
             P.ctx[b] = x;
             P.accepted_len[b] = acc;
         }
         if (t <= P.D)                                  // vr_final writes the drawn token at acc
             P.emitted[(size_t)b * (P.D + 1) + t] = t < acc ? P.draft_ids[b * P.D + t] : -1;
     }
+    // this workgroup's 2048 ids lie in one chunk of both draw rows
+    const int cc = (c * VR_DCHUNK) >> VR_CSHIFT;
+    const DrawChunk ct = draw_chunk(seq_maxk(P, b, acc, cc, sh), q.Mt);
+    const DrawChunk cd = draw_chunk(q.residual ? seq_maxk(P, b, P.D + 1 + acc, cc, sh) : 0u, q.Md);
     const int i0 = c * VR_DCHUNK + (int)threadIdx.x * 8;
     float xt[8], xd[8];
     load8(q.t, i0, P.V, xt);
@@ -405,9 +446,9 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
     uint64_t st = 0, sr = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const uint64_t wt = row_weight(xt[e], q.mt);
+        const uint32_t wt = draw_weight(xt[e], ct);
         st += wt;
-        if (q.residual) sr += residual_weight(q, wt, xd[e]);
+        if (q.residual) sr += residual_weight(q, wt, draw_weight(xd[e], cd));
     }
     st = quad_sum_u64(st);                            // 4 threads = one group of 32 ids
     sr = quad_sum_u64(sr);
@@ -439,12 +480,15 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
         vt0[j] = gt[gi];
     }
     const SeqCtx x = P.ctx[b];
+    const uint32_t u32 = uniform32(P.u_resample[b]);  // requested with the sums
     const int acc = x.acc;
     DrawCtx q;
-    q.residual = acc < P.D;
-    q.t = row_ptr(P, trow(P, b, acc));
-    q.d = q.residual ? row_ptr(P, drow(P, b, acc)) : nullptr;
-    q.mt = x.mt; q.md = x.md; q.zt = x.zt; q.zd = x.zd; q.shift = x.shift;
+    q.residual = x.residual != 0;
+    q.rt = trow(P, b, acc);
+    q.t = row_ptr(P, q.rt);
+    q.rd = q.residual ? drow(P, b, acc) : 0;
+    q.d = q.residual ? row_ptr(P, q.rd) : nullptr;
+    q.Mt = x.Mt; q.Md = x.Md; q.zt = x.zt; q.zd = x.zd;
     if (t == 0) {
         s_group = -1;
         s_tok = -1;
@@ -487,14 +531,16 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     const uint64_t s = q.residual ? sr : st;
     const uint64_t before = q.residual ? br + ir - sr : bt + it - st;
     const uint64_t total = q.residual ? tr : tt;
-    const uint64_t target = (uint64_t)(((llima_u128)uniform32(P.u_resample[b]) * total) >> 32);
+    const uint64_t target = (uint64_t)(((llima_u128)u32 * total) >> 32);
     if (total > 0 && s > 0 && before <= target && target < before + s) {
         uint64_t a = before;
         bool found = false;
         for (int gb = g0; gb < g1 && !found; gb += VR_GB) {
-            uint64_t v[VR_GB];
+            uint64_t v[VR_GB];               // the first block is still in registers
 #pragma unroll
-            for (int j = 0; j < VR_GB; ++j) v[j] = gb + j < g1 ? sums[gb + j] : 0ull;
+            for (int j = 0; j < VR_GB; ++j)
+                v[j] = gb + j >= g1 ? 0ull
+                     : gb == g0 ? (q.residual ? vr0[j] : vt0[j]) : sums[gb + j];
 #pragma unroll
             for (int j = 0; j < VR_GB; ++j) {
                 if (!found && a + v[j] > target) { s_group = gb + j; s_before = a; found = true; }
@@ -507,10 +553,13 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     if (grp >= 0 && t < 64) {
         // one id per lane: the group's weights, scanned in id order
         const int i = grp * VR_G + (int)t;
+        const int cc = (grp * VR_G) >> VR_CSHIFT;
+        const DrawChunk ct = draw_chunk(P.maxk[(size_t)q.rt * P.S + cc], q.Mt);
+        const DrawChunk cd = draw_chunk(q.residual ? P.maxk[(size_t)q.rd * P.S + cc] : 0u, q.Md);
         uint64_t w = 0;
         if (t < VR_G && i < P.V) {
-            const uint64_t wt = row_weight(q.t[i], q.mt);
-            w = q.residual ? residual_weight(q, wt, q.d[i]) : wt;
+            const uint32_t wt = draw_weight(q.t[i], ct);
+            w = q.residual ? residual_weight(q, wt, draw_weight(q.d[i], cd)) : wt;
         }
         const uint64_t inc = s_before + wave_incl_scan_u64(w);
         if (w > 0 && inc - w <= target && target < inc) s_tok = i;
@@ -534,18 +583,16 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
            al256((size_t)B * sizeof(SeqCtx));
 }
 
-extern "C" int llima_verify_rejection_ex(const float* target_logits, const float* draft_logits,
-                                         int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
-                                         const float* u_accept, const float* u_resample,
-                                         int32_t* accepted_len, int32_t* emitted,
-                                         int32_t help_after, uint32_t* help_count,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
+                                      int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
+                                      const float* u_accept, const float* u_resample,
+                                      int32_t* accepted_len, int32_t* emitted, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
     if (B > 0 && (!target_logits || !u_resample || !accepted_len || !emitted)) return LLIMA_E_INVAL;
     if (B > 0 && D > 0 && (!draft_logits || !draft_ids || !u_accept)) return LLIMA_E_INVAL;
     if (B < 0 || D < 0 || D > VR_MAX_D || V <= 0 || V > (1 << 22)) return LLIMA_E_INVAL;
     if ((uintptr_t)target_logits % 16 || (D > 0 && (uintptr_t)draft_logits % 16) || V % 4)
         return LLIMA_E_INVAL;                  // rows are read with 16-byte loads
-    if (help_after > (1 << 20)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_verify_rejection_workspace_bytes(B, D, V))
         return LLIMA_E_WORKSPACE;
@@ -558,8 +605,6 @@ extern "C" int llima_verify_rejection_ex(const float* target_logits, const float
     P.NR = B * (2 * D + 1);
     P.NG = (V + VR_G - 1) / VR_G;
     P.SD = (V + VR_DCHUNK - 1) / VR_DCHUNK;
-    P.help_after = help_after < 0 ? VR_HELP_AFTER : help_after;
-    P.help_count = help_count;
     char* w = (char*)workspace;
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
@@ -569,20 +614,8 @@ extern "C" int llima_verify_rejection_ex(const float* target_logits, const float
     P.ctx = (SeqCtx*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
-    const uint32_t gc = (g12 + LLIMA_WG - 1) / LLIMA_WG;
-    hipLaunchKernelGGL(vr_clear, dim3(gc < 64 ? gc : 64), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_rowpass, dim3(g12), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
-}
-
-extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
-                                      int32_t B, int32_t D, int32_t V, const int32_t* draft_ids,
-                                      const float* u_accept, const float* u_resample,
-                                      int32_t* accepted_len, int32_t* emitted, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
-    return llima_verify_rejection_ex(target_logits, draft_logits, B, D, V, draft_ids, u_accept,
-                                     u_resample, accepted_len, emitted, -1, nullptr, workspace,
-                                     workspace_bytes, stream);
 }

@@ -377,15 +377,10 @@ def verify_tree(tree_logits: torch.Tensor, retrieve_indices: torch.Tensor,
 
 
 def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
-                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_resample: torch.Tensor,
-                     help_after: Optional[int] = None, help_count: Optional[torch.Tensor] = None):
+                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_resample: torch.Tensor):
     """Stochastic verification: target [B, D+1, V] and draft [B, D, V] fp32
     logits, draft ids [B, D], uniforms u_accept [B, D] and u_resample [B] ->
-    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded).
-    help_after: polls (~1 us each) before a row-pass workgroup reads a late
-    chunk of its row itself (None: the library default); help_count (an int32
-    device tensor of one element, optional) receives how many chunks were read
-    that way.  The results do not depend on either."""
+    (accepted_len int32 [B], emitted int32 [B, D+1], -1 padded)."""
     t = target_logits.contiguous()
     dl = draft_logits.contiguous()
     if t.dtype != torch.float32 or dl.dtype != torch.float32:
@@ -398,15 +393,13 @@ def verify_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
     ids = draft_ids.to(device=dev, dtype=torch.int32).contiguous()
     ua = u_accept.to(device=dev, dtype=torch.float32).contiguous()
     ur = u_resample.to(device=dev, dtype=torch.float32).contiguous()
-    _on_gpu(t, dl, ids, ua, ur, help_count)
+    _on_gpu(t, dl, ids, ua, ur)
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     em = torch.empty((B, D1), dtype=torch.int32, device=dev)
     ws = Workspace.get(dev, "verify_rejection", lib().llima_verify_rejection_workspace_bytes(B, D, V))
-    check(lib().llima_verify_rejection_ex(t.data_ptr(), dl.data_ptr(), B, D, V, ids.data_ptr(),
-                                          ua.data_ptr(), ur.data_ptr(), acc.data_ptr(),
-                                          em.data_ptr(), -1 if help_after is None else help_after,
-                                          _ptr(help_count), ws.data_ptr(), ws.numel(),
-                                          _stream(dev)),
+    check(lib().llima_verify_rejection(t.data_ptr(), dl.data_ptr(), B, D, V, ids.data_ptr(),
+                                       ua.data_ptr(), ur.data_ptr(), acc.data_ptr(),
+                                       em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
           "llima_verify_rejection")
     return acc, em
 

@@ -459,20 +459,87 @@ int orc_tree_gather(const int32_t* row_tokens, int K, const int32_t* retrieve, i
     return ORC_OK;
 }
 
-// Row statistics for rejection verification: max (NaN -> -inf) and Z.
-static void row_stats(const float* row, int V, float* xmax, uint64_t* Z) {
-    float m = -std::numeric_limits<float>::infinity();
-    for (int i = 0; i < V; ++i) { float v = row[i]; if (v > m) m = v; }
-    uint64_t z = 0;
-    if (m > -std::numeric_limits<float>::infinity())
-        for (int i = 0; i < V; ++i) { float v = row[i]; if (v == v) z += orc_weight(v, m); }
-    *xmax = m; *Z = z;
+// Rejection verification weights (the specification of this build; the
+// reference verifies greedily).  A row is cut into chunks of 8192 ids; chunk c
+// has its maximum m_c (NaN ignored) and the row its maximum M = max m_c:
+//   w_i = rint(exp(x_i - m_c) 2^36)          (orc_weight, relative to the chunk)
+//   F_c = rint(exp(m_c - M) 2^27)            (2^27 for the maximum's chunks, 0
+//                                              below -26 or for an empty chunk)
+//   W_i = w_i F_c,  Z = sum_c F_c S_c,  S_c = sum_{i in c} w_i   (exact)
+// so a chunk's sum needs only its own maximum.  Acceptance compares
+// W_t(x) Z_d >= u W_d(x) Z_t in IEEE double; the draws use W~_i = W_i >> 32
+// (below 2^31), the residual max(0, W~_t z_d - W~_d z_t) >> 21 with
+// z = (Z >> 27) >> s, one shift s for both rows that leaves the larger 32 bits
+// wide (each product below 2^63, each residual below 2^42).
+#define ORC_VR_CHUNK 8192
+
+struct VrRow {
+    std::vector<float> m;      // chunk maxima
+    std::vector<uint32_t> F;   // chunk factors
+    u128 Z;
+};
+
+static uint32_t vr_factor(float mc, float M) {
+    if (!(mc > -std::numeric_limits<float>::infinity())) return 0;
+    if (mc == M) return 1u << 27;
+    const float d = mc - M;
+    if (!(d >= -26.0f)) return 0;
+    return (uint32_t)rintf(ldexpf(orc_exp_neg(d), 27));
 }
 
-static inline uint64_t wt(const float* row, int i, float m) {
-    float v = row[i];
-    if (v != v || !(m > -std::numeric_limits<float>::infinity())) return 0;
-    return orc_weight(v, m);
+static void vr_row(const float* row, int V, VrRow& r) {
+    const int nc = (V + ORC_VR_CHUNK - 1) / ORC_VR_CHUNK;
+    r.m.assign(nc, -std::numeric_limits<float>::infinity());
+    r.F.assign(nc, 0);
+    float M = -std::numeric_limits<float>::infinity();
+    for (int i = 0; i < V; ++i) {
+        float& mc = r.m[i / ORC_VR_CHUNK];
+        if (row[i] > mc) mc = row[i];
+    }
+    for (int c = 0; c < nc; ++c) M = r.m[c] > M ? r.m[c] : M;
+    r.Z = 0;
+    for (int c = 0; c < nc; ++c) {
+        r.F[c] = vr_factor(r.m[c], M);
+        uint64_t S = 0;
+        if (r.m[c] > -std::numeric_limits<float>::infinity())
+            for (int i = c * ORC_VR_CHUNK; i < std::min(V, (c + 1) * ORC_VR_CHUNK); ++i)
+                if (row[i] == row[i]) S += orc_weight(row[i], r.m[c]);
+        r.Z += (u128)S * r.F[c];
+    }
+}
+
+// W_i of the specification.
+static uint64_t vr_w(const float* row, const VrRow& r, int i) {
+    const float mc = r.m[i / ORC_VR_CHUNK];
+    const float v = row[i];
+    if (v != v || !(mc > -std::numeric_limits<float>::infinity())) return 0;
+    return orc_weight(v, mc) * (uint64_t)r.F[i / ORC_VR_CHUNK];
+}
+
+// W_i of every id and Z (as two 64-bit halves) of one row (for the tests).
+int orc_vr_weights(const float* row, int V, uint64_t* W, uint64_t* Z2) {
+    if (V <= 0) return ORC_E_INVAL;
+    VrRow r;
+    vr_row(row, V, r);
+    for (int i = 0; i < V; ++i) W[i] = vr_w(row, r, i);
+    Z2[0] = (uint64_t)r.Z;
+    Z2[1] = (uint64_t)(r.Z >> 64);
+    return ORC_OK;
+}
+
+static double u128_to_double(u128 z) {
+    return (double)(uint64_t)(z >> 64) * 18446744073709551616.0 + (double)(uint64_t)z;
+}
+
+static inline int bitlen64(uint64_t z) { return z ? 64 - __builtin_clzll(z) : 0; }
+
+// The residual's normalizers: (Z >> 27) of both rows, shifted together until
+// the larger is 32 bits wide.
+static void vr_z32(u128 Zt, u128 Zd, uint64_t* zt, uint64_t* zd) {
+    const uint64_t ht = (uint64_t)(Zt >> 27), hd = (uint64_t)(Zd >> 27);
+    const int s = std::max(0, std::max(bitlen64(ht), bitlen64(hd)) - 32);
+    *zt = ht >> s;
+    *zd = hd >> s;
 }
 
 }  // extern "C"
@@ -493,7 +560,8 @@ static int32_t draw_weights(int V, F f, uint64_t total, float u) {
 extern "C" {
 
 // Stochastic speculative verification (Leviathan et al. 2023; Chen et al. 2023)
-// on fixed-point softmax weights.  target: [B, D+1, V] fp32, draft: [B, D, V] fp32.
+// on the chunked fixed-point weights above.  target: [B, D+1, V] fp32, draft:
+// [B, D, V] fp32.
 int orc_verify_rejection(const float* tgt, const float* drf, int B, int D, int V,
                          const int32_t* draft_ids, const float* u_accept, const float* u_resample,
                          int32_t* accepted_len, int32_t* emitted) {
@@ -504,32 +572,36 @@ int orc_verify_rejection(const float* tgt, const float* drf, int B, int D, int V
         for (int j = 0; j <= D; ++j) em[j] = -1;
         int k = 0;
         bool rejected = false;
+        VrRow rt, rd;
+        auto plain = [&](const float* t) {           // a draw from W~_t
+            auto wh = [&](int i) { return vr_w(t, rt, i) >> 32; };
+            uint64_t tot = 0;
+            for (int i = 0; i < V; ++i) tot += wh(i);
+            return draw_weights(V, wh, tot, u_resample[b]);
+        };
         for (; k < D; ++k) {
             const float* t = tgt + ((size_t)b * (D + 1) + k) * V;
             const float* d = drf + ((size_t)b * D + k) * V;
-            float mt, md; uint64_t Zt, Zd;
-            row_stats(t, V, &mt, &Zt);
-            row_stats(d, V, &md, &Zd);
-            int32_t x = draft_ids[(size_t)b * D + k];
+            vr_row(t, V, rt);
+            vr_row(d, V, rd);
+            const int32_t x = draft_ids[(size_t)b * D + k];
             bool acc = false;
-            if (x >= 0 && x < V && Zt > 0) {
-                u128 lhs = ((u128)wt(t, x, mt) * Zd) << 32;
-                u128 rhs = (u128)uniform32(u_accept[(size_t)b * D + k]) * ((u128)wt(d, x, md) * Zt);
+            if (x >= 0 && x < V && rt.Z > 0) {
+                const double lhs = (double)vr_w(t, rt, x) * u128_to_double(rd.Z);
+                const double rhs = (double)u_accept[(size_t)b * D + k] * (double)vr_w(d, rd, x) *
+                                   u128_to_double(rt.Z);
                 acc = lhs >= rhs;
             }
             if (!acc) {
-                // Residual max(0, p_t - p_d), scaled by Zt*Zd and shifted into 64 bits.
-                int shift = std::max(0, bitlen128((u128)Zt) + bitlen128((u128)Zd) - 63);
+                uint64_t zt, zd;
+                vr_z32(rt.Z, rd.Z, &zt, &zd);
                 auto res = [&](int i) -> uint64_t {
-                    u128 a = (u128)wt(t, i, mt) * Zd, c = (u128)wt(d, i, md) * Zt;
-                    return a > c ? (uint64_t)((a - c) >> shift) : 0;
+                    const uint64_t a = (vr_w(t, rt, i) >> 32) * zd, c = (vr_w(d, rd, i) >> 32) * zt;
+                    return a > c ? (a - c) >> 21 : 0;
                 };
                 uint64_t R = 0;
                 for (int i = 0; i < V; ++i) R += res(i);
-                int32_t tok;
-                if (R > 0) tok = draw_weights(V, res, R, u_resample[b]);
-                else tok = draw_weights(V, [&](int i) { return wt(t, i, mt); }, Zt, u_resample[b]);
-                em[k] = tok;
+                em[k] = R > 0 ? draw_weights(V, res, R, u_resample[b]) : plain(t);
                 rejected = true;
                 break;
             }
@@ -537,9 +609,8 @@ int orc_verify_rejection(const float* tgt, const float* drf, int B, int D, int V
         }
         if (!rejected) {
             const float* t = tgt + ((size_t)b * (D + 1) + D) * V;
-            float mt; uint64_t Zt;
-            row_stats(t, V, &mt, &Zt);
-            em[D] = draw_weights(V, [&](int i) { return wt(t, i, mt); }, Zt, u_resample[b]);
+            vr_row(t, V, rt);
+            em[D] = plain(t);
         }
         accepted_len[b] = k;
     }

@@ -372,3 +372,14 @@ def calc_next_token_id_omp4(row) -> int:
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(int(n))
+
+
+def vr_weights(row):
+    """Rejection verification's per-id weights W (uint64) and Z (int) of one row."""
+    x = np.ascontiguousarray(row, np.float32).reshape(-1)
+    W = np.empty(len(x), np.uint64)
+    Z2 = np.empty(2, np.uint64)
+    rc = lib().orc_vr_weights(_ptr(x), len(x), _ptr(W), _ptr(Z2))
+    if rc:
+        raise ValueError(f"orc_vr_weights rc={rc}")
+    return W, int(Z2[0]) + (int(Z2[1]) << 64)

@@ -18,7 +18,7 @@ def _declared():
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ["llima_argmax", "llima_sample", "llima_verify_greedy", "llima_verify_tree",
-              "llima_verify_rejection", "llima_verify_rejection_ex", "llima_score_logits",
+              "llima_verify_rejection", "llima_topk", "llima_score_logits",
               "llima_mtp_masked_argmax"]:
         assert n in names
 

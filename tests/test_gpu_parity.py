@@ -470,32 +470,6 @@ def test_verify_rejection_edges(gpu, oracle):
     assert eacc[0] == D                                     # identical rows accept every draft
 
 
-@pytest.mark.parametrize("B,D,V", [(16, 7, 128256), (3, 2, 70000), (2, 0, 9000)])
-def test_verify_rejection_help_path(gpu, oracle, B, D, V):
-    """help_after = 0: a row-pass workgroup that finds one of its row's chunk
-    maxima unpublished reads that chunk itself at once, so the path that bounds
-    every wait runs; the device counter shows it did, and the results are
-    unchanged."""
-    import torch
-    import llima_amd
-    _say("verify_rejection help path", B, D, V)
-    w = wl.speculative(B=B, D=D, V=V, seed=61 + V)
-    cnt = torch.full((1,), -1, dtype=torch.int32, device=gpu)
-    acc, em = llima_amd.verify_rejection(_t(w["target"], gpu), _t(w["draft"], gpu),
-                                         _t(w["draft_ids"], gpu), _t(w["u_accept"], gpu),
-                                         _t(w["u_resample"], gpu), help_after=0, help_count=cnt)
-    eacc, eem = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
-                                        w["u_resample"])
-    assert (_np(acc) == eacc).all(), (_np(acc), eacc)
-    assert (_np(em) == eem).all()
-    n = int(_np(cnt)[0])
-    _say("help-path chunk reads", n)
-    assert n >= 0
-    if B * (2 * D + 1) >= 64:
-        # hundreds of rows of 16 chunks: some waiter polls before a partner publishes
-        assert n > 0
-
-
 def test_two_streams_use_separate_workspaces(gpu, oracle):
     """Two sampling calls on two streams with no synchronisation between them
     (each stream gets its own scratch), both checked against the oracle."""
@@ -560,8 +534,7 @@ def test_empty_batches(gpu, oracle):
 def test_workspace_garbage(gpu, oracle):
     """Every entry point gives the same results on a workspace that holds
     arbitrary bytes (all ones, then random): nothing in it is read before the
-    call wrote it (the rejection row pass marks its own slots unpublished
-    first)."""
+    call wrote it."""
     import torch
     import llima_amd
     from llima_amd.sampler import Workspace

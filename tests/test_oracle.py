@@ -434,6 +434,33 @@ def test_rejection_matches_float64_model(oracle):
     assert n >= 14
 
 
+def test_rejection_weights_chunked_definition(oracle):
+    """The chunked weights sum exactly to Z, equal w_i * 2^27 in the maximum's
+    chunk, and approximate the softmax to ~1e-6 relative (exp's error) plus an
+    absolute 2^-27: the 2^-36 step of w and the chunk factor's rounding, at
+    most half a step of 2^27 relative to the row maximum's weight."""
+    rng = np.random.default_rng(12)
+    for V in [5, 8192, 8193, 40000]:
+        x = rng.normal(0, 4, V).astype(np.float32)
+        x[rng.integers(0, V)] += 10.0
+        W, Z = oracle.vr_weights(x)
+        assert sum(int(w) for w in W) == Z
+        j = int(np.argmax(x))
+        assert int(W[j]) == (1 << 36) << 27
+        p = np.exp(x.astype(np.float64) - x.max())
+        p /= p.sum()
+        q = W.astype(np.float64) / float(Z)
+        assert (np.abs(q - p) <= 2e-6 * p + 2.0**-27).all()
+    # a row spread over chunks with its maximum in the last one; one-hot and -inf rows
+    x = np.full(3 * 8192, -1.0, np.float32)
+    x[-1] = 3.0
+    W, Z = oracle.vr_weights(x)
+    assert int(W[-1]) == 1 << 63 and int(W[0]) == oracle.weight(-1.0, -1.0) * \
+        int(np.rint(np.ldexp(np.float32(oracle.exp_neg(-4.0)), 27)))
+    W, Z = oracle.vr_weights(np.full(100, -np.inf, np.float32))
+    assert Z == 0 and not W.any()
+
+
 def test_rejection_output_distribution_is_target(oracle):
     """Leviathan et al.: the first emitted token is distributed as p_t whatever
     p_d is.  Exhaustive over draft tokens and fine uniform grids, tiny V."""
