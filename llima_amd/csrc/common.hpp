@@ -81,6 +81,36 @@ __device__ __forceinline__ uint64_t weight(float x, float xmax) {
     return x == xmax ? LLIMA_W_ONE : (d >= -26.0f ? w : 0ull);
 }
 
+// weight(x, xmax) for a finite xmax, as the integral float it converts
+// (W < 2^37, exact in fp32; sums of at most 2^16 of them are exact in double).
+// exp_neg's steps with three folds that leave every result unchanged:
+//   * d is clamped at -26 (NaN included) with no select after, since
+//     rint(e^-26 2^36) = rint(0.35) = 0;
+//   * the factor 2^36 is in the polynomial's coefficients: scaling every
+//     coefficient by a power of two scales every rounded step by it (the
+//     smallest, 2^36/5040, is far from the subnormals), and p 2^36 2^n with
+//     n >= -38 stays normal, so ldexp(p 2^36, n) = ldexp(ldexp(p, n), 36);
+//   * x == xmax needs no select: d = 0 gives n = 0, r = 0 and p = 2^36 exactly.
+#define LLIMA_TWO36 68719476736.0f
+__device__ __forceinline__ float weight_f(float x, float xmax) {
+    const float d = __builtin_fmaxf(x - xmax, -26.0f);   // fmaxf(NaN, -26) = -26
+    const float kLog2e = 1.44269502162933349609375f;
+    const float kLn2Hi = 0.693145751953125f;
+    const float kLn2Lo = 1.428606765330187045e-06f;
+    const float n = __builtin_rintf(d * kLog2e);
+    float r = __builtin_fmaf(n, -kLn2Hi, d);
+    r = __builtin_fmaf(n, -kLn2Lo, r);
+    float p = 1.98412698412698412698e-04f * LLIMA_TWO36;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f * LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f * LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f * LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f * LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, 0.5f * LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, LLIMA_TWO36);
+    p = __builtin_fmaf(p, r, LLIMA_TWO36);
+    return __builtin_rintf(__builtin_ldexpf(p, (int)n));
+}
+
 // rint(v * 2^32) clamped to [0, 2^32].
 __device__ __forceinline__ uint64_t frac32(float v) {
     double s = (double)v * 4294967296.0;

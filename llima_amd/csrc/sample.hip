@@ -60,6 +60,9 @@ namespace llima {
 #define SMP_SPARSE 12                              // lanes above the bound for a sparse sweep wave
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
+#define SMP_PBINS 256                              // top-p value bins: floor(8 (xmax - x)), the last open
+#define SMP_PBIN_SCALE 8.0f
+#define SMP_PBIN_SLOTS (SMP_PBINS + 64)            // + a spare bin per lane
 
 #define HF_OVERFLOW 1u
 
@@ -71,6 +74,25 @@ namespace llima {
 // SMP_SENTINEL, key 0.  Greedy rows: slot 1 holds (key << 32 | ~index) of the
 // chunk maximum.
 #define SMP_SENTINEL 0ull                          // key 0: no candidate
+
+// Phase trace of sample_finish, compiled in only with -DLLIMA_FINISH_TRACE:
+// thread 0 of each of the first SMP_TRACE_ROWS workgroups clears its row of
+// fin_trace, then stores the wall clock (100 MHz) at each mark it passes
+// (marks 14 and 15 hold counts); llima_finish_trace_read copies the table to
+// the host.
+#define SMP_TRACE_ROWS 512
+#define SMP_TRACE_MARKS 16
+#ifdef LLIMA_FINISH_TRACE
+__device__ unsigned long long fin_trace[SMP_TRACE_ROWS][SMP_TRACE_MARKS];
+#define FIN_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = wall_clock64(); } while (0)
+#define FIN_NOTE(i, v) do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = (v); } while (0)
+#define FIN_BEGIN() do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) { \
+        for (int m_ = 1; m_ < SMP_TRACE_MARKS; ++m_) fin_trace[blockIdx.x][m_] = 0; } FIN_MARK(0); } while (0)
+#else
+#define FIN_BEGIN() do { } while (0)
+#define FIN_MARK(i) do { } while (0)
+#define FIN_NOTE(i, v) do { } while (0)
+#endif
 struct SampleParams {
     const void* logits;
     int64_t row_stride;
@@ -615,7 +637,7 @@ struct FinShared {
     uint32_t r32[8][LLIMA_WAVES];
     uint32_t sel[4];
     uint64_t sel64[2];
-    uint32_t hflags, hgkey, hn;
+    uint32_t hflags, hgkey, hn, lcount;
     uint64_t hgreedy;
     uint32_t hc[LLIMA_WG];                           // survivors' history occurrences
     BlockScratch bs;
@@ -744,6 +766,87 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
     }
     __syncthreads();
     return d.prefix;
+}
+
+// Top-p boundary over value bins: the key fin_topp_desc returns, found with one
+// round of 64-bit LDS atomics ((mass << 13) + count) into bins of 1/8 nat below
+// the maximum (bin floor(8 (xmax - x)), a monotone function of the key, the
+// last bin open), then inside the one bin that holds the boundary: the last
+// non-empty bin whose mass above, times 2^32, is below p32 Z.  Its members (at
+// most 64) are ranked pairwise in every wave.  bins: SMP_PBIN_SLOTS zeroed
+// slots (a spare per lane), sh.lcount zero on entry.  Returns 0, with every
+// wave taking the same branch, when the maximum is infinite or the boundary
+// bin holds more than 64 values: the caller then runs fin_topp_desc.
+template <int EPT>
+__device__ __forceinline__ uint32_t fin_topp_bins(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
+                                                  uint64_t p32, uint32_t kmax, uint64_t* bins,
+                                                  FinShared& sh) {
+    const uint32_t lane = lane_id();
+    const float xmax = key_f32(kmax);
+    if (!(xmax < __builtin_inff())) return 0u;      // uniform
+    uint32_t bn[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const float d = __builtin_fminf((xmax - key_f32(key[j])) * SMP_PBIN_SCALE, (float)(SMP_PBINS - 1));
+        const uint32_t b = (uint32_t)d;                 // d in [0, SMP_PBINS - 1] for a present key
+        bn[j] = key[j] ? b : 0xFFFFFFFFu;
+        atomicAdd((unsigned long long*)&bins[key[j] ? b : SMP_PBINS + lane],
+                  (unsigned long long)((w[j] << 13) | 1ull));
+    }
+    __syncthreads();
+    // every wave reads every bin: lane l holds bins 4 l .. 4 l + 3
+    uint64_t m[4];
+    uint32_t cn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t v = bins[4u * lane + (uint32_t)i];
+        m[i] = v >> 13;
+        cn[i] = (uint32_t)(v & 0x1FFFu);
+    }
+    const uint64_t ms = m[0] + m[1] + m[2] + m[3];
+    const uint64_t inc = wave_incl_scan_u64(ms);
+    // a * 2^32 < p32 Z  <=>  a < ceil(p32 Z / 2^32)
+    const llima_u128 PZ = (llima_u128)p32 * readlane63(inc);
+    const uint64_t lim = (uint64_t)((PZ + 0xFFFFFFFFull) >> 32);
+    uint64_t a = inc - ms;                           // mass of the bins before this lane's
+    int qb = -1;
+    uint64_t qa = 0;
+    uint32_t qc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool q = cn[i] > 0u && a < lim;
+        qb = q ? (int)(4u * lane) + i : qb;
+        qa = q ? a : qa;
+        qc = q ? cn[i] : qc;
+        a += m[i];
+    }
+    const uint64_t bq = ballot(qb >= 0);
+    if (bq == 0) return kmax;                        // none qualifies (p32 Z < 2^32)
+    const uint32_t L = 63u - (uint32_t)__builtin_clzll(bq);
+    const uint32_t bstar = (uint32_t)readlane((uint32_t)qb, L), nb = readlane(qc, L);
+    const uint64_t above = readlane64(qa, L);
+    if (nb > 64u) return 0u;                         // uniform: every wave read the same bins
+    // the boundary bin's members -> sh.sv[0, nb): one atomic per thread
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) mine += bn[j] == bstar ? 1u : 0u;
+    if (mine) {
+        uint32_t o = atomicAdd(&sh.lcount, mine);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (bn[j] == bstar) sh.sv[o++] = llima_u32x4{key[j], 0u, (uint32_t)w[j], (uint32_t)(w[j] >> 32)};
+    }
+    __syncthreads();
+    const llima_u32x4 me = lane < nb ? sh.sv[lane] : llima_u32x4{0u, 0u, 0u, 0u};
+    uint64_t ab = above;
+    for (uint32_t i = 0; i < nb; ++i) {
+        const llima_u32x4 o = sh.sv[i];
+        ab += o.x > me.x ? (((uint64_t)o.w << 32) | o.z) : 0ull;
+    }
+    const bool q = lane < nb && ab < lim;
+    // the top member always qualifies (its mass above is the bin's); the
+    // boundary is the smallest qualifying key
+    return ~wave_max_u32(q ? ~me.x : 0u);
 }
 
 __device__ __forceinline__ void write_result(const SampleParams& P, int row, int32_t id, float prob) {
@@ -1027,6 +1130,7 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
         sh.pc[e][wave][lane] = gt[e] | (eq[e] << 16);
     }
     __syncthreads();
+    FIN_MARK(10);
     // tau: the key of a candidate with gt < k <= gt + eq; Z (the mass kept by
     // top-k) = mass above tau + mass equal to it, read off that candidate
     uint32_t tk = 0;
@@ -1056,6 +1160,7 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
         Zk = readlane64(zt, L);
     }
     if (c.k > 0 && tcut && !(tau > tcut)) return false;   // uniform: every wave has tau
+    FIN_MARK(11);
 
     bool fin[NPL];
     uint64_t zk = 0;
@@ -1136,6 +1241,7 @@ __device__ __forceinline__ bool fin_small(const SampleParams& P, int row, const 
             }
         }
     }
+    FIN_MARK(12);
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
 #pragma unroll
@@ -1150,8 +1256,9 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t id) {
     return (id * 2654435761u) >> (32 - 12);         // SMP_HASH = 4096 slots
 }
 
-// Candidates f = t + 256 j (j < EPT) of the N gathered in sh.u.cand (id
-// order).  False when the row needs the full-row path (nothing written yet).
+// Candidates f = EPT t + j (j < EPT) of the N gathered in sh.u.cand (id
+// order), so a thread's candidates are consecutive and (thread, j) order is id
+// order.  False when the row needs the full-row path (nothing written yet).
 template <int EPT>
 __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const RowCfg& c, uint32_t N,
                           uint32_t gkey, const int32_t (&hid)[SMP_HBATCH], FinShared& sh) {
@@ -1161,7 +1268,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     // every read at once from a clamped slot, the element past N made -inf
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        const uint32_t f = t + (uint32_t)j * LLIMA_WG;
+        const uint32_t f = t * EPT + (uint32_t)j;
         const uint32_t fc = f < N ? f : 0u;
         const uint64_t q = sh.u.cand[fc + (fc >> 4)];
         x[j] = f < N ? key_f32((uint32_t)(q >> 32)) : -__builtin_inff();
@@ -1181,7 +1288,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             slot[j] = 0;
-            if (t + (uint32_t)j * LLIMA_WG < N) {
+            if (t * EPT + (uint32_t)j < N) {
                 uint32_t h = hash_slot(id[j]);
                 for (int p = 0; p < SMP_HASH; ++p) {
                     const uint32_t prev = atomicCAS(&sh.u.hash.key[h], 0u, id[j] + 1u);
@@ -1210,7 +1317,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
-            if (t + (uint32_t)j * LLIMA_WG < N) {
+            if (t * EPT + (uint32_t)j < N) {
                 const uint32_t cn = sh.u.hash.cnt[slot[j]];
                 if (cn) x[j] = penalize(x[j], cn, c);
             }
@@ -1248,8 +1355,12 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
             nkmn = sh.r32[1][w] > nkmn ? sh.r32[1][w] : nkmn;
             nf += sh.r32[2][w];
         }
+        // the candidates are in registers: sh.u holds the top-p bins from here
+        for (uint32_t i = t; i < SMP_PBIN_SLOTS; i += LLIMA_WG) sh.u.cand[i] = 0;
+        if (t == 0) sh.lcount = 0;
         __syncthreads();
     }
+    FIN_MARK(5);
     const uint32_t kmax = kmx, kmin = ~nkmn;
     if (nf == 0) {
         if (gkey) return false;                      // skipped values may be finite
@@ -1307,6 +1418,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         if (dg >= -26.0f || !zero_weight_irrelevant(P, c)) return false;
     }
     if (c.k > 0 && exact && gkey && !(lowkey > gkey)) return false;
+    FIN_MARK(6);
 
     // ---- values at or above lowkey: at most 64 -> pairwise small path
     uint32_t ns = 0;
@@ -1314,6 +1426,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     for (int j = 0; j < EPT; ++j) ns += key[j] && key[j] >= lowkey ? 1u : 0u;
     uint32_t nst;
     const uint32_t so = block_excl_scan_u32(ns, &nst, sh.bs);
+    FIN_MARK(7);
     if (nst <= SMP_SMALL) {
         uint32_t o = so;
 #pragma unroll
@@ -1325,7 +1438,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
             }
         }
         __syncthreads();
-        return fin_small<1, false>(P, row, c, nst, kmax, c.k > 0 ? gkey : 0u, sh.sv, false, sh);
+        return fin_small<1, false>(P, row, c, nst, kmax, c.k > 0 ? gkey : 0u, sh.sv, true, sh);
     }
     // more than 64 remain only when lowkey is tau (ties) or there is no top-k
 
@@ -1333,13 +1446,28 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     const uint32_t tau = lowkey;
     uint64_t w[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        key[j] = key[j] < tau ? 0u : key[j];
-        const uint64_t wj = weight(key_f32(key[j]), xmax);   // no branch: key 0 is NaN, weight 0
-        w[j] = key[j] ? wj : 0ull;
+    for (int j = 0; j < EPT; ++j) key[j] = key[j] < tau ? 0u : key[j];
+    if (xmax < __builtin_inff()) {                   // uniform; key 0 decodes to NaN, weight 0
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const uint64_t wj = f32_integral_to_u64(weight_f(key_f32(key[j]), xmax));
+            w[j] = key[j] ? wj : 0ull;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const uint64_t wj = weight(key_f32(key[j]), xmax);
+            w[j] = key[j] ? wj : 0ull;
+        }
     }
+    FIN_MARK(8);
     uint32_t theta = 0;
-    if (c.p < 1.0f) theta = fin_topp_desc<EPT>(key, w, frac32(c.p), tau > kmin ? tau : kmin, kmax, sh);
+    if (c.p < 1.0f) {
+        theta = fin_topp_bins<EPT>(key, w, frac32(c.p), kmax, sh.u.cand, sh);
+        if (theta == 0u)                             // an infinite maximum or a crowded bin
+            theta = fin_topp_desc<EPT>(key, w, frac32(c.p), tau > kmin ? tau : kmin, kmax, sh);
+    }
+    FIN_MARK(9);
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
     uint32_t fmask = 0;
 #pragma unroll
@@ -1348,54 +1476,33 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
         fmask |= f ? (1u << j) : 0u;
         w[j] = f ? w[j] : 0ull;
     }
-    // final weights into LDS in id order (every slot below EPT * 256 <=
-    // SMP_FIN_CAP: elements past N hold weight 0), then 16 consecutive ids per
-    // thread (those past EPT * 256 are 0)
-    __syncthreads();
+    // the draw: a thread's candidates are consecutive ids, so one scan of the
+    // per-thread sums orders the whole row
+    uint64_t mysum = 0;
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        const uint32_t f = t + (uint32_t)j * LLIMA_WG;
-        sh.u.cand[f + (f >> 4)] = w[j];
-    }
-    __syncthreads();
-    uint64_t ws[16], mysum = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t f = t * 16u + (uint32_t)j;
-        const uint32_t fc = f < EPT * LLIMA_WG ? f : 0u;
-        const uint64_t v = sh.u.cand[fc + (fc >> 4)];
-        ws[j] = f < EPT * LLIMA_WG ? v : 0ull;
-        mysum += ws[j];
-    }
+    for (int j = 0; j < EPT; ++j) mysum += w[j];
+    FIN_MARK(10);
     uint64_t Zf;
     const uint64_t before = block_excl_scan_u64(mysum, &Zf, sh.bs);
+    FIN_MARK(11);
     if (Zf == 0) {
         if (t == 0) write_result(P, row, -1, 0.0f);
     } else {
         const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
         if (mysum > 0 && before <= target && target < before + mysum) {
             uint64_t acc = before;
-            int jt = -1;
-            uint64_t wt = 0;
+            bool hit = false;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (jt < 0 && ws[j] && acc <= target && target < acc + ws[j]) { jt = j; wt = ws[j]; }
-                acc += ws[j];
+            for (int j = 0; j < EPT; ++j) {
+                if (!hit && w[j] && acc <= target && target < acc + w[j]) {
+                    write_result(P, row, (int32_t)id[j], (float)((double)w[j] / (double)Zf));
+                    hit = true;
+                }
+                acc += w[j];
             }
-            const uint32_t f = t * 16u + (uint32_t)jt;
-            sh.sel[3] = f;
-            sh.sel64[1] = wt;
         }
     }
-    __syncthreads();
-    if (Zf > 0) {
-        // element f lives in thread f % 256, slot f / 256, which holds its id
-        const uint32_t ftok = sh.sel[3];
-#pragma unroll
-        for (int j = 0; j < EPT; ++j)
-            if (t + (uint32_t)j * LLIMA_WG == ftok)
-                write_result(P, row, (int32_t)id[j], (float)((double)sh.sel64[1] / (double)Zf));
-    }
+    FIN_MARK(12);
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
 #pragma unroll
@@ -1444,6 +1551,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             }
         }
         __syncthreads();
+        FIN_MARK(6);
         uint32_t cn[2] = {0u, 0u};
         // hv: this lane's history id; inlen: lanes whose entry lies before hlen
         auto count_pass = [&](uint32_t hv, uint64_t m, uint64_t inlen) {   // m: lanes that passed
@@ -1474,6 +1582,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             const uint64_t inlen = ballot(i < c.hlen);
             count_pass(hv, ballot((bm[h >> 5] >> (h & 31u)) & 1u) & inlen, inlen);
         }
+        FIN_MARK(7);
         // ids outside [0, V) match no survivor
 #pragma unroll
         for (int e = 0; e < 2; ++e)
@@ -1486,6 +1595,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             x[e] = cn ? xp : x[e];
         }
     }
+    FIN_MARK(8);
     // every wave: temperature, keys and weights of the survivors -> its own
     // copy sh.sv2[wave] (no barrier before the pairwise passes)
     uint32_t key[2], kmax = 0;
@@ -1503,6 +1613,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
         sh.sv2[wave][(uint32_t)e * 64u + lane] = llima_u32x4{key[e], id[e], (uint32_t)w, (uint32_t)(w >> 32)};
     }
     __builtin_amdgcn_wave_barrier();                 // the wave's LDS writes precede its reads
+    FIN_MARK(9);
     if (kmax == 0u) {
         if (gkey || lowkey > 1u) return false;
         if (t == 0) write_result(P, row, -1, 0.0f);
@@ -1542,6 +1653,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
         for (int i = 0; i < 2; ++i)                          // the 2^16-bit id bitmap
             ((llima_u32x4*)sh.u.hash.key)[t + i * LLIMA_WG] = llima_u32x4{0u, 0u, 0u, 0u};
     }
+    FIN_MARK(3);
     uint32_t lowkey = 1u;
     if (c.k > 0) {
         if (N < (uint32_t)c.k) {
@@ -1628,6 +1740,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
         const float dg = key_f32(gkey) - key_f32(kmax) / c.T;
         if (dg >= -26.0f || !zero_weight_irrelevant(P, c)) return false;
     }
+    FIN_MARK(4);
     uint32_t ns = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ns += kr[j] && kr[j] >= lowkey ? 1u : 0u;
@@ -1654,12 +1767,15 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
     }
     sh.hc[t] = 0;
     __syncthreads();
+    FIN_MARK(5);
+    FIN_NOTE(15, 1);
     return fin_survivors(P, row, c, nst, lowkey, gkey, hid, sh);
 }
 
 template <typename TL>
 __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     __shared__ FinShared sh;
+    FIN_BEGIN();
     const int row = blockIdx.x;
     const RowCfg c = load_cfg(P, row);
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -1722,6 +1838,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         const float gt0 = g0 / c.T;
         const uint32_t gk = (hdr & !c.greedy & (g0 > -__builtin_inff())) ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
         const uint64_t gr = hdr ? ((uint64_t)q[0].w << 32) | q[0].z : 0ull;
+        FIN_MARK(1);
         if (hdr) sh.ccount[ch] = count;
         {
             const uint32_t a = wave_max_u32(kmx), b = wave_max_u32(nkmn), s2 = wave_sum_u32(n);
@@ -1747,6 +1864,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
             best = sh.r64[1][w] > best ? sh.r64[1][w] : best;
         }
 
+        FIN_MARK(2);
+        FIN_NOTE(14, N);
         if (c.greedy) {
             const bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
             const uint32_t tok = ok ? ~(uint32_t)best : 0xFFFFFFFFu;
@@ -1782,6 +1901,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
                 if (lane == 63) sh.hn = inc;
             }
             __syncthreads();
+            FIN_MARK(3);
+            FIN_NOTE(15, 2);
             const uint32_t NG = sh.hn;
             if (NG <= SMP_FIN_CAP) {
                 if (mine) {
@@ -1816,12 +1937,14 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
                 sh.hcnt[0][t] = 0; sh.hcnt[1][t] = 0;
                 sh.hmass[0][t] = 0; sh.hmass[1][t] = 0;
                 __syncthreads();
+                FIN_MARK(4);
                 done = NG <= 4u * LLIMA_WG ? fin_elems<4>(P, row, c, NG, gkey, hid, sh)
                                            : fin_elems<16>(P, row, c, NG, gkey, hid, sh);
             }
         }
     }
     if (__builtin_expect(!done, 0)) finish_full_row<TL>(P, row, c, sh);
+    FIN_MARK(13);
 }
 
 // ================================================================== host side
@@ -1853,6 +1976,15 @@ extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dty
     const size_t S = (size_t)((V + chunk_values(dtype) - 1) / chunk_values(dtype));
     return (size_t)B * S * SMP_REGION * sizeof(uint64_t);
 }
+
+#ifdef LLIMA_FINISH_TRACE
+// Copies the phase-trace table ([SMP_TRACE_ROWS][SMP_TRACE_MARKS] uint64) of
+// the current device to host memory (traced builds only).
+extern "C" int llima_finish_trace_read(unsigned long long* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(llima::fin_trace), sizeof(llima::fin_trace)) == hipSuccess
+               ? LLIMA_OK : LLIMA_E_HIP;
+}
+#endif
 
 extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V,
                             int64_t row_stride, const int32_t* history,

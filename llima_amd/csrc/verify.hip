@@ -138,37 +138,6 @@ __device__ __forceinline__ uint32_t chunk_factor(uint32_t mck, uint32_t Mk) {
     return (uint32_t)__builtin_rintf(__builtin_ldexpf(exp_neg(d), VR_FBITS));
 }
 
-// weight(x, xmax) for a finite xmax, as the integral float it converts
-// (W < 2^37, exact in fp32): sums of at most 2^16 of them are exact in double,
-// so the chunk sums skip the per-value float -> uint64 conversion.  exp_neg's
-// steps with three folds that leave every result unchanged:
-//   * d is clamped at -26 (NaN included) with no select after, since
-//     rint(e^-26 2^36) = rint(0.35) = 0;
-//   * the factor 2^36 is in the polynomial's coefficients: scaling every
-//     coefficient by a power of two scales every rounded step by it (the
-//     smallest, 2^36/5040, is far from the subnormals), and p 2^36 2^n with
-//     n >= -38 stays normal, so ldexp(p 2^36, n) = ldexp(ldexp(p, n), 36);
-//   * x == xmax needs no select: d = 0 gives n = 0, r = 0 and p = 2^36 exactly.
-#define VR_TWO36 68719476736.0f
-__device__ __forceinline__ float weight_f(float x, float xmax) {
-    const float d = __builtin_fmaxf(x - xmax, -26.0f);   // fmaxf(NaN, -26) = -26
-    const float kLog2e = 1.44269502162933349609375f;
-    const float kLn2Hi = 0.693145751953125f;
-    const float kLn2Lo = 1.428606765330187045e-06f;
-    const float n = __builtin_rintf(d * kLog2e);
-    float r = __builtin_fmaf(n, -kLn2Hi, d);
-    r = __builtin_fmaf(n, -kLn2Lo, r);
-    float p = 1.98412698412698412698e-04f * VR_TWO36;
-    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f * VR_TWO36);
-    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f * VR_TWO36);
-    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f * VR_TWO36);
-    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f * VR_TWO36);
-    p = __builtin_fmaf(p, r, 0.5f * VR_TWO36);
-    p = __builtin_fmaf(p, r, VR_TWO36);
-    p = __builtin_fmaf(p, r, VR_TWO36);
-    return __builtin_rintf(__builtin_ldexpf(p, (int)n));
-}
-
 // ------------------------------------------------------------------ row pass
 // One workgroup per (row, chunk): the chunk's maximum, its sum of w (relative to
 // that maximum) and w at the row's draft token when it lies in the chunk.
@@ -189,7 +158,7 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
         double sd = 0.0;                                 // exact: 32 terms below 2^37
         if (xm == __builtin_inff()) {                    // w = 2^36 at every +inf, else 0
 #pragma unroll
-            for (int e = 0; e < VR_E; ++e) sd += v[e] == xm ? (double)VR_TWO36 : 0.0;
+            for (int e = 0; e < VR_E; ++e) sd += v[e] == xm ? (double)LLIMA_TWO36 : 0.0;
         } else {
 #pragma unroll
             for (int e = 0; e < VR_E; ++e) sd += (double)weight_f(v[e], xm);
@@ -391,7 +360,7 @@ __device__ __forceinline__ DrawChunk draw_chunk(uint32_t mck, uint32_t Mk) {
 // double and the conversion to uint32 truncates it.  In a chunk whose maximum
 // is +inf, w is 2^36 at the +inf values and 0 elsewhere.
 __device__ __forceinline__ uint32_t draw_weight(float x, const DrawChunk& c) {
-    const float w = c.inf ? (x == __builtin_inff() ? VR_TWO36 : 0.0f) : weight_f(x, c.xm);
+    const float w = c.inf ? (x == __builtin_inff() ? LLIMA_TWO36 : 0.0f) : weight_f(x, c.xm);
     return (uint32_t)((double)w * c.fs);
 }
 
