@@ -49,7 +49,8 @@ def parse():
                     choices=["batched_penalties", "single_row", "constrained",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
-                             "lm_head_argmax", "lm_head_argmax_b64"])
+                             "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
+                             "lm_head_argmax_b256"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -12,7 +12,7 @@
 //
 // At decode batch sizes the product is bound by reading the weights (V H 2
 // bytes, read once per pass of up to 8 hidden rows); batches that would need
-// more than one such pass take the MFMA tiling further down (one pass per 64
+// more than one such pass take the MFMA tiling further down (one pass per 256
 // rows).
 //
 // lmh_rows: 512-thread workgroups; the pass's hidden rows (NB of them) are
@@ -151,16 +151,17 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
 }
 
 // ------------------------------------------------------------------ MFMA path
-// Batches wider than one GEMV pass: v_mfma_f32_32x32x8_bf16 tiles, the weight read
-// once per 64 hidden rows.  Operand layout of the instruction (checked on the
-// GPU): lane l supplies row (A) or column (B) l % 32 and 4 values of k;
-// accumulator element i of lane l is C[i % 4 + 8 (i / 4) + 4 (l / 32)][l % 32].
-// Step j of a 64-id chunk gives lane half g the ids 8 j + 4 g .. 8 j + 4 g + 3,
-// the same for both operands, so every id of the chunk is used once; the order
-// of the fp32 sum over k is not the GEMV path's.
-typedef short lmh_s4 __attribute__((ext_vector_type(4)));
+// Batches wider than one GEMV pass: gfx950's v_mfma_f32_32x32x16_bf16 tiles,
+// the weight read once per pass of up to 256 hidden rows.  Lane l supplies row
+// (A: a hidden row) or column (B: a vocab row) l % 32 and 8 consecutive values
+// of k; the k assignment only has to be the same for both operands, and step s
+// of a 64-id chunk gives lane half g the ids 16 s + 8 g .. 16 s + 8 g + 7, so
+// every id of the chunk is used once.  Accumulator element i of lane l is
+// C[i % 4 + 8 (i / 4) + 4 (l / 32)][l % 32].  The order of the fp32 sum over k
+// is not the GEMV path's.
+typedef __bf16 lmh_b8 __attribute__((ext_vector_type(8)));
 typedef float lmh_acc __attribute__((ext_vector_type(16)));
-#define LMH_MB 64                      // hidden rows per pass
+#define LMH_MB 256                     // hidden rows per pass at most
 
 __device__ __forceinline__ uint64_t lmh_key(float s, int n, int V) {
     return s == s && n < V ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)n : 0ull;
@@ -178,90 +179,116 @@ __device__ __forceinline__ uint64_t half_max_u64(uint64_t v) {
     return v;
 }
 
-// Workgroup tile: 128 vocab rows (one 32-row tile per wave) x the pass's 64
-// hidden rows; k in chunks of 64 ids (128 bytes of a row), each chunk read with
-// coalesced 16-byte loads (8 threads per row: whole 128-byte lines) into LDS
-// rows padded to LMH_LDSR bytes, double-buffered with one barrier per chunk;
-// the next chunk's loads are in flight while the current one feeds the MFMAs.
-#define LMH_KC 64
-#define LMH_LDSR 136                   // bytes per staged row: 128 + 8 (2-way banks at most)
-#define LMH_WR 128                     // vocab rows per workgroup
+// Workgroup tile: 32 NWN vocab rows x 64 WM hidden rows, 64 NWN WM threads.
+// Wave w computes vocab rows 32 (w % NWN) .. + 31 against hidden rows
+// 64 (w / NWN) .. + 63 (two 32 x 32 accumulators); the WM groups of waves share
+// the staged weights, the NWN vocab tiles the staged hidden rows.  k in chunks of 64 ids (128 bytes of a row), each read with
+// coalesced 16-byte loads (8 threads per row: whole 128-byte lines) and taken
+// global -> registers -> LDS (rows padded by 16 bytes, double-buffered,
+// one barrier per chunk).  The registers form a ring of R chunks, so R chunks
+// are in flight while one feeds the MFMAs: a chunk's loads are requested R
+// iterations before it is staged.
+#define LMH_KC 64                      // the H multiple the MFMA path needs
 
-__global__ __launch_bounds__(LLIMA_WG) void lmh_mfma(LmhParams P, int b0, int nb) {
-    __shared__ __align__(16) uint8_t lw[2][LMH_WR * LMH_LDSR];
-    __shared__ __align__(16) uint8_t lx[2][LMH_MB * LMH_LDSR];
+template <int NWN, int WM, int R, int KC>
+__global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, int nb) {
+    constexpr int NT = 64 * NWN * WM;                        // threads
+    constexpr int WR = 32 * NWN;                             // vocab rows of the workgroup
+    constexpr int M = 64 * WM;                               // hidden rows of the pass
+    constexpr int PPR = KC / 8;                              // 16-byte pieces per row per chunk
+    constexpr int LDSR = 2 * KC + 16;                        // bytes per staged row (16-byte aligned)
+    constexpr int WQ = WR * PPR / NT;                        // weight pieces per thread per chunk
+    constexpr int XQ = M * PPR / NT;                         // hidden pieces per thread per chunk
+    static_assert(WQ * NT == WR * PPR && XQ * NT == M * PPR, "pieces split evenly");
+    __shared__ __align__(16) uint8_t lw[2][WR * LDSR];
+    __shared__ __align__(16) uint8_t lx[2][M * LDSR];
     const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r = lane & 31;
-    const int n0 = (int)blockIdx.x * LMH_WR;
-    const int H = P.H, V = P.V, nch = H / LMH_KC;
-    // global -> LDS mapping: thread t, row (t >> 3) + 32 q, 16-byte piece t & 7
-    const int pr = t >> 3, pc = t & 7;
-    const uint16_t* gw[4];
+    const int wn = wave % NWN, wm = wave / NWN;              // vocab tile, hidden group
+    const int n0 = (int)blockIdx.x * WR;
+    const int H = P.H, V = P.V, nch = H / KC;
+    // global -> LDS mapping: piece p = t + NT q is row p / PPR, 16-byte column p % PPR
+    const int pc = t % PPR;
+    const uint16_t* gw[WQ];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int n = n0 + pr + 32 * q;                      // rows past V read row V - 1
+    for (int q = 0; q < WQ; ++q) {
+        const int n = n0 + (t + NT * q) / PPR;               // rows past V read row V - 1
         gw[q] = P.weight + (size_t)(n < V ? n : V - 1) * H + pc * 8;
     }
-    const uint16_t* gx[2];
+    const uint16_t* gx[XQ];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int m = pr + 32 * q;                           // rows past nb read row b0
+    for (int q = 0; q < XQ; ++q) {
+        const int m = (t + NT * q) / PPR;                    // rows past nb read row b0
         gx[q] = P.hidden + (size_t)(b0 + (m < nb ? m : 0)) * H + pc * 8;
     }
-    llima_u32x4 rw[4], rx[2];
-    auto fetch = [&](int c) {
+    llima_u32x4 rw[R][WQ], rx[R][XQ];
+    auto fetch = [&](int c, llima_u32x4 (&fw)[WQ], llima_u32x4 (&fx)[XQ]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) rw[q] = __builtin_nontemporal_load((const llima_u32x4*)(gw[q] + c * LMH_KC));
+        for (int q = 0; q < WQ; ++q) fw[q] = __builtin_nontemporal_load((const llima_u32x4*)(gw[q] + c * KC));
 #pragma unroll
-        for (int q = 0; q < 2; ++q) rx[q] = *(const llima_u32x4*)(gx[q] + c * LMH_KC);
+        for (int q = 0; q < XQ; ++q) fx[q] = *(const llima_u32x4*)(gx[q] + c * KC);
     };
-    auto stage = [&](int buf) {                              // 8-byte LDS writes (rows are 8-aligned)
+    auto stage = [&](const llima_u32x4 (&fw)[WQ], const llima_u32x4 (&fx)[XQ], int buf) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint64_t* d = (uint64_t*)(lw[buf] + (pr + 32 * q) * LMH_LDSR + pc * 16);
-            d[0] = (uint64_t)rw[q].x | ((uint64_t)rw[q].y << 32);
-            d[1] = (uint64_t)rw[q].z | ((uint64_t)rw[q].w << 32);
-        }
+        for (int q = 0; q < WQ; ++q)
+            *(llima_u32x4*)(lw[buf] + (t + NT * q) / PPR * LDSR + pc * 16) = fw[q];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            uint64_t* d = (uint64_t*)(lx[buf] + (pr + 32 * q) * LMH_LDSR + pc * 16);
-            d[0] = (uint64_t)rx[q].x | ((uint64_t)rx[q].y << 32);
-            d[1] = (uint64_t)rx[q].z | ((uint64_t)rx[q].w << 32);
-        }
+        for (int q = 0; q < XQ; ++q)
+            *(llima_u32x4*)(lx[buf] + (t + NT * q) / PPR * LDSR + pc * 16) = fx[q];
     };
     lmh_acc acc[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[mt][i] = 0.0f;
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int c = 0; c < nch; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < nch) fetch(c + 1);
-        // 8 MFMA steps of 8 ids: lane half g supplies ids 8 j + 4 g .. + 3 of the chunk
-        const uint8_t* wrow = lw[buf] + (wave * 32 + r) * LMH_LDSR + 8 * g;
-        const uint8_t* x0 = lx[buf] + r * LMH_LDSR + 8 * g;
-        const uint8_t* x1 = lx[buf] + (32 + r) * LMH_LDSR + 8 * g;
+    // prologue: chunks 0 .. R-1 requested, chunk 0 staged
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const lmh_s4 bo = *(const lmh_s4*)(wrow + 16 * j);
-            const lmh_s4 a0 = *(const lmh_s4*)(x0 + 16 * j);
-            const lmh_s4 a1 = *(const lmh_s4*)(x1 + 16 * j);
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a0, bo, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a1, bo, acc[1], 0, 0, 0);
+    for (int i = 0; i < R; ++i) fetch(i < nch ? i : 0, rw[i], rx[i]);
+    stage(rw[0], rx[0], 0);
+    __syncthreads();
+    // Loads and stages are unconditional (a chunk index past the last reads
+    // the last chunk again, a stage past it fills a buffer nobody reads), so
+    // the loop body is straight-line code for the wait counters: staging chunk
+    // c + 1 waits only for its own loads, not for the R - 1 chunks behind it.
+    for (int c0 = 0; c0 < nch; c0 += R) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int c = c0 + i;                            // in LDS buffer c & 1
+            // ring slot i held chunk c (staged): it now receives chunk c + R
+            fetch(c + R < nch ? c + R : nch - 1, rw[i], rx[i]);
+            const int buf = c & 1;
+            if (c < nch) {                                   // uniform
+                const uint8_t* wrow = lw[buf] + (wn * 32 + r) * LDSR + 16 * g;
+                const uint8_t* xrow = lx[buf] + (wm * 64 + r) * LDSR + 16 * g;
+#pragma unroll
+                for (int s = 0; s < KC / 16; ++s) {
+                    const lmh_b8 bo = *(const lmh_b8*)(wrow + 32 * s);
+                    const lmh_b8 a0 = *(const lmh_b8*)(xrow + 32 * s);
+                    const lmh_b8 a1 = *(const lmh_b8*)(xrow + 32 * LDSR + 32 * s);
+                    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, bo, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, bo, acc[1], 0, 0, 0);
+                }
+            }
+            // chunk c + 1 (ring slot (i + 1) % R) into the other buffer, whose
+            // last readers passed the previous barrier
+            stage(rw[(i + 1) % R], rx[(i + 1) % R], buf ^ 1);
+            __syncthreads();
         }
-        if (c + 1 < nch) stage(buf ^ 1);                    // its last readers passed the previous barrier
-        __syncthreads();
+    }
+    // key slots past this grid's waves (a grid of 128-row tiles can leave up
+    // to 4 of the P.NW slots, counted in 256-row tiles): no logit
+    if (blockIdx.x == gridDim.x - 1) {
+        const int w0 = (int)gridDim.x * NWN, nx = P.NW - w0;
+        for (int e = t; e < nx * nb; e += NT)
+            P.keys[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0;
     }
     // epilogue: softcap, logits, and per hidden row the greatest key of the wave's 32 columns
-    const int wv = (int)blockIdx.x * LLIMA_WAVES + wave;
-    const int n = n0 + wave * 32 + r;
+    const int wv = (int)blockIdx.x * NWN + wn;
+    const int n = n0 + wn * 32 + r;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
+            const int m = wm * 64 + mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
             const float v = lmh_logit(acc[mt][i], P);
             if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
             const uint64_t best = half_max_u64(lmh_key(v, n, V));
@@ -319,9 +346,11 @@ static int lmh_rows_per_pass(int H) {
 
 using namespace llima;
 
-// Waves of the MFMA kernel: one per 32 vocab rows, whole workgroups.
+// Key slots per hidden row of the MFMA kernel: one per 32 vocab rows, in
+// whole 256-row tiles (a grid of 128-row tiles writes 0 to the up to 4 slots
+// it leaves).
 static int lmh_mfma_waves(int V) {
-    return (V + LMH_WR - 1) / LMH_WR * LLIMA_WAVES;
+    return (V + 255) / 256 * 8;
 }
 
 extern "C" size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V) {
@@ -357,10 +386,14 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     hipStream_t st = (hipStream_t)stream;
     if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
         P.NW = lmh_mfma_waves(V);
-        const dim3 gm((uint32_t)(P.NW / LLIMA_WAVES)), bm(LLIMA_WG);
+        const dim3 g128((uint32_t)((V + 127) / 128));
         for (int b0 = 0; b0 < B; b0 += LMH_MB) {
             const int nb = B - b0 < LMH_MB ? B - b0 : LMH_MB;
-            hipLaunchKernelGGL(lmh_mfma, gm, bm, 0, st, P, b0, nb);
+            // 128 vocab rows per workgroup; the narrowest tile that holds the
+            // pass: 64, 128 or 256 hidden rows
+            if (nb <= 64) hipLaunchKernelGGL((lmh_mfma<4, 1, 4, LMH_KC>), g128, dim3(256), 0, st, P, b0, nb);
+            else if (nb <= 128) hipLaunchKernelGGL((lmh_mfma<4, 2, 2, LMH_KC>), g128, dim3(512), 0, st, P, b0, nb);
+            else hipLaunchKernelGGL((lmh_mfma<4, 4, 2, LMH_KC>), g128, dim3(1024), 0, st, P, b0, nb);
         }
         hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
         return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;

@@ -178,4 +178,6 @@ WORKLOADS = {
     "mtp_masked_argmax": mtp_masked_argmax,
     "lm_head_argmax": lm_head_argmax,
     "lm_head_argmax_b64": lambda: dict(lm_head_argmax(B=64), name="lm_head_argmax_b64"),
+    "lm_head_argmax_b128": lambda: dict(lm_head_argmax(B=128), name="lm_head_argmax_b128"),
+    "lm_head_argmax_b256": lambda: dict(lm_head_argmax(B=256), name="lm_head_argmax_b256"),
 }

@@ -877,7 +877,9 @@ def _lm_head_check(ids, vals, logits, x, w, cap, bf16=True):
                                        (16, 4096, 128256, 0.0), (70, 1536, 3001, 30.0),
                                        (64, 2048, 50000, 0.0), (17, 512, 1000, 30.0),
                                        (20, 1000, 999, 0.0), (6, 4096, 70000, 30.0),
-                                       (1, 8192, 5000, 0.0), (3, 16384, 1000, 30.0)])
+                                       (1, 8192, 5000, 0.0), (3, 16384, 1000, 30.0),
+                                       (200, 512, 1000, 30.0), (300, 256, 777, 0.0),
+                                       (128, 1024, 2049, 0.0)])
 def test_lm_head_argmax_parity(gpu, B, H, V, cap):
     import llima_amd
     _say("lm head", B, H, V, cap)
