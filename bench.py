@@ -465,13 +465,19 @@ def cpu_baseline(name, w, seconds, greedy_variant):
 
 
 def _cpu_model():
-    """lscpu's model name (the /proc/cpuinfo line as a fallback)."""
+    """lscpu's model name with its CPU family and model numbers (the
+    /proc/cpuinfo line as a fallback)."""
     import subprocess
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {}
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                f[k.strip()] = v.strip()
+        if "Model name" in f:
+            extra = ", ".join("%s %s" % (k.lower(), f[k]) for k in ("CPU family", "Model") if k in f)
+            return f["Model name"] + (" (%s)" % extra if extra else "")
     except (OSError, subprocess.SubprocessError):
         pass
     try:

@@ -47,9 +47,9 @@ GATHER = {
     6: "top-k boundary rounds",
     7: "survivor count scanned",
     8: "weights computed",
-    9: "top-p threshold (radix rounds)",
-    10: "final weights to LDS in id order (2 barriers)",
-    11: "mass scan",
+    9: "top-p boundary (value bins, pairwise in one bin)",
+    10: "min-p cut, per-thread kept mass",
+    11: "id-order scan of the kept mass (block scan)",
     12: "draw written",
     13: "end",
 }
