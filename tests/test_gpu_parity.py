@@ -242,6 +242,49 @@ def test_sample_random_configs(gpu, oracle, seed):
     _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl, mask=mask)
 
 
+def _sparse_mask(rng, B, V, frac):
+    nw = (V + 31) // 32
+    keep = rng.random((B, V)) < frac
+    bits = np.zeros((B, nw * 32), np.uint32)
+    bits[:, :V] = keep
+    return (bits.reshape(B, nw, 32) << np.arange(32, dtype=np.uint32)).sum(axis=2, dtype=np.uint64).astype(np.uint32)
+
+
+@pytest.mark.parametrize("kind", ["normal", "integers", "fine_steps", "inf", "hot_history"])
+def test_sample_gather_path_top_p(gpu, oracle, kind):
+    """Rows whose candidates do not fit the finish's first round (a grammar mask
+    with a few percent of the ids allowed, no top-k): the gather path, where
+    the top-p boundary comes from value bins of 1/8 nat and a pairwise pass in
+    one bin.  Integer-valued rows and rows in 1/64 steps put more than 64 tied
+    or close values in the boundary bin (the radix rounds take over); an
+    infinite value takes the radix rounds too."""
+    _say("sample gather path", kind)
+    rng = np.random.default_rng(["normal", "integers", "fine_steps", "inf", "hot_history"].index(kind) + 90)
+    B, V = 8, 151936
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    if kind == "integers":
+        x = np.round(x)
+    elif kind == "fine_steps":
+        x = np.round(rng.normal(0, 0.4, (B, V)) * 64).astype(np.float32) / 64
+    elif kind == "inf":
+        x[1, 1000:1010] = np.inf
+    mask = _sparse_mask(rng, B, V, 0.02 if kind != "fine_steps" else 0.005)
+    if kind == "inf":
+        mask[1, 1000 >> 5] |= np.uint32(0xFFFFFFFF)          # the +inf ids are allowed
+    hist = hl = None
+    if kind == "hot_history":
+        allowed = np.flatnonzero((mask[0, np.arange(V) >> 5] >> (np.arange(V) & 31).astype(np.uint32)) & 1)
+        hist = np.tile(rng.choice(allowed, 300).astype(np.int32), (B, 1))
+        hl = np.full(B, 300, np.int32)
+    u = rng.random(B).astype(np.float32)
+    for cfgd in [dict(temperature=1.0, top_p=0.9), dict(temperature=0.5, top_p=0.5, min_p=0.05),
+                 dict(temperature=2.0, top_p=0.999),
+                 dict(temperature=1.0, top_p=0.95, presence_penalty=-0.3, repetition_penalty=1.2)]:
+        for dt in ("f32", "bf16"):
+            xx = wl.f32_to_bf16_bits(x) if dt == "bf16" else x
+            _sample_both(gpu, oracle, xx, u, cfgd, history=hist, hist_len=hl, mask=mask)
+
+
 def test_sample_masks_and_edges(gpu, oracle):
     _say("sample masks/edges")
     rng = np.random.default_rng(21)
