@@ -27,12 +27,13 @@
 //   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
 //               the chunk maxima and sums by every workgroup of the sequence),
 //               then, for every group of 32 ids of the draw row, the sum of the
-//               residual weights and the sum of the plain target weights.
-//               Workgroup 0 of a sequence also writes accepted_len, the emitted
-//               drafts and the draw context for vr_final
-//   vr_final    per sequence: the group holding the draw target (a block scan
-//               over the group sums), and the token inside it (one wave, one id
-//               per lane).
+//               residual weights and the sum of the plain target weights, and
+//               each wave's two totals.  Workgroup 0 of a sequence also
+//               writes accepted_len, the emitted drafts and the draw context for
+//               vr_final
+//   vr_final    per sequence: the workgroup block holding the draw target (a
+//               block scan over the block totals), then its group (one group
+//               per lane of a wave), then the token inside it (one id per lane).
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -44,7 +45,8 @@ namespace llima {
 #define VR_MAX_D 255
 #define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup (inside one chunk)
 #define VR_G 32                      // ids per draw group (4 threads of vr_drawsum)
-#define VR_GB 16                     // group sums a vr_final thread loads at once
+#define VR_GPB (VR_DCHUNK / VR_G)    // groups per vr_drawsum workgroup: one per lane of a wave
+#define VR_BPT 8                     // block sums per vr_final thread (V <= 2^22: <= 2048 blocks)
 #define VR_FBITS 27                  // chunk factor F_c = rint(exp(m_c - M) 2^27)
 #define VR_ZBITS 32                  // width of the residual's normalizers
 #define VR_RSHIFT 21                 // residual scaling (sums below 2^64 for V <= 2^22)
@@ -70,6 +72,8 @@ struct VerifyParams {
     uint64_t* wx;        // [NR] w at the row's draft token (relative to its chunk)
     uint64_t* gres;      // [B][NG] residual weight per group of VR_G ids
     uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
+    uint64_t* bres;      // [B][SD][4] residual weight per vr_drawsum wave (VR_DCHUNK / 4 ids)
+    uint64_t* btgt;      // [B][SD][4] target weight per vr_drawsum wave
     SeqCtx* ctx;         // [B]
     int32_t B, D, V, S, NR, NG, SD;
 };
@@ -419,6 +423,14 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
         st += wt;
         if (q.residual) sr += residual_weight(q, wt, draw_weight(xd[e], cd));
     }
+    // each wave's totals (every id once; vr_final adds a block's four), then
+    // the group sums
+    const uint64_t wt_ = wave_sum_u64(st), wr_ = wave_sum_u64(sr);
+    if (lane_id() == 0) {
+        const size_t o = ((size_t)b * P.SD + c) * LLIMA_WAVES + wave_id();
+        P.btgt[o] = wt_;
+        P.bres[o] = wr_;
+    }
     st = quad_sum_u64(st);                            // 4 threads = one group of 32 ids
     sr = quad_sum_u64(sr);
     const int g = i0 / VR_G;
@@ -428,25 +440,39 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
     }
 }
 
+// The draw in three steps, each one request round: the sequence's block sums
+// (one per vr_drawsum workgroup, scanned by the workgroup) give the block of
+// VR_DCHUNK ids holding the target; that block's VR_GPB group sums (one per
+// lane of wave 0) give the group; the group's 32 ids (one per lane) give the
+// token.
 __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     __shared__ uint64_t s_w2[2][LLIMA_WAVES];          // two scans at once
-    __shared__ int32_t s_group, s_tok;
+    __shared__ int32_t s_blk, s_tok;
     __shared__ uint64_t s_before;
     const int b = blockIdx.x;
     const uint32_t t = threadIdx.x;
-    // thread t owns the groups [t GPT, (t + 1) GPT): both arrays (residual and
+    // thread t owns the blocks [t BPT, (t + 1) BPT): both arrays (residual and
     // plain target sums) are read once and scanned together (the residual
     // total decides which one the draw uses)
-    const int NG = P.NG, GPT = (NG + LLIMA_WG - 1) / LLIMA_WG;
-    const int g0 = (int)t * GPT, g1 = g0 + GPT < NG ? g0 + GPT : NG;
-    const uint64_t* gr = P.gres + (size_t)b * NG;
-    const uint64_t* gt = P.gtgt + (size_t)b * NG;
-    uint64_t vr0[VR_GB], vt0[VR_GB];
+    const int SD = P.SD, BPT = (SD + LLIMA_WG - 1) / LLIMA_WG;     // <= VR_BPT
+    const int k0 = (int)t * BPT, k1 = k0 + BPT < SD ? k0 + BPT : SD;
+    const llima_u32x4* br = (const llima_u32x4*)(P.bres + (size_t)b * SD * LLIMA_WAVES);
+    const llima_u32x4* bt = (const llima_u32x4*)(P.btgt + (size_t)b * SD * LLIMA_WAVES);
+    uint64_t vr[VR_BPT], vt[VR_BPT];
+    {
+        llima_u32x4 qr[VR_BPT][2], qt[VR_BPT][2];         // a block's four wave totals: 32 bytes
 #pragma unroll
-    for (int j = 0; j < VR_GB; ++j) {
-        const int gi = g0 + j < g1 ? g0 + j : 0;
-        vr0[j] = gr[gi];
-        vt0[j] = gt[gi];
+        for (int j = 0; j < VR_BPT; ++j) {
+            const int kk = k0 + j < k1 ? k0 + j : 0;
+            qr[j][0] = br[2 * kk]; qr[j][1] = br[2 * kk + 1];
+            qt[j][0] = bt[2 * kk]; qt[j][1] = bt[2 * kk + 1];
+        }
+        auto sum4 = [](const llima_u32x4 (&h)[2]) {
+            return (((uint64_t)h[0].y << 32) | h[0].x) + (((uint64_t)h[0].w << 32) | h[0].z) +
+                   (((uint64_t)h[1].y << 32) | h[1].x) + (((uint64_t)h[1].w << 32) | h[1].z);
+        };
+#pragma unroll
+        for (int j = 0; j < VR_BPT; ++j) { vr[j] = sum4(qr[j]); vt[j] = sum4(qt[j]); }
     }
     const SeqCtx x = P.ctx[b];
     const uint32_t u32 = uniform32(P.u_resample[b]);  // requested with the sums
@@ -459,79 +485,67 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     q.d = q.residual ? row_ptr(P, q.rd) : nullptr;
     q.Mt = x.Mt; q.Md = x.Md; q.zt = x.zt; q.zd = x.zd;
     if (t == 0) {
-        s_group = -1;
+        s_blk = -1;
         s_tok = -1;
     }
     uint64_t sr = 0, st = 0;
 #pragma unroll
-    for (int j = 0; j < VR_GB; ++j) {
-        sr += g0 + j < g1 ? vr0[j] : 0ull;
-        st += g0 + j < g1 ? vt0[j] : 0ull;
-    }
-    for (int gb = g0 + VR_GB; gb < g1; gb += VR_GB) {
-        uint64_t vr[VR_GB], vt[VR_GB];
-#pragma unroll
-        for (int j = 0; j < VR_GB; ++j) {
-            const int gi = gb + j < g1 ? gb + j : g0;
-            vr[j] = gr[gi];
-            vt[j] = gt[gi];
-        }
-#pragma unroll
-        for (int j = 0; j < VR_GB; ++j) {
-            sr += gb + j < g1 ? vr[j] : 0ull;
-            st += gb + j < g1 ? vt[j] : 0ull;
-        }
+    for (int j = 0; j < VR_BPT; ++j) {
+        sr += k0 + j < k1 ? vr[j] : 0ull;
+        st += k0 + j < k1 ? vt[j] : 0ull;
     }
     // exclusive scans of both sums over the workgroup, and their totals
     const uint64_t ir = wave_incl_scan_u64(sr), it = wave_incl_scan_u64(st);
     const uint32_t wv = t >> 6;
     if (lane_id() == 63) { s_w2[0][wv] = ir; s_w2[1][wv] = it; }
     __syncthreads();
-    uint64_t br = 0, bt = 0, tr = 0, tt = 0;
+    uint64_t brr = 0, btt = 0, tr = 0, tt = 0;
 #pragma unroll
     for (int i = 0; i < LLIMA_WAVES; ++i) {
-        br += (uint32_t)i < wv ? s_w2[0][i] : 0ull;
-        bt += (uint32_t)i < wv ? s_w2[1][i] : 0ull;
+        brr += (uint32_t)i < wv ? s_w2[0][i] : 0ull;
+        btt += (uint32_t)i < wv ? s_w2[1][i] : 0ull;
         tr += s_w2[0][i];
         tt += s_w2[1][i];
     }
     if (q.residual && tr == 0) q.residual = false;          // p_t == p_d: draw from p_t
-    const uint64_t* sums = q.residual ? gr : gt;
     const uint64_t s = q.residual ? sr : st;
-    const uint64_t before = q.residual ? br + ir - sr : bt + it - st;
+    const uint64_t before = q.residual ? brr + ir - sr : btt + it - st;
     const uint64_t total = q.residual ? tr : tt;
     const uint64_t target = (uint64_t)(((llima_u128)u32 * total) >> 32);
     if (total > 0 && s > 0 && before <= target && target < before + s) {
         uint64_t a = before;
         bool found = false;
-        for (int gb = g0; gb < g1 && !found; gb += VR_GB) {
-            uint64_t v[VR_GB];               // the first block is still in registers
 #pragma unroll
-            for (int j = 0; j < VR_GB; ++j)
-                v[j] = gb + j >= g1 ? 0ull
-                     : gb == g0 ? (q.residual ? vr0[j] : vt0[j]) : sums[gb + j];
-#pragma unroll
-            for (int j = 0; j < VR_GB; ++j) {
-                if (!found && a + v[j] > target) { s_group = gb + j; s_before = a; found = true; }
-                a += found ? 0ull : v[j];
-            }
+        for (int j = 0; j < VR_BPT; ++j) {
+            const uint64_t v = k0 + j < k1 ? (q.residual ? vr[j] : vt[j]) : 0ull;
+            if (!found && a + v > target) { s_blk = k0 + j; s_before = a; found = true; }
+            a += found ? 0ull : v;
         }
     }
     __syncthreads();
-    const int grp = s_group;
-    if (grp >= 0 && t < 64) {
-        // one id per lane: the group's weights, scanned in id order
+    const int blk = s_blk;
+    if (blk >= 0 && t < 64) {
+        // the block's groups, one per lane
+        const uint64_t* gs = (q.residual ? P.gres : P.gtgt) + (size_t)b * P.NG;
+        const int g = blk * VR_GPB + (int)t;
+        const uint64_t v = g < P.NG ? gs[g] : 0ull;
+        const uint64_t inc = s_before + wave_incl_scan_u64(v);
+        const uint64_t hit = ballot(v > 0 && inc - v <= target && target < inc);
+        const uint32_t L = hit ? (uint32_t)__builtin_ffsll((long long)hit) - 1u : 0u;
+        const int grp = blk * VR_GPB + (int)L;
+        const uint64_t gbefore = readlane64(inc - v, L);
+        // the group's ids, one per lane, scanned in id order
         const int i = grp * VR_G + (int)t;
         const int cc = (grp * VR_G) >> VR_CSHIFT;
         const DrawChunk ct = draw_chunk(P.maxk[(size_t)q.rt * P.S + cc], q.Mt);
         const DrawChunk cd = draw_chunk(q.residual ? P.maxk[(size_t)q.rd * P.S + cc] : 0u, q.Md);
         uint64_t w = 0;
-        if (t < VR_G && i < P.V) {
+        if (hit && t < VR_G && i < P.V) {
             const uint32_t wt = draw_weight(q.t[i], ct);
             w = q.residual ? residual_weight(q, wt, draw_weight(q.d[i], cd)) : wt;
         }
-        const uint64_t inc = s_before + wave_incl_scan_u64(w);
-        if (w > 0 && inc - w <= target && target < inc) s_tok = i;
+        const uint64_t winc = gbefore + wave_incl_scan_u64(w);
+        if (w > 0 && winc - w <= target && target < winc) s_tok = i;
     }
     __syncthreads();
     if (t == 0) P.emitted[(size_t)b * (P.D + 1) + acc] = s_tok;
@@ -548,8 +562,9 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
     const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
     const size_t NR = (size_t)B * (2 * D + 1);
     const size_t NG = (size_t)(V + VR_G - 1) / VR_G;
+    const size_t SD = (size_t)(V + VR_DCHUNK - 1) / VR_DCHUNK;
     return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * NG * 8) +
-           al256((size_t)B * sizeof(SeqCtx));
+           2 * al256((size_t)B * SD * LLIMA_WAVES * 8) + al256((size_t)B * sizeof(SeqCtx));
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -580,6 +595,8 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
     P.gres = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
     P.gtgt = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
+    P.bres = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
+    P.btgt = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
     P.ctx = (SeqCtx*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
