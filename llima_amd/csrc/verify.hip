@@ -216,30 +216,25 @@ __device__ __forceinline__ uint32_t seq_maxk(const VerifyParams& P, int b, int q
     return n <= VR_MK_LDS ? sh.mk[q * P.S + c] : P.maxk[(size_t)row_of(P, b, q) * P.S + c];
 }
 
-// M and Z of every row of sequence b, then the acceptance scan.  Every input is
-// requested at once (up to VR_SEQ_ITEMS (row, chunk) items per thread, held in
-// registers): the chunk maxima combine with LDS atomics, then each chunk's
-// F_c S_c (below 2^77) is added to its row's Z in three 26-bit limbs, which sum
-// exactly.  The D acceptance tests run in parallel, one per thread; the only
+// M and Z of every row of sequence b, then the acceptance scan.  Rows of at
+// most 16 chunks take one DPP row each; otherwise every input is requested at
+// once (up to VR_SEQ_ITEMS (row, chunk) items per thread, held in registers),
+// the chunk maxima combine with LDS atomics, then each chunk's F_c S_c (below
+// 2^77) is added to its row's Z in three 26-bit limbs, which sum exactly.  The D acceptance tests run in parallel, one per thread; the only
 // serial part is the first failing test, found in LDS.  Returns the number of
 // accepted drafts (same in every thread).
+// Reduction over the 16 lanes of a DPP row (every lane gets the result).
+template <class Op>
+__device__ __forceinline__ uint32_t row16_reduce(uint32_t v, uint32_t identity, Op op) {
+    v = op(v, dppT<DPP_QUAD_XOR1, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_QUAD_XOR2, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_HALF_MIRROR, 0xF, false>(identity, v));
+    v = op(v, dppT<DPP_ROW_MIRROR, 0xF, false>(identity, v));
+    return v;
+}
+
 __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShared& sh) {
     const int nr = 2 * P.D + 1, t = (int)threadIdx.x, n = nr * P.S;
-    for (int q = t; q < nr; q += LLIMA_WG) {
-        sh.M[q] = 0;
-        sh.zl[q][0] = 0; sh.zl[q][1] = 0; sh.zl[q][2] = 0;
-    }
-    uint32_t km[VR_SEQ_ITEMS];
-    uint64_t sm[VR_SEQ_ITEMS];
-#pragma unroll
-    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
-        const int i = t + j * LLIMA_WG;
-        const int ic = i < n ? i : 0;
-        const int q = ic / P.S, c = ic - q * P.S;
-        const size_t rc = (size_t)row_of(P, b, q) * P.S + c;
-        km[j] = P.maxk[rc];
-        sm[j] = P.sums[rc];
-    }
     // per draft: w at the draft token in the target and the draft row
     int x = -1;
     uint64_t wt = 0, wd = 0;
@@ -250,34 +245,78 @@ __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShar
         wd = P.wx[drow(P, b, t)];
         ua = P.u_accept[b * P.D + t];
     }
-    __syncthreads();                                   // M and zl zeroed
-#pragma unroll
-    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
-        const int i = t + j * LLIMA_WG;
-        if (i < n) {
-            atomicMax(&sh.M[i / P.S], km[j]);
-            if (n <= VR_MK_LDS) sh.mk[i] = km[j];
+    if (P.S <= 16) {
+        // one DPP row of 16 lanes per sequence row, lane c holding chunk c: the
+        // row maximum and the three 26-bit limbs of Z (each limb's sum of 16
+        // values below 2^30) are row reductions, with no atomics
+        for (int q0 = 0; q0 < nr; q0 += LLIMA_WG / 16) {          // uniform
+            const int q = q0 + (t >> 4), c = t & 15;
+            const bool v = q < nr && c < P.S;
+            uint32_t kk = 0;
+            uint64_t ss = 0;
+            if (v) {
+                const size_t rc = (size_t)row_of(P, b, q) * P.S + c;
+                kk = P.maxk[rc];
+                ss = P.sums[rc];
+            }
+            const uint32_t Mq = row16_reduce(kk, 0u, [](uint32_t a, uint32_t e) { return a > e ? a : e; });
+            const llima_u128 fs = v ? (llima_u128)ss * chunk_factor(kk, Mq) : (llima_u128)0;
+            auto add = [](uint32_t a, uint32_t e) { return a + e; };
+            const uint32_t l0 = row16_reduce((uint32_t)(fs & 0x3FFFFFFu), 0u, add);
+            const uint32_t l1 = row16_reduce((uint32_t)((fs >> 26) & 0x3FFFFFFu), 0u, add);
+            const uint32_t l2 = row16_reduce((uint32_t)(fs >> 52), 0u, add);
+            if (v && c == 0) {
+                sh.M[q] = Mq;
+                sh.zl[q][0] = l0; sh.zl[q][1] = l1; sh.zl[q][2] = l2;
+            }
+            if (v && n <= VR_MK_LDS) sh.mk[q * P.S + c] = kk;
         }
-    }
-    for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG)  // sequences with more items than that
-        atomicMax(&sh.M[i / P.S], P.maxk[(size_t)row_of(P, b, i / P.S) * P.S + i % P.S]);
-    __syncthreads();
-    auto add_z = [&](int q, uint32_t kk, uint64_t ss) {
-        const llima_u128 fs = (llima_u128)ss * chunk_factor(kk, sh.M[q]);
-        atomicAdd(&sh.zl[q][0], (unsigned long long)(fs & 0x3FFFFFFull));
-        atomicAdd(&sh.zl[q][1], (unsigned long long)((fs >> 26) & 0x3FFFFFFull));
-        atomicAdd(&sh.zl[q][2], (unsigned long long)(fs >> 52));
-    };
+        __syncthreads();
+    } else {
+        for (int q = t; q < nr; q += LLIMA_WG) {
+            sh.M[q] = 0;
+            sh.zl[q][0] = 0; sh.zl[q][1] = 0; sh.zl[q][2] = 0;
+        }
+        uint32_t km[VR_SEQ_ITEMS];
+        uint64_t sm[VR_SEQ_ITEMS];
 #pragma unroll
-    for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
-        const int i = t + j * LLIMA_WG;
-        if (i < n) add_z(i / P.S, km[j], sm[j]);
+        for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+            const int i = t + j * LLIMA_WG;
+            const int ic = i < n ? i : 0;
+            const int q = ic / P.S, c = ic - q * P.S;
+            const size_t rc = (size_t)row_of(P, b, q) * P.S + c;
+            km[j] = P.maxk[rc];
+            sm[j] = P.sums[rc];
+        }
+        __syncthreads();                                   // M and zl zeroed
+#pragma unroll
+        for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+            const int i = t + j * LLIMA_WG;
+            if (i < n) {
+                atomicMax(&sh.M[i / P.S], km[j]);
+                if (n <= VR_MK_LDS) sh.mk[i] = km[j];
+            }
+        }
+        for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG)  // sequences with more items than that
+            atomicMax(&sh.M[i / P.S], P.maxk[(size_t)row_of(P, b, i / P.S) * P.S + i % P.S]);
+        __syncthreads();
+        auto add_z = [&](int q, uint32_t kk, uint64_t ss) {
+            const llima_u128 fs = (llima_u128)ss * chunk_factor(kk, sh.M[q]);
+            atomicAdd(&sh.zl[q][0], (unsigned long long)(fs & 0x3FFFFFFull));
+            atomicAdd(&sh.zl[q][1], (unsigned long long)((fs >> 26) & 0x3FFFFFFull));
+            atomicAdd(&sh.zl[q][2], (unsigned long long)(fs >> 52));
+        };
+#pragma unroll
+        for (int j = 0; j < VR_SEQ_ITEMS; ++j) {
+            const int i = t + j * LLIMA_WG;
+            if (i < n) add_z(i / P.S, km[j], sm[j]);
+        }
+        for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG) {
+            const size_t rc = (size_t)row_of(P, b, i / P.S) * P.S + i % P.S;
+            add_z(i / P.S, P.maxk[rc], P.sums[rc]);
+        }
+        __syncthreads();
     }
-    for (int i = t + VR_MK_LDS; i < n; i += LLIMA_WG) {
-        const size_t rc = (size_t)row_of(P, b, i / P.S) * P.S + i % P.S;
-        add_z(i / P.S, P.maxk[rc], P.sums[rc]);
-    }
-    __syncthreads();
     for (int k = t; k < P.D; k += LLIMA_WG) {
         if (k != t) {                                   // D > LLIMA_WG: the rest one by one
             x = P.draft_ids[b * P.D + k];
