@@ -97,28 +97,28 @@ __device__ __forceinline__ int drow(const VerifyParams& P, int b, int k) {
     return P.B * (P.D + 1) + b * P.D + k;
 }
 
-// Loads the chunk of 32 values per thread: 16-byte loads from clamped,
+// Loads a chunk, E values per thread of NT: 16-byte loads from clamped,
 // always-valid addresses (V is a multiple of 4), all in flight before the first
 // use; in a row's last, partial chunk the values past the end become -inf.
-__device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, int V,
-                                           float (&v)[VR_E]) {
-    llima_u32x4 q[VR_E / 4];
+template <int NT, int E>
+__device__ __forceinline__ void load_chunk(const float* rowp, int c0, int c1, int V, float (&v)[E]) {
+    llima_u32x4 q[E / 4];
 #pragma unroll
-    for (int j = 0; j < VR_E / 4; ++j) {
-        const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
+    for (int j = 0; j < E / 4; ++j) {
+        const int i0 = c0 + j * (NT * 4) + (int)threadIdx.x * 4;
         const int ia = i0 < V ? i0 : V - 4;
         q[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
     }
 #pragma unroll
-    for (int j = 0; j < VR_E / 4; ++j) {
+    for (int j = 0; j < E / 4; ++j) {
         const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[4 * j + e] = __uint_as_float(w4[e]);
     }
     if (c1 - c0 < VR_CHUNK) {
 #pragma unroll
-        for (int j = 0; j < VR_E / 4; ++j) {
-            const int i0 = c0 + j * (LLIMA_WG * 4) + (int)threadIdx.x * 4;
+        for (int j = 0; j < E / 4; ++j) {
+            const int i0 = c0 + j * (NT * 4) + (int)threadIdx.x * 4;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 v[4 * j + e] = i0 + e < c1 ? v[4 * j + e] : -__builtin_inff();
@@ -143,36 +143,53 @@ __device__ __forceinline__ uint32_t chunk_factor(uint32_t mck, uint32_t Mk) {
 }
 
 // ------------------------------------------------------------------ row pass
-// One workgroup per (row, chunk): the chunk's maximum, its sum of w (relative to
-// that maximum) and w at the row's draft token when it lies in the chunk.
-__global__ __launch_bounds__(LLIMA_WG) void vr_rowpass(VerifyParams P) {
-    __shared__ BlockScratch bs;
+// One workgroup of VR_RT threads per (row, chunk): the chunk's maximum, its sum
+// of w (relative to that maximum) and w at the row's draft token when it lies
+// in the chunk.  Each reduction over the workgroup takes one barrier.
+#ifndef VR_RT
+#define VR_RT 256
+#endif
+#define VR_RE (VR_CHUNK / VR_RT)       // values per thread
+
+__global__ __launch_bounds__(VR_RT) void vr_rowpass(VerifyParams P) {
+    __shared__ uint32_t s_m[VR_RT / 64];
+    __shared__ uint64_t s_s[VR_RT / 64];
     const int r = (int)blockIdx.x / P.S, c = (int)blockIdx.x - r * P.S;
     const int c0 = c * VR_CHUNK, c1 = c0 + VR_CHUNK < P.V ? c0 + VR_CHUNK : P.V;
     const float* rowp = row_ptr(P, r);
-    float v[VR_E];
-    load_chunk(rowp, c0, c1, P.V, v);
+    float v[VR_RE];
+    load_chunk<VR_RT, VR_RE>(rowp, c0, c1, P.V, v);
     float m = -__builtin_inff();
 #pragma unroll
-    for (int e = 0; e < VR_E; ++e) m = v[e] > m ? v[e] : m;   // NaN never counts
-    const uint32_t mkey = block_max_u32(f32_key(m), bs);       // >= f32_key(-inf) > 0
+    for (int e = 0; e < VR_RE; ++e) m = v[e] > m ? v[e] : m;   // NaN never counts
+    const uint32_t wm = wave_max_u32(f32_key(m));
+    if (lane_id() == 0) s_m[wave_id()] = wm;
+    __syncthreads();
+    uint32_t mkey = 0;                                  // >= f32_key(-inf) > 0
+#pragma unroll
+    for (int w = 0; w < VR_RT / 64; ++w) mkey = s_m[w] > mkey ? s_m[w] : mkey;
     uint64_t s = 0;
     if (mkey > LLIMA_KEY_NEG_INF) {
         const float xm = key_f32(mkey);
-        double sd = 0.0;                                 // exact: 32 terms below 2^37
+        double sd = 0.0;                                 // exact: VR_RE terms below 2^37
         if (xm == __builtin_inff()) {                    // w = 2^36 at every +inf, else 0
 #pragma unroll
-            for (int e = 0; e < VR_E; ++e) sd += v[e] == xm ? (double)LLIMA_TWO36 : 0.0;
+            for (int e = 0; e < VR_RE; ++e) sd += v[e] == xm ? (double)LLIMA_TWO36 : 0.0;
         } else {
 #pragma unroll
-            for (int e = 0; e < VR_E; ++e) sd += (double)weight_f(v[e], xm);
+            for (int e = 0; e < VR_RE; ++e) sd += (double)weight_f(v[e], xm);
         }
         s = (uint64_t)sd;
     }
-    s = block_sum_u64(s, bs);
+    s = wave_sum_u64(s);
+    if (lane_id() == 0) s_s[wave_id()] = s;
+    __syncthreads();
     if (threadIdx.x == 0) {
+        uint64_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < VR_RT / 64; ++w) tot += s_s[w];
         P.maxk[(size_t)r * P.S + c] = mkey;
-        P.sums[(size_t)r * P.S + c] = s;
+        P.sums[(size_t)r * P.S + c] = tot;
         const int b = seq_of(P, r), kk = pos_of(P, r);
         if (kk < P.D) {
             const int x = P.draft_ids[b * P.D + kk];
@@ -639,7 +656,7 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.ctx = (SeqCtx*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
-    hipLaunchKernelGGL(vr_rowpass, dim3(g12), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_rowpass, dim3(g12), dim3(VR_RT), 0, st, P);
     hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
