@@ -938,6 +938,35 @@ def test_lm_head_argmax_parity(gpu, B, H, V, cap):
         assert (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
 
 
+@pytest.mark.parametrize("ld", ["bf16", "f32"])
+def test_lm_head_then_sample(gpu, oracle, ld):
+    """A sampled decode step: the LM head's logits stay in device memory and feed
+    llima_sample directly; ids, probabilities and kept sets equal the oracle's
+    on the same logits (copied to the host), and the greedy sampler's ids equal
+    the LM head's fused argmax."""
+    import llima_amd
+    from oracle.oracle import SamplerConfig as OC
+    _say("lm head -> sample", ld)
+    rng = np.random.default_rng(31)
+    B, H, V = 8, 1024, 50000
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    ids_f, _, logits = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=30.0,
+                                                return_logits=True, logit_dtype=ld)
+    hist = rng.integers(0, V, size=(B, 256)).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    cfgd = dict(temperature=0.8, top_k=50, top_p=0.95, min_p=0.05, repetition_penalty=1.15,
+                presence_penalty=0.5, frequency_penalty=0.3)
+    ids, probs, keep = llima_amd.sample(logits, _t(u, gpu), llima_amd.SamplerConfig(**cfgd),
+                                        history=_t(hist, gpu), return_keep=True)
+    eids, eprobs, ekeep = oracle.sample(_np(logits), u, OC(**cfgd), history=hist, want_keep=True)
+    assert (_np(ids) == eids).all()
+    assert (_np(probs).view(np.uint32) == eprobs.view(np.uint32)).all()
+    assert (_np(keep).view(np.uint32) == ekeep).all()
+    gids, _ = llima_amd.sample(logits, _t(u, gpu), llima_amd.SamplerConfig(greedy=True))
+    assert (_np(gids) == _np(ids_f)).all()
+
+
 def test_lm_head_argmax_ties_and_nan(gpu):
     """Equal vocab rows tie: the lower index wins; a NaN logit never wins; a
     row whose logits are all NaN gives id 0 and a NaN value."""
