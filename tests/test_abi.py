@@ -77,6 +77,43 @@ def test_host_only_entry_points():
                                      None) == -1
     assert L.llima_mtp_masked_argmax(p, 4, 4, p, 1, p, 1, 1, 8, 8, p, p, None, None, 0,
                                      None) == -4              # no workspace
+    # heap top-k: k in [1, 32] (topk<T> throws outside it), at most the row's width
+    assert L.llima_topk(p, 0, 1, 100, 100, 0, p, p, None) == -1
+    assert L.llima_topk(p, 0, 1, 100, 100, 33, p, p, None) == -1
+    assert L.llima_topk(p, 0, 1, 4, 4, 5, p, p, None) == -1
+    assert L.llima_topk(p, 0, 1, 100, 50, 5, p, p, None) == -1      # stride below the width
+    assert L.llima_topk(p, 2, 1, 100, 100, 5, p, p, None) == -1      # dtype
+    assert L.llima_topk(None, 0, 0, 100, 100, 5, None, None, None) == 0
+    # EAGLE3 tree: K in [1, 32], depth in [1, 16], a state buffer of the stated size
+    tb = L.llima_eagle3_tree_bytes(5, 4)
+    assert tb > 0 and L.llima_eagle3_tree_bytes(0, 4) == 0
+    assert L.llima_eagle3_tree_begin(p, 1, 32000, p, 0, 4, p, tb, p, None) == -1
+    assert L.llima_eagle3_tree_begin(p, 1, 32000, p, 33, 4, p, tb, p, None) == -1
+    assert L.llima_eagle3_tree_begin(p, 1, 32000, p, 5, 17, p, tb, p, None) == -1
+    assert L.llima_eagle3_tree_begin(p, 1, 3, p, 5, 4, p, tb, p, None) == -1     # Vd < K
+    assert L.llima_eagle3_tree_begin(p, 1, 32000, p, 5, 4, p, tb - 1, p, None) == -4
+    assert L.llima_eagle3_tree_grow(p, 1, 32000, 32000, p, 5, 4, 0, p, tb, p, p, p, None) == -1
+    assert L.llima_eagle3_tree_grow(p, 1, 32000, 32000, p, 5, 4, 4, p, tb, p, p, p, None) == -1
+    assert L.llima_eagle3_tree_finish(p, tb, 5, 4, 33, 0, p, p, p, p, p, None) == -1
+    assert L.llima_eagle3_tree_finish(p, tb, 2, 2, 7, 0, p, p, p, p, p, None) == -1  # > nodes
+    # stop check: a vocabulary and a stop mask are required; B = 0 launches nothing
+    assert L.llima_stop_check(p, None, 1, 4, None, 100, None, p, None, None) == -1
+    assert L.llima_stop_check(p, None, 1, 4, p, 0, None, p, None, None) == -1
+    assert L.llima_stop_check(None, None, 0, 4, p, 100, None, None, None, None) == 0
+    # LM head: H a multiple of 8, a finite softcap, logit dtype f32 or bf16
+    wl = L.llima_lm_head_argmax_workspace_bytes(1, 1000)
+    assert L.llima_lm_head_argmax(p, p, 1, 12, 1000, 0.0, 1, p, None, None, p, wl, None) == -1
+    assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, float("nan"), 1, p, None, None, p, wl,
+                                  None) == -1
+    assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 7, p, None, None, p, wl, None) == -1
+    assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 1, p, None, None, p, 0, None) == -4
+    # rejection verification: V % 4 == 0, D <= 255, 16-byte aligned rows
+    vw = L.llima_verify_rejection_workspace_bytes(1, 1, 4096)
+    assert L.llima_verify_rejection(p, p, 1, 1, 4094, p, p, p, p, p, p, vw, None) == -1
+    assert L.llima_verify_rejection(p, p, 1, 256, 4096, p, p, p, p, p, p, vw, None) == -1
+    assert L.llima_verify_rejection(ctypes.c_void_p(20), p, 1, 1, 4096, p, p, p, p, p, p, vw,
+                                    None) == -1
+    assert L.llima_verify_rejection(p, p, 1, 1, 4096, p, p, p, p, p, p, vw - 1, None) == -4
 
 
 def _lib_cfg():
