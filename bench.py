@@ -140,7 +140,7 @@ def main():
         rows = B
         unit_rows = "sequences/s"
         dtype = "f32"
-        kernel_names = ["vr_clear", "vr_rowpass", "vr_drawsum", "vr_final"]
+        kernel_names = ["vr_rowpass", "vr_draw"]
         config = {"workload": "speculative", "B": B, "draft_len": D, "V": V}
     elif name in ("score_bf16", "mtp_masked_argmax"):
         lg = w["logits"]

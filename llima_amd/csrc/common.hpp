@@ -15,6 +15,9 @@
 
 #define LLIMA_WG 256
 #define LLIMA_WAVES (LLIMA_WG / 64)
+// s_waitcnt operand (gfx9 encoding) that waits for every vector memory
+// operation of the wave, stores included: vmcnt 0, expcnt 7, lgkmcnt 15.
+#define LLIMA_WAITCNT_VM0 0x0F70
 #define LLIMA_W_ONE (1ull << 36)
 
 typedef unsigned __int128 llima_u128;

@@ -20,20 +20,25 @@
 // sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111); with one-hot distributions
 // this reduces to that rule.
 //
-// Three launches:
+// Two launches:
 //   vr_rowpass  per (row, chunk of 8192 ids), one read of the rows: the chunk's
 //               maximum key, the sum of w over the chunk, and w at the row's
 //               draft token
-//   vr_drawsum  per (sequence, 2048 ids): the acceptance scan (recomputed from
+//   vr_draw     per (sequence, 2048 ids): the acceptance scan (recomputed from
 //               the chunk maxima and sums by every workgroup of the sequence),
-//               then, for every group of 32 ids of the draw row, the sum of the
-//               residual weights and the sum of the plain target weights, and
-//               each wave's two totals.  Workgroup 0 of a sequence also
-//               writes accepted_len, the emitted drafts and the draw context for
-//               vr_final
-//   vr_final    per sequence: the workgroup block holding the draw target (a
-//               block scan over the block totals), then its group (one group
-//               per lane of a wave), then the token inside it (one id per lane).
+//               then, for each wave's 512 ids of the draw rows, the sum of the
+//               residual weights and the sum of the plain target weights.  The
+//               sequence's last workgroup to finish (a per-sequence arrival
+//               counter) then draws: the wave slice holding the draw target (a
+//               block scan over the wave totals), then the token inside it (two
+//               ids per thread, a block scan in id order), and writes
+//               accepted_len and the emitted tokens.
+//
+// The sums that cross workgroups are stored and loaded as relaxed agent-scope
+// atomics (write-through stores, loads that miss stale cache lines), and each
+// workgroup waits for its stores to complete before it counts its arrival, so
+// no cache writeback or invalidation is needed for the last workgroup to see
+// every other workgroup's sums.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -44,20 +49,11 @@ namespace llima {
 #define VR_CSHIFT 13                 // log2(VR_CHUNK)
 #define VR_MAX_D 255
 #define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup (inside one chunk)
-#define VR_G 32                      // ids per draw group (4 threads of vr_drawsum)
-#define VR_GPB (VR_DCHUNK / VR_G)    // groups per vr_drawsum workgroup: one per lane of a wave
-#define VR_BPT 8                     // block sums per vr_final thread (V <= 2^22: <= 2048 blocks)
+#define VR_SLICE (VR_DCHUNK / LLIMA_WAVES)   // ids per vr_draw wave: two per thread of the draw
+#define VR_CNT_STRIDE 32             // arrival counters, one per 128-byte line
 #define VR_FBITS 27                  // chunk factor F_c = rint(exp(m_c - M) 2^27)
 #define VR_ZBITS 32                  // width of the residual's normalizers
 #define VR_RSHIFT 21                 // residual scaling (sums below 2^64 for V <= 2^22)
-
-// Draw context of a sequence: what vr_final needs of its acceptance step.
-struct SeqCtx {
-    uint32_t zt, zd;     // the residual's normalizers (32-bit z of the two draw rows)
-    uint32_t Mt, Md;     // maximum keys of the draw's target and draft rows
-    int32_t acc;         // accepted drafts: the draw uses target row acc
-    int32_t residual;    // a draft was rejected: the draw is from the residual
-};
 
 struct VerifyParams {
     const float* tgt;
@@ -70,12 +66,10 @@ struct VerifyParams {
     uint32_t* maxk;      // [NR][S] chunk maximum keys
     uint64_t* sums;      // [NR][S] chunk sums of w
     uint64_t* wx;        // [NR] w at the row's draft token (relative to its chunk)
-    uint64_t* gres;      // [B][NG] residual weight per group of VR_G ids
-    uint64_t* gtgt;      // [B][NG] target weight per group of VR_G ids
-    uint64_t* bres;      // [B][SD][4] residual weight per vr_drawsum wave (VR_DCHUNK / 4 ids)
-    uint64_t* btgt;      // [B][SD][4] target weight per vr_drawsum wave
-    SeqCtx* ctx;         // [B]
-    int32_t B, D, V, S, NR, NG, SD;
+    uint64_t* bres;      // [B][SD][4] residual weight per vr_draw wave (VR_DCHUNK / 4 ids)
+    uint64_t* btgt;      // [B][SD][4] target weight per vr_draw wave
+    uint32_t* cnt;       // [B][VR_CNT_STRIDE] arrival counters (zeroed by vr_rowpass)
+    int32_t B, D, V, S, NR, SD;
 };
 
 // Row r: target rows first ([B][D+1]), then draft rows ([B][D]).
@@ -159,6 +153,8 @@ __global__ __launch_bounds__(VR_RT) void vr_rowpass(VerifyParams P) {
     const float* rowp = row_ptr(P, r);
     float v[VR_RE];
     load_chunk<VR_RT, VR_RE>(rowp, c0, c1, P.V, v);
+    if (blockIdx.x == 0)                                 // vr_draw's arrival counters
+        for (int i = (int)threadIdx.x; i < P.B; i += VR_RT) P.cnt[(size_t)i * VR_CNT_STRIDE] = 0u;
     float m = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < VR_RE; ++e) m = v[e] > m ? v[e] : m;   // NaN never counts
@@ -208,6 +204,11 @@ struct SeqShared {
     uint32_t mk[VR_MK_LDS];                // chunk maxima [row q][chunk] (when they fit)
     uint8_t ok[VR_MAX_D];                  // draft k passes its acceptance test
     int32_t acc;
+    int32_t last;                          // this workgroup arrived last (vr_draw)
+    int32_t item, tok;                     // the draw's wave slice and token
+    uint64_t before;                       // weight before that wave slice
+    uint64_t w2[2][LLIMA_WAVES];           // wave totals of the draw's scans
+    uint64_t w3[LLIMA_WAVES];
     BlockScratch bs;
 };
 
@@ -334,31 +335,41 @@ __device__ __forceinline__ int accept_scan(const VerifyParams& P, int b, SeqShar
         }
         __syncthreads();
     }
-    for (int k = t; k < P.D; k += LLIMA_WG) {
-        if (k != t) {                                   // D > LLIMA_WG: the rest one by one
-            x = P.draft_ids[b * P.D + k];
-            wt = P.wx[trow(P, b, k)];
-            wd = P.wx[drow(P, b, k)];
-            ua = P.u_accept[b * P.D + k];
-        }
+    // draft k passes iff W_t(x) Z_d >= u W_d(x) Z_t
+    auto accept = [&](int k, int xk, uint64_t wtk, uint64_t wdk, float uk) {
         const llima_u128 zt = limbs_z(sh.zl[k]), zd = limbs_z(sh.zl[P.D + 1 + k]);
-        bool ok = false;
-        if (x >= 0 && x < P.V && zt > 0) {
-            const int cx = x >> VR_CSHIFT;
-            const uint64_t Wt = wt * chunk_factor(seq_maxk(P, b, k, cx, sh), sh.M[k]);
-            const uint64_t Wd = wd * chunk_factor(seq_maxk(P, b, P.D + 1 + k, cx, sh),
-                                                  sh.M[P.D + 1 + k]);
-            const double lhs = (double)Wt * u128_to_double(zd);
-            const double rhs = (double)ua * (double)Wd * u128_to_double(zt);
-            ok = lhs >= rhs;
+        if (!(xk >= 0 && xk < P.V && zt > 0)) return false;
+        const int cx = xk >> VR_CSHIFT;
+        const uint64_t Wt = wtk * chunk_factor(seq_maxk(P, b, k, cx, sh), sh.M[k]);
+        const uint64_t Wd = wdk * chunk_factor(seq_maxk(P, b, P.D + 1 + k, cx, sh),
+                                               sh.M[P.D + 1 + k]);
+        const double lhs = (double)Wt * u128_to_double(zd);
+        const double rhs = (double)uk * (double)Wd * u128_to_double(zt);
+        return lhs >= rhs;
+    };
+    if (P.D <= 64) {
+        // the tests of wave 0's lanes; the first failure is a ballot
+        if (t < 64) {
+            const bool ok = t < P.D && accept(t, x, wt, wd, ua);
+            const uint64_t rej = ballot(t < P.D && !ok);
+            if (t == 0) sh.acc = rej ? (int)__builtin_ffsll((long long)rej) - 1 : P.D;
         }
-        sh.ok[k] = ok ? 1 : 0;
-    }
-    __syncthreads();
-    if (t == 0) {
-        int acc = 0;
-        while (acc < P.D && sh.ok[acc]) ++acc;
-        sh.acc = acc;
+    } else {
+        for (int k = t; k < P.D; k += LLIMA_WG) {
+            if (k != t) {                               // D > LLIMA_WG: the rest one by one
+                x = P.draft_ids[b * P.D + k];
+                wt = P.wx[trow(P, b, k)];
+                wd = P.wx[drow(P, b, k)];
+                ua = P.u_accept[b * P.D + k];
+            }
+            sh.ok[k] = accept(k, x, wt, wd, ua) ? 1 : 0;
+        }
+        __syncthreads();
+        if (t == 0) {
+            int acc = 0;
+            while (acc < P.D && sh.ok[acc]) ++acc;
+            sh.acc = acc;
+        }
     }
     __syncthreads();
     return sh.acc;
@@ -431,137 +442,79 @@ __device__ __forceinline__ uint64_t residual_weight(const DrawCtx& q, uint32_t w
 }
 
 // 8 consecutive values from id i0 (a multiple of 8): two 16-byte loads from
-// clamped addresses; values past the row are -inf.
-__device__ __forceinline__ void load8(const float* rowp, int i0, int V, float (&x)[8]) {
+// clamped addresses, issued by load8 and unpacked (values past the row -inf)
+// by unpack8 where they are first used, so that no wait for them is placed
+// before the work in between.
+struct Raw8 {
+    llima_u32x4 a, b;
+};
+__device__ __forceinline__ Raw8 load8(const float* rowp, int i0, int V) {
     const int ia = i0 < V ? i0 : V - 4, ib = i0 + 4 < V ? i0 + 4 : V - 4;
-    const llima_u32x4 a = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
-    const llima_u32x4 b = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ib));
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    Raw8 r;
+    r.a = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+    r.b = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ib));
+    return r;
+}
+__device__ __forceinline__ void unpack8(const Raw8& r, int i0, int V, float (&x)[8]) {
+    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = i0 + e < V ? __uint_as_float(w[e]) : -__builtin_inff();
 }
 
-__device__ __forceinline__ uint64_t quad_sum_u64(uint64_t v) {
-    v += dpp64<DPP_QUAD_XOR1, 0xF, false>(0ull, v);
-    v += dpp64<DPP_QUAD_XOR2, 0xF, false>(0ull, v);
-    return v;
+// 2 consecutive values from id j0 (even): one 8-byte load from a clamped
+// address; values past the row are -inf.
+__device__ __forceinline__ void load2(const float* rowp, int j0, int V, float (&x)[2]) {
+    const int ja = j0 < V ? j0 : V - 2;
+    const float2 a = *(const float2*)(rowp + ja);
+    x[0] = j0 < V ? a.x : -__builtin_inff();
+    x[1] = j0 + 1 < V ? a.y : -__builtin_inff();
 }
 
-__global__ __launch_bounds__(LLIMA_WG) void vr_drawsum(VerifyParams P) {
-    __shared__ SeqShared sh;
-    const int b = blockIdx.x / P.SD, c = blockIdx.x % P.SD;
-    const int acc = accept_scan(P, b, sh);
-    const DrawCtx q = draw_ctx(P, b, acc, sh);       // residual iff a draft was rejected
-    if (c == 0) {
-        const int t = (int)threadIdx.x;
-        if (t == 0) {
-            SeqCtx x;
-            x.zt = q.zt; x.zd = q.zd; x.Mt = q.Mt; x.Md = q.Md;
-            x.acc = acc; x.residual = q.residual ? 1 : 0;
-            P.ctx[b] = x;
-            P.accepted_len[b] = acc;
-        }
-        if (t <= P.D)                                  // vr_final writes the drawn token at acc
-            P.emitted[(size_t)b * (P.D + 1) + t] = t < acc ? P.draft_ids[b * P.D + t] : -1;
-    }
-    // this workgroup's 2048 ids lie in one chunk of both draw rows
-    const int cc = (c * VR_DCHUNK) >> VR_CSHIFT;
-    const DrawChunk ct = draw_chunk(seq_maxk(P, b, acc, cc, sh), q.Mt);
-    const DrawChunk cd = draw_chunk(q.residual ? seq_maxk(P, b, P.D + 1 + acc, cc, sh) : 0u, q.Md);
-    const int i0 = c * VR_DCHUNK + (int)threadIdx.x * 8;
-    float xt[8], xd[8];
-    load8(q.t, i0, P.V, xt);
-    if (q.residual) load8(q.d, i0, P.V, xd);
-    uint64_t st = 0, sr = 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint32_t wt = draw_weight(xt[e], ct);
-        st += wt;
-        if (q.residual) sr += residual_weight(q, wt, draw_weight(xd[e], cd));
-    }
-    // each wave's totals (every id once; vr_final adds a block's four), then
-    // the group sums
-    const uint64_t wt_ = wave_sum_u64(st), wr_ = wave_sum_u64(sr);
-    if (lane_id() == 0) {
-        const size_t o = ((size_t)b * P.SD + c) * LLIMA_WAVES + wave_id();
-        P.btgt[o] = wt_;
-        P.bres[o] = wr_;
-    }
-    st = quad_sum_u64(st);                            // 4 threads = one group of 32 ids
-    sr = quad_sum_u64(sr);
-    const int g = i0 / VR_G;
-    if ((threadIdx.x & 3u) == 0u && g < P.NG) {
-        P.gtgt[(size_t)b * P.NG + g] = st;
-        P.gres[(size_t)b * P.NG + g] = sr;
-    }
+// Sums that other workgroups read inside the same launch: write-through
+// stores and loads at agent scope (see the header).
+__device__ __forceinline__ void store_agent(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent(uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The draw in three steps, each one request round: the sequence's block sums
-// (one per vr_drawsum workgroup, scanned by the workgroup) give the block of
-// VR_DCHUNK ids holding the target; that block's VR_GPB group sums (one per
-// lane of wave 0) give the group; the group's 32 ids (one per lane) give the
-// token.
-__global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
-    __shared__ uint64_t s_w2[2][LLIMA_WAVES];          // two scans at once
-    __shared__ int32_t s_blk, s_tok;
-    __shared__ uint64_t s_before;
-    const int b = blockIdx.x;
+// The draw of sequence b by its last workgroup, in two request rounds: the
+// wave totals (thread t owns a contiguous range of wave slices) give the wave
+// slice of VR_SLICE ids holding the target; that slice's ids, two per thread,
+// scanned in id order, give the token.  The draw uses the residual unless its
+// total is 0 (p_t == p_d), then the plain target weights.
+__device__ __forceinline__ void draw_final(const VerifyParams& P, int b, int acc, DrawCtx q,
+                                           SeqShared& sh) {
     const uint32_t t = threadIdx.x;
-    // thread t owns the blocks [t BPT, (t + 1) BPT): both arrays (residual and
-    // plain target sums) are read once and scanned together (the residual
-    // total decides which one the draw uses)
-    const int SD = P.SD, BPT = (SD + LLIMA_WG - 1) / LLIMA_WG;     // <= VR_BPT
-    const int k0 = (int)t * BPT, k1 = k0 + BPT < SD ? k0 + BPT : SD;
-    const llima_u32x4* br = (const llima_u32x4*)(P.bres + (size_t)b * SD * LLIMA_WAVES);
-    const llima_u32x4* bt = (const llima_u32x4*)(P.btgt + (size_t)b * SD * LLIMA_WAVES);
-    uint64_t vr[VR_BPT], vt[VR_BPT];
-    {
-        llima_u32x4 qr[VR_BPT][2], qt[VR_BPT][2];         // a block's four wave totals: 32 bytes
-#pragma unroll
-        for (int j = 0; j < VR_BPT; ++j) {
-            const int kk = k0 + j < k1 ? k0 + j : 0;
-            qr[j][0] = br[2 * kk]; qr[j][1] = br[2 * kk + 1];
-            qt[j][0] = bt[2 * kk]; qt[j][1] = bt[2 * kk + 1];
-        }
-        auto sum4 = [](const llima_u32x4 (&h)[2]) {
-            return (((uint64_t)h[0].y << 32) | h[0].x) + (((uint64_t)h[0].w << 32) | h[0].z) +
-                   (((uint64_t)h[1].y << 32) | h[1].x) + (((uint64_t)h[1].w << 32) | h[1].z);
-        };
-#pragma unroll
-        for (int j = 0; j < VR_BPT; ++j) { vr[j] = sum4(qr[j]); vt[j] = sum4(qt[j]); }
-    }
-    const SeqCtx x = P.ctx[b];
-    const uint32_t u32 = uniform32(P.u_resample[b]);  // requested with the sums
-    const int acc = x.acc;
-    DrawCtx q;
-    q.residual = x.residual != 0;
-    q.rt = trow(P, b, acc);
-    q.t = row_ptr(P, q.rt);
-    q.rd = q.residual ? drow(P, b, acc) : 0;
-    q.d = q.residual ? row_ptr(P, q.rd) : nullptr;
-    q.Mt = x.Mt; q.Md = x.Md; q.zt = x.zt; q.zd = x.zd;
+    const int NI = P.SD * LLIMA_WAVES, IPT = (NI + LLIMA_WG - 1) / LLIMA_WG;
+    const int i0 = (int)t * IPT, i1 = i0 + IPT < NI ? i0 + IPT : NI;
+    uint64_t* br = P.bres + (size_t)b * NI;
+    uint64_t* bt = P.btgt + (size_t)b * NI;
+    const uint32_t u32 = uniform32(P.u_resample[b]);
+    // the emitted drafts, requested with the totals
+    const int em = (int)t < acc && (int)t < P.D ? P.draft_ids[b * P.D + t] : -1;
     if (t == 0) {
-        s_blk = -1;
-        s_tok = -1;
+        sh.item = -1;
+        sh.tok = -1;
     }
     uint64_t sr = 0, st = 0;
-#pragma unroll
-    for (int j = 0; j < VR_BPT; ++j) {
-        sr += k0 + j < k1 ? vr[j] : 0ull;
-        st += k0 + j < k1 ? vt[j] : 0ull;
+    for (int i = i0; i < i1; ++i) {
+        sr += load_agent(br + i);
+        st += load_agent(bt + i);
     }
     // exclusive scans of both sums over the workgroup, and their totals
     const uint64_t ir = wave_incl_scan_u64(sr), it = wave_incl_scan_u64(st);
     const uint32_t wv = t >> 6;
-    if (lane_id() == 63) { s_w2[0][wv] = ir; s_w2[1][wv] = it; }
+    if (lane_id() == 63) { sh.w2[0][wv] = ir; sh.w2[1][wv] = it; }
     __syncthreads();
     uint64_t brr = 0, btt = 0, tr = 0, tt = 0;
 #pragma unroll
     for (int i = 0; i < LLIMA_WAVES; ++i) {
-        brr += (uint32_t)i < wv ? s_w2[0][i] : 0ull;
-        btt += (uint32_t)i < wv ? s_w2[1][i] : 0ull;
-        tr += s_w2[0][i];
-        tt += s_w2[1][i];
+        brr += (uint32_t)i < wv ? sh.w2[0][i] : 0ull;
+        btt += (uint32_t)i < wv ? sh.w2[1][i] : 0ull;
+        tr += sh.w2[0][i];
+        tt += sh.w2[1][i];
     }
     if (q.residual && tr == 0) q.residual = false;          // p_t == p_d: draw from p_t
     const uint64_t s = q.residual ? sr : st;
@@ -569,42 +522,99 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_final(VerifyParams P) {
     const uint64_t total = q.residual ? tr : tt;
     const uint64_t target = (uint64_t)(((llima_u128)u32 * total) >> 32);
     if (total > 0 && s > 0 && before <= target && target < before + s) {
-        uint64_t a = before;
-        bool found = false;
+        if (IPT == 1) {                                    // the owner's one slice
+            sh.item = i0;
+            sh.before = before;
+        } else {
+            uint64_t* bs = q.residual ? br : bt;
+            uint64_t a = before;
+            for (int i = i0; i < i1; ++i) {                // the owner's slices, once more
+                const uint64_t v = load_agent(bs + i);
+                if (a + v > target) { sh.item = i; sh.before = a; break; }
+                a += v;
+            }
+        }
+    }
+    __syncthreads();
+    const int item = sh.item;
+    if (item >= 0) {
+        // the slice's ids, two per thread (one chunk of both rows)
+        const int j0 = item * VR_SLICE + 2 * (int)t;
+        const int cc = (item * VR_SLICE) >> VR_CSHIFT;
+        float xt[2], xd[2];
+        load2(q.t, j0, P.V, xt);
+        if (q.residual) load2(q.d, j0, P.V, xd);
+        const DrawChunk ct = draw_chunk(seq_maxk(P, b, acc, cc, sh), q.Mt);
+        const DrawChunk cd = draw_chunk(q.residual ? seq_maxk(P, b, P.D + 1 + acc, cc, sh) : 0u, q.Md);
+        uint64_t w[2];
 #pragma unroll
-        for (int j = 0; j < VR_BPT; ++j) {
-            const uint64_t v = k0 + j < k1 ? (q.residual ? vr[j] : vt[j]) : 0ull;
-            if (!found && a + v > target) { s_blk = k0 + j; s_before = a; found = true; }
-            a += found ? 0ull : v;
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t wt = draw_weight(xt[e], ct);
+            w[e] = q.residual ? residual_weight(q, wt, draw_weight(xd[e], cd)) : wt;
         }
+        const uint64_t s2 = w[0] + w[1];
+        const uint64_t inc = wave_incl_scan_u64(s2);
+        if (lane_id() == 63) sh.w3[wv] = inc;
+        __syncthreads();
+        uint64_t a0 = sh.before + inc - s2;               // weight before id j0
+#pragma unroll
+        for (int i = 0; i < LLIMA_WAVES; ++i) a0 += (uint32_t)i < wv ? sh.w3[i] : 0ull;
+        if (w[0] > 0 && a0 <= target && target < a0 + w[0]) sh.tok = j0;
+        a0 += w[0];
+        if (w[1] > 0 && a0 <= target && target < a0 + w[1]) sh.tok = j0 + 1;
     }
     __syncthreads();
-    const int blk = s_blk;
-    if (blk >= 0 && t < 64) {
-        // the block's groups, one per lane
-        const uint64_t* gs = (q.residual ? P.gres : P.gtgt) + (size_t)b * P.NG;
-        const int g = blk * VR_GPB + (int)t;
-        const uint64_t v = g < P.NG ? gs[g] : 0ull;
-        const uint64_t inc = s_before + wave_incl_scan_u64(v);
-        const uint64_t hit = ballot(v > 0 && inc - v <= target && target < inc);
-        const uint32_t L = hit ? (uint32_t)__builtin_ffsll((long long)hit) - 1u : 0u;
-        const int grp = blk * VR_GPB + (int)L;
-        const uint64_t gbefore = readlane64(inc - v, L);
-        // the group's ids, one per lane, scanned in id order
-        const int i = grp * VR_G + (int)t;
-        const int cc = (grp * VR_G) >> VR_CSHIFT;
-        const DrawChunk ct = draw_chunk(P.maxk[(size_t)q.rt * P.S + cc], q.Mt);
-        const DrawChunk cd = draw_chunk(q.residual ? P.maxk[(size_t)q.rd * P.S + cc] : 0u, q.Md);
-        uint64_t w = 0;
-        if (hit && t < VR_G && i < P.V) {
-            const uint32_t wt = draw_weight(q.t[i], ct);
-            w = q.residual ? residual_weight(q, wt, draw_weight(q.d[i], cd)) : wt;
-        }
-        const uint64_t winc = gbefore + wave_incl_scan_u64(w);
-        if (w > 0 && winc - w <= target && target < winc) s_tok = i;
+    if ((int)t <= P.D) P.emitted[(size_t)b * (P.D + 1) + t] = (int)t == acc ? sh.tok : em;
+    if (t == 0) P.accepted_len[b] = acc;
+}
+
+__global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
+    __shared__ SeqShared sh;
+    const int b = blockIdx.x / P.SD, c = blockIdx.x % P.SD;
+    const int acc = accept_scan(P, b, sh);
+    // this workgroup's 2048 ids lie in one chunk of both draw rows: that
+    // chunk's maxima, then the rows' values are requested before the draw
+    // context is computed
+    const bool residual = acc < P.D;                  // a draft was rejected
+    const int cc = (c * VR_DCHUNK) >> VR_CSHIFT;
+    const int rti = trow(P, b, acc), rdi = residual ? drow(P, b, acc) : rti;
+    const uint32_t mkt = P.maxk[(size_t)rti * P.S + cc];
+    const uint32_t mkd0 = P.maxk[(size_t)rdi * P.S + cc];
+    const int i0 = c * VR_DCHUNK + (int)threadIdx.x * 8;
+    const Raw8 rt = load8(row_ptr(P, rti), i0, P.V);
+    Raw8 rd = {};
+    if (residual) rd = load8(row_ptr(P, rdi), i0, P.V);
+    const uint32_t mkd = residual ? mkd0 : 0u;
+    const DrawCtx q = draw_ctx(P, b, acc, sh);
+    const DrawChunk ct = draw_chunk(mkt, q.Mt);
+    const DrawChunk cd = draw_chunk(mkd, q.Md);
+    float xt[8], xd[8];
+    unpack8(rt, i0, P.V, xt);
+    unpack8(rd, i0, P.V, xd);
+    uint64_t st = 0, sr = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t wt = draw_weight(xt[e], ct);
+        st += wt;
+        if (q.residual) sr += residual_weight(q, wt, draw_weight(xd[e], cd));
+    }
+    // each wave's two totals (a wave slice of VR_SLICE ids)
+    const uint64_t wt_ = wave_sum_u64(st), wr_ = wave_sum_u64(sr);
+    if (lane_id() == 0) {
+        const size_t o = ((size_t)b * P.SD + c) * LLIMA_WAVES + wave_id();
+        store_agent(P.btgt + o, wt_);
+        store_agent(P.bres + o, wr_);
+    }
+    // every store of the workgroup completes before its arrival is counted
+    __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t n = __hip_atomic_fetch_add(P.cnt + (size_t)b * VR_CNT_STRIDE, 1u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = n + 1u == (uint32_t)P.SD;
     }
     __syncthreads();
-    if (t == 0) P.emitted[(size_t)b * (P.D + 1) + acc] = s_tok;
+    if (sh.last) draw_final(P, b, acc, q, sh);
 }
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -617,10 +627,8 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
     if (B <= 0 || D < 0 || V <= 0) return 0;
     const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
     const size_t NR = (size_t)B * (2 * D + 1);
-    const size_t NG = (size_t)(V + VR_G - 1) / VR_G;
     const size_t SD = (size_t)(V + VR_DCHUNK - 1) / VR_DCHUNK;
-    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * NG * 8) +
-           2 * al256((size_t)B * SD * LLIMA_WAVES * 8) + al256((size_t)B * sizeof(SeqCtx));
+    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * SD * LLIMA_WAVES * 8) + al256((size_t)B * VR_CNT_STRIDE * 4);
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -643,21 +651,17 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.B = B; P.D = D; P.V = V;
     P.S = (V + VR_CHUNK - 1) / VR_CHUNK;
     P.NR = B * (2 * D + 1);
-    P.NG = (V + VR_G - 1) / VR_G;
     P.SD = (V + VR_DCHUNK - 1) / VR_DCHUNK;
     char* w = (char*)workspace;
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
     P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
-    P.gres = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
-    P.gtgt = (uint64_t*)w;  w += al256((size_t)B * P.NG * 8);
     P.bres = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
     P.btgt = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
-    P.ctx = (SeqCtx*)w;
+    P.cnt = (uint32_t*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
     hipLaunchKernelGGL(vr_rowpass, dim3(g12), dim3(VR_RT), 0, st, P);
-    hipLaunchKernelGGL(vr_drawsum, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
-    hipLaunchKernelGGL(vr_final, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    hipLaunchKernelGGL(vr_draw, dim3((uint32_t)B * (uint32_t)P.SD), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }
