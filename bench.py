@@ -50,7 +50,8 @@ def parse():
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
-                             "lm_head_argmax_b256"])
+                             "lm_head_argmax_b256", "lm_head_argmax_b32_packed",
+                             "lm_head_argmax_b64_packed", "lm_head_argmax_b128_packed"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -95,19 +96,31 @@ def main():
         hid += [torch.randn((B, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(7)]
         ids_o = torch.empty(B, dtype=torch.int32, device=dev)
         vals_o = torch.empty(B, dtype=torch.float32, device=dev)
-        nws = L.llima_lm_head_argmax_workspace_bytes(B, V)
+        packed = name.endswith("_packed")
+        nws = (L.llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
+               else L.llima_lm_head_argmax_workspace_bytes(B, V))
         ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
+        if packed:       # the load-time layout, built once before any timing
+            wp = torch.empty(L.llima_lm_head_packed_bytes(V, H), dtype=torch.uint8, device=dev)
+            check(L.llima_lm_head_pack(weight.data_ptr(), V, H, wp.data_ptr(), wp.numel(),
+                                       torch.cuda.current_stream().cuda_stream), "llima_lm_head_pack")
+            torch.cuda.synchronize()
+            del weight
+            weight = wp
+        fn = L.llima_lm_head_argmax_packed if packed else L.llima_lm_head_argmax
         for x in hid:
-            launches.append(lambda sp, x=x: check(L.llima_lm_head_argmax(
+            launches.append(lambda sp, x=x: check(fn(
                 x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, ids_o.data_ptr(),
                 vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
-        per = weight.numel() * 2
+        per = V * H * 2
         alg_bytes = V * H * 2 + B * H * 2 + B * 8
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16"
-        kernel_names = ["lmh_mfma" if B > 4 else "lmh_rows", "lmh_finish"]
-        config = {"workload": name, "B": B, "H": H, "V": V, "weight": "bf16 [V, H]"}
+        kernel_names = (["lmh_packed", "lmh_xfrag", "lmh_finish"] if packed else
+                        ["lmh_mfma" if B > 4 else "lmh_rows", "lmh_finish"])
+        config = {"workload": name, "B": B, "H": H, "V": V,
+                  "weight": "bf16 [V, H] packed at load time" if packed else "bf16 [V, H]"}
         data_note = ("synthetic (seeded; one bf16 [%d, %d] weight, %.2f GiB, above the 256 MB "
                      "Infinity Cache; 8 rotating hidden rows)" % (V, H, per / 2**30))
     elif name == "speculative":

@@ -61,6 +61,8 @@
  *                            sima_lmm/model/language_part_base.py:171-180,
  *                            sima_lmm/model/model_graph.py:601, 868-870, whose
  *                            int32 the host reads at language_model.cpp:1607-1609
+ *   llima_lm_head_pack, llima_lm_head_argmax_packed <- the same, over a weight
+ *                            prepacked at load time (no counterpart)
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -288,12 +290,32 @@ int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_st
  * out_vals[B] (nullable) its value, out_logits (nullable, fp32 [B][V]) every
  * logit.  H % 8 == 0, and H <= 4096 unless H % 64 == 0 (then H <= 65536).  The
  * weights are read once per 8 hidden rows (H <= 2048) or 4 (H <= 4096); wider
- * batches, and rows wider than 4096, use MFMA tiles that read them once per 64
+ * batches, and rows wider than 4096, use MFMA tiles that read them once per 256
  * rows (H % 64 == 0). */
 size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V);
 int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
                          float softcap, int32_t logit_dtype, int32_t* out_ids, float* out_vals,
                          float* out_logits, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The same LM head over a weight prepacked once (at model load) by
+ * llima_lm_head_pack: llima_lm_head_packed_bytes(V, H) bytes (0: H is not a
+ * multiple of 256 or exceeds 65536), 16-byte aligned, holding the bf16 [V, H]
+ * weight in the MFMA's operand order (32 vocab rows x 16 ids per 1 KB, zero
+ * rows up to a multiple of 32; for each 128 ids, the row blocks in order).  llima_lm_head_argmax_packed takes the packed
+ * weight in place of `weight` and gives the same ids, values and logits as
+ * llima_lm_head_argmax's MFMA tiles; it reads the weight once per 64 hidden
+ * rows, each wave streaming contiguous memory.  Workspace:
+ * llima_lm_head_argmax_packed_workspace_bytes(B, H, V) (0 for invalid sizes).  No counterpart in the reference,
+ * whose LM head runs inside its compiled graph (language_part_base.py:171-180):
+ * a weight layout chosen at load time, as such graphs choose theirs. */
+size_t llima_lm_head_packed_bytes(int32_t V, int32_t H);
+size_t llima_lm_head_argmax_packed_workspace_bytes(int32_t B, int32_t H, int32_t V);
+int llima_lm_head_pack(const void* weight, int32_t V, int32_t H, void* packed, size_t packed_bytes,
+                       void* stream);
+int llima_lm_head_argmax_packed(const void* hidden, const void* packed, int32_t B, int32_t H,
+                                int32_t V, float softcap, int32_t logit_dtype, int32_t* out_ids,
+                                float* out_vals, float* out_logits, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
  * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):

@@ -325,6 +325,146 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_finish(LmhParams P) {
     }
 }
 
+// ------------------------------------------------------------------ packed weights
+// A weight prepacked once (at model load) in the order the MFMA reads it:
+// fragment (rb, s) is 1 KB, lane l's 16 bytes being
+//   weight[32 rb + l % 32][16 s + 8 (l / 32) .. + 7]
+// (rows past V zero), at offset ((s / 8) 8 NRB + 8 rb + s % 8) KB: a row
+// block's 8 k-steps of a group are 8 KB of contiguous memory, and the NRB row
+// blocks' groups follow each other.  A wave reads its row block as 1 KB loads
+// straight into the MFMA's B operand (no weight staging, no LDS for the
+// weight), 8 KB contiguous per group, and the waves, which take consecutive
+// row blocks and advance through k together, read adjacent groups: the device
+// reads a sliding window of the packed weight, as the matrix-vector path reads
+// whole rows of the plain one.
+//
+// lmh_packed: 256-thread workgroups; each wave takes WR consecutive row
+// blocks of 32 vocab rows (adjacent in the packed layout) against the pass's
+// 32 NMT hidden rows, which lmh_xfrag first writes in the same fragment order
+// (1 KB per 16 ids and 32 rows, NMT KB per k-step, into the workspace), so a
+// wave reads its A operands as 1 KB loads of contiguous memory too; they stay
+// in the L2 that all the waves of an XCD share, and each serves WR row blocks.
+// A wave's weight and hidden fragments form one ring of R k-steps, requested
+// R k-steps ahead in straight-line code; there is no LDS and no barrier, so no
+// wave waits for another.  The k order of the sums is the one of lmh_mfma
+// (k-step s, lane half g: ids 16 s + 8 g .. + 7), so the two give the same
+// logits.
+#define LMP_WG 256
+#define LMP_WAVES (LMP_WG / 64)
+#define LMP_SG 8                       // k-steps per contiguous group of a row block
+#define LMP_MB 64                      // hidden rows per pass
+#define LMP_HM 256                     // the H multiple of the packed layout
+
+template <int NMT, int WR, int R>
+__global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t* packed,
+                                                     const uint8_t* xfrag, int b0, int nb) {
+    const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r = lane & 31;
+    const int H = P.H, V = P.V, NS = H / 16, NRB = (V + 31) / 32;
+    const int wv = (int)blockIdx.x * LMP_WAVES + wave;       // key slot
+    const int rb0 = wv * WR;                                 // >= NRB: spare row blocks
+    const size_t gstride = (size_t)NRB * LMP_SG * 1024;      // bytes between groups
+    const uint8_t* wp[WR];
+#pragma unroll
+    for (int j = 0; j < WR; ++j)
+        wp[j] = packed + (size_t)(rb0 + j < NRB ? rb0 + j : NRB - 1) * LMP_SG * 1024 + lane * 16;
+    const uint8_t* xp = xfrag + lane * 16;
+    auto wfrag = [&](int j, int f) {
+        return __builtin_nontemporal_load(
+            (const lmh_b8*)(wp[j] + (size_t)(f / LMP_SG) * gstride + (f % LMP_SG) * 1024));
+    };
+    auto xfr = [&](int f, int mt) { return *(const lmh_b8*)(xp + (size_t)(f * NMT + mt) * 1024); };
+    lmh_b8 rw[R][WR], ra[R][NMT];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {                            // NS >= 16 >= R
+#pragma unroll
+        for (int j = 0; j < WR; ++j) rw[i][j] = wfrag(j, i);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) ra[i][mt] = xfr(i, mt);
+    }
+    lmh_acc acc[WR][NMT];
+#pragma unroll
+    for (int j = 0; j < WR; ++j)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[j][mt][i] = 0.0f;
+    for (int f0 = 0; f0 < NS; f0 += R) {                     // NS % R == 0
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            lmh_b8 bo[WR], a[NMT];
+#pragma unroll
+            for (int j = 0; j < WR; ++j) bo[j] = rw[i][j];
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt) a[mt] = ra[i][mt];
+            const int fn = f0 + i + R < NS ? f0 + i + R : NS - 1;
+#pragma unroll
+            for (int j = 0; j < WR; ++j) rw[i][j] = wfrag(j, fn);
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt) ra[i][mt] = xfr(fn, mt);
+#pragma unroll
+            for (int j = 0; j < WR; ++j)
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt)
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], bo[j], acc[j][mt], 0, 0, 0);
+        }
+    }
+    // key slots past this grid's waves (a pass with more row blocks per wave
+    // than another uses fewer of the P.NW slots): no logit
+    if (blockIdx.x == gridDim.x - 1) {
+        const int w0 = (int)gridDim.x * LMP_WAVES, nx = P.NW - w0;
+        for (int e = t; e < nx * nb; e += LMP_WG)
+            P.keys[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0;
+    }
+    // epilogue: softcap, logits, per hidden row the greatest key of the wave's
+    // 32 WR vocab rows
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
+            uint64_t key = 0;
+#pragma unroll
+            for (int j = 0; j < WR; ++j) {
+                const int n = 32 * (rb0 + j) + r;            // >= V for a spare row block
+                const float v = lmh_logit(acc[j][mt][i], P);
+                if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
+                const uint64_t k = lmh_key(v, n, V);
+                key = k > key ? k : key;
+            }
+            const uint64_t best = half_max_u64(key);
+            if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
+        }
+    }
+}
+
+// The pass's hidden rows in fragment order: piece p is lane p % 64 of
+// fragment (s, mt) = (p / 64 / nmt, p / 64 % nmt), i.e. 16 bytes of hidden row
+// 32 mt + p % 32 (zeros past nb) at ids 16 s + 8 (p % 64 / 32).
+__global__ __launch_bounds__(LLIMA_WG) void lmh_xfrag(const uint16_t* hidden, uint8_t* xfrag, int H,
+                                                      int b0, int nb, int nmt) {
+    const int p = (int)(blockIdx.x * LLIMA_WG + threadIdx.x);
+    if (p >= nmt * 64 * (H / 16)) return;
+    const int l = p & 63, fr = p >> 6, mt = fr % nmt, s = fr / nmt, m = 32 * mt + (l & 31);
+    llima_u32x4 v = {0u, 0u, 0u, 0u};
+    if (m < nb) v = *(const llima_u32x4*)(hidden + (size_t)(b0 + m) * H + 16 * s + 8 * (l >> 5));
+    *(llima_u32x4*)(xfrag + (size_t)p * 16) = v;
+}
+
+// One thread per 16-byte piece of the packed weight.
+__global__ __launch_bounds__(LLIMA_WG) void lmh_pack(const uint16_t* weight, uint8_t* packed,
+                                                     int V, int H, size_t npieces) {
+    const size_t p = (size_t)blockIdx.x * LLIMA_WG + threadIdx.x;
+    if (p >= npieces) return;
+    const int l = (int)(p & 63);
+    const size_t fr = p >> 6, nrb = (size_t)(V + 31) / 32, gs = nrb * LMP_SG;
+    const size_t rem = fr % gs, rb = rem / LMP_SG;           // group fr / gs, step rem % 8
+    const int s = (int)(fr / gs) * LMP_SG + (int)(rem % LMP_SG);
+    const size_t row = 32 * rb + (size_t)(l & 31);
+    llima_u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < (size_t)V) v = *(const llima_u32x4*)(weight + row * H + 16 * s + 8 * (l >> 5));
+    *(llima_u32x4*)(packed + p * 16) = v;
+}
+
 static size_t lmh_align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Waves of the rows kernel (a whole number of workgroups): two 512-thread
@@ -410,6 +550,86 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
             case 2: hipLaunchKernelGGL(lmh_rows<2>, g, blk, 0, st, P, b0, nb); break;
             default: hipLaunchKernelGGL(lmh_rows<1>, g, blk, 0, st, P, b0, nb); break;
         }
+    }
+    hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+// Row blocks per wave, and ring depth, of lmh_packed passes of 32 and of 64
+// hidden rows.
+#define LMP_WR1 2
+#define LMP_R1 8
+#define LMP_WR2 2
+#define LMP_R2 4
+
+// Workgroups of lmh_packed for WR row blocks per wave; its key slots per
+// hidden row are one per wave.
+static int lmp_groups(int V, int wr) {
+    return ((V + 31) / 32 + LMP_WAVES * wr - 1) / (LMP_WAVES * wr);
+}
+
+extern "C" size_t llima_lm_head_packed_bytes(int32_t V, int32_t H) {
+    if (V <= 0 || H <= 0 || H % LMP_HM != 0 || H > 65536) return 0;
+    return (size_t)((V + 31) / 32) * 32 * (size_t)H * 2;
+}
+
+extern "C" size_t llima_lm_head_argmax_packed_workspace_bytes(int32_t B, int32_t H, int32_t V) {
+    if (B <= 0 || llima_lm_head_packed_bytes(V, H) == 0) return 0;
+    const int g1 = lmp_groups(V, LMP_WR1), g2 = lmp_groups(V, LMP_WR2);
+    const int nw = (g1 > g2 ? g1 : g2) * LMP_WAVES;
+    return lmh_align256((size_t)B * nw * sizeof(uint64_t)) + (size_t)LMP_MB * H * 2;
+}
+
+extern "C" int llima_lm_head_pack(const void* weight, int32_t V, int32_t H, void* packed,
+                                  size_t packed_bytes, void* stream) {
+    const size_t need = llima_lm_head_packed_bytes(V, H);
+    if (need == 0 || !weight || !packed) return LLIMA_E_INVAL;
+    if ((uintptr_t)weight % 16 || (uintptr_t)packed % 16) return LLIMA_E_INVAL;
+    if (packed_bytes < need) return LLIMA_E_WORKSPACE;
+    const size_t npieces = need / 16;
+    hipLaunchKernelGGL(lmh_pack, dim3((uint32_t)((npieces + LLIMA_WG - 1) / LLIMA_WG)),
+                       dim3(LLIMA_WG), 0, (hipStream_t)stream, (const uint16_t*)weight,
+                       (uint8_t*)packed, V, H, npieces);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packed, int32_t B,
+                                           int32_t H, int32_t V, float softcap,
+                                           int32_t logit_dtype, int32_t* out_ids, float* out_vals,
+                                           float* out_logits, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+    if (B < 0 || llima_lm_head_packed_bytes(V, H) == 0) return LLIMA_E_INVAL;
+    if (!packed || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
+    if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
+    if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
+    if ((uintptr_t)packed % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
+    if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_lm_head_argmax_packed_workspace_bytes(B, H, V))
+        return LLIMA_E_WORKSPACE;
+    const int ng1 = lmp_groups(V, LMP_WR1), ng2 = lmp_groups(V, LMP_WR2);
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.out_logits = out_logits;
+    P.keys = (uint64_t*)workspace;
+    P.out_ids = out_ids;
+    P.out_vals = out_vals;
+    P.B = B; P.H = H; P.V = V;
+    P.NW = (ng1 > ng2 ? ng1 : ng2) * LMP_WAVES;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    uint8_t* xf = (uint8_t*)workspace + lmh_align256((size_t)B * P.NW * sizeof(uint64_t));
+    hipStream_t st = (hipStream_t)stream;
+    for (int b0 = 0; b0 < B; b0 += LMP_MB) {
+        const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB, nmt = nb <= 32 ? 1 : 2;
+        const int np = nmt * 64 * (H / 16);
+        hipLaunchKernelGGL(lmh_xfrag, dim3((uint32_t)((np + LLIMA_WG - 1) / LLIMA_WG)),
+                           dim3(LLIMA_WG), 0, st, P.hidden, xf, H, b0, nb, nmt);
+        if (nmt == 1)
+            hipLaunchKernelGGL((lmh_packed<1, LMP_WR1, LMP_R1>), dim3(ng1), dim3(LMP_WG), 0, st, P,
+                               (const uint8_t*)packed, (const uint8_t*)xf, b0, nb);
+        else
+            hipLaunchKernelGGL((lmh_packed<2, LMP_WR2, LMP_R2>), dim3(ng2), dim3(LMP_WG), 0, st, P,
+                               (const uint8_t*)packed, (const uint8_t*)xf, b0, nb);
     }
     hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;

@@ -42,6 +42,7 @@ __all__ = [
     "sample", "verify_greedy", "resolve_draft_tokens", "verify_tree", "verify_rejection",
     "Workspace", "score_logits", "select_candidate_tokens", "argmax_gemma4_mtp_masked_rows",
     "argmax_gemma4_mtp_masked_row", "topk", "Eagle3DraftTree", "stop_mask", "stop_check",
+    "lm_head_argmax", "lm_head_pack", "PackedLmHead",
 ]
 
 
@@ -520,7 +521,35 @@ def argmax_gemma4_mtp_masked_row(centroid_logits: torch.Tensor, token_ordering, 
                                              top_k, logits.reshape(1, -1))[0])
 
 
-def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 0.0,
+class PackedLmHead:
+    """An LM head weight prepacked once, at model load, by lm_head_pack: the
+    bf16 [V, H] weight rearranged into the MFMA's operand order (1 KB per 32
+    vocab rows x 16 ids, zero rows up to a multiple of 32), so that each wave
+    streams contiguous memory straight into the matrix cores.  `data` is the
+    uint8 device tensor; V and H are the weight's shape."""
+
+    def __init__(self, data: torch.Tensor, V: int, H: int):
+        self.data, self.V, self.H = data, V, H
+
+
+def lm_head_pack(weight: torch.Tensor) -> PackedLmHead:
+    """Prepack a bf16 [V, H] LM head weight (H a multiple of 256) for
+    lm_head_argmax (llima_lm_head_pack)."""
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2:
+        raise ValueError("lm_head_pack takes a bf16 [V, H] weight")
+    w = weight.contiguous()
+    V, H = w.shape
+    _on_gpu(w)
+    n = lib().llima_lm_head_packed_bytes(V, H)
+    if n == 0:
+        raise ValueError("lm_head_pack needs H a multiple of 256 (at most 65536)")
+    data = torch.empty(n, dtype=torch.uint8, device=w.device)
+    check(lib().llima_lm_head_pack(w.data_ptr(), V, H, data.data_ptr(), n, _stream(w.device)),
+          "llima_lm_head_pack")
+    return PackedLmHead(data, V, H)
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight, softcap: float = 0.0,
                    return_logits: bool = False, logit_dtype: str = "bf16"):
     """LM head + softcap + argmax, as the reference's graph computes them before
     the host reads one int32 (language_part_base.py:171-180,
@@ -528,28 +557,39 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor, softcap: float = 
     [V, H] -> (ids int32 [B], values float32 [B]) and, if return_logits, the
     float32 logits [B, V].  logit_dtype "bf16" rounds each logit to bf16
     before the argmax, as the reference's bf16 graphs produce them (equal bf16
-    logits tie, the lower index wins); "f32" keeps the fp32 sums."""
+    logits tie, the lower index wins); "f32" keeps the fp32 sums.  weight may
+    be a PackedLmHead (lm_head_pack): the same logits, read in the packed order
+    (llima_lm_head_argmax_packed)."""
     x = hidden.reshape(1, -1) if hidden.dim() == 1 else hidden
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    packed = isinstance(weight, PackedLmHead)
+    if x.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
         raise ValueError("lm_head_argmax takes bf16 hidden states and weights")
     if logit_dtype not in ("bf16", "f32"):
         raise ValueError("logit_dtype must be 'bf16' or 'f32'")
     x = x.contiguous()
-    w = weight.contiguous()
+    w = weight.data if packed else weight.contiguous()
     B, H = x.shape
-    if w.dim() != 2 or w.shape[1] != H:
-        raise ValueError("weight must be [V, H]")
-    V = w.shape[0]
+    if packed:
+        if weight.H != H:
+            raise ValueError("hidden width differs from the packed weight's H")
+        V = weight.V
+    else:
+        if w.dim() != 2 or w.shape[1] != H:
+            raise ValueError("weight must be [V, H]")
+        V = w.shape[0]
     dev = w.device
     _on_gpu(x, w)
     ids = torch.empty(B, dtype=torch.int32, device=dev)
     vals = torch.empty(B, dtype=torch.float32, device=dev)
     logits = torch.empty((B, V), dtype=torch.float32, device=dev) if return_logits else None
-    ws = Workspace.get(dev, "lm_head", lib().llima_lm_head_argmax_workspace_bytes(B, V))
+    nws = (lib().llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
+           else lib().llima_lm_head_argmax_workspace_bytes(B, V))
+    ws = Workspace.get(dev, "lm_head", nws)
     ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
-    check(lib().llima_lm_head_argmax(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap), ld,
-                                     ids.data_ptr(), vals.data_ptr(), _ptr(logits), ws.data_ptr(),
-                                     ws.numel(), _stream(dev)), "llima_lm_head_argmax")
+    fn = lib().llima_lm_head_argmax_packed if packed else lib().llima_lm_head_argmax
+    check(fn(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap), ld, ids.data_ptr(),
+             vals.data_ptr(), _ptr(logits), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_lm_head_argmax_packed" if packed else "llima_lm_head_argmax")
     return (ids, vals, logits) if return_logits else (ids, vals)
 
 

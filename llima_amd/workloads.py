@@ -180,4 +180,7 @@ WORKLOADS = {
     "lm_head_argmax_b64": lambda: dict(lm_head_argmax(B=64), name="lm_head_argmax_b64"),
     "lm_head_argmax_b128": lambda: dict(lm_head_argmax(B=128), name="lm_head_argmax_b128"),
     "lm_head_argmax_b256": lambda: dict(lm_head_argmax(B=256), name="lm_head_argmax_b256"),
+    "lm_head_argmax_b64_packed": lambda: dict(lm_head_argmax(B=64), name="lm_head_argmax_b64_packed"),
+    "lm_head_argmax_b32_packed": lambda: dict(lm_head_argmax(B=32), name="lm_head_argmax_b32_packed"),
+    "lm_head_argmax_b128_packed": lambda: dict(lm_head_argmax(B=128), name="lm_head_argmax_b128_packed"),
 }

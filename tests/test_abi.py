@@ -107,6 +107,26 @@ def test_host_only_entry_points():
                                   None) == -1
     assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 7, p, None, None, p, wl, None) == -1
     assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 1, p, None, None, p, 0, None) == -4
+    # packed LM head: H a multiple of 256 (at most 65536), the packed size as stated
+    assert L.llima_lm_head_packed_bytes(1000, 100) == 0
+    assert L.llima_lm_head_packed_bytes(1000, 65536 + 256) == 0
+    assert L.llima_lm_head_packed_bytes(1000, 256) == 32 * 32 * 256 * 2      # 1000 -> 1024 rows
+    assert L.llima_lm_head_pack(p, 1000, 100, p, 1 << 20, None) == -1
+    assert L.llima_lm_head_pack(p, 1000, 256, p, 32 * 32 * 256 * 2 - 1, None) == -4
+    assert L.llima_lm_head_pack(ctypes.c_void_p(24), 1000, 256, p, 1 << 20, None) == -1
+    assert L.llima_lm_head_argmax_packed_workspace_bytes(1, 100, 1000) == 0
+    wp = L.llima_lm_head_argmax_packed_workspace_bytes(1, 256, 1000)
+    assert wp >= 32 * 8 + 64 * 256 * 2                                     # keys + hidden fragments
+    assert L.llima_lm_head_argmax_packed(p, p, 1, 100, 1000, 0.0, 1, p, None, None, p, wp,
+                                         None) == -1
+    assert L.llima_lm_head_argmax_packed(p, p, 1, 256, 1000, float("inf"), 1, p, None, None, p,
+                                         wp, None) == -1
+    assert L.llima_lm_head_argmax_packed(p, p, 1, 256, 1000, 0.0, 1, p, None, None, p, wp - 1,
+                                         None) == -4
+    assert L.llima_lm_head_argmax_packed(p, p, 1, 256, 1000, 0.0, 1, p, None, None, p, 0,
+                                         None) == -4
+    assert L.llima_lm_head_argmax_packed(None, p, 0, 256, 1000, 0.0, 1, None, None, None, None,
+                                         0, None) == 0
     # rejection verification: V % 4 == 0, D <= 255, 16-byte aligned rows
     vw = L.llima_verify_rejection_workspace_bytes(1, 1, 4096)
     assert L.llima_verify_rejection(p, p, 1, 1, 4094, p, p, p, p, p, p, vw, None) == -1

@@ -938,6 +938,69 @@ def test_lm_head_argmax_parity(gpu, B, H, V, cap):
         assert (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
 
 
+def _lm_head_takes_mfma(B, H):
+    """Whether llima_lm_head_argmax takes its MFMA tiles (more hidden rows than
+    one matrix-vector pass stages, or rows wider than 4096)."""
+    per = 16384 // H
+    per = 8 if per >= 8 else 4 if per >= 4 else 2 if per >= 2 else 1
+    return (B > per or H > 4096) and H % 64 == 0
+
+
+@pytest.mark.parametrize("B,H,V,cap", [(1, 4096, 32768, 0.0), (64, 4096, 20000, 30.0),
+                                       (33, 512, 1000, 30.0), (64, 2048, 50000, 0.0),
+                                       (17, 256, 777, 0.0), (40, 1024, 70000, 30.0),
+                                       (100, 512, 3001, 0.0), (5, 256, 31, 0.0),
+                                       (32, 768, 4097, 0.0), (130, 256, 1000, 30.0),
+                                       (8, 8192, 3000, 0.0)])
+def test_lm_head_packed_parity(gpu, B, H, V, cap):
+    """The packed weight (llima_lm_head_pack) gives logits within the fp32 sum's
+    bound of the float64 product and, where the plain entry point takes its MFMA
+    tiles (the same k order), the same logits and ids bit for bit."""
+    import llima_amd
+    _say("lm head packed", B, H, V, cap)
+    rng = np.random.default_rng(B * 37 + H + V)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 1.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    pk = llima_amd.lm_head_pack(_t(w, gpu))
+    assert pk.data.numel() == (V + 31) // 32 * 32 * H * 2
+    for ld in ("bf16", "f32"):
+        ids, vals, logits = llima_amd.lm_head_argmax(_t(x, gpu), pk, softcap=cap,
+                                                     return_logits=True, logit_dtype=ld)
+        _lm_head_check(_np(ids), _np(vals), _np(logits), x, w, cap, bf16=ld == "bf16")
+        ids2, vals2 = llima_amd.lm_head_argmax(_t(x, gpu), pk, softcap=cap, logit_dtype=ld)
+        assert (_np(ids2) == _np(ids)).all()
+        assert (_np(vals2).view(np.uint32) == _np(vals).view(np.uint32)).all()
+        if _lm_head_takes_mfma(B, H):
+            ids3, vals3, logits3 = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=cap,
+                                                            return_logits=True, logit_dtype=ld)
+            assert (_np(logits3).view(np.uint32) == _np(logits).view(np.uint32)).all()
+            assert (_np(ids3) == _np(ids)).all()
+
+
+def test_lm_head_packed_ties_and_nan(gpu):
+    """The packed path's argmax rules: equal vocab rows tie and the lower index
+    wins, a NaN logit never wins, an all-NaN row gives id 0 and a NaN value."""
+    import llima_amd
+    _say("lm head packed ties / nan")
+    rng = np.random.default_rng(6)
+    B, H, V = 3, 256, 5000
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    wf = rng.normal(0, 0.05, (V, H)).astype(np.float32)
+    wf[4000] = wl.bf16_bits_to_f32(x[0]) * 0.5
+    wf[1234] = wf[4000]
+    wf[17, 3] = np.nan
+    w = wl.f32_to_bf16_bits(wf)
+    xn = x.copy()
+    xn[2] = wl.f32_to_bf16_bits(np.full(H, np.nan, np.float32))
+    pk = llima_amd.lm_head_pack(_t(w, gpu))
+    ids, vals, logits = llima_amd.lm_head_argmax(_t(xn, gpu), pk, return_logits=True)
+    ids, vals, logits = _np(ids), _np(vals), _np(logits)
+    assert ids[0] == 1234
+    assert np.isnan(logits[1, 17]) and ids[1] != 17
+    assert ids[2] == 0 and np.isnan(vals[2])
+    _lm_head_check(ids[:2], vals[:2], logits[:2], x[:2], w, 0.0)
+
+
 @pytest.mark.parametrize("ld", ["bf16", "f32"])
 def test_lm_head_then_sample(gpu, oracle, ld):
     """A sampled decode step: the LM head's logits stay in device memory and feed
