@@ -117,7 +117,7 @@ def main():
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16"
-        kernel_names = (["lmh_packed", "lmh_xfrag", "lmh_finish"] if packed else
+        kernel_names = (["lmh_packed", "lmh_finish"] if packed else
                         ["lmh_mfma" if B > 4 else "lmh_rows", "lmh_finish"])
         config = {"workload": name, "B": B, "H": H, "V": V,
                   "weight": "bf16 [V, H] packed at load time" if packed else "bf16 [V, H]"}

@@ -340,26 +340,30 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_finish(LmhParams P) {
 //
 // lmh_packed: 256-thread workgroups; each wave takes WR consecutive row
 // blocks of 32 vocab rows (adjacent in the packed layout) against the pass's
-// 32 NMT hidden rows, which lmh_xfrag first writes in the same fragment order
-// (1 KB per 16 ids and 32 rows, NMT KB per k-step, into the workspace), so a
-// wave reads its A operands as 1 KB loads of contiguous memory too; they stay
-// in the L2 that all the waves of an XCD share, and each serves WR row blocks.
-// A wave's weight and hidden fragments form one ring of R k-steps, requested
-// R k-steps ahead in straight-line code; there is no LDS and no barrier, so no
-// wave waits for another.  The k order of the sums is the one of lmh_mfma
-// (k-step s, lane half g: ids 16 s + 8 g .. + 7), so the two give the same
-// logits.
+// 32 NMT hidden rows.  Those are staged in LDS per range of KR ids, once per
+// workgroup, in the same fragment order (1 KB per 16 ids and 32 rows, a
+// 16-byte LDS read per lane), double-buffered with one barrier per range;
+// the next range's hidden values are requested before the current range's
+// MFMAs.  A wave's weight fragments form a ring of R k-steps, requested R
+// k-steps ahead in straight-line code.  The k order of the sums is the one of
+// lmh_mfma (k-step s, lane half g: ids 16 s + 8 g .. + 7), so the two give the
+// same logits.
 #define LMP_WG 256
 #define LMP_WAVES (LMP_WG / 64)
 #define LMP_SG 8                       // k-steps per contiguous group of a row block
 #define LMP_MB 64                      // hidden rows per pass
 #define LMP_HM 256                     // the H multiple of the packed layout
 
-template <int NMT, int WR, int R>
-__global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t* packed,
-                                                     const uint8_t* xfrag, int b0, int nb) {
+template <int NMT, int WR, int R, int KR>
+__global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t* packed, int b0,
+                                                     int nb) {
+    constexpr int SPR = KR / 16;                             // k-steps per range
+    constexpr int XB = SPR * NMT * 1024;                     // bytes of a staged range
+    constexpr int XQ = XB / 16 / LMP_WG;                     // 16-byte pieces per thread
+    static_assert(XQ * 16 * LMP_WG == XB && SPR % R == 0 && KR % LMP_HM == 0, "even split");
+    __shared__ __align__(16) uint8_t lx[2][XB];
     const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, r = lane & 31;
-    const int H = P.H, V = P.V, NS = H / 16, NRB = (V + 31) / 32;
+    const int H = P.H, V = P.V, NS = H / 16, NRB = (V + 31) / 32, nkr = H / KR;
     const int wv = (int)blockIdx.x * LMP_WAVES + wave;       // key slot
     const int rb0 = wv * WR;                                 // >= NRB: spare row blocks
     const size_t gstride = (size_t)NRB * LMP_SG * 1024;      // bytes between groups
@@ -367,20 +371,35 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
 #pragma unroll
     for (int j = 0; j < WR; ++j)
         wp[j] = packed + (size_t)(rb0 + j < NRB ? rb0 + j : NRB - 1) * LMP_SG * 1024 + lane * 16;
-    const uint8_t* xp = xfrag + lane * 16;
     auto wfrag = [&](int j, int f) {
         return __builtin_nontemporal_load(
             (const lmh_b8*)(wp[j] + (size_t)(f / LMP_SG) * gstride + (f % LMP_SG) * 1024));
     };
-    auto xfr = [&](int f, int mt) { return *(const lmh_b8*)(xp + (size_t)(f * NMT + mt) * 1024); };
-    lmh_b8 rw[R][WR], ra[R][NMT];
+    // staging: piece p = t + LMP_WG q is lane p % 64 of fragment (s, mt) =
+    // (p / 64 / NMT, p / 64 % NMT) of the range: 16 bytes of hidden row
+    // 32 mt + p % 32 (rows past nb read row b0; their sums are not used) at ids
+    // 16 s + 8 (p % 64 / 32) of the range
+    const uint16_t* gx[XQ];
 #pragma unroll
-    for (int i = 0; i < R; ++i) {                            // NS >= 16 >= R
+    for (int q = 0; q < XQ; ++q) {
+        const int p = t + LMP_WG * q, fr = p >> 6, mt = fr % NMT, s = fr / NMT;
+        const int m = 32 * mt + (p & 31);
+        gx[q] = P.hidden + (size_t)(b0 + (m < nb ? m : 0)) * H + 16 * s + 8 * ((p & 63) >> 5);
+    }
+    llima_u32x4 rx[XQ];
+    auto fetch_x = [&](int kr) {
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) rx[q] = *(const llima_u32x4*)(gx[q] + kr * KR);
+    };
+    auto stage_x = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) *(llima_u32x4*)(lx[buf] + (t + LMP_WG * q) * 16) = rx[q];
+    };
+    lmh_b8 rw[R][WR];
+#pragma unroll
+    for (int i = 0; i < R; ++i)                              // NS >= 16 >= R
 #pragma unroll
         for (int j = 0; j < WR; ++j) rw[i][j] = wfrag(j, i);
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) ra[i][mt] = xfr(i, mt);
-    }
     lmh_acc acc[WR][NMT];
 #pragma unroll
     for (int j = 0; j < WR; ++j)
@@ -388,25 +407,31 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
         for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[j][mt][i] = 0.0f;
-    for (int f0 = 0; f0 < NS; f0 += R) {                     // NS % R == 0
+    fetch_x(0);
+    stage_x(0);
+    __syncthreads();
+    for (int kr = 0; kr < nkr; ++kr) {
+        fetch_x(kr + 1 < nkr ? kr + 1 : nkr - 1);            // the next range, in flight
+        const uint8_t* xb = lx[kr & 1] + lane * 16;
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
+        for (int s = 0; s < SPR; ++s) {
+            const int f = kr * SPR + s, i = s % R;           // ring slot i holds k-step f
             lmh_b8 bo[WR], a[NMT];
 #pragma unroll
             for (int j = 0; j < WR; ++j) bo[j] = rw[i][j];
-#pragma unroll
-            for (int mt = 0; mt < NMT; ++mt) a[mt] = ra[i][mt];
-            const int fn = f0 + i + R < NS ? f0 + i + R : NS - 1;
+            const int fn = f + R < NS ? f + R : NS - 1;
 #pragma unroll
             for (int j = 0; j < WR; ++j) rw[i][j] = wfrag(j, fn);
 #pragma unroll
-            for (int mt = 0; mt < NMT; ++mt) ra[i][mt] = xfr(fn, mt);
+            for (int mt = 0; mt < NMT; ++mt) a[mt] = *(const lmh_b8*)(xb + (s * NMT + mt) * 1024);
 #pragma unroll
             for (int j = 0; j < WR; ++j)
 #pragma unroll
                 for (int mt = 0; mt < NMT; ++mt)
                     acc[j][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mt], bo[j], acc[j][mt], 0, 0, 0);
         }
+        stage_x((kr + 1) & 1);                               // its last readers passed the last barrier
+        __syncthreads();
     }
     // key slots past this grid's waves (a pass with more row blocks per wave
     // than another uses fewer of the P.NW slots): no logit
@@ -435,19 +460,6 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
         }
     }
-}
-
-// The pass's hidden rows in fragment order: piece p is lane p % 64 of
-// fragment (s, mt) = (p / 64 / nmt, p / 64 % nmt), i.e. 16 bytes of hidden row
-// 32 mt + p % 32 (zeros past nb) at ids 16 s + 8 (p % 64 / 32).
-__global__ __launch_bounds__(LLIMA_WG) void lmh_xfrag(const uint16_t* hidden, uint8_t* xfrag, int H,
-                                                      int b0, int nb, int nmt) {
-    const int p = (int)(blockIdx.x * LLIMA_WG + threadIdx.x);
-    if (p >= nmt * 64 * (H / 16)) return;
-    const int l = p & 63, fr = p >> 6, mt = fr % nmt, s = fr / nmt, m = 32 * mt + (l & 31);
-    llima_u32x4 v = {0u, 0u, 0u, 0u};
-    if (m < nb) v = *(const llima_u32x4*)(hidden + (size_t)(b0 + m) * H + 16 * s + 8 * (l >> 5));
-    *(llima_u32x4*)(xfrag + (size_t)p * 16) = v;
 }
 
 // One thread per 16-byte piece of the packed weight.
@@ -561,6 +573,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
 #define LMP_R1 8
 #define LMP_WR2 2
 #define LMP_R2 4
+#define LMP_KR 256                     // hidden ids per LDS-staged range
 
 // Workgroups of lmh_packed for WR row blocks per wave; its key slots per
 // hidden row are one per wave.
@@ -577,7 +590,7 @@ extern "C" size_t llima_lm_head_argmax_packed_workspace_bytes(int32_t B, int32_t
     if (B <= 0 || llima_lm_head_packed_bytes(V, H) == 0) return 0;
     const int g1 = lmp_groups(V, LMP_WR1), g2 = lmp_groups(V, LMP_WR2);
     const int nw = (g1 > g2 ? g1 : g2) * LMP_WAVES;
-    return lmh_align256((size_t)B * nw * sizeof(uint64_t)) + (size_t)LMP_MB * H * 2;
+    return lmh_align256((size_t)B * nw * sizeof(uint64_t));
 }
 
 extern "C" int llima_lm_head_pack(const void* weight, int32_t V, int32_t H, void* packed,
@@ -617,19 +630,15 @@ extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packe
     P.NW = (ng1 > ng2 ? ng1 : ng2) * LMP_WAVES;
     P.cap = softcap;
     P.round_bf16 = logit_dtype == LLIMA_BF16;
-    uint8_t* xf = (uint8_t*)workspace + lmh_align256((size_t)B * P.NW * sizeof(uint64_t));
     hipStream_t st = (hipStream_t)stream;
     for (int b0 = 0; b0 < B; b0 += LMP_MB) {
-        const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB, nmt = nb <= 32 ? 1 : 2;
-        const int np = nmt * 64 * (H / 16);
-        hipLaunchKernelGGL(lmh_xfrag, dim3((uint32_t)((np + LLIMA_WG - 1) / LLIMA_WG)),
-                           dim3(LLIMA_WG), 0, st, P.hidden, xf, H, b0, nb, nmt);
-        if (nmt == 1)
-            hipLaunchKernelGGL((lmh_packed<1, LMP_WR1, LMP_R1>), dim3(ng1), dim3(LMP_WG), 0, st, P,
-                               (const uint8_t*)packed, (const uint8_t*)xf, b0, nb);
+        const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB;
+        if (nb <= 32)
+            hipLaunchKernelGGL((lmh_packed<1, LMP_WR1, LMP_R1, LMP_KR>), dim3(ng1), dim3(LMP_WG), 0,
+                               st, P, (const uint8_t*)packed, b0, nb);
         else
-            hipLaunchKernelGGL((lmh_packed<2, LMP_WR2, LMP_R2>), dim3(ng2), dim3(LMP_WG), 0, st, P,
-                               (const uint8_t*)packed, (const uint8_t*)xf, b0, nb);
+            hipLaunchKernelGGL((lmh_packed<2, LMP_WR2, LMP_R2, LMP_KR>), dim3(ng2), dim3(LMP_WG), 0,
+                               st, P, (const uint8_t*)packed, b0, nb);
     }
     hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;

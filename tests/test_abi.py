@@ -116,7 +116,7 @@ def test_host_only_entry_points():
     assert L.llima_lm_head_pack(ctypes.c_void_p(24), 1000, 256, p, 1 << 20, None) == -1
     assert L.llima_lm_head_argmax_packed_workspace_bytes(1, 100, 1000) == 0
     wp = L.llima_lm_head_argmax_packed_workspace_bytes(1, 256, 1000)
-    assert wp >= 32 * 8 + 64 * 256 * 2                                     # keys + hidden fragments
+    assert wp >= 32 * 8                                       # a key per 32 vocab rows and row
     assert L.llima_lm_head_argmax_packed(p, p, 1, 100, 1000, 0.0, 1, p, None, None, p, wp,
                                          None) == -1
     assert L.llima_lm_head_argmax_packed(p, p, 1, 256, 1000, float("inf"), 1, p, None, None, p,
