@@ -434,10 +434,10 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
         __syncthreads();
     }
     // key slots past this grid's waves (a pass with more row blocks per wave
-    // than another uses fewer of the P.NW slots): no logit
-    if (blockIdx.x == gridDim.x - 1) {
+    // than another uses fewer of the P.NW slots): no logit, spread over the grid
+    {
         const int w0 = (int)gridDim.x * LMP_WAVES, nx = P.NW - w0;
-        for (int e = t; e < nx * nb; e += LMP_WG)
+        for (int e = (int)blockIdx.x * LMP_WG + t; e < nx * nb; e += (int)gridDim.x * LMP_WG)
             P.keys[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0;
     }
     // epilogue: softcap, logits, per hidden row the greatest key of the wave's

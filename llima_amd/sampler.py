@@ -524,9 +524,10 @@ def argmax_gemma4_mtp_masked_row(centroid_logits: torch.Tensor, token_ordering, 
 class PackedLmHead:
     """An LM head weight prepacked once, at model load, by lm_head_pack: the
     bf16 [V, H] weight rearranged into the MFMA's operand order (1 KB per 32
-    vocab rows x 16 ids, zero rows up to a multiple of 32), so that each wave
-    streams contiguous memory straight into the matrix cores.  `data` is the
-    uint8 device tensor; V and H are the weight's shape."""
+    vocab rows x 16 ids, zero rows up to a multiple of 32, 8 KB groups per 32
+    rows and 128 ids), so that each wave streams contiguous memory straight
+    into the matrix cores.  `data` is the uint8 device tensor; V and H are the
+    weight's shape.  It is read once per 64 hidden rows."""
 
     def __init__(self, data: torch.Tensor, V: int, H: int):
         self.data, self.V, self.H = data, V, H
