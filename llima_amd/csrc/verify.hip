@@ -51,6 +51,8 @@ namespace llima {
 #define VR_DCHUNK (LLIMA_WG * 8)     // ids per vr_drawsum workgroup (inside one chunk)
 #define VR_SLICE (VR_DCHUNK / LLIMA_WAVES)   // ids per vr_draw wave: two per thread of the draw
 #define VR_CNT_STRIDE 32             // arrival counters, one per 128-byte line
+#define VR_WS 16                     // uint64 per vr_draw workgroup's totals: one 128-byte line
+static_assert(LLIMA_WAVES == 4 && 2 * LLIMA_WAVES <= VR_WS, "a workgroup's 8 totals in its line");
 #define VR_FBITS 27                  // chunk factor F_c = rint(exp(m_c - M) 2^27)
 #define VR_ZBITS 32                  // width of the residual's normalizers
 #define VR_RSHIFT 21                 // residual scaling (sums below 2^64 for V <= 2^22)
@@ -66,8 +68,9 @@ struct VerifyParams {
     uint32_t* maxk;      // [NR][S] chunk maximum keys
     uint64_t* sums;      // [NR][S] chunk sums of w
     uint64_t* wx;        // [NR] w at the row's draft token (relative to its chunk)
-    uint64_t* bres;      // [B][SD][4] residual weight per vr_draw wave (VR_DCHUNK / 4 ids)
-    uint64_t* btgt;      // [B][SD][4] target weight per vr_draw wave
+    uint64_t* wsum;      // [B][SD][VR_WS]: per vr_draw workgroup, the target weight of each of
+                         // its 4 waves (VR_DCHUNK / 4 ids), then their residual weight; each
+                         // workgroup's line is written by it alone
     uint32_t* cnt;       // [B][VR_CNT_STRIDE] arrival counters (zeroed by vr_rowpass)
     int32_t B, D, V, S, NR, SD;
 };
@@ -489,8 +492,9 @@ __device__ __forceinline__ void draw_final(const VerifyParams& P, int b, int acc
     const uint32_t t = threadIdx.x;
     const int NI = P.SD * LLIMA_WAVES, IPT = (NI + LLIMA_WG - 1) / LLIMA_WG;
     const int i0 = (int)t * IPT, i1 = i0 + IPT < NI ? i0 + IPT : NI;
-    uint64_t* br = P.bres + (size_t)b * NI;
-    uint64_t* bt = P.btgt + (size_t)b * NI;
+    uint64_t* ws = P.wsum + (size_t)b * P.SD * VR_WS;
+    auto bt = [&](int i) { return ws + (i >> 2) * VR_WS + (i & 3); };      // wave slice i
+    auto br = [&](int i) { return ws + (i >> 2) * VR_WS + 4 + (i & 3); };
     const uint32_t u32 = uniform32(P.u_resample[b]);
     // the emitted drafts, requested with the totals
     const int em = (int)t < acc && (int)t < P.D ? P.draft_ids[b * P.D + t] : -1;
@@ -500,8 +504,8 @@ __device__ __forceinline__ void draw_final(const VerifyParams& P, int b, int acc
     }
     uint64_t sr = 0, st = 0;
     for (int i = i0; i < i1; ++i) {
-        sr += load_agent(br + i);
-        st += load_agent(bt + i);
+        sr += load_agent(br(i));
+        st += load_agent(bt(i));
     }
     // exclusive scans of both sums over the workgroup, and their totals
     const uint64_t ir = wave_incl_scan_u64(sr), it = wave_incl_scan_u64(st);
@@ -526,10 +530,9 @@ __device__ __forceinline__ void draw_final(const VerifyParams& P, int b, int acc
             sh.item = i0;
             sh.before = before;
         } else {
-            uint64_t* bs = q.residual ? br : bt;
             uint64_t a = before;
             for (int i = i0; i < i1; ++i) {                // the owner's slices, once more
-                const uint64_t v = load_agent(bs + i);
+                const uint64_t v = load_agent(q.residual ? br(i) : bt(i));
                 if (a + v > target) { sh.item = i; sh.before = a; break; }
                 a += v;
             }
@@ -601,9 +604,9 @@ __global__ __launch_bounds__(LLIMA_WG) void vr_draw(VerifyParams P) {
     // each wave's two totals (a wave slice of VR_SLICE ids)
     const uint64_t wt_ = wave_sum_u64(st), wr_ = wave_sum_u64(sr);
     if (lane_id() == 0) {
-        const size_t o = ((size_t)b * P.SD + c) * LLIMA_WAVES + wave_id();
-        store_agent(P.btgt + o, wt_);
-        store_agent(P.bres + o, wr_);
+        uint64_t* o = P.wsum + ((size_t)b * P.SD + c) * VR_WS + wave_id();
+        store_agent(o, wt_);
+        store_agent(o + 4, wr_);
     }
     // every store of the workgroup completes before its arrival is counted
     __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
@@ -628,7 +631,7 @@ extern "C" size_t llima_verify_rejection_workspace_bytes(int32_t B, int32_t D, i
     const size_t S = (size_t)(V + VR_CHUNK - 1) / VR_CHUNK;
     const size_t NR = (size_t)B * (2 * D + 1);
     const size_t SD = (size_t)(V + VR_DCHUNK - 1) / VR_DCHUNK;
-    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + 2 * al256((size_t)B * SD * LLIMA_WAVES * 8) + al256((size_t)B * VR_CNT_STRIDE * 4);
+    return al256(NR * S * 4) + al256(NR * S * 8) + al256(NR * 8) + al256((size_t)B * SD * VR_WS * 8) + al256((size_t)B * VR_CNT_STRIDE * 4);
 }
 
 extern "C" int llima_verify_rejection(const float* target_logits, const float* draft_logits,
@@ -656,8 +659,7 @@ extern "C" int llima_verify_rejection(const float* target_logits, const float* d
     P.maxk = (uint32_t*)w;  w += al256((size_t)P.NR * P.S * 4);
     P.sums = (uint64_t*)w;  w += al256((size_t)P.NR * P.S * 8);
     P.wx = (uint64_t*)w;    w += al256((size_t)P.NR * 8);
-    P.bres = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
-    P.btgt = (uint64_t*)w;  w += al256((size_t)B * P.SD * LLIMA_WAVES * 8);
+    P.wsum = (uint64_t*)w;  w += al256((size_t)B * P.SD * VR_WS * 8);
     P.cnt = (uint32_t*)w;
     hipStream_t st = (hipStream_t)stream;
     const uint32_t g12 = (uint32_t)P.NR * (uint32_t)P.S;
