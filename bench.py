@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="batched_penalties",
-                    choices=["batched_penalties", "single_row", "constrained",
+                    choices=["batched_penalties", "single_row", "constrained", "top_p_only",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
@@ -214,7 +214,8 @@ def main():
             base = torch.from_numpy(lg).to(dev)
         g = torch.Generator(device=dev)
         g.manual_seed(2000)
-        sigma = {"single_row": 3.0, "batched_penalties": 4.0, "constrained": 3.0}.get(name, 5.0)
+        sigma = {"single_row": 3.0, "batched_penalties": 4.0, "constrained": 3.0,
+                 "top_p_only": 4.0}.get(name, 5.0)
         bufs = [base]
         for i in range(1, nbuf):
             x = torch.randn((B, V), generator=g, device=dev) * sigma

@@ -886,6 +886,36 @@ __device__ __forceinline__ void count_history(const SampleParams& P, int row, in
 }
 
 // ------------------------------------------------------------------ full-row path
+#define SMP_FE 16                                  // values per thread per full-row step
+
+// SMP_FE consecutive values from id i0 of a row, ids at or past hi (a multiple
+// of the values per 16-byte load when vec) read from clamped addresses: 16-byte
+// loads when vec (the row 16-byte aligned), else one value per load, every
+// load issued before the first value is used.
+template <typename TL>
+__device__ __forceinline__ void load_fe(const TL* rowp, int i0, int hi, bool vec, float (&xs)[SMP_FE]) {
+    constexpr int EPL = 16 / sizeof(TL);             // values per 16-byte load
+    if (vec) {
+        llima_u32x4 q[SMP_FE / EPL];
+#pragma unroll
+        for (int j = 0; j < SMP_FE / EPL; ++j) {
+            const int ia = i0 + j * EPL < hi ? i0 + j * EPL : hi - EPL;
+            q[j] = *(const llima_u32x4*)(rowp + ia);
+        }
+#pragma unroll
+        for (int j = 0; j < SMP_FE / EPL; ++j) {
+            const uint32_t w4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                if constexpr (sizeof(TL) == 4) xs[j * EPL + e] = __uint_as_float(w4[e]);
+                else xs[j * EPL + e] = __uint_as_float((e & 1) ? (w4[e >> 1] & 0xFFFF0000u) : (w4[e >> 1] << 16));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < SMP_FE; ++e) xs[e] = load_one<TL>(rowp, i0 + e < hi ? i0 + e : hi - 1);
+    }
+}
 // Exact multi-pass selection by one workgroup; recomputes x for the whole row on
 // every pass (history table rebuilt per segment).
 template <typename TL>
@@ -896,19 +926,33 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * nw : nullptr;
     uint32_t* table = sh.u.table;
     __syncthreads();
+    // Every pass visits the row in steps of LLIMA_WG * SMP_FE ids: thread t
+    // takes SMP_FE consecutive ids and requests all of them (16-byte loads when
+    // the rows allow) before the first is used, so a step costs one memory
+    // round trip instead of one per value.
+    const bool vec = P.vec_ok != 0;
     auto for_each_x = [&](auto fn) {
         for (int lo = 0; lo < V; lo += SMP_SEG) {
             const int hi = lo + SMP_SEG < V ? lo + SMP_SEG : V;
             if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SMP_SEG / 2);
-            for (int i = lo + threadIdx.x; i < hi; i += LLIMA_WG) {
-                float l = load_one<TL>(rowp, i);
-                if (l != l) l = -__builtin_inff();
-                if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) l = -__builtin_inff();
-                if (c.pen) {
-                    const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
-                    if (cnt) l = penalize(l, cnt, c);
+            for (int b0 = lo; b0 < hi; b0 += LLIMA_WG * SMP_FE) {
+                const int i0 = b0 + (int)threadIdx.x * SMP_FE;
+                float xs[SMP_FE];
+                load_fe<TL>(rowp, i0, hi, vec, xs);
+#pragma unroll
+                for (int e = 0; e < SMP_FE; ++e) {
+                    const int i = i0 + e;
+                    if (i < hi) {
+                        float l = xs[e];
+                        if (l != l) l = -__builtin_inff();
+                        if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) l = -__builtin_inff();
+                        if (c.pen) {
+                            const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
+                            if (cnt) l = penalize(l, cnt, c);
+                        }
+                        fn(c.greedy ? l : l / c.T, (uint32_t)i);
+                    }
                 }
-                fn(c.greedy ? l : l / c.T, (uint32_t)i);
             }
             __syncthreads();
         }

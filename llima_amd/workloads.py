@@ -168,10 +168,23 @@ def lm_head_argmax(B=1, H=4096, V=128256, seed=1008):
     return dict(name="lm_head_argmax", hidden=hidden, B=B, H=H, V=V, seed=seed)
 
 
+def top_p_only(B=64, V=128256, seed=1002):
+    """The headline rows (B=64, fp32 vocab 128256, N(0, 4^2)) sampled with
+    top-p alone: T 1.0, top-p 0.9, no top-k, no penalties, no mask.  Nearly
+    every value lies within 27 T of its chunk's maximum, so no bound narrows the
+    candidates and every row takes the exact full-row path."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 4.0)
+    u = rng.random(B, dtype=np.float32)
+    return dict(name="top_p_only", logits=logits, history=None, uniforms=u, bitmask=None,
+                cfg=dict(temperature=1.0, top_p=0.9))
+
+
 WORKLOADS = {
     "single_row": single_row,
     "batched_penalties": batched_penalties,
     "constrained": constrained,
+    "top_p_only": top_p_only,
     "speculative": speculative,
     "large_vocab_bf16": large_vocab_bf16,
     "score_bf16": score_bf16,
