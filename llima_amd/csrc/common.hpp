@@ -267,6 +267,22 @@ __device__ __forceinline__ uint32_t wave_rth_largest_exp(uint32_t key, uint32_t 
     return wave_rth_largest(key, r, lowbit);
 }
 
+// ------------------------------------------------------------------ cross-workgroup sums
+// Values that other workgroups read inside the same launch: relaxed agent-scope
+// atomic stores (write-through) and loads (they miss stale cache lines).  The
+// writer waits for its stores (LLIMA_WAITCNT_VM0) before it counts its arrival
+// on an agent-scope counter, so the last workgroup to arrive sees every value
+// with no cache writeback or invalidation.
+__device__ __forceinline__ void store_agent(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent(uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t arrive_agent(uint32_t* counter, uint32_t n) {
+    return __hip_atomic_fetch_add(counter, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------ block primitives
 // All block helpers must be called by every thread of the workgroup.
 struct BlockScratch {

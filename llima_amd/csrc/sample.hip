@@ -679,12 +679,14 @@ __device__ __forceinline__ uint64_t wg_prefix_u64(uint64_t inc, uint64_t v, uint
 // into buffer r % 3 (buffers 0 and 1 zero on entry; non-members count into a
 // spare bin per lane), then every wave scans all 256 bins itself and zeroes
 // buffer (r + 2) % 3.  Round 0 holds every element, so its total is Z.  Stops
-// early when the selected bin holds one key.
+// early when the selected bin holds one key.  With pz_given the elements are
+// the part of a larger set below a mass `above`, and PZ0 = p32 * Z of that set.
 template <int EPT>
 __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
-                                  uint64_t p32, uint32_t kmin, uint32_t kmax, FinShared& sh) {
+                                  uint64_t p32, uint32_t kmin, uint32_t kmax, FinShared& sh,
+                                  uint64_t above = 0, llima_u128 PZ0 = 0, bool pz_given = false) {
     Digits d = digits_init(kmin, kmax);
-    uint64_t acc = 0;
+    uint64_t acc = above;
     llima_u128 PZ = 0;
     bool first = true;
     const uint32_t t = threadIdx.x, lane = lane_id();
@@ -715,7 +717,7 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
         sh.hmass[nxt][t] = 0;
         const uint64_t m4 = ms[0] + ms[1] + ms[2] + ms[3];
         const uint64_t inc = wave_incl_scan_u64(m4);
-        if (first) PZ = (llima_u128)p32 * readlane63(inc);          // p32 * Z
+        if (first) PZ = pz_given ? PZ0 : (llima_u128)p32 * readlane63(inc);   // p32 * Z
         first = false;
         uint64_t ab = acc + inc - m4;                               // mass above the lane's top bin
         // last qualifying bin of the lane (lowest key), first non-empty bin
@@ -1991,6 +1993,568 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     FIN_MARK(13);
 }
 
+// ================================================================== dense path
+// Rows without top-k and without a grammar mask: top-p, min-p or plain
+// temperature over the whole row.  The sweep's bound for such rows is the
+// chunk maximum - 27 T (a weight is nonzero down to 25.6 nats below the row
+// maximum), which on ordinary logits admits nearly every value: every region
+// would overflow and one workgroup per row would make the full-row passes.
+// These rows are selected instead by the workgroups of all their chunks in
+// parallel (one 16 KB chunk per workgroup, the sweep's lane layout), over
+// three reads of the row:
+//   dense_stats  the chunk's maximum key and finite count, or on greedy rows
+//                its (key, first id) maximum;
+//   dense_hist   rows with top-p: the chunk's exact weights counted into
+//                SMP_DBINS value bins of 1/16 nat below the row maximum (bin
+//                floor(16 (xmax - x)), monotone in the key, the last open) as
+//                (mass << 14) + count; the row's last workgroup to finish
+//                merges the chunks' bins and finds the bin holding the top-p
+//                boundary: the last non-empty bin whose mass above, times
+//                2^32, is below p32 Z (the top non-empty bin when none is);
+//   dense_keep   the chunk's kept mass strictly above that bin (min-p
+//                applied), its words of the kept-set mask, and the bin's
+//                members (key, id) appended to the row's member list;
+//   dense_final  one workgroup per row: the members ranked by radix rounds
+//                over their keys, starting from the mass above the bin, give
+//                theta (the full-row path's boundary: the smallest key whose
+//                mass strictly above, times 2^32, is below p32 Z); the kept
+//                members' weights are added to their chunks, a scan over the
+//                chunks' kept masses finds the chunk of the draw target and a
+//                scan of that chunk in id order the token.
+// Every weight, bin and test is the full-row path's arithmetic on the same
+// values, so the kept set, the token and its probability are the same.  A row
+// whose boundary bin holds more members than dense_final ranks (more than
+// 4096 values within 1/16 nat: a nearly flat row) is finished there by the
+// full-row path.
+//
+// Region use per row (the row's S regions of SMP_REGION slots):
+//   region c, slots [0, SMP_DBINS)  dense_hist's bins of chunk c, then the
+//                                   boundary members (member j at region
+//                                   j / SMP_DBINS, slot j % SMP_DBINS)
+//   region c, SMP_DSTAT / SMP_DBEST  dense_stats's results for chunk c
+//   region c, SMP_DKEPT             dense_keep's kept mass of chunk c
+//   region 0, SMP_DINFO..+2         boundary bin, mass above it, Z
+//   region 0, SMP_DARR / SMP_DMEM   counters (128-byte lines of their own),
+//                                   zeroed by dense_stats
+#define SMP_DBINS 448                              // value bins, 1/16 nat (28 nats; the last open)
+#define SMP_DBIN_SCALE 16.0f
+#define SMP_DSTAT 448                              // chunk max key << 32 | finite count
+#define SMP_DBEST 449                              // greedy: key << 32 | ~id of the chunk maximum
+#define SMP_DKEPT 450                              // kept mass strictly above the boundary bin
+#define SMP_DINFO 456                              // region 0: boundary bin, mass above it, Z
+#define SMP_DARR 480                               // region 0: dense_hist arrivals
+#define SMP_DMEM 496                               // region 0: boundary members appended
+#define SMP_DMCAP 4096                             // members dense_final ranks (16 per thread)
+static_assert(SMP_DBINS <= SMP_DSTAT && SMP_DMEM + 16 <= SMP_REGION, "dense region layout");
+static_assert(SMP_DMCAP == 16 * LLIMA_WG, "dense_final holds 16 members per thread");
+
+template <typename TL>
+struct DenseGeom {
+    static constexpr int EPL = 16 / (int)sizeof(TL);   // values per 16-byte load
+    static constexpr int NL = 4;                       // loads per thread and chunk
+    static constexpr int E = NL * EPL;                 // values per thread
+    static constexpr int CHUNK = LLIMA_WG * E;         // 4096 fp32 / 8192 bf16 (the sweep's chunk)
+    static constexpr int WS = CHUNK / LLIMA_WAVES;     // ids per wave
+};
+
+// The value bin of x below the row maximum xmax (x <= xmax, x not NaN).
+__device__ __forceinline__ uint32_t dense_bin(float x, float xmax) {
+    const float d = __builtin_fminf((xmax - x) * SMP_DBIN_SCALE, (float)(SMP_DBINS - 1));
+    return x == xmax ? 0u : (uint32_t)d;
+}
+
+__device__ __forceinline__ uint64_t* dense_member(uint64_t* r0, uint32_t j) {
+    return r0 + (size_t)(j / SMP_DBINS) * SMP_REGION + (j % SMP_DBINS);
+}
+
+__device__ __forceinline__ uint32_t dense_member_cap(int S) {
+    const uint32_t n = (uint32_t)S * SMP_DBINS;
+    return n < SMP_DMCAP ? n : SMP_DMCAP;
+}
+
+// A value after the row's transform, in the full-row path's order: NaN ->
+// -inf, the penalties (cnt occurrences in the history), / T unless greedy.
+__device__ __forceinline__ float dense_x(float l, uint32_t cnt, const RowCfg& c) {
+    if (l != l) l = -__builtin_inff();
+    if (cnt) l = penalize(l, cnt, c);
+    return c.greedy ? l : l / c.T;
+}
+
+// The loads of the row's first SMP_HBATCH * LLIMA_WG history ids (clamped to
+// H_max; the count checks the row's own length).
+__device__ __forceinline__ void dense_hist_ids(const SampleParams& P, int row, int32_t (&hid)[SMP_HBATCH]) {
+    const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+#pragma unroll
+    for (int b = 0; b < SMP_HBATCH; ++b) {
+        const int j = (int)threadIdx.x + b * LLIMA_WG;
+        hid[b] = hrow[j < P.H_max ? j : P.H_max - 1];
+    }
+}
+
+// Counts the row's history ids in [lo, lo + n) into table (n / 2 words, two
+// 16-bit counts each); the first batch of ids from hid.
+__device__ __forceinline__ void dense_count(const SampleParams& P, int row, const RowCfg& c,
+                                            const int32_t (&hid)[SMP_HBATCH], int lo, int n,
+                                            uint32_t* table) {
+    const int t = (int)threadIdx.x;
+    for (int i = t; i < n / 8; i += LLIMA_WG) ((llima_u32x4*)table)[i] = llima_u32x4{0, 0, 0, 0};
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < SMP_HBATCH; ++b) {
+        const int32_t id = hid[b];
+        if (t + b * LLIMA_WG < c.hlen && id >= lo && id < lo + n) {
+            const uint32_t off = (uint32_t)(id - lo);
+            atomicAdd(&table[off >> 1], 1u << ((off & 1u) * 16u));
+        }
+    }
+    const int32_t* hrow = P.hist + (size_t)row * P.H_max;
+    for (int j = t + SMP_HBATCH * LLIMA_WG; j < c.hlen; j += LLIMA_WG) {
+        const int32_t id = hrow[j];
+        if (id >= lo && id < lo + n) {
+            const uint32_t off = (uint32_t)(id - lo);
+            atomicAdd(&table[off >> 1], 1u << ((off & 1u) * 16u));
+        }
+    }
+    __syncthreads();
+}
+
+// Id of value (j, e) of this lane in the chunk from c0: wave w owns ids
+// [w WS, (w + 1) WS), load j of lane l covers EPL ids at j 64 EPL + l EPL.
+template <typename TL>
+__device__ __forceinline__ int dense_id(int c0, int j, int e) {
+    using G = DenseGeom<TL>;
+    return c0 + (int)wave_id() * G::WS + j * 64 * G::EPL + (int)lane_id() * G::EPL + e;
+}
+
+// The chunk's 16-byte loads (clamped, always-valid addresses), issued before
+// any use.
+template <typename TL>
+__device__ __forceinline__ void dense_issue(const SampleParams& P, int row, int c0,
+                                            llima_u32x4 (&raw)[DenseGeom<TL>::NL]) {
+    using G = DenseGeom<TL>;
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    const int V = P.V;
+    if (P.vec_ok) {
+#pragma unroll
+        for (int j = 0; j < G::NL; ++j) {
+            const int i0 = dense_id<TL>(c0, j, 0);
+            const int ia = i0 < V ? i0 : V - G::EPL;
+            raw[j] = __builtin_nontemporal_load((const llima_u32x4*)(rowp + ia));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < G::NL; ++j) {
+            const int i0 = dense_id<TL>(c0, j, 0);
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < G::EPL; ++e) {
+                const int ia = i0 + e < V ? i0 + e : V - 1;
+                const float f = load_one<TL>(rowp, ia);
+                if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
+                else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+            }
+            raw[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// The chunk's values after the row's transform; ids past the row are -inf.
+template <typename TL>
+__device__ __forceinline__ void dense_unpack(const SampleParams& P, const RowCfg& c, int c0,
+                                             const llima_u32x4 (&raw)[DenseGeom<TL>::NL],
+                                             const uint32_t* table, float (&x)[DenseGeom<TL>::E]) {
+    using G = DenseGeom<TL>;
+#pragma unroll
+    for (int j = 0; j < G::NL; ++j) {
+        const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+        for (int e = 0; e < G::EPL; ++e) {
+            const int i = dense_id<TL>(c0, j, e);
+            uint32_t bits;
+            if constexpr (sizeof(TL) == 4) bits = w4[e];
+            else bits = (e & 1) ? (w4[e >> 1] & 0xFFFF0000u) : (w4[e >> 1] << 16);
+            const float l = i < P.V ? __uint_as_float(bits) : -__builtin_inff();
+            const uint32_t cnt = c.pen ? table_count(table, (uint32_t)(i - c0)) : 0u;
+            x[j * G::EPL + e] = dense_x(l, cnt, c);
+        }
+    }
+}
+
+// The row's maximum key and finite count from the chunks' statistics, read
+// by every wave (lane i: chunks i, i + 64, ...) and reduced with DPP.
+__device__ __forceinline__ void dense_row_stats(const SampleParams& P, int row, uint32_t* kmax,
+                                                uint32_t* nfin) {
+    const uint64_t* r0 = region_of(P, (uint32_t)row, 0);
+    uint32_t km = 0, nf = 0;
+    for (int i = (int)lane_id(); i < P.S; i += 64) {
+        const uint64_t v = r0[(size_t)i * SMP_REGION + SMP_DSTAT];
+        const uint32_t k = (uint32_t)(v >> 32);
+        km = k > km ? k : km;
+        nf += (uint32_t)v;
+    }
+    *kmax = wave_max_u32(km);
+    *nfin = wave_sum_u32(nf);
+}
+
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void dense_stats(SampleParams P) {
+    using G = DenseGeom<TL>;
+    extern __shared__ __align__(16) uint32_t table[];   // history counts (rows with penalties)
+    __shared__ BlockScratch bs;
+    uint32_t row, chunk;
+    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
+    if (row >= (uint32_t)P.B) return;
+    const int c0 = (int)chunk * G::CHUNK;
+    int32_t hid[SMP_HBATCH];
+    if (P.H_max > 0) dense_hist_ids(P, (int)row, hid);
+    llima_u32x4 raw[G::NL];
+    dense_issue<TL>(P, (int)row, c0, raw);
+    const RowCfg c = load_cfg(P, (int)row);
+    if (c.pen) dense_count(P, (int)row, c, hid, c0, G::CHUNK, table);
+    float x[G::E];
+    dense_unpack<TL>(P, c, c0, raw, table, x);
+    uint64_t* reg = region_of(P, row, chunk);
+    if (c.greedy) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < G::NL; ++j)
+#pragma unroll
+            for (int e = 0; e < G::EPL; ++e) {
+                const uint32_t id = (uint32_t)dense_id<TL>(c0, j, e);
+                const uint64_t kk = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) | (uint64_t)(~id);
+                best = kk > best ? kk : best;
+            }
+        best = block_max_u64(best, bs);
+        if (threadIdx.x == 0) reg[SMP_DBEST] = best;
+    } else {
+        uint32_t km = 0, nf = 0;
+#pragma unroll
+        for (int i = 0; i < G::E; ++i) {
+            const uint32_t k = f32_key(x[i]);
+            const bool fin = k > LLIMA_KEY_NEG_INF;
+            nf += fin ? 1u : 0u;
+            km = fin && k > km ? k : km;
+        }
+        km = block_max_u32(km, bs);
+        nf = block_sum_u32(nf, bs);
+        if (threadIdx.x == 0) reg[SMP_DSTAT] = ((uint64_t)km << 32) | nf;
+    }
+    if (chunk == 0 && threadIdx.x == 0) {
+        reg[SMP_DARR] = 0;
+        reg[SMP_DMEM] = 0;
+    }
+}
+
+// The top-p boundary bin of a row from its chunks' bins, by the row's last
+// dense_hist workgroup: thread t merges bins 2t and 2t + 1 over the chunks.
+__device__ __forceinline__ void dense_boundary(const SampleParams& P, int row, const RowCfg& c,
+                                               BlockScratch& bs) {
+    const uint32_t t = threadIdx.x;
+    uint64_t* r0 = region_of(P, (uint32_t)row, 0);
+    uint32_t cn0 = 0, cn1 = 0;
+    uint64_t m0 = 0, m1 = 0;
+    if (t < SMP_DBINS / 2) {
+#pragma unroll 4
+        for (int i = 0; i < P.S; ++i) {
+            uint64_t* q = r0 + (size_t)i * SMP_REGION + 2u * t;
+            const uint64_t h0 = load_agent(q), h1 = load_agent(q + 1);
+            cn0 += (uint32_t)(h0 & 0x3FFFu);
+            m0 += h0 >> 14;
+            cn1 += (uint32_t)(h1 & 0x3FFFu);
+            m1 += h1 >> 14;
+        }
+    }
+    uint64_t Z;
+    const uint64_t ab = block_excl_scan_u64(m0 + m1, &Z, bs);   // mass above bin 2t
+    const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+    const bool q0 = cn0 > 0u && (((llima_u128)ab << 32) < PZ);
+    const bool q1 = cn1 > 0u && (((llima_u128)(ab + m0) << 32) < PZ);
+    const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), bs);
+    const uint32_t ne = cn0 ? 2u * t : (cn1 ? 2u * t + 1u : 0xFFFFFFFFu);
+    const uint32_t top = ~block_max_u32(~ne, bs);               // top non-empty bin
+    const uint32_t bstar = qb ? qb - 1u : top;
+    if ((bstar >> 1) == t) {
+        r0[SMP_DINFO] = bstar;
+        r0[SMP_DINFO + 1] = (bstar & 1u) ? ab + m0 : ab;
+        r0[SMP_DINFO + 2] = Z;
+    }
+}
+
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void dense_hist(SampleParams P) {
+    using G = DenseGeom<TL>;
+    extern __shared__ __align__(16) uint32_t table[];
+    __shared__ uint64_t hist[SMP_DBINS + 64];           // + a spare bin per lane
+    __shared__ BlockScratch bs;
+    __shared__ uint32_t last;
+    uint32_t row, chunk;
+    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
+    if (row >= (uint32_t)P.B) return;
+    const int c0 = (int)chunk * G::CHUNK;
+    int32_t hid[SMP_HBATCH];
+    if (P.H_max > 0) dense_hist_ids(P, (int)row, hid);
+    llima_u32x4 raw[G::NL];
+    dense_issue<TL>(P, (int)row, c0, raw);
+    const RowCfg c = load_cfg(P, (int)row);
+    if (c.greedy || !(c.p < 1.0f)) return;              // uniform: no top-p on this row
+    uint32_t kmax, nfin;
+    dense_row_stats(P, (int)row, &kmax, &nfin);
+    if (nfin == 0) return;
+    const uint32_t t = threadIdx.x, lane = lane_id();
+    for (uint32_t i = t; i < SMP_DBINS + 64; i += LLIMA_WG) hist[i] = 0;
+    if (c.pen) dense_count(P, (int)row, c, hid, c0, G::CHUNK, table);
+    __syncthreads();
+    float x[G::E];
+    dense_unpack<TL>(P, c, c0, raw, table, x);
+    const float xmax = key_f32(kmax);
+#pragma unroll
+    for (int i = 0; i < G::E; ++i) {
+        const bool fin = f32_key(x[i]) > LLIMA_KEY_NEG_INF;
+        const uint64_t w = weight(x[i], xmax);
+        const uint32_t b = fin ? dense_bin(x[i], xmax) : SMP_DBINS + lane;
+        atomicAdd((unsigned long long*)&hist[b], (unsigned long long)((w << 14) | 1ull));
+    }
+    __syncthreads();
+    uint64_t* reg = region_of(P, row, chunk);
+    for (uint32_t i = t; i < SMP_DBINS; i += LLIMA_WG) store_agent(reg + i, hist[i]);
+    __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
+    __syncthreads();
+    if (t == 0)
+        last = arrive_agent((uint32_t*)(region_of(P, row, 0) + SMP_DARR), 1u) == (uint32_t)P.S - 1u;
+    __syncthreads();
+    if (last) dense_boundary(P, (int)row, c, bs);
+}
+
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void dense_keep(SampleParams P) {
+    using G = DenseGeom<TL>;
+    extern __shared__ __align__(16) uint32_t table[];
+    __shared__ BlockScratch bs;
+    __shared__ uint32_t mbase;
+    uint32_t row, chunk;
+    map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
+    if (row >= (uint32_t)P.B) return;
+    const int c0 = (int)chunk * G::CHUNK;
+    int32_t hid[SMP_HBATCH];
+    if (P.H_max > 0) dense_hist_ids(P, (int)row, hid);
+    llima_u32x4 raw[G::NL];
+    dense_issue<TL>(P, (int)row, c0, raw);
+    const RowCfg c = load_cfg(P, (int)row);
+    if (c.greedy) return;                               // dense_final writes greedy rows
+    uint32_t kmax, nfin;
+    dense_row_stats(P, (int)row, &kmax, &nfin);
+    if (nfin == 0) return;
+    const bool topp = c.p < 1.0f;
+    uint64_t* r0 = region_of(P, row, 0);
+    const uint32_t bstar = topp ? (uint32_t)r0[SMP_DINFO] : (uint32_t)SMP_DBINS;
+    if (c.pen) dense_count(P, (int)row, c, hid, c0, G::CHUNK, table);
+    float x[G::E];
+    dense_unpack<TL>(P, c, c0, raw, table, x);
+    const float xmax = key_f32(kmax);
+    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    const uint32_t lane = lane_id();
+    uint64_t km = 0;
+    uint32_t nm = 0;
+    uint32_t kb[G::NL];
+#pragma unroll
+    for (int j = 0; j < G::NL; ++j) {
+        kb[j] = 0;
+#pragma unroll
+        for (int e = 0; e < G::EPL; ++e) {
+            const float xv = x[j * G::EPL + e];
+            const bool fin = f32_key(xv) > LLIMA_KEY_NEG_INF;
+            const uint64_t w = weight(xv, xmax);
+            const uint32_t b = dense_bin(xv, xmax);
+            const bool kept = fin && b < bstar && w >= mthr;
+            km += kept ? w : 0ull;
+            kb[j] |= kept ? 1u << e : 0u;
+            nm += fin && b == bstar ? 1u : 0u;
+        }
+    }
+    if (P.out_keep) {
+        // lanes sharing a 32-id word: 32 / EPL of them (the chunk starts on a word)
+        const int nw = (P.V + 31) >> 5;
+        uint32_t* kw = P.out_keep + (size_t)row * nw;
+        constexpr int LPW = 32 / G::EPL;
+#pragma unroll
+        for (int j = 0; j < G::NL; ++j) {
+            uint32_t word = kb[j] << ((lane * G::EPL) & 31u);
+#pragma unroll
+            for (int s = 1; s < LPW; s <<= 1) word |= (uint32_t)__shfl_xor((int)word, s);
+            const int i0 = dense_id<TL>(c0, j, 0);
+            if ((lane & (LPW - 1)) == 0 && i0 < P.V) kw[i0 >> 5] = word;
+        }
+    }
+    km = block_sum_u64(km, bs);
+    if (threadIdx.x == 0) region_of(P, row, chunk)[SMP_DKEPT] = km;
+    if (topp) {
+        uint32_t tot;
+        const uint32_t off = block_excl_scan_u32(nm, &tot, bs);
+        if (tot) {                                       // uniform
+            if (threadIdx.x == 0) mbase = arrive_agent((uint32_t*)(r0 + SMP_DMEM), tot);
+            __syncthreads();
+            const uint32_t cap = dense_member_cap(P.S);
+            uint32_t o = mbase + off;
+#pragma unroll
+            for (int j = 0; j < G::NL; ++j)
+#pragma unroll
+                for (int e = 0; e < G::EPL; ++e) {
+                    const float xv = x[j * G::EPL + e];
+                    const uint32_t k = f32_key(xv);
+                    if (k > LLIMA_KEY_NEG_INF && dense_bin(xv, xmax) == bstar) {
+                        if (o < cap)
+                            *dense_member(r0, o) = ((uint64_t)k << 32) | (uint32_t)dense_id<TL>(c0, j, e);
+                        ++o;
+                    }
+                }
+        }
+    }
+}
+
+template <typename TL>
+__global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
+    using G = DenseGeom<TL>;
+    constexpr int EPT = SMP_DMCAP / LLIMA_WG;
+    __shared__ FinShared sh;
+    __shared__ uint64_t cmass[SMP_MAX_S];
+    __shared__ uint32_t dsel;
+    __shared__ uint64_t drel;
+    const int row = blockIdx.x;
+    const RowCfg c = load_cfg(P, row);
+    const uint32_t t = threadIdx.x;
+    const int S = P.S;
+    uint64_t* r0 = region_of(P, (uint32_t)row, 0);
+    if (t == 0) {             // overwritten by the thread whose chunk holds the target
+        dsel = 0;
+        drel = 0;
+    }
+    if (c.greedy) {
+        uint64_t best = 0;
+        for (int i = (int)t; i < S; i += LLIMA_WG) {
+            const uint64_t v = r0[(size_t)i * SMP_REGION + SMP_DBEST];
+            best = v > best ? v : best;
+        }
+        best = block_max_u64(best, sh.bs);
+        const bool ok = (uint32_t)(best >> 32) > LLIMA_KEY_NEG_INF;
+        const uint32_t tok = ok ? ~(uint32_t)best : 0xFFFFFFFFu;
+        if (t == 0) write_result(P, row, ok ? (int32_t)tok : -1, ok ? 1.0f : 0.0f);
+        if (P.out_keep)
+            write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
+        return;
+    }
+    uint32_t kmax, nfin;
+    dense_row_stats(P, row, &kmax, &nfin);
+    if (nfin == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        if (P.out_keep) write_keep(P, row, [&](auto) {});
+        return;
+    }
+    const float xmax = key_f32(kmax);
+    const bool topp = c.p < 1.0f;
+    const uint32_t nmem = topp ? *(const uint32_t*)(r0 + SMP_DMEM) : 0u;
+    if (topp && (nmem == 0u || nmem > dense_member_cap(S))) {   // uniform
+        finish_full_row<TL>(P, row, c, sh);
+        return;
+    }
+    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    for (int i = (int)t; i < S; i += LLIMA_WG) cmass[i] = r0[(size_t)i * SMP_REGION + SMP_DKEPT];
+    uint32_t theta = 0;
+    if (topp) {
+        uint32_t key[EPT], mid[EPT];
+        uint64_t w[EPT];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            const uint32_t j = t + (uint32_t)e * LLIMA_WG;
+            const uint64_t v = j < nmem ? *dense_member(r0, j) : 0ull;
+            key[e] = (uint32_t)(v >> 32);
+            mid[e] = (uint32_t)v;
+        }
+        uint32_t mk = 0, nmk = 0;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            w[e] = key[e] ? weight(key_f32(key[e]), xmax) : 0ull;
+            mk = key[e] > mk ? key[e] : mk;
+            nmk = key[e] && ~key[e] > nmk ? ~key[e] : nmk;
+        }
+        sh.hmass[0][t] = 0;
+        sh.hmass[1][t] = 0;
+        mk = block_max_u32(mk, sh.bs);
+        const uint32_t mkmin = ~block_max_u32(nmk, sh.bs);
+        const uint64_t above = r0[SMP_DINFO + 1], Z = r0[SMP_DINFO + 2];
+        const uint64_t p32 = frac32(c.p);
+        theta = fin_topp_desc<EPT>(key, w, p32, mkmin, mk, sh, above, (llima_u128)p32 * Z, true);
+        const int nw = (P.V + 31) >> 5;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            if (key[e] && key[e] >= theta && w[e] >= mthr) {
+                atomicAdd((unsigned long long*)&cmass[mid[e] / (uint32_t)G::CHUNK], (unsigned long long)w[e]);
+                if (P.out_keep)
+                    atomicOr(P.out_keep + (size_t)row * nw + (mid[e] >> 5), 1u << (mid[e] & 31u));
+            }
+        }
+    }
+    __syncthreads();
+    // the chunk holding the draw target
+    const uint64_t m = (int)t < S ? cmass[t] : 0ull;
+    uint64_t Zf;
+    const uint64_t below = block_excl_scan_u64(m, &Zf, sh.bs);
+    if (Zf == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        return;
+    }
+    const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
+    if (m > 0 && below <= target && target < below + m) {
+        dsel = t;
+        drel = target - below;
+    }
+    __syncthreads();
+    const int cs = (int)dsel;
+    const uint64_t rel = drel;
+    // that chunk in id order: thread t holds ids c0 + E t .. c0 + E t + E - 1
+    const int c0 = cs * G::CHUNK;
+    const int c1 = c0 + G::CHUNK < P.V ? c0 + G::CHUNK : P.V;
+    if (c.pen) count_history(P, row, c.hlen, c0, c1, sh.u.table, G::CHUNK / 2);
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    const int i0 = c0 + (int)t * G::E;
+    float xs[G::E];
+#pragma unroll
+    for (int g = 0; g < G::E; g += SMP_FE) {
+        float sub[SMP_FE];
+        load_fe<TL>(rowp, i0 + g, c1, P.vec_ok != 0, sub);
+#pragma unroll
+        for (int e = 0; e < SMP_FE; ++e) xs[g + e] = sub[e];
+    }
+    uint64_t wk[G::E];
+    uint64_t s = 0;
+#pragma unroll
+    for (int e = 0; e < G::E; ++e) {
+        const int i = i0 + e;
+        const float l = i < c1 ? xs[e] : -__builtin_inff();
+        const uint32_t cnt = c.pen && i < c1 ? table_count(sh.u.table, (uint32_t)(i - c0)) : 0u;
+        const float xv = dense_x(l, cnt, c);
+        const uint32_t k = f32_key(xv);
+        const uint64_t w = weight(xv, xmax);
+        const bool kept = k > LLIMA_KEY_NEG_INF && k >= theta && w >= mthr;
+        wk[e] = kept ? w : 0ull;
+        s += wk[e];
+    }
+    uint64_t tot;
+    const uint64_t bl = block_excl_scan_u64(s, &tot, sh.bs);
+    if (s > 0 && bl <= rel && rel < bl + s) {
+        uint64_t acc = bl;
+        int32_t tok = -1;
+        uint64_t wtok = 0;
+#pragma unroll
+        for (int e = 0; e < G::E; ++e) {
+            const bool hit = tok < 0 && wk[e] > 0 && rel < acc + wk[e];
+            tok = hit ? i0 + e : tok;
+            wtok = hit ? wk[e] : wtok;
+            acc += wk[e];
+        }
+        write_result(P, row, tok, (float)((double)wtok / (double)Zf));
+    }
+}
+
 // ================================================================== host side
 static int chunk_values(int dtype) { return dtype == LLIMA_F32 ? 4096 : 8192; }
 
@@ -2009,6 +2573,18 @@ static void launch_sweep(const SampleParams& P, hipStream_t st) {
         if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, false, SC>), g, b, cnt_bytes, st, P);
         else hipLaunchKernelGGL((sample_sweep<TL, false, false, SC>), g, b, cnt_bytes, st, P);
     }
+}
+
+// The dense path's launches: three reads of the rows by B x S workgroups
+// (dense_hist only when some row has top-p), then one workgroup per row.
+template <typename TL>
+static void launch_dense(const SampleParams& P, bool topp, hipStream_t st) {
+    const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
+    const size_t tb = P.H_max > 0 ? (size_t)DenseGeom<TL>::CHUNK / 2 * sizeof(uint32_t) : 0;
+    hipLaunchKernelGGL(dense_stats<TL>, g, b, tb, st, P);
+    if (topp) hipLaunchKernelGGL(dense_hist<TL>, g, b, tb, st, P);
+    hipLaunchKernelGGL(dense_keep<TL>, g, b, tb, st, P);
+    hipLaunchKernelGGL(dense_final<TL>, dim3((uint32_t)P.B), b, 0, st, P);
 }
 
 }  // namespace llima
@@ -2089,7 +2665,16 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
              cfg->top_k > 0 && cfg->top_k < V && cfg->repetition_penalty >= 1.0f &&
              cfg->presence_penalty >= 0.0f && cfg->frequency_penalty >= 0.0f;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == LLIMA_F32) {
+    // Rows without top-k (and without a mask) take the dense path: their sweep
+    // bound would admit nearly every value of ordinary logits.
+    const bool dense = !bitmask && !cfg->greedy && !cfg->top_k_rows &&
+                       !(cfg->top_k > 0 && cfg->top_k < V) &&
+                       (cfg->temperature_rows || cfg->temperature > 0.0f) && P.S <= SMP_MAX_S;
+    if (dense) {
+        const bool topp = cfg->top_p_rows || cfg->top_p < 1.0f;
+        if (dtype == LLIMA_F32) launch_dense<float>(P, topp, st);
+        else launch_dense<uint16_t>(P, topp, st);
+    } else if (dtype == LLIMA_F32) {
         launch_sweep<float>(P, st);
         hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {

@@ -473,15 +473,6 @@ __device__ __forceinline__ void load2(const float* rowp, int j0, int V, float (&
     x[1] = j0 + 1 < V ? a.y : -__builtin_inff();
 }
 
-// Sums that other workgroups read inside the same launch: write-through
-// stores and loads at agent scope (see the header).
-__device__ __forceinline__ void store_agent(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_agent(uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // The draw of sequence b by its last workgroup, in two request rounds: the
 // wave totals (thread t owns a contiguous range of wave slices) give the wave
 // slice of VR_SLICE ids holding the target; that slice's ids, two per thread,

@@ -133,7 +133,7 @@ def test_sample_workloads(gpu, oracle, name, kw):
                  mask=w["bitmask"])
 
 
-@pytest.mark.parametrize("name", ["batched_penalties", "constrained", "large_vocab_bf16"])
+@pytest.mark.parametrize("name", ["batched_penalties", "constrained", "large_vocab_bf16", "top_p_only"])
 def test_sample_workloads_full_size(gpu, oracle, name):
     _say("sample full", name)
     w = wl.WORKLOADS[name]()
@@ -283,6 +283,98 @@ def test_sample_gather_path_top_p(gpu, oracle, kind):
         for dt in ("f32", "bf16"):
             xx = wl.f32_to_bf16_bits(x) if dt == "bf16" else x
             _sample_both(gpu, oracle, xx, u, cfgd, history=hist, hist_len=hl, mask=mask)
+
+
+DENSE_CONFIGS = [
+    dict(temperature=1.0, top_p=0.9),
+    dict(temperature=0.7, top_p=0.5, min_p=0.05),
+    dict(temperature=1.5),                                  # plain sampling: every finite value kept
+    dict(temperature=1.0, min_p=0.1),
+    dict(temperature=1.0, top_p=0.95, repetition_penalty=1.2, presence_penalty=-0.4,
+         frequency_penalty=0.1),
+    dict(temperature=1.0, top_p=0.0),
+    dict(temperature=3.0, top_p=0.999),
+]
+DENSE_KINDS = ["normal4", "normal1", "flat", "integers", "fine_steps", "specials", "small"]
+
+
+def _dense_rows(kind, rng):
+    if kind == "normal4":
+        return rng.normal(0, 4, (4, 128256)).astype(np.float32)
+    if kind == "normal1":                                    # V % 4 != 0: one value per load
+        return rng.normal(0, 1, (4, 70001)).astype(np.float32)
+    if kind == "flat":                                       # > 4096 values in the boundary bin
+        return rng.normal(0, 0.05, (3, 50000)).astype(np.float32)
+    if kind == "integers":
+        return np.round(rng.normal(0, 3, (4, 128256))).astype(np.float32)
+    if kind == "fine_steps":
+        return (np.round(rng.normal(0, 0.4, (4, 128256)) * 64) / 64).astype(np.float32)
+    if kind == "specials":
+        x = rng.normal(0, 2, (6, 4099)).astype(np.float32)
+        x[0, 10:300] = np.nan
+        x[1, 4000:4010] = np.inf                             # infinite maximum
+        x[2, :] = -np.inf                                    # no finite value: -1
+        x[3, :] = -np.inf
+        x[3, 4098] = 0.5                                     # one finite value, in the last chunk
+        x[4, ::2] = -np.inf
+        x[5, 7] = np.float32(3e38)
+        x[5, 8] = np.float32(-3e38)
+        return x
+    return rng.normal(0, 2, (3, 37)).astype(np.float32)      # small: one partial chunk
+
+
+@pytest.mark.parametrize("kind", DENSE_KINDS)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_dense_path(gpu, oracle, kind, dtype):
+    """Rows without top-k or mask take the dense path: per-chunk statistics,
+    chunk histograms of value bins (1/16 nat) merged by the row's last
+    workgroup, the boundary bin's members ranked, the draw's chunk scanned.
+    Flat rows put more than 4096 values into the boundary bin (the full-row
+    path finishes them); integer rows and rows in 1/64 steps put many tied or
+    close values there; an infinite maximum, NaN runs, rows without finite
+    values and a single finite value in the last chunk are the edge cases."""
+    _say("sample dense", kind, dtype)
+    rng = np.random.default_rng(DENSE_KINDS.index(kind) * 2 + (dtype == "bf16") + 300)
+    x = _dense_rows(kind, rng)
+    B, V = x.shape
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    hist = rng.integers(-3, V + 3, size=(B, 500)).astype(np.int32)
+    hist[:, :100] = rng.integers(0, min(V, 50), size=(B, 100))  # hot ids near the top
+    hl = rng.integers(0, 501, size=B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    u[0] = 0.0
+    u[-1] = np.float32(1.0) - np.float32(2**-24)
+    for cfgd in DENSE_CONFIGS:
+        _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl)
+
+
+def test_sample_dense_rows_config_and_strides(gpu, oracle):
+    """The dense path with per-row temperatures and top-p (a zero temperature
+    makes a greedy row) and on rows that start unaligned (a row stride of
+    V + 3 and an offset of 3 values: one value per load)."""
+    import llima_amd
+    import torch
+    from oracle.oracle import SamplerConfig as OC
+    _say("sample dense per-row / strided")
+    rng = np.random.default_rng(77)
+    B, V = 8, 20000
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    rows = dict(temperature=[1.0, 0.0, 0.7, 2.0, 1.0, 0.0, 0.3, 1.1],
+                top_p=[0.9, 0.9, 1.0, 0.5, 0.99, 1.0, 0.0, 0.8],
+                min_p=[0.0, 0.0, 0.05, 0.0, 0.2, 0.0, 0.0, 0.01])
+    _sample_both(gpu, oracle, x, u, None, cfg_rows=rows)
+    xs = np.zeros((B, V + 3), np.float32)
+    xs[:, 3:] = x
+    xt = _t(xs, gpu)[:, 3:]
+    for cfgd in [dict(temperature=1.0, top_p=0.9), dict(temperature=0.8, min_p=0.05)]:
+        ids, probs, keep = llima_amd.sample(xt, _t(u, gpu), llima_amd.SamplerConfig(**cfgd),
+                                            return_keep=True)
+        eids, eprobs, ekeep = oracle.sample(x, u, OC(**cfgd), want_keep=True)
+        assert (_np(ids) == eids).all()
+        assert (_np(probs).view(np.uint32) == eprobs.view(np.uint32)).all()
+        assert (_np(keep).view(np.uint32) == ekeep).all()
 
 
 def test_sample_masks_and_edges(gpu, oracle):
