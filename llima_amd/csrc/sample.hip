@@ -2007,13 +2007,15 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 //   dense_hist   rows with top-p: the chunk's exact weights counted into
 //                SMP_DBINS value bins of 1/16 nat below the row maximum (bin
 //                floor(16 (xmax - x)), monotone in the key, the last open) as
-//                (mass << 14) + count; the row's last workgroup to finish
-//                merges the chunks' bins and finds the bin holding the top-p
-//                boundary: the last non-empty bin whose mass above, times
-//                2^32, is below p32 Z (the top non-empty bin when none is);
+//                (mass << 14) + count;
+//   dense_bound  one workgroup per row with top-p: the chunks' bins merged,
+//                and the bin holding the top-p boundary: the last non-empty
+//                bin whose mass above, times 2^32, is below p32 Z (the top
+//                non-empty bin when none is);
 //   dense_keep   the chunk's kept mass strictly above that bin (min-p
 //                applied), its words of the kept-set mask, and the bin's
-//                members (key, id) appended to the row's member list;
+//                members (key, id), staged in LDS and appended to the row's
+//                member list;
 //   dense_final  one workgroup per row: the members ranked by radix rounds
 //                over their keys, starting from the mass above the bin, give
 //                theta (the full-row path's boundary: the smallest key whose
@@ -2024,8 +2026,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 // Every weight, bin and test is the full-row path's arithmetic on the same
 // values, so the kept set, the token and its probability are the same.  A row
 // whose boundary bin holds more members than dense_final ranks (more than
-// 4096 values within 1/16 nat: a nearly flat row) is finished there by the
-// full-row path.
+// 4096 values within 1/16 nat, or more than 512 in one chunk: a nearly flat
+// row) is finished there by the full-row path.
 //
 // Region use per row (the row's S regions of SMP_REGION slots):
 //   region c, slots [0, SMP_DBINS)  dense_hist's bins of chunk c, then the
@@ -2033,18 +2035,18 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 //                                   j / SMP_DBINS, slot j % SMP_DBINS)
 //   region c, SMP_DSTAT / SMP_DBEST  dense_stats's results for chunk c
 //   region c, SMP_DKEPT             dense_keep's kept mass of chunk c
-//   region 0, SMP_DINFO..+2         boundary bin, mass above it, Z
-//   region 0, SMP_DARR / SMP_DMEM   counters (128-byte lines of their own),
-//                                   zeroed by dense_stats
+//   region 0, SMP_DINFO..+2         dense_bound's boundary bin, mass above it, Z
+//   region 0, SMP_DMEM              members appended (a 128-byte line of its
+//                                   own), zeroed by dense_stats
 #define SMP_DBINS 448                              // value bins, 1/16 nat (28 nats; the last open)
 #define SMP_DBIN_SCALE 16.0f
 #define SMP_DSTAT 448                              // chunk max key << 32 | finite count
 #define SMP_DBEST 449                              // greedy: key << 32 | ~id of the chunk maximum
 #define SMP_DKEPT 450                              // kept mass strictly above the boundary bin
 #define SMP_DINFO 456                              // region 0: boundary bin, mass above it, Z
-#define SMP_DARR 480                               // region 0: dense_hist arrivals
 #define SMP_DMEM 496                               // region 0: boundary members appended
 #define SMP_DMCAP 4096                             // members dense_final ranks (16 per thread)
+#define SMP_DMWG 512                               // members a dense_keep workgroup stages
 static_assert(SMP_DBINS <= SMP_DSTAT && SMP_DMEM + 16 <= SMP_REGION, "dense region layout");
 static_assert(SMP_DMCAP == 16 * LLIMA_WG, "dense_final holds 16 members per thread");
 
@@ -2057,10 +2059,35 @@ struct DenseGeom {
     static constexpr int WS = CHUNK / LLIMA_WAVES;     // ids per wave
 };
 
-// The value bin of x below the row maximum xmax (x <= xmax, x not NaN).
-__device__ __forceinline__ uint32_t dense_bin(float x, float xmax) {
-    const float d = __builtin_fminf((xmax - x) * SMP_DBIN_SCALE, (float)(SMP_DBINS - 1));
-    return x == xmax ? 0u : (uint32_t)d;
+// 16 (xmax - x) clamped to the last bin, 0 at x == xmax (also when both are
+// +inf): the value bin of x (x <= xmax, not NaN) is its integral part, so
+// bin < b exactly when it is below b, and bin == b when it lies in [b, b + 1).
+__device__ __forceinline__ float dense_d16(float x, float xmax) {
+    return x == xmax ? 0.0f : __builtin_fminf((xmax - x) * SMP_DBIN_SCALE, (float)(SMP_DBINS - 1));
+}
+
+// weight(x, xmax) as an integral float: weight_f, and 2^36 at x == xmax also
+// when the maximum is +inf (every other value then weighs 0, as weight_f's
+// clamp at -26 gives).
+__device__ __forceinline__ float dense_wf(float x, float xmax) {
+    return x == xmax ? LLIMA_TWO36 : weight_f(x, xmax);
+}
+
+// An integral float below 2^52 as uint64 without branches: the part from 2^32
+// up and the rest are each exact (a float's significand has 24 bits).
+__device__ __forceinline__ uint64_t wf_u64(float wf) {
+    const float hi = __builtin_truncf(wf * 2.3283064365386963e-10f);
+    const uint32_t lo = (uint32_t)__builtin_fmaf(hi, -4294967296.0f, wf);
+    return ((uint64_t)(uint32_t)hi << 32) | lo;
+}
+
+// The min-p threshold frac32(m) 2^4 rounded up to a float: an integral float
+// weight W has W >= threshold exactly when W >= this.
+__device__ __forceinline__ float dense_mthr(const RowCfg& c) {
+    const uint64_t m = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    float f = (float)m;
+    if (f32_integral_to_u64(f) < m) f = __uint_as_float(__float_as_uint(f) + 1u);
+    return f;
 }
 
 __device__ __forceinline__ uint64_t* dense_member(uint64_t* r0, uint32_t j) {
@@ -2077,7 +2104,7 @@ __device__ __forceinline__ uint32_t dense_member_cap(int S) {
 __device__ __forceinline__ float dense_x(float l, uint32_t cnt, const RowCfg& c) {
     if (l != l) l = -__builtin_inff();
     if (cnt) l = penalize(l, cnt, c);
-    return c.greedy ? l : l / c.T;
+    return c.greedy || c.T == 1.0f ? l : l / c.T;      // l / 1 is l, exactly
 }
 
 // The loads of the row's first SMP_HBATCH * LLIMA_WG history ids (clamped to
@@ -2158,7 +2185,8 @@ __device__ __forceinline__ void dense_issue(const SampleParams& P, int row, int 
     }
 }
 
-// The chunk's values after the row's transform; ids past the row are -inf.
+// The chunk's values after NaN -> -inf and the penalties (not yet divided by
+// T); ids past the row are -inf.
 template <typename TL>
 __device__ __forceinline__ void dense_unpack(const SampleParams& P, const RowCfg& c, int c0,
                                              const llima_u32x4 (&raw)[DenseGeom<TL>::NL],
@@ -2173,10 +2201,20 @@ __device__ __forceinline__ void dense_unpack(const SampleParams& P, const RowCfg
             uint32_t bits;
             if constexpr (sizeof(TL) == 4) bits = w4[e];
             else bits = (e & 1) ? (w4[e >> 1] & 0xFFFF0000u) : (w4[e >> 1] << 16);
-            const float l = i < P.V ? __uint_as_float(bits) : -__builtin_inff();
+            float l = i < P.V ? __uint_as_float(bits) : -__builtin_inff();
+            if (l != l) l = -__builtin_inff();
             const uint32_t cnt = c.pen ? table_count(table, (uint32_t)(i - c0)) : 0u;
-            x[j * G::EPL + e] = dense_x(l, cnt, c);
+            x[j * G::EPL + e] = cnt ? penalize(l, cnt, c) : l;
         }
+    }
+}
+
+// x / T, skipped (a uniform branch) on greedy rows and at T == 1, where it is x.
+template <int E>
+__device__ __forceinline__ void dense_div(float (&x)[E], const RowCfg& c) {
+    if (!c.greedy && c.T != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < E; ++i) x[i] = x[i] / c.T;
     }
 }
 
@@ -2227,41 +2265,63 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_stats(SampleParams P) {
         best = block_max_u64(best, bs);
         if (threadIdx.x == 0) reg[SMP_DBEST] = best;
     } else {
-        uint32_t km = 0, nf = 0;
+        // no division: l / T is monotone in l, so the largest quotient is the
+        // quotient of the largest l, and l / T rounds to -inf exactly when
+        // l <= -T (2^128 - 2^103) (exact in double), so both follow from l
+        const double thr = -(double)c.T * 3.4028235677973366e38;
+        float lm = -__builtin_inff();
+        uint32_t nf = 0;
 #pragma unroll
         for (int i = 0; i < G::E; ++i) {
-            const uint32_t k = f32_key(x[i]);
-            const bool fin = k > LLIMA_KEY_NEG_INF;
-            nf += fin ? 1u : 0u;
-            km = fin && k > km ? k : km;
+            lm = __builtin_fmaxf(lm, x[i]);
+            nf += (double)x[i] > thr ? 1u : 0u;
         }
+        uint32_t km = f32_key(lm);
         km = block_max_u32(km, bs);
         nf = block_sum_u32(nf, bs);
-        if (threadIdx.x == 0) reg[SMP_DSTAT] = ((uint64_t)km << 32) | nf;
+        if (threadIdx.x == 0) {
+            const float xm = key_f32(km) / c.T;
+            reg[SMP_DSTAT] = ((uint64_t)(nf ? f32_key(xm) : 0u) << 32) | nf;
+        }
     }
-    if (chunk == 0 && threadIdx.x == 0) {
-        reg[SMP_DARR] = 0;
-        reg[SMP_DMEM] = 0;
-    }
+    if (chunk == 0 && threadIdx.x == 0) reg[SMP_DMEM] = 0;
 }
 
-// The top-p boundary bin of a row from its chunks' bins, by the row's last
-// dense_hist workgroup: thread t merges bins 2t and 2t + 1 over the chunks.
-__device__ __forceinline__ void dense_boundary(const SampleParams& P, int row, const RowCfg& c,
-                                               BlockScratch& bs) {
+// The top-p boundary bin of each row from its chunks' bins, one workgroup per
+// row: thread t merges bins 2t and 2t + 1 over the chunks (16-byte loads of up
+// to 32 chunks issued before any is used), then a block scan gives each bin's
+// mass above.
+__global__ __launch_bounds__(LLIMA_WG) void dense_bound(SampleParams P) {
+    __shared__ BlockScratch bs;
+    const int row = blockIdx.x;
+    const RowCfg c = load_cfg(P, row);
+    if (c.greedy || !(c.p < 1.0f)) return;              // uniform: no top-p on this row
+    uint32_t kmax, nfin;
+    dense_row_stats(P, row, &kmax, &nfin);
+    if (nfin == 0) return;
     const uint32_t t = threadIdx.x;
     uint64_t* r0 = region_of(P, (uint32_t)row, 0);
     uint32_t cn0 = 0, cn1 = 0;
     uint64_t m0 = 0, m1 = 0;
     if (t < SMP_DBINS / 2) {
-#pragma unroll 4
-        for (int i = 0; i < P.S; ++i) {
-            uint64_t* q = r0 + (size_t)i * SMP_REGION + 2u * t;
-            const uint64_t h0 = load_agent(q), h1 = load_agent(q + 1);
-            cn0 += (uint32_t)(h0 & 0x3FFFu);
-            m0 += h0 >> 14;
-            cn1 += (uint32_t)(h1 & 0x3FFFu);
-            m1 += h1 >> 14;
+        constexpr int NB = 32;
+        for (int b0 = 0; b0 < P.S; b0 += NB) {
+            llima_u32x4 q[NB];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int ci = b0 + i < P.S ? b0 + i : P.S - 1;
+                q[i] = *(const llima_u32x4*)(r0 + (size_t)ci * SMP_REGION + 2u * t);
+            }
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const bool in = b0 + i < P.S;
+                const uint64_t h0 = in ? ((uint64_t)q[i].y << 32) | q[i].x : 0ull;
+                const uint64_t h1 = in ? ((uint64_t)q[i].w << 32) | q[i].z : 0ull;
+                cn0 += (uint32_t)(h0 & 0x3FFFu);
+                m0 += h0 >> 14;
+                cn1 += (uint32_t)(h1 & 0x3FFFu);
+                m1 += h1 >> 14;
+            }
         }
     }
     uint64_t Z;
@@ -2285,8 +2345,6 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_hist(SampleParams P) {
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ uint64_t hist[SMP_DBINS + 64];           // + a spare bin per lane
-    __shared__ BlockScratch bs;
-    __shared__ uint32_t last;
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
@@ -2306,23 +2364,23 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_hist(SampleParams P) {
     __syncthreads();
     float x[G::E];
     dense_unpack<TL>(P, c, c0, raw, table, x);
+    dense_div(x, c);
     const float xmax = key_f32(kmax);
 #pragma unroll
     for (int i = 0; i < G::E; ++i) {
-        const bool fin = f32_key(x[i]) > LLIMA_KEY_NEG_INF;
-        const uint64_t w = weight(x[i], xmax);
-        const uint32_t b = fin ? dense_bin(x[i], xmax) : SMP_DBINS + lane;
-        atomicAdd((unsigned long long*)&hist[b], (unsigned long long)((w << 14) | 1ull));
+        const bool fin = x[i] > -__builtin_inff();
+        const float wf = dense_wf(x[i], xmax);
+        const uint32_t b = fin ? (uint32_t)dense_d16(x[i], xmax) : SMP_DBINS + lane;
+        // (W << 14) + 1: W 2^14 < 2^51 is an exact integral float
+        atomicAdd((unsigned long long*)&hist[b], (unsigned long long)(wf_u64(wf * 16384.0f) | 1ull));
     }
     __syncthreads();
     uint64_t* reg = region_of(P, row, chunk);
-    for (uint32_t i = t; i < SMP_DBINS; i += LLIMA_WG) store_agent(reg + i, hist[i]);
-    __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
-    __syncthreads();
-    if (t == 0)
-        last = arrive_agent((uint32_t*)(region_of(P, row, 0) + SMP_DARR), 1u) == (uint32_t)P.S - 1u;
-    __syncthreads();
-    if (last) dense_boundary(P, (int)row, c, bs);
+    if (t < SMP_DBINS / 2) {
+        const uint64_t h0 = hist[2u * t], h1 = hist[2u * t + 1u];
+        ((llima_u32x4*)reg)[t] = llima_u32x4{(uint32_t)h0, (uint32_t)(h0 >> 32), (uint32_t)h1,
+                                             (uint32_t)(h1 >> 32)};
+    }
 }
 
 template <typename TL>
@@ -2330,7 +2388,8 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_keep(SampleParams P) {
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ BlockScratch bs;
-    __shared__ uint32_t mbase;
+    __shared__ uint64_t mbuf[SMP_DMWG];                 // the chunk's boundary members
+    __shared__ uint32_t mcount, mbase;
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
@@ -2341,73 +2400,84 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_keep(SampleParams P) {
     dense_issue<TL>(P, (int)row, c0, raw);
     const RowCfg c = load_cfg(P, (int)row);
     if (c.greedy) return;                               // dense_final writes greedy rows
+    const bool topp = c.p < 1.0f;
+    uint64_t* r0 = region_of(P, row, 0);
+    // the boundary bin requested with the statistics (both written by earlier launches)
+    const uint64_t binfo = r0[SMP_DINFO];
     uint32_t kmax, nfin;
     dense_row_stats(P, (int)row, &kmax, &nfin);
     if (nfin == 0) return;
-    const bool topp = c.p < 1.0f;
-    uint64_t* r0 = region_of(P, row, 0);
-    const uint32_t bstar = topp ? (uint32_t)r0[SMP_DINFO] : (uint32_t)SMP_DBINS;
+    const uint32_t bstar = topp ? (uint32_t)binfo : (uint32_t)SMP_DBINS;
+    if (threadIdx.x == 0) mcount = 0;
     if (c.pen) dense_count(P, (int)row, c, hid, c0, G::CHUNK, table);
+    else __syncthreads();
     float x[G::E];
     dense_unpack<TL>(P, c, c0, raw, table, x);
+    dense_div(x, c);
     const float xmax = key_f32(kmax);
-    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    const float mthr = dense_mthr(c);
+    const float blo = (float)bstar, bhi = (float)bstar + 1.0f;   // bin b*: d16 in [blo, bhi)
     const uint32_t lane = lane_id();
-    uint64_t km = 0;
-    uint32_t nm = 0;
-    uint32_t kb[G::NL];
+    const int nw = (P.V + 31) >> 5;
+    uint32_t* kw = P.out_keep + (size_t)row * nw;
+    double kmd = 0.0;                                   // at most 32 weights below 2^37: exact
+    uint32_t mb = 0;                                    // this thread's boundary members
 #pragma unroll
     for (int j = 0; j < G::NL; ++j) {
-        kb[j] = 0;
+        uint32_t kb = 0;
 #pragma unroll
         for (int e = 0; e < G::EPL; ++e) {
             const float xv = x[j * G::EPL + e];
-            const bool fin = f32_key(xv) > LLIMA_KEY_NEG_INF;
-            const uint64_t w = weight(xv, xmax);
-            const uint32_t b = dense_bin(xv, xmax);
-            const bool kept = fin && b < bstar && w >= mthr;
-            km += kept ? w : 0ull;
-            kb[j] |= kept ? 1u << e : 0u;
-            nm += fin && b == bstar ? 1u : 0u;
+            const bool fin = xv > -__builtin_inff();
+            const float wf = dense_wf(xv, xmax);
+            const float d16 = dense_d16(xv, xmax);
+            const bool kept = fin && d16 < blo && wf >= mthr;
+            kmd += kept ? (double)wf : 0.0;
+            kb |= kept ? 1u << e : 0u;
+            mb |= fin && d16 >= blo && d16 < bhi ? 1u << (j * G::EPL + e) : 0u;
         }
-    }
-    if (P.out_keep) {
-        // lanes sharing a 32-id word: 32 / EPL of them (the chunk starts on a word)
-        const int nw = (P.V + 31) >> 5;
-        uint32_t* kw = P.out_keep + (size_t)row * nw;
-        constexpr int LPW = 32 / G::EPL;
-#pragma unroll
-        for (int j = 0; j < G::NL; ++j) {
-            uint32_t word = kb[j] << ((lane * G::EPL) & 31u);
+        if (P.out_keep) {
+            // lanes sharing a 32-id word: 32 / EPL of them (the chunk starts on a word)
+            constexpr int LPW = 32 / G::EPL;
+            uint32_t word = kb << ((lane * G::EPL) & 31u);
 #pragma unroll
             for (int s = 1; s < LPW; s <<= 1) word |= (uint32_t)__shfl_xor((int)word, s);
             const int i0 = dense_id<TL>(c0, j, 0);
             if ((lane & (LPW - 1)) == 0 && i0 < P.V) kw[i0 >> 5] = word;
         }
     }
-    km = block_sum_u64(km, bs);
-    if (threadIdx.x == 0) region_of(P, row, chunk)[SMP_DKEPT] = km;
-    if (topp) {
-        uint32_t tot;
-        const uint32_t off = block_excl_scan_u32(nm, &tot, bs);
-        if (tot) {                                       // uniform
-            if (threadIdx.x == 0) mbase = arrive_agent((uint32_t*)(r0 + SMP_DMEM), tot);
-            __syncthreads();
-            const uint32_t cap = dense_member_cap(P.S);
-            uint32_t o = mbase + off;
+    // boundary members, staged in LDS (one LDS atomic per wave that has any)
+    if (ballot(mb != 0u)) {                              // uniform
+        const uint32_t cnt = (uint32_t)__popc(mb);
+        const uint32_t inc = wave_incl_scan_u32(cnt);
+        uint32_t base = 0;
+        if (lane == 63) base = atomicAdd(&mcount, inc);
+        base = readlane(base, 63) + inc - cnt;
 #pragma unroll
-            for (int j = 0; j < G::NL; ++j)
+        for (int j = 0; j < G::NL; ++j)
 #pragma unroll
-                for (int e = 0; e < G::EPL; ++e) {
-                    const float xv = x[j * G::EPL + e];
-                    const uint32_t k = f32_key(xv);
-                    if (k > LLIMA_KEY_NEG_INF && dense_bin(xv, xmax) == bstar) {
-                        if (o < cap)
-                            *dense_member(r0, o) = ((uint64_t)k << 32) | (uint32_t)dense_id<TL>(c0, j, e);
-                        ++o;
-                    }
+            for (int e = 0; e < G::EPL; ++e)
+                if ((mb >> (j * G::EPL + e)) & 1u) {
+                    if (base < SMP_DMWG)
+                        mbuf[base] = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) |
+                                     (uint32_t)dense_id<TL>(c0, j, e);
+                    ++base;
                 }
-        }
+    }
+    const uint64_t km = block_sum_u64((uint64_t)kmd, bs);   // its barriers also settle mcount
+    if (threadIdx.x == 0) region_of(P, row, chunk)[SMP_DKEPT] = km;
+    const uint32_t n = mcount;
+    if (n) {                                             // uniform
+        // a workgroup with more members than it stages makes the row's count
+        // exceed what dense_final ranks (that row then takes the full-row path)
+        const uint32_t cap = dense_member_cap(P.S);
+        if (threadIdx.x == 0)
+            mbase = arrive_agent((uint32_t*)(r0 + SMP_DMEM), n <= SMP_DMWG ? n : cap + 1u);
+        __syncthreads();
+        const uint32_t o = mbase;
+        if (n <= SMP_DMWG)
+            for (uint32_t i = threadIdx.x; i < n; i += LLIMA_WG)
+                if (o + i < cap) *dense_member(r0, o + i) = mbuf[i];
     }
 }
 
@@ -2456,7 +2526,7 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         finish_full_row<TL>(P, row, c, sh);
         return;
     }
-    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    const float mthr = dense_mthr(c);
     for (int i = (int)t; i < S; i += LLIMA_WG) cmass[i] = r0[(size_t)i * SMP_REGION + SMP_DKEPT];
     uint32_t theta = 0;
     if (topp) {
@@ -2472,7 +2542,7 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         uint32_t mk = 0, nmk = 0;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-            w[e] = key[e] ? weight(key_f32(key[e]), xmax) : 0ull;
+            w[e] = key[e] ? wf_u64(dense_wf(key_f32(key[e]), xmax)) : 0ull;
             mk = key[e] > mk ? key[e] : mk;
             nmk = key[e] && ~key[e] > nmk ? ~key[e] : nmk;
         }
@@ -2486,7 +2556,7 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         const int nw = (P.V + 31) >> 5;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-            if (key[e] && key[e] >= theta && w[e] >= mthr) {
+            if (key[e] && key[e] >= theta && (float)w[e] >= mthr) {
                 atomicAdd((unsigned long long*)&cmass[mid[e] / (uint32_t)G::CHUNK], (unsigned long long)w[e]);
                 if (P.out_keep)
                     atomicOr(P.out_keep + (size_t)row * nw + (mid[e] >> 5), 1u << (mid[e] & 31u));
@@ -2533,9 +2603,9 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         const uint32_t cnt = c.pen && i < c1 ? table_count(sh.u.table, (uint32_t)(i - c0)) : 0u;
         const float xv = dense_x(l, cnt, c);
         const uint32_t k = f32_key(xv);
-        const uint64_t w = weight(xv, xmax);
-        const bool kept = k > LLIMA_KEY_NEG_INF && k >= theta && w >= mthr;
-        wk[e] = kept ? w : 0ull;
+        const float wf = dense_wf(xv, xmax);
+        const bool kept = k > LLIMA_KEY_NEG_INF && k >= theta && wf >= mthr;
+        wk[e] = kept ? wf_u64(wf) : 0ull;
         s += wk[e];
     }
     uint64_t tot;
@@ -2576,13 +2646,17 @@ static void launch_sweep(const SampleParams& P, hipStream_t st) {
 }
 
 // The dense path's launches: three reads of the rows by B x S workgroups
-// (dense_hist only when some row has top-p), then one workgroup per row.
+// (dense_hist and dense_bound only when some row has top-p), then one
+// workgroup per row.
 template <typename TL>
 static void launch_dense(const SampleParams& P, bool topp, hipStream_t st) {
     const dim3 g((uint32_t)P.B * (uint32_t)P.S), b(LLIMA_WG);
     const size_t tb = P.H_max > 0 ? (size_t)DenseGeom<TL>::CHUNK / 2 * sizeof(uint32_t) : 0;
     hipLaunchKernelGGL(dense_stats<TL>, g, b, tb, st, P);
-    if (topp) hipLaunchKernelGGL(dense_hist<TL>, g, b, tb, st, P);
+    if (topp) {
+        hipLaunchKernelGGL(dense_hist<TL>, g, b, tb, st, P);
+        hipLaunchKernelGGL(dense_bound, dim3((uint32_t)P.B), b, 0, st, P);
+    }
     hipLaunchKernelGGL(dense_keep<TL>, g, b, tb, st, P);
     hipLaunchKernelGGL(dense_final<TL>, dim3((uint32_t)P.B), b, 0, st, P);
 }
