@@ -95,8 +95,8 @@ __device__ __forceinline__ uint64_t weight(float x, float xmax) {
 //     n >= -38 stays normal, so ldexp(p 2^36, n) = ldexp(ldexp(p, n), 36);
 //   * x == xmax needs no select: d = 0 gives n = 0, r = 0 and p = 2^36 exactly.
 #define LLIMA_TWO36 68719476736.0f
-__device__ __forceinline__ float weight_f(float x, float xmax) {
-    const float d = __builtin_fmaxf(x - xmax, -26.0f);   // fmaxf(NaN, -26) = -26
+__device__ __forceinline__ float weight_fd(float d0) {   // d0 = x - xmax
+    const float d = __builtin_fmaxf(d0, -26.0f);         // fmaxf(NaN, -26) = -26
     const float kLog2e = 1.44269502162933349609375f;
     const float kLn2Hi = 0.693145751953125f;
     const float kLn2Lo = 1.428606765330187045e-06f;
@@ -113,6 +113,7 @@ __device__ __forceinline__ float weight_f(float x, float xmax) {
     p = __builtin_fmaf(p, r, LLIMA_TWO36);
     return __builtin_rintf(__builtin_ldexpf(p, (int)n));
 }
+__device__ __forceinline__ float weight_f(float x, float xmax) { return weight_fd(x - xmax); }
 
 // rint(v * 2^32) clamped to [0, 2^32].
 __device__ __forceinline__ uint64_t frac32(float v) {

@@ -2070,7 +2070,7 @@ __device__ __forceinline__ float dense_d16(float x, float xmax) {
 // when the maximum is +inf (every other value then weighs 0, as weight_f's
 // clamp at -26 gives).
 __device__ __forceinline__ float dense_wf(float x, float xmax) {
-    return x == xmax ? LLIMA_TWO36 : weight_f(x, xmax);
+    return weight_fd(x == xmax ? 0.0f : x - xmax);      // a select, not a branch per value
 }
 
 // An integral float below 2^52 as uint64 without branches: the part from 2^32
@@ -2512,6 +2512,14 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
             write_keep(P, row, [&](auto set) { if (t == 0 && ok) set(tok); });
         return;
     }
+    // requested together, before the statistics are reduced: the member
+    // count, the boundary's mass above and Z, the chunks' kept masses and the
+    // first LLIMA_WG member slots (always inside region 0's member slots)
+    const bool topp = c.p < 1.0f;
+    const uint32_t nmem = topp ? *(const uint32_t*)(r0 + SMP_DMEM) : 0u;
+    const uint64_t above = r0[SMP_DINFO + 1], Z = r0[SMP_DINFO + 2];
+    const uint64_t v0 = topp ? *dense_member(r0, t) : 0ull;
+    const uint64_t cm = (int)t < S ? r0[(size_t)t * SMP_REGION + SMP_DKEPT] : 0ull;
     uint32_t kmax, nfin;
     dense_row_stats(P, row, &kmax, &nfin);
     if (nfin == 0) {
@@ -2520,16 +2528,39 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         return;
     }
     const float xmax = key_f32(kmax);
-    const bool topp = c.p < 1.0f;
-    const uint32_t nmem = topp ? *(const uint32_t*)(r0 + SMP_DMEM) : 0u;
     if (topp && (nmem == 0u || nmem > dense_member_cap(S))) {   // uniform
         finish_full_row<TL>(P, row, c, sh);
         return;
     }
     const float mthr = dense_mthr(c);
-    for (int i = (int)t; i < S; i += LLIMA_WG) cmass[i] = r0[(size_t)i * SMP_REGION + SMP_DKEPT];
+    if ((int)t < S) cmass[t] = cm;
     uint32_t theta = 0;
-    if (topp) {
+    const int nw = (P.V + 31) >> 5;
+    if (topp && nmem <= 64u) {
+        // at most 64 members: ranked pairwise in every wave (lane l holds
+        // member l); theta is the smallest key whose mass strictly above,
+        // counted from the bin's, times 2^32, is below p32 Z (the largest key
+        // when none is: p32 Z < 2^32)
+        const uint32_t mk = (uint32_t)(v0 >> 32), mi = (uint32_t)v0;
+        const uint64_t mw = t < nmem ? wf_u64(dense_wf(key_f32(mk), xmax)) : 0ull;
+        if (t < nmem) sh.sv[t] = llima_u32x4{mk, mi, (uint32_t)mw, (uint32_t)(mw >> 32)};
+        __syncthreads();
+        const uint32_t lane = lane_id();
+        const llima_u32x4 me = lane < nmem ? sh.sv[lane] : llima_u32x4{0u, 0u, 0u, 0u};
+        uint64_t ab = above;
+        for (uint32_t i = 0; i < nmem; ++i) {
+            const llima_u32x4 o = sh.sv[i];
+            ab += o.x > me.x ? (((uint64_t)o.w << 32) | o.z) : 0ull;
+        }
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+        const uint64_t lim = (uint64_t)((PZ + 0xFFFFFFFFull) >> 32);   // a 2^32 < PZ  <=>  a < lim
+        const bool q = lane < nmem && ab < lim;
+        theta = ballot(q) ? ~wave_max_u32(q ? ~me.x : 0u) : wave_max_u32(me.x);
+        if (t < nmem && mk >= theta && (float)mw >= mthr) {
+            atomicAdd((unsigned long long*)&cmass[mi / (uint32_t)G::CHUNK], (unsigned long long)mw);
+            if (P.out_keep) atomicOr(P.out_keep + (size_t)row * nw + (mi >> 5), 1u << (mi & 31u));
+        }
+    } else if (topp) {
         uint32_t key[EPT], mid[EPT];
         uint64_t w[EPT];
 #pragma unroll
@@ -2550,10 +2581,8 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_final(SampleParams P) {
         sh.hmass[1][t] = 0;
         mk = block_max_u32(mk, sh.bs);
         const uint32_t mkmin = ~block_max_u32(nmk, sh.bs);
-        const uint64_t above = r0[SMP_DINFO + 1], Z = r0[SMP_DINFO + 2];
         const uint64_t p32 = frac32(c.p);
         theta = fin_topp_desc<EPT>(key, w, p32, mkmin, mk, sh, above, (llima_u128)p32 * Z, true);
-        const int nw = (P.V + 31) >> 5;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
             if (key[e] && key[e] >= theta && (float)w[e] >= mthr) {
