@@ -2235,7 +2235,7 @@ __device__ __forceinline__ void dense_row_stats(const SampleParams& P, int row, 
 }
 
 template <typename TL>
-__global__ __launch_bounds__(LLIMA_WG) void dense_stats(SampleParams P) {
+__global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))) void dense_stats(SampleParams P) {
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];   // history counts (rows with penalties)
     __shared__ BlockScratch bs;
@@ -2341,7 +2341,7 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_bound(SampleParams P) {
 }
 
 template <typename TL>
-__global__ __launch_bounds__(LLIMA_WG) void dense_hist(SampleParams P) {
+__global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))) void dense_hist(SampleParams P) {
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ uint64_t hist[SMP_DBINS + 64];           // + a spare bin per lane
@@ -2384,7 +2384,7 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_hist(SampleParams P) {
 }
 
 template <typename TL>
-__global__ __launch_bounds__(LLIMA_WG) void dense_keep(SampleParams P) {
+__global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof(TL) == 4 ? 8 : 1))) void dense_keep(SampleParams P) {
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ BlockScratch bs;
@@ -2429,10 +2429,13 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_keep(SampleParams P) {
         for (int e = 0; e < G::EPL; ++e) {
             const float xv = x[j * G::EPL + e];
             const bool fin = xv > -__builtin_inff();
-            const float wf = dense_wf(xv, xmax);
             const float d16 = dense_d16(xv, xmax);
-            const bool kept = fin && d16 < blo && wf >= mthr;
-            kmd += kept ? (double)wf : 0.0;
+            bool kept = fin && d16 < blo;
+            if (ballot(kept)) {                         // uniform: weights only where some lane keeps
+                const float wf = dense_wf(xv, xmax);
+                kept = kept && wf >= mthr;
+                kmd += kept ? (double)wf : 0.0;
+            }
             kb |= kept ? 1u << e : 0u;
             mb |= fin && d16 >= blo && d16 < bhi ? 1u << (j * G::EPL + e) : 0u;
         }
