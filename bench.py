@@ -263,7 +263,12 @@ def main():
             alg_bytes = lg.nbytes + (0 if hist is None else hist.numel() * 4) + \
                 (0 if mask is None else mask.numel() * 4) + u.numel() * 4 + out_ids.numel() * 4 + \
                 out_p.numel() * 4
-            kernel_names = ["sample_sweep", "sample_finish"]
+            # rows without top-k, mask or greedy take the library's dense path
+            dense = mask is None and not cfgd.get("greedy") and cfgd.get("temperature", 1.0) > 0 and \
+                not (0 < cfgd.get("top_k", 0) < V)
+            kernel_names = (["dense_stats"] + (["dense_hist", "dense_bound"] if cfgd.get("top_p", 1.0) < 1
+                                               else []) + ["dense_keep", "dense_final"]
+                            if dense else ["sample_sweep", "sample_finish"])
             config = {"workload": name, "B": B, "V": V, "history": H,
                       "logits_dtype": "bf16" if is_bf16 else "fp32"}
             config.update({k: v for k, v in cfgd.items()})

@@ -171,8 +171,9 @@ def lm_head_argmax(B=1, H=4096, V=128256, seed=1008):
 def top_p_only(B=64, V=128256, seed=1002):
     """The headline rows (B=64, fp32 vocab 128256, N(0, 4^2)) sampled with
     top-p alone: T 1.0, top-p 0.9, no top-k, no penalties, no mask.  Nearly
-    every value lies within 27 T of its chunk's maximum, so no bound narrows the
-    candidates and every row takes the exact full-row path."""
+    every value lies within 27 T of its chunk's maximum, so no candidate bound
+    narrows the row: the sampler's dense path (every chunk's workgroup takes
+    part in each of its passes)."""
     rng = np.random.Generator(np.random.PCG64(seed))
     logits = _normal(rng, (B, V), 4.0)
     u = rng.random(B, dtype=np.float32)
