@@ -687,6 +687,7 @@ def test_workspace_garbage(gpu, oracle):
     cent = wl.f32_to_bf16_bits(rng.normal(0, 2, (2, 512)).astype(np.float32))
     order = rng.permutation(65536).astype(np.uint32)
     xm = wl.f32_to_bf16_bits(rng.normal(0, 2, (2, 65536)).astype(np.float32))
+    xflat = rng.normal(0, 0.01, (4, 30000)).astype(np.float32)
 
     def run_all():
         out = []
@@ -697,6 +698,13 @@ def test_workspace_garbage(gpu, oracle):
         out += [_np(t) for t in llima_amd.sample(_t(cw["logits"], gpu), _t(cw["uniforms"], gpu),
                                                   llima_amd.SamplerConfig(**cw["cfg"]),
                                                   bitmask=_t(cw["bitmask"], gpu))]
+        for dcfg in (dict(temperature=0.9, top_p=0.9, min_p=0.01, repetition_penalty=1.1),
+                     dict(temperature=1.0)):                   # the dense path
+            out += [_np(t) for t in llima_amd.sample(_t(x, gpu), _t(u, gpu),
+                                                      llima_amd.SamplerConfig(**dcfg),
+                                                      history=_t(h, gpu), return_keep=True)]
+        out += [_np(t) for t in llima_amd.sample(_t(xflat, gpu), _t(u, gpu),   # dense, then full-row
+                                                  llima_amd.SamplerConfig(temperature=1.0, top_p=0.5))]
         out += [_np(t) for t in llima_amd.argmax(_t(xb, gpu))]
         out += [_np(t) for t in llima_amd.verify_greedy(_t(sp["target"], gpu),
                                                          _t(sp["draft_ids"], gpu))]

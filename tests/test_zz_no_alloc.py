@@ -63,18 +63,20 @@ def _call(L, entry, w, dev, ws=None):
 def _workloads():
     big = wl.batched_penalties(B=64, V=128256, H=2048)
     small = wl.constrained(B=3, V=20000, runs=40, seed=11)
-    return big, small
+    dense = wl.top_p_only(B=16, V=50000, seed=12)             # the dense path (no top-k)
+    return big, small, dense
 
 
 def test_noalloc_matches_workspace_entry_point(gpu, oracle):
     import torch
     from llima_amd import _lib
     L = _lib.lib()
-    big, small = _workloads()
+    big, small, dense = _workloads()
     wsb = L.llima_sample_workspace_bytes(64, 128256, _lib.LLIMA_F32)
     assert wsb <= L.llima_sample_noalloc_max_bytes()
     ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
     for w, what in ((big, "batched_penalties B=64 V=128256"), (small, "constrained B=3 V=20000"),
+                    (dense, "top_p_only B=16 V=50000"),
                     (big, "batched_penalties B=64 V=128256 again")):
         _say("llima_sample_noalloc vs llima_sample:", what)
         a = _call(L, "noalloc", w, gpu)
