@@ -2338,6 +2338,39 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_bound(SampleParams P) {
         r0[SMP_DINFO + 1] = (bstar & 1u) ? ab + m0 : ab;
         r0[SMP_DINFO + 2] = Z;
     }
+    if (!(c.m > 0.0f)) {
+        // Without min-p every value above b* is kept, so each chunk's kept
+        // mass is the sum of its bins before b*: 8 threads per chunk (32
+        // chunks per round), thread part p summing bin pairs p, p + 8, ...
+        // (4 loads in flight), then a reduction over the 8 lanes.
+        const uint32_t part = t & 7u, npairs = (bstar + 1u) >> 1;
+        for (int cb = 0; cb < P.S; cb += LLIMA_WG / 8) {
+            const int ci = cb + (int)(t >> 3);
+            const uint64_t* reg = r0 + (size_t)(ci < P.S ? ci : 0) * SMP_REGION;
+            uint64_t acc = 0;
+            for (uint32_t q0 = part; q0 < npairs; q0 += 32u) {
+                llima_u32x4 h[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t q = q0 + 8u * (uint32_t)k;
+                    h[k] = *(const llima_u32x4*)(reg + 2u * (q < npairs ? q : 0u));
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t q = q0 + 8u * (uint32_t)k;
+                    const uint64_t a = ((uint64_t)h[k].y << 32) | h[k].x, b = ((uint64_t)h[k].w << 32) | h[k].z;
+                    acc += q < npairs ? (a >> 14) + (2u * q + 1u < bstar ? b >> 14 : 0ull) : 0ull;
+                }
+            }
+#pragma unroll
+            for (int sft = 1; sft < 8; sft <<= 1) {
+                const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)acc, sft);
+                const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(acc >> 32), sft);
+                acc += ((uint64_t)hi << 32) | lo;
+            }
+            if (part == 0 && ci < P.S) r0[(size_t)ci * SMP_REGION + SMP_DKEPT] = acc;
+        }
+    }
 }
 
 template <typename TL>
@@ -2420,6 +2453,9 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof
     const uint32_t lane = lane_id();
     const int nw = (P.V + 31) >> 5;
     uint32_t* kw = P.out_keep + (size_t)row * nw;
+    // top-p rows without min-p: dense_bound summed each chunk's kept mass from
+    // its bins, and no weight is needed here
+    const bool need_w = !topp || c.m > 0.0f;
     double kmd = 0.0;                                   // at most 32 weights below 2^37: exact
     uint32_t mb = 0;                                    // this thread's boundary members
 #pragma unroll
@@ -2431,7 +2467,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof
             const bool fin = xv > -__builtin_inff();
             const float d16 = dense_d16(xv, xmax);
             bool kept = fin && d16 < blo;
-            if (ballot(kept)) {                         // uniform: weights only where some lane keeps
+            if (need_w && ballot(kept)) {               // uniform: weights only where some lane keeps
                 const float wf = dense_wf(xv, xmax);
                 kept = kept && wf >= mthr;
                 kmd += kept ? (double)wf : 0.0;
@@ -2468,7 +2504,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof
                 }
     }
     const uint64_t km = block_sum_u64((uint64_t)kmd, bs);   // its barriers also settle mcount
-    if (threadIdx.x == 0) region_of(P, row, chunk)[SMP_DKEPT] = km;
+    if (threadIdx.x == 0 && need_w) region_of(P, row, chunk)[SMP_DKEPT] = km;
     const uint32_t n = mcount;
     if (n) {                                             // uniform
         // a workgroup with more members than it stages makes the row's count
