@@ -2034,7 +2034,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 //                                   boundary members (member j at region
 //                                   j / SMP_DBINS, slot j % SMP_DBINS)
 //   region c, SMP_DSTAT / SMP_DBEST  dense_stats's results for chunk c
-//   region c, SMP_DKEPT             dense_keep's kept mass of chunk c
+//   region c, SMP_DKEPT             the kept mass of chunk c (dense_bound or dense_keep)
+//   region c, SMP_DMCNT             dense_bound: chunk c's count in the boundary bin
 //   region 0, SMP_DINFO..+2         dense_bound's boundary bin, mass above it, Z
 //   region 0, SMP_DMEM              members appended (a 128-byte line of its
 //                                   own), zeroed by dense_stats
@@ -2043,6 +2044,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 #define SMP_DSTAT 448                              // chunk max key << 32 | finite count
 #define SMP_DBEST 449                              // greedy: key << 32 | ~id of the chunk maximum
 #define SMP_DKEPT 450                              // kept mass strictly above the boundary bin
+#define SMP_DMCNT 451                              // the chunk's members of the boundary bin
 #define SMP_DINFO 456                              // region 0: boundary bin, mass above it, Z
 #define SMP_DMEM 496                               // region 0: boundary members appended
 #define SMP_DMCAP 4096                             // members dense_final ranks (16 per thread)
@@ -2338,6 +2340,11 @@ __global__ __launch_bounds__(LLIMA_WG) void dense_bound(SampleParams P) {
         r0[SMP_DINFO + 1] = (bstar & 1u) ? ab + m0 : ab;
         r0[SMP_DINFO + 2] = Z;
     }
+    // each chunk's count in b*, so that dense_keep skips the chunks without members
+    for (int i = (int)t; i < P.S; i += LLIMA_WG) {
+        uint64_t* reg = r0 + (size_t)i * SMP_REGION;
+        reg[SMP_DMCNT] = reg[bstar] & 0x3FFFu;
+    }
     if (!(c.m > 0.0f)) {
         // Without min-p every value above b* is kept, so each chunk's kept
         // mass is the sum of its bins before b*: 8 threads per chunk (32
@@ -2427,13 +2434,18 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
     const int c0 = (int)chunk * G::CHUNK;
+    const RowCfg c = load_cfg(P, (int)row);
+    if (c.greedy) return;                               // dense_final writes greedy rows
+    const bool topp = c.p < 1.0f;
+    // top-p rows without min-p or a kept-set output need this pass only for
+    // the boundary bin's members: chunks without any leave before loading
+    if (topp && !(c.m > 0.0f) && !P.out_keep &&
+        (uint32_t)region_of(P, row, chunk)[SMP_DMCNT] == 0u)
+        return;                                          // uniform
     int32_t hid[SMP_HBATCH];
     if (P.H_max > 0) dense_hist_ids(P, (int)row, hid);
     llima_u32x4 raw[G::NL];
     dense_issue<TL>(P, (int)row, c0, raw);
-    const RowCfg c = load_cfg(P, (int)row);
-    if (c.greedy) return;                               // dense_final writes greedy rows
-    const bool topp = c.p < 1.0f;
     uint64_t* r0 = region_of(P, row, 0);
     // the boundary bin requested with the statistics (both written by earlier launches)
     const uint64_t binfo = r0[SMP_DINFO];
