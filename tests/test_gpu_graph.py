@@ -1,0 +1,117 @@
+"""HIP graph replay: one llima_sample call (the sweep + finish kernels, or the
+dense path) and one llima_verify_rejection call captured into a graph through
+the C ABI, then replayed several times.  Between replays the program's own
+eager work writes new inputs into the captured buffers and synchronises; every
+replay is checked against the oracle on that replay's inputs."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from llima_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+REPLAYS = 3
+
+
+def _say(*a):
+    print("[gpu-case]", *a, flush=True)
+
+
+SAMPLE_CFGS = {
+    "sweep_finish": dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.02, repetition_penalty=1.2,
+                         presence_penalty=0.3, frequency_penalty=0.2),
+    "dense": dict(temperature=0.9, top_p=0.9, min_p=0.01, repetition_penalty=1.1),
+    "dense_plain": dict(temperature=1.0),
+}
+
+
+@pytest.mark.parametrize("name", list(SAMPLE_CFGS))
+def test_sample_graph_replays(gpu, oracle, name):
+    import torch
+    from llima_amd import SamplerConfig, _lib
+    from oracle.oracle import SamplerConfig as OC
+    _say("graph replay llima_sample", name)
+    L = _lib.lib()
+    cfgd = SAMPLE_CFGS[name]
+    rng = np.random.default_rng(31 + list(SAMPLE_CFGS).index(name))
+    B, V, H = 16, 50000, 300
+    xs = [rng.normal(0, 3, (B, V)).astype(np.float32) for _ in range(REPLAYS)]
+    hs = [rng.integers(0, V, size=(B, H)).astype(np.int32) for _ in range(REPLAYS)]
+    us = [rng.random(B).astype(np.float32) for _ in range(REPLAYS)]
+    x = torch.empty((B, V), dtype=torch.float32, device=gpu)
+    h = torch.empty((B, H), dtype=torch.int32, device=gpu)
+    u = torch.empty(B, dtype=torch.float32, device=gpu)
+    nw = (V + 31) // 32
+    ids = torch.empty(B, dtype=torch.int32, device=gpu)
+    probs = torch.empty(B, dtype=torch.float32, device=gpu)
+    keep = torch.empty((B, nw), dtype=torch.int32, device=gpu)
+    nws = L.llima_sample_workspace_bytes(B, V, _lib.LLIMA_F32)
+    ws = torch.empty(nws, dtype=torch.uint8, device=gpu)
+    cfg, keep_alive = SamplerConfig(**cfgd).to_c(B, gpu)
+
+    def launch(stream):
+        rc = L.llima_sample(x.data_ptr(), _lib.LLIMA_F32, B, V, V, h.data_ptr(), None, H, None,
+                            u.data_ptr(), ctypes.byref(cfg), ids.data_ptr(), probs.data_ptr(),
+                            keep.data_ptr(), ws.data_ptr(), nws, stream)
+        assert rc == 0
+
+    def load(i):
+        x.copy_(torch.from_numpy(xs[i]))
+        h.copy_(torch.from_numpy(hs[i]))
+        u.copy_(torch.from_numpy(us[i]))
+
+    load(0)
+    launch(torch.cuda.current_stream(gpu).cuda_stream)        # eager warmup
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(gpu)
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        launch(cap.cuda_stream)
+    torch.cuda.synchronize(gpu)
+    for i in range(REPLAYS):
+        load(i)
+        ids.fill_(-7)
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        eids, eprobs, ekeep = oracle.sample(xs[i], us[i], OC(**cfgd), history=hs[i], want_keep=True)
+        gi = ids.cpu().numpy()
+        assert (gi == eids).all(), (name, i, np.flatnonzero(gi != eids)[:8])
+        assert (probs.cpu().numpy().view(np.uint32) == eprobs.view(np.uint32)).all(), (name, i)
+        assert (keep.cpu().numpy().view(np.uint32) == ekeep).all(), (name, i)
+    del keep_alive
+
+
+def test_verify_rejection_graph_replays(gpu, oracle):
+    import torch
+    import llima_amd
+    _say("graph replay llima_verify_rejection")
+    ws_ = [wl.speculative(B=4, D=5, V=30000, seed=40 + i) for i in range(REPLAYS)]
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    cur = {k: dev(ws_[0][k]) for k in ("target", "draft", "draft_ids", "u_accept", "u_resample")}
+    out = llima_amd.verify_rejection(cur["target"], cur["draft"], cur["draft_ids"],
+                                     cur["u_accept"], cur["u_resample"])       # eager warmup
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(gpu)
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        out = llima_amd.verify_rejection(cur["target"], cur["draft"], cur["draft_ids"],
+                                         cur["u_accept"], cur["u_resample"])
+    torch.cuda.synchronize(gpu)
+    for i in range(REPLAYS):
+        for k in cur:
+            cur[k].copy_(dev(ws_[i][k]))
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        w = ws_[i]
+        exp = oracle.verify_rejection(w["target"], w["draft"], w["draft_ids"], w["u_accept"],
+                                      w["u_resample"])
+        for got, want in zip(out, exp):
+            assert np.array_equal(got.cpu().numpy(), want), i
