@@ -349,6 +349,45 @@ def test_sample_dense_path(gpu, oracle, kind, dtype):
         _sample_both(gpu, oracle, x, u, cfgd, history=hist, hist_len=hl)
 
 
+@pytest.mark.parametrize("seed", range(32))
+def test_sample_dense_random(gpu, oracle, seed):
+    """Seeded random rows and configurations without top-k or mask (the dense
+    path): shapes with a ragged last chunk, both dtypes, narrow to wide value
+    spreads, ties, histories, broadcast or per-row temperature / top-p / min-p
+    (a zero temperature makes a greedy row)."""
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 9))
+    V = int(rng.choice([37, 4096, 4097, 30001, 128256, 151936]))
+    dtype = "bf16" if rng.random() < 0.4 else "f32"
+    sigma = float(rng.choice([0.3, 1.0, 3.0, 8.0]))
+    x = rng.normal(0, sigma, (B, V)).astype(np.float32)
+    if rng.random() < 0.25:
+        x = np.round(x * 4) / 4
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    hist = hl = None
+    if rng.random() < 0.5:
+        H = int(rng.choice([8, 256, 2048]))
+        hist = rng.integers(-2, V + 2, size=(B, H)).astype(np.int32)
+        hl = rng.integers(0, H + 1, size=B).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    base = dict(temperature=float(rng.choice([0.3, 0.7, 1.0, 1.6])),
+                top_p=float(rng.choice([1.0, 0.5, 0.9, 0.99, 0.999])),
+                min_p=float(rng.choice([0.0, 0.0, 0.01, 0.2])))
+    if hist is not None and rng.random() < 0.7:
+        base.update(repetition_penalty=float(rng.choice([1.1, 0.9])),
+                    presence_penalty=float(rng.choice([0.0, 0.4, -0.2])),
+                    frequency_penalty=float(rng.choice([0.0, 0.25])))
+    _say("sample dense random", seed, B, V, dtype, sigma, base)
+    if rng.random() < 0.3:
+        rows = {k: v for k, v in base.items() if k not in ("temperature", "top_p")}
+        rows["temperature"] = [float(v) for v in rng.choice([0.0, 0.5, 1.0, 2.0], size=B)]
+        rows["top_p"] = [float(v) for v in rng.choice([1.0, 0.6, 0.95], size=B)]
+        _sample_both(gpu, oracle, x, u, None, history=hist, hist_len=hl, cfg_rows=rows)
+    else:
+        _sample_both(gpu, oracle, x, u, base, history=hist, hist_len=hl)
+
+
 def test_sample_dense_rows_config_and_strides(gpu, oracle):
     """The dense path with per-row temperatures and top-p (a zero temperature
     makes a greedy row) and on rows that start unaligned (a row stride of
