@@ -889,8 +889,46 @@ __device__ __forceinline__ void count_history(const SampleParams& P, int row, in
     __syncthreads();
 }
 
+// ------------------------------------------------------------------ value bins
+// Used by the full-row path and the dense path: bins of 1/16 nat below the
+// row maximum, exact weights in their float form.
+#define SMP_DBINS 448                              // value bins, 1/16 nat (28 nats; the last open)
+#define SMP_DBIN_SCALE 16.0f
+
+// 16 (xmax - x) clamped to the last bin, 0 at x == xmax (also when both are
+// +inf): the value bin of x (x <= xmax, not NaN) is its integral part, so
+// bin < b exactly when it is below b, and bin == b when it lies in [b, b + 1).
+__device__ __forceinline__ float dense_d16(float x, float xmax) {
+    return x == xmax ? 0.0f : __builtin_fminf((xmax - x) * SMP_DBIN_SCALE, (float)(SMP_DBINS - 1));
+}
+
+// weight(x, xmax) as an integral float: weight_f, and 2^36 at x == xmax also
+// when the maximum is +inf (every other value then weighs 0, as weight_f's
+// clamp at -26 gives).
+__device__ __forceinline__ float dense_wf(float x, float xmax) {
+    return weight_fd(x == xmax ? 0.0f : x - xmax);      // a select, not a branch per value
+}
+
+// An integral float below 2^52 as uint64 without branches: the part from 2^32
+// up and the rest are each exact (a float's significand has 24 bits).
+__device__ __forceinline__ uint64_t wf_u64(float wf) {
+    const float hi = __builtin_truncf(wf * 2.3283064365386963e-10f);
+    const uint32_t lo = (uint32_t)__builtin_fmaf(hi, -4294967296.0f, wf);
+    return ((uint64_t)(uint32_t)hi << 32) | lo;
+}
+
+// The min-p threshold frac32(m) 2^4 rounded up to a float: an integral float
+// weight W has W >= threshold exactly when W >= this.
+__device__ __forceinline__ float dense_mthr(const RowCfg& c) {
+    const uint64_t m = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    float f = (float)m;
+    if (f32_integral_to_u64(f) < m) f = __uint_as_float(__float_as_uint(f) + 1u);
+    return f;
+}
+
 // ------------------------------------------------------------------ full-row path
 #define SMP_FE 16                                  // values per thread per full-row step
+#define SMP_FRMCAP 1024                            // boundary-bin members the full-row path ranks
 
 // SMP_FE consecutive values from id i0 of a row, ids at or past hi (a multiple
 // of the values per 16-byte load when vec) read from clamped addresses: 16-byte
@@ -958,6 +996,35 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
                     }
                 }
             }
+            __syncthreads();
+        }
+    };
+    // for_each_x with seg_end(lo) called by every thread after the SMP_SEG ids
+    // from lo, before the barrier that ends them.
+    auto for_each_x_seg = [&](auto fn, auto seg_end) {
+        for (int lo = 0; lo < V; lo += SMP_SEG) {
+            const int hi = lo + SMP_SEG < V ? lo + SMP_SEG : V;
+            if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SMP_SEG / 2);
+            for (int b0 = lo; b0 < hi; b0 += LLIMA_WG * SMP_FE) {
+                const int i0 = b0 + (int)threadIdx.x * SMP_FE;
+                float xs[SMP_FE];
+                load_fe<TL>(rowp, i0, hi, vec, xs);
+#pragma unroll
+                for (int e = 0; e < SMP_FE; ++e) {
+                    const int i = i0 + e;
+                    if (i < hi) {
+                        float l = xs[e];
+                        if (l != l) l = -__builtin_inff();
+                        if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) l = -__builtin_inff();
+                        if (c.pen) {
+                            const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
+                            if (cnt) l = penalize(l, cnt, c);
+                        }
+                        fn(c.greedy ? l : l / c.T, (uint32_t)i);
+                    }
+                }
+            }
+            seg_end(lo);
             __syncthreads();
         }
     };
@@ -1055,30 +1122,20 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         (void)id;
     };
 
-    // top-p threshold
-    uint32_t theta = 0;
-    if (c.p < 1.0f) {
-        uint64_t Z = 0;
-        for_each_x([&](float x, uint32_t id) { elem_k(x, id, [&](uint32_t, uint64_t w) { Z += w; }); });
-        Z = block_sum_u64(Z, sh.bs);
-        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
-        uint64_t acc = 0;
-        theta = radix(elem_k, kmin_k, kmax, [&](int, uint64_t&, uint32_t&) {
-            const uint32_t t = threadIdx.x, bin = 255u - t;
-            const uint32_t cn = sh.hcnt[0][bin];
-            uint64_t m = sh.hmass[0][bin], tot;
-            const uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
-            const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
-            const uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
-            const uint32_t top_nonempty = 255u - block_max_u32(cn > 0 ? 255u - t : 0u, sh.bs);
-            const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
-            if (t == sel_t) { sh.sel[0] = bin; sh.sel64[0] = above; }
-            __syncthreads();
-            acc = sh.sel64[0];
-            return sh.sel[0];
-        });
-    }
+    // Top-p, min-p and the draw over value bins of 1/16 nat below the maximum.
+    // One pass counts the top-k set's mass into the bins: Z, and the bin b*
+    // holding the top-p boundary (the last non-empty bin whose mass above,
+    // times 2^32, is below p32 Z; the top non-empty bin when none is), which is
+    // where the radix rounds below would find it.  A second pass collects b*'s
+    // members and each segment's kept mass above b*; the members, ranked from
+    // the mass above b*, give theta; the draw scans the one segment that holds
+    // its target, in id order.  When b* has more members than the LDS holds,
+    // the radix rounds below run instead.
     const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
+    uint32_t theta = 0;
+    int32_t tok = -1;
+    float prob = 0.0f;
+    bool binned = false;
     auto fin_elem = [&](float x, uint32_t id, auto fn) {
         const uint32_t k = f32_key(x);
         if (k >= tau && k >= theta) {
@@ -1086,34 +1143,224 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
             if (w >= mthr) fn(id, w);
         }
     };
-    uint64_t Zf = 0;
-    for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t, uint64_t w) { Zf += w; }); });
-    Zf = block_sum_u64(Zf, sh.bs);
-    int32_t tok = -1;
-    float prob = 0.0f;
-    if (Zf > 0) {
-        const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
-        uint64_t acc = 0, wtok = 0;
-        tok = (int32_t)radix(
-            [&](float x, uint32_t id, auto fn) {
-                fin_elem(x, id, [&](uint32_t i, uint64_t w) { if (w) fn(i, w); });
+    {
+        int segw = SMP_SEG;
+        while ((V + segw - 1) / segw > LLIMA_WG) segw <<= 1;
+        const int nseg = (V + segw - 1) / segw;
+        uint64_t* seg = &sh.part[0][0][0];                     // nseg <= LLIMA_WG slots
+        uint64_t* mem = (uint64_t*)&sh.sv2[0][0];             // SMP_FRMCAP members
+        uint64_t* bins = &sh.hmass[0][0];                     // SMP_DBINS slots
+        const uint32_t t = threadIdx.x;
+        const bool topp = c.p < 1.0f;
+        const float mthr_f = dense_mthr(c);
+        uint32_t bstar = SMP_DBINS;
+        uint64_t above = 0, Zb = 0;
+        if (topp) {
+            for (uint32_t i = t; i < SMP_DBINS; i += LLIMA_WG) bins[i] = 0;
+            __syncthreads();
+            for_each_x([&](float x, uint32_t) {
+                if (f32_key(x) >= tau)
+                    atomicAdd((unsigned long long*)&bins[(uint32_t)dense_d16(x, xmax)],
+                              (unsigned long long)wf_u64(dense_wf(x, xmax)));
+            });
+            // a bin's mass is 0 only when it is empty or every value in it weighs
+            // 0, and such a bin never qualifies (its mass above is Z)
+            const uint64_t m0 = t < SMP_DBINS / 2 ? bins[2u * t] : 0ull;
+            const uint64_t m1 = t < SMP_DBINS / 2 ? bins[2u * t + 1u] : 0ull;
+            const uint64_t ab = block_excl_scan_u64(m0 + m1, &Zb, sh.bs);
+            const llima_u128 PZ = (llima_u128)frac32(c.p) * Zb;
+            const bool q0 = m0 > 0 && (((llima_u128)ab << 32) < PZ);
+            const bool q1 = m1 > 0 && (((llima_u128)(ab + m0) << 32) < PZ);
+            const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
+            const uint32_t ne = m0 ? 2u * t : (m1 ? 2u * t + 1u : 0xFFFFFFFFu);
+            const uint32_t top = ~block_max_u32(~ne, sh.bs);
+            bstar = qb ? qb - 1u : top;
+            if ((bstar >> 1) == t) sh.sel64[0] = (bstar & 1u) ? ab + m0 : ab;
+            __syncthreads();
+            above = sh.sel64[0];
+        }
+        for (int i = (int)t; i < nseg; i += LLIMA_WG) seg[i] = 0;
+        if (t == 0) sh.lcount = 0;
+        __syncthreads();
+        const float blo = (float)bstar, bhi = (float)bstar + 1.0f;
+        uint64_t acc = 0;
+        for_each_x_seg(
+            [&](float x, uint32_t id) {
+                const uint32_t k = f32_key(x);
+                if (k >= tau) {
+                    const float d16 = dense_d16(x, xmax);
+                    if (d16 < blo) {
+                        const float wf = dense_wf(x, xmax);
+                        if (wf >= mthr_f) acc += wf_u64(wf);
+                    } else if (d16 < bhi) {
+                        const uint32_t o = atomicAdd(&sh.lcount, 1u);
+                        if (o < SMP_FRMCAP) mem[o] = ((uint64_t)k << 32) | id;
+                    }
+                }
             },
-            0u, (uint32_t)(V > 1 ? V - 1 : 1),
-            [&](int, uint64_t&, uint32_t&) {
-                const uint32_t bin = threadIdx.x;
-                uint64_t m = sh.hmass[0][bin], tot;
-                const uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
+            [&](int lo) {
+                const uint64_t v = wave_sum_u64(acc);
+                if (lane_id() == 0 && v)
+                    atomicAdd((unsigned long long*)&seg[lo / segw], (unsigned long long)v);
+                acc = 0;
+            });
+        const uint32_t nmem = sh.lcount;
+        if (nmem <= SMP_FRMCAP && (!topp || nmem > 0)) {         // uniform
+            binned = true;
+            if (topp) {
+                constexpr int EPT = SMP_FRMCAP / LLIMA_WG;
+                uint32_t key[EPT], mid[EPT];
+                uint64_t w[EPT];
+                uint32_t mk = 0, nmk = 0;
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) {
+                    const uint32_t j = t + (uint32_t)e * LLIMA_WG;
+                    const uint64_t v = j < nmem ? mem[j] : 0ull;
+                    key[e] = (uint32_t)(v >> 32);
+                    mid[e] = (uint32_t)v;
+                    w[e] = key[e] ? wf_u64(dense_wf(key_f32(key[e]), xmax)) : 0ull;
+                    mk = key[e] > mk ? key[e] : mk;
+                    nmk = key[e] && ~key[e] > nmk ? ~key[e] : nmk;
+                }
+                sh.hmass[0][t] = 0;                                // the bins are no longer needed
+                sh.hmass[1][t] = 0;
+                mk = block_max_u32(mk, sh.bs);
+                const uint32_t mkmin = ~block_max_u32(nmk, sh.bs);
+                const uint64_t p32 = frac32(c.p);
+                theta = fin_topp_desc<EPT>(key, w, p32, mkmin, mk, sh, above, (llima_u128)p32 * Zb, true);
+#pragma unroll
+                for (int e = 0; e < EPT; ++e)
+                    if (key[e] && key[e] >= theta && w[e] >= mthr)
+                        atomicAdd((unsigned long long*)&seg[mid[e] / (uint32_t)segw], (unsigned long long)w[e]);
+            }
+            if (t == 0) {
+                sh.sel[0] = 0;
+                sh.sel64[0] = 0;
+            }
+            __syncthreads();
+            const uint64_t m = (int)t < nseg ? seg[t] : 0ull;
+            uint64_t Zf;
+            const uint64_t below = block_excl_scan_u64(m, &Zf, sh.bs);
+            if (Zf > 0) {
+                const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
                 if (m > 0 && below <= target && target < below + m) {
-                    sh.sel[0] = bin; sh.sel64[0] = below; sh.sel64[1] = m;
+                    sh.sel[0] = t;
+                    sh.sel64[0] = target - below;
                 }
                 __syncthreads();
+                const int sg = (int)sh.sel[0];
+                uint64_t rel = sh.sel64[0];
+                // the segment in blocks of SMP_SEG ids, each in id order: thread t
+                // holds SMP_SEG / LLIMA_WG consecutive ids of the block
+                constexpr int EPS = SMP_SEG / LLIMA_WG;
+                const int s1 = (sg + 1) * segw < V ? (sg + 1) * segw : V;
+                for (int lo = sg * segw; lo < s1; lo += SMP_SEG) {
+                    const int hi = lo + SMP_SEG < V ? lo + SMP_SEG : V;
+                    if (c.pen) count_history(P, row, c.hlen, lo, hi, table, SMP_SEG / 2);
+                    const int i0 = lo + (int)t * EPS;
+                    // the kept weight of id i (0 when not kept)
+                    auto kept_w = [&](float l, int i) -> uint64_t {
+                        if (l != l) l = -__builtin_inff();
+                        if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) l = -__builtin_inff();
+                        if (c.pen) {
+                            const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
+                            if (cnt) l = penalize(l, cnt, c);
+                        }
+                        const float x = l / c.T;
+                        const uint32_t k = f32_key(x);
+                        if (!(k >= tau && k >= theta)) return 0ull;
+                        const float wf = dense_wf(x, xmax);
+                        return wf >= mthr_f ? wf_u64(wf) : 0ull;
+                    };
+                    uint64_t sum = 0;
+                    for (int g = 0; g < EPS; g += SMP_FE) {
+                        float xs[SMP_FE];
+                        load_fe<TL>(rowp, i0 + g, hi, vec, xs);   // ids past hi: clamped addresses
+#pragma unroll
+                        for (int e = 0; e < SMP_FE; ++e)
+                            if (i0 + g + e < hi) sum += kept_w(xs[e], i0 + g + e);
+                    }
+                    uint64_t tot;
+                    const uint64_t bl = block_excl_scan_u64(sum, &tot, sh.bs);
+                    if (rel < tot) {                                   // uniform
+                        if (sum > 0 && bl <= rel && rel < bl + sum) {
+                            uint64_t a = bl, wtok = 0;
+                            for (int g = 0; g < EPS; g += SMP_FE) {
+                                float xs[SMP_FE];
+                                load_fe<TL>(rowp, i0 + g, hi, vec, xs);
+#pragma unroll
+                                for (int e = 0; e < SMP_FE; ++e) {
+                                    const int i = i0 + g + e;
+                                    const uint64_t w = i < hi ? kept_w(xs[e], i) : 0ull;
+                                    const bool hit = tok < 0 && w > 0 && rel < a + w;
+                                    tok = hit ? i : tok;
+                                    wtok = hit ? w : wtok;
+                                    a += w;
+                                }
+                            }
+                            prob = (float)((double)wtok / (double)Zf);
+                            write_result(P, row, tok, prob);
+                        }
+                        break;
+                    }
+                    rel -= tot;
+                    __syncthreads();
+                }
+            } else if (t == 0) {
+                write_result(P, row, -1, 0.0f);
+            }
+        }
+    }
+    if (!binned) {
+        // radix rounds over the keys: theta, then the draw over the ids
+        if (c.p < 1.0f) {
+            uint64_t Z = 0;
+            for_each_x([&](float x, uint32_t id) { elem_k(x, id, [&](uint32_t, uint64_t w) { Z += w; }); });
+            Z = block_sum_u64(Z, sh.bs);
+            const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+            uint64_t acc = 0;
+            theta = radix(elem_k, kmin_k, kmax, [&](int, uint64_t&, uint32_t&) {
+                const uint32_t t = threadIdx.x, bin = 255u - t;
+                const uint32_t cn = sh.hcnt[0][bin];
+                uint64_t m = sh.hmass[0][bin], tot;
+                const uint64_t above = acc + block_excl_scan_u64(m, &tot, sh.bs);
+                const bool cond = cn > 0 && (((llima_u128)above << 32) < PZ);
+                const uint32_t best_cond = block_max_u32(cond ? t + 1u : 0u, sh.bs);
+                const uint32_t top_nonempty = 255u - block_max_u32(cn > 0 ? 255u - t : 0u, sh.bs);
+                const uint32_t sel_t = best_cond ? best_cond - 1u : top_nonempty;
+                if (t == sel_t) { sh.sel[0] = bin; sh.sel64[0] = above; }
+                __syncthreads();
                 acc = sh.sel64[0];
-                wtok = sh.sel64[1];
                 return sh.sel[0];
             });
-        prob = (float)((double)wtok / (double)Zf);
+        }
+        uint64_t Zf = 0;
+        for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t, uint64_t w) { Zf += w; }); });
+        Zf = block_sum_u64(Zf, sh.bs);
+        if (Zf > 0) {
+            const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
+            uint64_t acc = 0, wtok = 0;
+            tok = (int32_t)radix(
+                [&](float x, uint32_t id, auto fn) {
+                    fin_elem(x, id, [&](uint32_t i, uint64_t w) { if (w) fn(i, w); });
+                },
+                0u, (uint32_t)(V > 1 ? V - 1 : 1),
+                [&](int, uint64_t&, uint32_t&) {
+                    const uint32_t bin = threadIdx.x;
+                    uint64_t m = sh.hmass[0][bin], tot;
+                    const uint64_t below = acc + block_excl_scan_u64(m, &tot, sh.bs);
+                    if (m > 0 && below <= target && target < below + m) {
+                        sh.sel[0] = bin; sh.sel64[0] = below; sh.sel64[1] = m;
+                    }
+                    __syncthreads();
+                    acc = sh.sel64[0];
+                    wtok = sh.sel64[1];
+                    return sh.sel[0];
+                });
+            prob = (float)((double)wtok / (double)Zf);
+        }
+        if (threadIdx.x == 0) write_result(P, row, tok, prob);
     }
-    if (threadIdx.x == 0) write_result(P, row, tok, prob);
     if (P.out_keep)
         write_keep(P, row, [&](auto set) {
             for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t i, uint64_t) { set(i); }); });
@@ -2041,8 +2288,6 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 //   region 0, SMP_DINFO..+2         dense_bound's boundary bin, mass above it, Z
 //   region 0, SMP_DMEM              members appended (a 128-byte line of its
 //                                   own), zeroed by dense_stats
-#define SMP_DBINS 448                              // value bins, 1/16 nat (28 nats; the last open)
-#define SMP_DBIN_SCALE 16.0f
 #define SMP_DSTAT 448                              // chunk max key << 32 | finite count
 #define SMP_DBEST 449                              // greedy: key << 32 | ~id of the chunk maximum
 #define SMP_DKEPT 450                              // kept mass strictly above the boundary bin
@@ -2062,37 +2307,6 @@ struct DenseGeom {
     static constexpr int CHUNK = LLIMA_WG * E;         // 4096 fp32 / 8192 bf16 (the sweep's chunk)
     static constexpr int WS = CHUNK / LLIMA_WAVES;     // ids per wave
 };
-
-// 16 (xmax - x) clamped to the last bin, 0 at x == xmax (also when both are
-// +inf): the value bin of x (x <= xmax, not NaN) is its integral part, so
-// bin < b exactly when it is below b, and bin == b when it lies in [b, b + 1).
-__device__ __forceinline__ float dense_d16(float x, float xmax) {
-    return x == xmax ? 0.0f : __builtin_fminf((xmax - x) * SMP_DBIN_SCALE, (float)(SMP_DBINS - 1));
-}
-
-// weight(x, xmax) as an integral float: weight_f, and 2^36 at x == xmax also
-// when the maximum is +inf (every other value then weighs 0, as weight_f's
-// clamp at -26 gives).
-__device__ __forceinline__ float dense_wf(float x, float xmax) {
-    return weight_fd(x == xmax ? 0.0f : x - xmax);      // a select, not a branch per value
-}
-
-// An integral float below 2^52 as uint64 without branches: the part from 2^32
-// up and the rest are each exact (a float's significand has 24 bits).
-__device__ __forceinline__ uint64_t wf_u64(float wf) {
-    const float hi = __builtin_truncf(wf * 2.3283064365386963e-10f);
-    const uint32_t lo = (uint32_t)__builtin_fmaf(hi, -4294967296.0f, wf);
-    return ((uint64_t)(uint32_t)hi << 32) | lo;
-}
-
-// The min-p threshold frac32(m) 2^4 rounded up to a float: an integral float
-// weight W has W >= threshold exactly when W >= this.
-__device__ __forceinline__ float dense_mthr(const RowCfg& c) {
-    const uint64_t m = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
-    float f = (float)m;
-    if (f32_integral_to_u64(f) < m) f = __uint_as_float(__float_as_uint(f) + 1u);
-    return f;
-}
 
 __device__ __forceinline__ uint64_t* dense_member(uint64_t* r0, uint32_t j) {
     return r0 + (size_t)(j / SMP_DBINS) * SMP_REGION + (j % SMP_DBINS);

@@ -416,6 +416,42 @@ def test_sample_dense_rows_config_and_strides(gpu, oracle):
         assert (_np(keep).view(np.uint32) == ekeep).all()
 
 
+FULL_ROW_CONFIGS = [
+    dict(temperature=1.0, top_p=0.9),
+    dict(temperature=0.7, top_p=0.6, min_p=0.02, repetition_penalty=1.2, presence_penalty=0.3),
+    dict(temperature=1.3, min_p=0.05),
+    dict(temperature=1.0),
+    dict(temperature=1.0, top_p=0.0),
+]
+
+
+@pytest.mark.parametrize("density", [0.5, 0.98])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_full_row_path(gpu, oracle, density, dtype):
+    """Rows whose grammar mask admits most ids and that have no top-k overflow
+    the candidate regions and take the full-row path: value bins for top-p
+    (the boundary bin's members ranked) and a one-segment scan for the draw;
+    flat rows put more than 1024 values in the boundary bin and take the radix
+    rounds instead; a row without an allowed id gives -1."""
+    _say("sample full-row path", density, dtype)
+    rng = np.random.default_rng(int(density * 100) + (dtype == "bf16") + 400)
+    B, V = 6, 70001
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    x[1] = rng.normal(0, 0.02, V).astype(np.float32)        # flat: the radix rounds
+    x[2] = np.round(x[2])                                    # ties
+    x[3, 500:520] = np.inf
+    if dtype == "bf16":
+        x = wl.f32_to_bf16_bits(x)
+    mask = _sparse_mask(rng, B, V, density)
+    mask[4] = 0                                              # nothing allowed
+    mask[3, 500 >> 5] |= np.uint32(0xFFFFFFFF)
+    hist = rng.integers(0, V, size=(B, 400)).astype(np.int32)
+    u = rng.random(B).astype(np.float32)
+    for cfgd in FULL_ROW_CONFIGS:
+        gi = _sample_both(gpu, oracle, x, u, cfgd, history=hist, mask=mask)
+        assert gi[4] == -1
+
+
 def test_sample_masks_and_edges(gpu, oracle):
     _say("sample masks/edges")
     rng = np.random.default_rng(21)
