@@ -87,6 +87,13 @@ enum {
 
 enum { LLIMA_F32 = 0, LLIMA_BF16 = 1 };
 
+/* OR'ed into the LM head's logit_dtype together with LLIMA_BF16: out_logits
+ * then points to bf16 [B][V] (uint16 bits) and receives each logit as the
+ * bf16 value it was rounded to, half the bytes of the fp32 output, which
+ * llima_sample reads as LLIMA_BF16 rows.  No counterpart in the reference,
+ * whose graphs keep their logits in bf16 (model_graph.py:30-45). */
+#define LLIMA_LOGITS_OUT_BF16 0x100
+
 /* A call with B = 0 rows (or sequences) launches nothing and returns LLIMA_OK
  * once its sizes and modes are valid; its per-row buffers may then be null. */
 
@@ -287,8 +294,8 @@ int llima_mtp_masked_argmax(const uint16_t* centroid_logits, int64_t centroid_st
  * (sima_lmm/model/model_graph.py:30-45), so logits equal in bf16 tie and the
  * lower index wins -- and none for LLIMA_F32.  out_ids[B] = first index of the
  * maximum logit (NaN never wins; a row with no non-NaN logit gives 0),
- * out_vals[B] (nullable) its value, out_logits (nullable, fp32 [B][V]) every
- * logit.  H % 8 == 0, and H <= 4096 unless H % 64 == 0 (then H <= 65536).  The
+ * out_vals[B] (nullable) its value, out_logits (nullable, fp32 [B][V], or bf16
+ * with LLIMA_LOGITS_OUT_BF16) every logit.  H % 8 == 0, and H <= 4096 unless H % 64 == 0 (then H <= 65536).  The
  * weights are read once per 8 hidden rows (H <= 2048) or 4 (H <= 4096); wider
  * batches, and rows wider than 4096, use MFMA tiles that read them once per 256
  * rows (H % 64 == 0). */

@@ -44,6 +44,7 @@ struct LmhParams {
     int32_t B, H, V, NW;
     float cap;
     int32_t round_bf16;                // logits rounded to bf16 before the argmax
+    int32_t logits_bf16;               // out_logits holds bf16 [B][V] (LLIMA_LOGITS_OUT_BF16)
 };
 
 // The logit as the argmax sees it: softcapped, then (round_bf16) rounded to
@@ -57,6 +58,15 @@ __device__ __forceinline__ float lmh_logit(float s, const LmhParams& P) {
         s = __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
     }
     return s;
+}
+
+// Writes logit i of the [B][V] output: fp32, or the bf16 it was rounded to
+// (its upper 16 bits; a NaN as the quiet NaN).
+__device__ __forceinline__ void lmh_store_logit(const LmhParams& P, size_t i, float v) {
+    if (P.logits_bf16)
+        ((uint16_t*)P.out_logits)[i] = v == v ? (uint16_t)(__float_as_uint(v) >> 16) : (uint16_t)0x7FC0u;
+    else
+        P.out_logits[i] = v;
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -135,7 +145,7 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const float s = lmh_logit(wave_sum_f32(acc[b]), P);
-            if (b < nb && P.out_logits && lane == 0) P.out_logits[(size_t)(b0 + b) * P.V + v] = s;
+            if (b < nb && P.out_logits && lane == 0) lmh_store_logit(P, (size_t)(b0 + b) * P.V + v, s);
             const uint64_t key = s == s ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)v : 0ull;
             best[b] = key > best[b] ? key : best[b];
         }
@@ -290,7 +300,7 @@ __global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, i
         for (int i = 0; i < 16; ++i) {
             const int m = wm * 64 + mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
             const float v = lmh_logit(acc[mt][i], P);
-            if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
+            if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
             const uint64_t best = half_max_u64(lmh_key(v, n, V));
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
         }
@@ -452,7 +462,7 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
             for (int j = 0; j < WR; ++j) {
                 const int n = 32 * (rb0 + j) + r;            // >= V for a spare row block
                 const float v = lmh_logit(acc[j][mt][i], P);
-                if (P.out_logits && m < nb && n < V) P.out_logits[(size_t)(b0 + m) * V + n] = v;
+                if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
                 const uint64_t k = lmh_key(v, n, V);
                 key = k > key ? k : key;
             }
@@ -519,7 +529,10 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     if (H > LMH_MAX_H && (H > 65536 || H % LMH_KC != 0)) return LLIMA_E_INVAL;   // MFMA path only
     if (!weight || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
     if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
+    const int32_t logits_bf16 = (logit_dtype & LLIMA_LOGITS_OUT_BF16) != 0;
+    logit_dtype &= ~LLIMA_LOGITS_OUT_BF16;
     if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
+    if (logits_bf16 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;   // bf16 output of bf16 logits
     if ((uintptr_t)weight % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_lm_head_argmax_workspace_bytes(B, V))
@@ -535,6 +548,7 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.NW = lmh_waves(V);
     P.cap = softcap;
     P.round_bf16 = logit_dtype == LLIMA_BF16;
+    P.logits_bf16 = logits_bf16;
     hipStream_t st = (hipStream_t)stream;
     if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
         P.NW = lmh_mfma_waves(V);
@@ -614,7 +628,10 @@ extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packe
     if (B < 0 || llima_lm_head_packed_bytes(V, H) == 0) return LLIMA_E_INVAL;
     if (!packed || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
     if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
+    const int32_t logits_bf16 = (logit_dtype & LLIMA_LOGITS_OUT_BF16) != 0;
+    logit_dtype &= ~LLIMA_LOGITS_OUT_BF16;
     if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
+    if (logits_bf16 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;   // bf16 output of bf16 logits
     if ((uintptr_t)packed % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_lm_head_argmax_packed_workspace_bytes(B, H, V))
@@ -630,6 +647,7 @@ extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packe
     P.NW = (ng1 > ng2 ? ng1 : ng2) * LMP_WAVES;
     P.cap = softcap;
     P.round_bf16 = logit_dtype == LLIMA_BF16;
+    P.logits_bf16 = logits_bf16;
     hipStream_t st = (hipStream_t)stream;
     for (int b0 = 0; b0 < B; b0 += LMP_MB) {
         const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB;

@@ -551,22 +551,29 @@ def lm_head_pack(weight: torch.Tensor) -> PackedLmHead:
 
 
 def lm_head_argmax(hidden: torch.Tensor, weight, softcap: float = 0.0,
-                   return_logits: bool = False, logit_dtype: str = "bf16"):
+                   return_logits: bool = False, logit_dtype: str = "bf16",
+                   logits_out: str = "f32"):
     """LM head + softcap + argmax, as the reference's graph computes them before
     the host reads one int32 (language_part_base.py:171-180,
     language_model.cpp:1607-1609): hidden bf16 [B, H] (or [H]), weight bf16
     [V, H] -> (ids int32 [B], values float32 [B]) and, if return_logits, the
-    float32 logits [B, V].  logit_dtype "bf16" rounds each logit to bf16
-    before the argmax, as the reference's bf16 graphs produce them (equal bf16
-    logits tie, the lower index wins); "f32" keeps the fp32 sums.  weight may
-    be a PackedLmHead (lm_head_pack): the same logits, read in the packed order
-    (llima_lm_head_argmax_packed)."""
+    logits [B, V].  logit_dtype "bf16" rounds each logit to bf16 before the
+    argmax, as the reference's bf16 graphs produce them (equal bf16 logits
+    tie, the lower index wins); "f32" keeps the fp32 sums.  logits_out "bf16"
+    (with logit_dtype "bf16") returns the logits as a bfloat16 tensor, half
+    the bytes of the float32 one and the same values, ready for sample().
+    weight may be a PackedLmHead (lm_head_pack): the same logits, read in the
+    packed order (llima_lm_head_argmax_packed)."""
     x = hidden.reshape(1, -1) if hidden.dim() == 1 else hidden
     packed = isinstance(weight, PackedLmHead)
     if x.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
         raise ValueError("lm_head_argmax takes bf16 hidden states and weights")
     if logit_dtype not in ("bf16", "f32"):
         raise ValueError("logit_dtype must be 'bf16' or 'f32'")
+    if logits_out not in ("bf16", "f32"):
+        raise ValueError("logits_out must be 'bf16' or 'f32'")
+    if logits_out == "bf16" and logit_dtype != "bf16":
+        raise ValueError("bf16 logits output needs logit_dtype 'bf16'")
     x = x.contiguous()
     w = weight.data if packed else weight.contiguous()
     B, H = x.shape
@@ -582,11 +589,14 @@ def lm_head_argmax(hidden: torch.Tensor, weight, softcap: float = 0.0,
     _on_gpu(x, w)
     ids = torch.empty(B, dtype=torch.int32, device=dev)
     vals = torch.empty(B, dtype=torch.float32, device=dev)
-    logits = torch.empty((B, V), dtype=torch.float32, device=dev) if return_logits else None
+    ldt = torch.bfloat16 if logits_out == "bf16" else torch.float32
+    logits = torch.empty((B, V), dtype=ldt, device=dev) if return_logits else None
     nws = (lib().llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
            else lib().llima_lm_head_argmax_workspace_bytes(B, V))
     ws = Workspace.get(dev, "lm_head", nws)
     ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
+    if logits_out == "bf16":
+        ld |= _lib.LLIMA_LOGITS_OUT_BF16
     fn = lib().llima_lm_head_argmax_packed if packed else lib().llima_lm_head_argmax
     check(fn(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap), ld, ids.data_ptr(),
              vals.data_ptr(), _ptr(logits), ws.data_ptr(), ws.numel(), _stream(dev)),

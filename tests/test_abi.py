@@ -106,6 +106,11 @@ def test_host_only_entry_points():
     assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, float("nan"), 1, p, None, None, p, wl,
                                   None) == -1
     assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 7, p, None, None, p, wl, None) == -1
+    # bf16 logits output only with bf16 logits
+    assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 0x100, p, None, None, p, wl, None) == -1
+    assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 0x300, p, None, None, p, wl, None) == -1
+    assert L.llima_lm_head_argmax(None, p, 0, 16, 1000, 0.0, 0x101, None, None, None, None, 0,
+                                  None) == 0
     assert L.llima_lm_head_argmax(p, p, 1, 16, 1000, 0.0, 1, p, None, None, p, 0, None) == -4
     # packed LM head: H a multiple of 256 (at most 65536), the packed size as stated
     assert L.llima_lm_head_packed_bytes(1000, 100) == 0

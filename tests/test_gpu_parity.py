@@ -1176,33 +1176,68 @@ def test_lm_head_packed_ties_and_nan(gpu):
     _lm_head_check(ids[:2], vals[:2], logits[:2], x[:2], w, 0.0)
 
 
-@pytest.mark.parametrize("ld", ["bf16", "f32"])
-def test_lm_head_then_sample(gpu, oracle, ld):
+@pytest.mark.parametrize("ld,out", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16")])
+def test_lm_head_then_sample(gpu, oracle, ld, out):
     """A sampled decode step: the LM head's logits stay in device memory and feed
-    llima_sample directly; ids, probabilities and kept sets equal the oracle's
-    on the same logits (copied to the host), and the greedy sampler's ids equal
-    the LM head's fused argmax."""
+    llima_sample directly (fp32, or bf16 with half the bytes); ids,
+    probabilities and kept sets equal the oracle's on the same logits (copied
+    to the host), and the greedy sampler's ids equal the LM head's fused
+    argmax."""
+    import torch
     import llima_amd
     from oracle.oracle import SamplerConfig as OC
-    _say("lm head -> sample", ld)
+    _say("lm head -> sample", ld, out)
     rng = np.random.default_rng(31)
     B, H, V = 8, 1024, 50000
     x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
     w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
     ids_f, _, logits = llima_amd.lm_head_argmax(_t(x, gpu), _t(w, gpu), softcap=30.0,
-                                                return_logits=True, logit_dtype=ld)
+                                                return_logits=True, logit_dtype=ld, logits_out=out)
     hist = rng.integers(0, V, size=(B, 256)).astype(np.int32)
     u = rng.random(B).astype(np.float32)
     cfgd = dict(temperature=0.8, top_k=50, top_p=0.95, min_p=0.05, repetition_penalty=1.15,
                 presence_penalty=0.5, frequency_penalty=0.3)
     ids, probs, keep = llima_amd.sample(logits, _t(u, gpu), llima_amd.SamplerConfig(**cfgd),
                                         history=_t(hist, gpu), return_keep=True)
-    eids, eprobs, ekeep = oracle.sample(_np(logits), u, OC(**cfgd), history=hist, want_keep=True)
+    host = _np(logits.view(torch.int16)).view(np.uint16) if out == "bf16" else _np(logits)
+    eids, eprobs, ekeep = oracle.sample(host, u, OC(**cfgd), history=hist, want_keep=True)
     assert (_np(ids) == eids).all()
     assert (_np(probs).view(np.uint32) == eprobs.view(np.uint32)).all()
     assert (_np(keep).view(np.uint32) == ekeep).all()
     gids, _ = llima_amd.sample(logits, _t(u, gpu), llima_amd.SamplerConfig(greedy=True))
     assert (_np(gids) == _np(ids_f)).all()
+
+
+@pytest.mark.parametrize("B,H,V,packed", [(2, 4096, 50000, False), (20, 1024, 30000, False),
+                                           (40, 512, 20000, True), (3, 256, 777, True)])
+def test_lm_head_bf16_logits_out(gpu, B, H, V, packed):
+    """bf16 logits output (LLIMA_LOGITS_OUT_BF16) on the matrix-vector path,
+    the MFMA tiles and the packed weight: every logit is the upper half of
+    the fp32 output of the same bf16-rounded logits (NaN as a NaN), and the
+    ids and values are unchanged."""
+    import torch
+    import llima_amd
+    _say("lm head bf16 logits out", B, H, V, packed)
+    rng = np.random.default_rng(B + H + V)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    wf = rng.normal(0, 3.0 / np.sqrt(H), (V, H)).astype(np.float32)
+    wf[5, 0] = np.nan                                           # a NaN logit in every row
+    w = _t(wl.f32_to_bf16_bits(wf), gpu)
+    wt = llima_amd.lm_head_pack(w) if packed else w
+    i32, v32, l32 = llima_amd.lm_head_argmax(_t(x, gpu), wt, softcap=30.0, return_logits=True)
+    i16, v16, l16 = llima_amd.lm_head_argmax(_t(x, gpu), wt, softcap=30.0, return_logits=True,
+                                             logits_out="bf16")
+    assert l16.dtype == torch.bfloat16
+    a = _np(l32).view(np.uint32)
+    b = _np(l16.view(torch.int16)).view(np.uint16).astype(np.uint32)
+    nan = np.isnan(_np(l32))
+    assert (b[~nan] == (a[~nan] >> 16)).all()
+    assert np.isnan(wl.bf16_bits_to_f32(b[nan].astype(np.uint16))).all() and nan[:, 5].all()
+    assert (_np(i16) == _np(i32)).all()
+    assert (_np(v16).view(np.uint32) == _np(v32).view(np.uint32)).all()
+    with pytest.raises(ValueError):
+        llima_amd.lm_head_argmax(_t(x, gpu), wt, return_logits=True, logit_dtype="f32",
+                                 logits_out="bf16")
 
 
 def test_lm_head_argmax_ties_and_nan(gpu):
