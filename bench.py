@@ -12,7 +12,7 @@ timed region starts.
 Prints ONE JSON line.  value = sampled rows/s (whole job), ms_per_step from a
 HIP-graph replay of K steps bracketed by synchronisation and timed with HIP
 events on the launch stream.  One step is one entry-point call (for the sampler
-its two kernels, sweep and finish), so roofline.achieved = algorithmic bytes per
+its kernels: sweep and finish, or the dense path's five), so roofline.achieved = algorithmic bytes per
 step / ms_per_step; eager_call_us is the mean of per-call HIP events without the
 graph (host launch gaps included).  roofline.traffic = HBM bytes per step from
 the committed rocprofv3 counter runs (profiles/traffic.json), when measured for
@@ -22,8 +22,10 @@ slice of the vocabulary, scaled to the whole).
 
 --workload selects the other configurations: single_row, constrained,
 large_vocab_bf16(_greedy), argmax_bf16, speculative, score_bf16,
-mtp_masked_argmax, and lm_head_argmax / lm_head_argmax_b64 (the LM head with
-its argmax at B = 1 and B = 64).
+mtp_masked_argmax, top_p_only (the default rows with top-p alone: the
+sampler's dense path, five kernels), and lm_head_argmax /
+lm_head_argmax_b64/b128/b256 (the LM head with its argmax at B = 1 to 256)
+and lm_head_argmax_b32/b64/b128_packed (over a weight packed at load time).
 """
 from __future__ import annotations
 
