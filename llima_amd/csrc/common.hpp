@@ -78,12 +78,6 @@ __device__ __forceinline__ uint64_t f32_integral_to_u64(float f) {
     return u ? r : 0ull;
 }
 
-__device__ __forceinline__ uint64_t weight(float x, float xmax) {
-    const float d = x - xmax;
-    const uint64_t w = f32_integral_to_u64(__builtin_rintf(__builtin_ldexpf(exp_neg(d), 36)));
-    return x == xmax ? LLIMA_W_ONE : (d >= -26.0f ? w : 0ull);
-}
-
 // weight(x, xmax) for a finite xmax, as the integral float it converts
 // (W < 2^37, exact in fp32; sums of at most 2^16 of them are exact in double).
 // exp_neg's steps with three folds that leave every result unchanged:
@@ -114,6 +108,21 @@ __device__ __forceinline__ float weight_fd(float d0) {   // d0 = x - xmax
     return __builtin_rintf(__builtin_ldexpf(p, (int)n));
 }
 __device__ __forceinline__ float weight_f(float x, float xmax) { return weight_fd(x - xmax); }
+
+// An integral float below 2^52 as uint64 without branches: the part from 2^32
+// up and the rest are each exact (a float's significand has 24 bits).
+__device__ __forceinline__ uint64_t wf_u64(float wf) {
+    const float hi = __builtin_truncf(wf * 2.3283064365386963e-10f);
+    const uint32_t lo = (uint32_t)__builtin_fmaf(hi, -4294967296.0f, wf);
+    return ((uint64_t)(uint32_t)hi << 32) | lo;
+}
+
+// The weight W = rint(exp(x - xmax) 2^36) of x <= xmax (LLIMA_W_ONE at x ==
+// xmax, also when both are +inf; 0 below xmax - 26 and for NaN): exp_neg's
+// value through weight_fd's folds, converted without branches.
+__device__ __forceinline__ uint64_t weight(float x, float xmax) {
+    return wf_u64(weight_fd(x == xmax ? 0.0f : x - xmax));
+}
 
 // rint(v * 2^32) clamped to [0, 2^32].
 __device__ __forceinline__ uint64_t frac32(float v) {

@@ -909,14 +909,6 @@ __device__ __forceinline__ float dense_wf(float x, float xmax) {
     return weight_fd(x == xmax ? 0.0f : x - xmax);      // a select, not a branch per value
 }
 
-// An integral float below 2^52 as uint64 without branches: the part from 2^32
-// up and the rest are each exact (a float's significand has 24 bits).
-__device__ __forceinline__ uint64_t wf_u64(float wf) {
-    const float hi = __builtin_truncf(wf * 2.3283064365386963e-10f);
-    const uint32_t lo = (uint32_t)__builtin_fmaf(hi, -4294967296.0f, wf);
-    return ((uint64_t)(uint32_t)hi << 32) | lo;
-}
-
 // The min-p threshold frac32(m) 2^4 rounded up to a float: an integral float
 // weight W has W >= threshold exactly when W >= this.
 __device__ __forceinline__ float dense_mthr(const RowCfg& c) {
@@ -1745,7 +1737,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     if (xmax < __builtin_inff()) {                   // uniform; key 0 decodes to NaN, weight 0
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
-            const uint64_t wj = f32_integral_to_u64(weight_f(key_f32(key[j]), xmax));
+            const uint64_t wj = wf_u64(weight_f(key_f32(key[j]), xmax));
             w[j] = key[j] ? wj : 0ull;
         }
     } else {
