@@ -67,6 +67,7 @@ namespace llima {
 #define SMP_PBIN_SLOTS (SMP_PBINS + 64)            // + a spare bin per lane
 
 #define HF_OVERFLOW 1u
+#define SMP_PENDING ((int32_t)0x80000000)          // out_ids of a row sample_finish_wide left
 
 // Chunk region: slot 0 is the header, low 32 bits: candidates written |
 // flags << 16; high 32 bits: the bound g (float bits): every finite value >= g
@@ -112,6 +113,7 @@ struct SampleParams {
     int32_t vec_ok;
     int32_t lazy;        // penalties are applied by the finish (see llima_sample)
     int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
+    int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
 };
 
 struct RowCfg {
@@ -781,10 +783,10 @@ __device__ __forceinline__ uint32_t fin_topp_desc(const uint32_t (&key)[EPT], co
 // slots (a spare per lane), sh.lcount zero on entry.  Returns 0, with every
 // wave taking the same branch, when the maximum is infinite or the boundary
 // bin holds more than 64 values: the caller then runs fin_topp_desc.
-template <int EPT>
+template <int EPT, class SH>
 __device__ __forceinline__ uint32_t fin_topp_bins(const uint32_t (&key)[EPT], const uint64_t (&w)[EPT],
                                                   uint64_t p32, uint32_t kmax, uint64_t* bins,
-                                                  FinShared& sh) {
+                                                  SH& sh) {
     const uint32_t lane = lane_id();
     const float xmax = key_f32(kmax);
     if (!(xmax < __builtin_inff())) return 0u;      // uniform
@@ -2064,6 +2066,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     __shared__ FinShared sh;
     FIN_BEGIN();
     const int row = blockIdx.x;
+    if (P.wide && P.out_ids[row] != SMP_PENDING) return;     // uniform: finished by the wide kernel
     const RowCfg c = load_cfg(P, row);
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     const int S = P.S;
@@ -2232,6 +2235,224 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     }
     if (__builtin_expect(!done, 0)) finish_full_row<TL>(P, row, c, sh);
     FIN_MARK(13);
+}
+
+// ================================================================== wide finish
+// The rows of a grammar-masked batch without top-k hold a few thousand
+// candidates each (every allowed value within the weight window), which one
+// 256-thread workgroup per row takes through its gather path at one wave per
+// SIMD.  This kernel runs before sample_finish on such batches and takes each
+// row with 1024 threads, 4 candidates each: the gather (every candidate of the
+// row requested at once, its chunk found by a binary search over the chunk
+// offsets), keys, weights, the top-p boundary over value bins (fin_topp_bins),
+// min-p and the draw as one block scan in id order: fin_elems' steps for rows
+// without top-k.  A row it does not finish (greedy, an overflowed region,
+// more than SMP_FIN_CAP candidates, a bound the exactness check rejects, an
+// infinite maximum or a boundary bin of more than 64 values) gets out_ids =
+// SMP_PENDING, and sample_finish finishes exactly those rows.
+#define SMP_WIDE 1024
+#define SMP_WIDE_WAVES (SMP_WIDE / 64)
+#define SMP_WEPT (SMP_FIN_CAP / SMP_WIDE)          // candidates per thread
+#define SMP_WPAD 3                                 // candidate f at f + f / 8 (no bank conflicts at 4 per thread)
+
+template <int NW>
+struct BlockScratchN {
+    uint64_t w64[NW];
+    uint32_t w32[NW];
+};
+
+template <int NW>
+__device__ __forceinline__ uint64_t blk_excl_scan_u64(uint64_t v, uint64_t* total, BlockScratchN<NW>& s) {
+    const uint64_t inc = wave_incl_scan_u64(v);
+    const uint32_t w = threadIdx.x >> 6;
+    if (lane_id() == 63) s.w64[w] = inc;
+    __syncthreads();
+    uint64_t before = 0, tt = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        before += (uint32_t)i < w ? s.w64[i] : 0ull;
+        tt += s.w64[i];
+    }
+    __syncthreads();
+    *total = tt;
+    return before + inc - v;
+}
+
+struct WideShared {
+    uint64_t cand[SMP_FIN_CAP + (SMP_FIN_CAP >> SMP_WPAD)];   // candidates, then the top-p bins
+    uint32_t coff[SMP_MAX_S];                                 // chunk offsets of the candidates
+    llima_u32x4 sv[2 * SMP_SMALL + 64];                       // fin_topp_bins's boundary members
+    uint32_t lcount;
+    uint32_t r[3][SMP_WIDE_WAVES];                            // per-wave facts
+    BlockScratchN<SMP_WIDE_WAVES> bs;
+};
+static_assert(SMP_PBIN_SLOTS <= SMP_FIN_CAP, "the top-p bins reuse the candidate array");
+
+template <typename TL>
+__global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
+    constexpr int NW = SMP_WIDE_WAVES, EPT = SMP_WEPT;
+    __shared__ WideShared sh;
+    const int row = blockIdx.x;
+    const RowCfg c = load_cfg(P, row);
+    const uint32_t t = threadIdx.x;
+    const int S = P.S;
+    if (c.greedy) {                                              // uniform
+        if (t == 0) P.out_ids[row] = SMP_PENDING;
+        return;
+    }
+    // ---- chunk headers: candidate counts, overflow, the largest bound g / T
+    uint32_t cnt = 0, ovf = 0, gk = 0;
+    if ((int)t < S) {
+        const uint64_t h = *region_of(P, (uint32_t)row, t);
+        const uint32_t lo = (uint32_t)h;
+        ovf = (lo >> 16) & HF_OVERFLOW;
+        cnt = ovf ? 0u : (lo & 0xFFFFu);
+        const float g0 = __uint_as_float((uint32_t)(h >> 32));
+        const float gt0 = g0 / c.T;
+        gk = g0 > -__builtin_inff() ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
+    }
+    // one exchange: the counts' scan, any overflow, the largest bound
+    const uint32_t wv = t >> 6, lane = lane_id();
+    uint32_t NG = 0, anyov = 0, gkey = 0, off = 0;
+    {
+        const uint32_t inc = wave_incl_scan_u32(cnt), wov = wave_max_u32(ovf), wgk = wave_max_u32(gk);
+        if (lane == 63) { sh.r[0][wv] = inc; sh.r[1][wv] = wov; sh.r[2][wv] = wgk; }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            off += (uint32_t)i < wv ? sh.r[0][i] : 0u;
+            NG += sh.r[0][i];
+            anyov = sh.r[1][i] > anyov ? sh.r[1][i] : anyov;
+            gkey = sh.r[2][i] > gkey ? sh.r[2][i] : gkey;
+        }
+        off += inc - cnt;
+    }
+    if ((int)t < S) sh.coff[t] = off;
+    __syncthreads();
+    if (anyov || NG > SMP_FIN_CAP) {                             // uniform
+        if (t == 0) P.out_ids[row] = SMP_PENDING;
+        return;
+    }
+    // ---- gather: candidate f (id order) from its chunk's region, all loads first
+    const uint64_t* rbase = P.ws + (size_t)row * (uint32_t)S * SMP_REGION + SMP_HDR;
+    uint64_t q[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const uint32_t f = t + (uint32_t)k * SMP_WIDE;
+        uint32_t lo = 0, hi = (uint32_t)S;                        // the last chunk with coff <= f
+        while (hi - lo > 1u) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (sh.coff[mid] <= f) lo = mid; else hi = mid;
+        }
+        const uint32_t sl = f < NG ? f - sh.coff[lo] : 0u;
+        q[k] = rbase[(size_t)(f < NG ? lo : 0u) * SMP_REGION + sl];
+    }
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const uint32_t f = t + (uint32_t)k * SMP_WIDE;
+        if (f < NG) sh.cand[f + (f >> SMP_WPAD)] = q[k];
+    }
+    __syncthreads();
+    // ---- this thread's candidates 4t .. 4t+3, their keys of x / T
+    uint32_t key[EPT], id[EPT];
+    uint32_t kmx = 0, nf = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const uint32_t f = t * EPT + (uint32_t)j;
+        const uint32_t fc = f < NG ? f : 0u;
+        const uint64_t v = sh.cand[fc + (fc >> SMP_WPAD)];
+        const float x = f < NG ? key_f32((uint32_t)(v >> 32)) : -__builtin_inff();
+        id[j] = (uint32_t)v;
+        const uint32_t k = f32_key(c.T == 1.0f ? x : x / c.T);
+        key[j] = k > LLIMA_KEY_NEG_INF ? k : 0u;
+        kmx = key[j] > kmx ? key[j] : kmx;
+        nf += key[j] ? 1u : 0u;
+    }
+    uint32_t kmax = 0, nft = 0;
+    {
+        const uint32_t a = wave_max_u32(kmx), b = wave_sum_u32(nf);
+        if (lane == 0) { sh.r[0][wv] = a; sh.r[1][wv] = b; }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            kmax = sh.r[0][i] > kmax ? sh.r[0][i] : kmax;
+            nft += sh.r[1][i];
+        }
+    }
+    const float xmax = key_f32(kmax);
+    // rows the standard finish takes: no finite candidate with values left
+    // out, a bound above the weight window, an infinite maximum
+    bool pend = nft == 0 && gkey != 0u;
+    if (nft > 0 && gkey) {
+        const float dg = key_f32(gkey) - xmax;
+        pend = dg >= -26.0f || !zero_weight_irrelevant(P, c);
+    }
+    pend = pend || (nft > 0 && !(xmax < __builtin_inff()));
+    if (pend) {                                                  // uniform
+        if (t == 0) P.out_ids[row] = SMP_PENDING;
+        return;
+    }
+    uint64_t w[EPT];
+    uint32_t theta = 0;
+    if (nft > 0) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) w[j] = key[j] ? wf_u64(weight_f(key_f32(key[j]), xmax)) : 0ull;
+        if (c.p < 1.0f) {
+            // the candidates are in registers: the array holds the top-p bins from here
+            for (uint32_t i = t; i < SMP_PBIN_SLOTS; i += SMP_WIDE) sh.cand[i] = 0;
+            if (t == 0) sh.lcount = 0;
+            __syncthreads();
+            theta = fin_topp_bins<EPT>(key, w, frac32(c.p), kmax, sh.cand, sh);
+            if (theta == 0u) {                                   // uniform: a crowded bin
+                if (t == 0) P.out_ids[row] = SMP_PENDING;
+                return;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) w[j] = 0;
+    }
+    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0;
+    uint32_t fmask = 0;
+    uint64_t mysum = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const bool f = key[j] && key[j] >= theta && w[j] >= mthr;
+        fmask |= f ? (1u << j) : 0u;
+        w[j] = f ? w[j] : 0ull;
+        mysum += w[j];
+    }
+    // ---- the draw: a thread's candidates are consecutive ids, so one scan of
+    //      the per-thread sums orders the whole row
+    uint64_t Zf;
+    const uint64_t before = blk_excl_scan_u64<NW>(mysum, &Zf, sh.bs);
+    if (Zf == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+    } else {
+        const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
+        if (mysum > 0 && before <= target && target < before + mysum) {
+            uint64_t acc = before;
+            bool hit = false;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                if (!hit && w[j] && acc <= target && target < acc + w[j]) {
+                    write_result(P, row, (int32_t)id[j], (float)((double)w[j] / (double)Zf));
+                    hit = true;
+                }
+                acc += w[j];
+            }
+        }
+    }
+    if (P.out_keep) {
+        const int nw = (P.V + 31) >> 5;
+        uint32_t* km = P.out_keep + (size_t)row * nw;
+        for (int i = (int)t; i < nw; i += SMP_WIDE) km[i] = 0;
+        __threadfence_block();
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if ((fmask >> j) & 1u) atomicOr(&km[id[j] >> 5], 1u << (id[j] & 31u));
+    }
 }
 
 // ================================================================== dense path
@@ -3027,6 +3248,10 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
              cfg->top_k > 0 && cfg->top_k < V && cfg->repetition_penalty >= 1.0f &&
              cfg->presence_penalty >= 0.0f && cfg->frequency_penalty >= 0.0f;
     hipStream_t st = (hipStream_t)stream;
+    // Masked batches without top-k: the wide finish first (sample_finish then
+    // takes only the rows it left)
+    P.wide = bitmask && !cfg->greedy && !cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V) &&
+             P.S <= SMP_MAX_S;
     // Rows without top-k (and without a mask) take the dense path: their sweep
     // bound would admit nearly every value of ordinary logits.
     const bool dense = !bitmask && !cfg->greedy && !cfg->top_k_rows &&
@@ -3038,9 +3263,11 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
         else launch_dense<uint16_t>(P, topp, st);
     } else if (dtype == LLIMA_F32) {
         launch_sweep<float>(P, st);
+        if (P.wide) hipLaunchKernelGGL(sample_finish_wide<float>, dim3(B), dim3(SMP_WIDE), 0, st, P);
         hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
         launch_sweep<uint16_t>(P, st);
+        if (P.wide) hipLaunchKernelGGL(sample_finish_wide<uint16_t>, dim3(B), dim3(SMP_WIDE), 0, st, P);
         hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
