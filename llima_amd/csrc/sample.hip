@@ -4,8 +4,9 @@
 // Rows with top-k (or a grammar mask) take two launches per step, with no
 // atomics or fences between workgroups (a device-scope release costs an L2
 // write-back per workgroup on this part, and same-address atomics from
-// thousands of workgroups serialise); rows without top-k or mask take the
-// dense path further down (five launches, every chunk's workgroup in each):
+// thousands of workgroups serialise); masked batches without top-k add
+// sample_finish_wide between them (further down); rows without top-k or mask
+// take the dense path (five launches, every chunk's workgroup in each):
 //
 // sample_sweep: B x S workgroups; workgroup (row, chunk) owns 16 KB of one row
 //   (4096 fp32 or 8192 bf16 values).  At 5 TB/s an fp32 value arrives every
