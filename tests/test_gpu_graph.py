@@ -24,6 +24,7 @@ SAMPLE_CFGS = {
                          presence_penalty=0.3, frequency_penalty=0.2),
     "dense": dict(temperature=0.9, top_p=0.9, min_p=0.01, repetition_penalty=1.1),
     "dense_plain": dict(temperature=1.0),
+    "masked_wide": dict(temperature=1.0, top_p=0.9),          # with a sparse mask: the wide finish
 }
 
 
@@ -44,6 +45,9 @@ def test_sample_graph_replays(gpu, oracle, name):
     h = torch.empty((B, H), dtype=torch.int32, device=gpu)
     u = torch.empty(B, dtype=torch.float32, device=gpu)
     nw = (V + 31) // 32
+    masked = name == "masked_wide"
+    ms = [(rng.random((B, nw)) < 0.05).astype(np.uint32) * np.uint32(0xFFFFFFFF) for _ in range(REPLAYS)]
+    m = torch.empty((B, nw), dtype=torch.int32, device=gpu)
     ids = torch.empty(B, dtype=torch.int32, device=gpu)
     probs = torch.empty(B, dtype=torch.float32, device=gpu)
     keep = torch.empty((B, nw), dtype=torch.int32, device=gpu)
@@ -52,15 +56,17 @@ def test_sample_graph_replays(gpu, oracle, name):
     cfg, keep_alive = SamplerConfig(**cfgd).to_c(B, gpu)
 
     def launch(stream):
-        rc = L.llima_sample(x.data_ptr(), _lib.LLIMA_F32, B, V, V, h.data_ptr(), None, H, None,
-                            u.data_ptr(), ctypes.byref(cfg), ids.data_ptr(), probs.data_ptr(),
-                            keep.data_ptr(), ws.data_ptr(), nws, stream)
+        rc = L.llima_sample(x.data_ptr(), _lib.LLIMA_F32, B, V, V, h.data_ptr(), None, H,
+                            m.data_ptr() if masked else None, u.data_ptr(), ctypes.byref(cfg),
+                            ids.data_ptr(), probs.data_ptr(), keep.data_ptr(), ws.data_ptr(), nws,
+                            stream)
         assert rc == 0
 
     def load(i):
         x.copy_(torch.from_numpy(xs[i]))
         h.copy_(torch.from_numpy(hs[i]))
         u.copy_(torch.from_numpy(us[i]))
+        m.copy_(torch.from_numpy(ms[i].view(np.int32)))
 
     load(0)
     launch(torch.cuda.current_stream(gpu).cuda_stream)        # eager warmup
@@ -77,7 +83,8 @@ def test_sample_graph_replays(gpu, oracle, name):
         torch.cuda.synchronize(gpu)
         graph.replay()
         torch.cuda.synchronize(gpu)
-        eids, eprobs, ekeep = oracle.sample(xs[i], us[i], OC(**cfgd), history=hs[i], want_keep=True)
+        eids, eprobs, ekeep = oracle.sample(xs[i], us[i], OC(**cfgd), history=hs[i],
+                                            bitmask=ms[i] if masked else None, want_keep=True)
         gi = ids.cpu().numpy()
         assert (gi == eids).all(), (name, i, np.flatnonzero(gi != eids)[:8])
         assert (probs.cpu().numpy().view(np.uint32) == eprobs.view(np.uint32)).all(), (name, i)
