@@ -25,7 +25,9 @@ large_vocab_bf16(_greedy), argmax_bf16, speculative, score_bf16,
 mtp_masked_argmax, top_p_only (the default rows with top-p alone: the
 sampler's dense path, five kernels), and lm_head_argmax /
 lm_head_argmax_b64/b128/b256 (the LM head with its argmax at B = 1 to 256)
-and lm_head_argmax_b32/b64/b128_packed (over a weight packed at load time).
+and lm_head_argmax_b32/b64/b128_packed (over a weight packed at load time);
+lm_head_score_b64_packed: the packed LM head with its scoring epilogue (the
+log-softmax at 64 target ids, no logits written).
 """
 from __future__ import annotations
 
@@ -53,7 +55,8 @@ def parse():
                              "speculative", "score_bf16", "mtp_masked_argmax",
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
                              "lm_head_argmax_b256", "lm_head_argmax_b32_packed",
-                             "lm_head_argmax_b64_packed", "lm_head_argmax_b128_packed"])
+                             "lm_head_argmax_b64_packed", "lm_head_argmax_b128_packed",
+                             "lm_head_score_b64_packed"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -89,8 +92,9 @@ def main():
 
     launches = []          # one callable per rotated input, taking a stream pointer
     data_note = None
-    if name.startswith("lm_head_argmax"):
+    if name.startswith("lm_head_"):
         B, H, V = w["B"], w["H"], w["V"]
+        scoring = name.startswith("lm_head_score")
         g = torch.Generator(device=dev)
         g.manual_seed(w["seed"])
         weight = (torch.randn((V, H), generator=g, device=dev) * (1.0 / H ** 0.5)).to(torch.bfloat16)
@@ -99,8 +103,12 @@ def main():
         ids_o = torch.empty(B, dtype=torch.int32, device=dev)
         vals_o = torch.empty(B, dtype=torch.float32, device=dev)
         packed = name.endswith("_packed")
-        nws = (L.llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
-               else L.llima_lm_head_argmax_workspace_bytes(B, V))
+        if scoring:
+            nws = (L.llima_lm_head_score_packed_workspace_bytes(B, H, V) if packed
+                   else L.llima_lm_head_score_workspace_bytes(B, V))
+        else:
+            nws = (L.llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
+                   else L.llima_lm_head_argmax_workspace_bytes(B, V))
         ws = torch.zeros(nws, dtype=torch.uint8, device=dev)
         if packed:       # the load-time layout, built once before any timing
             wp = torch.empty(L.llima_lm_head_packed_bytes(V, H), dtype=torch.uint8, device=dev)
@@ -109,18 +117,32 @@ def main():
             torch.cuda.synchronize()
             del weight
             weight = wp
-        fn = L.llima_lm_head_argmax_packed if packed else L.llima_lm_head_argmax
-        for x in hid:
-            launches.append(lambda sp, x=x: check(fn(
-                x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, ids_o.data_ptr(),
-                vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
+        if scoring:
+            fn = L.llima_lm_head_score_packed if packed else L.llima_lm_head_score
+            tgs = [torch.randint(0, V, (B,), generator=g, device=dev, dtype=torch.int32)
+                   for _ in hid]
+            lp_o = torch.empty(B, dtype=torch.float64, device=dev)
+            for x, tg in zip(hid, tgs):
+                launches.append(lambda sp, x=x, tg=tg: check(fn(
+                    x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, tg.data_ptr(),
+                    lp_o.data_ptr(), ids_o.data_ptr(), ws.data_ptr(), nws, sp),
+                    "llima_lm_head_score"))
+        else:
+            fn = L.llima_lm_head_argmax_packed if packed else L.llima_lm_head_argmax
+            for x in hid:
+                launches.append(lambda sp, x=x: check(fn(
+                    x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, ids_o.data_ptr(),
+                    vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
         per = V * H * 2
-        alg_bytes = V * H * 2 + B * H * 2 + B * 8
+        # weight, hidden rows, then the argmax's ids and values or the
+        # targets, log-probabilities and flags
+        alg_bytes = V * H * 2 + B * H * 2 + (B * 16 if scoring else B * 8)
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16"
-        kernel_names = (["lmh_packed", "lmh_finish"] if packed else
-                        ["lmh_mfma" if B > 4 else "lmh_rows", "lmh_finish"])
+        fin = "lmh_score_finish" if scoring else "lmh_finish"
+        kernel_names = (["lmh_packed", fin] if packed else
+                        ["lmh_mfma" if B > 4 else "lmh_rows", fin])
         config = {"workload": name, "B": B, "H": H, "V": V,
                   "weight": "bf16 [V, H] packed at load time" if packed else "bf16 [V, H]"}
         data_note = ("synthetic (seeded; one bf16 [%d, %d] weight, %.2f GiB, above the 256 MB "
@@ -404,7 +426,7 @@ def cpu_baseline(name, w, seconds, greedy_variant):
 
     info = {"kind": "port", "cpu": _cpu_model(), "nproc": nproc,
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
-    if name.startswith("lm_head_argmax"):
+    if name.startswith("lm_head_"):
         # numpy float32 matrix-vector products + argmax over a 16384-row slice
         # of a weight of the same shape, scaled to the full vocabulary
         rng = np.random.default_rng(w["seed"])
@@ -413,15 +435,22 @@ def cpu_baseline(name, w, seconds, greedy_variant):
         xs = np.ascontiguousarray(w["hidden"].astype(np.uint32) << 16).view(np.float32)
         t0 = time.time()
         reps = 0
+        scoring = name.startswith("lm_head_score")
         while time.time() < t0 + seconds or reps == 0:
-            np.argmax(xs @ wt.T, axis=1)
+            lg = xs @ wt.T
+            if scoring:                                      # the log-sum-exp of each row
+                m = lg.max(axis=1, keepdims=True)
+                np.log(np.exp(lg - m).sum(axis=1))
+            else:
+                np.argmax(lg, axis=1)
             reps += 1
         dt = time.time() - t0
         full = dt * (w["V"] / nv) / reps                     # seconds per full-vocabulary call
         info.update({"value": w["B"] / full, "unit": "rows/s", "cores": many,
-                     "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + argmax (a %d-row slice "
+                     "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + %s (a %d-row slice "
                                "of the vocabulary, scaled by V / %d), %.1f s" % (
-                                   reps, w["B"], w["H"], nv, w["H"], nv, nv, dt)})
+                                   reps, w["B"], w["H"], nv, w["H"],
+                                   "log-sum-exp" if scoring else "argmax", nv, nv, dt)})
         return info
     if name == "speculative":
         unit = "sequences/s"

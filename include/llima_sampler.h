@@ -63,6 +63,8 @@
  *                            int32 the host reads at language_model.cpp:1607-1609
  *   llima_lm_head_pack, llima_lm_head_argmax_packed <- the same, over a weight
  *                            prepacked at load time (no counterpart)
+ *   llima_lm_head_score(_packed) <- the LM head followed by score_logits
+ *                            (language_model.cpp:29-62), the logits never written
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -323,6 +325,34 @@ int llima_lm_head_argmax_packed(const void* hidden, const void* packed, int32_t 
                                 int32_t V, float softcap, int32_t logit_dtype, int32_t* out_ids,
                                 float* out_vals, float* out_logits, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/* LM head with a fused scoring epilogue: the log-likelihood of B target
+ * tokens under the LM head's logits, as llima_lm_head_argmax computes them
+ * (same softcap, logit_dtype LLIMA_BF16 or LLIMA_F32 rounding, same kernels),
+ * without writing or reading the [B][V] logits: the head's epilogue keeps,
+ * per wave and hidden row, its maximum and sum of exp(logit - maximum) beside
+ * the argmax key, and a per-row finish combines them in double.  Replaces the
+ * LM head followed by score_logits (sima_lmm/devkit/cpp/language_model.cpp:29-62;
+ * the reference scores the logits its graph wrote,
+ * sima_lmm/model/language_part_base.py:157-180).  targets [B] int32 (device);
+ * out_logprob [B] and out_is_greedy [B] as llima_score_logits (NaN with a NaN
+ * logit or an infinite maximum; LLIMA_E_RANGE and NaN for a target outside
+ * [0, V)).  The log-probability agrees with llima_score_logits over the same
+ * logits to about 1e-6 (fp32 exp terms, double combination); the flag is
+ * exact.  LLIMA_LOGITS_OUT_BF16 is rejected (no logits output).  Sizes,
+ * alignment and the _packed form (a weight from llima_lm_head_pack) as the
+ * argmax entry points. */
+size_t llima_lm_head_score_workspace_bytes(int32_t B, int32_t V);
+int llima_lm_head_score(const void* hidden, const void* weight, int32_t B, int32_t H, int32_t V,
+                        float softcap, int32_t logit_dtype, const int32_t* targets,
+                        double* out_logprob, int32_t* out_is_greedy, void* workspace,
+                        size_t workspace_bytes, void* stream);
+size_t llima_lm_head_score_packed_workspace_bytes(int32_t B, int32_t H, int32_t V);
+int llima_lm_head_score_packed(const void* hidden, const void* packed, int32_t B, int32_t H,
+                               int32_t V, float softcap, int32_t logit_dtype,
+                               const int32_t* targets, double* out_logprob,
+                               int32_t* out_is_greedy, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
  * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):

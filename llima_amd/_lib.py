@@ -58,6 +58,12 @@ SIGNATURES = {
     "llima_lm_head_pack": (ctypes.c_int, [_vp, _i32, _i32, _vp, _sz, _vp]),
     "llima_lm_head_argmax_packed": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _i32,
                                                    _vp, _vp, _vp, _vp, _sz, _vp]),
+    "llima_lm_head_score_workspace_bytes": (_sz, [_i32, _i32]),
+    "llima_lm_head_score": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float, _i32, _vp,
+                                           _vp, _vp, _vp, _sz, _vp]),
+    "llima_lm_head_score_packed_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "llima_lm_head_score_packed": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float,
+                                                  _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "llima_topk": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _i32, _vp, _vp, _vp]),
     "llima_eagle3_tree_bytes": (_sz, [_i32, _i32]),
     "llima_eagle3_tree_begin": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp,

@@ -302,6 +302,27 @@ struct BlockScratch {
     uint32_t bcast32;
 };
 
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    return __longlong_as_double((long long)wave_reduce<uint64_t>(
+        (uint64_t)__double_as_longlong(v), 0ull, [](uint64_t a, uint64_t b) {
+            return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) +
+                                                  __longlong_as_double((long long)b));
+        }));
+}
+
+// Sum over the workgroup in double (the waves' sums added in wave order).
+__device__ __forceinline__ double block_sum_f64(double v, BlockScratch& s) {
+    v = wave_sum_f64(v);
+    const uint32_t w = threadIdx.x >> 6;
+    if (lane_id() == 0) s.w64[w] = (uint64_t)__double_as_longlong(v);
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < LLIMA_WAVES; ++i) t += __longlong_as_double((long long)s.w64[i]);
+    __syncthreads();
+    return t;
+}
+
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, BlockScratch& s) {
     v = wave_sum_u64(v);
     const uint32_t w = threadIdx.x >> 6;

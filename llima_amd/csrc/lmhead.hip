@@ -23,6 +23,15 @@
 // writes the logits, and keeps per hidden row the 64-bit key
 // (value key << 32 | ~v) of its best vocab row.  lmh_finish: one workgroup per
 // hidden row reduces the waves' keys.
+//
+// Scoring epilogue (every path, a compile-time flag): beside its key, each key
+// slot (a wave's vocab rows of one hidden row) keeps s_w = sum of
+// exp(logit - m_w) over its logits, m_w its greatest non-NaN logit (the key's
+// value), and the wave holding the target id stores the target's logit;
+// lmh_score_finish combines the slots in double into the log-softmax at the
+// target and the first-maximum flag of score_logits
+// (sima_lmm/devkit/cpp/language_model.cpp:29-62) over the logits as the
+// argmax sees them, so scoring never writes or reads the [B][V] logits.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
@@ -45,6 +54,12 @@ struct LmhParams {
     float cap;
     int32_t round_bf16;                // logits rounded to bf16 before the argmax
     int32_t logits_bf16;               // out_logits holds bf16 [B][V] (LLIMA_LOGITS_OUT_BF16)
+    // scoring epilogue
+    float* sums;                       // [B][NW] s_w of each key slot (NaN: a NaN logit)
+    float* tval;                       // [B] the target's logit
+    const int32_t* targets;            // [B]
+    double* out_logprob;               // [B]
+    int32_t* out_greedy;               // [B]
 };
 
 // The logit as the argmax sees it: softcapped, then (round_bf16) rounded to
@@ -69,6 +84,30 @@ __device__ __forceinline__ void lmh_store_logit(const LmhParams& P, size_t i, fl
         P.out_logits[i] = v;
 }
 
+#define LMH_LOG2E 1.44269504088896340736f
+
+// Scoring statistics of one key slot, one logit at a time: m the greatest
+// non-NaN logit so far, s the sum of exp(v - m) over its logits above -inf
+// (rescaled when m grows).  A NaN logit makes s NaN for good (s * 0 keeps it),
+// and so does a second +inf: the row's result is NaN either way.
+__device__ __forceinline__ void lmh_stat_push(float& m, float& s, float v) {
+    if (v != v) {
+        s = __builtin_nanf("");
+    } else if (v > m) {
+        s = s * (m > -__builtin_inff() ? __builtin_amdgcn_exp2f((m - v) * LMH_LOG2E) : 0.0f) + 1.0f;
+        m = v;
+    } else if (v > -__builtin_inff()) {
+        s += __builtin_amdgcn_exp2f((v - m) * LMH_LOG2E);
+    }
+}
+
+// One logit's term of its key slot's sum, mw the slot's greatest non-NaN logit:
+// exp(v - mw); 0 past the vocabulary (in false) and for -inf, NaN for NaN.
+__device__ __forceinline__ float lmh_term(float v, float mw, bool in) {
+    const float e = v > -__builtin_inff() ? __builtin_amdgcn_exp2f((v - mw) * LMH_LOG2E) : 0.0f;
+    return !in ? 0.0f : v != v ? __builtin_nanf("") : e;
+}
+
 __device__ __forceinline__ float wave_sum_f32(float v) {
     return __uint_as_float(wave_reduce<uint32_t>(
         __float_as_uint(v), 0u,
@@ -87,7 +126,7 @@ __device__ __forceinline__ void issue_row(const LmhParams& P, int v, llima_u32x4
     }
 }
 
-template <int NB>
+template <int NB, bool SC>
 __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) {
     __shared__ __align__(16) float xs[LMH_LDS_FLOATS];
     const int H = P.H;
@@ -107,8 +146,15 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
     const uint32_t lane = lane_id();
     const int wg = (int)blockIdx.x * LMH_WAVES + (int)(threadIdx.x >> 6);
     uint64_t best[NB];
+    float sm[NB], ss[NB];                                    // scoring: m and s of this slot
+    int32_t tg[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) best[b] = 0;
+    for (int b = 0; b < NB; ++b) {
+        best[b] = 0;
+        sm[b] = -__builtin_inff();
+        ss[b] = 0.0f;
+        tg[b] = SC && b < nb ? P.targets[b0 + b] : -1;
+    }
     llima_u32x4 wc[LMH_R], wn[LMH_R];
     int v = wg;
     issue_row(P, v < P.V ? v : -1, wc);
@@ -148,6 +194,10 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
             if (b < nb && P.out_logits && lane == 0) lmh_store_logit(P, (size_t)(b0 + b) * P.V + v, s);
             const uint64_t key = s == s ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)v : 0ull;
             best[b] = key > best[b] ? key : best[b];
+            if constexpr (SC) {
+                lmh_stat_push(sm[b], ss[b], s);
+                if (lane == 0 && b < nb && v == tg[b]) P.tval[b0 + b] = s;
+            }
         }
 #pragma unroll
         for (int j = 0; j < LMH_R; ++j) wc[j] = wn[j];
@@ -156,7 +206,10 @@ __global__ __launch_bounds__(LMH_WG) void lmh_rows(LmhParams P, int b0, int nb) 
     if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-            if (b < nb) P.keys[(size_t)(b0 + b) * P.NW + wg] = best[b];
+            if (b < nb) {
+                P.keys[(size_t)(b0 + b) * P.NW + wg] = best[b];
+                if constexpr (SC) P.sums[(size_t)(b0 + b) * P.NW + wg] = ss[b];
+            }
     }
 }
 
@@ -175,6 +228,13 @@ typedef float lmh_acc __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ uint64_t lmh_key(float s, int n, int V) {
     return s == s && n < V ? ((uint64_t)f32_key(s) << 32) | (uint32_t)~(uint32_t)n : 0ull;
+}
+
+// Sum over the 32 lanes of this lane's half-wave.
+__device__ __forceinline__ float half_sum_f32(float v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
 }
 
 // Greatest 64-bit value over the 32 lanes of this lane's half-wave.
@@ -200,7 +260,7 @@ __device__ __forceinline__ uint64_t half_max_u64(uint64_t v) {
 // iterations before it is staged.
 #define LMH_KC 64                      // the H multiple the MFMA path needs
 
-template <int NWN, int WM, int R, int KC>
+template <int NWN, int WM, int R, int KC, bool SC>
 __global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, int nb) {
     constexpr int NT = 64 * NWN * WM;                        // threads
     constexpr int WR = 32 * NWN;                             // vocab rows of the workgroup
@@ -288,12 +348,24 @@ __global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, i
     // to 4 of the P.NW slots, counted in 256-row tiles): no logit
     if (blockIdx.x == gridDim.x - 1) {
         const int w0 = (int)gridDim.x * NWN, nx = P.NW - w0;
-        for (int e = t; e < nx * nb; e += NT)
+        for (int e = t; e < nx * nb; e += NT) {
             P.keys[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0;
+            if constexpr (SC) P.sums[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0.0f;
+        }
     }
     // epilogue: softcap, logits, and per hidden row the greatest key of the wave's 32 columns
     const int wv = (int)blockIdx.x * NWN + wn;
     const int n = n0 + wn * 32 + r;
+    int32_t tgv[2][16];                                      // scoring: the lane's rows' targets,
+    if constexpr (SC) {                                      // requested together (-1: no row)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = wm * 64 + mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
+                tgv[mt][i] = m < nb ? P.targets[b0 + m] : -1;
+            }
+    }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -303,6 +375,12 @@ __global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, i
             if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
             const uint64_t best = half_max_u64(lmh_key(v, n, V));
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
+            if constexpr (SC) {
+                const float mw = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
+                const float sw = half_sum_f32(lmh_term(v, mw, n < V));
+                if (r == 0 && m < nb) P.sums[(size_t)(b0 + m) * P.NW + wv] = sw;
+                if (n < V && n == tgv[mt][i]) P.tval[b0 + m] = v;
+            }
         }
     }
 }
@@ -335,6 +413,70 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_finish(LmhParams P) {
     }
 }
 
+// One workgroup per hidden row of a scoring call: the first maximum M (the
+// greatest key), S = sum over the key slots of exp(m_w - M) s_w in double, and
+// the target's log-probability x_t - (M + log S): NaN when a logit is NaN or M
+// is infinite (as the reference's double sum), a NaN and LLIMA_E_RANGE for a
+// target outside [0, V).  The flag is 1 when the target is the first maximum
+// (a row with no non-NaN logit has maximum id 0).  Slots are read 16 per
+// thread at a time (maximum, then sum; rows of at most 16 slots per thread
+// stay in registers between the two).
+__global__ __launch_bounds__(LLIMA_WG) void lmh_score_finish(LmhParams P) {
+    constexpr int SPAN = LLIMA_WG * 16;
+    __shared__ BlockScratch bs;
+    const int b = (int)blockIdx.x, t = (int)threadIdx.x;
+    const uint64_t* k = P.keys + (size_t)b * P.NW;
+    const float* sm = P.sums + (size_t)b * P.NW;
+    uint64_t kv[16];
+    float sv[16];
+    auto load = [&](int i0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = i0 + j * LLIMA_WG + t, ic = i < P.NW ? i : 0;
+            kv[j] = k[ic];
+            sv[j] = sm[ic];
+        }
+    };
+    uint64_t best = 0;
+    uint32_t nan = 0;
+    for (int i0 = 0; i0 < P.NW; i0 += SPAN) {
+        load(i0);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool in = i0 + j * LLIMA_WG + t < P.NW;
+            best = in && kv[j] > best ? kv[j] : best;
+            nan |= in && sv[j] != sv[j] ? 1u : 0u;
+        }
+    }
+    best = block_max_u64(best, bs);
+    nan = block_max_u32(nan, bs);
+    const float M = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
+    const bool finite = M > -__builtin_inff() && M < __builtin_inff();
+    double S = 0.0;
+    if (finite && !nan) {                                    // uniform
+        for (int i0 = 0; i0 < P.NW; i0 += SPAN) {
+            if (P.NW > SPAN) load(i0);                       // one span: still in registers
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const bool in = i0 + j * LLIMA_WG + t < P.NW;
+                const float mc = kv[j] ? key_f32((uint32_t)(kv[j] >> 32)) : -__builtin_inff();
+                if (in && mc > -__builtin_inff()) S += exp((double)mc - (double)M) * (double)sv[j];
+            }
+        }
+    }
+    S = block_sum_f64(S, bs);
+    if (t != 0) return;
+    const int32_t tg = P.targets[b];
+    if (tg < 0 || tg >= P.V) {
+        P.out_logprob[b] = __builtin_nan("");
+        P.out_greedy[b] = LLIMA_E_RANGE;
+        return;
+    }
+    const uint32_t am = best ? ~(uint32_t)best : 0u;
+    P.out_logprob[b] = (nan || !finite) ? __builtin_nan("") : (double)P.tval[b] - ((double)M + log(S));
+    P.out_greedy[b] = am == (uint32_t)tg ? 1 : 0;
+}
+
 // ------------------------------------------------------------------ packed weights
 // A weight prepacked once (at model load) in the order the MFMA reads it:
 // fragment (rb, s) is 1 KB, lane l's 16 bytes being
@@ -364,7 +506,7 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_finish(LmhParams P) {
 #define LMP_MB 64                      // hidden rows per pass
 #define LMP_HM 256                     // the H multiple of the packed layout
 
-template <int NMT, int WR, int R, int KR>
+template <int NMT, int WR, int R, int KR, bool SC>
 __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t* packed, int b0,
                                                      int nb) {
     constexpr int SPR = KR / 16;                             // k-steps per range
@@ -447,17 +589,30 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
     // than another uses fewer of the P.NW slots): no logit, spread over the grid
     {
         const int w0 = (int)gridDim.x * LMP_WAVES, nx = P.NW - w0;
-        for (int e = (int)blockIdx.x * LMP_WG + t; e < nx * nb; e += (int)gridDim.x * LMP_WG)
+        for (int e = (int)blockIdx.x * LMP_WG + t; e < nx * nb; e += (int)gridDim.x * LMP_WG) {
             P.keys[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0;
+            if constexpr (SC) P.sums[(size_t)(b0 + e / nx) * P.NW + w0 + e % nx] = 0.0f;
+        }
     }
     // epilogue: softcap, logits, per hidden row the greatest key of the wave's
     // 32 WR vocab rows
+    int32_t tgv[NMT][16];                                    // scoring: the lane's rows' targets,
+    if constexpr (SC) {                                      // requested together (-1: no row)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
+                tgv[mt][i] = m < nb ? P.targets[b0 + m] : -1;
+            }
+    }
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
             uint64_t key = 0;
+            float vj[WR];
 #pragma unroll
             for (int j = 0; j < WR; ++j) {
                 const int n = 32 * (rb0 + j) + r;            // >= V for a spare row block
@@ -465,9 +620,23 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
                 if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
                 const uint64_t k = lmh_key(v, n, V);
                 key = k > key ? k : key;
+                vj[j] = v;
             }
             const uint64_t best = half_max_u64(key);
             if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
+            if constexpr (SC) {
+                const float mw = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
+                const int32_t tg = tgv[mt][i];
+                float e = 0.0f;
+#pragma unroll
+                for (int j = 0; j < WR; ++j) {
+                    const int n = 32 * (rb0 + j) + r;
+                    e += lmh_term(vj[j], mw, n < V);
+                    if (n < V && n == tg) P.tval[b0 + m] = vj[j];
+                }
+                const float sw = half_sum_f32(e);
+                if (r == 0 && m < nb) P.sums[(size_t)(b0 + m) * P.NW + wv] = sw;
+            }
         }
     }
 }
@@ -515,25 +684,98 @@ static int lmh_mfma_waves(int V) {
     return (V + 255) / 256 * 8;
 }
 
+static int lmh_plain_slots(int V) {
+    return lmh_waves(V) > lmh_mfma_waves(V) ? lmh_waves(V) : lmh_mfma_waves(V);
+}
+
+// Workspace of B rows with nw key slots each: the keys, then (scoring) the
+// slots' sums and the targets' logits.
+static size_t lmh_ws_bytes(int32_t B, int nw, bool sc) {
+    const size_t keys = lmh_align256((size_t)B * nw * sizeof(uint64_t));
+    return sc ? keys + lmh_align256((size_t)B * nw * sizeof(float)) + lmh_align256((size_t)B * sizeof(float))
+              : keys;
+}
+
+static void lmh_ws_split(LmhParams& P, void* workspace, int nw) {
+    uint8_t* w = (uint8_t*)workspace;
+    P.keys = (uint64_t*)w;
+    w += lmh_align256((size_t)P.B * nw * sizeof(uint64_t));
+    P.sums = (float*)w;
+    w += lmh_align256((size_t)P.B * nw * sizeof(float));
+    P.tval = (float*)w;
+}
+
+// The softcap and logit dtype checks shared by the entry points; clears
+// LLIMA_LOGITS_OUT_BF16 from *logit_dtype into *out_bf16.
+static int lmh_check_dtype(float softcap, int32_t* logit_dtype, int32_t* out_bf16) {
+    if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
+    *out_bf16 = (*logit_dtype & LLIMA_LOGITS_OUT_BF16) != 0;
+    *logit_dtype &= ~LLIMA_LOGITS_OUT_BF16;
+    if (*logit_dtype != LLIMA_F32 && *logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
+    if (*out_bf16 && *logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;   // bf16 output of bf16 logits
+    return LLIMA_OK;
+}
+
+static int lmh_check_plain(const void* hidden, const void* weight, int32_t B, int32_t H,
+                           int32_t V) {
+    if (B < 0 || H <= 0 || V <= 0 || H % 8 != 0) return LLIMA_E_INVAL;
+    if (H > LMH_MAX_H && (H > 65536 || H % LMH_KC != 0)) return LLIMA_E_INVAL;   // MFMA path only
+    if (!weight || (B > 0 && !hidden)) return LLIMA_E_INVAL;
+    if ((uintptr_t)weight % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
+    return LLIMA_OK;
+}
+
+// The passes over the plain weight (MFMA tiles, or the matrix-vector rows
+// kernel) and the finish: lmh_finish, or lmh_score_finish with SC.
+template <bool SC>
+static int lmh_run_plain(LmhParams& P, hipStream_t st) {
+    const int B = P.B, H = P.H, V = P.V;
+    if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
+        P.NW = lmh_mfma_waves(V);
+        const dim3 g128((uint32_t)((V + 127) / 128));
+        for (int b0 = 0; b0 < B; b0 += LMH_MB) {
+            const int nb = B - b0 < LMH_MB ? B - b0 : LMH_MB;
+            // 128 vocab rows per workgroup; the narrowest tile that holds the
+            // pass: 64, 128 or 256 hidden rows
+            if (nb <= 64) hipLaunchKernelGGL((lmh_mfma<4, 1, 4, LMH_KC, SC>), g128, dim3(256), 0, st, P, b0, nb);
+            else if (nb <= 128) hipLaunchKernelGGL((lmh_mfma<4, 2, 2, LMH_KC, SC>), g128, dim3(512), 0, st, P, b0, nb);
+            else hipLaunchKernelGGL((lmh_mfma<4, 4, 2, LMH_KC, SC>), g128, dim3(1024), 0, st, P, b0, nb);
+        }
+    } else {
+        P.NW = lmh_waves(V);
+        // rows per pass: what H allows, but no more than the batch fills
+        int nbp = lmh_rows_per_pass(H);
+        while (nbp > 1 && nbp / 2 >= B) nbp /= 2;
+        const dim3 g((uint32_t)((P.NW + LMH_WAVES - 1) / LMH_WAVES)), blk(LMH_WG);
+        for (int b0 = 0; b0 < B; b0 += nbp) {
+            const int nb = B - b0 < nbp ? B - b0 : nbp;
+            switch (nbp) {
+                case 8: hipLaunchKernelGGL((lmh_rows<8, SC>), g, blk, 0, st, P, b0, nb); break;
+                case 4: hipLaunchKernelGGL((lmh_rows<4, SC>), g, blk, 0, st, P, b0, nb); break;
+                case 2: hipLaunchKernelGGL((lmh_rows<2, SC>), g, blk, 0, st, P, b0, nb); break;
+                default: hipLaunchKernelGGL((lmh_rows<1, SC>), g, blk, 0, st, P, b0, nb); break;
+            }
+        }
+    }
+    if (SC) hipLaunchKernelGGL(lmh_score_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    else hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
 extern "C" size_t llima_lm_head_argmax_workspace_bytes(int32_t B, int32_t V) {
     if (B <= 0 || V <= 0) return 0;
-    const int nw = lmh_waves(V) > lmh_mfma_waves(V) ? lmh_waves(V) : lmh_mfma_waves(V);
-    return lmh_align256((size_t)B * nw * sizeof(uint64_t));
+    return lmh_ws_bytes(B, lmh_plain_slots(V), false);
 }
 
 extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int32_t B, int32_t H,
                                     int32_t V, float softcap, int32_t logit_dtype,
                                     int32_t* out_ids, float* out_vals, float* out_logits,
                                     void* workspace, size_t workspace_bytes, void* stream) {
-    if (B < 0 || H <= 0 || V <= 0 || H % 8 != 0) return LLIMA_E_INVAL;
-    if (H > LMH_MAX_H && (H > 65536 || H % LMH_KC != 0)) return LLIMA_E_INVAL;   // MFMA path only
-    if (!weight || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
-    if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
-    const int32_t logits_bf16 = (logit_dtype & LLIMA_LOGITS_OUT_BF16) != 0;
-    logit_dtype &= ~LLIMA_LOGITS_OUT_BF16;
-    if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
-    if (logits_bf16 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;   // bf16 output of bf16 logits
-    if ((uintptr_t)weight % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
+    int st0 = lmh_check_plain(hidden, weight, B, H, V);
+    if (st0 != LLIMA_OK) return st0;
+    if (B > 0 && !out_ids) return LLIMA_E_INVAL;
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_lm_head_argmax_workspace_bytes(B, V))
         return LLIMA_E_WORKSPACE;
@@ -545,40 +787,42 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     P.out_ids = out_ids;
     P.out_vals = out_vals;
     P.B = B; P.H = H; P.V = V;
-    P.NW = lmh_waves(V);
     P.cap = softcap;
     P.round_bf16 = logit_dtype == LLIMA_BF16;
     P.logits_bf16 = logits_bf16;
-    hipStream_t st = (hipStream_t)stream;
-    if ((B > lmh_rows_per_pass(H) || H > LMH_MAX_H) && H % LMH_KC == 0) {   // MFMA tiles
-        P.NW = lmh_mfma_waves(V);
-        const dim3 g128((uint32_t)((V + 127) / 128));
-        for (int b0 = 0; b0 < B; b0 += LMH_MB) {
-            const int nb = B - b0 < LMH_MB ? B - b0 : LMH_MB;
-            // 128 vocab rows per workgroup; the narrowest tile that holds the
-            // pass: 64, 128 or 256 hidden rows
-            if (nb <= 64) hipLaunchKernelGGL((lmh_mfma<4, 1, 4, LMH_KC>), g128, dim3(256), 0, st, P, b0, nb);
-            else if (nb <= 128) hipLaunchKernelGGL((lmh_mfma<4, 2, 2, LMH_KC>), g128, dim3(512), 0, st, P, b0, nb);
-            else hipLaunchKernelGGL((lmh_mfma<4, 4, 2, LMH_KC>), g128, dim3(1024), 0, st, P, b0, nb);
-        }
-        hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
-        return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
-    }
-    // rows per pass: what H allows, but no more than the batch fills
-    int nbp = lmh_rows_per_pass(H);
-    while (nbp > 1 && nbp / 2 >= B) nbp /= 2;
-    const dim3 g((uint32_t)((P.NW + LMH_WAVES - 1) / LMH_WAVES)), blk(LMH_WG);
-    for (int b0 = 0; b0 < B; b0 += nbp) {
-        const int nb = B - b0 < nbp ? B - b0 : nbp;
-        switch (nbp) {
-            case 8: hipLaunchKernelGGL(lmh_rows<8>, g, blk, 0, st, P, b0, nb); break;
-            case 4: hipLaunchKernelGGL(lmh_rows<4>, g, blk, 0, st, P, b0, nb); break;
-            case 2: hipLaunchKernelGGL(lmh_rows<2>, g, blk, 0, st, P, b0, nb); break;
-            default: hipLaunchKernelGGL(lmh_rows<1>, g, blk, 0, st, P, b0, nb); break;
-        }
-    }
-    hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
-    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+    return lmh_run_plain<false>(P, (hipStream_t)stream);
+}
+
+extern "C" size_t llima_lm_head_score_workspace_bytes(int32_t B, int32_t V) {
+    if (B <= 0 || V <= 0) return 0;
+    return lmh_ws_bytes(B, lmh_plain_slots(V), true);
+}
+
+extern "C" int llima_lm_head_score(const void* hidden, const void* weight, int32_t B, int32_t H,
+                                   int32_t V, float softcap, int32_t logit_dtype,
+                                   const int32_t* targets, double* out_logprob,
+                                   int32_t* out_is_greedy, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    int st0 = lmh_check_plain(hidden, weight, B, H, V);
+    if (st0 != LLIMA_OK) return st0;
+    if (B > 0 && (!targets || !out_logprob || !out_is_greedy)) return LLIMA_E_INVAL;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
+    if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_lm_head_score_workspace_bytes(B, V))
+        return LLIMA_E_WORKSPACE;
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.weight = (const uint16_t*)weight;
+    P.B = B; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    P.targets = targets;
+    P.out_logprob = out_logprob;
+    P.out_greedy = out_is_greedy;
+    lmh_ws_split(P, workspace, lmh_plain_slots(V));
+    return lmh_run_plain<true>(P, (hipStream_t)stream);
 }
 
 // Row blocks per wave, and ring depth, of lmh_packed passes of 32 and of 64
@@ -600,11 +844,19 @@ extern "C" size_t llima_lm_head_packed_bytes(int32_t V, int32_t H) {
     return (size_t)((V + 31) / 32) * 32 * (size_t)H * 2;
 }
 
+static int lmp_slots(int V) {
+    const int g1 = lmp_groups(V, LMP_WR1), g2 = lmp_groups(V, LMP_WR2);
+    return (g1 > g2 ? g1 : g2) * LMP_WAVES;
+}
+
 extern "C" size_t llima_lm_head_argmax_packed_workspace_bytes(int32_t B, int32_t H, int32_t V) {
     if (B <= 0 || llima_lm_head_packed_bytes(V, H) == 0) return 0;
-    const int g1 = lmp_groups(V, LMP_WR1), g2 = lmp_groups(V, LMP_WR2);
-    const int nw = (g1 > g2 ? g1 : g2) * LMP_WAVES;
-    return lmh_align256((size_t)B * nw * sizeof(uint64_t));
+    return lmh_ws_bytes(B, lmp_slots(V), false);
+}
+
+extern "C" size_t llima_lm_head_score_packed_workspace_bytes(int32_t B, int32_t H, int32_t V) {
+    if (B <= 0 || llima_lm_head_packed_bytes(V, H) == 0) return 0;
+    return lmh_ws_bytes(B, lmp_slots(V), true);
 }
 
 extern "C" int llima_lm_head_pack(const void* weight, int32_t V, int32_t H, void* packed,
@@ -620,6 +872,26 @@ extern "C" int llima_lm_head_pack(const void* weight, int32_t V, int32_t H, void
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }
 
+// The passes over a packed weight and the finish (lmh_score_finish with SC).
+template <bool SC>
+static int lmh_run_packed(LmhParams& P, const uint8_t* packed, hipStream_t st) {
+    const int B = P.B, V = P.V;
+    const int ng1 = lmp_groups(V, LMP_WR1), ng2 = lmp_groups(V, LMP_WR2);
+    P.NW = lmp_slots(V);
+    for (int b0 = 0; b0 < B; b0 += LMP_MB) {
+        const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB;
+        if (nb <= 32)
+            hipLaunchKernelGGL((lmh_packed<1, LMP_WR1, LMP_R1, LMP_KR, SC>), dim3(ng1), dim3(LMP_WG), 0,
+                               st, P, packed, b0, nb);
+        else
+            hipLaunchKernelGGL((lmh_packed<2, LMP_WR2, LMP_R2, LMP_KR, SC>), dim3(ng2), dim3(LMP_WG), 0,
+                               st, P, packed, b0, nb);
+    }
+    if (SC) hipLaunchKernelGGL(lmh_score_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    else hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
 extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packed, int32_t B,
                                            int32_t H, int32_t V, float softcap,
                                            int32_t logit_dtype, int32_t* out_ids, float* out_vals,
@@ -627,16 +899,13 @@ extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packe
                                            size_t workspace_bytes, void* stream) {
     if (B < 0 || llima_lm_head_packed_bytes(V, H) == 0) return LLIMA_E_INVAL;
     if (!packed || (B > 0 && (!hidden || !out_ids))) return LLIMA_E_INVAL;
-    if (!(softcap == softcap) || __builtin_isinf(softcap)) return LLIMA_E_INVAL;
-    const int32_t logits_bf16 = (logit_dtype & LLIMA_LOGITS_OUT_BF16) != 0;
-    logit_dtype &= ~LLIMA_LOGITS_OUT_BF16;
-    if (logit_dtype != LLIMA_F32 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;
-    if (logits_bf16 && logit_dtype != LLIMA_BF16) return LLIMA_E_INVAL;   // bf16 output of bf16 logits
+    int32_t logits_bf16 = 0;
+    const int st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16);
+    if (st0 != LLIMA_OK) return st0;
     if ((uintptr_t)packed % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
     if (B == 0) return LLIMA_OK;
     if (!workspace || workspace_bytes < llima_lm_head_argmax_packed_workspace_bytes(B, H, V))
         return LLIMA_E_WORKSPACE;
-    const int ng1 = lmp_groups(V, LMP_WR1), ng2 = lmp_groups(V, LMP_WR2);
     LmhParams P = {};
     P.hidden = (const uint16_t*)hidden;
     P.out_logits = out_logits;
@@ -644,20 +913,36 @@ extern "C" int llima_lm_head_argmax_packed(const void* hidden, const void* packe
     P.out_ids = out_ids;
     P.out_vals = out_vals;
     P.B = B; P.H = H; P.V = V;
-    P.NW = (ng1 > ng2 ? ng1 : ng2) * LMP_WAVES;
     P.cap = softcap;
     P.round_bf16 = logit_dtype == LLIMA_BF16;
     P.logits_bf16 = logits_bf16;
-    hipStream_t st = (hipStream_t)stream;
-    for (int b0 = 0; b0 < B; b0 += LMP_MB) {
-        const int nb = B - b0 < LMP_MB ? B - b0 : LMP_MB;
-        if (nb <= 32)
-            hipLaunchKernelGGL((lmh_packed<1, LMP_WR1, LMP_R1, LMP_KR>), dim3(ng1), dim3(LMP_WG), 0,
-                               st, P, (const uint8_t*)packed, b0, nb);
-        else
-            hipLaunchKernelGGL((lmh_packed<2, LMP_WR2, LMP_R2, LMP_KR>), dim3(ng2), dim3(LMP_WG), 0,
-                               st, P, (const uint8_t*)packed, b0, nb);
-    }
-    hipLaunchKernelGGL(lmh_finish, dim3((uint32_t)B), dim3(LLIMA_WG), 0, st, P);
-    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+    return lmh_run_packed<false>(P, (const uint8_t*)packed, (hipStream_t)stream);
+}
+
+extern "C" int llima_lm_head_score_packed(const void* hidden, const void* packed, int32_t B,
+                                          int32_t H, int32_t V, float softcap,
+                                          int32_t logit_dtype, const int32_t* targets,
+                                          double* out_logprob, int32_t* out_is_greedy,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    if (B < 0 || llima_lm_head_packed_bytes(V, H) == 0) return LLIMA_E_INVAL;
+    if (!packed || (B > 0 && (!hidden || !targets || !out_logprob || !out_is_greedy)))
+        return LLIMA_E_INVAL;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    int32_t logits_bf16 = 0;
+    const int st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16);
+    if (st0 != LLIMA_OK) return st0;
+    if ((uintptr_t)packed % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
+    if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_lm_head_score_packed_workspace_bytes(B, H, V))
+        return LLIMA_E_WORKSPACE;
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.B = B; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    P.targets = targets;
+    P.out_logprob = out_logprob;
+    P.out_greedy = out_is_greedy;
+    lmh_ws_split(P, workspace, lmp_slots(V));
+    return lmh_run_packed<true>(P, (const uint8_t*)packed, (hipStream_t)stream);
 }

@@ -54,14 +54,6 @@ __device__ __forceinline__ float sc_ld1<uint16_t>(const uint16_t* p, int64_t i) 
     return bf16_bits_to_f32(p[i]);
 }
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    return __longlong_as_double((long long)wave_reduce<uint64_t>(
-        (uint64_t)__double_as_longlong(v), 0ull, [](uint64_t a, uint64_t b) {
-            return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) +
-                                                  __longlong_as_double((long long)b));
-        }));
-}
-
 template <typename TL, int E, bool VEC>
 __global__ __launch_bounds__(LLIMA_WG) void score_sweep(ScoreParams P) {
     constexpr int EPL = 16 / sizeof(TL);

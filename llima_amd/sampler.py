@@ -604,6 +604,61 @@ def lm_head_argmax(hidden: torch.Tensor, weight, softcap: float = 0.0,
     return (ids, vals, logits) if return_logits else (ids, vals)
 
 
+def lm_head_score(hidden: torch.Tensor, weight, target, softcap: float = 0.0,
+                  logit_dtype: str = "bf16"):
+    """The LM head followed by score_logits (language_model.cpp:29-62) in one
+    call, the logits never written (llima_lm_head_score): hidden bf16 [B, H]
+    with int targets [B] -> (float64 [B] log-probabilities, bool [B] greedy
+    flags), or hidden [H] with an int target -> (float, bool).  The logits are
+    lm_head_argmax's (the same softcap and logit_dtype); weight may be a
+    PackedLmHead.  A target outside the vocabulary raises RuntimeError, as
+    score_logits does."""
+    single = hidden.dim() == 1
+    x = hidden.reshape(1, -1) if single else hidden
+    packed = isinstance(weight, PackedLmHead)
+    if x.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
+        raise ValueError("lm_head_score takes bf16 hidden states and weights")
+    if logit_dtype not in ("bf16", "f32"):
+        raise ValueError("logit_dtype must be 'bf16' or 'f32'")
+    x = x.contiguous()
+    w = weight.data if packed else weight.contiguous()
+    B, H = x.shape
+    if packed:
+        if weight.H != H:
+            raise ValueError("hidden width differs from the packed weight's H")
+        V = weight.V
+    else:
+        if w.dim() != 2 or w.shape[1] != H:
+            raise ValueError("weight must be [V, H]")
+        V = w.shape[0]
+    dev = w.device
+    if single:
+        t = int(target)
+        if t < 0 or t >= V:
+            raise RuntimeError(f"Target token id {t} is outside logits vocabulary size {V}")
+        tg = torch.full((1,), t, dtype=torch.int32, device=dev)
+    else:
+        tg = torch.as_tensor(target).to(device=dev, dtype=torch.int32).contiguous().reshape(-1)
+        if tg.numel() != B:
+            raise ValueError("one target per row is required")
+    _on_gpu(x, w, tg)
+    lp = torch.empty(B, dtype=torch.float64, device=dev)
+    gr = torch.empty(B, dtype=torch.int32, device=dev)
+    nws = (lib().llima_lm_head_score_packed_workspace_bytes(B, H, V) if packed
+           else lib().llima_lm_head_score_workspace_bytes(B, V))
+    ws = Workspace.get(dev, "lm_head_score", nws)
+    ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
+    fn = lib().llima_lm_head_score_packed if packed else lib().llima_lm_head_score
+    check(fn(x.data_ptr(), w.data_ptr(), B, H, V, float(softcap), ld, tg.data_ptr(),
+             lp.data_ptr(), gr.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_lm_head_score_packed" if packed else "llima_lm_head_score")
+    if single:
+        return float(lp[0]), bool(gr[0] == 1)
+    if bool((gr < 0).any()):
+        raise RuntimeError(f"a target token id is outside logits vocabulary size {V}")
+    return lp, gr == 1
+
+
 def topk(x: torch.Tensor, k: int):
     """topk<T> (utils.hpp:216-281) over the rows of x ([cols] or [rows, cols],
     fp32 or bf16) -> (indices int32 [rows, k], values float32 [rows, k]) in the

@@ -132,6 +132,32 @@ def test_host_only_entry_points():
                                          None) == -4
     assert L.llima_lm_head_argmax_packed(None, p, 0, 256, 1000, 0.0, 1, None, None, None, None,
                                          0, None) == 0
+    # LM head scoring: the argmax checks, targets and both outputs required, no
+    # logits output flag; its workspace holds the keys and the slot sums
+    ws = L.llima_lm_head_score_workspace_bytes(2, 1000)
+    assert ws > L.llima_lm_head_argmax_workspace_bytes(2, 1000)
+    assert L.llima_lm_head_score_workspace_bytes(0, 1000) == 0
+    assert L.llima_lm_head_score(p, p, 1, 12, 1000, 0.0, 1, p, p, p, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 1, 16, 1000, float("nan"), 1, p, p, p, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 1, 16, 1000, 0.0, 0x101, p, p, p, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 1, 16, 1000, 0.0, 1, None, p, p, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 1, 16, 1000, 0.0, 1, p, None, p, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 1, 16, 1000, 0.0, 1, p, p, None, p, ws, None) == -1
+    assert L.llima_lm_head_score(p, p, 2, 16, 1000, 0.0, 1, p, p, p, p, ws - 1, None) == -4
+    assert L.llima_lm_head_score(None, p, 0, 16, 1000, 0.0, 1, None, None, None, None, 0,
+                                 None) == 0
+    wsp = L.llima_lm_head_score_packed_workspace_bytes(2, 256, 1000)
+    assert wsp > L.llima_lm_head_argmax_packed_workspace_bytes(2, 256, 1000)
+    assert L.llima_lm_head_score_packed_workspace_bytes(2, 100, 1000) == 0
+    assert L.llima_lm_head_score_packed(p, p, 1, 100, 1000, 0.0, 1, p, p, p, p, wsp, None) == -1
+    assert L.llima_lm_head_score_packed(p, p, 1, 256, 1000, 0.0, 0x101, p, p, p, p, wsp,
+                                        None) == -1
+    assert L.llima_lm_head_score_packed(p, p, 1, 256, 1000, 0.0, 1, None, p, p, p, wsp,
+                                        None) == -1
+    assert L.llima_lm_head_score_packed(p, p, 2, 256, 1000, 0.0, 1, p, p, p, p, wsp - 1,
+                                        None) == -4
+    assert L.llima_lm_head_score_packed(None, p, 0, 256, 1000, 0.0, 1, None, None, None, None,
+                                        0, None) == 0
     # rejection verification: V % 4 == 0, D <= 255, 16-byte aligned rows
     vw = L.llima_verify_rejection_workspace_bytes(1, 1, 4096)
     assert L.llima_verify_rejection(p, p, 1, 1, 4094, p, p, p, p, p, p, vw, None) == -1

@@ -1240,6 +1240,117 @@ def test_lm_head_bf16_logits_out(gpu, B, H, V, packed):
                                  logits_out="bf16")
 
 
+# LM head scoring: the (B, H, V, softcap, packed) cases cover the matrix-vector
+# path (B up to 8), the MFMA tiles (wider batches, H > 4096, two 256-row passes)
+# and the packed weight (32- and 64-row passes, two passes).
+LM_SCORE_CASES = [(1, 4096, 32768, 0.0, False), (3, 1024, 50000, 30.0, False),
+                  (8, 2048, 20000, 0.0, False), (17, 256, 777, 0.0, False),
+                  (64, 4096, 20000, 30.0, False), (300, 256, 3001, 0.0, False),
+                  (4, 8192, 3000, 0.0, False), (5, 256, 31, 0.0, True),
+                  (40, 1024, 70000, 30.0, True), (64, 4096, 20000, 0.0, True),
+                  (70, 512, 5000, 0.0, True)]
+
+
+@pytest.mark.parametrize("B,H,V,cap,packed", LM_SCORE_CASES)
+def test_lm_head_score(gpu, oracle, B, H, V, cap, packed):
+    """llima_lm_head_score: the log-probability and greedy flag of score_logits
+    over the logits lm_head_argmax writes for the same inputs (the oracle on
+    those logits, SCORE_TOL; the flag exact), for bf16-rounded and fp32
+    logits.  Half the targets are the row's argmax."""
+    import llima_amd
+    _say("lm head score", B, H, V, cap, packed)
+    rng = np.random.default_rng(B * 7 + H + V)
+    x = _t(wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32)), gpu)
+    w = _t(wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32)), gpu)
+    wt = llima_amd.lm_head_pack(w) if packed else w
+    for ld in ("bf16", "f32"):
+        ids, _, logits = llima_amd.lm_head_argmax(x, wt, softcap=cap, return_logits=True,
+                                                  logit_dtype=ld)
+        targets = rng.integers(0, V, B).astype(np.int32)
+        targets[::2] = _np(ids)[::2]
+        lp, g = llima_amd.lm_head_score(x, wt, torch_i32(targets, gpu), softcap=cap,
+                                        logit_dtype=ld)
+        _score_check(_np(lp), _np(g), _np(logits), targets, oracle)
+        assert _np(g)[::2].all()
+
+
+def torch_i32(a, gpu):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(gpu)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_lm_head_score_edges(gpu, oracle, packed):
+    """Scoring edge cases against the oracle on the written logits: equal
+    vocab rows (the lower id is the greedy one), a NaN hidden row (NaN), a row
+    with a +inf logit (NaN: infinite maximum), a -inf logit beside finite ones
+    (the target's log-probability -inf, the others finite); a single row with
+    an int target; a target outside the vocabulary raises (the C ABI's flag is
+    LLIMA_E_RANGE)."""
+    import torch
+    import llima_amd
+    from llima_amd import _lib
+    _say("lm head score edges", packed)
+    rng = np.random.default_rng(9)
+    B, H, V = 6, 256, 5000
+    xf = rng.normal(0, 1, (B, H)).astype(np.float32)
+    wf = rng.normal(0, 0.1, (V, H)).astype(np.float32)
+    wf[3000] = xf[0] * 0.5                                      # the maximum of row 0 ...
+    wf[1234] = wf[3000]                                         # ... tied at a lower id
+    xf[1] = np.nan                                              # all logits NaN
+    wf[:, :2] = 0.0                                             # ids 0 and 1 of the hidden rows
+    xf[:, :2] = 0.0                                             # reach only ids 7, 8 and 9
+    xf[2] = 1e20                                                # +inf at id 7, -inf at id 8
+    wf[7, 1] = 1e20
+    wf[8, 1] = -1e20
+    xf[3, 0] = 1e20                                             # -inf at id 9 only
+    wf[9, 0] = -1e20
+    x = _t(wl.f32_to_bf16_bits(xf), gpu)
+    w = _t(wl.f32_to_bf16_bits(wf), gpu)
+    wt = llima_amd.lm_head_pack(w) if packed else w
+    targets = np.array([1234, 5, 7, 9, 3000, 0], np.int32)
+    for ld in ("bf16", "f32"):
+        _, _, logits = llima_amd.lm_head_argmax(x, wt, return_logits=True, logit_dtype=ld)
+        lg = _np(logits)
+        assert np.isinf(lg[3, 9]) and np.isfinite(np.delete(lg[3], 9)).all()
+        for t4 in (9, 100):
+            targets[3] = t4
+            lp, g = llima_amd.lm_head_score(x, wt, torch_i32(targets, gpu), logit_dtype=ld)
+            _score_check(_np(lp), _np(g), lg, targets, oracle)
+        lp, g = _np(lp), _np(g)
+        assert g[0] and np.isnan(lp[1]) and np.isnan(lp[2]) and np.isfinite(lp[3]), (
+            ld, g, lp, lg[0, [1234, 3000]], np.argmax(lg[0]), np.nanmax(lg[0]))
+        lp1, g1 = llima_amd.lm_head_score(x[0], wt, 3000, logit_dtype=ld)
+        elp, eg = oracle.score_logits(lg[0], 3000)
+        assert abs(lp1 - elp) <= SCORE_TOL and g1 == eg == False
+    with pytest.raises(RuntimeError):
+        llima_amd.lm_head_score(x[0], wt, V)
+    with pytest.raises(RuntimeError):
+        llima_amd.lm_head_score(x, wt, torch_i32([0, 1, V, 3, 4, 5], gpu))
+    # through the C ABI: the flag of the out-of-range row, NaN beside it only there
+    L = _lib.lib()
+    tg = torch_i32([0, 1, -1, 3, 4, V + 5], gpu)
+    lp = torch.empty(B, dtype=torch.float64, device=gpu)
+    gr = torch.empty(B, dtype=torch.int32, device=gpu)
+    if packed:
+        n = L.llima_lm_head_score_packed_workspace_bytes(B, H, V)
+        ws = torch.empty(n, dtype=torch.uint8, device=gpu)
+        st = L.llima_lm_head_score_packed(x.data_ptr(), wt.data.data_ptr(), B, H, V, 0.0,
+                                          _lib.LLIMA_BF16, tg.data_ptr(), lp.data_ptr(),
+                                          gr.data_ptr(), ws.data_ptr(), n, None)
+    else:
+        n = L.llima_lm_head_score_workspace_bytes(B, V)
+        ws = torch.empty(n, dtype=torch.uint8, device=gpu)
+        st = L.llima_lm_head_score(x.data_ptr(), w.data_ptr(), B, H, V, 0.0, _lib.LLIMA_BF16,
+                                   tg.data_ptr(), lp.data_ptr(), gr.data_ptr(), ws.data_ptr(), n,
+                                   None)
+    assert st == 0
+    torch.cuda.synchronize()
+    lp, gr = _np(lp), _np(gr)
+    assert gr[2] == gr[5] == _lib.LLIMA_E_RANGE and np.isnan(lp[2]) and np.isnan(lp[5])
+    assert np.isfinite(lp[[0, 3, 4]]).all() and (gr[[0, 1, 3, 4]] >= 0).all()
+
+
 def test_lm_head_argmax_ties_and_nan(gpu):
     """Equal vocab rows tie: the lower index wins; a NaN logit never wins; a
     row whose logits are all NaN gives id 0 and a NaN value."""
