@@ -75,6 +75,29 @@ __device__ __forceinline__ float lmh_logit(float s, const LmhParams& P) {
     return s;
 }
 
+// lmh_logit over a tile's values, its two decisions taken once for the tile;
+// the rounding selects NaN through unchanged rather than branching.
+template <int WR>
+__device__ __forceinline__ void lmh_logit_tile(float (&v)[16][WR], const LmhParams& P) {
+    if (P.cap > 0.0f) {                                      // uniform
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int j = 0; j < WR; ++j) v[i][j] = P.cap * tanhf(v[i][j] / P.cap);
+    }
+    if (P.round_bf16) {                                      // uniform
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int j = 0; j < WR; ++j) {
+                const float s = v[i][j];
+                const uint32_t u = __float_as_uint(s);
+                const float q = __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+                v[i][j] = s == s ? q : s;
+            }
+    }
+}
+
 // Writes logit i of the [B][V] output: fp32, or the bf16 it was rounded to
 // (its upper 16 bits; a NaN as the quiet NaN).
 __device__ __forceinline__ void lmh_store_logit(const LmhParams& P, size_t i, float v) {
@@ -237,16 +260,119 @@ __device__ __forceinline__ float half_sum_f32(float v) {
     return v;
 }
 
-// Greatest 64-bit value over the 32 lanes of this lane's half-wave.
-__device__ __forceinline__ uint64_t half_max_u64(uint64_t v) {
+// Half-wave collectives over the 16 rows of a 32 x 32 accumulator tile, whose
+// lane (r, g) holds rows i % 4 + 8 (i / 4) + 4 g (i < 16).  The reduce-scatter
+// exchanges with lanes r ^ 16, r ^ 8, r ^ 4, r ^ 2 (each time keeping the half
+// of its rows the lane's bit selects and combining them with the partner's)
+// and r ^ 1, leaving lanes r and r ^ 1 with row (r >> 1) % 16's result over
+// the half-wave: 16 shuffles for 16 rows, where a reduction per row takes 80.
+// The all-gather returns every row's value to every lane (15 shuffles).
+__device__ __forceinline__ uint64_t shfl_xor_t(uint64_t v, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t shfl_xor_t(uint32_t v, int m) {
+    return (uint32_t)__shfl_xor((int)v, m, 64);
+}
+__device__ __forceinline__ float shfl_xor_t(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <class T, int N>
+__device__ __forceinline__ void half_rs_step(const T (&a)[2 * N], T (&b)[N], int r, int bit,
+                                             T (*op)(T, T)) {
+    const bool hi = (r & bit) != 0;
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
-        const uint64_t w = ((uint64_t)hi << 32) | lo;
-        v = w > v ? w : v;
+    for (int k = 0; k < N; ++k) {
+        const T send = hi ? a[k] : a[k + N], keep = hi ? a[k + N] : a[k];
+        b[k] = op(keep, shfl_xor_t(send, bit));
     }
-    return v;
+}
+
+template <class T>
+__device__ __forceinline__ T half_reduce_scatter16(const T (&a)[16], int r, T (*op)(T, T)) {
+    T b8[8], b4[4], b2[2], b1[1];
+    half_rs_step<T, 8>(a, b8, r, 16, op);
+    half_rs_step<T, 4>(b8, b4, r, 8, op);
+    half_rs_step<T, 2>(b4, b2, r, 4, op);
+    half_rs_step<T, 1>(b2, b1, r, 2, op);
+    return op(b1[0], shfl_xor_t(b1[0], 1));
+}
+
+__device__ __forceinline__ void half_all_gather16(uint32_t own, int r, uint32_t (&h)[16]) {
+    const int ir = (r >> 1) & 15;
+    h[0] = own;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const bool mine = ((ir >> s) & 1) != 0;
+#pragma unroll
+        for (int k = 0; k < (1 << s); ++k) {
+            const uint32_t cur = h[k], recv = shfl_xor_t(cur, 2 << s);
+            h[k] = mine ? recv : cur;
+            h[k + (1 << s)] = mine ? cur : recv;
+        }
+    }
+}
+
+__device__ __forceinline__ uint64_t lmh_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ float lmh_add_f32(float a, float b) { return a + b; }
+
+// The epilogue of one 32 x 32 accumulator tile over WR column blocks: lane
+// (r, g) holds v[i][j], the logit of tile row i % 4 + 8 (i / 4) + 4 g (pass row
+// mbase + that) and column ncol[j].  Writes the logits (when asked) and each
+// row's greatest key over the wave's 32 WR columns into key slot wv; with SC
+// also the slot's sum of exp(logit - its maximum) and the target's logit (tg[i]:
+// row i's target, -1 for rows past nb).
+template <int WR, bool SC>
+__device__ __forceinline__ void lmh_tile_out(const LmhParams& P, const float (&v)[16][WR],
+                                             const int (&ncol)[WR], int mbase, int b0, int nb,
+                                             int wv, int r, int g, const int32_t (&tg)[16]) {
+    const int V = P.V;
+    if (P.out_logits) {                                      // uniform
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = mbase + (i & 3) + 8 * (i >> 2) + 4 * g;
+#pragma unroll
+            for (int j = 0; j < WR; ++j)
+                if (m < nb && ncol[j] < V) lmh_store_logit(P, (size_t)(b0 + m) * V + ncol[j], v[i][j]);
+        }
+    }
+    uint64_t k[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        k[i] = 0;
+#pragma unroll
+        for (int j = 0; j < WR; ++j) k[i] = lmh_max_u64(k[i], lmh_key(v[i][j], ncol[j], V));
+    }
+    const uint64_t best = half_reduce_scatter16<uint64_t>(k, r, lmh_max_u64);
+    const int ir = (r >> 1) & 15, mr = mbase + (ir & 3) + 8 * (ir >> 2) + 4 * g;
+    const bool st = (r & 1) == 0 && mr < nb;                 // one lane per row stores
+    if (st) P.keys[(size_t)(b0 + mr) * P.NW + wv] = best;
+    if constexpr (SC) {
+        uint32_t hv[16];                                     // each row's maximum key
+        half_all_gather16((uint32_t)(best >> 32), r, hv);
+        float e[16];
+        bool hit = false;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float mw = hv[i] ? key_f32(hv[i]) : -__builtin_inff();
+            e[i] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < WR; ++j) {
+                e[i] += lmh_term(v[i][j], mw, ncol[j] < V);
+                hit |= ncol[j] < V && ncol[j] == tg[i];
+            }
+        }
+        const float sw = half_reduce_scatter16<float>(e, r, lmh_add_f32);
+        if (st) P.sums[(size_t)(b0 + mr) * P.NW + wv] = sw;
+        if (hit) {                                           // one lane of the grid per row
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+#pragma unroll
+                for (int j = 0; j < WR; ++j)
+                    if (ncol[j] < V && ncol[j] == tg[i])
+                        P.tval[b0 + mbase + (i & 3) + 8 * (i >> 2) + 4 * g] = v[i][j];
+        }
+    }
 }
 
 // Workgroup tile: 32 NWN vocab rows x 64 WM hidden rows, 64 NWN WM threads.
@@ -355,33 +481,22 @@ __global__ __launch_bounds__(64 * NWN * WM) void lmh_mfma(LmhParams P, int b0, i
     }
     // epilogue: softcap, logits, and per hidden row the greatest key of the wave's 32 columns
     const int wv = (int)blockIdx.x * NWN + wn;
-    const int n = n0 + wn * 32 + r;
+    const int ncol[1] = {n0 + wn * 32 + r};
     int32_t tgv[2][16];                                      // scoring: the lane's rows' targets,
-    if constexpr (SC) {                                      // requested together (-1: no row)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int m = wm * 64 + mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-                tgv[mt][i] = m < nb ? P.targets[b0 + m] : -1;
-            }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll                                               // requested together (-1: no row)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = wm * 64 + mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-            const float v = lmh_logit(acc[mt][i], P);
-            if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
-            const uint64_t best = half_max_u64(lmh_key(v, n, V));
-            if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
-            if constexpr (SC) {
-                const float mw = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
-                const float sw = half_sum_f32(lmh_term(v, mw, n < V));
-                if (r == 0 && m < nb) P.sums[(size_t)(b0 + m) * P.NW + wv] = sw;
-                if (n < V && n == tgv[mt][i]) P.tval[b0 + m] = v;
-            }
+            tgv[mt][i] = SC && m < nb ? P.targets[b0 + m] : -1;
         }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        float v[16][1];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i][0] = acc[mt][i];
+        lmh_logit_tile<1>(v, P);
+        lmh_tile_out<1, SC>(P, v, ncol, wm * 64 + mt * 32, b0, nb, wv, r, g, tgv[mt]);
     }
 }
 
@@ -596,52 +711,29 @@ __global__ __launch_bounds__(LMP_WG) void lmh_packed(LmhParams P, const uint8_t*
     }
     // epilogue: softcap, logits, per hidden row the greatest key of the wave's
     // 32 WR vocab rows
+    int ncol[WR];
+#pragma unroll
+    for (int j = 0; j < WR; ++j) ncol[j] = 32 * (rb0 + j) + r;   // >= V for a spare row block
     int32_t tgv[NMT][16];                                    // scoring: the lane's rows' targets,
-    if constexpr (SC) {                                      // requested together (-1: no row)
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-                tgv[mt][i] = m < nb ? P.targets[b0 + m] : -1;
-            }
-    }
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
+#pragma unroll                                               // requested together (-1: no row)
+    for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = mt * 32 + (i & 3) + 8 * (i >> 2) + 4 * g;
-            uint64_t key = 0;
-            float vj[WR];
-#pragma unroll
-            for (int j = 0; j < WR; ++j) {
-                const int n = 32 * (rb0 + j) + r;            // >= V for a spare row block
-                const float v = lmh_logit(acc[j][mt][i], P);
-                if (P.out_logits && m < nb && n < V) lmh_store_logit(P, (size_t)(b0 + m) * V + n, v);
-                const uint64_t k = lmh_key(v, n, V);
-                key = k > key ? k : key;
-                vj[j] = v;
-            }
-            const uint64_t best = half_max_u64(key);
-            if (r == 0 && m < nb) P.keys[(size_t)(b0 + m) * P.NW + wv] = best;
-            if constexpr (SC) {
-                const float mw = best ? key_f32((uint32_t)(best >> 32)) : -__builtin_inff();
-                const int32_t tg = tgv[mt][i];
-                float e = 0.0f;
-#pragma unroll
-                for (int j = 0; j < WR; ++j) {
-                    const int n = 32 * (rb0 + j) + r;
-                    e += lmh_term(vj[j], mw, n < V);
-                    if (n < V && n == tg) P.tval[b0 + m] = vj[j];
-                }
-                const float sw = half_sum_f32(e);
-                if (r == 0 && m < nb) P.sums[(size_t)(b0 + m) * P.NW + wv] = sw;
-            }
+            tgv[mt][i] = SC && m < nb ? P.targets[b0 + m] : -1;
         }
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+        float v[16][WR];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int j = 0; j < WR; ++j) v[i][j] = acc[j][mt][i];
+        lmh_logit_tile<WR>(v, P);
+        lmh_tile_out<WR, SC>(P, v, ncol, mt * 32, b0, nb, wv, r, g, tgv[mt]);
     }
 }
 
-// One thread per 16-byte piece of the packed weight.
 __global__ __launch_bounds__(LLIMA_WG) void lmh_pack(const uint16_t* weight, uint8_t* packed,
                                                      int V, int H, size_t npieces) {
     const size_t p = (size_t)blockIdx.x * LLIMA_WG + threadIdx.x;
