@@ -1,5 +1,5 @@
 """HIP graph replay: one llima_sample call (the sweep + finish kernels, or the
-dense path) and one llima_verify_rejection call captured into a graph through
+dense path) and one llima_verify_rejection call (and one llima_lm_head_score_packed call) captured into a graph through
 the C ABI, then replayed several times.  Between replays the program's own
 eager work writes new inputs into the captured buffers and synchronises; every
 replay is checked against the oracle on that replay's inputs."""
@@ -122,3 +122,63 @@ def test_verify_rejection_graph_replays(gpu, oracle):
                                       w["u_resample"])
         for got, want in zip(out, exp):
             assert np.array_equal(got.cpu().numpy(), want), i
+
+
+def test_lm_head_score_graph_replays(gpu, oracle):
+    """llima_lm_head_score_packed captured through the C ABI: each replay, on new
+    hidden rows and targets, equals an eager call bit for bit and the oracle's
+    score_logits over the head's logits within 1e-5."""
+    import torch
+    import llima_amd
+    from llima_amd import _lib
+    _say("graph replay llima_lm_head_score_packed")
+    L = _lib.lib()
+    rng = np.random.default_rng(77)
+    B, H, V = 40, 512, 20000
+    xs = [wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32)) for _ in range(REPLAYS)]
+    ts = [rng.integers(0, V, B).astype(np.int32) for _ in range(REPLAYS)]
+    wf = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    w = torch.from_numpy(wf.view(np.int16)).to(gpu).view(torch.bfloat16)
+    pk = llima_amd.lm_head_pack(w)
+    x = torch.empty((B, H), dtype=torch.bfloat16, device=gpu)
+    tg = torch.empty(B, dtype=torch.int32, device=gpu)
+    lp = torch.empty(B, dtype=torch.float64, device=gpu)
+    gr = torch.empty(B, dtype=torch.int32, device=gpu)
+    nws = L.llima_lm_head_score_packed_workspace_bytes(B, H, V)
+    ws = torch.empty(nws, dtype=torch.uint8, device=gpu)
+
+    def launch(stream):
+        rc = L.llima_lm_head_score_packed(x.data_ptr(), pk.data.data_ptr(), B, H, V, 0.0,
+                                          _lib.LLIMA_BF16, tg.data_ptr(), lp.data_ptr(),
+                                          gr.data_ptr(), ws.data_ptr(), nws, stream)
+        assert rc == 0
+
+    def load(i):
+        x.copy_(torch.from_numpy(xs[i].view(np.int16)).view(torch.bfloat16))
+        tg.copy_(torch.from_numpy(ts[i]))
+
+    load(0)
+    launch(torch.cuda.current_stream(gpu).cuda_stream)        # eager warmup
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(gpu)
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        launch(cap.cuda_stream)
+    torch.cuda.synchronize(gpu)
+    for i in range(REPLAYS):
+        load(i)
+        lp.fill_(0.0)
+        gr.fill_(-7)
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        got_lp, got_g = lp.cpu().numpy().copy(), gr.cpu().numpy().copy()
+        elp, eg = llima_amd.lm_head_score(x, pk, tg)
+        assert (got_lp.view(np.uint64) == elp.cpu().numpy().view(np.uint64)).all(), i
+        assert (got_g == eg.cpu().numpy().astype(np.int32)).all(), i
+        _, _, logits = llima_amd.lm_head_argmax(x, pk, return_logits=True)
+        lg = logits.cpu().numpy()
+        for r in range(B):
+            olp, og = oracle.score_logits(lg[r], int(ts[i][r]))
+            assert abs(got_lp[r] - olp) <= 1e-5 and bool(got_g[r]) == og, (i, r)

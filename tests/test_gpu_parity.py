@@ -1066,7 +1066,10 @@ def _lm_head_check(ids, vals, logits, x, w, cap, bf16=True):
     """Logits against a float64 product of the same bf16 values: the fp32 sum's
     error bound, plus half a bf16 ulp (2^-8 relative) when the logits are
     rounded to bf16 (then they must be bf16 values); the argmax exact with
-    respect to the logits returned (first index, NaN never wins)."""
+    respect to the logits returned (first index, NaN never wins), and against
+    the float64 logits: the id's logit within the two error bounds of the
+    float64 maximum, and the float64 argmax itself wherever it leads every
+    other id by more than both bounds."""
     xf = wl.bf16_bits_to_f32(x).astype(np.float64)
     wf = wl.bf16_bits_to_f32(w).astype(np.float64)
     s = xf @ wf.T
@@ -1087,6 +1090,13 @@ def _lm_head_check(ids, vals, logits, x, w, cap, bf16=True):
         m = row[ok].max()
         assert ids[b] == int(np.flatnonzero(ok & (row == m))[0]), b
         assert vals[b] == m
+        r, bd = ref[b], bound[b]
+        if np.isfinite(r).all():
+            top = int(np.argmax(r))
+            assert r[ids[b]] >= r[top] - bd[ids[b]] - bd[top], (b, ids[b], top)
+            rest = np.delete(r + bd, top)
+            if rest.size == 0 or r[top] - bd[top] > rest.max():
+                assert ids[b] == top, (b, ids[b], top)
 
 
 @pytest.mark.parametrize("B,H,V,cap", [(1, 4096, 128256, 0.0), (3, 1536, 262144, 30.0),
