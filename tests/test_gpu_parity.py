@@ -1284,6 +1284,34 @@ def test_lm_head_score(gpu, oracle, B, H, V, cap, packed):
         assert _np(g)[::2].all()
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_lm_head_random_configs(gpu, oracle, seed):
+    """Seeded random LM head cases over every path (matrix-vector, MFMA tiles,
+    packed; ragged batches and vocabularies, softcap on or off, bf16 or fp32
+    logits): ids against the float64 product (_lm_head_check), and the scoring
+    entry point against the oracle's score_logits on the head's logits."""
+    import llima_amd
+    rng = np.random.default_rng(9000 + seed)
+    packed = bool(rng.integers(0, 2))
+    H = int(rng.choice([256, 512, 1024, 4096] if packed else [8, 200, 256, 1000, 1536, 4096, 8192]))
+    B = int(rng.choice([1, 3, 8, 9, 31, 33, 64, 65, 129, 257]))
+    V = max(1, min(int(rng.integers(1, 40000)), int(1e9 // (B * H))))
+    cap = float(rng.choice([0.0, 30.0]))
+    ld = str(rng.choice(["bf16", "f32"]))
+    _say("lm head random", seed, B, H, V, cap, ld, packed)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B, H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    wt = llima_amd.lm_head_pack(_t(w, gpu)) if packed else _t(w, gpu)
+    ids, vals, logits = llima_amd.lm_head_argmax(_t(x, gpu), wt, softcap=cap, return_logits=True,
+                                                 logit_dtype=ld)
+    _lm_head_check(_np(ids), _np(vals), _np(logits), x, w, cap, bf16=ld == "bf16")
+    targets = rng.integers(0, V, B).astype(np.int32)
+    targets[::3] = _np(ids)[::3]
+    lp, g = llima_amd.lm_head_score(_t(x, gpu), wt, torch_i32(targets, gpu), softcap=cap,
+                                    logit_dtype=ld)
+    _score_check(_np(lp), _np(g), _np(logits), targets, oracle)
+
+
 def torch_i32(a, gpu):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(gpu)
