@@ -27,7 +27,9 @@ sampler's dense path, five kernels), and lm_head_argmax /
 lm_head_argmax_b64/b128/b256 (the LM head with its argmax at B = 1 to 256)
 and lm_head_argmax_b32/b64/b128_packed (over a weight packed at load time);
 lm_head_score_b64_packed: the packed LM head with its scoring epilogue (the
-log-softmax at 64 target ids, no logits written).
+log-softmax at 64 target ids, no logits written); lm_head_verify_b16_d7: the
+LM head over 16 sequences x 8 rows with greedy chain verification fused (no
+logits written).
 """
 from __future__ import annotations
 
@@ -56,7 +58,7 @@ def parse():
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
                              "lm_head_argmax_b256", "lm_head_argmax_b32_packed",
                              "lm_head_argmax_b64_packed", "lm_head_argmax_b128_packed",
-                             "lm_head_score_b64_packed"])
+                             "lm_head_score_b64_packed", "lm_head_verify_b16_d7"])
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -95,6 +97,7 @@ def main():
     if name.startswith("lm_head_"):
         B, H, V = w["B"], w["H"], w["V"]
         scoring = name.startswith("lm_head_score")
+        verifying = name.startswith("lm_head_verify")
         g = torch.Generator(device=dev)
         g.manual_seed(w["seed"])
         weight = (torch.randn((V, H), generator=g, device=dev) * (1.0 / H ** 0.5)).to(torch.bfloat16)
@@ -106,6 +109,10 @@ def main():
         if scoring:
             nws = (L.llima_lm_head_score_packed_workspace_bytes(B, H, V) if packed
                    else L.llima_lm_head_score_workspace_bytes(B, V))
+        elif verifying:                  # B hidden rows = seqs sequences of D + 1
+            nseq, D = w["seqs"], w["D"]
+            nws = (L.llima_lm_head_verify_greedy_packed_workspace_bytes(nseq, D, H, V) if packed
+                   else L.llima_lm_head_verify_greedy_workspace_bytes(nseq, D, V))
         else:
             nws = (L.llima_lm_head_argmax_packed_workspace_bytes(B, H, V) if packed
                    else L.llima_lm_head_argmax_workspace_bytes(B, V))
@@ -127,6 +134,17 @@ def main():
                     x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, tg.data_ptr(),
                     lp_o.data_ptr(), ids_o.data_ptr(), ws.data_ptr(), nws, sp),
                     "llima_lm_head_score"))
+        elif verifying:
+            fn = (L.llima_lm_head_verify_greedy_packed if packed
+                  else L.llima_lm_head_verify_greedy)
+            drs = [torch.randint(0, V, (nseq, D), generator=g, device=dev, dtype=torch.int32)
+                   for _ in hid]
+            em_o = torch.empty((nseq, D + 1), dtype=torch.int32, device=dev)
+            for x, dr in zip(hid, drs):
+                launches.append(lambda sp, x=x, dr=dr: check(fn(
+                    x.data_ptr(), weight.data_ptr(), nseq, D, H, V, 0.0, 1, dr.data_ptr(),
+                    ids_o.data_ptr(), em_o.data_ptr(), ws.data_ptr(), nws, sp),
+                    "llima_lm_head_verify_greedy"))
         else:
             fn = L.llima_lm_head_argmax_packed if packed else L.llima_lm_head_argmax
             for x in hid:
@@ -134,13 +152,18 @@ def main():
                     x.data_ptr(), weight.data_ptr(), B, H, V, 0.0, 1, ids_o.data_ptr(),
                     vals_o.data_ptr(), None, ws.data_ptr(), nws, sp), "llima_lm_head_argmax"))
         per = V * H * 2
-        # weight, hidden rows, then the argmax's ids and values or the
-        # targets, log-probabilities and flags
+        # weight, hidden rows, then the argmax's ids and values, the targets,
+        # log-probabilities and flags, or the drafts and the verification
+        # outputs
         alg_bytes = V * H * 2 + B * H * 2 + (B * 16 if scoring else B * 8)
+        if verifying:
+            alg_bytes = V * H * 2 + B * H * 2 + nseq * D * 4 + nseq * (D + 2) * 4
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16"
         fin = "lmh_score_finish" if scoring else "lmh_finish"
+        if verifying:
+            rows, unit_rows = nseq, "sequences/s"
         kernel_names = (["lmh_packed", fin] if packed else
                         ["lmh_mfma" if B > 4 else "lmh_rows", fin])
         config = {"workload": name, "B": B, "H": H, "V": V,
@@ -446,7 +469,8 @@ def cpu_baseline(name, w, seconds, greedy_variant):
             reps += 1
         dt = time.time() - t0
         full = dt * (w["V"] / nv) / reps                     # seconds per full-vocabulary call
-        info.update({"value": w["B"] / full, "unit": "rows/s", "cores": many,
+        per_call, unit_c = (w["seqs"], "sequences/s") if "seqs" in w else (w["B"], "rows/s")
+        info.update({"value": per_call / full, "unit": unit_c, "cores": many,
                      "sample": "%d x numpy float32 [%d, %d] x [%d, %d]^T + %s (a %d-row slice "
                                "of the vocabulary, scaled by V / %d), %.1f s" % (
                                    reps, w["B"], w["H"], nv, w["H"],

@@ -65,6 +65,8 @@
  *                            prepacked at load time (no counterpart)
  *   llima_lm_head_score(_packed) <- the LM head followed by score_logits
  *                            (language_model.cpp:29-62), the logits never written
+ *   llima_lm_head_verify_greedy(_packed) <- the verification step's LM head +
+ *                            _argmax_lm_head_rows + resolve_draft_tokens, no logits
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -353,6 +355,33 @@ int llima_lm_head_score_packed(const void* hidden, const void* packed, int32_t B
                                const int32_t* targets, double* out_logprob,
                                int32_t* out_is_greedy, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* LM head with greedy chain verification fused: for B sequences of D + 1
+ * hidden rows each (hidden bf16 [B][D+1][H]), the head's argmax of every row
+ * (as llima_lm_head_argmax: softcap, logit_dtype rounding, NaN never wins),
+ * then the chain rule of llima_verify_greedy on those ids: accepted_len[B] =
+ * the length of the prefix where draft_ids[b][k] equals row k's argmax;
+ * emitted[B][D+1] = the accepted drafts, then row accepted_len's argmax (the
+ * correction or the bonus token), then -1.  Replaces the verification step's
+ * LM head, its logits and _argmax_lm_head_rows + resolve_draft_tokens
+ * (sima_lmm/devkit/cpp/language_model.cpp:3636-3687,
+ * sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111): no [B(D+1)][V] logits are
+ * written.  Sizes and alignment as llima_lm_head_argmax (its B is B (D + 1));
+ * the _packed form takes a weight from llima_lm_head_pack.
+ * LLIMA_LOGITS_OUT_BF16 is rejected. */
+size_t llima_lm_head_verify_greedy_workspace_bytes(int32_t B, int32_t D, int32_t V);
+int llima_lm_head_verify_greedy(const void* hidden, const void* weight, int32_t B, int32_t D,
+                                int32_t H, int32_t V, float softcap, int32_t logit_dtype,
+                                const int32_t* draft_ids, int32_t* accepted_len,
+                                int32_t* emitted, void* workspace, size_t workspace_bytes,
+                                void* stream);
+size_t llima_lm_head_verify_greedy_packed_workspace_bytes(int32_t B, int32_t D, int32_t H,
+                                                         int32_t V);
+int llima_lm_head_verify_greedy_packed(const void* hidden, const void* packed, int32_t B,
+                                       int32_t D, int32_t H, int32_t V, float softcap,
+                                       int32_t logit_dtype, const int32_t* draft_ids,
+                                       int32_t* accepted_len, int32_t* emitted, void* workspace,
+                                       size_t workspace_bytes, void* stream);
 
 /* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
  * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):

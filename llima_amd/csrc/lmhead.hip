@@ -592,6 +592,25 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_score_finish(LmhParams P) {
     P.out_greedy[b] = am == (uint32_t)tg ? 1 : 0;
 }
 
+// Greedy chain verification from the head's ids, one thread per sequence
+// (resolve_draft_tokens, sima_lmm/devkit/cpp/gemma4_mtp_helpers.cpp:81-111):
+// accept while the draft equals the target row's argmax, then emit the
+// target's token at the first mismatch (or the bonus token), then -1.
+__global__ __launch_bounds__(LLIMA_WG) void lmh_chain(const int32_t* ids, const int32_t* draft_ids,
+                                                      int32_t* accepted_len, int32_t* emitted,
+                                                      int nseq, int D) {
+    const int g = (int)(blockIdx.x * LLIMA_WG + threadIdx.x);
+    if (g >= nseq) return;
+    const int32_t* tok = ids + (size_t)g * (D + 1);
+    const int32_t* dr = draft_ids + (size_t)g * D;
+    int32_t* em = emitted + (size_t)g * (D + 1);
+    int acc = 0;
+    while (acc < D && dr[acc] == tok[acc]) { em[acc] = dr[acc]; ++acc; }
+    em[acc] = tok[acc];
+    for (int j = acc + 1; j <= D; ++j) em[j] = -1;
+    accepted_len[g] = acc;
+}
+
 // ------------------------------------------------------------------ packed weights
 // A weight prepacked once (at model load) in the order the MFMA reads it:
 // fragment (rb, s) is 1 KB, lane l's 16 bytes being
@@ -885,6 +904,63 @@ extern "C" int llima_lm_head_argmax(const void* hidden, const void* weight, int3
     return lmh_run_plain<false>(P, (hipStream_t)stream);
 }
 
+// Workspace of the verification entry points: the head's own, then the ids
+// of the B (D + 1) target rows.
+static size_t lmh_verify_ws(size_t head, int64_t rows) {
+    return head == 0 ? 0 : head + lmh_align256((size_t)rows * sizeof(int32_t));
+}
+
+static int lmh_verify_check(int32_t B, int32_t D, const int32_t* draft_ids,
+                            const int32_t* accepted_len, const int32_t* emitted) {
+    if (B < 0 || D < 0 || (int64_t)B * (D + 1) > (int64_t)INT32_MAX) return LLIMA_E_INVAL;
+    if (B > 0 && (!accepted_len || !emitted || (D > 0 && !draft_ids))) return LLIMA_E_INVAL;
+    return LLIMA_OK;
+}
+
+static int lmh_launch_chain(const int32_t* ids, const int32_t* draft_ids, int32_t* accepted_len,
+                            int32_t* emitted, int32_t B, int32_t D, hipStream_t st) {
+    hipLaunchKernelGGL(lmh_chain, dim3((uint32_t)((B + LLIMA_WG - 1) / LLIMA_WG)), dim3(LLIMA_WG),
+                       0, st, ids, draft_ids, accepted_len, emitted, (int)B, (int)D);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+extern "C" size_t llima_lm_head_verify_greedy_workspace_bytes(int32_t B, int32_t D, int32_t V) {
+    if (B <= 0 || D < 0 || (int64_t)B * (D + 1) > (int64_t)INT32_MAX) return 0;
+    const int32_t rows = B * (D + 1);
+    return lmh_verify_ws(llima_lm_head_argmax_workspace_bytes(rows, V), rows);
+}
+
+extern "C" int llima_lm_head_verify_greedy(const void* hidden, const void* weight, int32_t B,
+                                           int32_t D, int32_t H, int32_t V, float softcap,
+                                           int32_t logit_dtype, const int32_t* draft_ids,
+                                           int32_t* accepted_len, int32_t* emitted,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    int st0 = lmh_verify_check(B, D, draft_ids, accepted_len, emitted);
+    if (st0 != LLIMA_OK) return st0;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    const int32_t rows = B * (D + 1);
+    if ((st0 = lmh_check_plain(hidden, weight, rows, H, V)) != LLIMA_OK) return st0;
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
+    if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_lm_head_verify_greedy_workspace_bytes(B, D, V))
+        return LLIMA_E_WORKSPACE;
+    const size_t head = llima_lm_head_argmax_workspace_bytes(rows, V);
+    int32_t* ids = (int32_t*)((uint8_t*)workspace + head);
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.weight = (const uint16_t*)weight;
+    P.keys = (uint64_t*)workspace;
+    P.out_ids = ids;
+    P.B = rows; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    hipStream_t st = (hipStream_t)stream;
+    if ((st0 = lmh_run_plain<false>(P, st)) != LLIMA_OK) return st0;
+    return lmh_launch_chain(ids, draft_ids, accepted_len, emitted, B, D, st);
+}
+
 extern "C" size_t llima_lm_head_score_workspace_bytes(int32_t B, int32_t V) {
     if (B <= 0 || V <= 0) return 0;
     return lmh_ws_bytes(B, lmh_plain_slots(V), true);
@@ -1037,4 +1113,42 @@ extern "C" int llima_lm_head_score_packed(const void* hidden, const void* packed
     P.out_greedy = out_is_greedy;
     lmh_ws_split(P, workspace, lmp_slots(V));
     return lmh_run_packed<true>(P, (const uint8_t*)packed, (hipStream_t)stream);
+}
+
+extern "C" size_t llima_lm_head_verify_greedy_packed_workspace_bytes(int32_t B, int32_t D,
+                                                                    int32_t H, int32_t V) {
+    if (B <= 0 || D < 0 || (int64_t)B * (D + 1) > (int64_t)INT32_MAX) return 0;
+    const int32_t rows = B * (D + 1);
+    return lmh_verify_ws(llima_lm_head_argmax_packed_workspace_bytes(rows, H, V), rows);
+}
+
+extern "C" int llima_lm_head_verify_greedy_packed(const void* hidden, const void* packed,
+                                                  int32_t B, int32_t D, int32_t H, int32_t V,
+                                                  float softcap, int32_t logit_dtype,
+                                                  const int32_t* draft_ids, int32_t* accepted_len,
+                                                  int32_t* emitted, void* workspace,
+                                                  size_t workspace_bytes, void* stream) {
+    int st0 = lmh_verify_check(B, D, draft_ids, accepted_len, emitted);
+    if (st0 != LLIMA_OK) return st0;
+    if (llima_lm_head_packed_bytes(V, H) == 0 || !packed || (B > 0 && !hidden)) return LLIMA_E_INVAL;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
+    if ((uintptr_t)packed % 16 || (B > 0 && (uintptr_t)hidden % 16)) return LLIMA_E_INVAL;
+    if (B == 0) return LLIMA_OK;
+    if (!workspace || workspace_bytes < llima_lm_head_verify_greedy_packed_workspace_bytes(B, D, H, V))
+        return LLIMA_E_WORKSPACE;
+    const int32_t rows = B * (D + 1);
+    const size_t head = llima_lm_head_argmax_packed_workspace_bytes(rows, H, V);
+    int32_t* ids = (int32_t*)((uint8_t*)workspace + head);
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.keys = (uint64_t*)workspace;
+    P.out_ids = ids;
+    P.B = rows; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    hipStream_t st = (hipStream_t)stream;
+    if ((st0 = lmh_run_packed<false>(P, (const uint8_t*)packed, st)) != LLIMA_OK) return st0;
+    return lmh_launch_chain(ids, draft_ids, accepted_len, emitted, B, D, st);
 }

@@ -659,6 +659,55 @@ def lm_head_score(hidden: torch.Tensor, weight, target, softcap: float = 0.0,
     return lp, gr == 1
 
 
+def lm_head_verify_greedy(hidden: torch.Tensor, weight, draft_ids: torch.Tensor,
+                          softcap: float = 0.0, logit_dtype: str = "bf16"):
+    """The verification step's LM head and greedy chain rule in one call, no
+    logits written (llima_lm_head_verify_greedy): hidden bf16 [B, D+1, H],
+    draft_ids int [B, D] -> (accepted_len int32 [B], emitted int32 [B, D+1]),
+    as verify_greedy over the logits lm_head_argmax would write (the same
+    softcap and logit_dtype).  weight may be a PackedLmHead."""
+    if hidden.dim() != 3:
+        raise ValueError("hidden must be [B, D+1, H]")
+    B, D1, H = hidden.shape
+    D = D1 - 1
+    packed = isinstance(weight, PackedLmHead)
+    if hidden.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
+        raise ValueError("lm_head_verify_greedy takes bf16 hidden states and weights")
+    if logit_dtype not in ("bf16", "f32"):
+        raise ValueError("logit_dtype must be 'bf16' or 'f32'")
+    x = hidden.contiguous()
+    w = weight.data if packed else weight.contiguous()
+    if packed:
+        if weight.H != H:
+            raise ValueError("hidden width differs from the packed weight's H")
+        V = weight.V
+    else:
+        if w.dim() != 2 or w.shape[1] != H:
+            raise ValueError("weight must be [V, H]")
+        V = w.shape[0]
+    dev = w.device
+    dr = torch.as_tensor(draft_ids).to(device=dev, dtype=torch.int32).contiguous()
+    if tuple(dr.shape) != (B, D):
+        raise ValueError("draft_ids must be [B, D]")
+    _on_gpu(x, w, dr)
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    em = torch.empty((B, D1), dtype=torch.int32, device=dev)
+    nws = (lib().llima_lm_head_verify_greedy_packed_workspace_bytes(B, D, H, V) if packed
+           else lib().llima_lm_head_verify_greedy_workspace_bytes(B, D, V))
+    ws = Workspace.get(dev, "lm_head_verify", nws)
+    ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
+    if packed:
+        st = lib().llima_lm_head_verify_greedy_packed(
+            x.data_ptr(), w.data_ptr(), B, D, H, V, float(softcap), ld, dr.data_ptr(),
+            acc.data_ptr(), em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    else:
+        st = lib().llima_lm_head_verify_greedy(
+            x.data_ptr(), w.data_ptr(), B, D, H, V, float(softcap), ld, dr.data_ptr(),
+            acc.data_ptr(), em.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    check(st, "llima_lm_head_verify_greedy_packed" if packed else "llima_lm_head_verify_greedy")
+    return acc, em
+
+
 def topk(x: torch.Tensor, k: int):
     """topk<T> (utils.hpp:216-281) over the rows of x ([cols] or [rows, cols],
     fp32 or bf16) -> (indices int32 [rows, k], values float32 [rows, k]) in the

@@ -198,4 +198,6 @@ WORKLOADS = {
     "lm_head_argmax_b32_packed": lambda: dict(lm_head_argmax(B=32), name="lm_head_argmax_b32_packed"),
     "lm_head_argmax_b128_packed": lambda: dict(lm_head_argmax(B=128), name="lm_head_argmax_b128_packed"),
     "lm_head_score_b64_packed": lambda: dict(lm_head_argmax(B=64), name="lm_head_score_b64_packed"),
+    "lm_head_verify_b16_d7": lambda: dict(lm_head_argmax(B=128), name="lm_head_verify_b16_d7",
+                                          seqs=16, D=7),
 }

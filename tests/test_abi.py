@@ -158,6 +158,28 @@ def test_host_only_entry_points():
                                         None) == -4
     assert L.llima_lm_head_score_packed(None, p, 0, 256, 1000, 0.0, 1, None, None, None, None,
                                         0, None) == 0
+    # LM head greedy verification: the head's checks over B (D + 1) rows, outputs required
+    wv = L.llima_lm_head_verify_greedy_workspace_bytes(2, 3, 1000)
+    assert wv > L.llima_lm_head_argmax_workspace_bytes(8, 1000)
+    assert L.llima_lm_head_verify_greedy_workspace_bytes(2, -1, 1000) == 0
+    assert L.llima_lm_head_verify_greedy(p, p, 2, -1, 16, 1000, 0.0, 1, p, p, p, p, wv, None) == -1
+    assert L.llima_lm_head_verify_greedy(p, p, 2, 3, 12, 1000, 0.0, 1, p, p, p, p, wv, None) == -1
+    assert L.llima_lm_head_verify_greedy(p, p, 2, 3, 16, 1000, 0.0, 0x101, p, p, p, p, wv,
+                                         None) == -1
+    assert L.llima_lm_head_verify_greedy(p, p, 2, 3, 16, 1000, 0.0, 1, None, p, p, p, wv,
+                                         None) == -1
+    assert L.llima_lm_head_verify_greedy(p, p, 2, 3, 16, 1000, 0.0, 1, p, None, p, p, wv,
+                                         None) == -1
+    assert L.llima_lm_head_verify_greedy(p, p, 2, 3, 16, 1000, 0.0, 1, p, p, p, p, wv - 1,
+                                         None) == -4
+    assert L.llima_lm_head_verify_greedy(None, p, 0, 3, 16, 1000, 0.0, 1, None, None, None,
+                                         None, 0, None) == 0
+    wvp = L.llima_lm_head_verify_greedy_packed_workspace_bytes(2, 3, 256, 1000)
+    assert wvp > 0 and L.llima_lm_head_verify_greedy_packed_workspace_bytes(2, 3, 100, 1000) == 0
+    assert L.llima_lm_head_verify_greedy_packed(p, p, 2, 3, 100, 1000, 0.0, 1, p, p, p, p, wvp,
+                                                None) == -1
+    assert L.llima_lm_head_verify_greedy_packed(p, p, 2, 3, 256, 1000, 0.0, 1, p, p, p, p,
+                                                wvp - 1, None) == -4
     # rejection verification: V % 4 == 0, D <= 255, 16-byte aligned rows
     vw = L.llima_verify_rejection_workspace_bytes(1, 1, 4096)
     assert L.llima_verify_rejection(p, p, 1, 1, 4094, p, p, p, p, p, p, vw, None) == -1

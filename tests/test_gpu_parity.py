@@ -1312,6 +1312,47 @@ def test_lm_head_random_configs(gpu, oracle, seed):
     _score_check(_np(lp), _np(g), _np(logits), targets, oracle)
 
 
+@pytest.mark.parametrize("B,D,H,V,cap,packed", [(1, 0, 4096, 32000, 0.0, False),
+                                                (4, 7, 4096, 128256, 0.0, True),
+                                                (16, 7, 1024, 50000, 30.0, False),
+                                                (9, 3, 256, 777, 0.0, True),
+                                                (3, 15, 512, 5000, 30.0, True),
+                                                (40, 5, 256, 3001, 0.0, False)])
+def test_lm_head_verify_greedy(gpu, B, D, H, V, cap, packed):
+    """llima_lm_head_verify_greedy: accepted lengths and emitted tokens equal the
+    chain rule (resolve_draft_tokens) over the head's own argmax ids, and
+    llima_verify_greedy over the logits the head writes; drafts built so that
+    every acceptance length from 0 to D occurs."""
+    import llima_amd
+    _say("lm head verify greedy", B, D, H, V, cap, packed)
+    rng = np.random.default_rng(B * 13 + D + H + V)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (B * (D + 1), H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    wt = llima_amd.lm_head_pack(_t(w, gpu)) if packed else _t(w, gpu)
+    for ld in ("bf16", "f32"):
+        ids, _, logits = llima_amd.lm_head_argmax(_t(x, gpu), wt, softcap=cap, return_logits=True,
+                                                  logit_dtype=ld)
+        tok = _np(ids).reshape(B, D + 1)
+        drafts = rng.integers(0, V, (B, D)).astype(np.int32)
+        for b in range(B):
+            L = b % (D + 1)
+            drafts[b, :L] = tok[b, :L]
+            if L < D and drafts[b, L] == tok[b, L]:
+                drafts[b, L] = (tok[b, L] + 1) % V
+        hid = _t(x, gpu).view(B, D + 1, H)
+        acc, em = llima_amd.lm_head_verify_greedy(hid, wt, torch_i32(drafts, gpu), softcap=cap,
+                                                  logit_dtype=ld)
+        acc, em = _np(acc), _np(em)
+        for b in range(B):
+            want = llima_amd.resolve_draft_tokens(drafts[b], tok[b])
+            assert acc[b] == len(want) - 1 == min(b % (D + 1), D), (b, acc[b])
+            assert list(em[b, :acc[b] + 1]) == [t for t, _ in want], b
+            assert (em[b, acc[b] + 1:] == -1).all(), b
+        if D + 1 <= 64:
+            acc2, em2 = llima_amd.verify_greedy(logits.reshape(B, D + 1, V), torch_i32(drafts, gpu))
+            assert (_np(acc2) == acc).all() and (_np(em2) == em).all()
+
+
 def torch_i32(a, gpu):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(gpu)
