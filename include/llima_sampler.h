@@ -67,6 +67,8 @@
  *                            (language_model.cpp:29-62), the logits never written
  *   llima_lm_head_verify_greedy(_packed) <- the verification step's LM head +
  *                            _argmax_lm_head_rows + resolve_draft_tokens, no logits
+ *   llima_lm_head_verify_tree(_packed) <- the EAGLE3 tree step's LM head + verify
+ *                            argmax + tree_decoding + evaluate_posterior, no logits
  */
 #ifndef LLIMA_SAMPLER_H
 #define LLIMA_SAMPLER_H
@@ -382,6 +384,29 @@ int llima_lm_head_verify_greedy_packed(const void* hidden, const void* packed, i
                                        int32_t logit_dtype, const int32_t* draft_ids,
                                        int32_t* accepted_len, int32_t* emitted, void* workspace,
                                        size_t workspace_bytes, void* stream);
+
+/* LM head with EAGLE3 tree verification fused: the head's argmax of each of
+ * the K tree rows (hidden bf16 [K][H]; a row whose greatest logit does not
+ * exceed -inf gives 0, as the reference's scan from -inf), then
+ * llima_verify_tree's gather and evaluate_posterior: out[3] = {best path,
+ * accept length, bonus token}.  Replaces the tree step's LM head, its logits
+ * and the verify argmax + tree_decoding + evaluate_posterior
+ * (sima_lmm/devkit/cpp/language_model_eagle3.cpp:486-567,
+ * sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195): no [K][V] logits are
+ * written.  Sizes and alignment as llima_lm_head_argmax; the _packed form
+ * takes a weight from llima_lm_head_pack.  LLIMA_LOGITS_OUT_BF16 is rejected. */
+size_t llima_lm_head_verify_tree_workspace_bytes(int32_t K, int32_t V);
+int llima_lm_head_verify_tree(const void* hidden, const void* weight, int32_t K, int32_t H,
+                              int32_t V, float softcap, int32_t logit_dtype,
+                              const int32_t* retrieve_indices, const int32_t* candidates,
+                              int32_t n_paths, int32_t L, int32_t* out, void* workspace,
+                              size_t workspace_bytes, void* stream);
+size_t llima_lm_head_verify_tree_packed_workspace_bytes(int32_t K, int32_t H, int32_t V);
+int llima_lm_head_verify_tree_packed(const void* hidden, const void* packed, int32_t K,
+                                     int32_t H, int32_t V, float softcap, int32_t logit_dtype,
+                                     const int32_t* retrieve_indices, const int32_t* candidates,
+                                     int32_t n_paths, int32_t L, int32_t* out, void* workspace,
+                                     size_t workspace_bytes, void* stream);
 
 /* Heap top-k of each of `rows` rows of `cols` values (row r at x + r*row_stride
  * elements), exactly as topk<T> (sima_lmm/devkit/cpp/utils.hpp:216-281):

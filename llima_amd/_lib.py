@@ -72,6 +72,13 @@ SIGNATURES = {
     "llima_lm_head_verify_greedy_packed": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _i32,
                                                           ctypes.c_float, _i32, _vp, _vp, _vp,
                                                           _vp, _sz, _vp]),
+    "llima_lm_head_verify_tree_workspace_bytes": (_sz, [_i32, _i32]),
+    "llima_lm_head_verify_tree": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, ctypes.c_float,
+                                                 _i32, _vp, _vp, _i32, _i32, _vp, _vp, _sz, _vp]),
+    "llima_lm_head_verify_tree_packed_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "llima_lm_head_verify_tree_packed": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32,
+                                                        ctypes.c_float, _i32, _vp, _vp, _i32,
+                                                        _i32, _vp, _vp, _sz, _vp]),
     "llima_topk": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i64, _i32, _vp, _vp, _vp]),
     "llima_eagle3_tree_bytes": (_sz, [_i32, _i32]),
     "llima_eagle3_tree_begin": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp,

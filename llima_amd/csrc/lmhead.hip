@@ -611,6 +611,35 @@ __global__ __launch_bounds__(LLIMA_WG) void lmh_chain(const int32_t* ids, const 
     accepted_len[g] = acc;
 }
 
+// EAGLE3 tree verification from the head's ids, one thread: each row's token
+// is its argmax when the row's maximum exceeds -inf, else 0 (the reference's
+// scan starts from -inf with a strict >, sima_lmm/devkit/cpp/language_model_eagle3.cpp:486-522);
+// the targets gathered along each path (-1 -> the last row), the first path
+// with the strictly longest accepted prefix, its bonus token
+// (sima_lmm/devkit/cpp/eagle_helpers.hpp:153-195).
+__global__ void lmh_tree(const int32_t* ids, const float* vals, int K, const int32_t* retrieve,
+                         const int32_t* candidates, int n_paths, int L, int32_t* out) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    auto tok = [&](int r) { return vals[r] > -__builtin_inff() ? ids[r] : 0; };
+    int32_t best_c = 0, max_acc = 0;
+    for (int p = 0; p < n_paths; ++p) {
+        int32_t acc = 0;
+        for (int i = 0; i + 1 < L; ++i) {
+            int32_t idx = retrieve[p * L + i];
+            if (idx < 0 || idx >= K) idx = K - 1;
+            const int32_t nxt = candidates[p * L + i + 1];
+            if (nxt < 0 || tok(idx) != nxt) break;
+            ++acc;
+        }
+        if (acc > max_acc) { max_acc = acc; best_c = p; }
+    }
+    int32_t idx = retrieve[best_c * L + max_acc];
+    if (idx < 0 || idx >= K) idx = K - 1;
+    out[0] = best_c;
+    out[1] = max_acc;
+    out[2] = tok(idx);
+}
+
 // ------------------------------------------------------------------ packed weights
 // A weight prepacked once (at model load) in the order the MFMA reads it:
 // fragment (rb, s) is 1 KB, lane l's 16 bytes being
@@ -961,6 +990,60 @@ extern "C" int llima_lm_head_verify_greedy(const void* hidden, const void* weigh
     return lmh_launch_chain(ids, draft_ids, accepted_len, emitted, B, D, st);
 }
 
+// Workspace of the tree entry points: the head's own, then the K rows' ids
+// and values.
+static size_t lmh_tree_ws(size_t head, int K) {
+    return head == 0 ? 0 : head + 2 * lmh_align256((size_t)K * 4);
+}
+
+static int lmh_tree_check(int32_t K, const int32_t* retrieve, const int32_t* candidates,
+                          int32_t n_paths, int32_t L, const int32_t* out) {
+    if (K <= 0 || n_paths <= 0 || L <= 0 || !retrieve || !candidates || !out) return LLIMA_E_INVAL;
+    if ((int64_t)n_paths * L > (int64_t)INT32_MAX) return LLIMA_E_INVAL;
+    return LLIMA_OK;
+}
+
+static int lmh_launch_tree(const LmhParams& P, const int32_t* retrieve, const int32_t* candidates,
+                           int32_t n_paths, int32_t L, int32_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(lmh_tree, dim3(1), dim3(64), 0, st, (const int32_t*)P.out_ids,
+                       (const float*)P.out_vals, P.B, retrieve, candidates, (int)n_paths, (int)L,
+                       out);
+    return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
+}
+
+extern "C" size_t llima_lm_head_verify_tree_workspace_bytes(int32_t K, int32_t V) {
+    if (K <= 0) return 0;
+    return lmh_tree_ws(llima_lm_head_argmax_workspace_bytes(K, V), K);
+}
+
+extern "C" int llima_lm_head_verify_tree(const void* hidden, const void* weight, int32_t K,
+                                         int32_t H, int32_t V, float softcap, int32_t logit_dtype,
+                                         const int32_t* retrieve_indices, const int32_t* candidates,
+                                         int32_t n_paths, int32_t L, int32_t* out, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+    int st0 = lmh_tree_check(K, retrieve_indices, candidates, n_paths, L, out);
+    if (st0 != LLIMA_OK) return st0;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    if ((st0 = lmh_check_plain(hidden, weight, K, H, V)) != LLIMA_OK) return st0;
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
+    if (!workspace || workspace_bytes < llima_lm_head_verify_tree_workspace_bytes(K, V))
+        return LLIMA_E_WORKSPACE;
+    uint8_t* rest = (uint8_t*)workspace + llima_lm_head_argmax_workspace_bytes(K, V);
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.weight = (const uint16_t*)weight;
+    P.keys = (uint64_t*)workspace;
+    P.out_ids = (int32_t*)rest;
+    P.out_vals = (float*)(rest + lmh_align256((size_t)K * 4));
+    P.B = K; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    hipStream_t st = (hipStream_t)stream;
+    if ((st0 = lmh_run_plain<false>(P, st)) != LLIMA_OK) return st0;
+    return lmh_launch_tree(P, retrieve_indices, candidates, n_paths, L, out, st);
+}
+
 extern "C" size_t llima_lm_head_score_workspace_bytes(int32_t B, int32_t V) {
     if (B <= 0 || V <= 0) return 0;
     return lmh_ws_bytes(B, lmh_plain_slots(V), true);
@@ -1151,4 +1234,39 @@ extern "C" int llima_lm_head_verify_greedy_packed(const void* hidden, const void
     hipStream_t st = (hipStream_t)stream;
     if ((st0 = lmh_run_packed<false>(P, (const uint8_t*)packed, st)) != LLIMA_OK) return st0;
     return lmh_launch_chain(ids, draft_ids, accepted_len, emitted, B, D, st);
+}
+
+extern "C" size_t llima_lm_head_verify_tree_packed_workspace_bytes(int32_t K, int32_t H, int32_t V) {
+    if (K <= 0) return 0;
+    return lmh_tree_ws(llima_lm_head_argmax_packed_workspace_bytes(K, H, V), K);
+}
+
+extern "C" int llima_lm_head_verify_tree_packed(const void* hidden, const void* packed, int32_t K,
+                                                int32_t H, int32_t V, float softcap,
+                                                int32_t logit_dtype,
+                                                const int32_t* retrieve_indices,
+                                                const int32_t* candidates, int32_t n_paths,
+                                                int32_t L, int32_t* out, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+    int st0 = lmh_tree_check(K, retrieve_indices, candidates, n_paths, L, out);
+    if (st0 != LLIMA_OK) return st0;
+    if (llima_lm_head_packed_bytes(V, H) == 0 || !packed || !hidden) return LLIMA_E_INVAL;
+    if (logit_dtype & LLIMA_LOGITS_OUT_BF16) return LLIMA_E_INVAL;       // no logits output
+    int32_t logits_bf16 = 0;
+    if ((st0 = lmh_check_dtype(softcap, &logit_dtype, &logits_bf16)) != LLIMA_OK) return st0;
+    if ((uintptr_t)packed % 16 || (uintptr_t)hidden % 16) return LLIMA_E_INVAL;
+    if (!workspace || workspace_bytes < llima_lm_head_verify_tree_packed_workspace_bytes(K, H, V))
+        return LLIMA_E_WORKSPACE;
+    uint8_t* rest = (uint8_t*)workspace + llima_lm_head_argmax_packed_workspace_bytes(K, H, V);
+    LmhParams P = {};
+    P.hidden = (const uint16_t*)hidden;
+    P.keys = (uint64_t*)workspace;
+    P.out_ids = (int32_t*)rest;
+    P.out_vals = (float*)(rest + lmh_align256((size_t)K * 4));
+    P.B = K; P.H = H; P.V = V;
+    P.cap = softcap;
+    P.round_bf16 = logit_dtype == LLIMA_BF16;
+    hipStream_t st = (hipStream_t)stream;
+    if ((st0 = lmh_run_packed<false>(P, (const uint8_t*)packed, st)) != LLIMA_OK) return st0;
+    return lmh_launch_tree(P, retrieve_indices, candidates, n_paths, L, out, st);
 }

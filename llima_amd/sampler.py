@@ -708,6 +708,50 @@ def lm_head_verify_greedy(hidden: torch.Tensor, weight, draft_ids: torch.Tensor,
     return acc, em
 
 
+def lm_head_verify_tree(hidden: torch.Tensor, weight, retrieve_indices: torch.Tensor,
+                        candidates: torch.Tensor, softcap: float = 0.0,
+                        logit_dtype: str = "bf16"):
+    """The EAGLE3 tree step's LM head and verification in one call, no logits
+    written (llima_lm_head_verify_tree): hidden bf16 [K, H] (the tree rows),
+    retrieve_indices and candidates [n_paths, L] -> (best_candidate,
+    accept_length, bonus_token), as verify_tree over the logits lm_head_argmax
+    would write.  weight may be a PackedLmHead."""
+    x = hidden.contiguous()
+    packed = isinstance(weight, PackedLmHead)
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or (not packed and weight.dtype != torch.bfloat16):
+        raise ValueError("lm_head_verify_tree takes bf16 hidden rows [K, H] and a bf16 weight")
+    if logit_dtype not in ("bf16", "f32"):
+        raise ValueError("logit_dtype must be 'bf16' or 'f32'")
+    K, H = x.shape
+    w = weight.data if packed else weight.contiguous()
+    if packed:
+        if weight.H != H:
+            raise ValueError("hidden width differs from the packed weight's H")
+        V = weight.V
+    else:
+        if w.dim() != 2 or w.shape[1] != H:
+            raise ValueError("weight must be [V, H]")
+        V = w.shape[0]
+    dev = w.device
+    ri = retrieve_indices.to(device=dev, dtype=torch.int32).contiguous()
+    ca = candidates.to(device=dev, dtype=torch.int32).contiguous()
+    if ri.shape != ca.shape or ri.dim() != 2:
+        raise ValueError("retrieve_indices and candidates must both be [n_paths, L]")
+    P, L = ri.shape
+    _on_gpu(x, w, ri, ca)
+    out = torch.empty(3, dtype=torch.int32, device=dev)
+    nws = (lib().llima_lm_head_verify_tree_packed_workspace_bytes(K, H, V) if packed
+           else lib().llima_lm_head_verify_tree_workspace_bytes(K, V))
+    ws = Workspace.get(dev, "lm_head_tree", nws)
+    ld = _lib.LLIMA_BF16 if logit_dtype == "bf16" else _lib.LLIMA_F32
+    fn = lib().llima_lm_head_verify_tree_packed if packed else lib().llima_lm_head_verify_tree
+    check(fn(x.data_ptr(), w.data_ptr(), K, H, V, float(softcap), ld, ri.data_ptr(),
+             ca.data_ptr(), P, L, out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "llima_lm_head_verify_tree_packed" if packed else "llima_lm_head_verify_tree")
+    o = out.tolist()
+    return o[0], o[1], o[2]
+
+
 def topk(x: torch.Tensor, k: int):
     """topk<T> (utils.hpp:216-281) over the rows of x ([cols] or [rows, cols],
     fp32 or bf16) -> (indices int32 [rows, k], values float32 [rows, k]) in the

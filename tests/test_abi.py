@@ -180,6 +180,23 @@ def test_host_only_entry_points():
                                                 None) == -1
     assert L.llima_lm_head_verify_greedy_packed(p, p, 2, 3, 256, 1000, 0.0, 1, p, p, p, p,
                                                 wvp - 1, None) == -4
+    # LM head tree verification: K, n_paths, L positive, the index arrays and out required
+    wt = L.llima_lm_head_verify_tree_workspace_bytes(16, 1000)
+    assert wt > L.llima_lm_head_argmax_workspace_bytes(16, 1000)
+    assert L.llima_lm_head_verify_tree_workspace_bytes(0, 1000) == 0
+    assert L.llima_lm_head_verify_tree(p, p, 0, 16, 1000, 0.0, 1, p, p, 2, 3, p, p, wt, None) == -1
+    assert L.llima_lm_head_verify_tree(p, p, 16, 16, 1000, 0.0, 1, p, p, 0, 3, p, p, wt, None) == -1
+    assert L.llima_lm_head_verify_tree(p, p, 16, 16, 1000, 0.0, 1, None, p, 2, 3, p, p, wt,
+                                       None) == -1
+    assert L.llima_lm_head_verify_tree(p, p, 16, 12, 1000, 0.0, 1, p, p, 2, 3, p, p, wt, None) == -1
+    assert L.llima_lm_head_verify_tree(p, p, 16, 16, 1000, 0.0, 0x101, p, p, 2, 3, p, p, wt,
+                                       None) == -1
+    assert L.llima_lm_head_verify_tree(p, p, 16, 16, 1000, 0.0, 1, p, p, 2, 3, p, p, wt - 1,
+                                       None) == -4
+    wtp = L.llima_lm_head_verify_tree_packed_workspace_bytes(16, 256, 1000)
+    assert wtp > 0 and L.llima_lm_head_verify_tree_packed_workspace_bytes(16, 100, 1000) == 0
+    assert L.llima_lm_head_verify_tree_packed(p, p, 16, 256, 1000, 0.0, 1, p, p, 2, 3, p, p,
+                                              wtp - 1, None) == -4
     # rejection verification: V % 4 == 0, D <= 255, 16-byte aligned rows
     vw = L.llima_verify_rejection_workspace_bytes(1, 1, 4096)
     assert L.llima_verify_rejection(p, p, 1, 1, 4094, p, p, p, p, p, p, vw, None) == -1

@@ -1353,6 +1353,35 @@ def test_lm_head_verify_greedy(gpu, B, D, H, V, cap, packed):
             assert (_np(acc2) == acc).all() and (_np(em2) == em).all()
 
 
+@pytest.mark.parametrize("K,H,V,packed", [(16, 4096, 128256, False), (16, 4096, 32000, True),
+                                           (26, 512, 5000, True), (5, 256, 777, False)])
+def test_lm_head_verify_tree(gpu, oracle, K, H, V, packed):
+    """llima_lm_head_verify_tree: (best path, accept length, bonus) equal
+    llima_verify_tree over the head's logits and the oracle's gather +
+    evaluate_posterior over the head's argmax, with paths built to match."""
+    import llima_amd
+    _say("lm head verify tree", K, H, V, packed)
+    rng = np.random.default_rng(K + H + V)
+    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (K, H)).astype(np.float32))
+    w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    wt = llima_amd.lm_head_pack(_t(w, gpu)) if packed else _t(w, gpu)
+    ids, _, logits = llima_amd.lm_head_argmax(_t(x, gpu), wt, return_logits=True)
+    row_tok = _np(ids)
+    for trial in range(4):
+        P, L = 10, 5
+        ri = rng.integers(-1, K, size=(P, L)).astype(np.int32)
+        gathered = oracle.tree_gather(row_tok, ri)
+        cand = rng.integers(0, V, size=(P, L)).astype(np.int32)
+        for p in range(P):
+            m = rng.integers(0, L)
+            cand[p, 1:m + 1] = gathered[p, :m]
+        cand[rng.random((P, L)) < 0.05] = -1
+        exp = oracle.evaluate_posterior(gathered, cand)
+        got = llima_amd.lm_head_verify_tree(_t(x, gpu), wt, _t(ri, gpu), _t(cand, gpu))
+        assert got == exp, (trial, got, exp)
+        assert got == llima_amd.verify_tree(logits, _t(ri, gpu), _t(cand, gpu)), trial
+
+
 def torch_i32(a, gpu):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(gpu)
