@@ -1362,11 +1362,14 @@ def test_lm_head_verify_tree(gpu, oracle, K, H, V, packed):
     import llima_amd
     _say("lm head verify tree", K, H, V, packed)
     rng = np.random.default_rng(K + H + V)
-    x = wl.f32_to_bf16_bits(rng.normal(0, 1, (K, H)).astype(np.float32))
+    xf = rng.normal(0, 1, (K, H)).astype(np.float32)
+    xf[K // 2] = np.nan                         # a row with no logit above -inf: token 0
+    x = wl.f32_to_bf16_bits(xf)
     w = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
     wt = llima_amd.lm_head_pack(_t(w, gpu)) if packed else _t(w, gpu)
     ids, _, logits = llima_amd.lm_head_argmax(_t(x, gpu), wt, return_logits=True)
     row_tok = _np(ids)
+    assert row_tok[K // 2] == 0 and np.isnan(_np(logits)[K // 2]).all()
     for trial in range(4):
         P, L = 10, 5
         ri = rng.integers(-1, K, size=(P, L)).astype(np.int32)
@@ -1376,6 +1379,9 @@ def test_lm_head_verify_tree(gpu, oracle, K, H, V, packed):
             m = rng.integers(0, L)
             cand[p, 1:m + 1] = gathered[p, :m]
         cand[rng.random((P, L)) < 0.05] = -1
+        ri[0, :] = K // 2                       # one path through the NaN row (token 0)
+        gathered = oracle.tree_gather(row_tok, ri)
+        cand[0, 1:] = 0
         exp = oracle.evaluate_posterior(gathered, cand)
         got = llima_amd.lm_head_verify_tree(_t(x, gpu), wt, _t(ri, gpu), _t(cand, gpu))
         assert got == exp, (trial, got, exp)
