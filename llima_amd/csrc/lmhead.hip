@@ -32,6 +32,11 @@
 // target and the first-maximum flag of score_logits
 // (sima_lmm/devkit/cpp/language_model.cpp:29-62) over the logits as the
 // argmax sees them, so scoring never writes or reads the [B][V] logits.
+//
+// Verification through the head: the argmax of every draft row, then
+// lmh_chain (greedy chains, one thread per sequence) or lmh_tree (the EAGLE3
+// tree, one thread) applies the rule of llima_verify_greedy / llima_verify_tree
+// to the ids, again with no logits written.
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
 
