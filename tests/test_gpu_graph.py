@@ -1,5 +1,6 @@
 """HIP graph replay: one llima_sample call (the sweep + finish kernels, or the
-dense path) and one llima_verify_rejection call (and one llima_lm_head_score_packed call) captured into a graph through
+dense path), one llima_verify_rejection call, and the LM head's scoring and
+greedy verification entry points captured into graphs through
 the C ABI, then replayed several times.  Between replays the program's own
 eager work writes new inputs into the captured buffers and synchronises; every
 replay is checked against the oracle on that replay's inputs."""
@@ -182,3 +183,66 @@ def test_lm_head_score_graph_replays(gpu, oracle):
         for r in range(B):
             olp, og = oracle.score_logits(lg[r], int(ts[i][r]))
             assert abs(got_lp[r] - olp) <= 1e-5 and bool(got_g[r]) == og, (i, r)
+
+
+def test_lm_head_verify_greedy_graph_replays(gpu):
+    """llima_lm_head_verify_greedy captured through the C ABI (the head's passes,
+    lmh_finish and lmh_chain): each replay, on new hidden rows and drafts,
+    equals an eager call."""
+    import torch
+    import llima_amd
+    from llima_amd import _lib
+    _say("graph replay llima_lm_head_verify_greedy")
+    L = _lib.lib()
+    rng = np.random.default_rng(78)
+    B, D, H, V = 6, 4, 512, 9000
+    xs = [wl.f32_to_bf16_bits(rng.normal(0, 1, (B * (D + 1), H)).astype(np.float32))
+          for _ in range(REPLAYS)]
+    wf = wl.f32_to_bf16_bits(rng.normal(0, 4.0 / np.sqrt(H), (V, H)).astype(np.float32))
+    w = torch.from_numpy(wf.view(np.int16)).to(gpu).view(torch.bfloat16)
+    x = torch.empty((B, D + 1, H), dtype=torch.bfloat16, device=gpu)
+    dr = torch.empty((B, D), dtype=torch.int32, device=gpu)
+    acc = torch.empty(B, dtype=torch.int32, device=gpu)
+    em = torch.empty((B, D + 1), dtype=torch.int32, device=gpu)
+    nws = L.llima_lm_head_verify_greedy_workspace_bytes(B, D, V)
+    ws = torch.empty(nws, dtype=torch.uint8, device=gpu)
+
+    def launch(stream):
+        rc = L.llima_lm_head_verify_greedy(x.data_ptr(), w.data_ptr(), B, D, H, V, 0.0,
+                                           _lib.LLIMA_BF16, dr.data_ptr(), acc.data_ptr(),
+                                           em.data_ptr(), ws.data_ptr(), nws, stream)
+        assert rc == 0
+
+    drafts = []
+    for i in range(REPLAYS):                     # drafts matching a prefix of the head's ids
+        xi = torch.from_numpy(xs[i].view(np.int16)).to(gpu).view(torch.bfloat16)
+        tok = llima_amd.lm_head_argmax(xi, w)[0].cpu().numpy().reshape(B, D + 1)
+        d = rng.integers(0, V, (B, D)).astype(np.int32)
+        for b in range(B):
+            d[b, :b % (D + 1)] = tok[b, :b % (D + 1)]
+        drafts.append(d)
+
+    def load(i):
+        x.copy_(torch.from_numpy(xs[i].view(np.int16)).view(torch.bfloat16).view(B, D + 1, H))
+        dr.copy_(torch.from_numpy(drafts[i]))
+
+    load(0)
+    launch(torch.cuda.current_stream(gpu).cuda_stream)        # eager warmup
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(gpu)
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        launch(cap.cuda_stream)
+    torch.cuda.synchronize(gpu)
+    for i in range(REPLAYS):
+        load(i)
+        acc.fill_(-7)
+        em.fill_(-7)
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        got_a, got_e = acc.cpu().numpy().copy(), em.cpu().numpy().copy()
+        ea, ee = llima_amd.lm_head_verify_greedy(x, w, dr)
+        assert (got_a == ea.cpu().numpy()).all() and (got_e == ee.cpu().numpy()).all(), i
+        assert (got_a >= np.arange(B) % (D + 1)).all(), i      # the planted prefixes accepted
