@@ -88,7 +88,8 @@ enum {
     LLIMA_E_RANGE = -2,      /* id or length out of range */
     LLIMA_E_HIP = -3,        /* the HIP runtime reported an error at launch */
     LLIMA_E_WORKSPACE = -4,  /* workspace missing or too small */
-    LLIMA_E_SCRATCH = -5     /* the call needs more than the static scratch holds */
+    LLIMA_E_SCRATCH = -5,    /* the call needs more than the static scratch holds */
+    LLIMA_E_CAPTURE = -6     /* a first call on a device made under stream capture */
 };
 
 enum { LLIMA_F32 = 0, LLIMA_BF16 = 1 };
@@ -197,7 +198,10 @@ int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_
  * (e.g. B*ceil(V/4096) <= 8192 for fp32 rows, B*ceil(V/8192) <= 8192 for bf16).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams, or different host threads without ordering) race.
- * Results are those of llima_sample on the same inputs. */
+ * The first call on a device looks the array's address up (once) and must be
+ * made outside stream capture: made under capture it launches nothing and
+ * returns LLIMA_E_CAPTURE.  Later calls on that device may be captured and
+ * replayed.  Results are those of llima_sample on the same inputs. */
 size_t llima_sample_noalloc_max_bytes(void);
 int llima_sample_noalloc(const void* logits, int32_t dtype, int32_t B, int32_t V,
                          int64_t row_stride, const int32_t* history, const int32_t* history_len,
@@ -457,7 +461,9 @@ int llima_eagle3_tree_finish(void* tree, size_t tree_bytes, int32_t K, int32_t d
  * set as a bitmask over V ids ([ceil(V/32)] uint32, bit id & 31 of word id >> 5,
  * LSB first); ids outside [0, V) never stop.  out_keep[B]: tokens to keep;
  * out_status[B] (nullable): LLIMA_STOP_TOKEN when a stop token ended the run,
- * else LLIMA_STOP_CACHE_FULL when room cut it, else LLIMA_STOP_NONE. */
+ * else LLIMA_STOP_CACHE_FULL when the run reached room[b] (cut there, or
+ * filling it exactly: language_model_gemma4_mtp.cpp:953-955, 1011-1012), else
+ * LLIMA_STOP_NONE. */
 enum { LLIMA_STOP_NONE = 0, LLIMA_STOP_TOKEN = 1, LLIMA_STOP_CACHE_FULL = 2 };
 int llima_stop_check(const int32_t* tokens, const int32_t* count, int32_t B, int32_t M,
                      const uint32_t* stop_mask, int32_t V, const int32_t* room,

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libllima_sampler.so")
 
 LLIMA_OK, LLIMA_E_INVAL, LLIMA_E_RANGE, LLIMA_E_HIP, LLIMA_E_WORKSPACE = 0, -1, -2, -3, -4
 LLIMA_E_SCRATCH = -5
+LLIMA_E_CAPTURE = -6
 LLIMA_F32, LLIMA_BF16 = 0, 1
 LLIMA_LOGITS_OUT_BF16 = 0x100   # with LLIMA_BF16 in the LM head's logit_dtype: bf16 logits out
 ARGMAX_SPLIT_FIRST, ARGMAX_NEG_INF, ARGMAX_QUARTERS, ARGMAX_LOWEST = 0, 1, 2, 3

@@ -571,6 +571,7 @@ extern "C" const char* llima_status_string(int status) {
         case LLIMA_E_HIP: return "HIP launch error";
         case LLIMA_E_WORKSPACE: return "workspace missing or too small";
         case LLIMA_E_SCRATCH: return "call exceeds the library's static scratch";
+        case LLIMA_E_CAPTURE: return "first call on this device made under stream capture";
         default: return "unknown status";
     }
 }

@@ -3293,12 +3293,18 @@ static __device__ __align__(256) uint64_t scratch[LLIMA_SAMPLE_SCRATCH_BYTES / s
 static std::mutex g_scratch_mu;
 static void* g_scratch_dev[LLIMA_SCRATCH_MAX_DEVICES];   // guarded by g_scratch_mu
 
-static int scratch_of_current_device(void** out) {
+static int scratch_of_current_device(hipStream_t stream, void** out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= LLIMA_SCRATCH_MAX_DEVICES)
         return LLIMA_E_HIP;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_dev[dev]) {
+        // the lookup may load the library's code object on this device, which
+        // is no stream operation a capture could record: the first call on a
+        // device must come before any capture
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return LLIMA_E_HIP;
+        if (cs != hipStreamCaptureStatusNone) return LLIMA_E_CAPTURE;
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LLIMA_E_HIP;
         g_scratch_dev[dev] = p;
@@ -3321,7 +3327,7 @@ extern "C" int llima_sample_noalloc(const void* logits, int32_t dtype, int32_t B
                             uniforms, cfg, out_ids, out_probs, out_keep, nullptr, 0, stream);
     if (need > LLIMA_SAMPLE_SCRATCH_BYTES) return LLIMA_E_SCRATCH;
     void* ws = nullptr;
-    const int rc = scratch_of_current_device(&ws);
+    const int rc = scratch_of_current_device((hipStream_t)stream, &ws);
     if (rc != LLIMA_OK) return rc;
     return llima_sample(logits, dtype, B, V, row_stride, history, history_len, H_max, bitmask,
                         uniforms, cfg, out_ids, out_probs, out_keep, ws,

@@ -32,8 +32,11 @@ __global__ __launch_bounds__(LLIMA_WG) void stop_check_kernel(StopParams P) {
     n = n < 0 ? 0 : (n > P.M ? P.M : n);
     int cap = n, status = LLIMA_STOP_NONE;
     if (P.room) {
+        // a run that reaches the room fills the cache, also when it fits
+        // exactly (language_model_gemma4_mtp.cpp:953-955, 1011-1012;
+        // language_model_dflash.cpp:625-626); a stop token inside it wins
         const int r = P.room[b] < 0 ? 0 : P.room[b];
-        if (r < n) { cap = r; status = LLIMA_STOP_CACHE_FULL; }
+        if (r <= n) { cap = r; status = LLIMA_STOP_CACHE_FULL; }
     }
     const int32_t* tk = P.tokens + (size_t)b * P.M;
     int keep = cap;

@@ -832,6 +832,20 @@ class Eagle3DraftTree:
         self.level += 1
         return ids, prow, mask
 
+    def node_scores(self) -> torch.Tensor:
+        """The cumulative log-probability of every node grown so far, in the
+        reference's flat order (scores_list flattened, language_model_eagle3.cpp:
+        1040-1048): the K root scores, then K*K per level.  A float32 view into
+        the tree state, whose regions (each on a 256-byte boundary) are: the
+        current scores [K], the parent groups [1 + (depth-1)K], the node
+        scores, ..."""
+        def take(o, nbytes):
+            return o + ((nbytes + 255) & ~255)
+        K, depth = self.K, self.depth
+        off = take(take(0, 4 * K), 4 * (1 + (depth - 1) * K))
+        n = K + (self.level - 1) * K * K if self.level else 0
+        return self.state[off:off + 4 * n].view(torch.float32)
+
     def finish(self, total_tokens: int, sample_token: int):
         if self.level != self.depth:
             raise RuntimeError("finish: grow depth - 1 levels first")

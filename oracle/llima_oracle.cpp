@@ -791,7 +791,8 @@ static int32_t lower_pos(const int32_t* sorted, int n, int32_t q) {
 int orc_eagle3_tree(const void* root_logits, const void* level_logits, int dtype, int Vd,
                     const int32_t* d2t, int K, int depth, int total_tokens, int32_t sample_token,
                     int cr, int32_t* inputs, int32_t* prow, float* masks, int32_t* tokens,
-                    float* mask, int32_t* pos, int32_t* retrieve, int32_t* dims) {
+                    float* mask, int32_t* pos, int32_t* retrieve, int32_t* dims,
+                    float* node_scores) {
     if (K < 1 || K > 32 || depth < 1 || Vd < K || total_tokens < 1 || total_tokens > 32)
         return ORC_E_INVAL;
     const int n_nodes = K + (depth - 1) * K * K;
@@ -854,6 +855,7 @@ int orc_eagle3_tree(const void* root_logits, const void* level_logits, int dtype
         std::copy(am.begin(), am.end(), masks + (size_t)i * K * mcols);
     }
     // finish
+    if (node_scores) std::copy(node_score.begin(), node_score.end(), node_scores);
     std::vector<int32_t> sel(total_tokens);
     std::vector<float> selv(total_tokens);
     heap_topk([&](int64_t q) { return node_score[q]; }, n_nodes, total_tokens, sel.data(),
@@ -914,7 +916,9 @@ int orc_stop_check(const int32_t* tokens, const int32_t* count, int B, int M,
     for (int b = 0; b < B; ++b) {
         int n = count ? std::min(std::max(count[b], 0), M) : M;
         int s = 0;
-        if (room && std::max(room[b], 0) < n) { n = std::max(room[b], 0); s = 2; }
+        // reaching the room fills the cache, also exactly (language_model_gemma4_mtp.cpp:
+        // 953-955 sets cache_full after the append that reaches max_length)
+        if (room && std::max(room[b], 0) <= n) { n = std::max(room[b], 0); s = 2; }
         int k = n;
         for (int i = 0; i < n; ++i) {
             if (std::binary_search(st.begin(), st.end(), tokens[(size_t)b * M + i])) {

@@ -331,15 +331,17 @@ def eagle3_tree(root_logits, level_logits, d2t, K: int, depth: int, total_tokens
     pos = np.zeros(N, np.int32)
     retrieve = np.zeros((N, N), np.int32)
     dims = np.zeros(2, np.int32)
+    node_scores = np.zeros(K + (depth - 1) * K * K, np.float32)
     rc = lib().orc_eagle3_tree(_ptr(r), _ptr(lv), dt, Vd, _ptr(d), K, depth, total_tokens,
                                int(sample_token), int(cr), _ptr(inputs), _ptr(prow), _ptr(masks),
-                               _ptr(tokens), _ptr(mask), _ptr(pos), _ptr(retrieve), _ptr(dims))
+                               _ptr(tokens), _ptr(mask), _ptr(pos), _ptr(retrieve), _ptr(dims),
+                               _ptr(node_scores))
     if rc:
         raise ValueError(f"orc_eagle3_tree rc={rc}")
     leaves, rcols = int(dims[0]), int(dims[1])
     return dict(inputs=inputs, parent_rows=prow[:depth - 1], masks=masks[:depth - 1],
                 tokens=tokens, tree_mask=mask, position_ids=pos,
-                retrieve=retrieve[:leaves, :rcols])
+                retrieve=retrieve[:leaves, :rcols], node_scores=node_scores)
 
 
 def stop_check(tokens, stop_ids, count=None, room=None):

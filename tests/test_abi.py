@@ -36,6 +36,7 @@ def test_host_only_entry_points():
     L = lib()
     assert L.llima_abi_version() == 2
     assert L.llima_status_string(-4).decode() == "workspace missing or too small"
+    assert L.llima_status_string(-6).decode() == "first call on this device made under stream capture"
     assert L.llima_sample_workspace_bytes(64, 128256, 0) > 0
     assert L.llima_argmax_workspace_bytes(0, 10, 0) == 0
     # argument validation happens before any launch

@@ -87,6 +87,12 @@ def _run_tree(gpu, oracle, root, levels, d2t, K, depth, total, sample):
         assert (_np(ids) == e["inputs"][lv]).all(), lv
         assert (_np(prow) == e["parent_rows"][lv - 1]).all(), lv
         assert (_np(mask) == e["masks"][lv - 1][:, :K * (lv + 1)]).all(), lv
+    # the node scores themselves (log-softmax plus the parent's score), to 1e-5
+    # relative: the kernels and this oracle round exp/log the same way, so they
+    # agree far closer than that
+    ns = _np(tree.node_scores())
+    assert ns.shape == e["node_scores"].shape
+    assert np.allclose(ns, e["node_scores"], rtol=1e-5, atol=1e-6, equal_nan=True)
     out = tree.finish(total, sample)
     assert (_np(out["tokens"]) == e["tokens"]).all()
     assert (_np(out["tree_mask"]) == e["tree_mask"]).all()

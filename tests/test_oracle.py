@@ -495,6 +495,12 @@ def test_stop_check_reference_rule(oracle):
     assert list(keep) == [3, 1, 4, 3, 3] and list(status) == [1, 1, 0, 1, 1]
     keep, status = oracle.stop_check(toks, stop, count=[4, 4, 2, 1, 4], room=[2, 9, 9, 9, 0])
     assert list(keep) == [2, 1, 2, 1, 0] and list(status) == [2, 1, 0, 0, 2]
+    # a run that fills the room exactly: the MTP loop appends the last token,
+    # finds input_ids.size() >= max_length and flags the cache full
+    # (language_model_gemma4_mtp.cpp:953-955); a stop token at that last
+    # position is checked first (:948-951) and wins
+    keep, status = oracle.stop_check(toks, stop, count=[2, 4, 4, 3, 0], room=[2, 1, 4, 3, 0])
+    assert list(keep) == [2, 1, 4, 3, 0] and list(status) == [2, 1, 2, 1, 2]
 
 
 def test_calc_next_token_id_omp4_matches_quarters_rule(oracle):

@@ -99,3 +99,67 @@ def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
     rc = L.llima_sample_noalloc(p, 0, 4096, 128256, 128256, None, None, 0, None, p,
                                 ctypes.byref(cfg), p, None, None, None)
     assert rc == _lib.LLIMA_E_SCRATCH
+
+
+def test_noalloc_graph_replays(gpu, oracle):
+    """llima_sample_noalloc captured into a HIP graph (its first call on the
+    device made eagerly, as the header requires) and replayed on new inputs
+    loaded into the captured buffers between replays: every replay equals the
+    oracle on that replay's inputs and an eager llima_sample call with a
+    workspace, bit for bit."""
+    import torch
+    from llima_amd import SamplerConfig, _lib
+    from oracle.oracle import SamplerConfig as OC
+    L = _lib.lib()
+    _say("graph replay llima_sample_noalloc")
+    B, V, H = 16, 50000, 300
+    cfgd = dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.02, repetition_penalty=1.2,
+                presence_penalty=0.3, frequency_penalty=0.2)
+    rng = np.random.default_rng(91)
+    xs = [rng.normal(0, 3, (B, V)).astype(np.float32) for _ in range(3)]
+    hs = [rng.integers(0, V, size=(B, H)).astype(np.int32) for _ in range(3)]
+    us = [rng.random(B).astype(np.float32) for _ in range(3)]
+    x = torch.empty((B, V), dtype=torch.float32, device=gpu)
+    h = torch.empty((B, H), dtype=torch.int32, device=gpu)
+    u = torch.empty(B, dtype=torch.float32, device=gpu)
+    ids = torch.empty(B, dtype=torch.int32, device=gpu)
+    probs = torch.empty(B, dtype=torch.float32, device=gpu)
+    cfg, keep_alive = SamplerConfig(**cfgd).to_c(B, gpu)
+
+    def launch(stream):
+        rc = L.llima_sample_noalloc(x.data_ptr(), _lib.LLIMA_F32, B, V, V, h.data_ptr(), None, H,
+                                    None, u.data_ptr(), ctypes.byref(cfg), ids.data_ptr(),
+                                    probs.data_ptr(), None, stream)
+        assert rc == 0, rc
+
+    def load(i):
+        x.copy_(torch.from_numpy(xs[i]))
+        h.copy_(torch.from_numpy(hs[i]))
+        u.copy_(torch.from_numpy(us[i]))
+
+    load(0)
+    launch(torch.cuda.current_stream(gpu).cuda_stream)        # eager: the first call on the device
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(gpu)
+    cap.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.graph(graph, stream=cap):
+        launch(cap.cuda_stream)
+    torch.cuda.synchronize(gpu)
+    wsb = L.llima_sample_workspace_bytes(B, V, _lib.LLIMA_F32)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    for i in range(3):
+        load(i)
+        ids.fill_(-7)
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        gi, gp = ids.cpu().numpy(), probs.cpu().numpy()
+        eids, eprobs = oracle.sample(xs[i], us[i], OC(**cfgd), history=hs[i])
+        assert np.array_equal(gi, eids), (i, np.flatnonzero(gi != eids)[:8])
+        assert np.array_equal(gp.view(np.uint32), eprobs.view(np.uint32)), i
+        # an eager call of the workspace entry point between replays
+        w = dict(logits=xs[i], history=hs[i], bitmask=None, uniforms=us[i], cfg=cfgd)
+        a = _call(L, "workspace", w, gpu, ws)
+        assert np.array_equal(a[0], gi) and np.array_equal(a[1].view(np.uint32), gp.view(np.uint32))
+    del keep_alive
