@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="batched_penalties",
-                    choices=["batched_penalties", "single_row", "constrained", "top_p_only",
+                    choices=["batched_penalties", "batched_penalties_rows", "mixed_topk_rows",
+                             "single_row", "constrained", "top_p_only",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
@@ -261,7 +262,8 @@ def main():
             base = torch.from_numpy(lg).to(dev)
         g = torch.Generator(device=dev)
         g.manual_seed(2000)
-        sigma = {"single_row": 3.0, "batched_penalties": 4.0, "constrained": 3.0,
+        sigma = {"single_row": 3.0, "batched_penalties": 4.0, "batched_penalties_rows": 4.0,
+                 "mixed_topk_rows": 4.0, "constrained": 3.0,
                  "top_p_only": 4.0}.get(name, 5.0)
         bufs = [base]
         for i in range(1, nbuf):
@@ -284,7 +286,10 @@ def main():
         cfgd = dict(w["cfg"])
         if greedy_variant:
             cfgd = dict(greedy=True)
-        cfg, keep_alive = llima_amd.SamplerConfig(**cfgd).to_c(B, dev)
+        cfg_c = dict(cfgd)
+        for k, arr in (w.get("cfg_rows") or {}).items():     # per-row settings
+            cfg_c[k] = torch.from_numpy(arr).to(dev)
+        cfg, keep_alive = llima_amd.SamplerConfig(**cfg_c).to_c(B, dev)
         out_ids = torch.empty(B, dtype=torch.int32, device=dev)
         out_p = torch.empty(B, dtype=torch.float32, device=dev)
         nws = L.llima_sample_workspace_bytes(B, V, dt)
@@ -319,6 +324,9 @@ def main():
             config = {"workload": name, "B": B, "V": V, "history": H,
                       "logits_dtype": "bf16" if is_bf16 else "fp32"}
             config.update({k: v for k, v in cfgd.items()})
+            for k, arr in (w.get("cfg_rows") or {}).items():
+                vals = sorted(set(arr.tolist()))
+                config[k] = "per-row array: " + ", ".join(str(round(v, 6)) for v in vals)
         rows = B
         unit_rows = "rows/s"
         dtype = "bf16" if is_bf16 else "f32"
@@ -518,6 +526,10 @@ def cpu_baseline(name, w, seconds, greedy_variant):
         unit = "rows/s"
         lg = w["logits"]
         cfg = orc.SamplerConfig(**w["cfg"])
+        if w.get("cfg_rows"):                       # per-row settings: one config per row
+            cfg = [orc.SamplerConfig(**{**w["cfg"], **{k: a[b].item() for k, a in
+                                                       w["cfg_rows"].items()}})
+                   for b in range(lg.shape[0])]
 
         def fn():
             orc.sample(lg, w["uniforms"], cfg, history=w["history"], bitmask=w["bitmask"])

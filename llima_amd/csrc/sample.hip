@@ -257,7 +257,10 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     const bool eager = H > 0 && !P.lazy;
 
     // ---- 1. loads, in the order their data is used, all before the first
-    //         wait: history ids (rows penalised here), mask words, the chunks
+    //         wait: the row's settings (per-row arrays: loaded first, since the
+    //         history count waits for them and a wait covers every older
+    //         load), history ids (rows penalised here), mask words, the chunks
+    const RowCfg c = load_cfg(P, row);
     int32_t hid[SMP_HBATCH];
     if (eager) {
         const int32_t* hrow = P.hist + (size_t)row * H;
@@ -299,7 +302,6 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     };
     issue(0);
     __builtin_amdgcn_sched_barrier(0);
-    const RowCfg c = load_cfg(P, row);
     const bool pen_here = eager && c.pen;
 
     // ---- 2. history counts of the group (waits for the history ids only)
@@ -1803,48 +1805,57 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
 }
 
 // ------------------------------------------------------------------ direct path
-// Survivors (at most 64), staged in sh.sv[0, ns) as {raw value bits, id}: the
+// Survivors (at most 64 NPL), in id order as {raw key, id} (me): the
 // candidates at or above the raw key lowkey (1: every candidate).  Every wave
-// holds all of them (lane l: survivor l).  Lazy rows take their penalties here
-// (history ids counted against a hash of the survivor ids); then x / T, the
-// weights and the pairwise passes of fin_small.  Returns false, before
-// writing anything, when the result cannot be proven: tau must exceed the
-// chunk bounds (gkey) and, when lowkey cut candidates off, fl(lowkey / T) (a
-// value below lowkey, penalised or not, is at most that).
-__device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, const RowCfg& c, uint32_t ns,
-                              uint32_t lowkey, uint32_t gkey, const int32_t (&hid)[SMP_HBATCH],
-                              FinShared& sh) {
+// holds all of them (element e of lane l: survivor 64 e + l).  Lazy rows take
+// their penalties here (history ids counted against a bitmap of the survivor
+// ids, two barriers); then every wave computes the same x / T, keys, row
+// maximum and weights, ranks the survivors against its quarter of them (ge:
+// keys at or above, above: the mass strictly above), and after one barrier
+// adds the quarters: tau = the largest key with ge >= k, the top-p and min-p
+// cuts and the draw as a scan in id order (wave 0 writes).  Returns false
+// (every wave alike), before writing anything, when the result cannot be
+// proven: tau must exceed the chunk bounds (gkey) and, when lowkey cut
+// candidates off, fl(lowkey / T) (a value below lowkey, penalised or not, is
+// at most that).
+template <int NPL>
+__device__ __forceinline__ bool fin_tail(const SampleParams& P, int row, const RowCfg& c,
+                                         const llima_u32x4 (&me)[2], uint32_t ns, uint32_t lowkey,
+                                         uint32_t gkey, const int32_t (&hid)[SMP_HBATCH],
+                                         FinShared& sh) {
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
-    float x[2];
-    uint32_t id[2];
+    float x[NPL];
+    uint32_t id[NPL];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NPL; ++e) {
         const uint32_t i = (uint32_t)e * 64u + lane;
-        const llima_u32x4 me = sh.sv[i];                // sv holds 2 * SMP_SMALL + 64 slots
-        x[e] = i < ns ? key_f32(me.x) : -__builtin_inff();
-        id[e] = i < ns ? me.y : 0xFFFFFFFFu;            // matches no history id
+        x[e] = i < ns ? key_f32(me[e].x) : -__builtin_inff();
+        id[e] = i < ns ? me[e].y : 0xFFFFFFFFu;         // matches no history id
     }
     if (P.lazy && c.pen) {
-        // A bitmap of the survivor ids (2^16 bits in sh.u.hash.key, zeroed by
-        // the caller) passes a history id with one LDS read; the few that pass
-        // (the survivors' own occurrences and about 0.1 % false hits) are
+        // A bitmap of the survivor ids (2^16 bits in sh.u.hash.key, cleared
+        // by fin_direct) passes a history id with one LDS read; the few that
+        // pass (the survivors' own occurrences and about 0.1 % false hits) are
         // broadcast one distinct id per wave at a time and counted by the lanes
-        // holding the survivors (every wave holds them all), together with the
-        // wave's other copies of that id.
+        // holding the survivors, together with the wave's other copies of that
+        // id; the waves' counts are added in sh.hc (zeroed by fin_direct).
         uint32_t* bm = sh.u.hash.key;
         auto bit_of = [](uint32_t v) { return (v * 2654435761u) >> 16; };
         if (wave == 0) {
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
+            for (int e = 0; e < NPL; ++e) {
                 const uint32_t h = bit_of(id[e]);
                 if ((uint32_t)e * 64u + lane < ns) atomicOr(&bm[h >> 5], 1u << (h & 31u));
             }
         }
         __syncthreads();
         FIN_MARK(6);
-        uint32_t cn[2] = {0u, 0u};
-        // hv: this lane's history id; inlen: lanes whose entry lies before hlen
-        auto count_pass = [&](uint32_t hv, uint64_t m, uint64_t inlen) {   // m: lanes that passed
+        uint32_t cn[NPL];
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) cn[e] = 0u;
+        // hv: this lane's history id; m: the lanes whose id passed; inlen:
+        // the lanes whose entry lies before hlen
+        auto count_pass = [&](uint32_t hv, uint64_t m, uint64_t inlen) {
             while (m) {
                 const uint32_t L = (uint32_t)__builtin_ctzll(m);
                 const uint32_t u = readlane(hv, L);
@@ -1852,7 +1863,7 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
                 m &= ~same;
                 const uint32_t k = (uint32_t)__popcll(same);
 #pragma unroll
-                for (int e = 0; e < 2; ++e) cn[e] += id[e] == u ? k : 0u;
+                for (int e = 0; e < NPL; ++e) cn[e] += id[e] == u ? k : 0u;
             }
         };
         uint32_t bw[SMP_HBATCH];                         // every bitmap read first
@@ -1875,40 +1886,87 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
         FIN_MARK(7);
         // ids outside [0, V) match no survivor
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+        for (int e = 0; e < NPL; ++e)
             if (cn[e]) atomicAdd(&sh.hc[(uint32_t)e * 64u + lane], cn[e]);
         __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const uint32_t cn = sh.hc[(uint32_t)e * 64u + lane];    // 0 past ns
-            const float xp = penalize(x[e], cn, c);
-            x[e] = cn ? xp : x[e];
+        for (int e = 0; e < NPL; ++e) {
+            const uint32_t n = sh.hc[(uint32_t)e * 64u + lane];    // 0 past ns
+            x[e] = n ? penalize(x[e], n, c) : x[e];
         }
     }
     FIN_MARK(8);
-    // every wave: temperature, keys and weights of the survivors -> its own
-    // copy sh.sv2[wave] (no barrier before the pairwise passes)
-    uint32_t key[2], kmax = 0;
+    uint32_t key[NPL], kmax = 0;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NPL; ++e) {
         const float xt = x[e] / c.T;
         key[e] = (uint32_t)e * 64u + lane < ns && xt > -__builtin_inff() ? f32_key(xt) : 0u;
         kmax = key[e] > kmax ? key[e] : kmax;
     }
     kmax = wave_max_u32(kmax);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const uint64_t w0 = weight(key_f32(key[e]), key_f32(kmax));
-        const uint64_t w = key[e] ? w0 : 0ull;
-        sh.sv2[wave][(uint32_t)e * 64u + lane] = llima_u32x4{key[e], id[e], (uint32_t)w, (uint32_t)(w >> 32)};
-    }
-    __builtin_amdgcn_wave_barrier();                 // the wave's LDS writes precede its reads
-    FIN_MARK(9);
-    if (kmax == 0u) {
+    if (kmax == 0u) {                                 // uniform: every wave holds every survivor
         if (gkey || lowkey > 1u) return false;
         if (t == 0) write_result(P, row, -1, 0.0f);
         if (P.out_keep) write_keep(P, row, [&](auto) {});
         return true;
+    }
+    uint64_t w[NPL];
+    llima_u32x4* sv = sh.sv2[wave];
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        const uint64_t w0 = weight(key_f32(key[e]), key_f32(kmax));
+        w[e] = key[e] ? w0 : 0ull;
+        sv[(uint32_t)e * 64u + lane] = llima_u32x4{key[e], 0u, (uint32_t)w[e], (uint32_t)(w[e] >> 32)};
+    }
+    __builtin_amdgcn_wave_barrier();                 // the wave's LDS writes precede its reads
+    FIN_MARK(9);
+    // this wave's quarter of the survivors against every survivor (entries
+    // past ns hold key 0 and weight 0: they count for no present key)
+    constexpr uint32_t PER = 16u * NPL;
+    const uint32_t j0 = wave * PER;
+    uint32_t ge[NPL];
+    uint64_t above[NPL];
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) { ge[e] = 0; above[e] = 0; }
+    llima_u32x4 ov[PER];
+#pragma unroll
+    for (uint32_t jj = 0; jj < PER; ++jj) ov[jj] = sv[j0 + jj];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t jj = 0; jj < PER; ++jj) {
+        const llima_u32x4 o = ov[jj];
+        const uint64_t wj = ((uint64_t)o.w << 32) | o.z;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+            ge[e] += o.x >= key[e] ? 1u : 0u;
+            above[e] += o.x > key[e] ? wj : 0ull;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        sh.part[e][wave][lane] = above[e];
+        sh.pc[e][wave][lane] = ge[e];
+    }
+    __syncthreads();
+    FIN_MARK(10);
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        above[e] = 0; ge[e] = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < LLIMA_WAVES; ++w2) {
+            above[e] += sh.part[e][w2][lane];
+            ge[e] += sh.pc[e][w2][lane];
+        }
+    }
+    // tau: the k-th largest key counted with multiplicity, the largest key
+    // with at least k keys at or above it
+    const bool has_k = c.k > 0 && (uint32_t)c.k <= ns;
+    uint32_t tau = 1u;
+    if (has_k) {
+        uint32_t tk = 0;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) tk = key[e] && ge[e] >= (uint32_t)c.k && key[e] > tk ? key[e] : tk;
+        tau = wave_max_u32(tk);
     }
     uint32_t tcut = 0;
     if (c.k > 0) {
@@ -1918,8 +1976,54 @@ __device__ __forceinline__ bool fin_survivors(const SampleParams& P, int row, co
             tcut = kl > tcut ? kl : tcut;
         }
     }
-    return ns <= SMP_SMALL ? fin_small<1, true>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh)
-                           : fin_small<2, true>(P, row, c, ns, kmax, tcut, sh.sv2[wave], true, sh);
+    if (c.k > 0 && tcut && !(tau > tcut)) return false;   // uniform: every wave has tau
+    FIN_MARK(11);
+    bool fin[NPL];
+    uint64_t zk = 0;
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        fin[e] = key[e] != 0u && key[e] >= tau;
+        zk += fin[e] ? w[e] : 0ull;
+    }
+    if (c.p < 1.0f) {
+        // (above << 32) < frac32(p) * Z  <=>  above < ceil(frac32(p) * Z / 2^32),
+        // Z the mass top-k keeps
+        const uint64_t Z = wave_sum_u64(zk);
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+        const uint64_t plim = (uint64_t)((PZ + 0xFFFFFFFFull) >> 32);
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) fin[e] = fin[e] && (above[e] < plim || key[e] == kmax);
+    }
+    if (c.m > 0.0f) {
+        const uint64_t mthr = frac32(c.m) << 4;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) fin[e] = fin[e] && w[e] >= mthr;
+    }
+    // element order (e, lane) is id order: the draw is a scan
+    uint64_t wf[NPL], upto[NPL], Zf = 0;
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+        wf[e] = fin[e] ? w[e] : 0ull;
+        upto[e] = wave_incl_scan_u64(wf[e]) + Zf;
+        Zf = readlane63(upto[e]);
+    }
+    if (Zf == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+    } else {
+        const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
+#pragma unroll
+        for (int e = 0; e < NPL; ++e)
+            if (wave == 0 && wf[e] > 0 && upto[e] - wf[e] <= target && target < upto[e])
+                write_result(P, row, (int32_t)id[e], (float)((double)wf[e] / (double)Zf));
+    }
+    FIN_MARK(12);
+    if (P.out_keep)
+        write_keep(P, row, [&](auto set) {
+#pragma unroll
+            for (int e = 0; e < NPL; ++e)
+                if (wave == 0 && fin[e]) set(id[e]);
+        });
+    return true;
 }
 
 // Candidates straight from the first-round loads: thread t holds the 8 slots
@@ -1940,7 +2044,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
     }
     if (P.lazy && c.pen) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)                          // the 2^16-bit id bitmap
+        for (int i = 0; i < 2; ++i)                          // the 2^16-bit survivor-id bitmap
             ((llima_u32x4*)sh.u.hash.key)[t + i * LLIMA_WG] = llima_u32x4{0u, 0u, 0u, 0u};
     }
     FIN_MARK(3);
@@ -2037,8 +2141,8 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
     // exclusive scan of the counts over the workgroup (sh.bs.w32 is not
     // written again before the barrier below)
     const uint32_t inc = wave_incl_scan_u32(ns);
-    const uint32_t wave = wave_id();
-    if (lane_id() == 63) sh.bs.w32[wave] = inc;
+    const uint32_t wave = wave_id(), lane = lane_id();
+    if (lane == 63) sh.bs.w32[wave] = inc;
     __syncthreads();
     uint32_t nst = 0, before = 0;
 #pragma unroll
@@ -2052,14 +2156,18 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const bool in = (kr[j] != 0u) & (kr[j] >= lowkey);
-        sh.sv[in ? o : 2u * SMP_SMALL + lane_id()] = llima_u32x4{kr[j], idv[j], 0u, 0u};
+        sh.sv[in ? o : 2u * SMP_SMALL + lane] = llima_u32x4{kr[j], idv[j], 0u, 0u};
         o += in ? 1u : 0u;
     }
     sh.hc[t] = 0;
     __syncthreads();
     FIN_MARK(5);
     FIN_NOTE(15, 1);
-    return fin_survivors(P, row, c, nst, lowkey, gkey, hid, sh);
+    llima_u32x4 me[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) me[e] = sh.sv[(uint32_t)e * 64u + lane];
+    return nst <= SMP_SMALL ? fin_tail<1>(P, row, c, me, nst, lowkey, gkey, hid, sh)
+                            : fin_tail<2>(P, row, c, me, nst, lowkey, gkey, hid, sh);
 }
 
 template <typename TL>
@@ -2089,8 +2197,9 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         int32_t hid[SMP_HBATCH];
         {
             const bool lp = P.lazy && c.pen;
+            // unused: every load reads the workspace's first word
             const int32_t* hrow = lp ? P.hist + (size_t)row * P.H_max : (const int32_t*)P.ws;
-            const int hl = lp ? c.hlen : LLIMA_WG * SMP_HBATCH;
+            const int hl = lp ? c.hlen : 1;
 #pragma unroll
             for (int b = 0; b < SMP_HBATCH; ++b) {
                 const int j = (int)t + b * LLIMA_WG;

@@ -181,7 +181,34 @@ def top_p_only(B=64, V=128256, seed=1002):
                 cfg=dict(temperature=1.0, top_p=0.9))
 
 
+def batched_penalties_rows(B=64, V=128256, H=2048, seed=1002):
+    """The headline workload with every setting passed as a per-row array (a
+    serving batch whose requests each carry their own sampler settings); the
+    values are the headline's.  cfg_rows names the fields given per row."""
+    w = batched_penalties(B, V, H, seed)
+    w["name"] = "batched_penalties_rows"
+    w["cfg_rows"] = {k: np.full(B, v, np.int32 if k == "top_k" else np.float32)
+                     for k, v in w["cfg"].items()}
+    return w
+
+
+def mixed_topk_rows(B=64, V=128256, seed=1002):
+    """The headline rows (no history) as a per-request serving batch: even
+    rows sample with top-k 50 and top-p 0.95, odd rows with top-p 0.9 alone
+    (per-row top_k 0), all at T 1.0."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 4.0)
+    u = rng.random(B, dtype=np.float32)
+    even = (np.arange(B) % 2) == 0
+    rows = dict(top_k=np.where(even, 50, 0).astype(np.int32),
+                top_p=np.where(even, 0.95, 0.9).astype(np.float32))
+    return dict(name="mixed_topk_rows", logits=logits, history=None, uniforms=u, bitmask=None,
+                cfg=dict(temperature=1.0, top_k=50, top_p=0.95), cfg_rows=rows)
+
+
 WORKLOADS = {
+    "batched_penalties_rows": batched_penalties_rows,
+    "mixed_topk_rows": mixed_topk_rows,
     "single_row": single_row,
     "batched_penalties": batched_penalties,
     "constrained": constrained,
