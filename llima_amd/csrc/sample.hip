@@ -112,7 +112,8 @@ struct SampleParams {
     int32_t B, V, H_max, S;
     int32_t lgs;         // log2 of S rounded up to a power of two (finish gather)
     int32_t vec_ok;
-    int32_t lazy;        // penalties are applied by the finish (see llima_sample)
+    int32_t lazy;        // rows may take their penalties in the finish (row_lazy decides per row)
+    int32_t eager;       // rows may take their penalties in the sweep (its history count table)
     int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
     int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
 };
@@ -154,6 +155,16 @@ __device__ __forceinline__ RowCfg load_cfg(const SampleParams& P, int row) {
     r.pen = h > 0 && (r.R != 1.0f || r.alpha != 0.0f || r.beta != 0.0f);
     if (!(r.k > 0 && r.k < P.V)) r.k = 0;
     return r;
+}
+
+// A row's penalties are applied by the finish, to its candidates only, when
+// they can only lower a value (repetition >= 1, presence and frequency >= 0)
+// and the row samples with top-k: a penalised value never exceeds its raw
+// value, so the sweep's bound on the raw values still holds.  Otherwise the
+// sweep applies them to every value of the row.
+__device__ __forceinline__ bool row_lazy(const SampleParams& P, const RowCfg& c) {
+    return P.lazy && c.pen && !c.greedy && c.k > 0 && c.R >= 1.0f && c.alpha >= 0.0f &&
+           c.beta >= 0.0f;
 }
 
 // Values of weight 0 can be left out of the candidates when they cannot be in
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     const int g1 = g0 + SC * CHUNK < V ? g0 + SC * CHUNK : V;
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
     const int H = P.H_max;
-    const bool eager = H > 0 && !P.lazy;
+    const bool eager = H > 0 && P.eager;
 
     // ---- 1. loads, in the order their data is used, all before the first
     //         wait: the row's settings (per-row arrays: loaded first, since the
@@ -302,7 +313,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     };
     issue(0);
     __builtin_amdgcn_sched_barrier(0);
-    const bool pen_here = eager && c.pen;
+    const bool pen_here = eager && c.pen && !row_lazy(P, c);
 
     // ---- 2. history counts of the group (waits for the history ids only)
     if (pen_here) {
@@ -1568,7 +1579,7 @@ __device__ __forceinline__ bool fin_elems(const SampleParams& P, int row, const 
     }
 
     // ---- lazy penalties: history ids counted against a hash of the candidate ids
-    if (P.lazy && c.pen) {
+    if (row_lazy(P, c)) {
         if (N > SMP_HASH / 2) return false;
         __syncthreads();                              // sh.u.cand is read
         for (uint32_t i = t; i < SMP_HASH / 4; i += LLIMA_WG) {
@@ -1832,7 +1843,7 @@ __device__ __forceinline__ bool fin_tail(const SampleParams& P, int row, const R
         x[e] = i < ns ? key_f32(me[e].x) : -__builtin_inff();
         id[e] = i < ns ? me[e].y : 0xFFFFFFFFu;         // matches no history id
     }
-    if (P.lazy && c.pen) {
+    if (row_lazy(P, c)) {
         // A bitmap of the survivor ids (2^16 bits in sh.u.hash.key, cleared
         // by fin_direct) passes a history id with one LDS read; the few that
         // pass (the survivors' own occurrences and about 0.1 % false hits) are
@@ -2042,7 +2053,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
         if (P.out_keep) write_keep(P, row, [&](auto) {});
         return true;
     }
-    if (P.lazy && c.pen) {
+    if (row_lazy(P, c)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)                          // the 2^16-bit survivor-id bitmap
             ((llima_u32x4*)sh.u.hash.key)[t + i * LLIMA_WG] = llima_u32x4{0u, 0u, 0u, 0u};
@@ -2060,7 +2071,7 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
             // a random history holds about one in a thousand ids, and a wider
             // margin narrows the window the first round can stop in)
             const uint32_t kk = (uint32_t)c.k;
-            const uint32_t margin = !(P.lazy && c.pen) ? 0u
+            const uint32_t margin = !row_lazy(P, c) ? 0u
                                   : kk + 6u <= SMP_SMALL ? 6u
                                   : kk < 2u * SMP_SMALL ? min(32u, 2u * SMP_SMALL - kk) : 0u;
             uint32_t rem = min(N, (uint32_t)c.k + margin), above_all = 0;
@@ -2196,7 +2207,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         // branch would make the first use of q wait for them as well
         int32_t hid[SMP_HBATCH];
         {
-            const bool lp = P.lazy && c.pen;
+            const bool lp = row_lazy(P, c);
             // unused: every load reads the workspace's first word
             const int32_t* hrow = lp ? P.hist + (size_t)row * P.H_max : (const int32_t*)P.ws;
             const int hl = lp ? c.hlen : 1;
@@ -3254,7 +3265,7 @@ static void launch_sweep(const SampleParams& P, hipStream_t st) {
     constexpr int SC = SMP_SWEEP_SC;
     const dim3 g((uint32_t)P.B * (uint32_t)((P.S + SC - 1) / SC)), b(LLIMA_WG);
     // the history count table (dynamic LDS) only when the sweep penalises
-    const size_t cnt_bytes = (P.H_max > 0 && !P.lazy) ? (size_t)SC * (16 / sizeof(TL)) * 4 * LLIMA_WG / 2 * 4 : 0;
+    const size_t cnt_bytes = (P.H_max > 0 && P.eager) ? (size_t)SC * (16 / sizeof(TL)) * 4 * LLIMA_WG / 2 * 4 : 0;
     if (P.bitmask) {
         if (P.vec_ok) hipLaunchKernelGGL((sample_sweep<TL, true, true, SC>), g, b, cnt_bytes, st, P);
         else hipLaunchKernelGGL((sample_sweep<TL, false, true, SC>), g, b, cnt_bytes, st, P);
@@ -3349,14 +3360,18 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     const size_t esz = dtype == LLIMA_F32 ? 4 : 2;
     P.vec_ok = ((uintptr_t)logits % 16 == 0) && ((row_stride * (int64_t)esz) % 16 == 0) &&
                (V % (int32_t)(16 / esz) == 0);
-    // The finish applies the penalties (to the candidates only) when every row
-    // samples with top-k and the penalties can only lower a value: repetition
-    // >= 1, presence and frequency >= 0 (one broadcast configuration).
+    // Penalties: a row takes them in the finish, to its candidates only, when
+    // it samples with top-k and they can only lower a value (row_lazy, decided
+    // per row on the device); otherwise in the sweep.  With one broadcast
+    // configuration every row decides alike, and the sweep's history count
+    // table is allocated only when they are applied there.
     const bool rows_cfg = cfg->temperature_rows || cfg->top_k_rows || cfg->repetition_penalty_rows ||
                           cfg->presence_penalty_rows || cfg->frequency_penalty_rows;
-    P.lazy = P.H_max > 0 && !rows_cfg && !cfg->greedy && cfg->temperature > 0.0f &&
-             cfg->top_k > 0 && cfg->top_k < V && cfg->repetition_penalty >= 1.0f &&
-             cfg->presence_penalty >= 0.0f && cfg->frequency_penalty >= 0.0f;
+    const bool all_lazy = !rows_cfg && !cfg->greedy && cfg->temperature > 0.0f &&
+                          cfg->top_k > 0 && cfg->top_k < V && cfg->repetition_penalty >= 1.0f &&
+                          cfg->presence_penalty >= 0.0f && cfg->frequency_penalty >= 0.0f;
+    P.lazy = P.H_max > 0 && !cfg->greedy && (rows_cfg || all_lazy);
+    P.eager = P.H_max > 0 && !all_lazy;
     hipStream_t st = (hipStream_t)stream;
     // Masked batches without top-k: the wide finish first (sample_finish then
     // takes only the rows it left)

@@ -506,6 +506,33 @@ def test_sample_per_row_configs(gpu, oracle):
     _sample_both(gpu, oracle, x, u, None, history=hist, cfg_rows=rows)
 
 
+def test_sample_per_row_lazy_and_eager_penalties(gpu, oracle):
+    """Per-row settings decide per row where the penalties are applied: rows
+    with top-k whose penalties only lower values take them in the finish, the
+    others (a repetition penalty below 1, negative presence or frequency, no
+    top-k, greedy) in the sweep.  One batch holds every kind, over the lazy
+    hit patterns of the test below (history ids among the survivors, hot ids
+    repeated), fp32 and bf16."""
+    _say("sample per-row lazy and eager penalties")
+    rng = np.random.default_rng(78)
+    B, V, H = 8, 50000, 1500
+    x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(4.0)).astype(np.float32)
+    hist = rng.integers(0, V, size=(B, H)).astype(np.int32)
+    for b in range(B):                                  # the row's top values, repeated
+        top = np.argsort(-x[b])[:40]
+        hist[b, :400] = np.resize(top, 400)
+    u = rng.random(B).astype(np.float32)
+    rows = dict(temperature=[0.8, 0.8, 1.0, 0.0, 0.7, 1.2, 0.8, 0.9],
+                top_k=[50, 50, 40, 50, 0, 30, 64, 50],
+                top_p=[0.95, 0.9, 1.0, 1.0, 0.9, 0.8, 0.95, 1.0],
+                min_p=[0.05, 0.0, 0.02, 0.0, 0.0, 0.1, 0.05, 0.0],
+                repetition_penalty=[1.15, 0.9, 1.0, 1.2, 1.3, 1.05, 1.15, 2.0],
+                presence_penalty=[0.5, 0.5, -0.4, 0.0, 0.2, 0.0, 0.5, 1.0],
+                frequency_penalty=[0.3, 0.3, 0.1, 0.0, 0.1, -0.2, 0.3, 0.5])
+    _sample_both(gpu, oracle, x, u, None, history=hist, cfg_rows=rows)
+    _sample_both(gpu, oracle, wl.f32_to_bf16_bits(x), u, None, history=hist, cfg_rows=rows)
+
+
 def test_sample_lazy_penalty_hits(gpu, oracle):
     """Penalties applied to the finish's survivors only (repetition >= 1,
     presence and frequency >= 0, broadcast top-k): history ids that are
