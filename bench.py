@@ -29,7 +29,12 @@ and lm_head_argmax_b32/b64/b128_packed (over a weight packed at load time);
 lm_head_score_b64_packed: the packed LM head with its scoring epilogue (the
 log-softmax at 64 target ids, no logits written); lm_head_verify_b16_d7: the
 LM head over 16 sequences x 8 rows with greedy chain verification fused (no
-logits written).
+logits written).  batched_penalties_rows: the default batch with every setting
+given per row (SamplerConfig tensors).  mixed_topk_rows: even rows top-k 50 /
+top-p 0.95, odd rows top-p 0.9 alone, no history.  topk_bf16: llima_topk, k 5
+over 5 bf16 rows of 32000 (the EAGLE3 draft head's top-k).  eagle3_tree: one
+whole EAGLE3 draft tree (K 5, depth 4, 15 tokens; draft vocabulary 32000,
+target 128256): tree_begin, three tree_grow, tree_finish.
 """
 from __future__ import annotations
 
@@ -53,6 +58,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="batched_penalties",
                     choices=["batched_penalties", "batched_penalties_rows", "mixed_topk_rows",
+                             "topk_bf16", "eagle3_tree",
                              "single_row", "constrained", "top_p_only",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
@@ -203,6 +209,78 @@ def main():
         dtype = "f32"
         kernel_names = ["vr_rowpass", "vr_draw"]
         config = {"workload": "speculative", "B": B, "draft_len": D, "V": V}
+    elif name in ("topk_bf16", "eagle3_tree"):
+        # EAGLE3 drafting: the inputs are small (a few hundred KB) and the draft
+        # model's LM head has just written them, so they rotate over a handful
+        # of buffers only (and may sit in the Infinity Cache, as in the loop)
+        nbuf = 8
+        g = torch.Generator(device=dev)
+        g.manual_seed(2002)
+        rows = 1
+        dtype = "bf16"
+        if name == "topk_bf16":
+            k = w["k"]
+            R_, C_ = w["logits"].shape
+            bufs = [torch.from_numpy(w["logits"].view(np.int16)).to(dev).view(torch.bfloat16)]
+            for i in range(1, nbuf):
+                bufs.append((torch.randn((R_, C_), generator=g, device=dev) * 3.0).to(torch.bfloat16))
+            idx_o = torch.empty((R_, k), dtype=torch.int32, device=dev)
+            val_o = torch.empty((R_, k), dtype=torch.float32, device=dev)
+            for x in bufs:
+                launches.append(lambda sp, x=x, R_=R_, C_=C_, k=k: check(L.llima_topk(
+                    x.data_ptr(), _lib.LLIMA_BF16, R_, C_, C_, k, idx_o.data_ptr(), val_o.data_ptr(),
+                    sp), "llima_topk"))
+            per = R_ * C_ * 2
+            alg_bytes = per + R_ * k * 8
+            unit_rows = "calls/s"
+            kernel_names = ["topk_rows_kernel"]
+            config = {"workload": name, "rows": R_, "cols": C_, "k": k, "logits_dtype": "bf16"}
+        else:
+            K, depth, total, Vd = w["K"], w["depth"], w["total"], w["root"].shape[0]
+            d2t = torch.from_numpy(w["d2t"]).to(dev)
+            nb = L.llima_eagle3_tree_bytes(K, depth)
+            state = torch.empty(nb, dtype=torch.uint8, device=dev)
+            roots = [torch.from_numpy(w["root"].view(np.int16)).to(dev).view(torch.bfloat16)]
+            levs = [torch.from_numpy(w["levels"].view(np.int16)).to(dev).view(torch.bfloat16)]
+            for i in range(1, nbuf):
+                roots.append((torch.randn((Vd,), generator=g, device=dev) * 3.0).to(torch.bfloat16))
+                levs.append((torch.randn((depth - 1, K, Vd), generator=g, device=dev) * 3.0)
+                            .to(torch.bfloat16))
+            N = total + 1
+            ids_o = torch.empty(K, dtype=torch.int32, device=dev)
+            prow_o = torch.empty(K, dtype=torch.int32, device=dev)
+            mask_o = torch.empty((K, K * depth), dtype=torch.float32, device=dev)
+            tok_o = torch.empty(N, dtype=torch.int32, device=dev)
+            tm_o = torch.empty((N, N), dtype=torch.float32, device=dev)
+            pos_o = torch.empty(N, dtype=torch.int32, device=dev)
+            ret_o = torch.empty((N, N), dtype=torch.int32, device=dev)
+            dims_o = torch.empty(2, dtype=torch.int32, device=dev)
+
+            def tree(sp, r, lv, K=K, depth=depth, total=total, Vd=Vd):   # bound now: main reuses K
+                check(L.llima_eagle3_tree_begin(r.data_ptr(), _lib.LLIMA_BF16, Vd, d2t.data_ptr(), K,
+                                                depth, state.data_ptr(), nb, ids_o.data_ptr(), sp),
+                      "llima_eagle3_tree_begin")
+                for lvl in range(1, depth):
+                    check(L.llima_eagle3_tree_grow(lv[lvl - 1].data_ptr(), _lib.LLIMA_BF16, Vd, Vd,
+                                                   d2t.data_ptr(), K, depth, lvl, state.data_ptr(), nb,
+                                                   ids_o.data_ptr(), prow_o.data_ptr(),
+                                                   mask_o.data_ptr(), sp), "llima_eagle3_tree_grow")
+                check(L.llima_eagle3_tree_finish(state.data_ptr(), nb, K, depth, total,
+                                                 w["sample_token"], tok_o.data_ptr(), tm_o.data_ptr(),
+                                                 pos_o.data_ptr(), ret_o.data_ptr(), dims_o.data_ptr(),
+                                                 sp), "llima_eagle3_tree_finish")
+            for r, lv in zip(roots, levs):
+                launches.append(lambda sp, r=r, lv=lv: tree(sp, r, lv))
+            per = (1 + (depth - 1) * K) * Vd * 2
+            alg_bytes = per + Vd * 4 + N * 4 * 3 + N * N * 8
+            unit_rows = "trees/s"
+            kernel_names = ["eagle3_begin_kernel", "eagle3_rows_kernel", "eagle3_combine_kernel",
+                            "eagle3_finish_kernel"]
+            config = {"workload": name, "K": K, "depth": depth, "total_tokens": total,
+                      "draft_vocab": Vd, "logits_dtype": "bf16",
+                      "calls": "begin + %d grow + finish" % (depth - 1)}
+        data_note = ("synthetic (seeded; %d input sets of %d KB, small enough for the Infinity "
+                     "Cache, as a draft LM head's fresh output is)" % (nbuf, per // 1024))
     elif name in ("score_bf16", "mtp_masked_argmax"):
         lg = w["logits"]
         B, V = lg.shape
@@ -483,6 +561,26 @@ def cpu_baseline(name, w, seconds, greedy_variant):
                                "of the vocabulary, scaled by V / %d), %.1f s" % (
                                    reps, w["B"], w["H"], nv, w["H"],
                                    "log-sum-exp" if scoring else "argmax", nv, nv, dt)})
+        return info
+    if name in ("topk_bf16", "eagle3_tree"):
+        if name == "topk_bf16":
+            unit = "calls/s"
+
+            def fn():                    # topk<bf16> over the K rows (OpenMP over rows)
+                orc.topk(w["logits"], w["k"])
+                return 1
+            what = "topk<bf16> calls over [%d, %d], k = %d" % (w["logits"].shape + (w["k"],))
+        else:
+            unit = "trees/s"
+
+            def fn():
+                orc.eagle3_tree(w["root"], w["levels"], w["d2t"], w["K"], w["depth"], w["total"],
+                                w["sample_token"], cr=False)
+                return 1
+            what = "trees (K = %d, depth %d, %d tokens, Vd = %d)" % (
+                w["K"], w["depth"], w["total"], w["root"].shape[0])
+        v, reps, dt = timed(fn, 1)
+        info.update({"value": v, "unit": unit, "cores": 1, "sample": f"{reps} {what}, {dt:.1f} s"})
         return info
     if name == "speculative":
         unit = "sequences/s"

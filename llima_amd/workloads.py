@@ -206,7 +206,33 @@ def mixed_topk_rows(B=64, V=128256, seed=1002):
                 cfg=dict(temperature=1.0, top_k=50, top_p=0.95), cfg_rows=rows)
 
 
+def topk_bf16(rows=5, cols=32000, k=5, seed=1009):
+    """One EAGLE3 draft level's row top-k as the reference calls it
+    (language_model_eagle3.cpp:914-920): topk<bf16> over K = 5 rows of a
+    32000-id draft vocabulary, k = 5.  Draft logits ~ N(0, 3^2), bf16."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = f32_to_bf16_bits(_normal(rng, (rows, cols), 3.0))
+    return dict(name="topk_bf16", logits=x, k=k)
+
+
+def eagle3_tree(K=5, depth=4, total=15, Vd=32000, V=128256, seed=1010):
+    """The EAGLE3 draft tree at the reference's shape (topk_generate,
+    language_model_eagle3.cpp:808-1164): K = 5, depth 4, 15 draft tokens, a
+    32000-id bf16 draft vocabulary mapped to 128256 target ids by d2t.  The
+    draft logits of every level are given (the draft model's forward passes
+    between levels are the caller's): root [Vd], levels [depth - 1, K, Vd],
+    ~ N(0, 3^2)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    root = f32_to_bf16_bits(_normal(rng, (Vd,), 3.0))
+    levels = f32_to_bf16_bits(_normal(rng, (depth - 1, K, Vd), 3.0))
+    d2t = (np.sort(rng.choice(V, Vd, replace=False)) - np.arange(Vd)).astype(np.int32)
+    return dict(name="eagle3_tree", root=root, levels=levels, d2t=d2t, K=K, depth=depth,
+                total=total, sample_token=int(rng.integers(0, V)))
+
+
 WORKLOADS = {
+    "topk_bf16": topk_bf16,
+    "eagle3_tree": eagle3_tree,
     "batched_penalties_rows": batched_penalties_rows,
     "mixed_topk_rows": mixed_topk_rows,
     "single_row": single_row,
