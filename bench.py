@@ -31,7 +31,8 @@ log-softmax at 64 target ids, no logits written); lm_head_verify_b16_d7: the
 LM head over 16 sequences x 8 rows with greedy chain verification fused (no
 logits written).  batched_penalties_rows: the default batch with every setting
 given per row (SamplerConfig tensors).  mixed_topk_rows: even rows top-k 50 /
-top-p 0.95, odd rows top-p 0.9 alone, no history.  topk_bf16: llima_topk, k 5
+top-p 0.95, odd rows top-p 0.9 alone, no history.  constrained_half: the
+constrained rows under a mask allowing half of the ids.  topk_bf16: llima_topk, k 5
 over 5 bf16 rows of 32000 (the EAGLE3 draft head's top-k).  eagle3_tree: one
 whole EAGLE3 draft tree (K 5, depth 4, 15 tokens; draft vocabulary 32000,
 target 128256): tree_begin, three tree_grow, tree_finish.
@@ -59,7 +60,7 @@ def parse():
     ap.add_argument("--workload", default="batched_penalties",
                     choices=["batched_penalties", "batched_penalties_rows", "mixed_topk_rows",
                              "topk_bf16", "eagle3_tree",
-                             "single_row", "constrained", "top_p_only",
+                             "single_row", "constrained", "constrained_half", "top_p_only",
                              "large_vocab_bf16", "large_vocab_bf16_greedy", "argmax_bf16",
                              "speculative", "score_bf16", "mtp_masked_argmax",
                              "lm_head_argmax", "lm_head_argmax_b64", "lm_head_argmax_b128",
@@ -341,7 +342,7 @@ def main():
         g = torch.Generator(device=dev)
         g.manual_seed(2000)
         sigma = {"single_row": 3.0, "batched_penalties": 4.0, "batched_penalties_rows": 4.0,
-                 "mixed_topk_rows": 4.0, "constrained": 3.0,
+                 "mixed_topk_rows": 4.0, "constrained": 3.0, "constrained_half": 3.0,
                  "top_p_only": 4.0}.get(name, 5.0)
         bufs = [base]
         for i in range(1, nbuf):
@@ -398,7 +399,9 @@ def main():
                 not (0 < cfgd.get("top_k", 0) < V)
             kernel_names = (["dense_stats"] + (["dense_hist", "dense_bound"] if cfgd.get("top_p", 1.0) < 1
                                                else []) + ["dense_keep", "dense_final"]
-                            if dense else ["sample_sweep", "sample_finish"])
+                            if dense else ["sample_sweep"] +
+                            (["sample_finish_wide"] if mask is not None and not cfgd.get("greedy") and
+                             not (0 < cfgd.get("top_k", 0) < V) else []) + ["sample_finish"])
             config = {"workload": name, "B": B, "V": V, "history": H,
                       "logits_dtype": "bf16" if is_bf16 else "fp32"}
             config.update({k: v for k, v in cfgd.items()})

@@ -45,6 +45,7 @@
 // sima_lmm/devkit/cpp/language_model.cpp:3689-3714); greedy rows follow that
 // argmax (first index of the maximum) over the masked, penalised row.
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include "../../include/llima_sampler.h"
@@ -63,6 +64,7 @@ namespace llima {
 #define SMP_SPARSE 12                              // lanes above the bound for a sparse sweep wave
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
+#define SMP_RCNT 16                                // split-row arrival counter stride (u32: 64 bytes)
 #define SMP_PBINS 256                              // top-p value bins: floor(8 (xmax - x)), the last open
 #define SMP_PBIN_SCALE 8.0f
 #define SMP_PBIN_SLOTS (SMP_PBINS + 64)            // + a spare bin per lane
@@ -71,8 +73,9 @@ namespace llima {
 #define SMP_PENDING ((int32_t)0x80000000)          // out_ids of a row sample_finish_wide left
 
 // Chunk region: slot 0 is the header, low 32 bits: candidates written |
-// flags << 16; high 32 bits: the bound g (float bits): every finite value >= g
-// was written (-inf: all).  Candidates follow from slot 1 as (key << 32 | id)
+// flags << 16; high 32 bits (float bits): on top-k rows the bound g, every
+// finite value >= g was written (-inf: all); on other rows the chunk maximum M,
+// the bound being nontopk_bound(M).  Candidates follow from slot 1 as (key << 32 | id)
 // in id order (the key of a finite value is never 0); the slots the finish
 // reads in its first round (pre_slots) that hold no candidate carry
 // SMP_SENTINEL, key 0.  Greedy rows: slot 1 holds (key << 32 | ~index) of the
@@ -88,13 +91,16 @@ namespace llima {
 #define SMP_TRACE_MARKS 16
 #ifdef LLIMA_FINISH_TRACE
 __device__ unsigned long long fin_trace[SMP_TRACE_ROWS][SMP_TRACE_MARKS];
-#define FIN_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = wall_clock64(); } while (0)
-#define FIN_NOTE(i, v) do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = (v); } while (0)
-#define FIN_BEGIN() do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) { \
+#define FIN_MARK(i) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = wall_clock64(); } while (0)
+#define FIN_NOTE(i, v) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = (v); } while (0)
+// any part of a split row (the one that finishes it)
+#define FIN_MARK_ANY(i) do { if (threadIdx.x == 0 && blockIdx.x < SMP_TRACE_ROWS) fin_trace[blockIdx.x][i] = wall_clock64(); } while (0)
+#define FIN_BEGIN() do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < SMP_TRACE_ROWS) { \
         for (int m_ = 1; m_ < SMP_TRACE_MARKS; ++m_) fin_trace[blockIdx.x][m_] = 0; } FIN_MARK(0); } while (0)
 #else
 #define FIN_BEGIN() do { } while (0)
 #define FIN_MARK(i) do { } while (0)
+#define FIN_MARK_ANY(i) do { } while (0)
 #define FIN_NOTE(i, v) do { } while (0)
 #endif
 struct SampleParams {
@@ -116,6 +122,8 @@ struct SampleParams {
     int32_t eager;       // rows may take their penalties in the sweep (its history count table)
     int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
     int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
+    int32_t fsplit;      // sample_finish workgroups per row (> 1: rows without top-k may be split)
+    uint32_t* rcnt;      // [B][SMP_RCNT] split-row arrival counters, zeroed by the sweep
 };
 
 struct RowCfg {
@@ -173,6 +181,17 @@ __device__ __forceinline__ bool row_lazy(const SampleParams& P, const RowCfg& c)
 // they never affect the draw.
 __device__ __forceinline__ bool zero_weight_irrelevant(const SampleParams& P, const RowCfg& c) {
     return P.out_keep == nullptr || c.p < 1.0f || (c.m > 0.0f && frac32(c.m) > 0);
+}
+
+// The sweep's chunk bound on a row without top-k, from the chunk maximum M
+// (penalised and masked, before / T; -inf when the chunk has no value above
+// -inf): M - 27 T when values of zero weight cannot matter, else -inf (every
+// finite value is a candidate).  The sweep and the finish evaluate it with the
+// same operations, so the header holds M and both derive the same bound.
+__device__ __forceinline__ float nontopk_bound(const SampleParams& P, const RowCfg& c, float M) {
+    if (!(M > -__builtin_inff()) || !zero_weight_irrelevant(P, c)) return -__builtin_inff();
+    const float gm = M - 27.0f * c.T;
+    return gm == gm ? gm : -__builtin_inff();
 }
 
 // Lane maxima ranked, per wave, for the top-k chunk bound: a wave (1024 fp32
@@ -266,6 +285,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
     const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
     const int H = P.H_max;
     const bool eager = H > 0 && P.eager;
+    if (P.fsplit > 1 && grp == 0 && t == 0) P.rcnt[(size_t)row * SMP_RCNT] = 0u;   // split-row arrivals
 
     // ---- 1. loads, in the order their data is used, all before the first
     //         wait: the row's settings (per-row arrays: loaded first, since the
@@ -441,7 +461,7 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
 
         // ---- 4. the chunk bound g
         const uint32_t lk = lm > NEG_INF ? f32_key(lm) : 0u;
-        float g = NEG_INF;
+        float g = NEG_INF, cmax = NEG_INF;
         if (c.k > 0) {
             // g = the largest of the four waves' r-th largest lane maxima (low
             // key bits cleared: a lower value).  Any g is correct, since every
@@ -457,19 +477,18 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
 #pragma unroll
             for (int w = 0; w < LLIMA_WAVES; ++w) gk = xa[cc][w] > gk ? xa[cc][w] : gk;
             if (gk) g = key_f32(gk);
-        } else if (zero_weight_irrelevant(P, c)) {
-            // values this far below the chunk maximum have weight 0 (checked
-            // exactly by the finish against the row maximum)
+        } else {
+            // the chunk maximum (the header keeps it for the finish), and the
+            // bound below which values have weight 0 (checked exactly by the
+            // finish against the row maximum)
             const uint32_t wm = wave_max_u32(lk);
             if (lane == 0) xa[cc][wave] = wm;
             __syncthreads();
             uint32_t mk = 0;
 #pragma unroll
             for (int w = 0; w < LLIMA_WAVES; ++w) mk = xa[cc][w] > mk ? xa[cc][w] : mk;
-            if (mk) {
-                const float gm = key_f32(mk) - 27.0f * c.T;
-                g = gm == gm ? gm : NEG_INF;
-            }
+            if (mk) cmax = key_f32(mk);
+            g = nontopk_bound(P, c, cmax);
         }
         // the smallest finite float stands for -inf: -inf and NaN never pass
         const float g2 = g > NEG_INF ? g : -__FLT_MAX__;
@@ -628,7 +647,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_sweep(SampleParams P) {
             for (uint32_t i = SMP_HDR + total + (uint32_t)t; i < pre; i += LLIMA_WG) reg[i] = SMP_SENTINEL;
         }
         if (t == 0)
-            *(uint64_t*)reg = ((uint64_t)__float_as_uint(g) << 32) | (fits ? total : (HF_OVERFLOW << 16));
+            *(uint64_t*)reg = ((uint64_t)__float_as_uint(c.k > 0 ? g : cmax) << 32) |
+                              (fits ? total : (HF_OVERFLOW << 16));
     }
 }
 
@@ -966,6 +986,174 @@ __device__ __forceinline__ void load_fe(const TL* rowp, int i0, int hi, bool vec
         for (int e = 0; e < SMP_FE; ++e) xs[e] = load_one<TL>(rowp, i0 + e < hi ? i0 + e : hi - 1);
     }
 }
+// The full-row path's step: FE consecutive ids per thread (16-byte loads when
+// the rows allow), NB steps in flight per thread.
+template <typename TL>
+struct FrGeom {
+    static constexpr int EPL = 16 / (int)sizeof(TL);   // values per 16-byte load
+    static constexpr int FE = 16;                      // ids per thread and step
+    static constexpr int NL = FE / EPL;                // 16-byte loads per thread and step
+    static constexpr int STEP = LLIMA_WG * FE;         // 4096 ids
+    static constexpr int NB = 2;                       // steps in flight
+    static constexpr int CHUNK = LLIMA_WG * 64 / (int)sizeof(TL);   // the sweep's chunk
+};
+static_assert(SMP_SEG % FrGeom<float>::STEP == 0 && SMP_SEG % FrGeom<uint16_t>::STEP == 0,
+              "full-row steps tile a segment");
+
+// Requests FE consecutive values from id i0 (ids at or past V from clamped
+// addresses; V a multiple of EPL when VEC), packed as they lie in memory.  VEC
+// is a template argument so that every path issues the same loads: the
+// compiler's wait counts then let later steps' loads stay in flight.
+template <typename TL, bool VEC>
+__device__ __forceinline__ void fr_issue(const TL* rowp, int i0, int V, llima_u32x4 (&q)[FrGeom<TL>::NL]) {
+    constexpr int EPL = FrGeom<TL>::EPL;
+    if constexpr (VEC) {
+#pragma unroll
+        for (int j = 0; j < FrGeom<TL>::NL; ++j) {
+            const int ia = i0 + j * EPL < V ? i0 + j * EPL : V - EPL;
+            q[j] = *(const llima_u32x4*)(rowp + ia);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < FrGeom<TL>::NL; ++j) {
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const int ia = i0 + j * EPL + e < V ? i0 + j * EPL + e : V - 1;
+                const float f = load_one<TL>(rowp, ia);
+                if constexpr (sizeof(TL) == 4) w[e] = __float_as_uint(f);
+                else w[e >> 1] |= (__float_as_uint(f) >> 16) << ((e & 1) * 16);
+            }
+            q[j] = llima_u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// Value e of a step fr_issue requested.
+template <typename TL>
+__device__ __forceinline__ float fr_value(const llima_u32x4 (&q)[FrGeom<TL>::NL], int e) {
+    constexpr int EPL = FrGeom<TL>::EPL;
+    const llima_u32x4 v = q[e / EPL];
+    const int d = sizeof(TL) == 4 ? e % 4 : (e % EPL) / 2;
+    const uint32_t w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+    if constexpr (sizeof(TL) == 4) return __uint_as_float(w);
+    else return __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+
+// The value transform of one step, ids from i0 (NaN -> -inf, mask, penalties,
+// / T unless greedy; ids past the row -inf); lo: the segment table's first id.
+template <typename TL, bool PEN>
+__device__ __forceinline__ void fr_transform(const SampleParams& P, const RowCfg& c,
+                                             const llima_u32x4 (&qq)[FrGeom<TL>::NL], uint32_t m,
+                                             const uint32_t* mrow, int i0, int lo, const uint32_t* table,
+                                             float (&x)[FrGeom<TL>::FE]) {
+#pragma unroll
+    for (int e = 0; e < FrGeom<TL>::FE; ++e) {
+        const int i = i0 + e;
+        float l = i < P.V ? fr_value<TL>(qq, e) : -__builtin_inff();
+        if (l != l) l = -__builtin_inff();
+        if (mrow && !((m >> (i & 31)) & 1u)) l = -__builtin_inff();
+        if (PEN && i < P.V) {
+            const uint32_t cnt = table_count(table, (uint32_t)(i - lo));
+            if (cnt) l = penalize(l, cnt, c);
+        }
+        x[e] = l;
+    }
+    if (!c.greedy && c.T != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < FrGeom<TL>::FE; ++e) x[e] = x[e] / c.T;
+    }
+}
+
+// Streams steps [s_begin, s_end) of a row through fn(x, i0): x[e] is the value
+// of id i0 + e after the row's transform (NaN -> -inf, mask, penalties, / T
+// unless greedy; -inf past the row), a whole step's values at once so that
+// fn can work on them without a branch per value: step s
+// covers the FrGeom::STEP ids from step_base(s) (a multiple of FrGeom::FE),
+// thread t taking FE consecutive ids (within one mask word).  The loads of step
+// s + NB - 1 are requested before step s is worked on, so NB steps (64 KB of
+// fp32 per workgroup) are in flight instead of one; barriers do not wait for
+// outstanding global loads.  step_end(s) is called by every thread after step
+// s.  table holds the history counts of the SMP_SEG segment in use (rows with
+// penalties), rebuilt when a step enters another segment.
+template <typename TL, int NB, bool VEC, bool PEN, class Base, class Fn, class StepEnd>
+__device__ __forceinline__ void fr_stream(const SampleParams& P, int row, const RowCfg& c, uint32_t* table,
+                                          int s_begin, int s_end, Base step_base, Fn fn, StepEnd step_end) {
+    using FG = FrGeom<TL>;
+    if (s_end <= s_begin) {                                   // uniform
+        __syncthreads();
+        return;
+    }
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    const int V = P.V;
+    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
+    // the mask word is loaded on every row (from the uniforms when there is no
+    // mask) so that every step issues the same loads
+    const uint32_t* mload = mrow ? mrow : (const uint32_t*)P.uniforms;
+    const int mlast = mrow ? (V - 1) >> 5 : 0;
+    int seg = -1;                                             // the segment table holds
+    llima_u32x4 q[NB][FG::NL];
+    uint32_t mw[NB] = {};
+    auto issue = [&](llima_u32x4 (&qq)[FG::NL], uint32_t& m, int s) __attribute__((always_inline)) {
+        // past the range: the last step again (cache hits, no new traffic)
+        const int i0 = step_base(s < s_end ? s : s_end - 1) + (int)threadIdx.x * FG::FE;
+        const int mi = i0 >> 5;
+        m = mload[mi < mlast ? mi : mlast];
+        fr_issue<TL, VEC>(rowp, i0, V, qq);
+    };
+    auto work = [&](const llima_u32x4 (&qq)[FG::NL], uint32_t m, int s) __attribute__((always_inline)) {
+        const int base = step_base(s);
+        const int lo = base & ~(SMP_SEG - 1);
+        if constexpr (PEN) {
+            if (lo != seg) {                                  // uniform
+                if (seg >= 0) __syncthreads();                // every thread is done with the old table
+                count_history(P, row, c.hlen, lo, lo + SMP_SEG < V ? lo + SMP_SEG : V, table, SMP_SEG / 2);
+                seg = lo;
+            }
+        }
+        const int i0 = base + (int)threadIdx.x * FG::FE;
+        float x[FG::FE];
+        fr_transform<TL, PEN>(P, c, qq, m, mrow, i0, lo, table, x);
+        fn(x, i0);                                            // ids past the row: -inf
+        step_end(s);
+    };
+    // the scheduling barriers keep the loads in step order (waiting for one
+    // step's data then waits for no later step's)
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b) {
+        issue(q[b], mw[b], s_begin + b);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the step loop stays rolled: its body is executed from the instruction
+    // cache after the first round (fully unrolled, every step would be code
+    // fetched once)
+#pragma clang loop unroll(disable)
+    for (int s0 = s_begin; s0 < s_end; s0 += NB) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int nb = (b + NB - 1) % NB;                 // the slot worked on last
+            issue(q[nb], mw[nb], s0 + b + NB - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s0 + b < s_end) work(q[b], mw[b], s0 + b);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __syncthreads();
+}
+
+// fr_stream with the row's load width and penalties as template arguments.
+template <typename TL, int NB, class Base, class Fn, class StepEnd>
+__device__ __forceinline__ void fr_stream_row(const SampleParams& P, int row, const RowCfg& c, uint32_t* table,
+                                              int s_begin, int s_end, Base step_base, Fn fn, StepEnd step_end) {
+    if (P.vec_ok) {
+        if (c.pen) fr_stream<TL, NB, true, true>(P, row, c, table, s_begin, s_end, step_base, fn, step_end);
+        else fr_stream<TL, NB, true, false>(P, row, c, table, s_begin, s_end, step_base, fn, step_end);
+    } else {
+        if (c.pen) fr_stream<TL, NB, false, true>(P, row, c, table, s_begin, s_end, step_base, fn, step_end);
+        else fr_stream<TL, NB, false, false>(P, row, c, table, s_begin, s_end, step_base, fn, step_end);
+    }
+}
+
 // Exact multi-pass selection by one workgroup; recomputes x for the whole row on
 // every pass (history table rebuilt per segment).
 template <typename TL>
@@ -1373,6 +1561,482 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
         write_keep(P, row, [&](auto set) {
             for_each_x([&](float x, uint32_t id) { fin_elem(x, id, [&](uint32_t i, uint64_t) { set(i); }); });
         });
+}
+
+// ------------------------------------------------------------------ split rows
+// Rows without top-k whose candidates overflow the sweep's regions (ordinary
+// logits under top-p alone, or a grammar mask that allows much of the row) in
+// a batch whose other rows keep the two-launch path (per-row settings, or a
+// mask): sample_finish then runs with P.fsplit workgroups per row, and such a
+// row is binned by all of them in parallel instead of by one workgroup's
+// full-row passes.  Part f takes chunks [f SMP_RCPW, (f + 1) SMP_RCPW): every
+// value's exact weight into the full-row path's SMP_DBINS value bins below the
+// row maximum (fl(max M / T) from the sweep's headers), written per chunk to
+// the chunk's region as the mass above each bin and the bin's count, with the
+// chunk's mass and the first bin holding a value below the min-p threshold.
+// The stores are write-through (agent scope) and complete before the part is
+// counted on the row's arrival counter; the last part to arrive reads them
+// back (agent-scope loads miss stale lines) and finishes the row: the
+// boundary bin bb (the top-p boundary bin b* or the min-p bin, the higher of
+// the two), the members of bb from a pass over the chunks holding any, theta
+// among them, each chunk's kept mass, the chunk of the draw target and a scan
+// of it in id order.  Every weight, bin and test is the full-row path's, so
+// the kept set, the token and its probability are the same; a row whose
+// boundary bin holds more than SMP_FRMCAP values takes the full-row path.
+//
+// Region use (slot 0, the sweep's header, is kept; the candidate slots are
+// not read on such rows):
+//   SMP_RCUM + b, b < SMP_DBINS  (mass of the chunk above bin b) << 14 | count of b
+//   SMP_RCUM + SMP_DBINS         the chunk's mass << 14
+//   SMP_RBMF                     the chunk's first bin with a value below min-p
+//   SMP_RSTGI, SMP_RSTG          staged values: every value of the chunk in bins
+//                                [lo, hi], a window around the boundary bin of
+//                                the part's own chunks (at most SMP_RSTG_CAP);
+//                                the last part reads a chunk again only when
+//                                the row's boundary bin lies outside it
+#define SMP_RCUM 1
+#define SMP_RBMF (SMP_RCUM + SMP_DBINS + 1)
+#define SMP_RSTGI (SMP_RBMF + 1)                   // staged bins lo | hi << 16 | count << 32
+#define SMP_RSTG (SMP_RSTGI + 1)                   // staged values (key << 32 | id)
+#define SMP_RSTG_CAP (SMP_REGION - SMP_RSTG)       // 60
+#define SMP_RCPW 4                                 // chunks per part
+static_assert(SMP_RBMF < SMP_REGION, "split-row region layout");
+
+// Whether the row is split (every part of it decides alike, from the sweep's
+// headers): no top-k, not greedy, a finite T, a region that overflowed or
+// more candidates than the finish gathers, and a value above -inf.  Returns
+// the row's maximum key, or 0.
+__device__ __forceinline__ uint32_t split_row(const SampleParams& P, int row, const RowCfg& c, FinShared& sh) {
+    if (P.fsplit <= 1 || c.greedy || c.k > 0 || !(c.T < __builtin_inff()) || P.S > SMP_MAX_S) return 0u;
+    const uint32_t t = threadIdx.x;
+    uint32_t ov = 0, cnt = 0, mk = 0;
+    if ((int)t < P.S) {
+        const uint64_t h = *region_of(P, (uint32_t)row, t);
+        const uint32_t lo = (uint32_t)h;
+        ov = (lo >> 16) & HF_OVERFLOW;
+        cnt = ov ? 0u : (lo & 0xFFFFu);
+        const float M = __uint_as_float((uint32_t)(h >> 32));
+        mk = M > -__builtin_inff() ? f32_key(M / c.T) : 0u;
+    }
+    ov = block_max_u32(ov, sh.bs);
+    cnt = block_sum_u32(cnt, sh.bs);
+    mk = block_max_u32(mk, sh.bs);
+    return ((ov != 0u || cnt > SMP_FIN_CAP) && mk > LLIMA_KEY_NEG_INF) ? mk : 0u;
+}
+
+// The last part of a split row to arrive: the chunks' bins merged, the
+// boundary, its members, theta, the kept masses and the draw.
+template <typename TL>
+__device__ __forceinline__ void split_final(const SampleParams& P, int row, const RowCfg& c, uint32_t kmax, FinShared& sh) {
+    using FG = FrGeom<TL>;
+    constexpr int CV = FG::CHUNK;
+    constexpr int SPC = CV / FG::STEP;
+    const int S = P.S, V = P.V;
+    const uint32_t t = threadIdx.x;
+    const float xmax = key_f32(kmax);
+    uint64_t* r0 = region_of(P, (uint32_t)row, 0);
+    // ---- the chunks merged: mass above bins 2t and 2t + 1 and their counts;
+    //      Z; the first bin below min-p
+    uint64_t a0 = 0, a1 = 0;
+    uint32_t n0 = 0, n1 = 0;
+    if (t < SMP_DBINS / 2) {
+        constexpr int NB = 16;
+        for (int b0 = 0; b0 < S; b0 += NB) {
+            uint64_t v0[NB], v1[NB];
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int ci = b0 + i < S ? b0 + i : S - 1;
+                uint64_t* q = r0 + (size_t)ci * SMP_REGION + SMP_RCUM + 2u * t;
+                v0[i] = load_agent(q);
+                v1[i] = load_agent(q + 1);
+            }
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const bool in = b0 + i < S;
+                a0 += in ? v0[i] >> 14 : 0ull;
+                n0 += in ? (uint32_t)(v0[i] & 0x3FFFu) : 0u;
+                a1 += in ? v1[i] >> 14 : 0ull;
+                n1 += in ? (uint32_t)(v1[i] & 0x3FFFu) : 0u;
+            }
+        }
+    }
+    uint64_t zc = 0;
+    uint32_t bmc = SMP_DBINS;
+    if ((int)t < S) {
+        uint64_t* reg = r0 + (size_t)t * SMP_REGION;
+        zc = load_agent(reg + SMP_RCUM + SMP_DBINS) >> 14;
+        bmc = (uint32_t)load_agent(reg + SMP_RBMF);
+    }
+    const uint64_t Z = block_sum_u64(zc, sh.bs);
+    const uint32_t bmf = ~block_max_u32(~bmc, sh.bs);
+    FIN_MARK_ANY(8);
+    // ---- the top-p boundary bin b*: the last non-empty bin whose mass above,
+    //      times 2^32, is below p32 Z; the top non-empty bin when none is
+    const bool topp = c.p < 1.0f;
+    uint32_t bstar = SMP_DBINS;
+    if (topp) {                                              // uniform
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Z;
+        const bool q0 = n0 > 0u && (((llima_u128)a0 << 32) < PZ);
+        const bool q1 = n1 > 0u && (((llima_u128)a1 << 32) < PZ);
+        const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
+        const uint32_t ne = n0 ? 2u * t : (n1 ? 2u * t + 1u : 0xFFFFFFFFu);
+        const uint32_t top = ~block_max_u32(~ne, sh.bs);
+        bstar = qb ? qb - 1u : top;
+    }
+    // the boundary: values in bins below bb are kept, above it not
+    const uint32_t bb = bstar < bmf ? bstar : bmf;
+    if ((bb >> 1) == t) sh.sel64[0] = (bb & 1u) ? a1 : a0;   // mass above bb (when bb < SMP_DBINS)
+    // ---- each chunk's mass above bb and its members of bb: from the chunk's
+    //      staging when bb lies in its window, else from a read of the chunk
+    uint64_t* kc = &sh.part[0][0][0];                        // kept mass per chunk (SMP_MAX_S)
+    uint32_t mc = 0, sn = 0;
+    bool staged = false;
+    if ((int)t < S) {
+        uint64_t* reg = r0 + (size_t)t * SMP_REGION;
+        const uint64_t v = load_agent(reg + SMP_RCUM + bb);
+        const uint64_t si = load_agent(reg + SMP_RSTGI);
+        kc[t] = v >> 14;
+        mc = bb < SMP_DBINS ? (uint32_t)(v & 0x3FFFu) : 0u;
+        const uint32_t lo = (uint32_t)si & 0xFFFFu, hi = ((uint32_t)si >> 16) & 0xFFFFu;
+        sn = (uint32_t)(si >> 32);
+        staged = mc > 0u && lo <= bb && bb <= hi;
+    }
+    uint32_t nlist, nstg;
+    const uint32_t li = block_excl_scan_u32(mc > 0u && !staged ? 1u : 0u, &nlist, sh.bs);
+    if (mc > 0u && !staged) sh.ccount[li] = t;               // the chunks read again
+    const uint32_t ls = block_excl_scan_u32(staged ? 1u : 0u, &nstg, sh.bs);
+    if (staged) sh.coff[ls] = t | (sn << 16);                // the chunks whose staging holds them
+    const uint32_t nm = block_sum_u32(mc, sh.bs);            // its barriers publish the lists
+    const uint64_t above = sh.sel64[0];
+    FIN_MARK_ANY(9);
+    if (nm > SMP_FRMCAP) {                                   // uniform: a nearly flat row
+        finish_full_row<TL>(P, row, c, sh);
+        return;
+    }
+    // ---- the members of bb: from the staging (a wave per chunk), then a pass
+    //      over the chunks whose staging does not hold them
+    uint64_t* mem = (uint64_t*)&sh.sv2[0][0];                // SMP_FRMCAP members
+    if (t == 0) sh.lcount = 0;
+    __syncthreads();
+    const uint32_t lane = lane_id();
+    for (uint32_t k = wave_id(); k < nstg; k += LLIMA_WAVES) {
+        const uint32_t e = sh.coff[k];
+        uint64_t* st = r0 + (size_t)(e & 0xFFFFu) * SMP_REGION + SMP_RSTG;
+        const bool in = lane < (e >> 16);
+        const uint64_t v = in ? load_agent(st + lane) : 0ull;
+        const uint32_t key = (uint32_t)(v >> 32);
+        if (in && (uint32_t)dense_d16(key_f32(key), xmax) == bb) {
+            const uint32_t o = atomicAdd(&sh.lcount, 1u);
+            if (o < SMP_FRMCAP) mem[o] = v;
+        }
+    }
+    auto listed = [&](int s) { return (int)sh.ccount[s / SPC] * CV + (s % SPC) * FG::STEP; };
+    auto member = [&](const float (&x)[FG::FE], int i0) {
+        uint32_t hm = 0;
+#pragma unroll
+        for (int e = 0; e < FG::FE; ++e)
+            hm |= x[e] > -__builtin_inff() && (uint32_t)dense_d16(x[e], xmax) == bb ? 1u << e : 0u;
+        const uint32_t n = (uint32_t)__popc(hm);
+        if (ballot(n != 0u)) {                               // uniform in the wave
+            const uint32_t inc = wave_incl_scan_u32(n);
+            uint32_t base = 0;
+            if (lane == 63) base = atomicAdd(&sh.lcount, inc);
+            uint32_t o = readlane(base, 63) + inc - n;
+            while (hm) {
+                const int e = __builtin_ctz(hm);
+                hm &= hm - 1u;
+                if (o < SMP_FRMCAP) mem[o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
+                ++o;
+            }
+        }
+    };
+    fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, 0, (int)nlist * SPC, listed, member, [](int) {});
+    if (sh.lcount != nm) {                                   // uniform: never (the counts are the bins')
+        finish_full_row<TL>(P, row, c, sh);
+        return;
+    }
+    const uint32_t nmem = nm;
+    FIN_MARK_ANY(10);
+    // ---- theta among the members (top-p boundary), the kept members' weights
+    //      added to their chunks
+    constexpr int EPT = SMP_FRMCAP / LLIMA_WG;
+    uint32_t key[EPT], mid[EPT];
+    uint64_t w[EPT];
+    uint32_t mk = 0, nmk = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const uint32_t j = t + (uint32_t)e * LLIMA_WG;
+        const uint64_t v = j < nmem ? mem[j] : 0ull;
+        key[e] = (uint32_t)(v >> 32);
+        mid[e] = (uint32_t)v;
+        w[e] = key[e] ? wf_u64(dense_wf(key_f32(key[e]), xmax)) : 0ull;
+        mk = key[e] > mk ? key[e] : mk;
+        nmk = key[e] && ~key[e] > nmk ? ~key[e] : nmk;
+    }
+    uint32_t theta = 0;
+    if (topp && bb == bstar && nmem > 0u) {                  // uniform
+        sh.hmass[0][t] = 0;
+        sh.hmass[1][t] = 0;
+        mk = block_max_u32(mk, sh.bs);
+        const uint32_t mkmin = ~block_max_u32(nmk, sh.bs);
+        const uint64_t p32 = frac32(c.p);
+        theta = fin_topp_desc<EPT>(key, w, p32, mkmin, mk, sh, above, (llima_u128)p32 * Z, true);
+    }
+    const uint64_t mthr = c.m > 0.0f ? frac32(c.m) << 4 : 0ull;
+    const bool tb = bb == bstar, mb = bb == bmf;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+        if (key[e] && (!tb || key[e] >= theta) && (!mb || w[e] >= mthr))
+            atomicAdd((unsigned long long*)&kc[mid[e] / (uint32_t)CV], (unsigned long long)w[e]);
+    if (t == 0) {             // overwritten by the thread whose chunk holds the target
+        sh.sel[0] = 0;
+        sh.sel64[1] = 0;
+    }
+    __syncthreads();
+    FIN_MARK_ANY(11);
+    // ---- the chunk of the draw target, then that chunk in id order
+    const uint64_t m = (int)t < S ? kc[t] : 0ull;
+    uint64_t Zf;
+    const uint64_t below = block_excl_scan_u64(m, &Zf, sh.bs);
+    if (Zf == 0) {
+        if (t == 0) write_result(P, row, -1, 0.0f);
+        return;
+    }
+    const uint64_t target = (uint64_t)(((llima_u128)uniform32(c.u) * Zf) >> 32);
+    if (m > 0 && below <= target && target < below + m) {
+        sh.sel[0] = t;
+        sh.sel64[1] = target - below;
+    }
+    __syncthreads();
+    const int cs = (int)sh.sel[0];
+    uint64_t rel = sh.sel64[1];
+    const float mthr_f = dense_mthr(c);
+    const TL* rowp = (const TL*)P.logits + (size_t)row * P.row_stride;
+    const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * ((V + 31) >> 5) : nullptr;
+    const int c0 = cs * CV;
+    const int lo = c0 & ~(SMP_SEG - 1);
+    llima_u32x4 qd[SPC][FG::NL];
+    uint32_t mw[SPC] = {};
+#pragma unroll
+    for (int j = 0; j < SPC; ++j) {
+        const int i0 = c0 + j * FG::STEP + (int)t * FG::FE;
+        if (mrow) mw[j] = mrow[(i0 < V ? i0 : V - 1) >> 5];
+        if (P.vec_ok) fr_issue<TL, true>(rowp, i0, V, qd[j]);
+        else fr_issue<TL, false>(rowp, i0, V, qd[j]);
+    }
+    if (c.pen) count_history(P, row, c.hlen, lo, lo + SMP_SEG < V ? lo + SMP_SEG : V, sh.u.table, SMP_SEG / 2);
+    const float blo = (float)bb;
+#pragma unroll
+    for (int j = 0; j < SPC; ++j) {
+        const int i0 = c0 + j * FG::STEP + (int)t * FG::FE;
+        float x[FG::FE];
+        if (c.pen) fr_transform<TL, true>(P, c, qd[j], mw[j], mrow, i0, lo, sh.u.table, x);
+        else fr_transform<TL, false>(P, c, qd[j], mw[j], mrow, i0, lo, sh.u.table, x);
+        uint64_t wv[FG::FE], sum = 0;
+#pragma unroll
+        for (int e = 0; e < FG::FE; ++e) {
+            uint64_t we = 0;
+            if (i0 + e < V && x[e] > -__builtin_inff()) {
+                const float d16 = dense_d16(x[e], xmax);
+                const float wf = dense_wf(x[e], xmax);
+                const bool kept = d16 < blo ||
+                                  ((uint32_t)d16 == bb && (!tb || f32_key(x[e]) >= theta) && (!mb || wf >= mthr_f));
+                we = kept ? wf_u64(wf) : 0ull;
+            }
+            wv[e] = we;
+            sum += we;
+        }
+        uint64_t tot;
+        const uint64_t bl = block_excl_scan_u64(sum, &tot, sh.bs);
+        if (rel < tot) {                                     // uniform
+            if (sum > 0 && bl <= rel && rel < bl + sum) {
+                uint64_t a = bl, wtok = 0;
+                int32_t tok = -1;
+#pragma unroll
+                for (int e = 0; e < FG::FE; ++e) {
+                    const bool hit = tok < 0 && wv[e] > 0 && rel < a + wv[e];
+                    tok = hit ? i0 + e : tok;
+                    wtok = hit ? wv[e] : wtok;
+                    a += wv[e];
+                }
+                write_result(P, row, tok, (float)((double)wtok / (double)Zf));
+            }
+            FIN_MARK_ANY(12);
+            return;
+        }
+        rel -= tot;
+    }
+}
+
+// Part `part` of a split row: its chunks' bins (kept in LDS), the staging of
+// each chunk's values around the boundary bin the part's own chunks give (a
+// second read of the chunks, from the cache), then the arrival; the last part
+// finishes the row.
+template <typename TL>
+__device__ __forceinline__ void split_part(const SampleParams& P, int row, const RowCfg& c, uint32_t kmax,
+                                           int part, FinShared& sh) {
+    using FG = FrGeom<TL>;
+    constexpr int CV = FG::CHUNK;
+    constexpr int SPC = CV / FG::STEP;                       // steps per chunk
+    static_assert(SPC * FG::STEP == CV, "steps tile a chunk");
+    static_assert(SMP_SEG / 2 * sizeof(uint32_t) + (SMP_RCPW * SMP_DBINS + 64) * sizeof(uint64_t) <=
+                      sizeof(FinShared::u),
+                  "the part's chunk bins fit beside the history table");
+    static_assert(SMP_RCPW <= LLIMA_WAVES, "one wave per chunk of a part");
+    const int S = P.S;
+    const int ch0 = part * SMP_RCPW, ch1 = ch0 + SMP_RCPW < S ? ch0 + SMP_RCPW : S;
+    const int nch = ch1 - ch0;
+    const float xmax = key_f32(kmax);
+    const float mthr_f = dense_mthr(c);
+    const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
+    // [SMP_RCPW][SMP_DBINS] chunk bins, then a spare bin per lane (-inf values)
+    uint64_t* cb = (uint64_t*)(sh.u.table + SMP_SEG / 2);
+    for (uint32_t i = t; i < (uint32_t)nch * SMP_DBINS; i += LLIMA_WG) cb[i] = 0;
+    __syncthreads();
+    FIN_MARK(5);
+    uint32_t bmf = SMP_DBINS;                                // this thread's first bin below min-p
+    uint32_t bmf_part = SMP_DBINS;                           // the part's (uniform)
+    auto bin = [&](const float (&x)[FG::FE], int i0) {
+        // every weight first (independent chains), then the LDS atomics, -inf
+        // values into the lane's spare bin: no branch per value
+        const uint32_t cbase = (uint32_t)(i0 / CV - ch0) * SMP_DBINS;
+        uint32_t slot[FG::FE];
+        uint64_t add[FG::FE];
+#pragma unroll
+        for (int e = 0; e < FG::FE; ++e) {
+            const bool fin = x[e] > -__builtin_inff();
+            const float wf = dense_wf(x[e], xmax);
+            const uint32_t b = (uint32_t)dense_d16(x[e], xmax);
+            slot[e] = fin ? cbase + b : SMP_RCPW * SMP_DBINS + lane;
+            add[e] = fin ? (wf_u64(wf) << 14) | 1ull : 0ull;
+            bmf = fin && wf < mthr_f && b < bmf ? b : bmf;
+        }
+#pragma unroll
+        for (int e = 0; e < FG::FE; ++e) atomicAdd((unsigned long long*)&cb[slot[e]], (unsigned long long)add[e]);
+    };
+    auto chunk_end = [&](int s) {
+        if (s % SPC != SPC - 1) return;                      // uniform: not the chunk's last step
+        const uint32_t bm = ~block_max_u32(~bmf, sh.bs);     // its barriers complete the bins
+        const uint64_t* bins = cb + (size_t)(s / SPC - ch0) * SMP_DBINS;
+        const bool mine = t < SMP_DBINS / 2;
+        const uint64_t h0 = mine ? bins[2u * t] : 0ull, h1 = mine ? bins[2u * t + 1u] : 0ull;
+        uint64_t tot;
+        const uint64_t ab = block_excl_scan_u64((h0 >> 14) + (h1 >> 14), &tot, sh.bs);
+        uint64_t* reg = region_of(P, (uint32_t)row, (uint32_t)(s / SPC));
+        if (mine) {
+            store_agent(reg + SMP_RCUM + 2u * t, (ab << 14) | (h0 & 0x3FFFu));
+            store_agent(reg + SMP_RCUM + 2u * t + 1u, ((ab + (h0 >> 14)) << 14) | (h1 & 0x3FFFu));
+        }
+        if (t == 0) {
+            store_agent(reg + SMP_RCUM + SMP_DBINS, tot << 14);
+            store_agent(reg + SMP_RBMF, bm);
+        }
+        bmf_part = bm < bmf_part ? bm : bmf_part;
+        bmf = SMP_DBINS;
+    };
+    auto by_step = [](int s) { return s * FG::STEP; };
+    fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, ch0 * SPC, ch1 * SPC, by_step, bin, chunk_end);
+    FIN_MARK(6);
+    // ---- the boundary bin of the part's own chunks (the row's, estimated)
+    uint64_t m0 = 0, m1 = 0;
+    uint32_t n0 = 0, n1 = 0;
+    if (t < SMP_DBINS / 2) {
+        for (int cl = 0; cl < nch; ++cl) {
+            const uint64_t h0 = cb[cl * SMP_DBINS + 2 * (int)t], h1 = cb[cl * SMP_DBINS + 2 * (int)t + 1];
+            m0 += h0 >> 14;
+            n0 += (uint32_t)(h0 & 0x3FFFu);
+            m1 += h1 >> 14;
+            n1 += (uint32_t)(h1 & 0x3FFFu);
+        }
+    }
+    uint64_t Zp;
+    const uint64_t ab = block_excl_scan_u64(m0 + m1, &Zp, sh.bs);
+    uint32_t bhat = SMP_DBINS;
+    if (c.p < 1.0f) {                                        // uniform
+        const llima_u128 PZ = (llima_u128)frac32(c.p) * Zp;
+        const bool q0 = n0 > 0u && (((llima_u128)ab << 32) < PZ);
+        const bool q1 = n1 > 0u && (((llima_u128)(ab + m0) << 32) < PZ);
+        const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
+        const uint32_t ne = n0 ? 2u * t : (n1 ? 2u * t + 1u : 0xFFFFFFFFu);
+        const uint32_t top = ~block_max_u32(~ne, sh.bs);
+        bhat = qb ? qb - 1u : (top < SMP_DBINS ? top : SMP_DBINS);
+    }
+    const uint32_t bbh = bhat < bmf_part ? bhat : bmf_part;
+    FIN_MARK(13);
+    // ---- each chunk's window: wave cl, lane d: bins bbh - d and bbh + d; the
+    //      widest window whose values fit the staging
+    if (bbh < SMP_DBINS && (int)wave < nch) {
+        const uint64_t* bins = cb + (size_t)wave * SMP_DBINS;
+        const int lo_b = (int)bbh - (int)lane, hi_b = (int)bbh + (int)lane;
+        uint32_t cnt = hi_b < SMP_DBINS ? (uint32_t)(bins[hi_b] & 0x3FFFu) : 0u;
+        cnt += lane > 0 && lo_b >= 0 ? (uint32_t)(bins[lo_b] & 0x3FFFu) : 0u;
+        const uint32_t inc = wave_incl_scan_u32(cnt);
+        const uint64_t fits = ballot(inc <= SMP_RSTG_CAP);   // a prefix of the lanes
+        const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest half-width
+        if (lane == 0) {
+            const uint32_t lo = w < 0 ? 1u : (uint32_t)((int)bbh - w > 0 ? (int)bbh - w : 0);
+            const uint32_t hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
+            sh.ccount[wave] = lo | (hi << 16);
+            sh.coff[wave] = 0;
+        }
+    } else if ((int)wave < nch && lane == 0) {
+        sh.ccount[wave] = 1u;                                // empty: lo 1, hi 0
+        sh.coff[wave] = 0;
+    }
+    __syncthreads();
+    uint32_t win[SMP_RCPW];
+#pragma unroll
+    for (int cl = 0; cl < SMP_RCPW; ++cl) win[cl] = cl < nch ? sh.ccount[cl] : 1u;
+    // staged values gather in LDS during the pass (a global store in it
+    // would make every step wait for all loads), then go to the regions
+    static_assert(SMP_RCPW * SMP_RSTG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv), "staging in LDS");
+    uint64_t* stg = (uint64_t*)&sh.sv[0];                    // [SMP_RCPW][SMP_RSTG_CAP]
+    if (bbh < SMP_DBINS) {                                   // uniform
+        // ---- the chunks again: each window's values to the chunk's staging
+        auto stage = [&](const float (&x)[FG::FE], int i0) {
+            // the step's window values: a bit mask per thread, one LDS atomic
+            // per wave for their places (the step lies in one chunk)
+            const uint32_t cl = (uint32_t)(i0 / CV - ch0);
+            uint32_t wc = win[0];
+#pragma unroll
+            for (int k = 1; k < SMP_RCPW; ++k) wc = cl == (uint32_t)k ? win[k] : wc;
+            uint32_t hm = 0;
+#pragma unroll
+            for (int e = 0; e < FG::FE; ++e) {
+                const uint32_t b = (uint32_t)dense_d16(x[e], xmax);
+                hm |= x[e] > -__builtin_inff() && b >= (wc & 0xFFFFu) && b <= (wc >> 16) ? 1u << e : 0u;
+            }
+            const uint32_t n = (uint32_t)__popc(hm);
+            if (ballot(n != 0u)) {                           // uniform in the wave
+                const uint32_t inc = wave_incl_scan_u32(n);
+                uint32_t base = 0;
+                if (lane == 63) base = atomicAdd(&sh.coff[cl], inc);
+                uint32_t o = readlane(base, 63) + inc - n;
+                while (hm) {
+                    const int e = __builtin_ctz(hm);
+                    hm &= hm - 1u;
+                    if (o < SMP_RSTG_CAP) stg[cl * SMP_RSTG_CAP + o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
+                    ++o;
+                }
+            }
+        };
+        fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, ch0 * SPC, ch1 * SPC, by_step, stage, [](int) {});
+    }
+    FIN_MARK(14);
+    for (int cl = (int)wave; cl < nch; cl += LLIMA_WAVES) {
+        const uint32_t n = sh.coff[cl] < SMP_RSTG_CAP ? sh.coff[cl] : SMP_RSTG_CAP;
+        uint64_t* reg = region_of(P, (uint32_t)row, (uint32_t)(ch0 + cl));
+        if (lane < n) store_agent(reg + SMP_RSTG + lane, stg[cl * SMP_RSTG_CAP + lane]);
+        if (lane == 0) store_agent(reg + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
+    }
+    // every store of the part completes before its arrival is counted
+    __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
+    __syncthreads();
+    FIN_MARK(15);
+    if (t == 0) sh.sel[3] = arrive_agent(P.rcnt + (size_t)row * SMP_RCNT, 1u) + 1u == (uint32_t)P.fsplit;
+    __syncthreads();
+    FIN_MARK(7);
+    if (sh.sel[3]) split_final<TL>(P, row, c, kmax, sh);
 }
 
 // ------------------------------------------------------------------ small path
@@ -2181,13 +2845,25 @@ __device__ __forceinline__ bool fin_direct(const SampleParams& P, int row, const
                             : fin_tail<2>(P, row, c, me, nst, lowkey, gkey, hid, sh);
 }
 
-template <typename TL>
+// SPLIT: the instantiation launched when rows may be split (P.fsplit > 1); the
+// split code stays out of the other one, whose registers it would crowd.
+template <typename TL, bool SPLIT>
 __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
     __shared__ FinShared sh;
     FIN_BEGIN();
     const int row = blockIdx.x;
     if (P.wide && P.out_ids[row] != SMP_PENDING) return;     // uniform: finished by the wide kernel
     const RowCfg c = load_cfg(P, row);
+    if constexpr (SPLIT) {
+        if (!c.greedy && c.k == 0) {                          // uniform: the row may be split
+            const uint32_t kx = split_row(P, row, c, sh);
+            if (kx) {
+                split_part<TL>(P, row, c, kx, (int)blockIdx.y, sh);
+                return;
+            }
+        }
+        if (blockIdx.y > 0) return;                           // the other parts serve split rows only
+    }
     const uint32_t t = threadIdx.x, lane = lane_id(), wave = wave_id();
     const int S = P.S;
     bool done = false;
@@ -2245,7 +2921,8 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
         const uint32_t flags = q[0].x >> 16;
         const uint32_t count = (flags & HF_OVERFLOW) ? 0u : (q[0].x & 0xFFFFu);
         const uint32_t ovf = !hdr ? 0u : (flags & HF_OVERFLOW) ? 2u : (SMP_HDR + count > pre ? 1u : 0u);
-        const float g0 = __uint_as_float(q[0].y);
+        const float h0 = __uint_as_float(q[0].y);
+        const float g0 = c.k > 0 ? h0 : nontopk_bound(P, c, h0);
         const float gt0 = g0 / c.T;
         const uint32_t gk = (hdr & !c.greedy & (g0 > -__builtin_inff())) ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
         const uint64_t gr = hdr ? ((uint64_t)q[0].w << 32) | q[0].z : 0ull;
@@ -2428,7 +3105,7 @@ __global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
         const uint32_t lo = (uint32_t)h;
         ovf = (lo >> 16) & HF_OVERFLOW;
         cnt = ovf ? 0u : (lo & 0xFFFFu);
-        const float g0 = __uint_as_float((uint32_t)(h >> 32));
+        const float g0 = nontopk_bound(P, c, __uint_as_float((uint32_t)(h >> 32)));   // no top-k here
         const float gt0 = g0 / c.T;
         gk = g0 > -__builtin_inff() ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
     }
@@ -2641,6 +3318,8 @@ struct DenseGeom {
     static constexpr int CHUNK = LLIMA_WG * E;         // 4096 fp32 / 8192 bf16 (the sweep's chunk)
     static constexpr int WS = CHUNK / LLIMA_WAVES;     // ids per wave
 };
+static_assert(DenseGeom<float>::CHUNK == FrGeom<float>::CHUNK &&
+              DenseGeom<uint16_t>::CHUNK == FrGeom<uint16_t>::CHUNK, "one chunk size");
 
 __device__ __forceinline__ uint64_t* dense_member(uint64_t* r0, uint32_t j) {
     return r0 + (size_t)(j / SMP_DBINS) * SMP_REGION + (j % SMP_DBINS);
@@ -3298,7 +3977,8 @@ using namespace llima;
 extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
     if (B <= 0 || V <= 0 || (dtype != LLIMA_F32 && dtype != LLIMA_BF16)) return 0;
     const size_t S = (size_t)((V + chunk_values(dtype) - 1) / chunk_values(dtype));
-    return (size_t)B * S * SMP_REGION * sizeof(uint64_t);
+    // the chunk regions, then one split-row arrival counter (64 bytes) per row
+    return (size_t)B * S * SMP_REGION * sizeof(uint64_t) + (size_t)B * SMP_RCNT * sizeof(uint32_t);
 }
 
 #ifdef LLIMA_FINISH_TRACE
@@ -3377,6 +4057,12 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     // takes only the rows it left)
     P.wide = bitmask && !cfg->greedy && !cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V) &&
              P.S <= SMP_MAX_S;
+    // Rows without top-k whose candidates overflow are split over
+    // ceil(S / SMP_RCPW) finish workgroups in batches that keep the two-launch
+    // path: per-row top-k (rows of either kind), or a mask without top-k
+    P.rcnt = (uint32_t*)(P.ws + (size_t)B * P.S * SMP_REGION);
+    P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (cfg->top_k_rows || P.wide))
+                   ? (P.S + SMP_RCPW - 1) / SMP_RCPW : 1;
     // Rows without top-k (and without a mask) take the dense path: their sweep
     // bound would admit nearly every value of ordinary logits.
     const bool dense = !bitmask && !cfg->greedy && !cfg->top_k_rows &&
@@ -3389,11 +4075,13 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     } else if (dtype == LLIMA_F32) {
         launch_sweep<float>(P, st);
         if (P.wide) hipLaunchKernelGGL(sample_finish_wide<float>, dim3(B), dim3(SMP_WIDE), 0, st, P);
-        hipLaunchKernelGGL(sample_finish<float>, dim3(B), dim3(LLIMA_WG), 0, st, P);
+        if (P.fsplit > 1) hipLaunchKernelGGL((sample_finish<float, true>), dim3(B, P.fsplit), dim3(LLIMA_WG), 0, st, P);
+        else hipLaunchKernelGGL((sample_finish<float, false>), dim3(B), dim3(LLIMA_WG), 0, st, P);
     } else {
         launch_sweep<uint16_t>(P, st);
         if (P.wide) hipLaunchKernelGGL(sample_finish_wide<uint16_t>, dim3(B), dim3(SMP_WIDE), 0, st, P);
-        hipLaunchKernelGGL(sample_finish<uint16_t>, dim3(B), dim3(LLIMA_WG), 0, st, P);
+        if (P.fsplit > 1) hipLaunchKernelGGL((sample_finish<uint16_t, true>), dim3(B, P.fsplit), dim3(LLIMA_WG), 0, st, P);
+        else hipLaunchKernelGGL((sample_finish<uint16_t, false>), dim3(B), dim3(LLIMA_WG), 0, st, P);
     }
     return hipGetLastError() == hipSuccess ? LLIMA_OK : LLIMA_E_HIP;
 }

@@ -97,6 +97,27 @@ def constrained(B=32, V=151936, runs=47, seed=1003):
                 cfg=cfg)
 
 
+def constrained_half(B=32, V=151936, seed=1011):
+    """The C3 rows (B=32, fp32 vocab 151936, N(0, 3^2)) under a grammar mask
+    that allows about half of the ids (independent bits), each row's maximum
+    moved onto a masked-out id; T 1.0, top-p 0.9.  About 4700 candidates per
+    16 KB chunk pass the weight window: no candidate region holds them, so
+    the finish takes every row through its full-row path."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    logits = _normal(rng, (B, V), 3.0)
+    nw = (V + 31) // 32
+    mask = rng.integers(0, 2**32, size=(B, nw), dtype=np.uint64).astype(np.uint32)
+    ids = np.arange(V)
+    for b in range(B):
+        allowed = (mask[b, ids >> 5] >> (ids & 31).astype(np.uint32)) & 1
+        banned = np.flatnonzero(allowed == 0)
+        j = banned[rng.integers(0, len(banned))]
+        logits[b, j] = logits[b].max() + np.float32(5.0)
+    u = rng.random(B, dtype=np.float32)
+    return dict(name="constrained_half", logits=logits, history=None, uniforms=u, bitmask=mask,
+                cfg=dict(temperature=1.0, top_p=0.9))
+
+
 def _softmax64(x):
     x = x.astype(np.float64)
     x = x - x.max(axis=-1, keepdims=True)
@@ -238,6 +259,7 @@ WORKLOADS = {
     "single_row": single_row,
     "batched_penalties": batched_penalties,
     "constrained": constrained,
+    "constrained_half": constrained_half,
     "top_p_only": top_p_only,
     "speculative": speculative,
     "large_vocab_bf16": large_vocab_bf16,

@@ -91,7 +91,7 @@ def _cfg_obj(d, rows=None):
 
 
 def _sample_both(gpu, oracle, logits, u, cfgd, history=None, hist_len=None, mask=None,
-                 cfg_rows=None):
+                 cfg_rows=None, want_keep=True):
     import llima_amd
     from oracle.oracle import SamplerConfig as OC
     if cfg_rows is None:
@@ -104,16 +104,21 @@ def _sample_both(gpu, oracle, logits, u, cfgd, history=None, hist_len=None, mask
         B = logits.shape[0]
         ocfg = [OC(**{k: (v[b] if isinstance(v, list) else v) for k, v in cfg_rows.items()})
                 for b in range(B)]
-    ids, probs, keep = llima_amd.sample(_t(logits, gpu), _t(u, gpu), gcfg,
-                                        history=_t(history, gpu), history_len=_t(hist_len, gpu),
-                                        bitmask=_t(mask, gpu), return_keep=True)
-    eids, eprobs, ekeep = oracle.sample(logits, u, ocfg, history=history, hist_len=hist_len,
-                                        bitmask=mask, want_keep=True)
-    gi, gp, gk = _np(ids), _np(probs), _np(keep).view(np.uint32)
+    # without the kept-set output the batch may take other paths (rows split
+    # over several finish workgroups need none)
+    out = llima_amd.sample(_t(logits, gpu), _t(u, gpu), gcfg, history=_t(history, gpu),
+                           history_len=_t(hist_len, gpu), bitmask=_t(mask, gpu),
+                           return_keep=want_keep)
+    eout = oracle.sample(logits, u, ocfg, history=history, hist_len=hist_len, bitmask=mask,
+                         want_keep=want_keep)
+    eids, eprobs = eout[0], eout[1]
+    gi, gp = _np(out[0]), _np(out[1])
     bad = np.flatnonzero(gi != eids)
     assert bad.size == 0, f"ids differ at rows {bad[:8]}: gpu {gi[bad[:8]]} oracle {eids[bad[:8]]}"
     assert (gp.view(np.uint32) == eprobs.view(np.uint32)).all()
-    assert (gk == ekeep).all(), np.flatnonzero((gk != ekeep).any(axis=1))[:8]
+    if want_keep:
+        gk, ekeep = _np(out[2]).view(np.uint32), eout[2]
+        assert (gk == ekeep).all(), np.flatnonzero((gk != ekeep).any(axis=1))[:8]
     return gi
 
 
@@ -531,6 +536,56 @@ def test_sample_per_row_lazy_and_eager_penalties(gpu, oracle):
                 frequency_penalty=[0.3, 0.3, 0.1, 0.0, 0.1, -0.2, 0.3, 0.5])
     _sample_both(gpu, oracle, x, u, None, history=hist, cfg_rows=rows)
     _sample_both(gpu, oracle, wl.f32_to_bf16_bits(x), u, None, history=hist, cfg_rows=rows)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_split_rows(gpu, oracle, dtype):
+    """Rows without top-k whose candidates overflow the sweep's regions, in a
+    batch with per-row top-k: the finish splits each over ceil(S / 8)
+    workgroups (bins per chunk, the last to arrive finishes the row).  Every
+    kind of such row: top-p alone, min-p alone, both (either boundary the
+    higher), plain temperature, penalties of either sign, T != 1, a flat row
+    whose boundary bin holds more values than the split finish ranks (the
+    full-row path), an all -inf row; beside top-k rows and a greedy row."""
+    _say("sample split rows", dtype)
+    rng = np.random.default_rng(91)
+    B, V, H = 12, 128256, 700
+    x = (rng.standard_normal((B, V), dtype=np.float32) * np.float32(4.0)).astype(np.float32)
+    x[6] = np.float32(0.5) * np.round(rng.standard_normal(V).astype(np.float32) * 4)   # flat: few values
+    x[7] = -np.inf
+    x[8, :300] = np.nan
+    hist = rng.integers(0, V, size=(B, H)).astype(np.int32)
+    for b in range(B):
+        hist[b, :200] = np.resize(np.argsort(-np.nan_to_num(x[b], nan=-1e30))[:50], 200)
+    u = rng.random(B).astype(np.float32)
+    rows = dict(temperature=[1.0, 0.8, 1.3, 1.0, 0.7, 1.0, 1.0, 1.0, 0.9, 1.0, 0.0, 1.0],
+                top_k=[0, 0, 0, 0, 0, 0, 0, 0, 0, 50, 0, 40],
+                top_p=[0.9, 1.0, 0.95, 0.5, 1.0, 0.9, 0.9, 0.9, 0.99, 0.95, 1.0, 1.0],
+                min_p=[0.0, 0.1, 0.02, 0.3, 0.0, 0.0, 0.0, 0.0, 0.0, 0.05, 0.0, 0.0],
+                repetition_penalty=[1.0, 1.0, 1.2, 1.0, 1.0, 0.8, 1.0, 1.0, 1.1, 1.15, 1.0, 1.0],
+                presence_penalty=[0.0, 0.0, 0.5, 0.0, 0.0, -0.3, 0.0, 0.0, 0.2, 0.5, 0.0, 0.0],
+                frequency_penalty=[0.0, 0.0, 0.3, 0.0, 0.0, 0.1, 0.0, 0.0, 0.0, 0.3, 0.0, 0.0])
+    xx = x if dtype == "f32" else wl.f32_to_bf16_bits(x)
+    _sample_both(gpu, oracle, xx, u, None, history=hist, cfg_rows=rows, want_keep=False)
+    # the same rows again with other uniforms (other draw chunks)
+    _sample_both(gpu, oracle, xx, rng.random(B).astype(np.float32), None, history=hist,
+                 cfg_rows=rows, want_keep=False)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sample_split_masked_rows(gpu, oracle, dtype):
+    """A grammar mask that allows about half of each row, top-p without
+    top-k (the wide finish leaves these rows, whose regions overflow, to the
+    split finish); also min-p, and a mask allowing 3 of every 4 ids."""
+    _say("sample split masked rows", dtype)
+    w = wl.constrained_half(B=8)
+    x = w["logits"] if dtype == "f32" else wl.f32_to_bf16_bits(w["logits"])
+    _sample_both(gpu, oracle, x, w["uniforms"], w["cfg"], mask=w["bitmask"], want_keep=False)
+    _sample_both(gpu, oracle, x, w["uniforms"], dict(temperature=0.8, top_p=0.95, min_p=0.05),
+                 mask=w["bitmask"], want_keep=False)
+    m3 = w["bitmask"] | np.uint32(0x77777777)
+    _sample_both(gpu, oracle, x, w["uniforms"], dict(temperature=1.0, min_p=0.2), mask=m3,
+                 want_keep=False)
 
 
 def test_sample_lazy_penalty_hits(gpu, oracle):
