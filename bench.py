@@ -366,9 +366,11 @@ def main():
         if greedy_variant:
             cfgd = dict(greedy=True)
         cfg_c = dict(cfgd)
-        for k, arr in (w.get("cfg_rows") or {}).items():     # per-row settings
-            cfg_c[k] = torch.from_numpy(arr).to(dev)
-        cfg, keep_alive = llima_amd.SamplerConfig(**cfg_c).to_c(B, dev)
+        # per-row settings, from host memory as a serving loop holds its requests'
+        # settings (uploaded once, before timing)
+        for k, arr in (w.get("cfg_rows") or {}).items():
+            cfg_c[k] = torch.from_numpy(arr)
+        cfg, keep_alive = llima_amd.SamplerConfig(**cfg_c).to_c(B, dev, V)
         out_ids = torch.empty(B, dtype=torch.int32, device=dev)
         out_p = torch.empty(B, dtype=torch.float32, device=dev)
         nws = L.llima_sample_workspace_bytes(B, V, dt)

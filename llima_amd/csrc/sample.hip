@@ -4059,9 +4059,13 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
              P.S <= SMP_MAX_S;
     // Rows without top-k whose candidates overflow are split over
     // ceil(S / SMP_RCPW) finish workgroups in batches that keep the two-launch
-    // path: per-row top-k (rows of either kind), or a mask without top-k
+    // path: per-row top-k (rows of either kind), or a mask without top-k.  With
+    // per-row top-k, a scalar top_k in (0, V) is the caller's word that every
+    // row has top-k (a row without then takes the full-row path: slower, not
+    // wrong), and the lean finish is launched.
+    const bool rows_may_lack_topk = cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V);
     P.rcnt = (uint32_t*)(P.ws + (size_t)B * P.S * SMP_REGION);
-    P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (cfg->top_k_rows || P.wide))
+    P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (rows_may_lack_topk || P.wide))
                    ? (P.S + SMP_RCPW - 1) / SMP_RCPW : 1;
     // Rows without top-k (and without a mask) take the dense path: their sweep
     // bound would admit nearly every value of ordinary logits.

@@ -59,8 +59,14 @@ class SamplerConfig:
     presence_penalty: float | torch.Tensor = 0.0
     frequency_penalty: float | torch.Tensor = 0.0
     greedy: bool = False
+    # per-row top_k only: every row's entry is in (0, V).  Found by itself when
+    # the per-row top_k is given in host memory; a device tensor needs the
+    # caller's word.  It lets the call skip the finish that can split rows
+    # without top-k; a wrong True costs time (such a row takes the slower
+    # full-row path), never the result.
+    top_k_every_row: bool = False
 
-    def to_c(self, B: int, device) -> tuple[_lib.SamplerConfigC, list]:
+    def to_c(self, B: int, device, V: int | None = None) -> tuple[_lib.SamplerConfigC, list]:
         c = _lib.SamplerConfigC()
         keep = []
         for name, dtype, default in (("temperature", torch.float32, 1.0),
@@ -82,6 +88,12 @@ class SamplerConfig:
                 setattr(c, name, v)
                 setattr(c, name + "_rows", None)
         c.greedy = int(bool(self.greedy))
+        k = self.top_k
+        if isinstance(k, torch.Tensor):
+            every = self.top_k_every_row
+            if not every and k.device.type == "cpu" and k.numel() > 0:
+                every = bool((k > 0).all()) and (V is None or bool((k < V).all()))
+            c.top_k = 1 if every else 0                  # the statement (header: top_k)
         return c, keep
 
 
@@ -285,7 +297,7 @@ def sample(logits: torch.Tensor, uniforms: torch.Tensor, config: SamplerConfig,
         if tuple(bitmask.shape) != (B, nw):
             raise ValueError(f"bitmask must be [{B}, {nw}]")
     _on_gpu(x, u, history, history_len, bitmask)
-    cfg, keep_alive = config.to_c(B, dev)
+    cfg, keep_alive = config.to_c(B, dev, V)
     ids = torch.empty(B, dtype=torch.int32, device=dev)
     probs = torch.empty(B, dtype=torch.float32, device=dev)
     keep = torch.empty((B, nw), dtype=torch.int32, device=dev) if return_keep else None

@@ -233,6 +233,20 @@ def test_sampler_config_rows_to_c():
         cfg.to_c(3, torch.device("cpu"))
 
 
+def test_sampler_config_top_k_statement():
+    """Per-row top_k from host memory: the scalar states whether every row has
+    top-k in (0, V) (1) or makes no statement (0); a device tensor needs the
+    caller's word (top_k_every_row)."""
+    import torch
+    from llima_amd import SamplerConfig
+    dev = torch.device("cpu")
+    assert SamplerConfig(top_k=torch.tensor([5, 50])).to_c(2, dev, 100)[0].top_k == 1
+    assert SamplerConfig(top_k=torch.tensor([5, 0])).to_c(2, dev, 100)[0].top_k == 0
+    assert SamplerConfig(top_k=torch.tensor([5, 100])).to_c(2, dev, 100)[0].top_k == 0
+    assert SamplerConfig(top_k=torch.tensor([0, 0]), top_k_every_row=True).to_c(2, dev, 100)[0].top_k == 1
+    assert SamplerConfig(top_k=7).to_c(2, dev, 100)[0].top_k == 7
+
+
 def test_python_api_rejects_host_tensors():
     import torch
     import llima_amd

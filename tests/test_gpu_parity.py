@@ -102,7 +102,8 @@ def _sample_both(gpu, oracle, logits, u, cfgd, history=None, hist_len=None, mask
         gcfg = llima_amd.SamplerConfig(**{k: (torch.tensor(v) if isinstance(v, list) else v)
                                           for k, v in cfg_rows.items()})
         B = logits.shape[0]
-        ocfg = [OC(**{k: (v[b] if isinstance(v, list) else v) for k, v in cfg_rows.items()})
+        ocfg = [OC(**{k: (v[b] if isinstance(v, list) else v) for k, v in cfg_rows.items()
+                      if k != "top_k_every_row"})     # a launch hint, not a setting
                 for b in range(B)]
     # without the kept-set output the batch may take other paths (rows split
     # over several finish workgroups need none)
@@ -570,6 +571,10 @@ def test_sample_split_rows(gpu, oracle, dtype):
     # the same rows again with other uniforms (other draw chunks)
     _sample_both(gpu, oracle, xx, rng.random(B).astype(np.float32), None, history=hist,
                  cfg_rows=rows, want_keep=False)
+    # a wrong statement that every row has top-k: the rows without take the
+    # full-row path, and the tokens stay the same
+    _sample_both(gpu, oracle, xx, u, None, history=hist, cfg_rows=dict(rows, top_k_every_row=True),
+                 want_keep=False)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
