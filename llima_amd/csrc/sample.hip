@@ -1068,7 +1068,8 @@ __device__ __forceinline__ void fr_transform(const SampleParams& P, const RowCfg
 // Streams steps [s_begin, s_end) of a row through fn(x, i0): x[e] is the value
 // of id i0 + e after the row's transform (NaN -> -inf, mask, penalties, / T
 // unless greedy; -inf past the row), a whole step's values at once so that
-// fn can work on them without a branch per value: step s
+// fn can work on them without a branch per value; step_end(s, x, i0) after
+// it, with the same values: step s
 // covers the FrGeom::STEP ids from step_base(s) (a multiple of FrGeom::FE),
 // thread t taking FE consecutive ids (within one mask word).  The loads of step
 // s + NB - 1 are requested before step s is worked on, so NB steps (64 KB of
@@ -1115,7 +1116,7 @@ __device__ __forceinline__ void fr_stream(const SampleParams& P, int row, const 
         float x[FG::FE];
         fr_transform<TL, PEN>(P, c, qq, m, mrow, i0, lo, table, x);
         fn(x, i0);                                            // ids past the row: -inf
-        step_end(s);
+        step_end(s, x, i0);
     };
     // the scheduling barriers keep the loads in step order (waiting for one
     // step's data then waits for no later step's)
@@ -1750,7 +1751,7 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
             }
         }
     };
-    fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, 0, (int)nlist * SPC, listed, member, [](int) {});
+    fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, 0, (int)nlist * SPC, listed, member, [](int, const auto&, int) {});
     if (sh.lcount != nm) {                                   // uniform: never (the counts are the bins')
         finish_full_row<TL>(P, row, c, sh);
         return;
@@ -1896,6 +1897,73 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     FIN_MARK(5);
     uint32_t bmf = SMP_DBINS;                                // this thread's first bin below min-p
     uint32_t bmf_part = SMP_DBINS;                           // the part's (uniform)
+    // staged values gather in LDS (a global store inside a pass would make
+    // every step wait for all loads), then go to the regions
+    static_assert(SMP_RCPW * SMP_RSTG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv), "staging in LDS");
+    uint64_t* stg = (uint64_t*)&sh.sv[0];                    // [SMP_RCPW][SMP_RSTG_CAP]
+    if (t < (uint32_t)SMP_RCPW) {
+        sh.ccount[t] = 1u;                                   // windows: empty (lo 1, hi 0)
+        sh.coff[t] = 0;
+    }
+    // the part's own mass and count per bin pair (2t, 2t + 1), so far
+    uint64_t pm0 = 0, pm1 = 0;
+    uint32_t pn0 = 0, pn1 = 0;
+    // the boundary bin of the part's chunks so far (top-p and min-p over the
+    // part's own masses): an estimate of the row's
+    auto estimate = [&]() -> uint32_t {
+        uint64_t Zp;
+        const uint64_t ab = block_excl_scan_u64(pm0 + pm1, &Zp, sh.bs);
+        uint32_t bhat = SMP_DBINS;
+        if (c.p < 1.0f) {                                    // uniform
+            const llima_u128 PZ = (llima_u128)frac32(c.p) * Zp;
+            const bool q0 = pn0 > 0u && (((llima_u128)ab << 32) < PZ);
+            const bool q1 = pn1 > 0u && (((llima_u128)(ab + pm0) << 32) < PZ);
+            const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
+            const uint32_t ne = pn0 ? 2u * t : (pn1 ? 2u * t + 1u : 0xFFFFFFFFu);
+            const uint32_t top = ~block_max_u32(~ne, sh.bs);
+            bhat = qb ? qb - 1u : (top < SMP_DBINS ? top : SMP_DBINS);
+        }
+        return bhat < bmf_part ? bhat : bmf_part;
+    };
+    // chunk cl's window (by the wave `wave`): lane d counts bins bbh - d and
+    // bbh + d; the widest window whose values fit the staging
+    auto window = [&](int cl, uint32_t bbh) {
+        const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
+        const int lo_b = (int)bbh - (int)lane, hi_b = (int)bbh + (int)lane;
+        uint32_t cnt = hi_b < SMP_DBINS ? (uint32_t)(bins[hi_b] & 0x3FFFu) : 0u;
+        cnt += lane > 0 && lo_b >= 0 ? (uint32_t)(bins[lo_b] & 0x3FFFu) : 0u;
+        const uint32_t inc = wave_incl_scan_u32(cnt);
+        const uint64_t fits = ballot(inc <= SMP_RSTG_CAP);   // a prefix of the lanes
+        const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest half-width
+        if (lane == 0) {
+            const uint32_t lo = w < 0 ? 1u : (uint32_t)((int)bbh - w > 0 ? (int)bbh - w : 0);
+            const uint32_t hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
+            sh.ccount[cl] = lo | (hi << 16);
+        }
+    };
+    // one step's values of chunk cl inside window wc to the chunk's staging:
+    // a bit mask per thread, one LDS atomic per wave for their places
+    auto stage_step = [&](const float (&x)[FG::FE], int i0, uint32_t cl, uint32_t wc) {
+        uint32_t hm = 0;
+#pragma unroll
+        for (int e = 0; e < FG::FE; ++e) {
+            const uint32_t b = (uint32_t)dense_d16(x[e], xmax);
+            hm |= x[e] > -__builtin_inff() && b >= (wc & 0xFFFFu) && b <= (wc >> 16) ? 1u << e : 0u;
+        }
+        const uint32_t n = (uint32_t)__popc(hm);
+        if (ballot(n != 0u)) {                               // uniform in the wave
+            const uint32_t inc = wave_incl_scan_u32(n);
+            uint32_t base = 0;
+            if (lane == 63) base = atomicAdd(&sh.coff[cl], inc);
+            uint32_t o = readlane(base, 63) + inc - n;
+            while (hm) {
+                const int e = __builtin_ctz(hm);
+                hm &= hm - 1u;
+                if (o < SMP_RSTG_CAP) stg[cl * SMP_RSTG_CAP + o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
+                ++o;
+            }
+        }
+    };
     auto bin = [&](const float (&x)[FG::FE], int i0) {
         // every weight first (independent chains), then the LDS atomics, -inf
         // values into the lane's spare bin: no branch per value
@@ -1914,10 +1982,11 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
 #pragma unroll
         for (int e = 0; e < FG::FE; ++e) atomicAdd((unsigned long long*)&cb[slot[e]], (unsigned long long)add[e]);
     };
-    auto chunk_end = [&](int s) {
+    auto chunk_end = [&](int s, const float (&x)[FG::FE], int i0) {
         if (s % SPC != SPC - 1) return;                      // uniform: not the chunk's last step
+        const int cl = s / SPC - ch0;
         const uint32_t bm = ~block_max_u32(~bmf, sh.bs);     // its barriers complete the bins
-        const uint64_t* bins = cb + (size_t)(s / SPC - ch0) * SMP_DBINS;
+        const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
         const bool mine = t < SMP_DBINS / 2;
         const uint64_t h0 = mine ? bins[2u * t] : 0ull, h1 = mine ? bins[2u * t + 1u] : 0ull;
         uint64_t tot;
@@ -1933,94 +2002,45 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
         }
         bmf_part = bm < bmf_part ? bm : bmf_part;
         bmf = SMP_DBINS;
+        pm0 += h0 >> 14;
+        pm1 += h1 >> 14;
+        pn0 += (uint32_t)(h0 & 0x3FFFu);
+        pn1 += (uint32_t)(h1 & 0x3FFFu);
+        if constexpr (SPC == 1) {
+            // the chunk's values are this step's, still in registers: its
+            // window from the part's estimate so far, and the staging now
+            const uint32_t bbh = estimate();
+            if (bbh < SMP_DBINS) {                           // uniform
+                if (wave == 0) window(cl, bbh);
+                __syncthreads();
+                stage_step(x, i0, (uint32_t)cl, sh.ccount[cl]);
+            }
+        }
     };
     auto by_step = [](int s) { return s * FG::STEP; };
     fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, ch0 * SPC, ch1 * SPC, by_step, bin, chunk_end);
     FIN_MARK(6);
-    // ---- the boundary bin of the part's own chunks (the row's, estimated)
-    uint64_t m0 = 0, m1 = 0;
-    uint32_t n0 = 0, n1 = 0;
-    if (t < SMP_DBINS / 2) {
-        for (int cl = 0; cl < nch; ++cl) {
-            const uint64_t h0 = cb[cl * SMP_DBINS + 2 * (int)t], h1 = cb[cl * SMP_DBINS + 2 * (int)t + 1];
-            m0 += h0 >> 14;
-            n0 += (uint32_t)(h0 & 0x3FFFu);
-            m1 += h1 >> 14;
-            n1 += (uint32_t)(h1 & 0x3FFFu);
+    if constexpr (SPC != 1) {
+        // chunks of two steps: the estimate from all of the part's chunks,
+        // each chunk's window, and a second read of the chunks for the staging
+        const uint32_t bbh = estimate();
+        FIN_MARK(13);
+        if (bbh < SMP_DBINS) {                               // uniform
+            if ((int)wave < nch) window((int)wave, bbh);
+            __syncthreads();
+            uint32_t win[SMP_RCPW];
+#pragma unroll
+            for (int cl = 0; cl < SMP_RCPW; ++cl) win[cl] = cl < nch ? sh.ccount[cl] : 1u;
+            auto stage = [&](const float (&x)[FG::FE], int i0) {
+                const uint32_t cl = (uint32_t)(i0 / CV - ch0);   // the step lies in one chunk
+                uint32_t wc = win[0];
+#pragma unroll
+                for (int k = 1; k < SMP_RCPW; ++k) wc = cl == (uint32_t)k ? win[k] : wc;
+                stage_step(x, i0, cl, wc);
+            };
+            fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, ch0 * SPC, ch1 * SPC, by_step, stage,
+                                      [](int, const auto&, int) {});
         }
-    }
-    uint64_t Zp;
-    const uint64_t ab = block_excl_scan_u64(m0 + m1, &Zp, sh.bs);
-    uint32_t bhat = SMP_DBINS;
-    if (c.p < 1.0f) {                                        // uniform
-        const llima_u128 PZ = (llima_u128)frac32(c.p) * Zp;
-        const bool q0 = n0 > 0u && (((llima_u128)ab << 32) < PZ);
-        const bool q1 = n1 > 0u && (((llima_u128)(ab + m0) << 32) < PZ);
-        const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
-        const uint32_t ne = n0 ? 2u * t : (n1 ? 2u * t + 1u : 0xFFFFFFFFu);
-        const uint32_t top = ~block_max_u32(~ne, sh.bs);
-        bhat = qb ? qb - 1u : (top < SMP_DBINS ? top : SMP_DBINS);
-    }
-    const uint32_t bbh = bhat < bmf_part ? bhat : bmf_part;
-    FIN_MARK(13);
-    // ---- each chunk's window: wave cl, lane d: bins bbh - d and bbh + d; the
-    //      widest window whose values fit the staging
-    if (bbh < SMP_DBINS && (int)wave < nch) {
-        const uint64_t* bins = cb + (size_t)wave * SMP_DBINS;
-        const int lo_b = (int)bbh - (int)lane, hi_b = (int)bbh + (int)lane;
-        uint32_t cnt = hi_b < SMP_DBINS ? (uint32_t)(bins[hi_b] & 0x3FFFu) : 0u;
-        cnt += lane > 0 && lo_b >= 0 ? (uint32_t)(bins[lo_b] & 0x3FFFu) : 0u;
-        const uint32_t inc = wave_incl_scan_u32(cnt);
-        const uint64_t fits = ballot(inc <= SMP_RSTG_CAP);   // a prefix of the lanes
-        const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest half-width
-        if (lane == 0) {
-            const uint32_t lo = w < 0 ? 1u : (uint32_t)((int)bbh - w > 0 ? (int)bbh - w : 0);
-            const uint32_t hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
-            sh.ccount[wave] = lo | (hi << 16);
-            sh.coff[wave] = 0;
-        }
-    } else if ((int)wave < nch && lane == 0) {
-        sh.ccount[wave] = 1u;                                // empty: lo 1, hi 0
-        sh.coff[wave] = 0;
-    }
-    __syncthreads();
-    uint32_t win[SMP_RCPW];
-#pragma unroll
-    for (int cl = 0; cl < SMP_RCPW; ++cl) win[cl] = cl < nch ? sh.ccount[cl] : 1u;
-    // staged values gather in LDS during the pass (a global store in it
-    // would make every step wait for all loads), then go to the regions
-    static_assert(SMP_RCPW * SMP_RSTG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv), "staging in LDS");
-    uint64_t* stg = (uint64_t*)&sh.sv[0];                    // [SMP_RCPW][SMP_RSTG_CAP]
-    if (bbh < SMP_DBINS) {                                   // uniform
-        // ---- the chunks again: each window's values to the chunk's staging
-        auto stage = [&](const float (&x)[FG::FE], int i0) {
-            // the step's window values: a bit mask per thread, one LDS atomic
-            // per wave for their places (the step lies in one chunk)
-            const uint32_t cl = (uint32_t)(i0 / CV - ch0);
-            uint32_t wc = win[0];
-#pragma unroll
-            for (int k = 1; k < SMP_RCPW; ++k) wc = cl == (uint32_t)k ? win[k] : wc;
-            uint32_t hm = 0;
-#pragma unroll
-            for (int e = 0; e < FG::FE; ++e) {
-                const uint32_t b = (uint32_t)dense_d16(x[e], xmax);
-                hm |= x[e] > -__builtin_inff() && b >= (wc & 0xFFFFu) && b <= (wc >> 16) ? 1u << e : 0u;
-            }
-            const uint32_t n = (uint32_t)__popc(hm);
-            if (ballot(n != 0u)) {                           // uniform in the wave
-                const uint32_t inc = wave_incl_scan_u32(n);
-                uint32_t base = 0;
-                if (lane == 63) base = atomicAdd(&sh.coff[cl], inc);
-                uint32_t o = readlane(base, 63) + inc - n;
-                while (hm) {
-                    const int e = __builtin_ctz(hm);
-                    hm &= hm - 1u;
-                    if (o < SMP_RSTG_CAP) stg[cl * SMP_RSTG_CAP + o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
-                    ++o;
-                }
-            }
-        };
-        fr_stream_row<TL, FG::NB>(P, row, c, sh.u.table, ch0 * SPC, ch1 * SPC, by_step, stage, [](int) {});
     }
     FIN_MARK(14);
     for (int cl = (int)wave; cl < nch; cl += LLIMA_WAVES) {
