@@ -65,6 +65,7 @@ namespace llima {
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
 #define SMP_RCNT 16                                // split-row arrival counter stride (u32: 64 bytes)
+#define SMP_XSTG 64                                // split-row staging slots per chunk beyond its region
 #define SMP_PBINS 256                              // top-p value bins: floor(8 (xmax - x)), the last open
 #define SMP_PBIN_SCALE 8.0f
 #define SMP_PBIN_SLOTS (SMP_PBINS + 64)            // + a spare bin per lane
@@ -123,6 +124,7 @@ struct SampleParams {
     int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
     int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
     int32_t fsplit;      // sample_finish workgroups per row (> 1: rows without top-k may be split)
+    uint64_t* xstg;      // [B][S][SMP_XSTG] split-row staging beyond the regions
     uint32_t* rcnt;      // [B][SMP_RCNT] split-row arrival counters, zeroed by the sweep
 };
 
@@ -1591,17 +1593,31 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 //   SMP_RCUM + SMP_DBINS         the chunk's mass << 14
 //   SMP_RBMF                     the chunk's first bin with a value below min-p
 //   SMP_RSTGI, SMP_RSTG          staged values: every value of the chunk in bins
-//                                [lo, hi], a window around the boundary bin of
-//                                the part's own chunks (at most SMP_RSTG_CAP);
-//                                the last part reads a chunk again only when
-//                                the row's boundary bin lies outside it
+//                                [lo, hi] (at most SMP_STG_CAP: the first
+//                                SMP_RSTG_CAP here, the rest in the chunk's
+//                                SMP_XSTG slots after the regions); the last
+//                                part reads a chunk again only when the row's
+//                                boundary bin lies outside the window
+// The window: the part's own chunks (those binned so far, for fp32) give an
+// estimate bh of the row's boundary bin.  The row's mass is dominated by its
+// highest values, so bh misses both ways; when the chunk's highest bins
+// [0, hi] that fit the staging reach bh, they are the window, else the widest
+// [bh - 4w, bh + w] that fits (the miss is more often upward).
 #define SMP_RCUM 1
 #define SMP_RBMF (SMP_RCUM + SMP_DBINS + 1)
 #define SMP_RSTGI (SMP_RBMF + 1)                   // staged bins lo | hi << 16 | count << 32
 #define SMP_RSTG (SMP_RSTGI + 1)                   // staged values (key << 32 | id)
 #define SMP_RSTG_CAP (SMP_REGION - SMP_RSTG)       // 60
+#define SMP_STG_CAP (SMP_RSTG_CAP + SMP_XSTG)      // 124
 #define SMP_RCPW 4                                 // chunks per part
 static_assert(SMP_RBMF < SMP_REGION, "split-row region layout");
+static_assert(SMP_STG_CAP <= 128, "a wave reads a chunk's staging in two loads per lane");
+
+// Staged value j of a chunk: in its region, then beyond the regions.
+__device__ __forceinline__ uint64_t* stg_slot(const SampleParams& P, uint32_t row, uint32_t chunk, uint32_t j) {
+    return j < SMP_RSTG_CAP ? region_of(P, row, chunk) + SMP_RSTG + j
+                            : P.xstg + ((size_t)row * (uint32_t)P.S + chunk) * SMP_XSTG + (j - SMP_RSTG_CAP);
+}
 
 // Whether the row is split (every part of it decides alike, from the sweep's
 // headers): no top-k, not greedy, a finite T, a region that overflowed or
@@ -1722,13 +1738,16 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
     const uint32_t lane = lane_id();
     for (uint32_t k = wave_id(); k < nstg; k += LLIMA_WAVES) {
         const uint32_t e = sh.coff[k];
-        uint64_t* st = r0 + (size_t)(e & 0xFFFFu) * SMP_REGION + SMP_RSTG;
-        const bool in = lane < (e >> 16);
-        const uint64_t v = in ? load_agent(st + lane) : 0ull;
-        const uint32_t key = (uint32_t)(v >> 32);
-        if (in && (uint32_t)dense_d16(key_f32(key), xmax) == bb) {
-            const uint32_t o = atomicAdd(&sh.lcount, 1u);
-            if (o < SMP_FRMCAP) mem[o] = v;
+        const uint32_t ch = e & 0xFFFFu, n = e >> 16;
+        const bool in0 = lane < n, in1 = lane + 64u < n;
+        const uint64_t v0 = in0 ? load_agent(stg_slot(P, (uint32_t)row, ch, lane)) : 0ull;
+        const uint64_t v1 = in1 ? load_agent(stg_slot(P, (uint32_t)row, ch, lane + 64u)) : 0ull;
+        const bool m0 = in0 && (uint32_t)dense_d16(key_f32((uint32_t)(v0 >> 32)), xmax) == bb;
+        const bool m1 = in1 && (uint32_t)dense_d16(key_f32((uint32_t)(v1 >> 32)), xmax) == bb;
+        if (m0 || m1) {
+            const uint32_t o = atomicAdd(&sh.lcount, (m0 ? 1u : 0u) + (m1 ? 1u : 0u));
+            if (m0 && o < SMP_FRMCAP) mem[o] = v0;
+            if (m1 && o + (m0 ? 1u : 0u) < SMP_FRMCAP) mem[o + (m0 ? 1u : 0u)] = v1;
         }
     }
     auto listed = [&](int s) { return (int)sh.ccount[s / SPC] * CV + (s % SPC) * FG::STEP; };
@@ -1899,8 +1918,8 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     uint32_t bmf_part = SMP_DBINS;                           // the part's (uniform)
     // staged values gather in LDS (a global store inside a pass would make
     // every step wait for all loads), then go to the regions
-    static_assert(SMP_RCPW * SMP_RSTG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv), "staging in LDS");
-    uint64_t* stg = (uint64_t*)&sh.sv[0];                    // [SMP_RCPW][SMP_RSTG_CAP]
+    static_assert(SMP_RCPW * SMP_STG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv2), "staging in LDS");
+    uint64_t* stg = (uint64_t*)&sh.sv2[0][0];                // [SMP_RCPW][SMP_STG_CAP]
     if (t < (uint32_t)SMP_RCPW) {
         sh.ccount[t] = 1u;                                   // windows: empty (lo 1, hi 0)
         sh.coff[t] = 0;
@@ -1925,21 +1944,54 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
         }
         return bhat < bmf_part ? bhat : bmf_part;
     };
-    // chunk cl's window (by the wave `wave`): lane d counts bins bbh - d and
-    // bbh + d; the widest window whose values fit the staging
+    // chunk cl's window (by the wave `wave`), for the estimate bbh
     auto window = [&](int cl, uint32_t bbh) {
+        static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
+        constexpr int BPL = SMP_DBINS / 64;
         const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
-        const int lo_b = (int)bbh - (int)lane, hi_b = (int)bbh + (int)lane;
-        uint32_t cnt = hi_b < SMP_DBINS ? (uint32_t)(bins[hi_b] & 0x3FFFu) : 0u;
-        cnt += lane > 0 && lo_b >= 0 ? (uint32_t)(bins[lo_b] & 0x3FFFu) : 0u;
-        const uint32_t inc = wave_incl_scan_u32(cnt);
-        const uint64_t fits = ballot(inc <= SMP_RSTG_CAP);   // a prefix of the lanes
-        const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest half-width
-        if (lane == 0) {
-            const uint32_t lo = w < 0 ? 1u : (uint32_t)((int)bbh - w > 0 ? (int)bbh - w : 0);
-            const uint32_t hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
-            sh.ccount[cl] = lo | (hi << 16);
+        // the highest bins: lane d holds bins [BPL d, BPL d + BPL); the
+        // deepest bin hi_top with bins [0, hi_top] fitting (-1: none)
+        uint32_t bc[BPL], lsum = 0;
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            bc[i] = (uint32_t)(bins[BPL * lane + i] & 0x3FFFu);
+            lsum += bc[i];
         }
+        const uint32_t cum = wave_incl_scan_u32(lsum);
+        const uint64_t full = ballot(cum <= SMP_STG_CAP);    // a prefix of the lanes
+        const int j = __builtin_popcountll(full);            // the first lane that does not fit
+        int hi_top = SMP_DBINS - 1;
+        if (j < 64) {                                        // uniform
+            uint32_t run = cum - lsum, nf = 0;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+                run += bc[i];
+                nf += run <= SMP_STG_CAP && nf == (uint32_t)i ? 1u : 0u;
+            }
+            hi_top = BPL * j + (int)readlane(nf, (uint32_t)j) - 1;
+        }
+        uint32_t lo, hi;
+        if (hi_top >= (int)bbh) {                            // uniform
+            lo = 0;
+            hi = (uint32_t)hi_top;
+        } else {
+            // lane w adds bins [bbh - 4w, bbh - 4w + 3] and bbh + w: window
+            // w is [bbh - 4w, bbh + w]
+            const int b0 = (int)bbh - 4 * (int)lane, bu = (int)bbh + (int)lane;
+            uint32_t cnt = 0;
+            if (lane == 0) cnt = (uint32_t)(bins[bbh] & 0x3FFFu);
+            else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) cnt += b0 + i >= 0 ? (uint32_t)(bins[b0 + i] & 0x3FFFu) : 0u;
+                cnt += bu < SMP_DBINS ? (uint32_t)(bins[bu] & 0x3FFFu) : 0u;
+            }
+            const uint32_t inc = wave_incl_scan_u32(cnt);
+            const uint64_t fits = ballot(inc <= SMP_STG_CAP);   // a prefix of the lanes
+            const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest window
+            lo = w < 0 ? 1u : (uint32_t)((int)bbh - 4 * w > 0 ? (int)bbh - 4 * w : 0);
+            hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
+        }
+        if (lane == 0) sh.ccount[cl] = lo | (hi << 16);
     };
     // one step's values of chunk cl inside window wc to the chunk's staging:
     // a bit mask per thread, one LDS atomic per wave for their places
@@ -1959,7 +2011,7 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
             while (hm) {
                 const int e = __builtin_ctz(hm);
                 hm &= hm - 1u;
-                if (o < SMP_RSTG_CAP) stg[cl * SMP_RSTG_CAP + o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
+                if (o < SMP_STG_CAP) stg[cl * SMP_STG_CAP + o] = ((uint64_t)f32_key(x[e]) << 32) | (uint32_t)(i0 + e);
                 ++o;
             }
         }
@@ -2044,10 +2096,11 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     }
     FIN_MARK(14);
     for (int cl = (int)wave; cl < nch; cl += LLIMA_WAVES) {
-        const uint32_t n = sh.coff[cl] < SMP_RSTG_CAP ? sh.coff[cl] : SMP_RSTG_CAP;
-        uint64_t* reg = region_of(P, (uint32_t)row, (uint32_t)(ch0 + cl));
-        if (lane < n) store_agent(reg + SMP_RSTG + lane, stg[cl * SMP_RSTG_CAP + lane]);
-        if (lane == 0) store_agent(reg + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
+        const uint32_t n = sh.coff[cl] < SMP_STG_CAP ? sh.coff[cl] : SMP_STG_CAP;
+        const uint32_t ch = (uint32_t)(ch0 + cl);
+        if (lane < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane), stg[cl * SMP_STG_CAP + lane]);
+        if (lane + 64u < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane + 64u), stg[cl * SMP_STG_CAP + lane + 64u]);
+        if (lane == 0) store_agent(region_of(P, (uint32_t)row, ch) + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
     }
     // every store of the part completes before its arrival is counted
     __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
@@ -3997,8 +4050,9 @@ using namespace llima;
 extern "C" size_t llima_sample_workspace_bytes(int32_t B, int32_t V, int32_t dtype) {
     if (B <= 0 || V <= 0 || (dtype != LLIMA_F32 && dtype != LLIMA_BF16)) return 0;
     const size_t S = (size_t)((V + chunk_values(dtype) - 1) / chunk_values(dtype));
-    // the chunk regions, then one split-row arrival counter (64 bytes) per row
-    return (size_t)B * S * SMP_REGION * sizeof(uint64_t) + (size_t)B * SMP_RCNT * sizeof(uint32_t);
+    // the chunk regions, the split-row staging of every chunk, then one
+    // split-row arrival counter (64 bytes) per row
+    return (size_t)B * S * (SMP_REGION + SMP_XSTG) * sizeof(uint64_t) + (size_t)B * SMP_RCNT * sizeof(uint32_t);
 }
 
 #ifdef LLIMA_FINISH_TRACE
@@ -4084,7 +4138,8 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     // row has top-k (a row without then takes the full-row path: slower, not
     // wrong), and the lean finish is launched.
     const bool rows_may_lack_topk = cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V);
-    P.rcnt = (uint32_t*)(P.ws + (size_t)B * P.S * SMP_REGION);
+    P.xstg = P.ws + (size_t)B * P.S * SMP_REGION;
+    P.rcnt = (uint32_t*)(P.xstg + (size_t)B * P.S * SMP_XSTG);
     P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (rows_may_lack_topk || P.wide))
                    ? (P.S + SMP_RCPW - 1) / SMP_RCPW : 1;
     // Rows without top-k (and without a mask) take the dense path: their sweep
@@ -4121,7 +4176,7 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
 // The sampler keeps no state in its workspace between calls (every slot a call
 // reads is written earlier in the same call), so nothing needs clearing; calls
 // that overlap on one GPU share the array and race.
-#define LLIMA_SAMPLE_SCRATCH_BYTES ((size_t)32 << 20)
+#define LLIMA_SAMPLE_SCRATCH_BYTES ((size_t)48 << 20)
 #define LLIMA_SCRATCH_MAX_DEVICES 64
 
 static __device__ __align__(256) uint64_t scratch[LLIMA_SAMPLE_SCRATCH_BYTES / sizeof(uint64_t)];
