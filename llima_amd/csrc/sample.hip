@@ -1888,10 +1888,13 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
     }
 }
 
-// Part `part` of a split row: its chunks' bins (kept in LDS), the staging of
-// each chunk's values around the boundary bin the part's own chunks give (a
-// second read of the chunks, from the cache), then the arrival; the last part
-// finishes the row.
+// Part `part` of a split row: its chunks' bins (kept in LDS); the staging of
+// each chunk's values in a window chosen for the boundary bin that the part's
+// own chunks give (fp32: at each chunk's end, from the chunks binned so far,
+// while the chunk's values are in registers; bf16: after the pass, from all of
+// them, by a second read of the chunks from the cache); the cumulative bins
+// and staging written to the workspace (a wave per chunk), then the arrival;
+// the last part finishes the row.
 template <typename TL>
 __device__ __forceinline__ void split_part(const SampleParams& P, int row, const RowCfg& c, uint32_t kmax,
                                            int part, FinShared& sh) {
@@ -1912,42 +1915,27 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     // [SMP_RCPW][SMP_DBINS] chunk bins, then a spare bin per lane (-inf values)
     uint64_t* cb = (uint64_t*)(sh.u.table + SMP_SEG / 2);
     for (uint32_t i = t; i < (uint32_t)nch * SMP_DBINS; i += LLIMA_WG) cb[i] = 0;
-    __syncthreads();
-    FIN_MARK(5);
-    uint32_t bmf = SMP_DBINS;                                // this thread's first bin below min-p
-    uint32_t bmf_part = SMP_DBINS;                           // the part's (uniform)
     // staged values gather in LDS (a global store inside a pass would make
-    // every step wait for all loads), then go to the regions
+    // every step wait for all loads), then go to the workspace
     static_assert(SMP_RCPW * SMP_STG_CAP * sizeof(uint64_t) <= sizeof(FinShared::sv2), "staging in LDS");
     uint64_t* stg = (uint64_t*)&sh.sv2[0][0];                // [SMP_RCPW][SMP_STG_CAP]
+    uint32_t* bmfc = sh.hcnt[0];                             // per chunk: its first bin below min-p
     if (t < (uint32_t)SMP_RCPW) {
         sh.ccount[t] = 1u;                                   // windows: empty (lo 1, hi 0)
         sh.coff[t] = 0;
+        bmfc[t] = SMP_DBINS;
     }
-    // the part's own mass and count per bin pair (2t, 2t + 1), so far
-    uint64_t pm0 = 0, pm1 = 0;
-    uint32_t pn0 = 0, pn1 = 0;
-    // the boundary bin of the part's chunks so far (top-p and min-p over the
-    // part's own masses): an estimate of the row's
-    auto estimate = [&]() -> uint32_t {
-        uint64_t Zp;
-        const uint64_t ab = block_excl_scan_u64(pm0 + pm1, &Zp, sh.bs);
-        uint32_t bhat = SMP_DBINS;
-        if (c.p < 1.0f) {                                    // uniform
-            const llima_u128 PZ = (llima_u128)frac32(c.p) * Zp;
-            const bool q0 = pn0 > 0u && (((llima_u128)ab << 32) < PZ);
-            const bool q1 = pn1 > 0u && (((llima_u128)(ab + pm0) << 32) < PZ);
-            const uint32_t qb = block_max_u32(q1 ? 2u * t + 2u : (q0 ? 2u * t + 1u : 0u), sh.bs);
-            const uint32_t ne = pn0 ? 2u * t : (pn1 ? 2u * t + 1u : 0xFFFFFFFFu);
-            const uint32_t top = ~block_max_u32(~ne, sh.bs);
-            bhat = qb ? qb - 1u : (top < SMP_DBINS ? top : SMP_DBINS);
-        }
-        return bhat < bmf_part ? bhat : bmf_part;
-    };
-    // chunk cl's window (by the wave `wave`), for the estimate bbh
+    __syncthreads();
+    FIN_MARK(5);
+    uint32_t bmf = SMP_DBINS;                                // this thread's, in the current chunk
+    static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
+    constexpr int BPL = SMP_DBINS / 64;                      // bins per lane
+    // chunk cl's window (by one wave) for the estimate bbh
     auto window = [&](int cl, uint32_t bbh) {
-        static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
-        constexpr int BPL = SMP_DBINS / 64;
+        if (bbh >= SMP_DBINS) {                              // uniform: no estimate, nothing staged
+            if (lane == 0) sh.ccount[cl] = 1u;
+            return;
+        }
         const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
         // the highest bins: lane d holds bins [BPL d, BPL d + BPL); the
         // deepest bin hi_top with bins [0, hi_top] fitting (-1: none)
@@ -1993,6 +1981,50 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
         }
         if (lane == 0) sh.ccount[cl] = lo | (hi << 16);
     };
+    // by one wave: the boundary bin of the part's chunks [0, ne) (top-p and
+    // min-p over their own masses), an estimate of the row's, and chunk cl's
+    // window for it
+    auto plan = [&](int cl, int ne) {
+        uint64_t m[BPL];
+        uint32_t n[BPL];
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            m[i] = 0;
+            n[i] = 0;
+        }
+        uint32_t bbh = SMP_DBINS;
+        for (int k = 0; k < ne; ++k) {
+            const uint64_t* bins = cb + (size_t)k * SMP_DBINS + BPL * lane;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+                const uint64_t v = bins[i];
+                m[i] += v >> 14;
+                n[i] += (uint32_t)(v & 0x3FFFu);
+            }
+            bbh = bmfc[k] < bbh ? bmfc[k] : bbh;
+        }
+        if (c.p < 1.0f) {                                    // uniform
+            uint64_t lm = 0;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) lm += m[i];
+            const uint64_t incl = wave_incl_scan_u64(lm);
+            const llima_u128 PZ = (llima_u128)frac32(c.p) * readlane63(incl);
+            uint64_t above = incl - lm;
+            uint32_t qb = 0, top = 0xFFFFFFFFu;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+                const uint32_t b = BPL * lane + (uint32_t)i;
+                qb = n[i] > 0u && ((llima_u128)above << 32) < PZ ? b + 1u : qb;
+                top = n[i] > 0u && top == 0xFFFFFFFFu ? b : top;
+                above += m[i];
+            }
+            qb = wave_max_u32(qb);
+            top = wave_min_u32(top);
+            const uint32_t bhat = qb ? qb - 1u : (top < SMP_DBINS ? top : SMP_DBINS);
+            bbh = bhat < bbh ? bhat : bbh;
+        }
+        window(cl, bbh);
+    };
     // one step's values of chunk cl inside window wc to the chunk's staging:
     // a bit mask per thread, one LDS atomic per wave for their places
     auto stage_step = [&](const float (&x)[FG::FE], int i0, uint32_t cl, uint32_t wc) {
@@ -2037,36 +2069,17 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     auto chunk_end = [&](int s, const float (&x)[FG::FE], int i0) {
         if (s % SPC != SPC - 1) return;                      // uniform: not the chunk's last step
         const int cl = s / SPC - ch0;
-        const uint32_t bm = ~block_max_u32(~bmf, sh.bs);     // its barriers complete the bins
-        const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
-        const bool mine = t < SMP_DBINS / 2;
-        const uint64_t h0 = mine ? bins[2u * t] : 0ull, h1 = mine ? bins[2u * t + 1u] : 0ull;
-        uint64_t tot;
-        const uint64_t ab = block_excl_scan_u64((h0 >> 14) + (h1 >> 14), &tot, sh.bs);
-        uint64_t* reg = region_of(P, (uint32_t)row, (uint32_t)(s / SPC));
-        if (mine) {
-            store_agent(reg + SMP_RCUM + 2u * t, (ab << 14) | (h0 & 0x3FFFu));
-            store_agent(reg + SMP_RCUM + 2u * t + 1u, ((ab + (h0 >> 14)) << 14) | (h1 & 0x3FFFu));
-        }
-        if (t == 0) {
-            store_agent(reg + SMP_RCUM + SMP_DBINS, tot << 14);
-            store_agent(reg + SMP_RBMF, bm);
-        }
-        bmf_part = bm < bmf_part ? bm : bmf_part;
+        const uint32_t wbm = wave_min_u32(bmf);
+        if (lane == 0) atomicMin(&bmfc[cl], wbm);
         bmf = SMP_DBINS;
-        pm0 += h0 >> 14;
-        pm1 += h1 >> 14;
-        pn0 += (uint32_t)(h0 & 0x3FFFu);
-        pn1 += (uint32_t)(h1 & 0x3FFFu);
         if constexpr (SPC == 1) {
             // the chunk's values are this step's, still in registers: its
-            // window from the part's estimate so far, and the staging now
-            const uint32_t bbh = estimate();
-            if (bbh < SMP_DBINS) {                           // uniform
-                if (wave == 0) window(cl, bbh);
-                __syncthreads();
-                stage_step(x, i0, (uint32_t)cl, sh.ccount[cl]);
-            }
+            // window from the part's chunks binned so far, and the staging now
+            __syncthreads();                                 // the chunk's bins are complete
+            if (wave == 0) plan(cl, cl + 1);
+            __syncthreads();
+            const uint32_t wc = sh.ccount[cl];
+            if ((wc & 0xFFFFu) <= (wc >> 16)) stage_step(x, i0, (uint32_t)cl, wc);   // uniform
         }
     };
     auto by_step = [](int s) { return s * FG::STEP; };
@@ -2075,14 +2088,17 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
     if constexpr (SPC != 1) {
         // chunks of two steps: the estimate from all of the part's chunks,
         // each chunk's window, and a second read of the chunks for the staging
-        const uint32_t bbh = estimate();
-        FIN_MARK(13);
-        if (bbh < SMP_DBINS) {                               // uniform
-            if ((int)wave < nch) window((int)wave, bbh);
-            __syncthreads();
-            uint32_t win[SMP_RCPW];
+        if ((int)wave < nch) plan((int)wave, nch);
+        __syncthreads();
+        uint32_t win[SMP_RCPW];
+        bool any = false;
 #pragma unroll
-            for (int cl = 0; cl < SMP_RCPW; ++cl) win[cl] = cl < nch ? sh.ccount[cl] : 1u;
+        for (int cl = 0; cl < SMP_RCPW; ++cl) {
+            win[cl] = cl < nch ? sh.ccount[cl] : 1u;
+            any = any || (win[cl] & 0xFFFFu) <= (win[cl] >> 16);
+        }
+        FIN_MARK(13);
+        if (any) {                                           // uniform
             auto stage = [&](const float (&x)[FG::FE], int i0) {
                 const uint32_t cl = (uint32_t)(i0 / CV - ch0);   // the step lies in one chunk
                 uint32_t wc = win[0];
@@ -2095,12 +2111,29 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
         }
     }
     FIN_MARK(14);
+    // each chunk's cumulative bins, first bin below min-p and staging to the
+    // workspace, a wave per chunk
     for (int cl = (int)wave; cl < nch; cl += LLIMA_WAVES) {
-        const uint32_t n = sh.coff[cl] < SMP_STG_CAP ? sh.coff[cl] : SMP_STG_CAP;
         const uint32_t ch = (uint32_t)(ch0 + cl);
+        uint64_t* reg = region_of(P, (uint32_t)row, ch);
+        const uint64_t* bins = cb + (size_t)cl * SMP_DBINS;
+        uint64_t above = 0;                                  // the chunk's mass above bin 64 i
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const uint64_t v = bins[64 * i + lane];
+            const uint64_t mv = v >> 14;
+            const uint64_t inc = wave_incl_scan_u64(mv);
+            store_agent(reg + SMP_RCUM + 64 * i + lane, ((above + inc - mv) << 14) | (v & 0x3FFFu));
+            above += readlane63(inc);
+        }
+        if (lane == 0) {
+            store_agent(reg + SMP_RCUM + SMP_DBINS, above << 14);
+            store_agent(reg + SMP_RBMF, (uint64_t)bmfc[cl]);
+        }
+        const uint32_t n = sh.coff[cl] < SMP_STG_CAP ? sh.coff[cl] : SMP_STG_CAP;
         if (lane < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane), stg[cl * SMP_STG_CAP + lane]);
         if (lane + 64u < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane + 64u), stg[cl * SMP_STG_CAP + lane + 64u]);
-        if (lane == 0) store_agent(region_of(P, (uint32_t)row, ch) + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
+        if (lane == 0) store_agent(reg + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
     }
     // every store of the part completes before its arrival is counted
     __builtin_amdgcn_s_waitcnt(LLIMA_WAITCNT_VM0);
