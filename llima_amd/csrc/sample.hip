@@ -3402,6 +3402,10 @@ __global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
 //   region c, SMP_DSTAT / SMP_DBEST  dense_stats's results for chunk c
 //   region c, SMP_DKEPT             the kept mass of chunk c (dense_bound or dense_keep)
 //   region c, SMP_DMCNT             dense_bound: chunk c's count in the boundary bin
+//   region c, SMP_DSWIN             dense_hist: the chunk's highest bins [0, hi]
+//                                   holding at most SMP_XSTG values, staged in
+//                                   the chunk's SMP_XSTG slots after the regions
+//                                   (hi + 1, 0 for none | the count << 32)
 //   region 0, SMP_DINFO..+2         dense_bound's boundary bin, mass above it, Z
 //   region 0, SMP_DMEM              members appended (a 128-byte line of its
 //                                   own), zeroed by dense_stats
@@ -3409,6 +3413,7 @@ __global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
 #define SMP_DBEST 449                              // greedy: key << 32 | ~id of the chunk maximum
 #define SMP_DKEPT 450                              // kept mass strictly above the boundary bin
 #define SMP_DMCNT 451                              // the chunk's members of the boundary bin
+#define SMP_DSWIN 452                              // the chunk's staged top window
 #define SMP_DINFO 456                              // region 0: boundary bin, mass above it, Z
 #define SMP_DMEM 496                               // region 0: boundary members appended
 #define SMP_DMCAP 4096                             // members dense_final ranks (16 per thread)
@@ -3720,6 +3725,9 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ uint64_t hist[SMP_DBINS + 64];           // + a spare bin per lane
+    __shared__ uint64_t swin[SMP_XSTG];                 // the staged top window
+    __shared__ int32_t swin_hi;
+    __shared__ uint32_t swin_n;
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
@@ -3741,11 +3749,13 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
     dense_unpack<TL>(P, c, c0, raw, table, x);
     dense_div(x, c);
     const float xmax = key_f32(kmax);
+    uint32_t bin[G::E];                                 // kept for the staging (fp32)
 #pragma unroll
     for (int i = 0; i < G::E; ++i) {
         const bool fin = x[i] > -__builtin_inff();
         const float wf = dense_wf(x[i], xmax);
         const uint32_t b = fin ? (uint32_t)dense_d16(x[i], xmax) : SMP_DBINS + lane;
+        bin[i] = b;
         // (W << 14) + 1: W 2^14 < 2^51 is an exact integral float
         atomicAdd((unsigned long long*)&hist[b], (unsigned long long)(wf_u64(wf * 16384.0f) | 1ull));
     }
@@ -3756,6 +3766,71 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
         ((llima_u32x4*)reg)[t] = llima_u32x4{(uint32_t)h0, (uint32_t)(h0 >> 32), (uint32_t)h1,
                                              (uint32_t)(h1 >> 32)};
     }
+    // the chunk's highest values: bins [0, hi] with at most SMP_XSTG values
+    // (wave 0: BPL bins per lane), staged so that dense_keep takes the
+    // boundary bin's members from them instead of reading the chunk again.
+    // fp32 only: a bf16 thread's 32 values kept live past the binning would
+    // not fit the 64 registers of eight waves per SIMD.
+    if constexpr (sizeof(TL) != 4) {
+        if (t == 0) reg[SMP_DSWIN] = 0;                  // no window
+        return;
+    }
+    if (wave_id() == 0) {
+        static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
+        constexpr int BPL = SMP_DBINS / 64;
+        uint32_t bc[BPL], lsum = 0;
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            bc[i] = (uint32_t)(hist[BPL * lane + i] & 0x3FFFu);
+            lsum += bc[i];
+        }
+        const uint32_t cum = wave_incl_scan_u32(lsum);
+        const int j = __builtin_popcountll(ballot(cum <= SMP_XSTG));   // the first lane that does not fit
+        int hi = SMP_DBINS - 1;
+        if (j < 64) {                                        // uniform
+            uint32_t run = cum - lsum, nf = 0;
+#pragma unroll
+            for (int i = 0; i < BPL; ++i) {
+                run += bc[i];
+                nf += run <= SMP_XSTG && nf == (uint32_t)i ? 1u : 0u;
+            }
+            hi = BPL * j + (int)readlane(nf, (uint32_t)j) - 1;
+        }
+        if (lane == 0) {
+            swin_hi = hi;
+            swin_n = 0;
+        }
+    }
+    __syncthreads();
+    const int hi = swin_hi;
+    uint32_t n = 0;
+    if (hi >= 0) {                                           // uniform
+        uint32_t sm = 0;
+#pragma unroll
+        for (int i = 0; i < G::E; ++i)
+            sm |= (int)bin[i] <= hi ? 1u << i : 0u;          // -inf: a spare bin, above hi
+        if (ballot(sm != 0u)) {                              // uniform in the wave
+            const uint32_t cnt = (uint32_t)__popc(sm);
+            const uint32_t inc = wave_incl_scan_u32(cnt);
+            uint32_t base = 0;
+            if (lane == 63) base = atomicAdd(&swin_n, inc);
+            base = readlane(base, 63) + inc - cnt;
+#pragma unroll
+            for (int j = 0; j < G::NL; ++j)
+#pragma unroll
+                for (int e = 0; e < G::EPL; ++e)
+                    if ((sm >> (j * G::EPL + e)) & 1u) {
+                        if (base < SMP_XSTG)                 // always: the window's count
+                            swin[base] = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) |
+                                         (uint32_t)dense_id<TL>(c0, j, e);
+                        ++base;
+                    }
+        }
+        __syncthreads();
+        n = swin_n < SMP_XSTG ? swin_n : SMP_XSTG;
+        if (t < n) P.xstg[((size_t)row * (uint32_t)P.S + chunk) * SMP_XSTG + t] = swin[t];
+    }
+    if (t == 0) reg[SMP_DSWIN] = (uint64_t)(uint32_t)(hi + 1) | ((uint64_t)n << 32);
 }
 
 template <typename TL>
@@ -3773,10 +3848,40 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(sizeof
     if (c.greedy) return;                               // dense_final writes greedy rows
     const bool topp = c.p < 1.0f;
     // top-p rows without min-p or a kept-set output need this pass only for
-    // the boundary bin's members: chunks without any leave before loading
-    if (topp && !(c.m > 0.0f) && !P.out_keep &&
-        (uint32_t)region_of(P, row, chunk)[SMP_DMCNT] == 0u)
-        return;                                          // uniform
+    // the boundary bin's members: chunks without any leave before loading,
+    // and chunks whose staged top window holds the boundary bin take them
+    // from it (wave 0) instead of reading the chunk
+    if (topp && !(c.m > 0.0f) && !P.out_keep) {         // uniform
+        const uint64_t* creg = region_of(P, row, chunk);
+        uint64_t* r0s = region_of(P, row, 0);
+        const uint32_t lane = lane_id();
+        // the staged path's loads, all requested before any is used (a lane
+        // past the window's count reads an unused slot)
+        const uint64_t mv = creg[SMP_DMCNT], win = creg[SMP_DSWIN], binfo = r0s[SMP_DINFO];
+        const uint64_t v = P.xstg[((size_t)row * (uint32_t)P.S + chunk) * SMP_XSTG + lane];
+        uint32_t kmax, nfin;
+        dense_row_stats(P, (int)row, &kmax, &nfin);
+        const uint32_t mcnt = (uint32_t)mv;
+        if (mcnt == 0u) return;                          // uniform
+        const uint32_t bs_ = (uint32_t)binfo;
+        if ((uint32_t)win > bs_) {                       // uniform: bins [0, hi] hold b*
+            if (wave_id() != 0 || nfin == 0) return;     // (nfin == 0: dense_bound did not run)
+            const float xmax = key_f32(kmax);
+            const uint32_t n = (uint32_t)(win >> 32);
+            const bool mem = lane < n && (uint32_t)dense_d16(key_f32((uint32_t)(v >> 32)), xmax) == bs_;
+            const uint64_t bm = ballot(mem);
+            const uint32_t nm = (uint32_t)__popcll(bm);
+            const uint32_t cap = dense_member_cap(P.S);
+            // the bin's count from dense_bound: a mismatch (never) leaves the
+            // row's member count above the cap, so dense_final takes the full-row path
+            uint32_t base = 0;
+            if (lane == 0) base = arrive_agent((uint32_t*)(r0s + SMP_DMEM), nm == mcnt ? nm : cap + 1u);
+            base = readlane(base, 0);
+            const uint32_t o = base + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull));
+            if (mem && nm == mcnt && o < cap) *dense_member(r0s, o) = v;
+            return;
+        }
+    }
     int32_t hid[SMP_HBATCH];
     if (P.H_max > 0) dense_hist_ids(P, (int)row, hid);
     llima_u32x4 raw[G::NL];
