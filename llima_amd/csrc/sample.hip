@@ -3725,9 +3725,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
     using G = DenseGeom<TL>;
     extern __shared__ __align__(16) uint32_t table[];
     __shared__ uint64_t hist[SMP_DBINS + 64];           // + a spare bin per lane
-    __shared__ uint64_t swin[SMP_XSTG];                 // the staged top window
-    __shared__ int32_t swin_hi;
-    __shared__ uint32_t swin_n;
+    __shared__ uint32_t swin_n;                         // values staged so far
     uint32_t row, chunk;
     map_row_chunk(blockIdx.x, (uint32_t)P.B, (uint32_t)P.S, &row, &chunk);
     if (row >= (uint32_t)P.B) return;
@@ -3743,6 +3741,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
     if (nfin == 0) return;
     const uint32_t t = threadIdx.x, lane = lane_id();
     for (uint32_t i = t; i < SMP_DBINS + 64; i += LLIMA_WG) hist[i] = 0;
+    if (t == 0) swin_n = 0;
     if (c.pen) dense_count(P, (int)row, c, hid, c0, G::CHUNK, table);
     __syncthreads();
     float x[G::E];
@@ -3767,7 +3766,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
                                              (uint32_t)(h1 >> 32)};
     }
     // the chunk's highest values: bins [0, hi] with at most SMP_XSTG values
-    // (wave 0: BPL bins per lane), staged so that dense_keep takes the
+    // (BPL bins per lane), staged so that dense_keep takes the
     // boundary bin's members from them instead of reading the chunk again.
     // fp32 only: a bf16 thread's 32 values kept live past the binning would
     // not fit the 64 registers of eight waves per SIMD.
@@ -3775,35 +3774,33 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
         if (t == 0) reg[SMP_DSWIN] = 0;                  // no window
         return;
     }
-    if (wave_id() == 0) {
-        static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
-        constexpr int BPL = SMP_DBINS / 64;
-        uint32_t bc[BPL], lsum = 0;
+    // Every wave finds the window itself from the same bins, and stores its
+    // own staged values at places from one LDS atomic: no barrier.
+    static_assert(SMP_DBINS % 64 == 0, "bins tile the lanes");
+    constexpr int BPL = SMP_DBINS / 64;
+    uint32_t bc[BPL], lsum = 0;
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) {
+        bc[i] = (uint32_t)(hist[BPL * lane + i] & 0x3FFFu);
+        lsum += bc[i];
+    }
+    const uint32_t cum = wave_incl_scan_u32(lsum);
+    const int jl = __builtin_popcountll(ballot(cum <= SMP_XSTG));   // the first lane that does not fit
+    int hi = SMP_DBINS - 1;
+    uint32_t n = readlane(cum, 63);                          // the window's count
+    if (jl < 64) {                                           // uniform
+        uint32_t run = cum - lsum, nf = 0, fit = run;
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
-            bc[i] = (uint32_t)(hist[BPL * lane + i] & 0x3FFFu);
-            lsum += bc[i];
+            run += bc[i];
+            const bool in = run <= SMP_XSTG && nf == (uint32_t)i;
+            nf += in ? 1u : 0u;
+            fit = in ? run : fit;
         }
-        const uint32_t cum = wave_incl_scan_u32(lsum);
-        const int j = __builtin_popcountll(ballot(cum <= SMP_XSTG));   // the first lane that does not fit
-        int hi = SMP_DBINS - 1;
-        if (j < 64) {                                        // uniform
-            uint32_t run = cum - lsum, nf = 0;
-#pragma unroll
-            for (int i = 0; i < BPL; ++i) {
-                run += bc[i];
-                nf += run <= SMP_XSTG && nf == (uint32_t)i ? 1u : 0u;
-            }
-            hi = BPL * j + (int)readlane(nf, (uint32_t)j) - 1;
-        }
-        if (lane == 0) {
-            swin_hi = hi;
-            swin_n = 0;
-        }
+        hi = BPL * jl + (int)readlane(nf, (uint32_t)jl) - 1;
+        n = readlane(fit, (uint32_t)jl);
     }
-    __syncthreads();
-    const int hi = swin_hi;
-    uint32_t n = 0;
+    if (t == 0) reg[SMP_DSWIN] = (uint64_t)(uint32_t)(hi + 1) | ((uint64_t)n << 32);
     if (hi >= 0) {                                           // uniform
         uint32_t sm = 0;
 #pragma unroll
@@ -3815,22 +3812,19 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
             uint32_t base = 0;
             if (lane == 63) base = atomicAdd(&swin_n, inc);
             base = readlane(base, 63) + inc - cnt;
+            uint64_t* dst = P.xstg + ((size_t)row * (uint32_t)P.S + chunk) * SMP_XSTG;
 #pragma unroll
             for (int j = 0; j < G::NL; ++j)
 #pragma unroll
                 for (int e = 0; e < G::EPL; ++e)
                     if ((sm >> (j * G::EPL + e)) & 1u) {
                         if (base < SMP_XSTG)                 // always: the window's count
-                            swin[base] = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) |
-                                         (uint32_t)dense_id<TL>(c0, j, e);
+                            dst[base] = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) |
+                                        (uint32_t)dense_id<TL>(c0, j, e);
                         ++base;
                     }
         }
-        __syncthreads();
-        n = swin_n < SMP_XSTG ? swin_n : SMP_XSTG;
-        if (t < n) P.xstg[((size_t)row * (uint32_t)P.S + chunk) * SMP_XSTG + t] = swin[t];
     }
-    if (t == 0) reg[SMP_DSWIN] = (uint64_t)(uint32_t)(hi + 1) | ((uint64_t)n << 32);
 }
 
 template <typename TL>
