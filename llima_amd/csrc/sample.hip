@@ -124,6 +124,7 @@ struct SampleParams {
     int32_t rank;        // bound_rank of the broadcast top-k (per-row k: computed per row)
     int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
     int32_t fsplit;      // sample_finish workgroups per row (> 1: rows without top-k may be split)
+    int32_t rcpw;        // chunks per part of a split row (at most SMP_RCPW)
     uint64_t* xstg;      // [B][S][SMP_XSTG] split-row staging beyond the regions
     uint32_t* rcnt;      // [B][SMP_RCNT] split-row arrival counters, zeroed by the sweep
 };
@@ -1572,7 +1573,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 // a batch whose other rows keep the two-launch path (per-row settings, or a
 // mask): sample_finish then runs with P.fsplit workgroups per row, and such a
 // row is binned by all of them in parallel instead of by one workgroup's
-// full-row passes.  Part f takes chunks [f SMP_RCPW, (f + 1) SMP_RCPW): every
+// full-row passes.  Part f takes chunks [f P.rcpw, (f + 1) P.rcpw): every
 // value's exact weight into the full-row path's SMP_DBINS value bins below the
 // row maximum (fl(max M / T) from the sweep's headers), written per chunk to
 // the chunk's region as the mass above each bin and the bin's count, with the
@@ -1609,7 +1610,7 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 #define SMP_RSTG (SMP_RSTGI + 1)                   // staged values (key << 32 | id)
 #define SMP_RSTG_CAP (SMP_REGION - SMP_RSTG)       // 60
 #define SMP_STG_CAP (SMP_RSTG_CAP + SMP_XSTG)      // 124
-#define SMP_RCPW 4                                 // chunks per part
+#define SMP_RCPW 4                                 // chunks per part, at most
 static_assert(SMP_RBMF < SMP_REGION, "split-row region layout");
 static_assert(SMP_STG_CAP <= 128, "a wave reads a chunk's staging in two loads per lane");
 
@@ -1907,7 +1908,7 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
                   "the part's chunk bins fit beside the history table");
     static_assert(SMP_RCPW <= LLIMA_WAVES, "one wave per chunk of a part");
     const int S = P.S;
-    const int ch0 = part * SMP_RCPW, ch1 = ch0 + SMP_RCPW < S ? ch0 + SMP_RCPW : S;
+    const int ch0 = part * P.rcpw, ch1 = ch0 + P.rcpw < S ? ch0 + P.rcpw : S;
     const int nch = ch1 - ch0;
     const float xmax = key_f32(kmax);
     const float mthr_f = dense_mthr(c);
@@ -4264,7 +4265,7 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     P.wide = bitmask && !cfg->greedy && !cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V) &&
              P.S <= SMP_MAX_S;
     // Rows without top-k whose candidates overflow are split over
-    // ceil(S / SMP_RCPW) finish workgroups in batches that keep the two-launch
+    // ceil(S / P.rcpw) finish workgroups in batches that keep the two-launch
     // path: per-row top-k (rows of either kind), or a mask without top-k.  With
     // per-row top-k, a scalar top_k in (0, V) is the caller's word that every
     // row has top-k (a row without then takes the full-row path: slower, not
@@ -4272,8 +4273,13 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     const bool rows_may_lack_topk = cfg->top_k_rows && !(cfg->top_k > 0 && cfg->top_k < V);
     P.xstg = P.ws + (size_t)B * P.S * SMP_REGION;
     P.rcnt = (uint32_t*)(P.xstg + (size_t)B * P.S * SMP_XSTG);
+    // Chunks per part: three under a mask (every row of such a batch may be
+    // split, and the finish's two workgroups per CU still hold all the parts
+    // of 32 rows of 38 chunks), four with per-row top-k (the rows with top-k
+    // finish beside the parts; three measured slower there).
+    P.rcpw = P.wide ? 3 : SMP_RCPW;
     P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (rows_may_lack_topk || P.wide))
-                   ? (P.S + SMP_RCPW - 1) / SMP_RCPW : 1;
+                   ? (P.S + P.rcpw - 1) / P.rcpw : 1;
     // Rows without top-k (and without a mask) take the dense path: their sweep
     // bound would admit nearly every value of ordinary logits.
     const bool dense = !bitmask && !cfg->greedy && !cfg->top_k_rows &&
