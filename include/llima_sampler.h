@@ -200,8 +200,8 @@ int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_
  * per GPU, allocated when the library is loaded on that GPU and held until the
  * process ends; the call allocates nothing.  Calls whose
  * llima_sample_workspace_bytes(B, V, dtype) exceed it return LLIMA_E_SCRATCH
- * (the workspace is 4.5 KB per row and 16 KB chunk plus 64 bytes per row:
- * B*(4608*ceil(V/4096) + 64) <= 48 MiB for fp32 rows, with ceil(V/8192) for bf16).
+ * (the workspace is 5 KB per row and 16 KB chunk plus 64 bytes per row:
+ * B*(5120*ceil(V/4096) + 64) <= 48 MiB for fp32 rows, with ceil(V/8192) for bf16).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams, or different host threads without ordering) race.
  * The first call on a device looks the array's address up (once) and must be

@@ -65,7 +65,9 @@ namespace llima {
 #define SMP_SEG 8192                               // full-row path segment
 #define SMP_HASH 4096                              // lazy-penalty hash slots
 #define SMP_RCNT 16                                // split-row arrival counter stride (u32: 64 bytes)
-#define SMP_XSTG 64                                // split-row staging slots per chunk beyond its region
+#define SMP_XSTG 128                               // staging slots per chunk beyond its region
+#define SMP_DSTG 64                                // of which the dense path's window uses
+static_assert(SMP_DSTG <= 64 && SMP_DSTG <= SMP_XSTG, "one wave reads a dense window");
 #define SMP_PBINS 256                              // top-p value bins: floor(8 (xmax - x)), the last open
 #define SMP_PBIN_SCALE 8.0f
 #define SMP_PBIN_SLOTS (SMP_PBINS + 64)            // + a spare bin per lane
@@ -125,6 +127,7 @@ struct SampleParams {
     int32_t wide;        // sample_finish_wide ran first: finish only the rows it left pending
     int32_t fsplit;      // sample_finish workgroups per row (> 1: rows without top-k may be split)
     int32_t rcpw;        // chunks per part of a split row (at most SMP_RCPW)
+    int32_t scap;        // values a split row's chunk stages (at most SMP_STG_CAP)
     uint64_t* xstg;      // [B][S][SMP_XSTG] split-row staging beyond the regions
     uint32_t* rcnt;      // [B][SMP_RCNT] split-row arrival counters, zeroed by the sweep
 };
@@ -1609,10 +1612,10 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 #define SMP_RSTGI (SMP_RBMF + 1)                   // staged bins lo | hi << 16 | count << 32
 #define SMP_RSTG (SMP_RSTGI + 1)                   // staged values (key << 32 | id)
 #define SMP_RSTG_CAP (SMP_REGION - SMP_RSTG)       // 60
-#define SMP_STG_CAP (SMP_RSTG_CAP + SMP_XSTG)      // 124
+#define SMP_STG_CAP (SMP_RSTG_CAP + SMP_XSTG)      // 188
 #define SMP_RCPW 4                                 // chunks per part, at most
 static_assert(SMP_RBMF < SMP_REGION, "split-row region layout");
-static_assert(SMP_STG_CAP <= 128, "a wave reads a chunk's staging in two loads per lane");
+static_assert(SMP_STG_CAP <= 192, "a wave reads a chunk's staging in three loads per lane");
 
 // Staged value j of a chunk: in its region, then beyond the regions.
 __device__ __forceinline__ uint64_t* stg_slot(const SampleParams& P, uint32_t row, uint32_t chunk, uint32_t j) {
@@ -1740,15 +1743,27 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
     for (uint32_t k = wave_id(); k < nstg; k += LLIMA_WAVES) {
         const uint32_t e = sh.coff[k];
         const uint32_t ch = e & 0xFFFFu, n = e >> 16;
-        const bool in0 = lane < n, in1 = lane + 64u < n;
-        const uint64_t v0 = in0 ? load_agent(stg_slot(P, (uint32_t)row, ch, lane)) : 0ull;
-        const uint64_t v1 = in1 ? load_agent(stg_slot(P, (uint32_t)row, ch, lane + 64u)) : 0ull;
-        const bool m0 = in0 && (uint32_t)dense_d16(key_f32((uint32_t)(v0 >> 32)), xmax) == bb;
-        const bool m1 = in1 && (uint32_t)dense_d16(key_f32((uint32_t)(v1 >> 32)), xmax) == bb;
-        if (m0 || m1) {
-            const uint32_t o = atomicAdd(&sh.lcount, (m0 ? 1u : 0u) + (m1 ? 1u : 0u));
-            if (m0 && o < SMP_FRMCAP) mem[o] = v0;
-            if (m1 && o + (m0 ? 1u : 0u) < SMP_FRMCAP) mem[o + (m0 ? 1u : 0u)] = v1;
+        uint64_t v[3];
+        bool m[3];
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {                        // all three requested first
+            const uint32_t j = lane + 64u * (uint32_t)h;
+            v[h] = j < n ? load_agent(stg_slot(P, (uint32_t)row, ch, j)) : 0ull;
+        }
+        uint32_t nmh = 0;
+#pragma unroll
+        for (int h = 0; h < 3; ++h) {
+            m[h] = lane + 64u * (uint32_t)h < n && (uint32_t)dense_d16(key_f32((uint32_t)(v[h] >> 32)), xmax) == bb;
+            nmh += m[h] ? 1u : 0u;
+        }
+        if (nmh) {
+            uint32_t o = atomicAdd(&sh.lcount, nmh);
+#pragma unroll
+            for (int h = 0; h < 3; ++h)
+                if (m[h]) {
+                    if (o < SMP_FRMCAP) mem[o] = v[h];
+                    ++o;
+                }
         }
     }
     auto listed = [&](int s) { return (int)sh.ccount[s / SPC] * CV + (s % SPC) * FG::STEP; };
@@ -1947,7 +1962,8 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
             lsum += bc[i];
         }
         const uint32_t cum = wave_incl_scan_u32(lsum);
-        const uint64_t full = ballot(cum <= SMP_STG_CAP);    // a prefix of the lanes
+        const uint32_t scap = (uint32_t)P.scap;
+        const uint64_t full = ballot(cum <= scap);           // a prefix of the lanes
         const int j = __builtin_popcountll(full);            // the first lane that does not fit
         int hi_top = SMP_DBINS - 1;
         if (j < 64) {                                        // uniform
@@ -1955,7 +1971,7 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
 #pragma unroll
             for (int i = 0; i < BPL; ++i) {
                 run += bc[i];
-                nf += run <= SMP_STG_CAP && nf == (uint32_t)i ? 1u : 0u;
+                nf += run <= scap && nf == (uint32_t)i ? 1u : 0u;
             }
             hi_top = BPL * j + (int)readlane(nf, (uint32_t)j) - 1;
         }
@@ -1975,7 +1991,7 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
                 cnt += bu < SMP_DBINS ? (uint32_t)(bins[bu] & 0x3FFFu) : 0u;
             }
             const uint32_t inc = wave_incl_scan_u32(cnt);
-            const uint64_t fits = ballot(inc <= SMP_STG_CAP);   // a prefix of the lanes
+            const uint64_t fits = ballot(inc <= scap);          // a prefix of the lanes
             const int w = fits ? 63 - __builtin_clzll(fits) : -1;  // the widest window
             lo = w < 0 ? 1u : (uint32_t)((int)bbh - 4 * w > 0 ? (int)bbh - 4 * w : 0);
             hi = w < 0 ? 0u : (uint32_t)((int)bbh + w < SMP_DBINS - 1 ? (int)bbh + w : SMP_DBINS - 1);
@@ -2132,8 +2148,9 @@ __device__ __forceinline__ void split_part(const SampleParams& P, int row, const
             store_agent(reg + SMP_RBMF, (uint64_t)bmfc[cl]);
         }
         const uint32_t n = sh.coff[cl] < SMP_STG_CAP ? sh.coff[cl] : SMP_STG_CAP;
-        if (lane < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane), stg[cl * SMP_STG_CAP + lane]);
-        if (lane + 64u < n) store_agent(stg_slot(P, (uint32_t)row, ch, lane + 64u), stg[cl * SMP_STG_CAP + lane + 64u]);
+#pragma unroll
+        for (uint32_t j = lane; j < SMP_STG_CAP; j += 64u)
+            if (j < n) store_agent(stg_slot(P, (uint32_t)row, ch, j), stg[cl * SMP_STG_CAP + j]);
         if (lane == 0) store_agent(reg + SMP_RSTGI, ((uint64_t)n << 32) | sh.ccount[cl]);
     }
     // every store of the part completes before its arrival is counted
@@ -3404,8 +3421,8 @@ __global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
 //   region c, SMP_DKEPT             the kept mass of chunk c (dense_bound or dense_keep)
 //   region c, SMP_DMCNT             dense_bound: chunk c's count in the boundary bin
 //   region c, SMP_DSWIN             dense_hist: the chunk's highest bins [0, hi]
-//                                   holding at most SMP_XSTG values, staged in
-//                                   the chunk's SMP_XSTG slots after the regions
+//                                   holding at most SMP_DSTG values, staged in
+//                                   the chunk's slots after the regions
 //                                   (hi + 1, 0 for none | the count << 32)
 //   region 0, SMP_DINFO..+2         dense_bound's boundary bin, mass above it, Z
 //   region 0, SMP_DMEM              members appended (a 128-byte line of its
@@ -3766,7 +3783,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
         ((llima_u32x4*)reg)[t] = llima_u32x4{(uint32_t)h0, (uint32_t)(h0 >> 32), (uint32_t)h1,
                                              (uint32_t)(h1 >> 32)};
     }
-    // the chunk's highest values: bins [0, hi] with at most SMP_XSTG values
+    // the chunk's highest values: bins [0, hi] with at most SMP_DSTG values
     // (BPL bins per lane), staged so that dense_keep takes the
     // boundary bin's members from them instead of reading the chunk again.
     // fp32 only: a bf16 thread's 32 values kept live past the binning would
@@ -3786,7 +3803,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
         lsum += bc[i];
     }
     const uint32_t cum = wave_incl_scan_u32(lsum);
-    const int jl = __builtin_popcountll(ballot(cum <= SMP_XSTG));   // the first lane that does not fit
+    const int jl = __builtin_popcountll(ballot(cum <= SMP_DSTG));   // the first lane that does not fit
     int hi = SMP_DBINS - 1;
     uint32_t n = readlane(cum, 63);                          // the window's count
     if (jl < 64) {                                           // uniform
@@ -3794,7 +3811,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             run += bc[i];
-            const bool in = run <= SMP_XSTG && nf == (uint32_t)i;
+            const bool in = run <= SMP_DSTG && nf == (uint32_t)i;
             nf += in ? 1u : 0u;
             fit = in ? run : fit;
         }
@@ -3819,7 +3836,7 @@ __global__ __launch_bounds__(LLIMA_WG) __attribute__((amdgpu_waves_per_eu(8, 8))
 #pragma unroll
                 for (int e = 0; e < G::EPL; ++e)
                     if ((sm >> (j * G::EPL + e)) & 1u) {
-                        if (base < SMP_XSTG)                 // always: the window's count
+                        if (base < SMP_DSTG)                 // always: the window's count
                             dst[base] = ((uint64_t)f32_key(x[j * G::EPL + e]) << 32) |
                                         (uint32_t)dense_id<TL>(c0, j, e);
                         ++base;
@@ -4278,6 +4295,10 @@ extern "C" int llima_sample(const void* logits, int32_t dtype, int32_t B, int32_
     // of 32 rows of 38 chunks), four with per-row top-k (the rows with top-k
     // finish beside the parts; three measured slower there).
     P.rcpw = P.wide ? 3 : SMP_RCPW;
+    // Staged values per chunk: masked rows need more of them for a window that
+    // holds the row's boundary bin (about 135 values of a half-masked chunk lie
+    // at or above it) than unmasked ones, whose extra staging only costs time.
+    P.scap = P.wide ? SMP_STG_CAP : 124;
     P.fsplit = (!cfg->greedy && !out_keep && P.S <= SMP_MAX_S && (rows_may_lack_topk || P.wide))
                    ? (P.S + P.rcpw - 1) / P.rcpw : 1;
     // Rows without top-k (and without a mask) take the dense path: their sweep

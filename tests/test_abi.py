@@ -38,10 +38,10 @@ def test_host_only_entry_points():
     assert L.llima_status_string(-4).decode() == "workspace missing or too small"
     assert L.llima_status_string(-6).decode() == "first call on this device made under stream capture"
     assert L.llima_sample_workspace_bytes(64, 128256, 0) > 0
-    # the documented size rule: B (4608 S + 64) bytes, S chunks of 4096 fp32
+    # the documented size rule: B (5120 S + 64) bytes, S chunks of 4096 fp32
     # or 8192 bf16 values; the C5 shape fits the no-allocation scratch
     for B, V, dt, S in ((64, 128256, 0, 32), (32, 151936, 0, 38), (256, 262144, 1, 32), (3, 8193, 1, 2)):
-        assert L.llima_sample_workspace_bytes(B, V, dt) == B * (4608 * S + 64)
+        assert L.llima_sample_workspace_bytes(B, V, dt) == B * (5120 * S + 64)
     assert L.llima_sample_noalloc_max_bytes() == 48 << 20
     assert L.llima_sample_workspace_bytes(256, 262144, 1) <= L.llima_sample_noalloc_max_bytes()
     assert L.llima_argmax_workspace_bytes(0, 10, 0) == 0

@@ -94,7 +94,7 @@ def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
     L = _lib.lib()
     cfg, _ = SamplerConfig(top_k=5).to_c(4096, gpu)
     p = ctypes.c_void_p(256)
-    # 4096 rows of 128256 fp32 values need 4096 * 32 regions of 4.5 KB = 576 MiB
+    # 4096 rows of 128256 fp32 values need 4096 * 32 regions of 5 KB = 640 MiB
     assert L.llima_sample_workspace_bytes(4096, 128256, 0) > L.llima_sample_noalloc_max_bytes()
     rc = L.llima_sample_noalloc(p, 0, 4096, 128256, 128256, None, None, 0, None, p,
                                 ctypes.byref(cfg), p, None, None, None)
