@@ -1661,7 +1661,7 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
     uint64_t a0 = 0, a1 = 0;
     uint32_t n0 = 0, n1 = 0;
     if (t < SMP_DBINS / 2) {
-        constexpr int NB = 16;
+        constexpr int NB = 20;                               // 38 chunks: two rounds
         for (int b0 = 0; b0 < S; b0 += NB) {
             uint64_t v0[NB], v1[NB];
 #pragma unroll
@@ -1740,30 +1740,43 @@ __device__ __forceinline__ void split_final(const SampleParams& P, int row, cons
     if (t == 0) sh.lcount = 0;
     __syncthreads();
     const uint32_t lane = lane_id();
-    for (uint32_t k = wave_id(); k < nstg; k += LLIMA_WAVES) {
-        const uint32_t e = sh.coff[k];
-        const uint32_t ch = e & 0xFFFFu, n = e >> 16;
-        uint64_t v[3];
-        bool m[3];
+    // a wave takes chunks k, k + 4, k + 8 per round: their staging (three
+    // slots per lane each) requested together, one memory wait per round
+    constexpr int SQ = 3;
+    for (uint32_t k0 = wave_id(); k0 < nstg; k0 += SQ * LLIMA_WAVES) {
+        uint64_t v[SQ][3];
+        uint32_t ns[SQ];
 #pragma unroll
-        for (int h = 0; h < 3; ++h) {                        // all three requested first
-            const uint32_t j = lane + 64u * (uint32_t)h;
-            v[h] = j < n ? load_agent(stg_slot(P, (uint32_t)row, ch, j)) : 0ull;
+        for (int q = 0; q < SQ; ++q) {
+            const uint32_t k = k0 + (uint32_t)q * LLIMA_WAVES;
+            const uint32_t e = k < nstg ? sh.coff[k] : 0u;
+            const uint32_t ch = e & 0xFFFFu;
+            ns[q] = e >> 16;
+#pragma unroll
+            for (int h = 0; h < 3; ++h) {
+                const uint32_t j = lane + 64u * (uint32_t)h;
+                v[q][h] = j < ns[q] ? load_agent(stg_slot(P, (uint32_t)row, ch, j)) : 0ull;
+            }
         }
-        uint32_t nmh = 0;
 #pragma unroll
-        for (int h = 0; h < 3; ++h) {
-            m[h] = lane + 64u * (uint32_t)h < n && (uint32_t)dense_d16(key_f32((uint32_t)(v[h] >> 32)), xmax) == bb;
-            nmh += m[h] ? 1u : 0u;
-        }
-        if (nmh) {
-            uint32_t o = atomicAdd(&sh.lcount, nmh);
+        for (int q = 0; q < SQ; ++q) {
+            bool m[3];
+            uint32_t nmh = 0;
 #pragma unroll
-            for (int h = 0; h < 3; ++h)
-                if (m[h]) {
-                    if (o < SMP_FRMCAP) mem[o] = v[h];
-                    ++o;
-                }
+            for (int h = 0; h < 3; ++h) {
+                m[h] = lane + 64u * (uint32_t)h < ns[q] &&
+                       (uint32_t)dense_d16(key_f32((uint32_t)(v[q][h] >> 32)), xmax) == bb;
+                nmh += m[h] ? 1u : 0u;
+            }
+            if (nmh) {
+                uint32_t o = atomicAdd(&sh.lcount, nmh);
+#pragma unroll
+                for (int h = 0; h < 3; ++h)
+                    if (m[h]) {
+                        if (o < SMP_FRMCAP) mem[o] = v[q][h];
+                        ++o;
+                    }
+            }
         }
     }
     auto listed = [&](int s) { return (int)sh.ccount[s / SPC] * CV + (s % SPC) * FG::STEP; };
