@@ -3177,9 +3177,10 @@ __global__ __launch_bounds__(LLIMA_WG) void sample_finish(SampleParams P) {
 // candidates each (every allowed value within the weight window), which one
 // 256-thread workgroup per row takes through its gather path at one wave per
 // SIMD.  This kernel runs before sample_finish on such batches and takes each
-// row with 1024 threads, 4 candidates each: the gather (every candidate of the
-// row requested at once, its chunk found by a binary search over the chunk
-// offsets), keys, weights, the top-p boundary over value bins (fin_topp_bins),
+// row with 1024 threads, 4 candidates each: the gather (one round of loads
+// brings every chunk's header and its first 8 tpc - 1 candidates, tpc =
+// 1024 / 2^lgs threads per chunk; only chunks with more are read again),
+// keys, weights, the top-p boundary over value bins (fin_topp_bins),
 // min-p and the draw as one block scan in id order: fin_elems' steps for rows
 // without top-k.  A row it does not finish (greedy, an overflowed region,
 // more than SMP_FIN_CAP candidates, a bound the exactness check rejects, an
@@ -3215,6 +3216,7 @@ __device__ __forceinline__ uint64_t blk_excl_scan_u64(uint64_t v, uint64_t* tota
 
 struct WideShared {
     uint64_t cand[SMP_FIN_CAP + (SMP_FIN_CAP >> SMP_WPAD)];   // candidates, then the top-p bins
+    uint32_t ccount[SMP_MAX_S];                               // chunk candidate counts
     uint32_t coff[SMP_MAX_S];                                 // chunk offsets of the candidates
     llima_u32x4 sv[2 * SMP_SMALL + 64];                       // fin_topp_bins's boundary members
     uint32_t lcount;
@@ -3235,57 +3237,96 @@ __global__ __launch_bounds__(SMP_WIDE) void sample_finish_wide(SampleParams P) {
         if (t == 0) P.out_ids[row] = SMP_PENDING;
         return;
     }
-    // ---- chunk headers: candidate counts, overflow, the largest bound g / T
+    // ---- one round of loads: thread t reads 8 slots (64 bytes) of chunk
+    //      t >> sh8, part t & (tpc - 1), so up to pre - 1 candidates of every
+    //      chunk arrive with its header (slot 0 of part 0)
+    const uint32_t wv = t >> 6, lane = lane_id();
+    const int sh8 = 10 - P.lgs;                                  // S <= 2^lgs, lgs <= 8
+    const uint32_t tpc = 1u << sh8;
+    const uint32_t ch = t >> sh8, pt = t & (tpc - 1u);
+    const bool mine = (int)ch < S && pt * 8u < SMP_REGION;
+    const uint32_t pre = 8u * tpc < SMP_REGION ? 8u * tpc : SMP_REGION;   // first-round slots per chunk
+    const uint64_t* reg = P.ws + ((size_t)row * S + (mine ? ch : 0u)) * SMP_REGION + (mine ? pt * 8u : 0u);
+    llima_u32x4 q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = ((const llima_u32x4*)reg)[i];
+    // the header facts: candidate count, overflow, the largest bound g / T
+    const bool hdr = mine && pt == 0u;
     uint32_t cnt = 0, ovf = 0, gk = 0;
-    if ((int)t < S) {
-        const uint64_t h = *region_of(P, (uint32_t)row, t);
-        const uint32_t lo = (uint32_t)h;
+    if (hdr) {
+        const uint32_t lo = q[0].x;
         ovf = (lo >> 16) & HF_OVERFLOW;
         cnt = ovf ? 0u : (lo & 0xFFFFu);
-        const float g0 = nontopk_bound(P, c, __uint_as_float((uint32_t)(h >> 32)));   // no top-k here
+        const float g0 = nontopk_bound(P, c, __uint_as_float(q[0].y));   // no top-k here
         const float gt0 = g0 / c.T;
         gk = g0 > -__builtin_inff() ? (gt0 == gt0 ? f32_key(gt0) : 0xFFFFFFFFu) : 0u;
+        sh.ccount[ch] = cnt;
     }
-    // one exchange: the counts' scan, any overflow, the largest bound
-    const uint32_t wv = t >> 6, lane = lane_id();
-    uint32_t NG = 0, anyov = 0, gkey = 0, off = 0;
+    // one exchange: the count, any overflow, the largest bound
+    uint32_t NG = 0, anyov = 0, gkey = 0;
     {
-        const uint32_t inc = wave_incl_scan_u32(cnt), wov = wave_max_u32(ovf), wgk = wave_max_u32(gk);
-        if (lane == 63) { sh.r[0][wv] = inc; sh.r[1][wv] = wov; sh.r[2][wv] = wgk; }
+        const uint32_t sc = wave_sum_u32(cnt), wov = wave_max_u32(ovf), wgk = wave_max_u32(gk);
+        if (lane == 63) { sh.r[0][wv] = sc; sh.r[1][wv] = wov; sh.r[2][wv] = wgk; }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
-            off += (uint32_t)i < wv ? sh.r[0][i] : 0u;
             NG += sh.r[0][i];
             anyov = sh.r[1][i] > anyov ? sh.r[1][i] : anyov;
             gkey = sh.r[2][i] > gkey ? sh.r[2][i] : gkey;
         }
-        off += inc - cnt;
     }
-    if ((int)t < S) sh.coff[t] = off;
-    __syncthreads();
     if (anyov || NG > SMP_FIN_CAP) {                             // uniform
         if (t == 0) P.out_ids[row] = SMP_PENDING;
         return;
     }
-    // ---- gather: candidate f (id order) from its chunk's region, all loads first
-    const uint64_t* rbase = P.ws + (size_t)row * (uint32_t)S * SMP_REGION + SMP_HDR;
-    uint64_t q[EPT];
+    // the chunks' offsets in id order: wave 0, lane l owns chunks 4l .. 4l+3
+    if (wv == 0) {
+        uint32_t cc[4], s4 = 0;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        const uint32_t f = t + (uint32_t)k * SMP_WIDE;
-        uint32_t lo = 0, hi = (uint32_t)S;                        // the last chunk with coff <= f
-        while (hi - lo > 1u) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (sh.coff[mid] <= f) lo = mid; else hi = mid;
+        for (int i = 0; i < 4; ++i) {
+            const int cix = (int)lane * 4 + i;
+            cc[i] = cix < S ? sh.ccount[cix] : 0u;
+            s4 += cc[i];
         }
-        const uint32_t sl = f < NG ? f - sh.coff[lo] : 0u;
-        q[k] = rbase[(size_t)(f < NG ? lo : 0u) * SMP_REGION + sl];
-    }
+        const uint32_t inc = wave_incl_scan_u32(s4);
+        uint32_t o = inc - s4;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        const uint32_t f = t + (uint32_t)k * SMP_WIDE;
-        if (f < NG) sh.cand[f + (f >> SMP_WPAD)] = q[k];
+        for (int i = 0; i < 4; ++i) {
+            const int cix = (int)lane * 4 + i;
+            if (cix < S) sh.coff[cix] = o;
+            o += cc[i];
+        }
+    }
+    __syncthreads();
+    // ---- the candidates into LDS in id order (candidate f at f + f / 8):
+    //      this thread's first-round slots, then the rest of any chunk with
+    //      more than the first round covered
+    if (mine) {
+        const uint32_t n_c = sh.ccount[ch], o_c = sh.coff[ch];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int sl = (int)(pt * 8u) + 2 * i + h - SMP_HDR;   // candidate index
+                if (sl >= 0 && (uint32_t)sl < n_c) {
+                    const uint32_t f = o_c + (uint32_t)sl;
+                    sh.cand[f + (f >> SMP_WPAD)] = h ? (((uint64_t)q[i].w << 32) | q[i].z)
+                                                     : (((uint64_t)q[i].y << 32) | q[i].x);
+                }
+            }
+        }
+    }
+    const uint32_t pre_c = pre - SMP_HDR;
+    for (int cc = (int)wv; cc < S; cc += NW) {
+        const uint32_t n_c = sh.ccount[cc];
+        if (n_c > pre_c) {                                       // uniform in the wave
+            const uint32_t o_c = sh.coff[cc];
+            const uint64_t* src = P.ws + ((size_t)row * S + cc) * SMP_REGION + SMP_HDR;
+            for (uint32_t sl = pre_c + lane; sl < n_c; sl += 64) {
+                const uint32_t f = o_c + sl;
+                sh.cand[f + (f >> SMP_WPAD)] = src[sl];
+            }
+        }
     }
     __syncthreads();
     // ---- this thread's candidates 4t .. 4t+3, their keys of x / T
