@@ -1597,9 +1597,9 @@ __device__ __forceinline__ void finish_full_row(const SampleParams& P, int row, 
 //   SMP_RCUM + SMP_DBINS         the chunk's mass << 14
 //   SMP_RBMF                     the chunk's first bin with a value below min-p
 //   SMP_RSTGI, SMP_RSTG          staged values: every value of the chunk in bins
-//                                [lo, hi] (at most SMP_STG_CAP: the first
-//                                SMP_RSTG_CAP here, the rest in the chunk's
-//                                SMP_XSTG slots after the regions); the last
+//                                [lo, hi] (at most P.scap <= SMP_STG_CAP: the
+//                                first SMP_RSTG_CAP here, the rest in the
+//                                chunk's SMP_XSTG slots after the regions); the last
 //                                part reads a chunk again only when the row's
 //                                boundary bin lies outside the window
 // The window: the part's own chunks (those binned so far, for fp32) give an
