@@ -291,6 +291,30 @@ def test_sample_gather_path_top_p(gpu, oracle, kind):
             _sample_both(gpu, oracle, xx, u, cfgd, history=hist, hist_len=hl, mask=mask)
 
 
+@pytest.mark.parametrize("V", [151936, 100000])
+def test_sample_wide_dense_chunk(gpu, oracle, V):
+    """A grammar mask allowing 1 % of the ids, plus 300 or 350 consecutive
+    allowed ids inside one chunk (fewer than a region holds): that chunk's
+    candidates exceed what the wide finish's first round of loads brings (127
+    per chunk at 38 fp32 chunks, 255 at 25 fp32 or 19 bf16 chunks), so the
+    rest come from its second round.  Each row has its dense block elsewhere."""
+    _say("sample wide dense chunk", V)
+    rng = np.random.default_rng(V + 7)
+    B = 6
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    mask = _sparse_mask(rng, B, V, 0.01)
+    nchunks = V // 8192
+    for b in range(B):
+        c0 = ((3 * b + 1) % nchunks) * 8192 + 100            # inside one fp32 and one bf16 chunk
+        ids = np.arange(c0, c0 + (300 if b % 2 == 0 else 350))
+        np.bitwise_or.at(mask[b], ids >> 5, (np.uint32(1) << (ids & 31).astype(np.uint32)))
+    u = rng.random(B).astype(np.float32)
+    for cfgd in [dict(temperature=1.0, top_p=0.9), dict(temperature=0.7, top_p=0.95, min_p=0.02)]:
+        for dt in ("f32", "bf16"):
+            xx = wl.f32_to_bf16_bits(x) if dt == "bf16" else x
+            _sample_both(gpu, oracle, xx, u, cfgd, mask=mask)
+
+
 DENSE_CONFIGS = [
     dict(temperature=1.0, top_p=0.9),
     dict(temperature=0.7, top_p=0.5, min_p=0.05),
